@@ -1,0 +1,856 @@
+// hx_api.cpp -- the C ABI of libhxmi (declared in include/hx.h): argument
+// validation, the per-stream workspace, the resident-weight registry, the
+// pinned-config table, and dispatch onto the kernel families.
+//
+// Ownership follows the reference runtime (QHB/bin/runtime/include/
+// HexagonCAPI.h:21-68): callers own tensors, the library owns resident
+// weights (hexagon_runtime_weight_resident_v2) and workspace
+// (hexagon_runtime_workspace_resident_v2).  Unlike the reference, a failure
+// returns a status instead of aborting, and resident weights are keyed by
+// content, not by source address, so a changed weight is a new registration
+// rather than a stale image (QHB/include/hexagon/Dialect/Hmx/Transforms/
+// Passes.td:381-389 documents the reference's never-revalidated contents).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <set>
+#include <string>
+#include <tuple>
+#include <vector>
+
+#include "../../include/hx.h"
+#include "hx_device.hpp"
+#include "hx_internal.hpp"
+
+#ifndef HX_BUILD_ID
+#define HX_BUILD_ID "hxmi-dev"
+#endif
+
+using namespace hx;
+
+// ---------------------------------------------------------------------------
+// Errors
+// ---------------------------------------------------------------------------
+static thread_local std::string g_err;
+
+static int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define HX_HIP_TRY(expr)                                                              \
+  do {                                                                                \
+    hipError_t e_ = (expr);                                                           \
+    if (e_ != hipSuccess) return fail(HX_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
+  } while (0)
+
+static int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(HX_ERR_HIP, "%s launch: %s", what, hipGetErrorString(e));
+  return HX_OK;
+}
+
+static int map_internal(int rc, const char* what) {
+  if (rc == HXI_OK) return check_launch(what);
+  switch (rc) {
+    case HXI_ERR_UNSUPPORTED: return fail(HX_ERR_UNSUPPORTED, "%s: shape not supported", what);
+    case HXI_ERR_DTYPE: return fail(HX_ERR_DTYPE, "%s: dtype not supported", what);
+    case HXI_ERR_SHAPE: return fail(HX_ERR_SHAPE, "%s: bad shape", what);
+    default: return fail(HX_ERR_ARG, "%s: internal argument error %d", what, rc);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Device / workspace
+// ---------------------------------------------------------------------------
+static std::mutex g_mu;
+
+static int current_device(int* dev) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return fail(HX_ERR_NODEVICE, "no HIP device visible");
+  HX_HIP_TRY(hipGetDevice(dev));
+  return HX_OK;
+}
+
+struct Workspace {
+  char* buf = nullptr;       // carved by the top-level entry point of a call
+  size_t bytes = 0;
+  float* part = nullptr;     // split-K partial sums of the GEMV (its own region)
+  size_t part_bytes = 0;
+  unsigned* counters = nullptr;
+  size_t ncounters = 0;
+};
+static std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+
+// A scratch region of at least `bytes` for work enqueued on `s`.  Growing it
+// synchronizes `s` first, so kernels still reading the old region finish.
+static int ws_get(hipStream_t s, size_t bytes, char** out) {
+  int dev;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(g_mu);
+  Workspace& w = g_ws[{dev, s}];
+  if (w.bytes < bytes) {
+    size_t nb = bytes > 2 * w.bytes ? bytes : 2 * w.bytes;
+    nb = (nb + 4095) & ~(size_t)4095;
+    HX_HIP_TRY(hipStreamSynchronize(s));
+    if (w.buf) HX_HIP_TRY(hipFree(w.buf));
+    w.buf = nullptr;
+    w.bytes = 0;
+    if (hipMalloc(&w.buf, nb) != hipSuccess) return fail(HX_ERR_NOMEM, "workspace of %zu bytes", nb);
+    w.bytes = nb;
+  }
+  *out = w.buf;
+  return HX_OK;
+}
+
+// Split-K partial sums.  A region of its own, so that a GEMV launched from
+// inside an entry point never aliases the scratch that entry point carved.
+static int ws_partials(hipStream_t s, size_t bytes, float** out) {
+  int dev;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(g_mu);
+  Workspace& w = g_ws[{dev, s}];
+  if (w.part_bytes < bytes) {
+    size_t nb = bytes > 2 * w.part_bytes ? bytes : 2 * w.part_bytes;
+    nb = (nb + 4095) & ~(size_t)4095;
+    HX_HIP_TRY(hipStreamSynchronize(s));
+    if (w.part) HX_HIP_TRY(hipFree(w.part));
+    w.part = nullptr;
+    w.part_bytes = 0;
+    if (hipMalloc((void**)&w.part, nb) != hipSuccess) return fail(HX_ERR_NOMEM, "partials of %zu bytes", nb);
+    w.part_bytes = nb;
+  }
+  *out = w.part;
+  return HX_OK;
+}
+
+// Zero-initialised ticket counters (reset to zero by the kernels that use
+// them, so they are cleared only when allocated).
+static int ws_counters(hipStream_t s, size_t n, unsigned** out) {
+  int dev;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(g_mu);
+  Workspace& w = g_ws[{dev, s}];
+  if (w.ncounters < n) {
+    size_t nn = n > 2 * w.ncounters ? n : 2 * w.ncounters;
+    HX_HIP_TRY(hipStreamSynchronize(s));
+    if (w.counters) HX_HIP_TRY(hipFree(w.counters));
+    w.counters = nullptr;
+    w.ncounters = 0;
+    if (hipMalloc(&w.counters, nn * sizeof(unsigned)) != hipSuccess)
+      return fail(HX_ERR_NOMEM, "counters");
+    HX_HIP_TRY(hipMemset(w.counters, 0, nn * sizeof(unsigned)));
+    w.ncounters = nn;
+  }
+  *out = w.counters;
+  return HX_OK;
+}
+
+// Carve 256-byte aligned sub-buffers out of one workspace region.
+struct Carver {
+  size_t used = 0;
+  size_t take(size_t bytes) {
+    size_t at = used;
+    used += (bytes + 255) & ~(size_t)255;
+    return at;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Descriptors
+// ---------------------------------------------------------------------------
+static size_t dt_size(int dt) {
+  switch (dt) {
+    case HX_F16: case HX_BF16: return 2;
+    case HX_F32: case HX_I32: return 4;
+    case HX_I8: return 1;
+    default: return 0;
+  }
+}
+static const char* dt_name(int dt) {
+  switch (dt) {
+    case HX_F16: return "f16"; case HX_BF16: return "bf16"; case HX_F32: return "f32";
+    case HX_I8: return "i8"; case HX_I32: return "i32"; default: return "?";
+  }
+}
+
+struct View2 {
+  char* p;
+  int64_t rows, cols, ld;
+};
+struct View1 {
+  char* p;
+  int64_t n;
+};
+
+static int view2(const hx_memref2d* m, int dt, const char* name, View2* v) {
+  if (!m) return fail(HX_ERR_ARG, "%s: null descriptor", name);
+  const size_t es = dt_size(dt);
+  if (!es) return fail(HX_ERR_DTYPE, "%s: unknown dtype %d", name, dt);
+  if (m->sizes[0] < 0 || m->sizes[1] < 0 || m->offset < 0)
+    return fail(HX_ERR_ARG, "%s: negative size/offset", name);
+  v->rows = m->sizes[0];
+  v->cols = m->sizes[1];
+  if (v->rows > 0 && v->cols > 1 && m->strides[1] != 1)
+    return fail(HX_ERR_LAYOUT, "%s: innermost stride %lld != 1", name, (long long)m->strides[1]);
+  v->ld = m->strides[0];
+  if (v->rows > 1 && v->ld < v->cols)
+    return fail(HX_ERR_LAYOUT, "%s: row stride %lld < row length %lld", name, (long long)v->ld,
+                (long long)v->cols);
+  if (v->rows <= 1 && v->ld < v->cols) v->ld = v->cols;
+  if (v->rows * v->cols > 0 && !m->aligned) return fail(HX_ERR_ARG, "%s: null data", name);
+  v->p = (char*)m->aligned + m->offset * (int64_t)es;
+  return HX_OK;
+}
+
+static int view1(const hx_memref1d* m, int dt, const char* name, int64_t expect, View1* v) {
+  if (!m) return fail(HX_ERR_ARG, "%s: null descriptor", name);
+  const size_t es = dt_size(dt);
+  if (!es) return fail(HX_ERR_DTYPE, "%s: unknown dtype %d", name, dt);
+  if (m->sizes[0] != expect)
+    return fail(HX_ERR_SHAPE, "%s: length %lld, expected %lld", name, (long long)m->sizes[0],
+                (long long)expect);
+  if (m->sizes[0] > 1 && m->strides[0] != 1)
+    return fail(HX_ERR_LAYOUT, "%s: stride %lld != 1", name, (long long)m->strides[0]);
+  if (m->sizes[0] > 0 && !m->aligned) return fail(HX_ERR_ARG, "%s: null data", name);
+  v->p = (char*)m->aligned + m->offset * (int64_t)es;
+  v->n = m->sizes[0];
+  return HX_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Pinned configurations
+// ---------------------------------------------------------------------------
+static std::map<std::tuple<int, int, int64_t, int64_t, int64_t>, int> g_pins;
+
+// (gemm mode, epilogue) of each GEMM family
+static bool op_gemm(int op, int* mode, int* epi) {
+  switch (op) {
+    case HX_OP_GEMM_I8: *mode = GM_I8; *epi = GE_STORE; return true;
+    case HX_OP_MATMUL_F16: *mode = GM_F16; *epi = GE_STORE; return true;
+    case HX_OP_MATMUL_BF16: *mode = GM_BF16; *epi = GE_STORE; return true;
+    case HX_OP_MATMUL_W8: *mode = GM_W8; *epi = GE_STORE; return true;
+    case HX_OP_SWIGLU_W8: *mode = GM_W8; *epi = GE_SWIGLU; return true;
+    default: return false;
+  }
+}
+
+// Table indices (into the mode's table) of the configs of one family.
+static std::vector<int> family_indices(int op) {
+  std::vector<int> out;
+  int mode, epi;
+  if (op == HX_OP_GEMV_W8) {
+    for (int i = 0; i < gemv_config_count(); ++i) out.push_back(i);
+    return out;
+  }
+  if (!op_gemm(op, &mode, &epi)) return out;
+  for (int i = 0; i < gemm_config_count(mode); ++i)
+    if (gemm_config(mode, i)->epi == epi) out.push_back(i);
+  return out;
+}
+
+static int pinned(int op, int64_t m, int64_t n, int64_t k) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_pins.find(std::make_tuple(dev, op, m, n, k));
+  return it == g_pins.end() ? -1 : it->second;
+}
+
+// Mode-table index a call of family `op` runs with.
+static int resolve_gemm(int op, int64_t M, int64_t N, int64_t K) {
+  int mode, epi;
+  op_gemm(op, &mode, &epi);
+  const int pin = pinned(op, M, N, K);
+  if (pin >= 0) {
+    std::vector<int> idx = family_indices(op);
+    if (pin < (int)idx.size()) return idx[pin];
+  }
+  return gemm_default_config(mode, epi, M, N, K);
+}
+static int resolve_gemv(int64_t M, int64_t N, int64_t K) {
+  const int pin = pinned(HX_OP_GEMV_W8, M, N, K);
+  if (pin >= 0 && pin < gemv_config_count()) return pin;
+  return gemv_default_config(M, N, K);
+}
+
+static int run_gemm(int op, GemmArgs& a, hipStream_t s) {
+  int mode, epi;
+  op_gemm(op, &mode, &epi);
+  if (a.M == 0 || a.N == 0) return HX_OK;
+  if (gemm_fast_ok(mode, a)) {
+    const int cfg = resolve_gemm(op, a.M, a.N, a.K);
+    if (cfg >= 0) return map_internal(launch_gemm(mode, cfg, a, s), "gemm");
+  }
+  return map_internal(launch_gemm_generic(mode, a, s), "gemm_generic");
+}
+
+static int run_gemv(GemvArgs& a, hipStream_t s) {
+  const int cfg = resolve_gemv(a.M, a.N, a.K);
+  const int64_t pf = gemv_partial_floats(cfg, a.M, a.N);
+  if (pf > 0) {
+    float* part;
+    int rc = ws_partials(s, (size_t)pf * sizeof(float), &part);
+    if (rc) return rc;
+    unsigned* ctr;
+    rc = ws_counters(s, (size_t)gemv_counter_count(cfg, a.N), &ctr);
+    if (rc) return rc;
+    a.partial = part;
+    a.counters = ctr;
+  }
+  return map_internal(launch_gemv_w8a16(cfg, a, s), "gemv_w8a16");
+}
+
+// ---------------------------------------------------------------------------
+// Library state
+// ---------------------------------------------------------------------------
+extern "C" int hx_init(void) {
+  int dev;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  hipDeviceProp_t prop;
+  HX_HIP_TRY(hipGetDeviceProperties(&prop, dev));
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(HX_ERR_UNSUPPORTED, "device %d is %s; libhxmi is built for gfx950 only", dev,
+                prop.gcnArchName);
+  return HX_OK;
+}
+
+extern "C" const char* hx_last_error(void) { return g_err.c_str(); }
+extern "C" const char* hx_build_id(void) { return HX_BUILD_ID; }
+
+// ---------------------------------------------------------------------------
+// Matmul family
+// ---------------------------------------------------------------------------
+
+// Bring B into the kernels' K-contiguous [N][K] form.  Returns the pointer
+// and leading dimension to use; KN operands are transposed into `dst`.
+static void* b_as_nk(const View2& b, int layout, size_t es, void* dst, int64_t* ld, hipStream_t s,
+                     int* rc) {
+  *rc = HX_OK;
+  if (layout == HX_LAYOUT_NK) {
+    *ld = b.ld;
+    return b.p;
+  }
+  // b is [K][N] -> dst [N][K]
+  int r = launch_transpose(b.p, b.ld, dst, b.rows, b.rows, b.cols, (int)es, s);
+  *rc = map_internal(r, "transpose");
+  *ld = b.rows;
+  return dst;
+}
+
+static int scale_f32(const hx_memref1d* sc, int sdt, int64_t n, const char* name, float* dst,
+                     const float** out, hipStream_t s) {
+  *out = nullptr;
+  if (!sc) return HX_OK;
+  View1 v;
+  int rc = view1(sc, sdt, name, n, &v);
+  if (rc) return rc;
+  if (sdt == HX_F32) {
+    *out = (const float*)v.p;
+    return HX_OK;
+  }
+  if (sdt != HX_F16) return fail(HX_ERR_DTYPE, "%s: scale dtype %s (f16 or f32)", name, dt_name(sdt));
+  rc = map_internal(launch_f16_to_f32(v.p, dst, n, s), "scale widen");
+  *out = dst;
+  return rc;
+}
+
+extern "C" int hx_matmul(const hx_memref2d* a, int a_dtype, const hx_memref2d* b, int b_dtype,
+                         int b_layout, const hx_memref1d* col_scale, int scale_dtype,
+                         const hx_memref2d* residual, int residual_dtype, hx_memref2d* c,
+                         int c_dtype, hx_stream_t stream) {
+  hipStream_t s = (hipStream_t)stream;
+  int op;
+  if (a_dtype == HX_F16 && b_dtype == HX_F16) op = HX_OP_MATMUL_F16;
+  else if (a_dtype == HX_BF16 && b_dtype == HX_BF16) op = HX_OP_MATMUL_BF16;
+  else if (a_dtype == HX_F16 && b_dtype == HX_I8) op = HX_OP_MATMUL_W8;
+  else return fail(HX_ERR_DTYPE, "hx_matmul: a=%s b=%s (f16.f16, bf16.bf16 or f16.i8)",
+                   dt_name(a_dtype), dt_name(b_dtype));
+  if (c_dtype != HX_F16 && c_dtype != HX_BF16 && c_dtype != HX_F32)
+    return fail(HX_ERR_DTYPE, "hx_matmul: c dtype %s", dt_name(c_dtype));
+  if (b_layout != HX_LAYOUT_KN && b_layout != HX_LAYOUT_NK) return fail(HX_ERR_ARG, "hx_matmul: b_layout");
+  View2 va, vb, vc, vr{};
+  int rc;
+  if ((rc = view2(a, a_dtype, "a", &va))) return rc;
+  if ((rc = view2(b, b_dtype, "b", &vb))) return rc;
+  if ((rc = view2(c, c_dtype, "c", &vc))) return rc;
+  const int64_t M = va.rows, K = va.cols;
+  const int64_t N = b_layout == HX_LAYOUT_KN ? vb.cols : vb.rows;
+  const int64_t Kb = b_layout == HX_LAYOUT_KN ? vb.rows : vb.cols;
+  if (Kb != K) return fail(HX_ERR_SHAPE, "hx_matmul: a is [%lld,%lld] but b has K=%lld", (long long)M, (long long)K, (long long)Kb);
+  if (vc.rows != M || vc.cols != N)
+    return fail(HX_ERR_SHAPE, "hx_matmul: c is [%lld,%lld], expected [%lld,%lld]", (long long)vc.rows,
+                (long long)vc.cols, (long long)M, (long long)N);
+  if (residual) {
+    if (residual_dtype != HX_F16 && residual_dtype != HX_BF16 && residual_dtype != HX_F32)
+      return fail(HX_ERR_DTYPE, "hx_matmul: residual dtype %s", dt_name(residual_dtype));
+    if ((rc = view2(residual, residual_dtype, "residual", &vr))) return rc;
+    if (vr.rows != M || vr.cols != N) return fail(HX_ERR_SHAPE, "hx_matmul: residual shape");
+  }
+  if (M == 0 || N == 0) return HX_OK;
+
+  const size_t eb = dt_size(b_dtype);
+  Carver cv;
+  const size_t off_bt = b_layout == HX_LAYOUT_KN ? cv.take((size_t)N * K * eb) : 0;
+  const size_t off_sc = (col_scale && scale_dtype == HX_F16) ? cv.take((size_t)N * 4) : 0;
+  char* ws = nullptr;
+  if (cv.used && (rc = ws_get(s, cv.used, &ws))) return rc;
+
+  GemmArgs g{};
+  g.a = va.p; g.lda = va.ld;
+  g.b = b_as_nk(vb, b_layout, eb, ws + off_bt, &g.ldb, s, &rc);
+  if (rc) return rc;
+  g.c = vc.p; g.ldc = vc.ld;
+  g.M = M; g.N = N; g.K = K;
+  g.out_dtype = c_dtype;
+  if ((rc = scale_f32(col_scale, scale_dtype, N, "col_scale", (float*)(ws + off_sc), &g.col_scale, s)))
+    return rc;
+  if (residual) { g.res = vr.p; g.ldr = vr.ld; g.res_dtype = residual_dtype; }
+
+  if (op == HX_OP_MATMUL_W8 && M <= 16 && !residual && c_dtype == HX_F16) {
+    GemvArgs v{};
+    v.x = g.a; v.ldx = g.lda; v.w = (const int8_t*)g.b; v.ldw = g.ldb;
+    v.scale = g.col_scale; v.y = g.c; v.ldy = g.ldc; v.M = M; v.N = N; v.K = K;
+    if (gemv_fast_ok(v)) return run_gemv(v, s);
+  }
+  return run_gemm(op, g, s);
+}
+
+extern "C" int hx_gemm_i8(const hx_memref2d* a, const hx_memref2d* b, int b_layout,
+                          const hx_memref1d* row_scale, const hx_memref1d* col_scale,
+                          hx_memref2d* c, int c_dtype, hx_stream_t stream) {
+  hipStream_t s = (hipStream_t)stream;
+  if (c_dtype != HX_I32 && c_dtype != HX_F16 && c_dtype != HX_BF16 && c_dtype != HX_F32)
+    return fail(HX_ERR_DTYPE, "hx_gemm_i8: c dtype %s", dt_name(c_dtype));
+  if (b_layout != HX_LAYOUT_KN && b_layout != HX_LAYOUT_NK) return fail(HX_ERR_ARG, "hx_gemm_i8: b_layout");
+  View2 va, vb, vc;
+  int rc;
+  if ((rc = view2(a, HX_I8, "a", &va))) return rc;
+  if ((rc = view2(b, HX_I8, "b", &vb))) return rc;
+  if ((rc = view2(c, c_dtype, "c", &vc))) return rc;
+  const int64_t M = va.rows, K = va.cols;
+  const int64_t N = b_layout == HX_LAYOUT_KN ? vb.cols : vb.rows;
+  const int64_t Kb = b_layout == HX_LAYOUT_KN ? vb.rows : vb.cols;
+  if (Kb != K) return fail(HX_ERR_SHAPE, "hx_gemm_i8: K mismatch %lld vs %lld", (long long)K, (long long)Kb);
+  if (vc.rows != M || vc.cols != N) return fail(HX_ERR_SHAPE, "hx_gemm_i8: c shape");
+  if (c_dtype == HX_I32 && (row_scale || col_scale))
+    return fail(HX_ERR_ARG, "hx_gemm_i8: scales apply only to a floating output");
+  View1 vrs{}, vcs{};
+  if (row_scale && (rc = view1(row_scale, HX_F32, "row_scale", M, &vrs))) return rc;
+  if (col_scale && (rc = view1(col_scale, HX_F32, "col_scale", N, &vcs))) return rc;
+  if (M == 0 || N == 0) return HX_OK;
+
+  Carver cv;
+  const size_t off_bt = b_layout == HX_LAYOUT_KN ? cv.take((size_t)N * K) : 0;
+  char* ws = nullptr;
+  if (cv.used && (rc = ws_get(s, cv.used, &ws))) return rc;
+  GemmArgs g{};
+  g.a = va.p; g.lda = va.ld;
+  g.b = b_as_nk(vb, b_layout, 1, ws + off_bt, &g.ldb, s, &rc);
+  if (rc) return rc;
+  g.c = vc.p; g.ldc = vc.ld;
+  g.M = M; g.N = N; g.K = K;
+  g.out_dtype = c_dtype;
+  g.row_scale = row_scale ? (const float*)vrs.p : nullptr;
+  g.col_scale = col_scale ? (const float*)vcs.p : nullptr;
+  return run_gemm(HX_OP_GEMM_I8, g, s);
+}
+
+extern "C" int hx_gemv_w8a16(const hx_memref2d* x, const hx_memref2d* w, int w_layout,
+                             const hx_memref1d* scale, int scale_dtype, hx_memref2d* y,
+                             hx_stream_t stream) {
+  return hx_matmul(x, HX_F16, w, HX_I8, w_layout, scale, scale_dtype, nullptr, 0, y, HX_F16, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Row reductions
+// ---------------------------------------------------------------------------
+static int row_dtype_ok(int dt, const char* who) {
+  if (dt != HX_F16 && dt != HX_BF16 && dt != HX_F32)
+    return fail(HX_ERR_DTYPE, "%s: dtype %s (f16, bf16 or f32)", who, dt_name(dt));
+  return HX_OK;
+}
+
+extern "C" int hx_softmax(const hx_memref2d* x, hx_memref2d* y, int dtype, hx_stream_t stream) {
+  int rc;
+  if ((rc = row_dtype_ok(dtype, "hx_softmax"))) return rc;
+  View2 vx, vy;
+  if ((rc = view2(x, dtype, "x", &vx)) || (rc = view2(y, dtype, "y", &vy))) return rc;
+  if (vx.rows != vy.rows || vx.cols != vy.cols) return fail(HX_ERR_SHAPE, "hx_softmax: x/y shape");
+  if (vx.rows == 0 || vx.cols == 0) return HX_OK;
+  return map_internal(launch_softmax(dtype, vx.p, vx.ld, vy.p, vy.ld, vx.rows, vx.cols, (hipStream_t)stream),
+                      "softmax");
+}
+
+extern "C" int hx_rmsnorm(const hx_memref2d* x, const hx_memref1d* gamma, float eps, hx_memref2d* y,
+                          int dtype, hx_stream_t stream) {
+  int rc;
+  if ((rc = row_dtype_ok(dtype, "hx_rmsnorm"))) return rc;
+  View2 vx, vy;
+  View1 vg{};
+  if ((rc = view2(x, dtype, "x", &vx)) || (rc = view2(y, dtype, "y", &vy))) return rc;
+  if (vx.rows != vy.rows || vx.cols != vy.cols) return fail(HX_ERR_SHAPE, "hx_rmsnorm: x/y shape");
+  if (gamma && (rc = view1(gamma, dtype, "gamma", vx.cols, &vg))) return rc;
+  if (vx.rows == 0 || vx.cols == 0) return HX_OK;
+  return map_internal(launch_rmsnorm(dtype, vx.p, vx.ld, gamma ? vg.p : nullptr, eps, vy.p, vy.ld,
+                                     vx.rows, vx.cols, (hipStream_t)stream),
+                      "rmsnorm");
+}
+
+extern "C" int hx_layernorm(const hx_memref2d* x, const hx_memref1d* w, const hx_memref1d* b, float eps,
+                            hx_memref2d* y, hx_memref1d* mean, hx_memref1d* rstd, int dtype,
+                            hx_stream_t stream) {
+  int rc;
+  if ((rc = row_dtype_ok(dtype, "hx_layernorm"))) return rc;
+  View2 vx, vy;
+  View1 vw{}, vb{}, vm{}, vr{};
+  if ((rc = view2(x, dtype, "x", &vx)) || (rc = view2(y, dtype, "y", &vy))) return rc;
+  if (vx.rows != vy.rows || vx.cols != vy.cols) return fail(HX_ERR_SHAPE, "hx_layernorm: x/y shape");
+  if (w && (rc = view1(w, dtype, "w", vx.cols, &vw))) return rc;
+  if (b && (rc = view1(b, dtype, "b", vx.cols, &vb))) return rc;
+  if (mean && (rc = view1(mean, HX_F32, "mean", vx.rows, &vm))) return rc;
+  if (rstd && (rc = view1(rstd, HX_F32, "rstd", vx.rows, &vr))) return rc;
+  if (vx.rows == 0 || vx.cols == 0) return HX_OK;
+  return map_internal(launch_layernorm(dtype, vx.p, vx.ld, w ? vw.p : nullptr, b ? vb.p : nullptr, eps,
+                                       vy.p, vy.ld, mean ? (float*)vm.p : nullptr,
+                                       rstd ? (float*)vr.p : nullptr, vx.rows, vx.cols,
+                                       (hipStream_t)stream),
+                      "layernorm");
+}
+
+extern "C" int hx_silu_mul(const hx_memref2d* g, const hx_memref2d* u, hx_memref2d* out, int dtype,
+                           hx_stream_t stream) {
+  if (dtype != HX_F16) return fail(HX_ERR_DTYPE, "hx_silu_mul: f16 only");
+  int rc;
+  View2 vg, vu, vo;
+  if ((rc = view2(g, dtype, "g", &vg)) || (rc = view2(u, dtype, "u", &vu)) || (rc = view2(out, dtype, "out", &vo)))
+    return rc;
+  if (vg.rows != vu.rows || vg.cols != vu.cols || vg.rows != vo.rows || vg.cols != vo.cols)
+    return fail(HX_ERR_SHAPE, "hx_silu_mul: shapes differ");
+  if (vg.rows == 0 || vg.cols == 0) return HX_OK;
+  return map_internal(launch_silu_mul_f16(vg.p, vg.ld, vu.p, vu.ld, vo.p, vo.ld, vg.rows, vg.cols,
+                                          (hipStream_t)stream),
+                      "silu_mul");
+}
+
+// ---------------------------------------------------------------------------
+// Resident weights
+// ---------------------------------------------------------------------------
+struct hx_weight {
+  int device;
+  int64_t K, N;
+  int dtype;
+  void* image;    // [N][K], K-contiguous
+  float* scale;   // [N] or null
+  uint64_t hash;
+  int refcount;
+};
+static std::set<hx_weight*> g_weights;
+
+extern "C" int hx_weight_register(const hx_memref2d* w, int w_dtype, int w_layout,
+                                  const hx_memref1d* scale, int scale_dtype, hx_stream_t stream,
+                                  hx_weight_t* out) {
+  hipStream_t s = (hipStream_t)stream;
+  if (!out) return fail(HX_ERR_ARG, "hx_weight_register: null out");
+  *out = nullptr;
+  if (w_dtype != HX_I8 && w_dtype != HX_F16 && w_dtype != HX_BF16)
+    return fail(HX_ERR_DTYPE, "hx_weight_register: dtype %s", dt_name(w_dtype));
+  if (w_layout != HX_LAYOUT_KN && w_layout != HX_LAYOUT_NK) return fail(HX_ERR_ARG, "hx_weight_register: layout");
+  if (w_dtype == HX_I8 && !scale) return fail(HX_ERR_ARG, "hx_weight_register: int8 weights need scales");
+  int dev, rc;
+  if ((rc = current_device(&dev))) return rc;
+  View2 vw;
+  if ((rc = view2(w, w_dtype, "w", &vw))) return rc;
+  const int64_t K = w_layout == HX_LAYOUT_KN ? vw.rows : vw.cols;
+  const int64_t N = w_layout == HX_LAYOUT_KN ? vw.cols : vw.rows;
+  if (K <= 0 || N <= 0) return fail(HX_ERR_SHAPE, "hx_weight_register: empty weight");
+  View1 vs{};
+  if (scale && (rc = view1(scale, scale_dtype, "scale", N, &vs))) return rc;
+  if (scale && scale_dtype != HX_F16 && scale_dtype != HX_F32)
+    return fail(HX_ERR_DTYPE, "hx_weight_register: scale dtype %s", dt_name(scale_dtype));
+
+  const size_t es = dt_size(w_dtype);
+  void* image = nullptr;
+  float* sc = nullptr;
+  uint64_t* hdev = nullptr;
+  auto cleanup = [&]() {
+    if (image) (void)hipFree(image);
+    if (sc) (void)hipFree(sc);
+    if (hdev) (void)hipFree(hdev);
+  };
+  if (hipMalloc(&image, (size_t)N * K * es) != hipSuccess) { cleanup(); return fail(HX_ERR_NOMEM, "weight image"); }
+  if (scale && hipMalloc((void**)&sc, (size_t)N * 4) != hipSuccess) { cleanup(); return fail(HX_ERR_NOMEM, "weight scale"); }
+  if (hipMalloc((void**)&hdev, 16) != hipSuccess) { cleanup(); return fail(HX_ERR_NOMEM, "hash"); }
+  hipError_t e;
+  if (w_layout == HX_LAYOUT_KN) {
+    rc = map_internal(launch_transpose(vw.p, vw.ld, image, K, K, N, (int)es, s), "transpose");
+  } else {
+    e = hipMemcpy2DAsync(image, K * es, vw.p, vw.ld * es, K * es, N, hipMemcpyDeviceToDevice, s);
+    rc = e == hipSuccess ? HX_OK : fail(HX_ERR_HIP, "weight copy: %s", hipGetErrorString(e));
+  }
+  if (!rc && scale) {
+    if (scale_dtype == HX_F16) rc = map_internal(launch_f16_to_f32(vs.p, sc, N, s), "scale widen");
+    else {
+      e = hipMemcpyAsync(sc, vs.p, (size_t)N * 4, hipMemcpyDeviceToDevice, s);
+      rc = e == hipSuccess ? HX_OK : fail(HX_ERR_HIP, "scale copy: %s", hipGetErrorString(e));
+    }
+  }
+  uint64_t h[2] = {0, 0};
+  if (!rc) {
+    e = hipMemsetAsync(hdev, 0, 16, s);
+    if (e != hipSuccess) rc = fail(HX_ERR_HIP, "hash clear: %s", hipGetErrorString(e));
+  }
+  if (!rc) rc = map_internal(launch_hash64(image, N * K * (int64_t)es, hdev, s), "hash");
+  if (!rc && scale) rc = map_internal(launch_hash64(sc, N * 4, hdev + 1, s), "hash");
+  if (!rc) {
+    e = hipMemcpyAsync(h, hdev, 16, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) rc = fail(HX_ERR_HIP, "hash readback: %s", hipGetErrorString(e));
+  }
+  (void)hipFree(hdev);
+  hdev = nullptr;
+  if (rc) { cleanup(); return rc; }
+  uint64_t key = h[0] ^ (h[1] * 0x9e3779b97f4a7c15ull) ^ ((uint64_t)K << 40) ^ ((uint64_t)N << 8) ^
+                 (uint64_t)w_dtype ^ (scale ? 0x5ca1e5ull : 0);
+
+  std::lock_guard<std::mutex> lk(g_mu);
+  for (hx_weight* x : g_weights) {
+    if (x->device == dev && x->hash == key && x->K == K && x->N == N && x->dtype == w_dtype &&
+        (x->scale != nullptr) == (scale != nullptr)) {
+      ++x->refcount;
+      cleanup();
+      *out = x;
+      return HX_OK;
+    }
+  }
+  hx_weight* x = new hx_weight{dev, K, N, w_dtype, image, sc, key, 1};
+  g_weights.insert(x);
+  *out = x;
+  return HX_OK;
+}
+
+static hx_weight* lookup(hx_weight_t w) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  return g_weights.count(w) ? w : nullptr;
+}
+
+extern "C" int hx_weight_release(hx_weight_t w) {
+  hx_weight* x = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!g_weights.count(w)) return fail(HX_ERR_HANDLE, "hx_weight_release: unknown handle");
+    if (--w->refcount > 0) return HX_OK;
+    g_weights.erase(w);
+    x = w;
+  }
+  int cur = 0;
+  (void)hipGetDevice(&cur);
+  (void)hipSetDevice(x->device);
+  (void)hipDeviceSynchronize();  // no kernel may still read the image
+  (void)hipFree(x->image);
+  if (x->scale) (void)hipFree(x->scale);
+  (void)hipSetDevice(cur);
+  delete x;
+  return HX_OK;
+}
+
+extern "C" int hx_weight_info(hx_weight_t w, int64_t* k, int64_t* n, int* dtype, uint64_t* content_hash,
+                              int* refcount) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!g_weights.count(w)) return fail(HX_ERR_HANDLE, "hx_weight_info: unknown handle");
+  if (k) *k = w->K;
+  if (n) *n = w->N;
+  if (dtype) *dtype = w->dtype;
+  if (content_hash) *content_hash = w->hash;
+  if (refcount) *refcount = w->refcount;
+  return HX_OK;
+}
+
+static int matmul_resident_impl(const View2& vx, hx_weight* w, const View2* vr, int r_dt,
+                                const View2& vy, int y_dt, hipStream_t s) {
+  const int64_t M = vx.rows;
+  if (M == 0) return HX_OK;
+  if (w->dtype == HX_I8 && M <= 16 && !vr && y_dt == HX_F16) {
+    GemvArgs v{};
+    v.x = vx.p; v.ldx = vx.ld; v.w = (const int8_t*)w->image; v.ldw = w->K;
+    v.scale = w->scale; v.y = vy.p; v.ldy = vy.ld; v.M = M; v.N = w->N; v.K = w->K;
+    if (gemv_fast_ok(v)) return run_gemv(v, s);
+  }
+  GemmArgs g{};
+  g.a = vx.p; g.lda = vx.ld;
+  g.b = w->image; g.ldb = w->K;
+  g.c = vy.p; g.ldc = vy.ld;
+  g.M = M; g.N = w->N; g.K = w->K;
+  g.out_dtype = y_dt;
+  g.col_scale = w->scale;
+  if (vr) { g.res = vr->p; g.ldr = vr->ld; g.res_dtype = r_dt; }
+  const int op = w->dtype == HX_I8 ? HX_OP_MATMUL_W8 : w->dtype == HX_F16 ? HX_OP_MATMUL_F16 : HX_OP_MATMUL_BF16;
+  return run_gemm(op, g, s);
+}
+
+extern "C" int hx_matmul_resident(const hx_memref2d* x, int x_dtype, hx_weight_t wt,
+                                  const hx_memref2d* residual, int residual_dtype, hx_memref2d* y,
+                                  int y_dtype, hx_stream_t stream) {
+  hx_weight* w = lookup(wt);
+  if (!w) return fail(HX_ERR_HANDLE, "hx_matmul_resident: unknown weight handle");
+  const int want_x = w->dtype == HX_BF16 ? HX_BF16 : HX_F16;
+  if (x_dtype != want_x)
+    return fail(HX_ERR_DTYPE, "hx_matmul_resident: x is %s, weight %s needs %s", dt_name(x_dtype),
+                dt_name(w->dtype), dt_name(want_x));
+  if (y_dtype != HX_F16 && y_dtype != HX_BF16 && y_dtype != HX_F32)
+    return fail(HX_ERR_DTYPE, "hx_matmul_resident: y dtype %s", dt_name(y_dtype));
+  int rc, dev;
+  if ((rc = current_device(&dev))) return rc;
+  if (dev != w->device) return fail(HX_ERR_HANDLE, "hx_matmul_resident: weight lives on device %d", w->device);
+  View2 vx, vy, vr;
+  if ((rc = view2(x, x_dtype, "x", &vx)) || (rc = view2(y, y_dtype, "y", &vy))) return rc;
+  if (vx.cols != w->K) return fail(HX_ERR_SHAPE, "hx_matmul_resident: x has K=%lld, weight K=%lld", (long long)vx.cols, (long long)w->K);
+  if (vy.rows != vx.rows || vy.cols != w->N) return fail(HX_ERR_SHAPE, "hx_matmul_resident: y shape");
+  if (residual) {
+    if (residual_dtype != HX_F16 && residual_dtype != HX_BF16 && residual_dtype != HX_F32)
+      return fail(HX_ERR_DTYPE, "hx_matmul_resident: residual dtype");
+    if ((rc = view2(residual, residual_dtype, "residual", &vr))) return rc;
+    if (vr.rows != vx.rows || vr.cols != w->N) return fail(HX_ERR_SHAPE, "hx_matmul_resident: residual shape");
+  }
+  return matmul_resident_impl(vx, w, residual ? &vr : nullptr, residual_dtype, vy, y_dtype,
+                              (hipStream_t)stream);
+}
+
+extern "C" int hx_swiglu_ffn(const hx_memref2d* x, const hx_memref1d* gamma, float eps, hx_weight_t w_gate,
+                             hx_weight_t w_up, hx_weight_t w_down, hx_memref2d* y, hx_stream_t stream) {
+  hipStream_t s = (hipStream_t)stream;
+  hx_weight *wg = lookup(w_gate), *wu = lookup(w_up), *wd = lookup(w_down);
+  if (!wg || !wu || !wd) return fail(HX_ERR_HANDLE, "hx_swiglu_ffn: unknown weight handle");
+  if (wg->dtype != HX_I8 || wu->dtype != HX_I8 || wd->dtype != HX_I8)
+    return fail(HX_ERR_DTYPE, "hx_swiglu_ffn: int8 weights expected");
+  int rc, dev;
+  if ((rc = current_device(&dev))) return rc;
+  if (wg->device != dev || wu->device != dev || wd->device != dev)
+    return fail(HX_ERR_HANDLE, "hx_swiglu_ffn: weights live on another device");
+  View2 vx, vy;
+  View1 vg{};
+  if ((rc = view2(x, HX_F16, "x", &vx)) || (rc = view2(y, HX_F16, "y", &vy))) return rc;
+  const int64_t T = vx.rows, H = vx.cols, I = wg->N;
+  if (wg->K != H || wu->K != H || wu->N != I || wd->K != I || wd->N != H)
+    return fail(HX_ERR_SHAPE, "hx_swiglu_ffn: weights [%lld,%lld] [%lld,%lld] [%lld,%lld] vs hidden %lld",
+                (long long)wg->K, (long long)wg->N, (long long)wu->K, (long long)wu->N, (long long)wd->K,
+                (long long)wd->N, (long long)H);
+  if (vy.rows != T || vy.cols != H) return fail(HX_ERR_SHAPE, "hx_swiglu_ffn: y shape");
+  if (gamma && (rc = view1(gamma, HX_F16, "gamma", H, &vg))) return rc;
+  if (T == 0) return HX_OK;
+
+  const bool skinny = T <= 16;
+  Carver cv;
+  const size_t off_h = cv.take((size_t)T * H * 2);
+  const size_t off_a = cv.take((size_t)T * I * 2);
+  const size_t off_g = skinny ? cv.take((size_t)T * I * 2) : 0;
+  const size_t off_u = skinny ? cv.take((size_t)T * I * 2) : 0;
+  char* ws;
+  if ((rc = ws_get(s, cv.used, &ws))) return rc;
+  char* h = ws + off_h;
+  char* act = ws + off_a;
+  rc = map_internal(launch_rmsnorm(HX_F16, vx.p, vx.ld, gamma ? vg.p : nullptr, eps, h, H, T, H, s), "rmsnorm");
+  if (rc) return rc;
+  View2 vh{h, T, H, H}, va{act, T, I, I};
+  if (skinny) {
+    View2 vgo{ws + off_g, T, I, I}, vuo{ws + off_u, T, I, I};
+    if ((rc = matmul_resident_impl(vh, wg, nullptr, 0, vgo, HX_F16, s))) return rc;
+    if ((rc = matmul_resident_impl(vh, wu, nullptr, 0, vuo, HX_F16, s))) return rc;
+    rc = map_internal(launch_silu_mul_f16(vgo.p, I, vuo.p, I, act, I, T, I, s), "silu_mul");
+    if (rc) return rc;
+  } else {
+    GemmArgs g{};
+    g.a = h; g.lda = H;
+    g.b = wg->image; g.b2 = wu->image; g.ldb = H;
+    g.c = act; g.ldc = I;
+    g.M = T; g.N = I; g.K = H;
+    g.out_dtype = HX_F16;
+    g.col_scale = wg->scale; g.col_scale2 = wu->scale;
+    if ((rc = run_gemm(HX_OP_SWIGLU_W8, g, s))) return rc;
+  }
+  return matmul_resident_impl(va, wd, nullptr, 0, vy, HX_F16, s);
+}
+
+// ---------------------------------------------------------------------------
+// Configurations
+// ---------------------------------------------------------------------------
+extern "C" int hx_config_count(int op) {
+  std::vector<int> idx = family_indices(op);
+  if (idx.empty()) return fail(HX_ERR_ARG, "hx_config_count: unknown op %d", op);
+  return (int)idx.size();
+}
+
+extern "C" int hx_config_get(int op, int index, hx_kernel_config* out) {
+  if (!out) return fail(HX_ERR_ARG, "hx_config_get: null out");
+  std::vector<int> idx = family_indices(op);
+  if (idx.empty()) return fail(HX_ERR_ARG, "hx_config_get: unknown op %d", op);
+  if (index < 0 || index >= (int)idx.size()) return fail(HX_ERR_ARG, "hx_config_get: index %d", index);
+  memset(out, 0, sizeof(*out));
+  out->op = op;
+  out->index = index;
+  if (op == HX_OP_GEMV_W8) {
+    const GemvConfig* c = gemv_config(idx[index]);
+    out->bm = 16; out->bn = 16 * c->ct; out->bk = 128;
+    out->waves_m = 1; out->waves_n = 4;
+    out->lds_stages = 0; out->split_k = c->ks; out->col_tiles = c->ct;
+    out->lds_bytes = 4 * c->ct * 64 * 4 * 4 + 4;
+    snprintf(out->name, sizeof(out->name), "gemv_%s", c->name);
+    return HX_OK;
+  }
+  int mode, epi;
+  op_gemm(op, &mode, &epi);
+  const GemmConfig* c = gemm_config(mode, idx[index]);
+  const int bk = mode == GM_I8 ? 128 : 64;
+  const int brow = mode == GM_F16 || mode == GM_BF16 || mode == GM_I8 ? 128 : 64;
+  out->bm = c->bm; out->bn = c->bn; out->bk = bk;
+  out->waves_m = c->wm; out->waves_n = c->wn;
+  out->lds_stages = 2; out->split_k = 1; out->col_tiles = 0;
+  out->lds_bytes = 2 * (c->bm * 128 + (epi == GE_SWIGLU ? 2 : 1) * c->bn * brow);
+  snprintf(out->name, sizeof(out->name), "%s", c->name);
+  return HX_OK;
+}
+
+extern "C" int hx_config_select(int op, int64_t m, int64_t n, int64_t k, int index) {
+  std::vector<int> idx = family_indices(op);
+  if (idx.empty()) return fail(HX_ERR_ARG, "hx_config_select: unknown op %d", op);
+  if (index < -1 || index >= (int)idx.size()) return fail(HX_ERR_ARG, "hx_config_select: index %d", index);
+  int dev;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto key = std::make_tuple(dev, op, m, n, k);
+  if (index < 0) g_pins.erase(key);
+  else g_pins[key] = index;
+  return HX_OK;
+}
+
+extern "C" int hx_config_lookup(int op, int64_t m, int64_t n, int64_t k, int* index) {
+  if (!index) return fail(HX_ERR_ARG, "hx_config_lookup: null out");
+  std::vector<int> idx = family_indices(op);
+  if (idx.empty()) return fail(HX_ERR_ARG, "hx_config_lookup: unknown op %d", op);
+  int dev;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  if (op == HX_OP_GEMV_W8) {
+    *index = resolve_gemv(m, n, k);
+    return HX_OK;
+  }
+  const int t = resolve_gemm(op, m, n, k);
+  *index = -1;
+  for (size_t i = 0; i < idx.size(); ++i)
+    if (idx[i] == t) *index = (int)i;
+  return HX_OK;
+}

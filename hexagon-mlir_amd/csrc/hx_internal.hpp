@@ -1,0 +1,101 @@
+// hx_internal.hpp -- host-side declarations shared by the kernel translation
+// units and the C ABI layer (hx_api.cpp).  Nothing here is exported.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hx {
+
+enum : int {
+  HXI_OK = 0,
+  HXI_ERR_ARG = -1,
+  HXI_ERR_SHAPE = -2,
+  HXI_ERR_DTYPE = -3,
+  HXI_ERR_LAYOUT = -4,
+  HXI_ERR_HIP = -5,
+  HXI_ERR_NOMEM = -6,
+  HXI_ERR_UNSUPPORTED = -7,
+};
+
+// ---- row kernels (hx_rows.hip) -------------------------------------------
+int launch_softmax(int dtype, const void* x, int64_t ldx, void* y, int64_t ldy,
+                   int64_t rows, int64_t cols, hipStream_t s);
+int launch_rmsnorm(int dtype, const void* x, int64_t ldx, const void* gamma, float eps,
+                   void* y, int64_t ldy, int64_t rows, int64_t cols, hipStream_t s);
+int launch_layernorm(int dtype, const void* x, int64_t ldx, const void* w, const void* b,
+                     float eps, void* y, int64_t ldy, float* mean, float* rstd,
+                     int64_t rows, int64_t cols, hipStream_t s);
+int launch_silu_mul_f16(const void* g, int64_t ldg, const void* u, int64_t ldu, void* o,
+                        int64_t ldo, int64_t rows, int64_t cols, hipStream_t s);
+
+// ---- MFMA GEMM (hx_gemm.hip) ---------------------------------------------
+// Operand modes.  B is always consumed K-contiguous ([N][K], "NK").
+enum GemmMode : int {
+  GM_I8 = 0,    // int8 x int8 -> int32      (v_mfma_i32_32x32x32_i8)
+  GM_F16 = 1,   // f16 x f16 -> f32          (v_mfma_f32_32x32x16_f16)
+  GM_BF16 = 2,  // bf16 x bf16 -> f32        (v_mfma_f32_32x32x16_bf16)
+  GM_W8 = 3,    // f16 x int8 -> f32, int8 widened to f16 in registers
+  GM_COUNT = 4,
+};
+
+enum GemmEpi : int { GE_STORE = 0, GE_SWIGLU = 1 };
+
+struct GemmArgs {
+  const void* a; int64_t lda;   // [M][K], elements
+  const void* b; int64_t ldb;   // [N][K], elements
+  const void* b2;               // second weight for GE_SWIGLU (same ldb)
+  void* c; int64_t ldc;         // [M][N]
+  int64_t M, N, K;
+  int out_dtype;                // DT_I32 / DT_F16 / DT_BF16 / DT_F32
+  const float* row_scale;       // [M] (int8 dequant), may be null
+  const float* col_scale;       // [N], may be null
+  const float* col_scale2;      // [N] scale of b2 (GE_SWIGLU)
+  const void* res; int64_t ldr; int res_dtype;  // residual, may be null
+};
+
+struct GemmConfig {
+  int bm, bn, wm, wn;   // block tile and wave grid
+  int epi;              // GemmEpi
+  const char* name;
+};
+
+int gemm_config_count(int mode);
+const GemmConfig* gemm_config(int mode, int idx);
+// Default (untuned) config index for a shape.
+int gemm_default_config(int mode, int epi, int64_t M, int64_t N, int64_t K);
+// True when the fast kernel's alignment preconditions hold for these args.
+bool gemm_fast_ok(int mode, const GemmArgs& a);
+int launch_gemm(int mode, int cfg_idx, const GemmArgs& a, hipStream_t s);
+// Any shape / alignment; simple tiled kernel, same arithmetic contract.
+int launch_gemm_generic(int mode, const GemmArgs& a, hipStream_t s);
+
+// ---- W8A16 skinny GEMM / GEMV (hx_gemv.hip) ------------------------------
+struct GemvArgs {
+  const void* x; int64_t ldx;   // f16 [M][K]
+  const int8_t* w; int64_t ldw; // int8 [N][K]
+  const float* scale;           // [N], may be null (scale 1)
+  void* y; int64_t ldy;         // f16 [M][N]
+  int64_t M, N, K;
+  float* partial;               // [ks][M][N] workspace when ks > 1
+  unsigned* counters;           // [n_tiles] zeroed, when ks > 1
+};
+struct GemvConfig { int ct, ks; const char* name; };
+int gemv_config_count();
+const GemvConfig* gemv_config(int idx);
+int gemv_default_config(int64_t M, int64_t N, int64_t K);
+int64_t gemv_partial_floats(int cfg_idx, int64_t M, int64_t N);
+int64_t gemv_counter_count(int cfg_idx, int64_t N);
+bool gemv_fast_ok(const GemvArgs& a);
+int launch_gemv_w8a16(int cfg_idx, const GemvArgs& a, hipStream_t s);
+
+// ---- layout utilities (hx_pack.hip) --------------------------------------
+// dst[c][r] = src[r][c] for a rows x cols matrix of 1/2/4-byte elements.
+int launch_transpose(const void* src, int64_t lds, void* dst, int64_t ldd, int64_t rows,
+                     int64_t cols, int elem_bytes, hipStream_t s);
+// f16 -> f32 widening of a vector (scales).
+int launch_f16_to_f32(const void* src, float* dst, int64_t n, hipStream_t s);
+// 64-bit content hash of a byte range (order-dependent, deterministic).
+int launch_hash64(const void* src, int64_t bytes, uint64_t* out_dev, hipStream_t s);
+
+}  // namespace hx

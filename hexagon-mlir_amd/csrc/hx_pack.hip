@@ -1,0 +1,104 @@
+// hx_pack.hip -- layout utilities behind the resident-weight registry and the
+// [K][N] (linalg orientation) operand path:
+//   * transpose [R][C] -> [C][R] for 1/2/4-byte elements (64x64 LDS tiles,
+//     coalesced reads and writes).  This builds the K-contiguous weight image
+//     that the GEMM / GEMV kernels consume -- the role the host-side crouton
+//     pre-pack plays in hexagon-mlir (QHB/backend/hmx_weight_prepack.py:
+//     171-212; QHB/lib/Dialect/Hmx/Transforms/WeightResidentPass.cpp:1-60);
+//   * f16 -> f32 widening of per-channel scales (exact);
+//   * a 64-bit content hash used to key registered weights by content, as
+//     the reference keys its prepack cache (hmx_weight_prepack.py:155-168).
+#include "hx_device.hpp"
+#include "hx_internal.hpp"
+
+namespace hx {
+
+template <typename E>
+__global__ void __launch_bounds__(256) transpose_kernel(const E* __restrict__ src, int64_t lds,
+                                                        E* __restrict__ dst, int64_t ldd,
+                                                        int64_t rows, int64_t cols) {
+  __shared__ E tile[64][65];
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // ty 0..3
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int r = ty + 4 * i;
+    const int64_t gr = r0 + r, gc = c0 + tx;
+    if (gr < rows && gc < cols) tile[r][tx] = src[gr * lds + gc];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int c = ty + 4 * i;  // output row = input column
+    const int64_t gc = c0 + c, gr = r0 + tx;
+    if (gc < cols && gr < rows) dst[gc * ldd + gr] = tile[tx][c];
+  }
+}
+
+int launch_transpose(const void* src, int64_t lds, void* dst, int64_t ldd, int64_t rows,
+                     int64_t cols, int elem_bytes, hipStream_t s) {
+  if (rows <= 0 || cols <= 0) return HXI_OK;
+  const dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
+  switch (elem_bytes) {
+    case 1: transpose_kernel<uint8_t><<<grid, dim3(256), 0, s>>>((const uint8_t*)src, lds, (uint8_t*)dst, ldd, rows, cols); break;
+    case 2: transpose_kernel<uint16_t><<<grid, dim3(256), 0, s>>>((const uint16_t*)src, lds, (uint16_t*)dst, ldd, rows, cols); break;
+    case 4: transpose_kernel<uint32_t><<<grid, dim3(256), 0, s>>>((const uint32_t*)src, lds, (uint32_t*)dst, ldd, rows, cols); break;
+    default: return HXI_ERR_ARG;
+  }
+  return HXI_OK;
+}
+
+__global__ void __launch_bounds__(256) f16_to_f32_kernel(const uint16_t* src, float* dst, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    dst[i] = f16_bits_to_f32(src[i]);
+}
+
+int launch_f16_to_f32(const void* src, float* dst, int64_t n, hipStream_t s) {
+  if (n <= 0) return HXI_OK;
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 1024) blocks = 1024;
+  f16_to_f32_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>((const uint16_t*)src, dst, n);
+  return HXI_OK;
+}
+
+// Content hash: H = sum over 8-byte words i of mix(word_i + (i+1)*phi), plus
+// the tail bytes folded into one last word.  The per-word mix includes the
+// position, so permutations change H; the sum is order-free, so the result
+// does not depend on scheduling.  mix() is the splitmix64 finaliser.
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+__global__ void __launch_bounds__(256) hash64_kernel(const uint8_t* src, int64_t bytes, uint64_t* out) {
+  const int64_t words = bytes / 8;
+  uint64_t h = 0;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < words; i += (int64_t)gridDim.x * 256) {
+    uint64_t w;
+    __builtin_memcpy(&w, src + 8 * i, 8);
+    h += mix64(w + (uint64_t)(i + 1) * 0x9e3779b97f4a7c15ull);
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0 && (bytes & 7)) {
+    uint64_t w = 0;
+    for (int64_t j = 0; j < (bytes & 7); ++j) w |= (uint64_t)src[8 * words + j] << (8 * j);
+    h += mix64(w + (uint64_t)(words + 1) * 0x9e3779b97f4a7c15ull);
+  }
+  // wave then block reduction, one atomic per block
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) h += __shfl_xor(h, o, 64);
+  __shared__ uint64_t part[4];
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = h;
+  __syncthreads();
+  if (threadIdx.x == 0) atomicAdd((unsigned long long*)out, (unsigned long long)(part[0] + part[1] + part[2] + part[3]));
+}
+
+int launch_hash64(const void* src, int64_t bytes, uint64_t* out_dev, hipStream_t s) {
+  int64_t blocks = (bytes / 8 + 255) / 256;
+  if (blocks > 2048) blocks = 2048;
+  if (blocks < 1) blocks = 1;
+  hash64_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>((const uint8_t*)src, bytes, out_dev);
+  return HXI_OK;
+}
+
+}  // namespace hx

@@ -1,0 +1,331 @@
+// hx_rows.hip -- single-pass row reductions over the last dimension:
+// softmax, RMSNorm and LayerNorm, plus the elementwise SiLU*mul of the FFN.
+//
+// Reference semantics (hexagon-mlir paths, QHB = qcom_hexagon_backend):
+//   softmax   docs/tutorials/torch-mlir/softmax.md:178-226,
+//             test/python/triton/test_softmax.py:41-69, DivToMul
+//             (QHB/lib/Transforms/DivToMulOptimizationPass.cpp:9-18)
+//   RMSNorm   test/python/triton/test_rms_norm.py:34-59, FastInverse
+//             (QHB/lib/Transforms/FastInversePass.cpp:97-140)
+//   LayerNorm test/python/triton/test_layer_norm.py:39-79
+// The reference folds each row 128 bytes at a time on HVX and finishes with a
+// log2(lanes) rotate-and-fold (QHB/lib/Conversion/LinalgToLLVM/
+// VectorRowReducePass.cpp:17-28).  Here a row is held in VGPRs by one wave
+// (or by the four waves of a workgroup for long rows): every element is read
+// from HBM once with 16-byte loads and written once, and the reductions are
+// 64-lane butterflies (plus one LDS exchange when four waves share a row).
+// All arithmetic is binary32 with one rounding to the storage type.
+#include "hx_device.hpp"
+#include "hx_internal.hpp"
+
+namespace hx {
+
+enum RowOp : int { ROW_SOFTMAX = 0, ROW_RMSNORM = 1, ROW_LAYERNORM = 2 };
+
+struct RowArgs {
+  const void* x; int64_t ldx;
+  void* y; int64_t ldy;
+  const void* w;   // gamma (RMSNorm) / weight (LayerNorm), may be null
+  const void* b;   // LayerNorm bias, may be null
+  float* mean;     // LayerNorm per-row outputs, may be null
+  float* rstd;
+  float eps;
+  int64_t rows, cols;
+};
+
+// Sum / max across the WPR waves of a workgroup that share one row.
+template <int WPR>
+__device__ __forceinline__ float group_sum(float v, float* red) {
+  v = wave_sum(v);
+  if constexpr (WPR == 1) {
+    return v;
+  } else {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __syncthreads();  // the previous use of `red` is finished everywhere
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < WPR; ++i) s += red[i];
+    return s;
+  }
+}
+template <int WPR>
+__device__ __forceinline__ float group_max(float v, float* red) {
+  v = wave_max(v);
+  if constexpr (WPR == 1) {
+    return v;
+  } else {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float m = red[0];
+#pragma unroll
+    for (int i = 1; i < WPR; ++i) m = fmaxf(m, red[i]);
+    return m;
+  }
+}
+
+// One kernel template for the three ops.
+//   DT   storage dtype (f16 / bf16 / f32)
+//   WPR  waves per row (1: a 256-thread block handles 4 rows; 4: one row)
+//   VPL  16-byte vectors per lane
+//   VEC  true when rows are 16-byte aligned and cols is a multiple of the
+//        vector width, so whole vectors are loaded; false loads element by
+//        element with a mask.
+// Column of element e of vector v in lane l of wave w (of the row's group):
+//   ((v * WPR + w) * 64 + l) * EV + e
+// so every load instruction of a wave covers 1 KiB of contiguous row.
+template <int OP, int DT, int WPR, int VPL, bool VEC>
+__global__ void __launch_bounds__(256) row_kernel(RowArgs a) {
+  typedef typename Elem<DT>::storage S;
+  constexpr int EV = 16 / sizeof(S);
+  constexpr int N = VPL * EV;
+  __shared__ float red[4];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int rows_per_block = 4 / WPR;
+  const int wave_in_row = (WPR == 1) ? 0 : wave;
+  const int64_t row = (int64_t)blockIdx.x * rows_per_block + (WPR == 1 ? wave : 0);
+  if (row >= a.rows) return;  // uniform per wave; WPR==4 blocks have row < rows
+  const int64_t cols = a.cols;
+  const S* xr = reinterpret_cast<const S*>(a.x) + row * a.ldx;
+  S* yr = reinterpret_cast<S*>(a.y) + row * a.ldy;
+
+  float v[N];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int64_t c0 = ((int64_t)(i * WPR + wave_in_row) * 64 + lane) * EV;
+    if constexpr (VEC) {
+      if (c0 < cols) {
+        const v4u raw = *reinterpret_cast<const v4u*>(xr + c0);
+        const S* e = reinterpret_cast<const S*>(&raw);
+#pragma unroll
+        for (int j = 0; j < EV; ++j) v[i * EV + j] = Elem<DT>::load(e[j]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < EV; ++j) v[i * EV + j] = 0.f;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < EV; ++j)
+        v[i * EV + j] = (c0 + j < cols) ? Elem<DT>::load(xr[c0 + j]) : 0.f;
+    }
+  }
+  auto valid = [&](int i, int j) -> bool {
+    return ((int64_t)(i * WPR + wave_in_row) * 64 + lane) * EV + j < cols;
+  };
+
+  float scale = 1.f, shift = 0.f;
+  if constexpr (OP == ROW_SOFTMAX) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+#pragma unroll
+      for (int j = 0; j < EV; ++j)
+        if (valid(i, j)) m = fmaxf(m, v[i * EV + j]);
+    m = group_max<WPR>(m, red);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+#pragma unroll
+      for (int j = 0; j < EV; ++j) {
+        const float e = valid(i, j) ? fast_exp(v[i * EV + j] - m) : 0.f;
+        v[i * EV + j] = e;
+        s += e;
+      }
+    s = group_sum<WPR>(s, red);
+    scale = 1.0f / s;  // DivToMul: one reciprocal, then multiplies
+  } else if constexpr (OP == ROW_RMSNORM) {
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < N; ++k) ss += v[k] * v[k];  // masked lanes hold 0
+    ss = group_sum<WPR>(ss, red);
+    scale = 1.0f / sqrtf(ss / (float)cols + a.eps);
+  } else {
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < N; ++k) s += v[k];
+    s = group_sum<WPR>(s, red);
+    const float mean = s / (float)cols;
+    float vs = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+#pragma unroll
+      for (int j = 0; j < EV; ++j) {
+        const float d = valid(i, j) ? v[i * EV + j] - mean : 0.f;
+        vs += d * d;
+      }
+    vs = group_sum<WPR>(vs, red);
+    scale = 1.0f / sqrtf(vs / (float)cols + a.eps);
+    shift = mean;
+    if (threadIdx.x == (WPR == 1 ? wave * 64 : 0)) {
+      if (a.mean) a.mean[row] = mean;
+      if (a.rstd) a.rstd[row] = scale;
+    }
+  }
+
+  const S* wp = reinterpret_cast<const S*>(a.w);
+  const S* bp = reinterpret_cast<const S*>(a.b);
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int64_t c0 = ((int64_t)(i * WPR + wave_in_row) * 64 + lane) * EV;
+    S out[EV];
+    S wv[EV], bv[EV];
+    if constexpr (OP != ROW_SOFTMAX) {
+      if (VEC && c0 < cols) {
+        if (wp) *reinterpret_cast<v4u*>(wv) = *reinterpret_cast<const v4u*>(wp + c0);
+        if (bp) *reinterpret_cast<v4u*>(bv) = *reinterpret_cast<const v4u*>(bp + c0);
+      } else if (!VEC) {
+#pragma unroll
+        for (int j = 0; j < EV; ++j) {
+          if (wp && c0 + j < cols) wv[j] = wp[c0 + j];
+          if (bp && c0 + j < cols) bv[j] = bp[c0 + j];
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < EV; ++j) {
+      float r;
+      if constexpr (OP == ROW_SOFTMAX) {
+        r = v[i * EV + j] * scale;
+      } else if constexpr (OP == ROW_RMSNORM) {
+        r = v[i * EV + j] * scale;
+        if (wp) r = r * Elem<DT>::load(wv[j]);
+      } else {
+        r = (v[i * EV + j] - shift) * scale;
+        if (wp) r = r * Elem<DT>::load(wv[j]);
+        if (bp) r = r + Elem<DT>::load(bv[j]);
+      }
+      out[j] = Elem<DT>::store(r);
+    }
+    if constexpr (VEC) {
+      if (c0 < cols) *reinterpret_cast<v4u*>(yr + c0) = *reinterpret_cast<const v4u*>(out);
+    } else {
+#pragma unroll
+      for (int j = 0; j < EV; ++j)
+        if (c0 + j < cols) yr[c0 + j] = out[j];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host dispatch
+// ---------------------------------------------------------------------------
+template <int OP, int DT, bool VEC>
+static int launch_row_cfg(const RowArgs& a, hipStream_t s) {
+  typedef typename Elem<DT>::storage S;
+  constexpr int EV = 16 / sizeof(S);
+  const int64_t vecs = (a.cols + EV - 1) / EV;  // 16-byte vectors per row
+  const dim3 block(256);
+  const int64_t g1 = (a.rows + 3) / 4;
+  if (vecs <= 64 * 1) { row_kernel<OP, DT, 1, 1, VEC><<<dim3(g1), block, 0, s>>>(a); }
+  else if (vecs <= 64 * 4) { row_kernel<OP, DT, 1, 4, VEC><<<dim3(g1), block, 0, s>>>(a); }
+  else if (vecs <= 64 * 8) { row_kernel<OP, DT, 1, 8, VEC><<<dim3(g1), block, 0, s>>>(a); }
+  else if (vecs <= 256 * 8) { row_kernel<OP, DT, 4, 8, VEC><<<dim3(a.rows), block, 0, s>>>(a); }
+  else if (vecs <= 256 * 16) { row_kernel<OP, DT, 4, 16, VEC><<<dim3(a.rows), block, 0, s>>>(a); }
+  else return HXI_ERR_UNSUPPORTED;
+  return 0;
+}
+
+template <int OP, int DT>
+static int launch_row_dt(const RowArgs& a, hipStream_t s) {
+  typedef typename Elem<DT>::storage S;
+  constexpr int EV = 16 / sizeof(S);
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  bool vec = (a.cols % EV) == 0 && al16(a.x) && al16(a.y) &&
+             ((a.ldx * (int64_t)sizeof(S)) % 16) == 0 && ((a.ldy * (int64_t)sizeof(S)) % 16) == 0 &&
+             (a.w == nullptr || al16(a.w)) && (a.b == nullptr || al16(a.b));
+  return vec ? launch_row_cfg<OP, DT, true>(a, s) : launch_row_cfg<OP, DT, false>(a, s);
+}
+
+template <int OP>
+static int launch_row_op(int dtype, const RowArgs& a, hipStream_t s) {
+  switch (dtype) {
+    case DT_F16: return launch_row_dt<OP, DT_F16>(a, s);
+    case DT_BF16: return launch_row_dt<OP, DT_BF16>(a, s);
+    case DT_F32: return launch_row_dt<OP, DT_F32>(a, s);
+    default: return HXI_ERR_DTYPE;
+  }
+}
+
+int launch_softmax(int dtype, const void* x, int64_t ldx, void* y, int64_t ldy,
+                   int64_t rows, int64_t cols, hipStream_t s) {
+  RowArgs a{x, ldx, y, ldy, nullptr, nullptr, nullptr, nullptr, 0.f, rows, cols};
+  return launch_row_op<ROW_SOFTMAX>(dtype, a, s);
+}
+
+int launch_rmsnorm(int dtype, const void* x, int64_t ldx, const void* gamma, float eps,
+                   void* y, int64_t ldy, int64_t rows, int64_t cols, hipStream_t s) {
+  RowArgs a{x, ldx, y, ldy, gamma, nullptr, nullptr, nullptr, eps, rows, cols};
+  return launch_row_op<ROW_RMSNORM>(dtype, a, s);
+}
+
+int launch_layernorm(int dtype, const void* x, int64_t ldx, const void* w, const void* b,
+                     float eps, void* y, int64_t ldy, float* mean, float* rstd,
+                     int64_t rows, int64_t cols, hipStream_t s) {
+  RowArgs a{x, ldx, y, ldy, w, b, mean, rstd, eps, rows, cols};
+  return launch_row_op<ROW_LAYERNORM>(dtype, a, s);
+}
+
+// ---------------------------------------------------------------------------
+// SiLU * mul: out = RNE(silu(g) * u), silu(g) = g / (1 + exp(-g)).  fp16
+// rows, 16-byte vectors; a grid-stride loop over 8-element groups.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) silu_mul_f16_kernel(
+    const uint16_t* g, int64_t ldg, const uint16_t* u, int64_t ldu, uint16_t* o, int64_t ldo,
+    int64_t rows, int64_t cols) {
+  const int64_t groups_per_row = cols / 8;
+  const int64_t total = rows * groups_per_row;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = t / groups_per_row, c = (t - r * groups_per_row) * 8;
+    const v4u gv = *reinterpret_cast<const v4u*>(g + r * ldg + c);
+    const v4u uv = *reinterpret_cast<const v4u*>(u + r * ldu + c);
+    const uint16_t* ge = reinterpret_cast<const uint16_t*>(&gv);
+    const uint16_t* ue = reinterpret_cast<const uint16_t*>(&uv);
+    uint16_t out[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float x = f16_bits_to_f32(ge[j]);
+      const float sx = x / (1.0f + fast_exp(-x));
+      out[j] = f32_to_f16_bits(sx * f16_bits_to_f32(ue[j]));
+    }
+    *reinterpret_cast<v4u*>(o + r * ldo + c) = *reinterpret_cast<const v4u*>(out);
+  }
+}
+
+__global__ void __launch_bounds__(256) silu_mul_f16_scalar_kernel(
+    const uint16_t* g, int64_t ldg, const uint16_t* u, int64_t ldu, uint16_t* o, int64_t ldo,
+    int64_t rows, int64_t cols) {
+  const int64_t total = rows * cols;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = t / cols, c = t - r * cols;
+    const float x = f16_bits_to_f32(g[r * ldg + c]);
+    const float sx = x / (1.0f + fast_exp(-x));
+    o[r * ldo + c] = f32_to_f16_bits(sx * f16_bits_to_f32(u[r * ldu + c]));
+  }
+}
+
+int launch_silu_mul_f16(const void* g, int64_t ldg, const void* u, int64_t ldu, void* o,
+                        int64_t ldo, int64_t rows, int64_t cols, hipStream_t s) {
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  const bool vec = cols % 8 == 0 && ldg % 8 == 0 && ldu % 8 == 0 && ldo % 8 == 0 && al16(g) &&
+                   al16(u) && al16(o);
+  const int64_t work = vec ? rows * (cols / 8) : rows * cols;
+  int64_t blocks = (work + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  if (blocks < 1) blocks = 1;
+  if (vec)
+    silu_mul_f16_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
+        (const uint16_t*)g, ldg, (const uint16_t*)u, ldu, (uint16_t*)o, ldo, rows, cols);
+  else
+    silu_mul_f16_scalar_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
+        (const uint16_t*)g, ldg, (const uint16_t*)u, ldu, (uint16_t*)o, ldo, rows, cols);
+  return 0;
+}
+
+}  // namespace hx

@@ -1,0 +1,262 @@
+/*
+ * hx.h -- C ABI of libhxmi, the MI355X (gfx950) implementation of the
+ * hexagon-mlir hot path: the weight-resident tiled matmul (f16/bf16 and
+ * int8), the W8A16 decode GEMV, the softmax / RMSNorm / LayerNorm row
+ * reductions, the SwiGLU FFN composition, and the kernel-config surface the
+ * tile autotuner searches.
+ *
+ * Reference paths below are relative to the hexagon-mlir checkout;
+ * QHB = qcom_hexagon_backend.
+ *
+ * Conventions (all entry points):
+ *   - Tensors are MLIR-style strided memref descriptors (hx_memref2d /
+ *     hx_memref1d), the layout the reference's compiled kernels receive
+ *     (test/utils/dsp/include/tensor.h:73-90, CRunnerUtils.h
+ *     MemRefDescriptor<T,N>: allocated, aligned, offset, sizes, strides).
+ *     Strides and offsets are in elements.  The innermost stride must be 1;
+ *     the outer stride may exceed the row length (the multi-span output ABI
+ *     of test/python/triton/test_matmul_multispan.py:71-78).
+ *   - Data pointers are device pointers.  The caller owns every tensor; the
+ *     library owns registered weights and a per-stream workspace.
+ *   - Work is enqueued on `stream` (NULL = the null stream); no entry point
+ *     synchronizes the device except hx_weight_register.
+ *   - Return value: HX_OK or a negative HX_ERR_*; hx_last_error() returns a
+ *     thread-local message for the last failure.  Failures are closed: there
+ *     is no silent fallback to another arithmetic path (the reference aborts
+ *     on allocation failure, QHB/bin/runtime/include/HexagonCAPI.h:21-25;
+ *     here the caller gets the code instead).
+ *   - Safe to call from several host threads on distinct streams.
+ */
+#ifndef HX_H
+#define HX_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HX_ABI_VERSION 1
+
+/* Same tag as hipStream_t, so a hipStream_t converts without a cast. */
+typedef struct ihipStream_t* hx_stream_t;
+
+/* Element types (the reference's admitted matmul dtypes are f16/f32 on HMX,
+ * QHB/include/hexagon/Dialect/Hmx/IR/HmxDType.h:59-75; int8 runs on the HVX
+ * linalg path, QHB/lib/Transforms/ScheduleMatmulForHVXPass.cpp:169-196). */
+enum { HX_F16 = 1, HX_BF16 = 2, HX_F32 = 3, HX_I8 = 4, HX_I32 = 5 };
+
+/* Orientation of a right-hand operand / weight.  KN is linalg.matmul's
+ * [K, N]; NK is the transposed source [N, K] that hmx.pack_weight accepts
+ * with src_transposed (QHB/include/hexagon/Dialect/Hmx/IR/HmxOps.td:259-266)
+ * and the layout the kernels consume directly. */
+enum { HX_LAYOUT_KN = 0, HX_LAYOUT_NK = 1 };
+
+enum {
+    HX_OK = 0,
+    HX_ERR_ARG = -1,         /* null / malformed argument */
+    HX_ERR_SHAPE = -2,       /* operand shapes do not agree */
+    HX_ERR_DTYPE = -3,       /* dtype combination not supported */
+    HX_ERR_LAYOUT = -4,      /* innermost stride != 1, bad outer stride */
+    HX_ERR_HIP = -5,         /* a HIP runtime call failed */
+    HX_ERR_NOMEM = -6,       /* device allocation failed */
+    HX_ERR_UNSUPPORTED = -7, /* valid request outside what is implemented */
+    HX_ERR_HANDLE = -8,      /* unknown or released weight handle */
+    HX_ERR_NODEVICE = -9     /* no HIP device visible */
+};
+
+typedef struct hx_memref2d {
+    void* allocated;
+    void* aligned;
+    int64_t offset;
+    int64_t sizes[2];
+    int64_t strides[2];
+} hx_memref2d;
+
+typedef struct hx_memref1d {
+    void* allocated;
+    void* aligned;
+    int64_t offset;
+    int64_t sizes[1];
+    int64_t strides[1];
+} hx_memref1d;
+
+/* ---------------------------------------------------------------------- */
+/* Library state                                                           */
+/* ---------------------------------------------------------------------- */
+
+/* Initialise per-device state for the current HIP device.  Optional: every
+ * entry point initialises lazily.  Replaces the runtime's power/HVX/HMX
+ * acquire (QHB/bin/runtime/src/HexagonAPI.cpp:160-261). */
+int hx_init(void);
+const char* hx_last_error(void);
+/* Identity of this build (compiler, arch, source digest); part of every
+ * tuned-config cache key, as tuning_key_int is in QHB/backend/hmx_search.py:
+ * 416-452. */
+const char* hx_build_id(void);
+
+/* ---------------------------------------------------------------------- */
+/* Matmul family                                                           */
+/* ---------------------------------------------------------------------- */
+
+/* C = A . B  (overwrite), or C = A . B * col_scale + residual.
+ *   a        [M, K]  f16 or bf16
+ *   b        [K, N] (HX_LAYOUT_KN) or [N, K] (HX_LAYOUT_NK); same dtype as
+ *            a, or int8 with a = f16 (W8A16: int8 widened exactly to f16)
+ *   col_scale NULL or [N] f32/f16: per-output-channel scale applied to the
+ *            binary32 accumulator (the HMX conversion state's per-channel
+ *            Scale, QHB/bin/runtime/hmx/src/HMXAPI.c:15-27, 39-44)
+ *   residual NULL or [M, N] f16/bf16/f32, added after the scale
+ *   c        [M, N] f16, bf16 or f32; one rounding from binary32
+ * Replaces: linalg.matmul -> hmx.matmul (write-only, empty init) and the
+ * residual/widening read-out (QHB/lib/Dialect/Hmx/Transforms/
+ * MatmulToHmxPass.cpp:1-48, 100-121, 1369-1470; HmxOps.td:47-110,
+ * 362-430; the leaves hmx_mma_f16 / hmx_acc_store_f16 / hmx_unpack_acc_f32,
+ * QHB/bin/runtime/hmx/include/HMXAPI.h:66-80, 217-230). */
+int hx_matmul(const hx_memref2d* a, int a_dtype,
+              const hx_memref2d* b, int b_dtype, int b_layout,
+              const hx_memref1d* col_scale, int scale_dtype,
+              const hx_memref2d* residual, int residual_dtype,
+              hx_memref2d* c, int c_dtype, hx_stream_t stream);
+
+/* int8 x int8 -> int32, exact: C[i][j] = sum_k sext(A[i][k]) * sext(B[k][j]).
+ *   c_dtype HX_I32: the int32 product itself.
+ *   c_dtype HX_F16: RNE_f16(((float)C[i][j] * row_scale[i]) * col_scale[j]),
+ *                   binary32, in that order; either scale may be NULL (1).
+ * Scales are f32.  Replaces linalg.matmul(i8, i8 -> i32) as lowered by
+ * ScheduleMatmulForHVX (QHB/lib/Transforms/ScheduleMatmulForHVXPass.cpp:
+ * 48-199), the path matmul-to-hmx leaves int8 on (`unsupported-dtype`,
+ * QHB/include/hexagon/Dialect/Hmx/Transforms/HmxTarget.h:198-200). */
+int hx_gemm_i8(const hx_memref2d* a, const hx_memref2d* b, int b_layout,
+               const hx_memref1d* row_scale, const hx_memref1d* col_scale,
+               hx_memref2d* c, int c_dtype, hx_stream_t stream);
+
+/* W8A16 decode GEMV / skinny GEMM, M <= 16 (any M is accepted; M > 16 runs
+ * the MFMA GEMM with the same contract):
+ *   Y[m][n] = RNE_f16( (sum_k X[m][k] * W[k][n]) * scale[n] ),
+ *   X [M, K] f16, W int8 [K, N] (KN) or [N, K] (NK), scale [N] f16/f32.
+ * Replaces the HVX dequant-generic + matmul that skinny shapes take
+ * (HmxTarget.h:100 `min-rows`, :208-216 `tile-alignment`;
+ * ScheduleMatmulForHVXPass.cpp:169-196). */
+int hx_gemv_w8a16(const hx_memref2d* x, const hx_memref2d* w, int w_layout,
+                  const hx_memref1d* scale, int scale_dtype,
+                  hx_memref2d* y, hx_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* Row reductions over the last dimension (f16, bf16 or f32 in and out,   */
+/* binary32 inside, one rounding)                                          */
+/* ---------------------------------------------------------------------- */
+
+/* y = exp(x - max) * (1 / sum exp(x - max)).
+ * Replaces the softmax generic chain (docs/tutorials/torch-mlir/
+ * softmax.md:178-226; test/python/triton/test_softmax.py:41-69) as fused by
+ * HexagonFusion and VectorRowReduce (QHB/lib/Conversion/LinalgToLLVM/
+ * FusionPass.cpp:223, VectorRowReducePass.cpp:1-31) with DivToMul
+ * (QHB/lib/Transforms/DivToMulOptimizationPass.cpp:9-18). */
+int hx_softmax(const hx_memref2d* x, hx_memref2d* y, int dtype, hx_stream_t stream);
+
+/* y = x * rsqrt(sum(x^2)/N + eps) * gamma   (gamma may be NULL).
+ * Replaces test/python/triton/test_rms_norm.py:34-59 after FastInverse
+ * (QHB/lib/Transforms/FastInversePass.cpp:97-140). */
+int hx_rmsnorm(const hx_memref2d* x, const hx_memref1d* gamma, float eps,
+               hx_memref2d* y, int dtype, hx_stream_t stream);
+
+/* y = (x - mean) * rstd * w + b; mean / rstd (f32 [rows]) are written when
+ * non-NULL.  w, b may be NULL.  Replaces test/python/triton/
+ * test_layer_norm.py:39-79 (mean and rstd stored as at :70-72). */
+int hx_layernorm(const hx_memref2d* x, const hx_memref1d* w, const hx_memref1d* b,
+                 float eps, hx_memref2d* y, hx_memref1d* mean, hx_memref1d* rstd,
+                 int dtype, hx_stream_t stream);
+
+/* out = RNE(silu(g) * u), silu(g) = g / (1 + exp(-g)); f16 only.
+ * The SiLU of test/python/triton/test_silu.py applied as the SwiGLU gate. */
+int hx_silu_mul(const hx_memref2d* g, const hx_memref2d* u, hx_memref2d* out,
+                int dtype, hx_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* Resident weights                                                        */
+/* ---------------------------------------------------------------------- */
+
+typedef struct hx_weight* hx_weight_t;
+
+/* Register a weight once: the library builds its K-contiguous device image
+ * ([N, K]) and f32 per-channel scales, keyed by content (a second
+ * registration of identical bytes, shape, dtype and scales returns the same
+ * handle with its reference count raised).  w_dtype HX_I8 (scale required,
+ * [N] f16/f32), HX_F16 or HX_BF16 (scale optional).  Synchronizes `stream`.
+ * Replaces the resident-weight ABI hexagon_runtime_weight_resident_v2
+ * (QHB/bin/runtime/include/HexagonCAPI.h:39-57) together with the host
+ * pre-pack and its content-hash cache (QHB/backend/hmx_weight_prepack.py:
+ * 124-212) and WeightResidentPass (QHB/lib/Dialect/Hmx/Transforms/
+ * WeightResidentPass.cpp:1-60). */
+int hx_weight_register(const hx_memref2d* w, int w_dtype, int w_layout,
+                       const hx_memref1d* scale, int scale_dtype,
+                       hx_stream_t stream, hx_weight_t* out);
+/* Drop one reference; the image is freed when the count reaches zero. */
+int hx_weight_release(hx_weight_t w);
+int hx_weight_info(hx_weight_t w, int64_t* k, int64_t* n, int* dtype,
+                   uint64_t* content_hash, int* refcount);
+
+/* Y = X . W * scale (+ residual) with a registered weight.  X [M, K] f16
+ * (bf16 for a bf16 weight), Y [M, N] f16/bf16/f32.  int8 weights with
+ * M <= 16 run the decode GEMV, larger M the W8A16 MFMA GEMM. */
+int hx_matmul_resident(const hx_memref2d* x, int x_dtype, hx_weight_t w,
+                       const hx_memref2d* residual, int residual_dtype,
+                       hx_memref2d* y, int y_dtype, hx_stream_t stream);
+
+/* Llama-style SwiGLU FFN block on registered int8 weights:
+ *   h = RMSNorm(x, gamma, eps); a = silu(h.Wg*sg) * (h.Wu*su); y = a.Wd*sd
+ * with fp16 rounding after each linalg op (RMSNorm out, gate, up, SiLU*mul,
+ * down).  x [T, H] f16, Wg/Wu [H, I], Wd [I, H] (as registered), y [T, H].
+ * The gate and up GEMMs share one kernel whose epilogue applies SiLU*mul. */
+int hx_swiglu_ffn(const hx_memref2d* x, const hx_memref1d* gamma, float eps,
+                  hx_weight_t w_gate, hx_weight_t w_up, hx_weight_t w_down,
+                  hx_memref2d* y, hx_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* Kernel configurations (the autotuner's search space)                    */
+/* ---------------------------------------------------------------------- */
+
+/* Kernel families. */
+enum {
+    HX_OP_GEMM_I8 = 1,      /* hx_gemm_i8 */
+    HX_OP_MATMUL_F16 = 2,   /* hx_matmul f16 x f16 */
+    HX_OP_MATMUL_BF16 = 3,  /* hx_matmul bf16 x bf16 */
+    HX_OP_MATMUL_W8 = 4,    /* f16 x int8 GEMM (M > 16) */
+    HX_OP_SWIGLU_W8 = 5,    /* fused gate/up GEMM of hx_swiglu_ffn */
+    HX_OP_GEMV_W8 = 6       /* W8A16 decode GEMV (M <= 16) */
+};
+
+/* One compiled configuration.  GEMM families fill bm/bn/bk (K elements per
+ * LDS stage)/waves_m/waves_n/lds_stages; the GEMV family fills col_tiles
+ * (16-column tiles per wave) and split_k (workgroups per column tile).
+ * Replaces the (BM, BN, BK) tile space of enumerate_tile_configs
+ * (QHB/backend/hmx_search.py:246-332), widened to the knobs that matter on
+ * gfx950. */
+typedef struct hx_kernel_config {
+    int32_t op;
+    int32_t index;
+    int32_t bm, bn, bk;
+    int32_t waves_m, waves_n;
+    int32_t lds_stages;
+    int32_t split_k;
+    int32_t col_tiles;
+    int32_t lds_bytes;
+    char name[40];
+} hx_kernel_config;
+
+int hx_config_count(int op);
+int hx_config_get(int op, int index, hx_kernel_config* out);
+/* Pin configuration `index` for calls of family `op` with exactly this
+ * (M, N, K) on the current device; index -1 removes the pin. */
+int hx_config_select(int op, int64_t m, int64_t n, int64_t k, int index);
+/* The configuration a call of this shape will run: the pinned one, else
+ * the untuned default.  *index = -1 means the generic (any-alignment)
+ * kernel. */
+int hx_config_lookup(int op, int64_t m, int64_t n, int64_t k, int* index);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HX_H */

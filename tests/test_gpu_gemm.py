@@ -1,0 +1,219 @@
+"""GPU parity for the MFMA GEMM family.
+
+int8 x int8 -> int32 is compared BIT-EXACT with the oracle (integer sums are
+order-free); the fused dequant to fp16 is bit-exact too (the epilogue computes
+RNE_f16(((float)acc * sa) * sb) in the same binary32 order).  Floating GEMMs
+are within rtol 1e-2 / atol 1e-3 of the oracle, and additionally under the
+reference's own relative-Frobenius gate rel < 2e-3 against an f32 product
+(test/python/triton/test_matmul_kloop.py:68, test_matmul_multispan.py:69).
+At the full 4096^3 size, exactness is checked on sampled rows plus the
+size-independent identities colsum(C) = colsum(A).B and C.1 = A.(B.1).
+"""
+import numpy as np
+import pytest
+
+from conftest import assert_close, bf16_from_f32, rng, to_dev, to_np
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def i8(shape, seed):
+    return rng(seed).integers(-127, 128, shape, dtype=np.int8)
+
+
+def rel_fro(got, want):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    return np.linalg.norm(got - want) / np.linalg.norm(want)
+
+
+I8_SHAPES = [(256, 256, 256), (128, 256, 512), (100, 72, 48), (64, 80, 160), (1, 300, 4096),
+             (333, 257, 96), (17, 33, 50), (513, 1030, 4112)]
+
+
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+@pytest.mark.parametrize("shape", I8_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_gemm_i8_exact(hx, dev, shape, layout):
+    M, N, K = shape
+    a = i8((M, K), 1)
+    b = i8((K, N), 2)
+    bt = np.ascontiguousarray(b.T)
+    c = hx.gemm_i8(to_dev(a, dev), to_dev(b if layout == "kn" else bt, dev), b_layout=layout)
+    want = oracle.gemm_i8_i32(a, b)
+    got = to_np(c)
+    assert np.array_equal(got, want), f"int8 GEMM {shape} {layout}: {int((got != want).sum())} differ"
+
+
+@pytest.mark.parametrize("shape", [(256, 256, 256), (300, 500, 4096), (64, 64, 64)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_gemm_i8_dequant_f16_bitexact(hx, dev, shape):
+    M, N, K = shape
+    a, b = i8((M, K), 3), i8((K, N), 4)
+    sa = rng(5).uniform(0.001, 0.02, M).astype(np.float32)
+    sb = rng(6).uniform(0.001, 0.02, N).astype(np.float32)
+    import torch
+    c = hx.gemm_i8(to_dev(a, dev), to_dev(b, dev), row_scale=to_dev(sa, dev), col_scale=to_dev(sb, dev),
+                   out_dtype=torch.float16)
+    want = oracle.dequant_i32_f16(oracle.gemm_i8_i32(a, b), sa, sb)
+    got = to_np(c)
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16)), \
+        f"dequant differs in {int((got.view(np.uint16) != want.view(np.uint16)).sum())} elements"
+
+
+def test_gemm_i8_extremes_closed_form(hx, dev):
+    """All +127 times all -127: every entry is -K*127^2 (no int32 overflow
+    at K=4096: 66,064,384 < 2^31); identity B reproduces A exactly."""
+    K = 4096
+    a = np.full((64, K), 127, np.int8)
+    b = np.full((K, 96), -127, np.int8)
+    c = to_np(hx.gemm_i8(to_dev(a, dev), to_dev(b, dev)))
+    assert (c == -K * 127 * 127).all()
+    a2 = i8((128, 256), 7)
+    eye = np.eye(256, dtype=np.int8)
+    c2 = to_np(hx.gemm_i8(to_dev(a2, dev), to_dev(eye, dev)))
+    assert np.array_equal(c2, a2.astype(np.int32))
+
+
+def test_gemm_i8_4096_cube(hx, dev):
+    """BASELINE config C2 at full size: exact on sampled rows, and the exact
+    column/row checksum identities over every entry."""
+    import torch
+    M = N = K = 4096
+    a = i8((M, K), 11)
+    b = i8((K, N), 12)
+    bt = np.ascontiguousarray(b.T)
+    c = hx.gemm_i8(to_dev(a, dev), to_dev(bt, dev), b_layout="nk")
+    got = to_np(c)
+    rows = np.sort(rng(13).choice(M, 48, replace=False))
+    rows = np.unique(np.concatenate([rows, [0, 255, 256, M - 1]]))
+    want_rows = oracle.gemm_i8_i32(np.ascontiguousarray(a[rows]), b)
+    assert np.array_equal(got[rows], want_rows), "sampled rows differ"
+    a64, b64 = a.astype(np.int64), b.astype(np.int64)
+    assert np.array_equal(got.astype(np.int64).sum(axis=0), a64.sum(axis=0) @ b64), "column checksums"
+    assert np.array_equal(got.astype(np.int64).sum(axis=1), a64 @ b64.sum(axis=1)), "row checksums"
+    # the fused-dequant output of the same call shape, bit-exact on the sampled rows
+    sa = rng(14).uniform(0.001, 0.02, M).astype(np.float32)
+    sb = rng(15).uniform(0.001, 0.02, N).astype(np.float32)
+    c16 = hx.gemm_i8(to_dev(a, dev), to_dev(bt, dev), b_layout="nk", row_scale=to_dev(sa, dev),
+                     col_scale=to_dev(sb, dev), out_dtype=torch.float16)
+    want16 = oracle.dequant_i32_f16(got, sa, sb)
+    assert np.array_equal(to_np(c16).view(np.uint16), want16.view(np.uint16))
+
+
+@pytest.mark.parametrize("cfg", range(6))
+def test_gemm_i8_every_config(hx, dev, cfg):
+    """Every compiled int8 configuration is exact (the autotuner may pick any)."""
+    M, N, K = 384, 640, 1024
+    a, b = i8((M, K), 20), i8((K, N), 21)
+    hx.config_select(1, M, N, K, cfg)
+    try:
+        got = to_np(hx.gemm_i8(to_dev(a, dev), to_dev(np.ascontiguousarray(b.T), dev), b_layout="nk"))
+    finally:
+        hx.config_select(1, M, N, K, -1)
+    assert np.array_equal(got, oracle.gemm_i8_i32(a, b))
+
+
+def _fp(dtype, shape, seed, lo=-1.0, hi=1.0):
+    x = rng(seed).uniform(lo, hi, shape).astype(np.float32)
+    if dtype == "f16":
+        return x.astype(np.float16)
+    return bf16_from_f32(x)
+
+
+def _torch(h, dtype, dev):
+    import torch
+    if dtype == "bf16":
+        return to_dev(h.view(np.int16), dev).view(torch.bfloat16)
+    return to_dev(h, dev)
+
+
+def _vals(h, dtype):
+    return oracle.bf16_bits_to_f32(h) if dtype == "bf16" else np.asarray(h, np.float32)
+
+
+F_SHAPES = [(256, 256, 256), (256, 256, 512), (1024, 512, 64), (100, 200, 72), (33, 65, 17), (512, 384, 1024)]
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+@pytest.mark.parametrize("shape", F_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_matmul_float(hx, dev, dtype, layout, shape):
+    M, N, K = shape
+    a = _fp(dtype, (M, K), 30)
+    b = _fp(dtype, (K, N), 31)
+    bb = b if layout == "kn" else np.ascontiguousarray(b.T)
+    c = hx.matmul(_torch(a, dtype, dev), _torch(bb, dtype, dev), b_layout=layout)
+    bf = dtype == "bf16"
+    want = oracle.matmul(a, b, a_bf16=bf, b_bf16=bf, out_bf16=bf)
+    rtol, atol = (1e-2, 1e-3) if dtype == "f16" else (2e-2, 1e-2)
+    got = _vals(to_np(c), dtype)
+    assert_close(got, _vals(want, dtype), rtol, atol, f"matmul {dtype} {shape} {layout}")
+    exact = _vals(a, dtype).astype(np.float64) @ _vals(b, dtype).astype(np.float64)
+    assert rel_fro(got, exact) < (2e-3 if dtype == "f16" else 8e-3)
+
+
+def test_matmul_multispan_output_stride(hx, dev):
+    """The multi-span ABI: a 2048^3 product written into a window of a wider
+    output (row stride 2304), as test/python/triton/test_matmul_multispan.py
+    exercises; nothing outside the window may change, rel < 2e-3."""
+    import torch
+    M = N = K = 2048
+    a = _fp("f16", (M, K), 40, 0.0, 1.0)
+    b = _fp("f16", (K, N), 41, 0.0, 1.0)
+    big = torch.full((M, N + 256), -3.0, dtype=torch.float16, device=dev)
+    hx.matmul(to_dev(a, dev), to_dev(b, dev), out=big[:, :N])
+    got = to_np(big)
+    assert (got[:, N:] == np.float16(-3.0)).all()
+    exact = a.astype(np.float64) @ b.astype(np.float64)
+    assert rel_fro(got[:, :N], exact) < 2e-3
+
+
+def test_matmul_residual_scale_f32_out(hx, dev):
+    """C = A.B * col_scale + residual, f32 out (the widened read-out with a
+    residual, QHB/bin/runtime/hmx/src/HMXLayout.c:868-999)."""
+    import torch
+    M, N, K = 192, 320, 256
+    a, b = _fp("f16", (M, K), 50), _fp("f16", (K, N), 51)
+    r = rng(52).normal(0, 1, (M, N)).astype(np.float32)
+    s = rng(53).uniform(0.5, 2.0, N).astype(np.float32)
+    c = hx.matmul(to_dev(a, dev), to_dev(b, dev), col_scale=to_dev(s, dev), residual=to_dev(r, dev),
+                  out_dtype=torch.float32)
+    want = oracle.matmul(a, b, scale_n=s, residual=r, out_dtype=np.float32)
+    assert_close(to_np(c), want, 1e-4, 1e-4, "residual+scale f32")
+    # dropping either term is caught
+    assert not np.allclose(to_np(c), oracle.matmul(a, b, residual=r, out_dtype=np.float32), atol=1e-3)
+    assert not np.allclose(to_np(c), oracle.matmul(a, b, scale_n=s, out_dtype=np.float32), atol=1e-3)
+
+
+@pytest.mark.parametrize("shape", [(512, 1024, 512), (2048, 704, 4096), (40, 96, 64), (77, 130, 48)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_matmul_w8a16_gemm(hx, dev, shape):
+    """f16 activations x int8 weights (per-channel f16 scales), M > 16 GEMM."""
+    M, N, K = shape
+    x = rng(60).normal(0, 1, (M, K)).astype(np.float16)
+    w = i8((K, N), 61)
+    s = rng(62).uniform(0.001, 0.02, N).astype(np.float16)
+    y = hx.matmul(to_dev(x, dev), to_dev(w, dev), col_scale=to_dev(s, dev))
+    want = oracle.matmul(x, w, scale_n=s.astype(np.float32))
+    assert_close(to_np(y).astype(np.float32), want.astype(np.float32), 1e-2, 1e-3, f"w8a16 {shape}")
+
+
+@pytest.mark.parametrize("op,cfgs", [(2, range(6)), (4, range(6))])
+def test_float_every_config(hx, dev, op, cfgs):
+    M, N, K = 320, 448, 512
+    a = _fp("f16", (M, K), 70)
+    if op == 2:
+        b = _fp("f16", (N, K), 71)
+        want = oracle.matmul(a, b, b_trans=True)
+    else:
+        b = i8((N, K), 71)
+        want = oracle.matmul(a, b, b_trans=True)
+    for cfg in cfgs:
+        hx.config_select(op, M, N, K, cfg)
+        try:
+            got = to_np(hx.matmul(to_dev(a, dev), to_dev(b, dev), b_layout="nk"))
+        finally:
+            hx.config_select(op, M, N, K, -1)
+        assert_close(got.astype(np.float32), want.astype(np.float32), 1e-2, 1e-3, f"op {op} cfg {cfg}")

@@ -1,0 +1,85 @@
+"""GPU parity for the W8A16 decode GEMV (M in {1, 4, 16},
+N = 11008, K = 4096, int8 weights, per-output-channel fp16 scales, fp16
+activations N(0,1), binary32 accumulation, fp16 out) within rtol 1e-2 /
+atol 1e-3 of the oracle, for every compiled configuration, both weight
+orientations, ragged N / K, and the resident-weight path."""
+import numpy as np
+import pytest
+
+from conftest import assert_close, rng, to_dev, to_np
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def case(M, N, K, seed=0):
+    x = rng(seed).normal(0, 1, (M, K)).astype(np.float16)
+    w = rng(seed + 1).integers(-127, 128, (K, N), dtype=np.int8)
+    s = rng(seed + 2).uniform(0.001, 0.02, N).astype(np.float16)
+    return x, w, s
+
+
+@pytest.fixture(scope="module")
+def c3():
+    N, K = 11008, 4096
+    x, w, s = case(16, N, K, seed=100)
+    wt = np.ascontiguousarray(w.T)
+    want = {M: oracle.matmul(np.ascontiguousarray(x[:M]), wt, b_trans=True, scale_n=s.astype(np.float32))
+            for M in (1, 4, 16)}
+    return x, w, wt, s, want
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_gemv_c3_kn(hx, dev, c3, M):
+    x, w, wt, s, want = c3
+    y = hx.gemv_w8a16(to_dev(np.ascontiguousarray(x[:M]), dev), to_dev(w, dev), to_dev(s, dev), w_layout="kn")
+    assert_close(to_np(y).astype(np.float32), want[M].astype(np.float32), 1e-2, 1e-3, f"gemv M={M}")
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_gemv_c3_every_config(hx, dev, c3, M):
+    x, w, wt, s, want = c3
+    N, K = wt.shape
+    xt, wtt, st = to_dev(np.ascontiguousarray(x[:M]), dev), to_dev(wt, dev), to_dev(s, dev)
+    for cfg in range(hx.config_count(6)):
+        hx.config_select(6, M, N, K, cfg)
+        try:
+            y = hx.gemv_w8a16(xt, wtt, st, w_layout="nk")
+            got = to_np(y)
+            y2 = to_np(hx.gemv_w8a16(xt, wtt, st, w_layout="nk"))  # counters reset between calls
+        finally:
+            hx.config_select(6, M, N, K, -1)
+        assert_close(got.astype(np.float32), want[M].astype(np.float32), 1e-2, 1e-3, f"cfg {cfg} M={M}")
+        assert np.array_equal(got.view(np.uint16), y2.view(np.uint16)), f"cfg {cfg}: not deterministic"
+
+
+@pytest.mark.parametrize("shape", [(3, 1000, 4096), (16, 11008, 4112), (7, 37, 144), (2, 5000, 16)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_gemv_ragged(hx, dev, shape):
+    M, N, K = shape
+    x, w, s = case(M, N, K, seed=200)
+    y = hx.gemv_w8a16(to_dev(x, dev), to_dev(w, dev), to_dev(s, dev))
+    want = oracle.matmul(x, w, scale_n=s.astype(np.float32))
+    assert_close(to_np(y).astype(np.float32), want.astype(np.float32), 1e-2, 1e-3, f"ragged {shape}")
+
+
+def test_gemv_resident_matches_raw(hx, dev, c3):
+    """The resident (registered, pre-packed) weight gives the same bits as
+    the raw call, and registering identical content returns the same handle."""
+    x, w, wt, s, want = c3
+    wd, sd = to_dev(w, dev), to_dev(s, dev)
+    rw = hx.ResidentWeight(wd, sd, layout="kn")
+    rw2 = hx.ResidentWeight(to_dev(wt, dev), sd, layout="nk")
+    try:
+        assert rw.handle == rw2.handle, "identical content must map to one resident image"
+        assert rw.info()["refcount"] == 2
+        for M in (1, 4, 16):
+            xm = to_dev(np.ascontiguousarray(x[:M]), dev)
+            y_res = to_np(hx.matmul_resident(xm, rw))
+            y_raw = to_np(hx.gemv_w8a16(xm, wd, sd))
+            assert np.array_equal(y_res.view(np.uint16), y_raw.view(np.uint16))
+            assert_close(y_res.astype(np.float32), want[M].astype(np.float32), 1e-2, 1e-3, "resident")
+    finally:
+        rw2.release()
+        rw.release()

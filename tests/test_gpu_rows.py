@@ -1,0 +1,119 @@
+"""GPU parity: softmax / RMSNorm / LayerNorm / SiLU*mul against the oracle.
+
+Tolerances: fp16 / bf16 outputs within rtol 1e-2, atol 1e-3 (BASELINE.json
+north star; the reference's own softmax gate is atol 1e-3 for fp16,
+test/python/triton/test_softmax.py:27-28); f32 within rtol 1e-4, atol 1e-5
+(test_layer_norm.py:22, test_softmax.py:27).  The fp32 results differ from the
+oracle only by reduction order and the hardware exp2 / rsqrt-free chain.
+"""
+import numpy as np
+import pytest
+
+from conftest import assert_close, bf16_from_f32, rng, to_dev, to_np
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"f16": (1e-2, 1e-3), "bf16": (1e-2, 1e-3), "f32": (1e-4, 1e-5)}
+
+
+def make(dtype, shape, sigma=2.0, seed=0, mean=0.0):
+    """Host array in the test dtype (bf16 as uint16 bits) + its f32 values."""
+    x = rng(seed).normal(mean, sigma, shape).astype(np.float32)
+    if dtype == "f16":
+        h = x.astype(np.float16)
+        return h, h.astype(np.float32)
+    if dtype == "bf16":
+        b = bf16_from_f32(x)
+        return b, oracle.bf16_bits_to_f32(b)
+    return x, x
+
+
+def to_torch(h, dtype, dev):
+    import torch
+    t = to_dev(h.view(np.int16) if dtype == "bf16" else h, dev)
+    return t.view(torch.bfloat16) if dtype == "bf16" else t
+
+
+def values(arr, dtype):
+    if dtype == "bf16":
+        return oracle.bf16_bits_to_f32(arr)
+    return np.asarray(arr, np.float32)
+
+
+SHAPES = [(8192, 4096), (128, 128), (127, 513), (27, 8192), (3, 1), (5, 16384), (64, 100)]
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"{s[0]}x{s[1]}")
+def test_softmax(hx, dev, dtype, shape):
+    xh, _ = make(dtype, shape, seed=1)
+    y = hx.softmax(to_torch(xh, dtype, dev))
+    want = oracle.softmax(xh, bf16=(dtype == "bf16"))
+    rtol, atol = TOL[dtype]
+    got = values(to_np(y), dtype)
+    assert_close(got, values(want, dtype), rtol, atol, f"softmax {dtype} {shape}")
+    # rows of a softmax sum to one (to the output's rounding)
+    assert np.allclose(got.astype(np.float64).sum(axis=1), 1.0, atol=2e-2 if dtype != "f32" else 1e-4)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"{s[0]}x{s[1]}")
+def test_rmsnorm(hx, dev, dtype, shape):
+    xh, _ = make(dtype, shape, seed=2)
+    gh, _ = make(dtype, (shape[1],), sigma=0.1, mean=1.0, seed=3)
+    y = hx.rms_norm(to_torch(xh, dtype, dev), to_torch(gh, dtype, dev), eps=1e-6)
+    want = oracle.rmsnorm(xh, gh, 1e-6, bf16=(dtype == "bf16"))
+    rtol, atol = TOL[dtype]
+    assert_close(values(to_np(y), dtype), values(want, dtype), rtol, atol, f"rmsnorm {dtype} {shape}")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"{s[0]}x{s[1]}")
+def test_layernorm(hx, dev, dtype, shape):
+    xh, _ = make(dtype, shape, seed=4, mean=0.5)
+    wh, _ = make(dtype, (shape[1],), sigma=0.2, mean=1.0, seed=5)
+    bh, _ = make(dtype, (shape[1],), sigma=0.2, seed=6)
+    y, mean, rstd = hx.layer_norm(to_torch(xh, dtype, dev), to_torch(wh, dtype, dev),
+                                  to_torch(bh, dtype, dev), eps=1e-5, return_stats=True)
+    want, wm, wr = oracle.layernorm(xh, wh, bh, 1e-5, bf16=(dtype == "bf16"))
+    rtol, atol = TOL[dtype]
+    assert_close(values(to_np(y), dtype), values(want, dtype), rtol, atol, f"layernorm {dtype} {shape}")
+    assert_close(to_np(mean), wm, 1e-5, 1e-5, "mean")
+    assert_close(to_np(rstd), wr, 1e-4, 1e-5, "rstd")
+
+
+def test_rmsnorm_no_gamma_and_strided_rows(hx, dev):
+    """gamma=None is the identity; an outer stride > cols (a view into a
+    wider buffer) reads and writes only the view."""
+    import torch
+    x, _ = make("f16", (64, 4096 + 64), seed=7)
+    xt = to_dev(x, dev)[:, :4096]
+    out_full = torch.full((64, 4096 + 64), 7.0, dtype=torch.float16, device=dev)
+    hx.rms_norm(xt, None, eps=1e-6, out=out_full[:, :4096])
+    want = oracle.rmsnorm(np.ascontiguousarray(x[:, :4096]), None, 1e-6)
+    got = to_np(out_full)
+    assert_close(got[:, :4096].astype(np.float32), want.astype(np.float32), 1e-2, 1e-3, "strided rmsnorm")
+    assert (got[:, 4096:] == np.float16(7.0)).all(), "wrote outside the view"
+
+
+def test_softmax_reference_shape_against_torch(hx, dev):
+    """The reference test's own oracle and gate: torch softmax, atol 1e-3
+    (test/python/triton/test_softmax.py:88-93), at its 128x128 shape."""
+    import torch
+    x = torch.rand(128, 128, dtype=torch.float16, generator=torch.Generator().manual_seed(0))
+    y = hx.softmax(x.to(dev)).cpu()
+    ref = torch.nn.functional.softmax(x.float(), dim=1).half()
+    assert torch.allclose(y, ref, atol=1e-3)
+
+
+def test_silu_mul(hx, dev):
+    g, _ = make("f16", (64, 11008), sigma=2.0, seed=8)
+    u, _ = make("f16", (64, 11008), sigma=1.0, seed=9)
+    y = hx.silu_mul(to_dev(g, dev), to_dev(u, dev))
+    want = oracle.silu_mul(g, u)
+    assert_close(to_np(y).astype(np.float32), want.astype(np.float32), 1e-2, 1e-3, "silu_mul")
+    # odd width takes the element path
+    y2 = hx.silu_mul(to_dev(g[:, :1001].copy(), dev), to_dev(u[:, :1001].copy(), dev))
+    assert_close(to_np(y2).astype(np.float32), want[:, :1001].astype(np.float32), 1e-2, 1e-3, "silu_mul odd")

@@ -1,0 +1,268 @@
+"""Pins for the CPU oracle (oracle/hx_oracle.c).  Every oracle function is
+checked against something that does not share its code: numpy / torch-CPU
+library routines, closed forms, invariants or brute force -- chosen so that
+a plausible mistake (a dropped term, a wrong order, a transposed operand)
+fails one of them.  The reference ships no numeric fixtures for this path
+(its device tests draw torch.rand at run time), so the reference tests'
+own oracles and tolerances are reproduced at their shapes
+(test/python/triton/test_softmax.py, test_rms_norm.py, test_layer_norm.py),
+plus small committed fixtures under tests/golden/."""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import assert_close, rng
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+# --------------------------------------------------------------------------- #
+# Conversions
+# --------------------------------------------------------------------------- #
+
+def test_f32_to_f16_matches_numpy_rne():
+    specials = np.array([0.0, -0.0, 1.0, -1.0, 65504.0, 65519.996, 65520.0, 65536.0, 1e9, -1e9,
+                         np.inf, -np.inf, 2.0 ** -14, 2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26,
+                         2.0 ** -25 * 1.0000001, 2.0 ** -14 - 2.0 ** -25, 1e-8, 5.96e-8, 0.1, 1 / 3],
+                        dtype=np.float32)
+    # ties: exactly halfway between two f16 values, at several binades
+    base = np.arange(1024, 2048, dtype=np.float32)
+    ties = np.concatenate([(base + 0.5) * 2.0 ** e for e in (-24, -20, -10, 0, 5)]).astype(np.float32)
+    bits = rng(0).integers(0, 2 ** 32, 1 << 20, dtype=np.uint64).astype(np.uint32)
+    rand = bits.view(np.float32)
+    rand = rand[np.isfinite(rand)]
+    for x in (specials, ties, rand):
+        got = oracle.f32_to_f16_bits(x)
+        want = x.astype(np.float16).view(np.uint16)
+        assert np.array_equal(got, want)
+    nan = oracle.f32_to_f16_bits(np.array([np.nan], np.float32))
+    assert np.isnan(nan.view(np.float16)).all()
+
+
+def test_f16_to_f32_all_65536_patterns():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = oracle.f16_bits_to_f32(h)
+    want = h.view(np.float16).astype(np.float32)
+    finite = np.isfinite(want)
+    assert np.array_equal(got[finite].view(np.uint32), want[finite].view(np.uint32))
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(np.isinf(got), np.isinf(want))
+
+
+def test_f32_to_bf16_matches_torch_rne():
+    torch = pytest.importorskip("torch")
+    bits = rng(1).integers(0, 2 ** 32, 1 << 20, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    x = x[~np.isnan(x)]
+    got = oracle.f32_to_bf16_bits(x)
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+    assert np.array_equal(oracle.bf16_bits_to_f32(got).view(np.uint32),
+                          torch.from_numpy(want.view(np.int16)).view(torch.bfloat16).float().numpy().view(np.uint32))
+
+
+# --------------------------------------------------------------------------- #
+# int8 GEMM
+# --------------------------------------------------------------------------- #
+
+def test_gemm_i8_brute_force_small():
+    a = rng(2).integers(-127, 128, (5, 3), dtype=np.int8)
+    b = rng(3).integers(-127, 128, (3, 7), dtype=np.int8)
+    want = [[sum(int(a[i, k]) * int(b[k, j]) for k in range(3)) for j in range(7)] for i in range(5)]
+    assert oracle.gemm_i8_i32(a, b).tolist() == want
+
+
+@pytest.mark.parametrize("shape", [(64, 64, 64), (37, 129, 260), (1, 4096, 512), (200, 3, 1000)])
+def test_gemm_i8_matches_numpy_int64(shape):
+    M, N, K = shape
+    a = rng(4).integers(-127, 128, (M, K), dtype=np.int8)
+    b = rng(5).integers(-127, 128, (K, N), dtype=np.int8)
+    want = a.astype(np.int64) @ b.astype(np.int64)
+    got = oracle.gemm_i8_i32(a, b)
+    assert np.array_equal(got, want)
+    assert np.array_equal(oracle.gemm_i8_i32(a, np.ascontiguousarray(b.T), b_trans=True), want)
+    # negative control: the transposed-operand mistake is visible to this check
+    if M == N == K:
+        assert not np.array_equal(got, a.astype(np.int64) @ b.T.astype(np.int64))
+
+
+def test_gemm_i8_closed_forms():
+    K = 4096
+    a = np.full((3, K), 127, np.int8)
+    b = np.full((K, 2), -127, np.int8)
+    assert (oracle.gemm_i8_i32(a, b) == -K * 127 * 127).all()        # no int32 overflow at K=4096
+    a = np.full((2, K), -127, np.int8)
+    assert (oracle.gemm_i8_i32(a, np.full((K, 2), -127, np.int8)) == K * 127 * 127).all()
+    x = rng(6).integers(-127, 128, (9, 9), dtype=np.int8)
+    assert np.array_equal(oracle.gemm_i8_i32(x, np.eye(9, dtype=np.int8)), x.astype(np.int32))
+    u = rng(7).integers(-127, 128, (8, 1), dtype=np.int8)
+    v = rng(8).integers(-127, 128, (1, 6), dtype=np.int8)
+    assert np.array_equal(oracle.gemm_i8_i32(u, v), np.outer(u.astype(np.int32), v.astype(np.int32)))
+
+
+def test_dequant_matches_numpy_binary32_bitwise():
+    c = rng(9).integers(-66_064_384, 66_064_385, (64, 96), dtype=np.int64).astype(np.int32)
+    sa = rng(10).uniform(0.001, 0.02, 64).astype(np.float32)
+    sb = rng(11).uniform(0.001, 0.02, 96).astype(np.float32)
+    want = ((c.astype(np.float32) * sa[:, None]).astype(np.float32) * sb[None, :]).astype(np.float16)
+    got = oracle.dequant_i32_f16(c, sa, sb)
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+    # dropping the column scale is caught
+    assert not np.array_equal(oracle.dequant_i32_f16(c, sa, None).view(np.uint16), want.view(np.uint16))
+    # small accumulators land in the fp16 subnormal range and still agree
+    tiny = rng(12).integers(-3, 4, (8, 8)).astype(np.int32)
+    want_t = ((tiny.astype(np.float32) * sa[:8, None]) * sb[None, :8]).astype(np.float16)
+    assert np.array_equal(oracle.dequant_i32_f16(tiny, sa[:8], sb[:8]).view(np.uint16), want_t.view(np.uint16))
+
+
+# --------------------------------------------------------------------------- #
+# Floating matmul
+# --------------------------------------------------------------------------- #
+
+def _bound(a, b):
+    """binary32 accumulation bound K*eps*sum|a||b| plus the output rounding."""
+    K = a.shape[1]
+    return K * 2.0 ** -24 * (np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64))
+
+
+def test_matmul_f16_within_accumulation_bound():
+    a = rng(13).uniform(-1, 1, (48, 300)).astype(np.float16)
+    b = rng(14).uniform(-1, 1, (300, 80)).astype(np.float16)
+    exact = a.astype(np.float64) @ b.astype(np.float64)
+    got32 = oracle.matmul(a, b, out_dtype=np.float32).astype(np.float64)
+    assert (np.abs(got32 - exact) <= _bound(a, b) + 1e-12).all()
+    got16 = oracle.matmul(a, b).astype(np.float64)
+    assert np.array_equal(got16, got32.astype(np.float32).astype(np.float16).astype(np.float64))
+    assert np.array_equal(oracle.matmul(a, np.ascontiguousarray(b.T), b_trans=True), oracle.matmul(a, b))
+
+
+def test_matmul_identity_is_exact():
+    a = rng(15).normal(0, 3, (17, 64)).astype(np.float16)
+    eye = np.eye(64, dtype=np.float16)
+    assert np.array_equal(oracle.matmul(a, eye).view(np.uint16), a.view(np.uint16))
+
+
+def test_matmul_bf16_and_w8a16():
+    a32 = rng(16).uniform(-1, 1, (20, 96)).astype(np.float32)
+    b32 = rng(17).uniform(-1, 1, (96, 24)).astype(np.float32)
+    ab, bb = oracle.f32_to_bf16_bits(a32), oracle.f32_to_bf16_bits(b32)
+    got = oracle.bf16_bits_to_f32(oracle.matmul(ab, bb, a_bf16=True, b_bf16=True, out_bf16=True))
+    exact = oracle.bf16_bits_to_f32(ab).astype(np.float64) @ oracle.bf16_bits_to_f32(bb).astype(np.float64)
+    assert_close(got, exact, 2 ** -8, 1e-6, "bf16 matmul")
+    x = rng(18).normal(0, 1, (4, 256)).astype(np.float16)
+    w = rng(19).integers(-127, 128, (256, 40), dtype=np.int8)
+    s = rng(20).uniform(0.001, 0.02, 40).astype(np.float32)
+    exact = (x.astype(np.float64) @ w.astype(np.float64)) * s.astype(np.float64)
+    got = oracle.matmul(x, w, scale_n=s).astype(np.float64)
+    assert_close(got, exact, 1e-3, 1e-4, "w8a16")
+    assert not np.allclose(oracle.matmul(x, w).astype(np.float64), exact, rtol=1e-2)  # scale not dropped
+
+
+def test_matmul_residual_term():
+    a = rng(21).uniform(-1, 1, (16, 32)).astype(np.float16)
+    b = rng(22).uniform(-1, 1, (32, 16)).astype(np.float16)
+    r = rng(23).normal(0, 1, (16, 16)).astype(np.float32)
+    got = oracle.matmul(a, b, residual=r, out_dtype=np.float32)
+    want = oracle.matmul(a, b, out_dtype=np.float32) + r
+    assert np.array_equal(got, want)
+
+
+# --------------------------------------------------------------------------- #
+# Row reductions
+# --------------------------------------------------------------------------- #
+
+def _softmax64(x):
+    x = x.astype(np.float64)
+    e = np.exp(x - x.max(axis=1, keepdims=True))
+    return e / e.sum(axis=1, keepdims=True)
+
+
+def test_softmax_vs_float64_and_invariants():
+    x = rng(24).normal(0, 2, (64, 4096)).astype(np.float32)
+    y = oracle.softmax(x)
+    assert_close(y, _softmax64(x), 1e-5, 1e-8, "softmax f32")
+    assert np.allclose(y.astype(np.float64).sum(axis=1), 1.0, atol=1e-5)
+    # shift invariance (integer shifts are exact in binary32 at this range)
+    assert_close(oracle.softmax(x + np.float32(8.0)), y, 1e-5, 1e-9, "shift")
+    u = np.full((3, 100), 0.25, np.float32)
+    assert np.allclose(oracle.softmax(u), 0.01, rtol=1e-6)
+    xh = x.astype(np.float16)
+    assert_close(oracle.softmax(xh).astype(np.float64), _softmax64(xh), 1e-3, 1e-4, "softmax f16")
+
+
+def test_softmax_reference_test_against_torch():
+    """test/python/triton/test_softmax.py:75-93: 128x128, torch.rand inputs,
+    torch softmax reference, atol 1e-3 (fp16) / 1e-5 (fp32)."""
+    torch = pytest.importorskip("torch")
+    for dt, atol in ((torch.float16, 1e-3), (torch.float32, 1e-5)):
+        x = torch.rand(128, 128, dtype=dt, generator=torch.Generator().manual_seed(0))
+        got = torch.from_numpy(oracle.softmax(x.numpy()))
+        ref = torch.nn.functional.softmax(x.float(), dim=1).to(dt)
+        assert torch.allclose(got, ref, atol=atol)
+
+
+def test_rmsnorm_vs_float64_and_scale_invariance():
+    x = rng(25).normal(0, 2, (32, 4096)).astype(np.float32)
+    g = rng(26).normal(1, 0.1, 4096).astype(np.float32)
+    x64 = x.astype(np.float64)
+    want = x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + 1e-6) * g
+    y = oracle.rmsnorm(x, g, 1e-6)
+    assert_close(y, want, 1e-5, 1e-6, "rmsnorm")
+    assert_close(oracle.rmsnorm(x * np.float32(4.0), g, 0.0), oracle.rmsnorm(x, g, 0.0), 1e-5, 1e-6, "scale")
+    assert_close(oracle.rmsnorm(x, None, 1e-6), want / g, 1e-5, 1e-6, "no gamma")
+
+
+def test_rmsnorm_reference_test_against_torch():
+    """test/python/triton/test_rms_norm.py:61-86: 127x513, eps 1e-5, torch
+    rms_norm reference, atol 1e-2."""
+    torch = pytest.importorskip("torch")
+    for dt in (torch.float16, torch.float32):
+        g = torch.Generator().manual_seed(1)
+        x = torch.rand(127, 513, dtype=dt, generator=g)
+        w = torch.rand(513, dtype=dt, generator=g)
+        got = torch.from_numpy(oracle.rmsnorm(x.numpy(), w.numpy(), 1e-5))
+        ref = torch.nn.functional.rms_norm(x.float(), (513,), weight=w.float(), eps=1e-5).to(dt)
+        assert torch.allclose(got, ref, atol=1e-2)
+
+
+def test_layernorm_vs_float64_and_torch():
+    """test/python/triton/test_layer_norm.py:84-112: 27x8192 fp32, eps 1e-5,
+    torch layer_norm reference, atol 1e-5; mean / rstd as stored at :70-72."""
+    torch = pytest.importorskip("torch")
+    g = torch.Generator().manual_seed(2)
+    x = torch.rand(27, 8192, dtype=torch.float32, generator=g)
+    w = torch.rand(8192, dtype=torch.float32, generator=g)
+    b = torch.rand(8192, dtype=torch.float32, generator=g)
+    y, mean, rstd = oracle.layernorm(x.numpy(), w.numpy(), b.numpy(), 1e-5)
+    ref = torch.nn.functional.layer_norm(x, (8192,), weight=w, bias=b, eps=1e-5)
+    assert torch.allclose(torch.from_numpy(y), ref, atol=1e-5)
+    x64 = x.numpy().astype(np.float64)
+    assert_close(mean, x64.mean(axis=1), 2e-5, 1e-7, "mean")  # sequential binary32 sum of 8192
+    assert_close(rstd, 1 / np.sqrt(x64.var(axis=1) + 1e-5), 5e-5, 0, "rstd")
+
+
+def test_silu_mul_vs_float64():
+    gv = rng(27).normal(0, 3, (8, 500)).astype(np.float32)
+    uv = rng(28).normal(0, 1, (8, 500)).astype(np.float32)
+    g64, u64 = gv.astype(np.float64), uv.astype(np.float64)
+    assert_close(oracle.silu_mul(gv, uv), g64 / (1 + np.exp(-g64)) * u64, 1e-5, 1e-7, "silu_mul")
+
+
+# --------------------------------------------------------------------------- #
+# Committed fixtures (tests/golden/, written by tests/golden/make_golden.py)
+# --------------------------------------------------------------------------- #
+
+def test_golden_fixtures_reproduce():
+    meta = json.loads((GOLDEN / "golden.json").read_text())
+    data = np.load(GOLDEN / "golden.npz", allow_pickle=False)
+    a, b = data["i8_a"], data["i8_b"]
+    assert np.array_equal(oracle.gemm_i8_i32(a, b), data["i8_c"])
+    assert np.array_equal(oracle.dequant_i32_f16(data["i8_c"], data["i8_sa"], data["i8_sb"]).view(np.uint16),
+                          data["i8_c16"])
+    assert np.array_equal(oracle.softmax(data["sm_x"]).view(np.uint16), data["sm_y"])
+    assert np.array_equal(oracle.rmsnorm(data["rms_x"], data["rms_g"], meta["rms_eps"]).view(np.uint16),
+                          data["rms_y"])
+    assert meta["seed"] == 20261201
