@@ -74,7 +74,7 @@ def build(verbose: bool = False) -> Path:
     vscript.write_text("{ global: hx_*; local: *; };\n")
     tmp = OUT.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs),
-           f"-Wl,--version-script={vscript}", "-o", str(tmp)]
+           f"-Wl,--version-script={vscript}", "-Wl,--no-undefined", "-o", str(tmp)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)

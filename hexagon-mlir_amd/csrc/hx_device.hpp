@@ -6,7 +6,22 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 namespace hx {
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I = 0..N-1, as a
+// fold expression, so indices into register arrays are constants no matter
+// how large the body is (an unroller threshold cannot demote the array to
+// scratch memory).
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 typedef _Float16 f16;
 typedef uint16_t bf16_bits;  // bf16 is carried as raw bits and converted by hand

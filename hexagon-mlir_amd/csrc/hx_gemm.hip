@@ -101,31 +101,53 @@ __device__ __forceinline__ void tile_of(int tiles_m, int tiles_n, int& tm, int& 
   tn = in_group / gm;
 }
 
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// One direct-to-LDS load: every lane fetches 16 bytes at voff + soff of the
+// buffer and the wave's 64 results land contiguously (lane order) at `lds`
+// (a wave-uniform address).  A plain function, not a template member: the
+// builtin inside a kernel template stops the host pass from emitting the
+// kernel's launch stub.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* lds, uint32_t voff,
+                                      uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voff, soff, 0, 0);
+}
+
+// vmcnt(0): this wave's direct-to-LDS loads have landed.
+__device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 template <int MODE, int BM, int BN, int WM, int WN, int EPI>
 __global__ void __launch_bounds__(64 * WM * WN)
 gemm_kernel(GemmArgs p) {
   typedef ModeTraits<MODE> T;
   typedef typename T::Acc Acc;
-  constexpr int NT = 64 * WM * WN;
+  constexpr int NW = WM * WN;
   constexpr int NB = (EPI == GE_SWIGLU) ? 2 : 1;
   constexpr int A_BYTES = BM * 128;
   constexpr int B_BYTES = BN * T::BROW;
   constexpr int STAGE = A_BYTES + NB * B_BYTES;
-  constexpr int CA = 8;
-  constexpr int CB = T::BROW / 16;
-  constexpr int LA = BM * CA / NT;
-  constexpr int LB = BN * CB / NT;
-  static_assert((BM * CA) % NT == 0 && (BN * CB) % NT == 0, "load split");
+  // 1 KiB direct-load blocks: 8 rows of a 128-byte row, or 16 of a 64-byte row
+  constexpr int A_BLK = A_BYTES / 1024;
+  constexpr int B_BLK = B_BYTES / 1024;
+  constexpr int B_RPB = 1024 / T::BROW;
+  constexpr int A_PER_W = A_BLK / NW;
+  constexpr int B_PER_W = B_BLK / NW;
+  static_assert(A_BLK % NW == 0 && B_BLK % NW == 0, "block split");
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
   static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
   static_assert(2 * STAGE <= 160 * 1024, "LDS budget");
 
-  __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+  // Two stages as two distinct arrays: the compiler can then see that a
+  // direct load into one stage never aliases the reads of the other.
+  __shared__ __attribute__((aligned(1024))) char st0[STAGE];
+  __shared__ __attribute__((aligned(1024))) char st1[STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // wave index as a provably uniform (scalar) value: the direct-load LDS
+  // address and scalar offset derive from it and must live in SGPRs
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const int tiles_m = (int)((p.M + BM - 1) / BM);
   const int tiles_n = (int)((p.N + BN - 1) / BN);
@@ -137,11 +159,9 @@ gemm_kernel(GemmArgs p) {
   const uint32_t lda_b = (uint32_t)(p.lda * T::EA);
   const uint32_t ldb_b = (uint32_t)(p.ldb * T::EB);
   const uint32_t ka_bytes = (uint32_t)(p.K * T::EA);
-  const uint32_t kb_bytes = (uint32_t)(p.K * T::EB);
 
-  const char* abase = reinterpret_cast<const char*>(p.a) + m0 * lda_b;
   __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)abase, 0, (int)(rows_a * lda_b), 0x00020000);
+      (void*)(reinterpret_cast<const char*>(p.a) + m0 * lda_b), 0, (int)(rows_a * lda_b), 0x00020000);
   __amdgpu_buffer_rsrc_t rb[NB];
   rb[0] = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(reinterpret_cast<const char*>(p.b) + n0 * ldb_b), 0, (int)(rows_b * ldb_b), 0x00020000);
@@ -150,45 +170,49 @@ gemm_kernel(GemmArgs p) {
         (void*)(reinterpret_cast<const char*>(p.b2) + n0 * ldb_b), 0, (int)(rows_b * ldb_b),
         0x00020000);
 
+  // Direct-load addressing.  Lane L of a 1 KiB block fills physical chunk
+  // L % cpr of block row L / cpr (cpr = 16-byte chunks per row) and fetches
+  // the logical chunk the XOR swizzle maps there.  The block's first row is
+  // a wave-uniform offset (the instruction's scalar offset); the lane part
+  // is a row offset plus the swizzled chunk, recomputed per block from the
+  // block index rather than kept in registers.
+  const uint32_t a_lane_row = (uint32_t)(lane >> 3) * lda_b;
+  const uint32_t b_lane_row = (uint32_t)(T::BROW == 128 ? (lane >> 3) : (lane >> 2)) * ldb_b;
   const int nk = (int)((p.K + T::BK - 1) / T::BK);
+  const uint32_t kb_bytes = (uint32_t)(p.K * T::EB);
 
-  v4i ga[LA];
-  v4i gb[NB][LB];
-  auto gload = [&](int kt) {
+  // Enqueue the direct loads of K-stage kt into `st`.  Only the last stage
+  // can overhang K; its chunks past K read as zero (offset out of range).
+  auto dma_stage = [&](char* st, int kt) {
+    const uint32_t ka = (uint32_t)kt * 128u;
+    const uint32_t kb = (uint32_t)kt * T::BROW;
+    const bool tail = ka + 128u > ka_bytes;
 #pragma unroll
-    for (int i = 0; i < LA; ++i) {
-      const int q = tid + i * NT, row = q / CA, c = q % CA;
-      const uint32_t kbyte = (uint32_t)kt * 128u + (uint32_t)c * 16u;
-      const uint32_t off = kbyte < ka_bytes ? (uint32_t)row * lda_b + kbyte : 0x80000000u;
-      ga[i] = buf_load16(ra, off);
+    for (int i = 0; i < A_PER_W; ++i) {
+      const int blk = wave + i * NW;
+      // row = 8*blk + lane/8, so swz128(row) = (lane/8 ^ blk) & 7
+      const uint32_t kc = (uint32_t)(((lane & 7) ^ (lane >> 3) ^ blk) & 7) * 16u;
+      uint32_t off = a_lane_row + kc + ka;
+      if (tail && ka + kc >= ka_bytes) off = 0x80000000u;
+      dma16(ra, st + blk * 1024, off, (uint32_t)blk * 8u * lda_b);
     }
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int i = 0; i < LB; ++i) {
-        const int q = tid + i * NT, row = q / CB, c = q % CB;
-        const uint32_t kbyte = (uint32_t)kt * T::BROW + (uint32_t)c * 16u;
-        const uint32_t off = kbyte < kb_bytes ? (uint32_t)row * ldb_b + kbyte : 0x80000000u;
-        gb[nb][i] = buf_load16(rb[nb], off);
+      for (int i = 0; i < B_PER_W; ++i) {
+        const int blk = wave + i * NW;
+        uint32_t kc;
+        if constexpr (T::BROW == 128) {
+          kc = (uint32_t)(((lane & 7) ^ (lane >> 3) ^ blk) & 7) * 16u;
+        } else {
+          const int row = blk * 16 + (lane >> 2);
+          kc = (uint32_t)((lane & 3) ^ swz64(row)) * 16u;
+        }
+        uint32_t off = b_lane_row + kc + kb;
+        if (tail && kb + kc >= kb_bytes) off = 0x80000000u;
+        dma16(rb[nb], st + A_BYTES + nb * B_BYTES + blk * 1024, off,
+              (uint32_t)blk * (uint32_t)B_RPB * ldb_b);
       }
-  };
-  auto sstore = [&](int stage) {
-    char* sa = smem + stage * STAGE;
-#pragma unroll
-    for (int i = 0; i < LA; ++i) {
-      const int q = tid + i * NT, row = q / CA, c = q % CA;
-      *reinterpret_cast<v4i*>(sa + row * 128 + ((c ^ swz128(row)) << 4)) = ga[i];
-    }
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      char* sb = sa + A_BYTES + nb * B_BYTES;
-#pragma unroll
-      for (int i = 0; i < LB; ++i) {
-        const int q = tid + i * NT, row = q / CB, c = q % CB;
-        const int pc = (T::BROW == 128) ? (c ^ swz128(row)) : (c ^ swz64(row));
-        *reinterpret_cast<v4i*>(sb + row * T::BROW + (pc << 4)) = gb[nb][i];
-      }
-    }
   };
 
   Acc acc[NB][TM][TN];
@@ -201,14 +225,7 @@ gemm_kernel(GemmArgs p) {
 
   const int lrow = lane & 31, lg = lane >> 5;
 
-  gload(0);
-  sstore(0);
-  __syncthreads();
-
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) gload(kt + 1);
-    const char* sa = smem + cur * STAGE;
+  auto compute = [&](const char* sa) {
     if constexpr (MODE != GM_W8) {
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
@@ -272,48 +289,102 @@ gemm_kernel(GemmArgs p) {
         }
       }
     }
-    if (kt + 1 < nk) sstore(cur ^ 1);
+  };
+
+  // Ping-pong over the two stages: the loads of stage k+1 are in flight
+  // while stage k is consumed; one wait + barrier per stage.  The steady
+  // state loop body is straight-line code (no conditional loads), so the
+  // accumulators stay in one register class across iterations; the last one
+  // or two stages are peeled after it.
+  dma_stage(st0, 0);
+  wait_dma();
+  __syncthreads();
+  // sched_barrier(0) pins each stage's load issue ahead of the MFMA block;
+  // left alone, the scheduler sinks the loads to just before the wait,
+  // which serializes load latency with compute.
+  int kt = 0;
+  for (; kt + 2 < nk; kt += 2) {
+    dma_stage(st1, kt + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(st0);
+    wait_dma();
     __syncthreads();
+    dma_stage(st0, kt + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(st1);
+    wait_dma();
+    __syncthreads();
+  }
+  if (kt + 1 < nk) {
+    dma_stage(st1, kt + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(st0);
+    wait_dma();
+    __syncthreads();
+    compute(st1);
+  } else {
+    compute(st0);
   }
 
   // ---- epilogue ----------------------------------------------------------
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int64_t col = n0 + wn * WTN + j * 32 + lrow;
-      if (col >= p.N) continue;
-      float cs = 1.f, cs2 = 1.f;
-      if (p.col_scale) cs = p.col_scale[col];
-      if constexpr (NB == 2) cs2 = p.col_scale2 ? p.col_scale2[col] : 1.f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
-        if (row >= p.M) continue;
-        const int64_t idx = row * p.ldc + col;
-        if constexpr (MODE == GM_I8) {
-          const int v = acc[0][i][j][r];
-          if (p.out_dtype == DT_I32) {
-            reinterpret_cast<int*>(p.c)[idx] = v;
-          } else {
-            float t = (float)v;
-            if (p.row_scale) t = t * p.row_scale[row];
-            if (p.col_scale) t = t * cs;
-            store_out(p.c, p.out_dtype, idx, t);
+  // Lane (lrow, lg) of sub-tile (i, j) holds column lrow and rows
+  // 8*(r/4) + 4*lg + (r%4) in accumulator register r.  All loops are
+  // compile-time (static_for), so the accumulators never leave registers;
+  // per-column scales are loaded once per sub-tile column, per-row scales
+  // once per sub-tile row.
+  const int64_t row_base = m0 + wm * WTM + 4 * lg;
+  const int64_t col_base = n0 + wn * WTN + lrow;
+  float cs[TN], cs2[TN];
+  static_for<TN>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    const int64_t col = col_base + j * 32;
+    cs[j] = (p.col_scale && col < p.N) ? p.col_scale[col] : 1.f;
+    cs2[j] = (NB == 2 && p.col_scale2 && col < p.N) ? p.col_scale2[col] : 1.f;
+  });
+  const int odt = p.out_dtype;
+  static_for<TM>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    float rs[16];
+    static_for<16>([&](auto rc) {
+      constexpr int r = decltype(rc)::value;
+      const int64_t row = row_base + i * 32 + 8 * (r >> 2) + (r & 3);
+      rs[r] = (MODE == GM_I8 && p.row_scale && row < p.M) ? p.row_scale[row] : 1.f;
+    });
+    static_for<TN>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      const int64_t col = col_base + j * 32;
+      if (col < p.N) {
+        static_for<16>([&](auto rc) {
+          constexpr int r = decltype(rc)::value;
+          const int64_t row = row_base + i * 32 + 8 * (r >> 2) + (r & 3);
+          if (row < p.M) {
+            const int64_t idx = row * p.ldc + col;
+            if constexpr (MODE == GM_I8) {
+              const int v = acc[0][i][j][r];
+              if (odt == DT_I32) {
+                reinterpret_cast<int*>(p.c)[idx] = v;
+              } else {
+                float t = (float)v;
+                if (p.row_scale) t = t * rs[r];
+                if (p.col_scale) t = t * cs[j];
+                store_out(p.c, odt, idx, t);
+              }
+            } else if constexpr (EPI == GE_SWIGLU) {
+              const float g = f16_bits_to_f32(f32_to_f16_bits(acc[0][i][j][r] * cs[j]));
+              const float u = f16_bits_to_f32(f32_to_f16_bits(acc[NB - 1][i][j][r] * cs2[j]));
+              const float sg = g / (1.0f + fast_exp(-g));
+              reinterpret_cast<uint16_t*>(p.c)[idx] = f32_to_f16_bits(sg * u);
+            } else {
+              float t = acc[0][i][j][r];
+              if (p.col_scale) t = t * cs[j];
+              if (p.res) t = t + load_any(p.res, p.res_dtype, row * p.ldr + col);
+              store_out(p.c, odt, idx, t);
+            }
           }
-        } else if constexpr (EPI == GE_SWIGLU) {
-          const float g = f16_bits_to_f32(f32_to_f16_bits(acc[0][i][j][r] * cs));
-          const float u = f16_bits_to_f32(f32_to_f16_bits(acc[1][i][j][r] * cs2));
-          const float sg = g / (1.0f + fast_exp(-g));
-          reinterpret_cast<uint16_t*>(p.c)[idx] = f32_to_f16_bits(sg * u);
-        } else {
-          float t = acc[0][i][j][r];
-          if (p.col_scale) t = t * cs;
-          if (p.res) t = t + load_any(p.res, p.res_dtype, row * p.ldr + col);
-          store_out(p.c, p.out_dtype, idx, t);
-        }
+        });
       }
-    }
+    });
+  });
 }
 
 // ---------------------------------------------------------------------------

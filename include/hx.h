@@ -10,9 +10,10 @@
  *
  * Conventions (all entry points):
  *   - Tensors are MLIR-style strided memref descriptors (hx_memref2d /
- *     hx_memref1d), the layout the reference's compiled kernels receive
- *     (test/utils/dsp/include/tensor.h:73-90, CRunnerUtils.h
- *     MemRefDescriptor<T,N>: allocated, aligned, offset, sizes, strides).
+ *     hx_memref1d), field for field the MemRefDescriptor<T,N> the
+ *     reference's compiled kernels receive (test/utils/dsp/include/
+ *     common.h:15-21: allocated, aligned, offset, sizes[N], strides[N];
+ *     built by Tensor::toMemRefDesc, tensor.h:73-90).
  *     Strides and offsets are in elements.  The innermost stride must be 1;
  *     the outer stride may exceed the row length (the multi-span output ABI
  *     of test/python/triton/test_matmul_multispan.py:71-78).
