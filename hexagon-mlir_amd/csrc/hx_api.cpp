@@ -82,12 +82,8 @@ static int current_device(int* dev) {
 }
 
 struct Workspace {
-  char* buf = nullptr;       // carved by the top-level entry point of a call
+  char* buf = nullptr;  // carved by the top-level entry point of a call
   size_t bytes = 0;
-  float* part = nullptr;     // split-K partial sums of the GEMV (its own region)
-  size_t part_bytes = 0;
-  unsigned* counters = nullptr;
-  size_t ncounters = 0;
 };
 static std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 
@@ -110,51 +106,6 @@ static int ws_get(hipStream_t s, size_t bytes, char** out) {
     w.bytes = nb;
   }
   *out = w.buf;
-  return HX_OK;
-}
-
-// Split-K partial sums.  A region of its own, so that a GEMV launched from
-// inside an entry point never aliases the scratch that entry point carved.
-static int ws_partials(hipStream_t s, size_t bytes, float** out) {
-  int dev;
-  int rc = current_device(&dev);
-  if (rc) return rc;
-  std::lock_guard<std::mutex> lk(g_mu);
-  Workspace& w = g_ws[{dev, s}];
-  if (w.part_bytes < bytes) {
-    size_t nb = bytes > 2 * w.part_bytes ? bytes : 2 * w.part_bytes;
-    nb = (nb + 4095) & ~(size_t)4095;
-    HX_HIP_TRY(hipStreamSynchronize(s));
-    if (w.part) HX_HIP_TRY(hipFree(w.part));
-    w.part = nullptr;
-    w.part_bytes = 0;
-    if (hipMalloc((void**)&w.part, nb) != hipSuccess) return fail(HX_ERR_NOMEM, "partials of %zu bytes", nb);
-    w.part_bytes = nb;
-  }
-  *out = w.part;
-  return HX_OK;
-}
-
-// Zero-initialised ticket counters (reset to zero by the kernels that use
-// them, so they are cleared only when allocated).
-static int ws_counters(hipStream_t s, size_t n, unsigned** out) {
-  int dev;
-  int rc = current_device(&dev);
-  if (rc) return rc;
-  std::lock_guard<std::mutex> lk(g_mu);
-  Workspace& w = g_ws[{dev, s}];
-  if (w.ncounters < n) {
-    size_t nn = n > 2 * w.ncounters ? n : 2 * w.ncounters;
-    HX_HIP_TRY(hipStreamSynchronize(s));
-    if (w.counters) HX_HIP_TRY(hipFree(w.counters));
-    w.counters = nullptr;
-    w.ncounters = 0;
-    if (hipMalloc(&w.counters, nn * sizeof(unsigned)) != hipSuccess)
-      return fail(HX_ERR_NOMEM, "counters");
-    HX_HIP_TRY(hipMemset(w.counters, 0, nn * sizeof(unsigned)));
-    w.ncounters = nn;
-  }
-  *out = w.counters;
   return HX_OK;
 }
 
@@ -252,7 +203,7 @@ static std::vector<int> family_indices(int op) {
   std::vector<int> out;
   int mode, epi;
   if (op == HX_OP_GEMV_W8) {
-    for (int i = 0; i < gemv_config_count(); ++i) out.push_back(i);
+    for (int i = 0; i < gemv_packed_config_count(); ++i) out.push_back(i);
     return out;
   }
   if (!op_gemm(op, &mode, &epi)) return out;
@@ -282,8 +233,11 @@ static int resolve_gemm(int op, int64_t M, int64_t N, int64_t K) {
 }
 static int resolve_gemv(int64_t M, int64_t N, int64_t K) {
   const int pin = pinned(HX_OP_GEMV_W8, M, N, K);
-  if (pin >= 0 && pin < gemv_config_count()) return pin;
-  return gemv_default_config(M, N, K);
+  if (pin >= 0 && pin < gemv_packed_config_count()) return pin;
+  (void)N; (void)K;
+  // untuned choice from the MI355X sweep: one column tile per workgroup for
+  // few rows; four tiles (activation fragments reused 4x) for larger M
+  return M <= 8 ? 1 : 2;
 }
 
 static int run_gemm(int op, GemmArgs& a, hipStream_t s) {
@@ -298,19 +252,7 @@ static int run_gemm(int op, GemmArgs& a, hipStream_t s) {
 }
 
 static int run_gemv(GemvArgs& a, hipStream_t s) {
-  const int cfg = resolve_gemv(a.M, a.N, a.K);
-  const int64_t pf = gemv_partial_floats(cfg, a.M, a.N);
-  if (pf > 0) {
-    float* part;
-    int rc = ws_partials(s, (size_t)pf * sizeof(float), &part);
-    if (rc) return rc;
-    unsigned* ctr;
-    rc = ws_counters(s, (size_t)gemv_counter_count(cfg, a.N), &ctr);
-    if (rc) return rc;
-    a.partial = part;
-    a.counters = ctr;
-  }
-  return map_internal(launch_gemv_w8a16(cfg, a, s), "gemv_w8a16");
+  return map_internal(launch_gemv_w8a16(a, s), "gemv_w8a16");
 }
 
 // ---------------------------------------------------------------------------
@@ -553,8 +495,9 @@ struct hx_weight {
   int device;
   int64_t K, N;
   int dtype;
-  void* image;    // [N][K], K-contiguous
-  float* scale;   // [N] or null
+  void* image;     // [N][K], K-contiguous (the GEMM operand)
+  int8_t* packed;  // int8 only: MFMA-fragment-ordered copy for the decode GEMV
+  float* scale;    // [N] or null
   uint64_t hash;
   int refcount;
 };
@@ -636,7 +579,21 @@ extern "C" int hx_weight_register(const hx_memref2d* w, int w_dtype, int w_layou
       return HX_OK;
     }
   }
-  hx_weight* x = new hx_weight{dev, K, N, w_dtype, image, sc, key, 1};
+  int8_t* packed = nullptr;
+  if (w_dtype == HX_I8) {
+    if (hipMalloc((void**)&packed, (size_t)gemv_packed_bytes(N, K)) != hipSuccess) {
+      cleanup();
+      return fail(HX_ERR_NOMEM, "packed weight image");
+    }
+    rc = map_internal(launch_gemv_pack((const int8_t*)image, K, N, K, packed, s), "gemv pack");
+    hipError_t se = hipStreamSynchronize(s);
+    if (rc || se != hipSuccess) {
+      (void)hipFree(packed);
+      cleanup();
+      return rc ? rc : fail(HX_ERR_HIP, "gemv pack: %s", hipGetErrorString(se));
+    }
+  }
+  hx_weight* x = new hx_weight{dev, K, N, w_dtype, image, packed, sc, key, 1};
   g_weights.insert(x);
   *out = x;
   return HX_OK;
@@ -661,6 +618,7 @@ extern "C" int hx_weight_release(hx_weight_t w) {
   (void)hipSetDevice(x->device);
   (void)hipDeviceSynchronize();  // no kernel may still read the image
   (void)hipFree(x->image);
+  if (x->packed) (void)hipFree(x->packed);
   if (x->scale) (void)hipFree(x->scale);
   (void)hipSetDevice(cur);
   delete x;
@@ -683,11 +641,14 @@ static int matmul_resident_impl(const View2& vx, hx_weight* w, const View2* vr, 
                                 const View2& vy, int y_dt, hipStream_t s) {
   const int64_t M = vx.rows;
   if (M == 0) return HX_OK;
-  if (w->dtype == HX_I8 && M <= 16 && !vr && y_dt == HX_F16) {
+  // The packed GEMV reads activations as 8-element (16-byte) groups.
+  if (w->dtype == HX_I8 && w->packed && M <= 16 && !vr && y_dt == HX_F16 && w->K % 8 == 0 &&
+      ((uintptr_t)vx.p & 15u) == 0 && (vx.ld * 2) % 16 == 0) {
     GemvArgs v{};
-    v.x = vx.p; v.ldx = vx.ld; v.w = (const int8_t*)w->image; v.ldw = w->K;
+    v.x = vx.p; v.ldx = vx.ld; v.w = nullptr; v.ldw = 0;
     v.scale = w->scale; v.y = vy.p; v.ldy = vy.ld; v.M = M; v.N = w->N; v.K = w->K;
-    if (gemv_fast_ok(v)) return run_gemv(v, s);
+    return map_internal(launch_gemv_packed(resolve_gemv(M, w->N, w->K), v, w->packed, s),
+                        "gemv_packed");
   }
   GemmArgs g{};
   g.a = vx.p; g.lda = vx.ld;
@@ -802,11 +763,11 @@ extern "C" int hx_config_get(int op, int index, hx_kernel_config* out) {
   out->op = op;
   out->index = index;
   if (op == HX_OP_GEMV_W8) {
-    const GemvConfig* c = gemv_config(idx[index]);
-    out->bm = 16; out->bn = 16 * c->ct; out->bk = 128;
-    out->waves_m = 1; out->waves_n = 4;
-    out->lds_stages = 0; out->split_k = c->ks; out->col_tiles = c->ct;
-    out->lds_bytes = 4 * c->ct * 64 * 4 * 4 + 4;
+    const GemvConfig* c = gemv_packed_config(idx[index]);
+    out->bm = 16; out->bn = 16 * c->ct; out->bk = 64;
+    out->waves_m = c->kw; out->waves_n = 1;
+    out->lds_stages = 0; out->split_k = c->kw; out->col_tiles = c->ct;
+    out->lds_bytes = c->kw * c->ct * 64 * 4 * 4;
     snprintf(out->name, sizeof(out->name), "gemv_%s", c->name);
     return HX_OK;
   }

@@ -8,18 +8,17 @@
 // (QHB/lib/Transforms/ScheduleMatmulForHVXPass.cpp:169-196) with the
 // dequantised weight (sitofp, then the per-channel scale).
 //
-// MI355X design: the kernel is an HBM stream over the int8 weight, read once,
-// K-contiguous ([N][K], the resident image).  One wave owns 16*CT output
-// columns and a slice of K; every 128-wide K window it loads, per column, 128
-// contiguous weight bytes (two 16-byte loads per lane, each covering 64
-// contiguous bytes of 16 rows), widens int8 -> f16 exactly in registers and
-// feeds v_mfma_f32_16x16x32_f16 with the (zero-padded to 16 rows)
-// activations.  Lane group g = lane/16 supplies k = 64*h + 16*g + 8*e + (0..7)
-// in step s = 2h + e for both operands, so every k of the window is summed
-// exactly once.  The four waves of a workgroup split K and reduce through
-// LDS; with KS > 1 workgroups split K further and the last one to finish a
-// column tile (atomic ticket) sums the KS partials in a fixed order, so the
-// result is deterministic.
+// MI355X design: an HBM stream over the int8 weight, read once, widened to
+// f16 exactly in registers and fed to v_mfma_f32_16x16x32_f16 with the
+// activations zero-padded to 16 rows.  Two kernels:
+//   * gemv_packed_kernel -- registered (resident) weights, stored in MFMA
+//     fragment order so that every wave load is one contiguous KiB and each
+//     wave issues its whole K slice before its first MFMA (below);
+//   * gemv_w8a16_kernel -- an unregistered K-contiguous [N][K] weight: per
+//     128-wide K window each lane loads 2 x 16 bytes of one column; lane
+//     group g = lane/16 supplies k = 64*h + 16*g + 8*e + (0..7) in step
+//     s = 2h + e for both operands, so every k is summed exactly once; the
+//     four waves of a workgroup split K and reduce through LDS.
 #include "hx_device.hpp"
 #include "hx_internal.hpp"
 
@@ -29,13 +28,12 @@ __device__ __forceinline__ v4i gv_load16(__amdgpu_buffer_rsrc_t r, uint32_t off)
   return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
 
-template <int CT, int KS>
+template <int CT>
 __global__ void __launch_bounds__(256) gemv_w8a16_kernel(GemvArgs p) {
   constexpr int UNR = 4;  // K windows loaded per batch
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nl = lane & 15, g = lane >> 4;
   const int col_tile = blockIdx.x;
-  const int ks = (KS > 1) ? blockIdx.y : 0;
   const int64_t n0 = (int64_t)col_tile * 16 * CT;
   const int64_t cols_valid = min((int64_t)16 * CT, p.N - n0);
 
@@ -49,10 +47,8 @@ __global__ void __launch_bounds__(256) gemv_w8a16_kernel(GemvArgs p) {
       (void*)p.x, 0, (int)(p.M * ldx_b), 0x00020000);
   const bool xrow = nl < p.M;
 
-  const int nwin = (int)((p.K + 127) / 128);
-  const int per_split = (nwin + KS - 1) / KS;
-  const int w_begin = ks * per_split;
-  const int w_end = min(nwin, w_begin + per_split);
+  const int w_begin = 0;
+  const int w_end = (int)((p.K + 127) / 128);
 
   v4f acc[CT];
 #pragma unroll
@@ -100,7 +96,6 @@ __global__ void __launch_bounds__(256) gemv_w8a16_kernel(GemvArgs p) {
 
   // ---- reduce the four waves' partial tiles through LDS ----------------
   __shared__ float red[4][CT][64][4];
-  __shared__ int is_last;
 #pragma unroll
   for (int c = 0; c < CT; ++c)
 #pragma unroll
@@ -116,84 +111,174 @@ __global__ void __launch_bounds__(256) gemv_w8a16_kernel(GemvArgs p) {
     sum[c] = ((red[0][c][fl][fr] + red[1][c][fl][fr]) + red[2][c][fl][fr]) + red[3][c][fl][fr];
 
   uint16_t* y = reinterpret_cast<uint16_t*>(p.y);
-  if constexpr (KS == 1) {
 #pragma unroll
-    for (int c = 0; c < CT; ++c) {
-      const int64_t n = n0 + 16 * c + (fl & 15);
-      if (fm < p.M && n < p.N)
-        y[(int64_t)fm * p.ldy + n] = f32_to_f16_bits(p.scale ? sum[c] * p.scale[n] : sum[c]);
-    }
-  } else {
-    // partial[ks][m][n]
+  for (int c = 0; c < CT; ++c) {
+    const int64_t n = n0 + 16 * c + (fl & 15);
+    if (fm < p.M && n < p.N)
+      y[(int64_t)fm * p.ldy + n] = f32_to_f16_bits(p.scale ? sum[c] * p.scale[n] : sum[c]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fragment-packed variant (resident weights).  The weight image is stored in
+// MFMA B-fragment order: for column tile t (16 columns) and K chunk j (64 k)
+// one 1 KiB block at ((t * KC) + j) * 1024 (KC = K/64 chunks), in which byte
+// 256*g + 16*c + i holds W[64*j + 16*g + i][16*t + c] (g 0..3, c 0..15,
+// i 0..15).  Lane l of a wave then loads its operand as the 16 contiguous
+// bytes at 16*l: column l % 16, k = 64*j + 16*(l/16) + (0..15), which feeds
+// two v_mfma_f32_16x16x32_f16 steps (e = 0, 1: k = .. + 8*e + (0..7)); the
+// activation operand uses the same k mapping.  Every wave load is one
+// contiguous KiB, and a workgroup of KW waves splits K so that each wave
+// issues its whole K slice (CT tiles x chunks) before the first MFMA: the
+// kernel is a single round trip to HBM.
+// ---------------------------------------------------------------------------
+template <int CT, int KW, int CPW>
+__global__ void __launch_bounds__(64 * KW) gemv_packed_kernel(GemvArgs p, const int8_t* packed,
+                                                              int kchunks) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, g = lane >> 4;
+  const int t0 = blockIdx.x * CT;                    // first column tile
+  const int ntiles = (int)((p.N + 15) / 16);
+  const bool xrow = col < p.M;
+  const uint16_t* x = reinterpret_cast<const uint16_t*>(p.x);
+
+  v4f acc[CT];
 #pragma unroll
-    for (int c = 0; c < CT; ++c) {
-      const int64_t n = n0 + 16 * c + (fl & 15);
-      if (fm < p.M && n < p.N) p.partial[((int64_t)ks * p.M + fm) * p.N + n] = sum[c];
-    }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-      const unsigned ticket = atomicAdd(&p.counters[col_tile], 1u);
-      is_last = (ticket == (unsigned)(KS - 1));
-    }
-    __syncthreads();
-    if (is_last) {
-      __threadfence();
+  for (int c = 0; c < CT; ++c) acc[c] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  // chunks [c0, c0 + CPW * KW) are split as wave w -> c0 + w + KW * u
+  for (int c0 = 0; c0 < kchunks; c0 += CPW * KW) {
+    v4u wq[CPW][CT];
+    v4u xq[CPW][2];
+#pragma unroll
+    for (int u = 0; u < CPW; ++u) {
+      const int j = c0 + wave + KW * u;
+      const bool jv = j < kchunks;
 #pragma unroll
       for (int c = 0; c < CT; ++c) {
-        const int64_t n = n0 + 16 * c + (fl & 15);
-        if (fm < p.M && n < p.N) {
-          float t = 0.f;
-          for (int s = 0; s < KS; ++s)
-            t += __builtin_nontemporal_load(&p.partial[((int64_t)s * p.M + fm) * p.N + n]);
-          y[(int64_t)fm * p.ldy + n] = f32_to_f16_bits(p.scale ? t * p.scale[n] : t);
+        const int t = t0 + c;
+        wq[u][c] = (jv && t < ntiles)
+                       ? __builtin_nontemporal_load(reinterpret_cast<const v4u*>(
+                             packed + ((int64_t)t * kchunks + j) * 1024 + 16 * lane))
+                       : v4u{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int64_t k = (int64_t)j * 64 + 16 * g + 8 * e;
+        xq[u][e] = (jv && xrow && k < p.K)
+                       ? *reinterpret_cast<const v4u*>(x + (int64_t)col * p.ldx + k)
+                       : v4u{0u, 0u, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < CPW; ++u)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const v8h xa = __builtin_bit_cast(v8h, xq[u][e]);
+#pragma unroll
+        for (int c = 0; c < CT; ++c) {
+          const v8h wb = i8x8_to_v8h(wq[u][c][2 * e], wq[u][c][2 * e + 1]);
+          acc[c] = mfma16_f16(xa, wb, acc[c]);
         }
       }
-      if (tid == 0) p.counters[col_tile] = 0u;  // ready for the next call
-    }
   }
+
+  // reduce the KW waves' partial tiles through LDS, thread t finalises
+  // (c, l, r) = (t / 256, (t / 4) % 64, t % 4)
+  __shared__ float red[KW][CT][64][4];
+#pragma unroll
+  for (int c = 0; c < CT; ++c)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][c][lane][r] = acc[c][r];
+  __syncthreads();
+  uint16_t* y = reinterpret_cast<uint16_t*>(p.y);
+  for (int e = tid; e < CT * 256; e += 64 * KW) {
+    const int c = e >> 8, l = (e >> 2) & 63, r = e & 3;
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < KW; ++w) s += red[w][c][l][r];
+    const int m = 4 * (l >> 4) + r;
+    const int64_t n = (int64_t)(t0 + c) * 16 + (l & 15);
+    if (m < p.M && n < p.N) y[(int64_t)m * p.ldy + n] = f32_to_f16_bits(p.scale ? s * p.scale[n] : s);
+  }
+}
+
+// Build the fragment-packed image from a K-contiguous [N][K] int8 weight:
+// packed block (t, j) byte 256*g + 16*c + i = W[n = 16t + c][k = 64j + 16g + i]
+// (zero beyond N or K).  One thread per 16-byte run (t, j, g, c).
+__global__ void __launch_bounds__(256) gemv_pack_kernel(const int8_t* w, int64_t ldw, int64_t N,
+                                                        int64_t K, int kchunks, int8_t* out) {
+  const int64_t ntiles = (N + 15) / 16;
+  const int64_t runs = ntiles * kchunks * 64;
+  for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < runs; q += (int64_t)gridDim.x * 256) {
+    const int64_t blk = q >> 6;
+    const int lane = (int)(q & 63);
+    const int64_t t = blk / kchunks, j = blk - t * kchunks;
+    const int c = lane & 15, g = lane >> 4;
+    const int64_t n = t * 16 + c, k0 = j * 64 + 16 * g;
+    int8_t v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = (n < N && k0 + i < K) ? w[n * ldw + k0 + i] : (int8_t)0;
+    *reinterpret_cast<v4u*>(out + blk * 1024 + 16 * lane) = *reinterpret_cast<const v4u*>(v);
+  }
+}
+
+int64_t gemv_packed_bytes(int64_t N, int64_t K) {
+  return ((N + 15) / 16) * ((K + 63) / 64) * 1024;
+}
+
+int launch_gemv_pack(const int8_t* w, int64_t ldw, int64_t N, int64_t K, int8_t* out, hipStream_t s) {
+  const int kchunks = (int)((K + 63) / 64);
+  const int64_t runs = ((N + 15) / 16) * kchunks * 64;
+  int64_t blocks = (runs + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  gemv_pack_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(w, ldw, N, K, kchunks, out);
+  return HXI_OK;
+}
+
+typedef void (*GemvPackedLaunch)(const GemvArgs&, const int8_t*, int, hipStream_t);
+template <int CT, int KW, int CPW>
+static void gemv_packed_one(const GemvArgs& a, const int8_t* packed, int kchunks, hipStream_t s) {
+  const int64_t ntiles = (a.N + 15) / 16;
+  const int64_t blocks = (ntiles + CT - 1) / CT;
+  gemv_packed_kernel<CT, KW, CPW><<<dim3((unsigned)blocks), dim3(64 * KW), 0, s>>>(a, packed, kchunks);
+}
+struct GemvPackedEntry {
+  GemvConfig cfg;
+  GemvPackedLaunch fn;
+};
+static const GemvPackedEntry kGemvPacked[] = {
+    {{2, 8, "packed_ct2_kw8"}, &gemv_packed_one<2, 8, 8>},
+    {{1, 8, "packed_ct1_kw8"}, &gemv_packed_one<1, 8, 8>},
+    {{4, 8, "packed_ct4_kw8"}, &gemv_packed_one<4, 8, 4>},
+    {{2, 4, "packed_ct2_kw4"}, &gemv_packed_one<2, 4, 8>},
+    {{1, 4, "packed_ct1_kw4"}, &gemv_packed_one<1, 4, 16>},
+};
+int gemv_packed_config_count() { return (int)(sizeof(kGemvPacked) / sizeof(kGemvPacked[0])); }
+const GemvConfig* gemv_packed_config(int idx) {
+  if (idx < 0 || idx >= gemv_packed_config_count()) return nullptr;
+  return &kGemvPacked[idx].cfg;
+}
+int launch_gemv_packed(int cfg_idx, const GemvArgs& a, const int8_t* packed, hipStream_t s) {
+  if (cfg_idx < 0 || cfg_idx >= gemv_packed_config_count()) return HXI_ERR_ARG;
+  if (a.M < 1 || a.M > 16) return HXI_ERR_SHAPE;
+  kGemvPacked[cfg_idx].fn(a, packed, (int)((a.K + 63) / 64), s);
+  return HXI_OK;
 }
 
 typedef void (*GemvLaunch)(const GemvArgs&, hipStream_t);
 
-template <int CT, int KS>
+template <int CT>
 static void gemv_launch_one(const GemvArgs& a, hipStream_t s) {
   const int64_t tiles = (a.N + 16 * CT - 1) / (16 * CT);
-  gemv_w8a16_kernel<CT, KS><<<dim3((unsigned)tiles, KS), dim3(256), 0, s>>>(a);
+  gemv_w8a16_kernel<CT><<<dim3((unsigned)tiles), dim3(256), 0, s>>>(a);
 }
 
-struct GemvEntry {
-  GemvConfig cfg;
-  GemvLaunch fn;
-};
+// Kernels for a K-contiguous [N][K] weight that is not registered (no packed
+// image): 16*CT columns per workgroup, the four waves split K.
+static const GemvLaunch kGemvNK[] = {&gemv_launch_one<1>, &gemv_launch_one<2>, &gemv_launch_one<4>};
 
-static const GemvEntry kGemv[] = {
-    {{1, 1, "ct1_ks1"}, &gemv_launch_one<1, 1>},
-    {{2, 1, "ct2_ks1"}, &gemv_launch_one<2, 1>},
-    {{1, 2, "ct1_ks2"}, &gemv_launch_one<1, 2>},
-    {{2, 2, "ct2_ks2"}, &gemv_launch_one<2, 2>},
-    {{4, 2, "ct4_ks2"}, &gemv_launch_one<4, 2>},
-    {{4, 4, "ct4_ks4"}, &gemv_launch_one<4, 4>},
-    {{2, 4, "ct2_ks4"}, &gemv_launch_one<2, 4>},
-};
-
-int gemv_config_count() { return (int)(sizeof(kGemv) / sizeof(kGemv[0])); }
-const GemvConfig* gemv_config(int idx) {
-  if (idx < 0 || idx >= gemv_config_count()) return nullptr;
-  return &kGemv[idx].cfg;
-}
-int gemv_default_config(int64_t M, int64_t N, int64_t K) {
-  (void)N; (void)K;
-  return M <= 4 ? 0 : 3;
-}
-int64_t gemv_partial_floats(int cfg_idx, int64_t M, int64_t N) {
-  const GemvConfig* c = gemv_config(cfg_idx);
-  return (c && c->ks > 1) ? (int64_t)c->ks * M * N : 0;
-}
-int64_t gemv_counter_count(int cfg_idx, int64_t N) {
-  const GemvConfig* c = gemv_config(cfg_idx);
-  return (c && c->ks > 1) ? (N + 16 * c->ct - 1) / (16 * c->ct) : 0;
-}
 bool gemv_fast_ok(const GemvArgs& a) {
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
   if (a.M < 1 || a.M > 16 || a.N < 1 || a.K < 1) return false;
@@ -203,10 +288,8 @@ bool gemv_fast_ok(const GemvArgs& a) {
   if ((int64_t)a.M * a.ldx * 2 >= ((int64_t)1 << 31)) return false;
   return true;
 }
-int launch_gemv_w8a16(int cfg_idx, const GemvArgs& a, hipStream_t s) {
-  if (cfg_idx < 0 || cfg_idx >= gemv_config_count()) return HXI_ERR_ARG;
-  if (kGemv[cfg_idx].cfg.ks > 1 && (a.partial == nullptr || a.counters == nullptr)) return HXI_ERR_ARG;
-  kGemv[cfg_idx].fn(a, s);
+int launch_gemv_w8a16(const GemvArgs& a, hipStream_t s) {
+  kGemvNK[a.N >= 4096 ? 1 : 0](a, s);
   return HXI_OK;
 }
 

@@ -73,21 +73,21 @@ int launch_gemm_generic(int mode, const GemmArgs& a, hipStream_t s);
 // ---- W8A16 skinny GEMM / GEMV (hx_gemv.hip) ------------------------------
 struct GemvArgs {
   const void* x; int64_t ldx;   // f16 [M][K]
-  const int8_t* w; int64_t ldw; // int8 [N][K]
+  const int8_t* w; int64_t ldw; // int8 [N][K] (unregistered weights)
   const float* scale;           // [N], may be null (scale 1)
   void* y; int64_t ldy;         // f16 [M][N]
   int64_t M, N, K;
-  float* partial;               // [ks][M][N] workspace when ks > 1
-  unsigned* counters;           // [n_tiles] zeroed, when ks > 1
 };
-struct GemvConfig { int ct, ks; const char* name; };
-int gemv_config_count();
-const GemvConfig* gemv_config(int idx);
-int gemv_default_config(int64_t M, int64_t N, int64_t K);
-int64_t gemv_partial_floats(int cfg_idx, int64_t M, int64_t N);
-int64_t gemv_counter_count(int cfg_idx, int64_t N);
+struct GemvConfig { int ct, kw; const char* name; };
 bool gemv_fast_ok(const GemvArgs& a);
-int launch_gemv_w8a16(int cfg_idx, const GemvArgs& a, hipStream_t s);
+// [N][K] weight GEMV (unregistered weights).
+int launch_gemv_w8a16(const GemvArgs& a, hipStream_t s);
+// Fragment-packed resident image for the decode GEMV (see hx_gemv.hip).
+int64_t gemv_packed_bytes(int64_t N, int64_t K);
+int launch_gemv_pack(const int8_t* w_nk, int64_t ldw, int64_t N, int64_t K, int8_t* out, hipStream_t s);
+int gemv_packed_config_count();
+const GemvConfig* gemv_packed_config(int idx);
+int launch_gemv_packed(int cfg_idx, const GemvArgs& a, const int8_t* packed, hipStream_t s);
 
 // ---- layout utilities (hx_pack.hip) --------------------------------------
 // dst[c][r] = src[r][c] for a rows x cols matrix of 1/2/4-byte elements.

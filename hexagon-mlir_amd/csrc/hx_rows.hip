@@ -11,9 +11,10 @@
 // The reference folds each row 128 bytes at a time on HVX and finishes with a
 // log2(lanes) rotate-and-fold (QHB/lib/Conversion/LinalgToLLVM/
 // VectorRowReducePass.cpp:17-28).  Here a row is held in VGPRs by one wave
-// (or by the four waves of a workgroup for long rows): every element is read
-// from HBM once with 16-byte loads and written once, and the reductions are
-// 64-lane butterflies (plus one LDS exchange when four waves share a row).
+// (rows up to 4 KiB) or by the four waves of a workgroup (longer rows):
+// every element is read from HBM once with 16-byte loads and written once,
+// and the reductions are 64-lane butterflies (plus one LDS exchange when
+// four waves share a row).
 // All arithmetic is binary32 with one rounding to the storage type.
 #include "hx_device.hpp"
 #include "hx_internal.hpp"
@@ -211,6 +212,139 @@ __global__ void __launch_bounds__(256) row_kernel(RowArgs a) {
   }
 }
 
+// Vector path: rows are 16-byte aligned and cols is a multiple of the vector
+// width.  The row stays in registers as raw 16-byte vectors (4 VGPRs per
+// vector, independent of the element type) and is widened to binary32 on the
+// fly in each pass, so a wave holding a 4096-wide fp16 row needs ~32 VGPRs
+// for it and eight waves fit per SIMD: every row of an 8192-row problem is
+// in flight at once.  Loads and stores are non-temporal (streamed once).
+template <int DT>
+__device__ __forceinline__ float vec_elem(const v4u& v, int j) {
+  if constexpr (DT == DT_F32) {
+    return __uint_as_float(v[j]);
+  } else {
+    const uint32_t w = v[j >> 1];
+    const uint16_t h = (j & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xffffu);
+    return Elem<DT>::load(h);
+  }
+}
+
+template <int OP, int DT, int WPR, int VPL>
+__global__ void __launch_bounds__(256) row_vec_kernel(RowArgs a) {
+  typedef typename Elem<DT>::storage S;
+  constexpr int EV = 16 / sizeof(S);
+  __shared__ float red[4];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int rows_per_block = 4 / WPR;
+  const int wave_in_row = (WPR == 1) ? 0 : wave;
+  const int64_t row = (int64_t)blockIdx.x * rows_per_block + (WPR == 1 ? wave : 0);
+  if (row >= a.rows) return;
+  const int64_t cols = a.cols;
+  const S* xr = reinterpret_cast<const S*>(a.x) + row * a.ldx;
+  S* yr = reinterpret_cast<S*>(a.y) + row * a.ldy;
+
+  v4u raw[VPL];
+  bool ok[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int64_t c0 = ((int64_t)(i * WPR + wave_in_row) * 64 + lane) * EV;
+    ok[i] = c0 < cols;
+    raw[i] = ok[i] ? __builtin_nontemporal_load(reinterpret_cast<const v4u*>(xr + c0))
+                   : v4u{0u, 0u, 0u, 0u};
+  }
+
+  float scale = 1.f, shift = 0.f;
+  if constexpr (OP == ROW_SOFTMAX) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+      if (ok[i]) {
+#pragma unroll
+        for (int j = 0; j < EV; ++j) m = fmaxf(m, vec_elem<DT>(raw[i], j));
+      }
+    m = group_max<WPR>(m, red);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+      if (ok[i]) {
+#pragma unroll
+        for (int j = 0; j < EV; ++j) s += fast_exp(vec_elem<DT>(raw[i], j) - m);
+      }
+    s = group_sum<WPR>(s, red);
+    scale = 1.0f / s;  // DivToMul: one reciprocal, then multiplies
+    shift = m;
+  } else if constexpr (OP == ROW_RMSNORM) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+#pragma unroll
+      for (int j = 0; j < EV; ++j) {
+        const float v = vec_elem<DT>(raw[i], j);  // zero where not loaded
+        ss += v * v;
+      }
+    ss = group_sum<WPR>(ss, red);
+    scale = 1.0f / sqrtf(ss / (float)cols + a.eps);
+  } else {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+#pragma unroll
+      for (int j = 0; j < EV; ++j) s += vec_elem<DT>(raw[i], j);
+    s = group_sum<WPR>(s, red);
+    const float mean = s / (float)cols;
+    float vs = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+      if (ok[i]) {
+#pragma unroll
+        for (int j = 0; j < EV; ++j) {
+          const float d = vec_elem<DT>(raw[i], j) - mean;
+          vs += d * d;
+        }
+      }
+    vs = group_sum<WPR>(vs, red);
+    scale = 1.0f / sqrtf(vs / (float)cols + a.eps);
+    shift = mean;
+    if (threadIdx.x == (WPR == 1 ? wave * 64 : 0)) {
+      if (a.mean) a.mean[row] = mean;
+      if (a.rstd) a.rstd[row] = scale;
+    }
+  }
+
+  const S* wp = reinterpret_cast<const S*>(a.w);
+  const S* bp = reinterpret_cast<const S*>(a.b);
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    if (!ok[i]) continue;
+    const int64_t c0 = ((int64_t)(i * WPR + wave_in_row) * 64 + lane) * EV;
+    v4u wv = {0u, 0u, 0u, 0u}, bv = {0u, 0u, 0u, 0u};
+    if constexpr (OP != ROW_SOFTMAX) {
+      if (wp) wv = *reinterpret_cast<const v4u*>(wp + c0);
+      if (bp) bv = *reinterpret_cast<const v4u*>(bp + c0);
+    }
+    S out[EV];
+#pragma unroll
+    for (int j = 0; j < EV; ++j) {
+      const float x = vec_elem<DT>(raw[i], j);
+      float r;
+      if constexpr (OP == ROW_SOFTMAX) {
+        r = fast_exp(x - shift) * scale;
+      } else if constexpr (OP == ROW_RMSNORM) {
+        r = x * scale;
+        if (wp) r = r * vec_elem<DT>(wv, j);
+      } else {
+        r = (x - shift) * scale;
+        if (wp) r = r * vec_elem<DT>(wv, j);
+        if (bp) r = r + vec_elem<DT>(bv, j);
+      }
+      out[j] = Elem<DT>::store(r);
+    }
+    __builtin_nontemporal_store(*reinterpret_cast<const v4u*>(out), reinterpret_cast<v4u*>(yr + c0));
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Host dispatch
 // ---------------------------------------------------------------------------
@@ -221,12 +355,26 @@ static int launch_row_cfg(const RowArgs& a, hipStream_t s) {
   const int64_t vecs = (a.cols + EV - 1) / EV;  // 16-byte vectors per row
   const dim3 block(256);
   const int64_t g1 = (a.rows + 3) / 4;
-  if (vecs <= 64 * 1) { row_kernel<OP, DT, 1, 1, VEC><<<dim3(g1), block, 0, s>>>(a); }
-  else if (vecs <= 64 * 4) { row_kernel<OP, DT, 1, 4, VEC><<<dim3(g1), block, 0, s>>>(a); }
-  else if (vecs <= 64 * 8) { row_kernel<OP, DT, 1, 8, VEC><<<dim3(g1), block, 0, s>>>(a); }
-  else if (vecs <= 256 * 8) { row_kernel<OP, DT, 4, 8, VEC><<<dim3(a.rows), block, 0, s>>>(a); }
-  else if (vecs <= 256 * 16) { row_kernel<OP, DT, 4, 16, VEC><<<dim3(a.rows), block, 0, s>>>(a); }
-  else return HXI_ERR_UNSUPPORTED;
+  if constexpr (VEC) {
+    // Short rows: one wave per row.  From 512 vectors (8 KiB) up, four waves
+    // share a row with few vectors each, which keeps every wave small enough
+    // for eight waves per SIMD (measured faster on MI355X than one wave
+    // holding the whole row).
+    if (vecs <= 64 * 1) { row_vec_kernel<OP, DT, 1, 1><<<dim3(g1), block, 0, s>>>(a); }
+    else if (vecs <= 64 * 4) { row_vec_kernel<OP, DT, 1, 4><<<dim3(g1), block, 0, s>>>(a); }
+    else if (vecs <= 256 * 2) { row_vec_kernel<OP, DT, 4, 2><<<dim3(a.rows), block, 0, s>>>(a); }
+    else if (vecs <= 256 * 4) { row_vec_kernel<OP, DT, 4, 4><<<dim3(a.rows), block, 0, s>>>(a); }
+    else if (vecs <= 256 * 8) { row_vec_kernel<OP, DT, 4, 8><<<dim3(a.rows), block, 0, s>>>(a); }
+    else if (vecs <= 256 * 16) { row_vec_kernel<OP, DT, 4, 16><<<dim3(a.rows), block, 0, s>>>(a); }
+    else return HXI_ERR_UNSUPPORTED;
+  } else {
+    if (vecs <= 64 * 1) { row_kernel<OP, DT, 1, 1, false><<<dim3(g1), block, 0, s>>>(a); }
+    else if (vecs <= 64 * 4) { row_kernel<OP, DT, 1, 4, false><<<dim3(g1), block, 0, s>>>(a); }
+    else if (vecs <= 64 * 8) { row_kernel<OP, DT, 1, 8, false><<<dim3(g1), block, 0, s>>>(a); }
+    else if (vecs <= 256 * 8) { row_kernel<OP, DT, 4, 8, false><<<dim3(a.rows), block, 0, s>>>(a); }
+    else if (vecs <= 256 * 16) { row_kernel<OP, DT, 4, 16, false><<<dim3(a.rows), block, 0, s>>>(a); }
+    else return HXI_ERR_UNSUPPORTED;
+  }
   return 0;
 }
 
