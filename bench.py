@@ -44,24 +44,70 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+_SLEEP_CYCLES_PER_MS = None
+
+
+def _sleep_cycles_per_ms() -> float:
+    """Rate of torch.cuda._sleep (a bounded spin kernel) on this device."""
+    global _SLEEP_CYCLES_PER_MS
+    if _SLEEP_CYCLES_PER_MS is None:
+        import torch
+        s = torch.cuda.current_stream()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(10_000)
+        a.record(s)
+        torch.cuda._sleep(5_000_000)
+        b.record(s)
+        torch.cuda.synchronize()
+        _SLEEP_CYCLES_PER_MS = 5_000_000 / max(a.elapsed_time(b), 1e-3)
+    return _SLEEP_CYCLES_PER_MS
+
+
 def event_timed(calls, iters: int):
-    """Run ``iters`` calls (cycling through ``calls``), one HIP event pair per
-    launch on the current stream.  Returns (mean event ms per launch, wall ms
-    per launch), both over exactly these launches."""
+    """Mean device time per launch of ``iters`` calls (cycling through
+    ``calls``) issued back-to-back on the current stream, between one HIP
+    event pair.  A spin kernel holds the stream while the host queues the
+    launches, so host launch cost does not open gaps between them.  Returns
+    (ms per launch, whether the queue stayed ahead of the device)."""
     import torch
     s = torch.cuda.current_stream()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(iters)]
     torch.cuda.synchronize()
+    n = min(len(calls), 8)
+    t = time.perf_counter()
+    for c in calls[:n]:
+        c()
+    host_ms = (time.perf_counter() - t) * 1e3 / n
+    torch.cuda.synchronize()
+    hold_ms = 1.0 + 2.0 * host_ms * iters
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(int(hold_ms * _sleep_cycles_per_ms()))
+    a.record(s)
     t0 = time.perf_counter()
     for i in range(iters):
-        evs[i][0].record(s)
         calls[i % len(calls)]()
-        evs[i][1].record(s)
+    queued_ms = (time.perf_counter() - t0) * 1e3
+    b.record(s)
     torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) * 1e3 / iters
-    ev = sum(a.elapsed_time(b) for a, b in evs) / iters
-    return ev, wall
+    return a.elapsed_time(b) / iters, queued_ms < hold_ms
+
+
+PROFILES = ROOT / "profiles"
+
+
+def traffic_of(kernel_key: str):
+    """HBM bytes per launch of one kernel from the committed rocprofv3 --pmc
+    summary (profiles/traffic.txt: FETCH_SIZE + WRITE_SIZE, each scaled by
+    the same counter's reading on a copy kernel of known size), or None."""
+    f = PROFILES / "traffic.txt"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith(kernel_key + "="):
+            try:
+                return int(float(line.split("=", 1)[1].split("#", 1)[0]))
+            except ValueError:
+                return None
+    return None
 
 
 def roofline(bound, achieved, peak, unit, traffic=None):
@@ -73,7 +119,16 @@ def roofline(bound, achieved, peak, unit, traffic=None):
 # Headline: int8 GEMM 4096^3 + dequant
 # --------------------------------------------------------------------------- #
 
-def bench_gemm_i8(hx, steps: int, warmup: int):
+def tune_summary(report):
+    """The autotuner's verdict, trimmed for the bench line."""
+    return {"champion": report.get("champion"), "round_verdict": report.get("round_verdict"),
+            "default": next((r["cfg"] for r in report.get("measurements", [])
+                             if r.get("index") == report.get("default_index")), None),
+            "q50_us": {r["cfg"]: (round(r["q50_us"], 2) if r.get("q50_us") is not None else None)
+                       for r in report.get("measurements", [])}}
+
+
+def bench_gemm_i8(hx, steps: int, warmup: int, tune: bool = True):
     import numpy as np
     import torch
     import oracle
@@ -85,17 +140,20 @@ def bench_gemm_i8(hx, steps: int, warmup: int):
     sa = torch.empty(M, dtype=torch.float32, device=dev).uniform_(0.001, 0.02, generator=g)
     sb = torch.empty(N, dtype=torch.float32, device=dev).uniform_(0.001, 0.02, generator=g)
     c = torch.empty((M, N), dtype=torch.float16, device=dev)
-
-    def step():
-        hx.gemm_i8(a, bt, b_layout="nk", row_scale=sa, col_scale=sb, out=c)
+    step = hx.bind_gemm_i8(a, bt, c, b_layout="nk", row_scale=sa, col_scale=sb)
+    tune_report = None
+    if tune:
+        tune_report = tune_summary(hx.search.tune(1, M, N, K, step))
 
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    ev_ms, _ = event_timed([step], steps)
+    for _ in range(steps):
+        step()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    ev_ms, fed = event_timed([step], steps)
     ops = 2.0 * M * N * K
     tops_wall = ops / (wall_ms * 1e-3) / 1e12
     tops_kernel = ops / (ev_ms * 1e-3) / 1e12
@@ -111,12 +169,15 @@ def bench_gemm_i8(hx, steps: int, warmup: int):
     cfg_idx = hx.config_lookup(1, M, N, K)
     cfg = hx.config_get(1, cfg_idx)["name"] if cfg_idx >= 0 else "generic"
     return dict(ms_per_step=wall_ms, kernel_ms=ev_ms, tops=tops_wall, tops_kernel=tops_kernel,
-                parity_sampled_rows_bitexact=exact, kernel=cfg, inputs=(a, bt, sa, sb))
+                parity_sampled_rows_bitexact=exact, kernel=cfg, inputs=(a, bt, sa, sb),
+                tune=tune_report, queue_fed=fed)
 
 
-def cpu_baseline_gemm_i8(inputs, target_s: float = 12.0):
-    """The oracle's (i,k,j) int32 loop + dequant on a row sample of the same
-    inputs, all host threads (OpenMP).  Returns TOPS over the sample."""
+def cpu_baseline_gemm_i8(inputs, reps: int = 5):
+    """The oracle's (i,k,j) int32 loop + dequant over the same inputs: one
+    warm-up, then the median of ``reps`` runs of the full 4096^3 product on
+    all host threads (OpenMP), plus a 256-row sample on one thread."""
+    import statistics
     import numpy as np
     import oracle
     a, bt, sa, sb = inputs
@@ -124,6 +185,7 @@ def cpu_baseline_gemm_i8(inputs, target_s: float = 12.0):
     a_h = a.cpu().numpy()
     sa_h, sb_h = sa.cpu().numpy(), sb.cpu().numpy()
     K, N = b_kn.shape
+    M = a_h.shape[0]
 
     def run(rows):
         t = time.perf_counter()
@@ -131,26 +193,41 @@ def cpu_baseline_gemm_i8(inputs, target_s: float = 12.0):
         oracle.dequant_i32_f16(acc, sa_h[:rows], sb_h)
         return time.perf_counter() - t
 
-    run(8)  # warm-up (thread pool, page-in)
-    t8 = run(16)
-    rows = int(min(4096, max(16, 16 * target_s / max(t8, 1e-6))))
-    rows = max(16, (rows // 16) * 16)
-    dt = run(rows)
     try:
-        threads = ctypes.CDLL("libgomp.so.1").omp_get_max_threads()
+        gomp = ctypes.CDLL("libgomp.so.1")
+        threads = gomp.omp_get_max_threads()
     except OSError:
-        threads = os.cpu_count()
-    return {"value": round(2.0 * rows * N * K / dt / 1e12, 5), "unit": "TOPS", "cores": int(threads),
+        gomp, threads = None, os.cpu_count()
+    run(64)  # warm-up (thread pool, page-in)
+    times = [run(M) for _ in range(reps)]
+    med = statistics.median(times)
+    one_core = None
+    if gomp is not None:
+        gomp.omp_set_num_threads(1)
+        t1 = run(256)
+        gomp.omp_set_num_threads(threads)
+        one_core = round(2.0 * 256 * N * K / t1 / 1e12, 5)
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(2.0 * M * N * K / med / 1e12, 5), "unit": "TOPS", "cores": int(threads),
             "kind": "port",
-            "sample": f"{rows} of 4096 rows of the int8 4096^3 GEMM + dequant "
-                      f"(oracle/hx_oracle.c hxo_gemm_i8_i32 (i,k,j) loop), {dt:.2f} s"}
+            "sample": f"full int8 4096^3 GEMM + dequant, oracle/hx_oracle.c hxo_gemm_i8_i32 "
+                      f"(i,k,j) loop, median of {reps} runs ({med:.3f} s each) after a warm-up",
+            "one_core_tops": one_core, "one_core_sample": "256 of 4096 rows on 1 thread",
+            "cpu_model": cpu}
 
 
 # --------------------------------------------------------------------------- #
 # Secondary workloads
 # --------------------------------------------------------------------------- #
 
-def bench_gemv(hx, iters: int = 200):
+def bench_gemv(hx, iters: int = 200, tune: bool = True):
     import torch
     N, K = 11008, 4096
     dev = torch.device("cuda:0")
@@ -167,17 +244,21 @@ def bench_gemv(hx, iters: int = 200):
         for M in (1, 4, 16):
             x = torch.randn((M, K), dtype=torch.float16, device=dev, generator=g)
             y = torch.empty((M, N), dtype=torch.float16, device=dev)
-            calls = [(lambda w=w: hx.matmul_resident(x, w, out=y)) for w in weights]
+            calls = [hx.bind_matmul_resident(x, w, y) for w in weights]
             for c in calls:
                 c()
-            ev_ms, wall_ms = event_timed(calls, iters)
+            rot = iter(range(1 << 30))
+            tuned = (tune_summary(hx.search.tune(6, M, N, K, lambda: calls[next(rot) % copies]()))
+                     if tune else None)
+            ev_ms, fed = event_timed(calls, iters)
             nbytes = N * K + 2 * N + 2 * M * K + 2 * M * N
             gbs = nbytes / (ev_ms * 1e-3) / 1e9
             cfg = hx.config_get(6, hx.config_lookup(6, M, N, K))["name"]
             res.append({"workload": f"W8A16 GEMV M={M} N={N} K={K}", "value": round(gbs, 1),
                         "unit": "GB/s", "us_per_call": round(ev_ms * 1e3, 3),
-                        "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s"),
-                        "bytes_per_call": nbytes, "kernel": cfg,
+                        "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s",
+                                             traffic_of(f"gemv_w8a16_m{M}:{cfg}")),
+                        "bytes_per_call": nbytes, "kernel": cfg, "tune": tuned, "queue_fed": fed,
                         "mall_defeat": f"rotating {copies} resident weight copies (541 MB)"})
     finally:
         for w in weights:
@@ -196,17 +277,17 @@ def bench_rows(hx, iters: int = 60):
     gamma = (torch.randn(C, dtype=torch.float16, device=dev, generator=g) * 0.1 + 1.0)
     out = []
     nbytes = 2 * R * C * 2
-    for name, fn in (("softmax", lambda i: hx.softmax(xs[i], out=ys[i])),
-                     ("rmsnorm", lambda i: hx.rms_norm(xs[i], gamma, 1e-6, out=ys[i]))):
-        calls = [(lambda i=i: fn(i)) for i in range(sets)]
+    for name in ("softmax", "rmsnorm"):
+        calls = [hx.bind_row_op(name, xs[i], ys[i], weight=gamma if name == "rmsnorm" else None)
+                 for i in range(sets)]
         for c in calls:
             c()
-        ev_ms, _ = event_timed(calls, iters)
+        ev_ms, fed = event_timed(calls, iters)
         gbs = (nbytes + (2 * C if name == "rmsnorm" else 0)) / (ev_ms * 1e-3) / 1e9
         out.append({"workload": f"{name} fp16 [{R} x {C}]", "value": round(gbs, 1), "unit": "GB/s",
                     "us_per_call": round(ev_ms * 1e3, 3),
-                    "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s"),
-                    "mall_defeat": "rotating 6 input/output sets (768 MiB)"})
+                    "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s", traffic_of(f"{name}_f16_8192x4096")),
+                    "mall_defeat": "rotating 6 input/output sets (768 MiB)", "queue_fed": fed})
     return out
 
 
@@ -226,7 +307,7 @@ def bench_gemm_f16_small(hx, iters: int = 200):
             "roofline": roofline("mfma", tf, PEAK_F16_TFLOPS, "TFLOP/s")}
 
 
-def bench_ffn(hx, iters: int = 20):
+def bench_ffn(hx, iters: int = 20, tune: bool = True):
     import torch
     T, H, I = 2048, 4096, 11008
     dev = torch.device("cuda:0")
@@ -244,6 +325,11 @@ def bench_ffn(hx, iters: int = 20):
         y = torch.empty_like(x)
         call = lambda: hx.swiglu_ffn(x, gamma, 1e-6, Wg, Wu, Wd, out=y)  # noqa: E731
         call()
+        tuned = None
+        if tune:
+            # gate/up stage (fused SwiGLU epilogue), then the down projection
+            tuned = {"swiglu": tune_summary(hx.search.tune(5, T, I, H, call)),
+                     "down": tune_summary(hx.search.tune(4, T, H, I, call))}
         ev_ms, _ = event_timed([call], iters)
     finally:
         Wg.release(); Wu.release(); Wd.release()
@@ -251,10 +337,109 @@ def bench_ffn(hx, iters: int = 20):
     tf = flops / (ev_ms * 1e-3) / 1e12
     return {"workload": f"SwiGLU FFN tokens={T} hidden={H} inter={I}, int8 weights",
             "value": round(tf, 1), "unit": "TFLOP/s", "us_per_call": round(ev_ms * 1e3, 1),
-            "roofline": roofline("mfma", tf, PEAK_F16_TFLOPS, "TFLOP/s")}
+            "roofline": roofline("mfma", tf, PEAK_F16_TFLOPS, "TFLOP/s"), "tune": tuned}
 
 
 # --------------------------------------------------------------------------- #
+
+def pmc_workload(hx) -> None:
+    """A few launches of every benchmarked kernel -- every compiled config of
+    the headline GEMM and of the decode GEMV, so whichever one the tuner
+    picks has a reading -- plus a plain 64 MiB copy of known size, for
+    ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` runs (the copy's readings
+    give the scale factor from counter to bytes)."""
+    import torch
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(3)
+    src = torch.empty(64 << 20, dtype=torch.uint8, device=dev).random_(generator=g)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    M = N = K = 4096
+    a = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev, generator=g)
+    bt = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+    sa = torch.rand(M, device=dev) * 0.02
+    sb = torch.rand(N, device=dev) * 0.02
+    c = torch.empty((M, N), dtype=torch.float16, device=dev)
+    for idx in range(hx.config_count(1)):
+        hx.config_select(1, M, N, K, idx)
+        for _ in range(3):
+            hx.gemm_i8(a, bt, b_layout="nk", row_scale=sa, col_scale=sb, out=c)
+    hx.config_select(1, M, N, K, -1)
+    w = torch.randint(-127, 128, (11008, 4096), dtype=torch.int8, device=dev, generator=g)
+    rw = hx.ResidentWeight(w, torch.rand(11008, device=dev).half() * 0.02, layout="nk")
+    for m in (1, 4, 16):
+        x = torch.randn((m, 4096), dtype=torch.float16, device=dev, generator=g)
+        for idx in range(hx.config_count(6)):
+            hx.config_select(6, m, 11008, 4096, idx)
+            for _ in range(3):
+                hx.matmul_resident(x, rw)
+        hx.config_select(6, m, 11008, 4096, -1)
+    rw.release()
+    xr = torch.randn((8192, 4096), dtype=torch.float16, device=dev, generator=g)
+    yr = torch.empty_like(xr)
+    gam = torch.ones(4096, dtype=torch.float16, device=dev)
+    for _ in range(3):
+        hx.softmax(xr, out=yr)
+    for _ in range(3):
+        hx.rms_norm(xr, gam, 1e-6, out=yr)
+    torch.cuda.synchronize()
+    print("pmc workload done", flush=True)
+
+
+def traffic_from_pmc(fetch_csv: str, write_csv: str, hx) -> str:
+    """Turn the two counter-collection CSVs of ``--pmc-workload`` runs into
+    the key=value lines of profiles/traffic.txt (bytes per launch).  Launch
+    order follows pmc_workload; each counter is scaled by its reading on the
+    64 MiB copies (bytes / counter value)."""
+    import csv
+    import re
+    import statistics
+
+    def per_dispatch(path):
+        rows = {}
+        for r in csv.DictReader(open(path)):
+            d = int(r["Dispatch_Id"])
+            rows.setdefault(d, [r["Kernel_Name"], 0.0])
+            rows[d][1] += float(r["Counter_Value"])
+        return [rows[d] for d in sorted(rows)]
+
+    fetch, write = per_dispatch(fetch_csv), per_dispatch(write_csv)
+    assert [k for k, _ in fetch] == [k for k, _ in write], "the two runs launched different kernels"
+    copy = 64 << 20
+    cf = [v for k, v in fetch if k == "__amd_rocclr_copyBuffer"][:3]
+    cw = [v for k, v in write if k == "__amd_rocclr_copyBuffer"][:3]
+    f_scale = copy / 1024 / statistics.median(cf)   # counter unit is KiB
+    w_scale = copy / 1024 / statistics.median(cw)
+    measured = re.compile(r"void hx::(gemm_kernel|gemm_generic_kernel|gemv_packed_kernel|row_vec_kernel|"
+                          r"row_kernel)<")
+    seq = [(k, f * f_scale * 1024 + w * w_scale * 1024) for (k, f), (_, w) in zip(fetch, write)
+           if measured.match(k)]
+    lines = [f"# HBM bytes per launch = FETCH_SIZE*{f_scale:.4f} + WRITE_SIZE*{w_scale:.4f} (KiB -> bytes)",
+             f"# scale factors: 64 MiB copy read FETCH_SIZE {statistics.median(cf):.1f} KiB, "
+             f"WRITE_SIZE {statistics.median(cw):.1f} KiB"]
+    pos = 0
+
+    def take(n):
+        nonlocal pos
+        vals = seq[pos:pos + n]
+        pos += n
+        return vals
+
+    def fill(key, vals):
+        assert len({k for k, _ in vals}) == 1, f"{key}: mixed kernels {vals}"
+        lines.append(f"{key}={int(statistics.median(v for _, v in vals))}  # {vals[0][0].split('(')[0]}")
+
+    for idx in range(hx.config_count(1)):
+        fill(f"gemm_i8_4096_dequant_f16:{hx.config_get(1, idx)['name']}", take(3))
+    for m in (1, 4, 16):
+        for idx in range(hx.config_count(6)):
+            fill(f"gemv_w8a16_m{m}:{hx.config_get(6, idx)['name']}", take(3))
+    fill("softmax_f16_8192x4096", take(3))
+    fill("rmsnorm_f16_8192x4096", take(3))
+    assert pos == len(seq), f"{len(seq) - pos} unmatched launches"
+    return "\n".join(lines) + "\n"
+
 
 def main() -> int:
     ap = argparse.ArgumentParser()
@@ -263,6 +448,12 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", choices=["headline", "all"], default="all")
+    ap.add_argument("--no-tune", action="store_true",
+                    help="time the untuned default configs (skip the tile search)")
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="launch each benchmarked kernel a few times for rocprofv3 --pmc")
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="write profiles/traffic.txt from two --pmc-workload counter CSVs and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -272,6 +463,10 @@ def main() -> int:
     import torch
     from __graft_entry__ import load_package
     hx = load_package()
+    if args.traffic_from:
+        (PROFILES / "traffic.txt").write_text(traffic_from_pmc(*args.traffic_from, hx))
+        print((PROFILES / "traffic.txt").read_text())
+        return 0
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
@@ -279,21 +474,25 @@ def main() -> int:
     if rc != 0:
         print(f"bench.py: hx_init failed: {hx._abi.last_error()}", file=sys.stderr)
         return 1
+    if args.pmc_workload:
+        pmc_workload(hx)
+        return 0
 
     log("[bench] int8 GEMM 4096^3 + dequant")
-    h = bench_gemm_i8(hx, args.steps, args.warmup)
+    tune = not args.no_tune
+    h = bench_gemm_i8(hx, args.steps, args.warmup, tune=tune)
     log(f"[bench] int8 GEMM: {h['tops']:.1f} TOPS wall, {h['tops_kernel']:.1f} TOPS kernel, "
         f"{h['kernel_ms']*1e3:.1f} us/launch, parity={h['parity_sampled_rows_bitexact']}")
     secondary = []
     if args.only == "all":
         log("[bench] W8A16 GEMV")
-        secondary += bench_gemv(hx)
+        secondary += bench_gemv(hx, tune=tune)
         log("[bench] row ops")
         secondary += bench_rows(hx)
         log("[bench] fp16 GEMM 256^3")
         secondary.append(bench_gemm_f16_small(hx))
         log("[bench] SwiGLU FFN")
-        secondary.append(bench_ffn(hx))
+        secondary.append(bench_ffn(hx, tune=tune))
         for s in secondary:
             log(f"[bench]   {s['workload']}: {s['value']} {s['unit']}")
     cpu = None
@@ -319,10 +518,15 @@ def main() -> int:
                                "scales -> fp16 (BASELINE configs[1])",
                    "M": 4096, "N": 4096, "K": 4096, "b_layout": "nk (resident weight image)",
                    "kernel": h["kernel"], "parallelism": "single GPU"},
-        "roofline": roofline("mfma", h["tops_kernel"], PEAK_INT8_TOPS, "TFLOP/s"),
-        "roofline_note": "int8 ops counted as 2 per MAC; achieved = 2*4096^3 / mean per-launch "
-                         "HIP-event duration over the timed steps",
+        "roofline": roofline("mfma", h["tops_kernel"], PEAK_INT8_TOPS, "TFLOP/s",
+                             traffic_of(f"gemm_i8_4096_dequant_f16:{h['kernel']}")),
+        "roofline_note": "int8 ops counted as 2 per MAC; achieved = 2*4096^3 / mean device time "
+                         "per launch, one HIP event pair around the K back-to-back steps on the "
+                         "launch stream",
+        "kernel_us": round(h["kernel_ms"] * 1e3, 3),
+        "queue_fed": h["queue_fed"],
         "parity": {"int8_sampled_rows_bitexact": h["parity_sampled_rows_bitexact"]},
+        "tune": h["tune"],
         "cpu_baseline": cpu,
         "secondary": secondary,
     }

@@ -547,8 +547,10 @@ static int num_cus() {
   return g_num_cus;
 }
 
-// Untuned choice: estimated time = waves_of_tiles * tile_area / efficiency,
-// efficiency falling with tile size (operand reuse per LDS byte).
+// Untuned choice: estimated time = waves_of_tiles * tile_area / efficiency.
+// The efficiencies are relative throughputs measured on MI355X at 4096^3
+// (the 8-wave 256x256 tile is the fastest per MAC; 128x128 beats the
+// 4-wave 256-wide tiles); the autotuner replaces this guess per shape.
 int gemm_default_config(int mode, int epi, int64_t M, int64_t N, int64_t K) {
   (void)K;
   int n;
@@ -560,11 +562,14 @@ int gemm_default_config(int mode, int epi, int64_t M, int64_t N, int64_t K) {
   for (int i = 0; i < n; ++i) {
     const GemmConfig& c = t[i].cfg;
     if (c.epi != epi) continue;
-    if (c.wm * c.wn != 4) continue;  // the 8-wave variants are tuner-only
     const double tiles = (double)((M + c.bm - 1) / c.bm) * (double)((N + c.bn - 1) / c.bn);
     const double waves = (double)(int64_t)((tiles + cus - 1) / cus);
     const double area = (double)c.bm * c.bn;
-    const double eff = area >= 65536 ? 1.0 : area >= 32768 ? 0.93 : area >= 16384 ? 0.8 : 0.5;
+    double eff;
+    if (area >= 65536) eff = (c.wm * c.wn == 8) ? 1.0 : 0.72;
+    else if (area >= 32768) eff = 0.68;
+    else if (area >= 16384) eff = 0.78;
+    else eff = 0.55;
     const double cost = waves * area / eff;
     if (best < 0 || cost < best_cost - 1e-9) {
       best = i;

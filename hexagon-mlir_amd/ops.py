@@ -289,3 +289,52 @@ def config_lookup(op: int, m: int, n: int, k: int) -> int:
 
 def build_id() -> str:
     return load().hx_build_id().decode()
+
+
+# --------------------------------------------------------------------------- #
+# Pre-bound calls: descriptors built once, so a repeated call costs one C-ABI
+# entry (for timing loops and serving loops; tensors must stay alive).
+# --------------------------------------------------------------------------- #
+
+class Bound:
+    """A zero-argument callable around one C-ABI call with fixed arguments."""
+
+    def __init__(self, fn, args, keep):
+        self._fn, self._args, self._keep = fn, args, keep
+
+    def __call__(self):
+        rc = self._fn(*self._args)
+        if rc != 0:
+            check(rc, self._fn.__name__)
+
+
+def bind_gemm_i8(a, b, out, *, b_layout="kn", row_scale=None, col_scale=None) -> Bound:
+    ma, mb, mc = memref2d(a, "a"), memref2d(b, "b"), memref2d(out, "out")
+    mrs = memref1d(row_scale, "row_scale") if row_scale is not None else None
+    mcs = memref1d(col_scale, "col_scale") if col_scale is not None else None
+    args = (ctypes.byref(ma), ctypes.byref(mb), _LAYOUT[b_layout], _ref(mrs), _ref(mcs),
+            ctypes.byref(mc), dtype_code(out), _stream())
+    return Bound(load().hx_gemm_i8, args, (ma, mb, mc, mrs, mcs, a, b, out, row_scale, col_scale))
+
+
+def bind_matmul_resident(x, w: ResidentWeight, out) -> Bound:
+    mx, my = memref2d(x, "x"), memref2d(out, "out")
+    args = (ctypes.byref(mx), dtype_code(x), w.handle, None, 0, ctypes.byref(my), dtype_code(out),
+            _stream())
+    return Bound(load().hx_matmul_resident, args, (mx, my, x, out, w))
+
+
+def bind_row_op(op: str, x, out, weight=None, bias=None, eps: float = 1e-6) -> Bound:
+    mx, my = memref2d(x, "x"), memref2d(out, "out")
+    mw = memref1d(weight, "weight") if weight is not None else None
+    mb = memref1d(bias, "bias") if bias is not None else None
+    L = load()
+    if op == "softmax":
+        args, fn = (ctypes.byref(mx), ctypes.byref(my), dtype_code(x), _stream()), L.hx_softmax
+    elif op == "rmsnorm":
+        args, fn = (ctypes.byref(mx), _ref(mw), float(eps), ctypes.byref(my), dtype_code(x),
+                    _stream()), L.hx_rmsnorm
+    else:
+        args, fn = (ctypes.byref(mx), _ref(mw), _ref(mb), float(eps), ctypes.byref(my), None, None,
+                    dtype_code(x), _stream()), L.hx_layernorm
+    return Bound(fn, args, (mx, my, mw, mb, x, out, weight, bias))
