@@ -24,8 +24,12 @@ ARCH = "gfx950"
 SOURCES = ["hx_rows.hip", "hx_gemm.hip", "hx_gemv.hip", "hx_pack.hip", "hx_api.cpp"]
 
 # Packed-FP32 VALU forms are disabled for all device code (they are not
-# needed: the hot loops are MFMA or memory bound).
-COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
+# needed: the hot loops are MFMA or memory bound).  Floating-point
+# contraction is off: every product and sum is rounded on its own, as the
+# reference arithmetic (and its CPU restatement) specifies -- a fused
+# multiply-add, or a multiply fused into its conversion to fp16, rounds once
+# and can land one ulp away.
+COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-ffp-contract=off",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
           "-Wno-unused-command-line-argument"]
 

@@ -113,8 +113,55 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* lds, uint3
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voff, soff, 0, 0);
 }
 
-// vmcnt(0): this wave's direct-to-LDS loads have landed.
-__device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding):
+// all but this wave's N most recent direct-to-LDS loads have landed.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier that orders LDS only.  __syncthreads() is a release
+// fence on all memory, which counts outstanding direct-to-LDS loads as
+// pending LDS writes and forces vmcnt(0); here every wave has already waited
+// for its own loads of the stage it is about to publish (wait_vm), so the
+// barrier needs only this wave's LDS reads retired (lgkmcnt(0)).  The
+// "memory" clobber keeps the compiler from moving memory operations across
+// it, the sched_barriers keep the machine scheduler from doing so.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Store four consecutive outputs (16-byte aligned for 4-byte types, 8-byte
+// aligned for 2-byte types).
+__device__ __forceinline__ void store4(void* c, int dt, int64_t idx, float v0, float v1, float v2,
+                                       float v3) {
+  if (dt == DT_F32) {
+    *reinterpret_cast<v4f*>(reinterpret_cast<float*>(c) + idx) = v4f{v0, v1, v2, v3};
+  } else {
+    uint32_t lo, hi;
+    if (dt == DT_F16) {
+      lo = (uint32_t)f32_to_f16_bits(v0) | ((uint32_t)f32_to_f16_bits(v1) << 16);
+      hi = (uint32_t)f32_to_f16_bits(v2) | ((uint32_t)f32_to_f16_bits(v3) << 16);
+    } else {
+      lo = (uint32_t)f32_to_bf16(v0) | ((uint32_t)f32_to_bf16(v1) << 16);
+      hi = (uint32_t)f32_to_bf16(v2) | ((uint32_t)f32_to_bf16(v3) << 16);
+    }
+    *reinterpret_cast<v2i*>(reinterpret_cast<uint16_t*>(c) + idx) = v2i{(int)lo, (int)hi};
+  }
+}
+__device__ __forceinline__ v4f load4(const void* p, int dt, int64_t idx) {
+  if (dt == DT_F32) return *reinterpret_cast<const v4f*>(reinterpret_cast<const float*>(p) + idx);
+  const v2i w = *reinterpret_cast<const v2i*>(reinterpret_cast<const uint16_t*>(p) + idx);
+  const uint32_t lo = (uint32_t)w[0], hi = (uint32_t)w[1];
+  if (dt == DT_F16)
+    return v4f{f16_bits_to_f32((uint16_t)lo), f16_bits_to_f32((uint16_t)(lo >> 16)),
+               f16_bits_to_f32((uint16_t)hi), f16_bits_to_f32((uint16_t)(hi >> 16))};
+  return v4f{bf16_to_f32((uint16_t)lo), bf16_to_f32((uint16_t)(lo >> 16)), bf16_to_f32((uint16_t)hi),
+             bf16_to_f32((uint16_t)(hi >> 16))};
+}
 
 template <int MODE, int BM, int BN, int WM, int WN, int EPI>
 __global__ void __launch_bounds__(64 * WM * WN)
@@ -132,11 +179,13 @@ gemm_kernel(GemmArgs p) {
   constexpr int B_RPB = 1024 / T::BROW;
   constexpr int A_PER_W = A_BLK / NW;
   constexpr int B_PER_W = B_BLK / NW;
+  constexpr int P = A_PER_W + NB * B_PER_W;  // direct loads per wave per stage
   static_assert(A_BLK % NW == 0 && B_BLK % NW == 0, "block split");
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
   static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
   static_assert(2 * STAGE <= 160 * 1024, "LDS budget");
+  static_assert(2 * P < 64, "vmcnt range");
 
   // Two stages as two distinct arrays: the compiler can then see that a
   // direct load into one stage never aliases the reads of the other.
@@ -183,24 +232,24 @@ gemm_kernel(GemmArgs p) {
 
   // Enqueue the direct loads of K-stage kt into `st`.  Only the last stage
   // can overhang K; its chunks past K read as zero (offset out of range).
-  auto dma_stage = [&](char* st, int kt) {
+  // MASK = false is for stages known not to be the last one.
+  auto dma_stage = [&](char* st, int kt, auto maskc) {
+    constexpr bool MASK = decltype(maskc)::value;
     const uint32_t ka = (uint32_t)kt * 128u;
     const uint32_t kb = (uint32_t)kt * T::BROW;
-    const bool tail = ka + 128u > ka_bytes;
-#pragma unroll
-    for (int i = 0; i < A_PER_W; ++i) {
-      const int blk = wave + i * NW;
+    const bool tail = MASK && ka + 128u > ka_bytes;
+    static_for<A_PER_W>([&](auto ic) {
+      const int blk = wave + decltype(ic)::value * NW;
       // row = 8*blk + lane/8, so swz128(row) = (lane/8 ^ blk) & 7
       const uint32_t kc = (uint32_t)(((lane & 7) ^ (lane >> 3) ^ blk) & 7) * 16u;
       uint32_t off = a_lane_row + kc + ka;
       if (tail && ka + kc >= ka_bytes) off = 0x80000000u;
       dma16(ra, st + blk * 1024, off, (uint32_t)blk * 8u * lda_b);
-    }
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int i = 0; i < B_PER_W; ++i) {
-        const int blk = wave + i * NW;
+    });
+    static_for<NB>([&](auto nbc) {
+      constexpr int nb = decltype(nbc)::value;
+      static_for<B_PER_W>([&](auto ic) {
+        const int blk = wave + decltype(ic)::value * NW;
         uint32_t kc;
         if constexpr (T::BROW == 128) {
           kc = (uint32_t)(((lane & 7) ^ (lane >> 3) ^ blk) & 7) * 16u;
@@ -212,174 +261,240 @@ gemm_kernel(GemmArgs p) {
         if (tail && kb + kc >= kb_bytes) off = 0x80000000u;
         dma16(rb[nb], st + A_BYTES + nb * B_BYTES + blk * 1024, off,
               (uint32_t)blk * (uint32_t)B_RPB * ldb_b);
-      }
+      });
+    });
   };
 
   Acc acc[NB][TM][TN];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) acc[nb][i][j] = Acc{};
+  static_for<NB>([&](auto nbc) {
+    static_for<TM>([&](auto ic) {
+      static_for<TN>([&](auto jc) {
+        acc[decltype(nbc)::value][decltype(ic)::value][decltype(jc)::value] = Acc{};
+      });
+    });
+  });
 
   const int lrow = lane & 31, lg = lane >> 5;
 
-  auto compute = [&](const char* sa) {
+  // Operand fragments, double-buffered in registers: while the MFMAs of
+  // k-step ks run, the LDS reads of step ks+1 are in flight.  A stage is 4
+  // k-steps.  For W8 one 16-byte int8 B read covers two steps (it is widened
+  // to f16 half by half), so B is read on even steps into its own pair of
+  // buffers, indexed by the step pair.
+  v4i fa[2][TM];
+  v4i fb[2][NB][TN];
+
+  auto read_frags = [&](const char* sa, auto ksc) {
+    constexpr int ks = decltype(ksc)::value;
+    constexpr int s = ks & 1;
+    // step ks reads A chunk ca (W8: A is f16, step ks = 2*jp + h covers
+    // k = 32*jp + 16*g + 8*h + (0..7) for lane group g, both operands, so
+    // every k of the stage is summed exactly once)
+    const int ca = (MODE != GM_W8) ? ks * 2 + lg : 4 * (ks >> 1) + 2 * lg + (ks & 1);
+    static_for<TM>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      const int row = wm * WTM + i * 32 + lrow;
+      fa[s][i] = *reinterpret_cast<const v4i*>(sa + row * 128 + ((ca ^ swz128(row)) << 4));
+    });
     if constexpr (MODE != GM_W8) {
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        v4i af[TM];
-        v4i bf[NB][TN];
-        const int c = ks * 2 + lg;
-#pragma unroll
-        for (int i = 0; i < TM; ++i) {
-          const int row = wm * WTM + i * 32 + lrow;
-          af[i] = *reinterpret_cast<const v4i*>(sa + row * 128 + ((c ^ swz128(row)) << 4));
-        }
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int j = 0; j < TN; ++j) {
-            const int row = wn * WTN + j * 32 + lrow;
-            bf[nb][j] = *reinterpret_cast<const v4i*>(sa + A_BYTES + nb * B_BYTES + row * 128 +
-                                                      ((c ^ swz128(row)) << 4));
-          }
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j) acc[nb][i][j] = mfma32<MODE>(af[i], bf[nb][j], acc[nb][i][j]);
-      }
-    } else {
-      // W8: a 16-byte int8 B read covers two MFMA k-steps.  Lane group g
-      // supplies k = 32*jp + 16*g + 8*h + (0..7) in step h of pair jp, for
-      // both operands, so every k of the stage is summed exactly once.
-#pragma unroll
-      for (int jp = 0; jp < 2; ++jp) {
-        v4i bq[NB][TN];
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int j = 0; j < TN; ++j) {
-            const int row = wn * WTN + j * 32 + lrow;
-            const int c = 2 * jp + lg;
-            bq[nb][j] = *reinterpret_cast<const v4i*>(sa + A_BYTES + nb * B_BYTES + row * 64 +
-                                                      ((c ^ swz64(row)) << 4));
-          }
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          v4i af[TM];
-          const int c = 4 * jp + 2 * lg + h;
-#pragma unroll
-          for (int i = 0; i < TM; ++i) {
-            const int row = wm * WTM + i * 32 + lrow;
-            af[i] = *reinterpret_cast<const v4i*>(sa + row * 128 + ((c ^ swz128(row)) << 4));
-          }
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-              const v4i bw = __builtin_bit_cast(
-                  v4i, i8x8_to_v8h((uint32_t)bq[nb][j][2 * h], (uint32_t)bq[nb][j][2 * h + 1]));
-#pragma unroll
-              for (int i = 0; i < TM; ++i) acc[nb][i][j] = mfma32_f16(af[i], bw, acc[nb][i][j]);
-            }
-        }
-      }
+      static_for<NB>([&](auto nbc) {
+        constexpr int nb = decltype(nbc)::value;
+        static_for<TN>([&](auto jc) {
+          constexpr int j = decltype(jc)::value;
+          const int row = wn * WTN + j * 32 + lrow;
+          fb[s][nb][j] = *reinterpret_cast<const v4i*>(sa + A_BYTES + nb * B_BYTES + row * 128 +
+                                                       ((ca ^ swz128(row)) << 4));
+        });
+      });
+    } else if constexpr ((ks & 1) == 0) {
+      constexpr int jp = ks >> 1;
+      const int cb = 2 * jp + lg;
+      static_for<NB>([&](auto nbc) {
+        constexpr int nb = decltype(nbc)::value;
+        static_for<TN>([&](auto jc) {
+          constexpr int j = decltype(jc)::value;
+          const int row = wn * WTN + j * 32 + lrow;
+          fb[jp][nb][j] = *reinterpret_cast<const v4i*>(sa + A_BYTES + nb * B_BYTES + row * 64 +
+                                                        ((cb ^ swz64(row)) << 4));
+        });
+      });
     }
   };
 
-  // Ping-pong over the two stages: the loads of stage k+1 are in flight
-  // while stage k is consumed; one wait + barrier per stage.  The steady
-  // state loop body is straight-line code (no conditional loads), so the
-  // accumulators stay in one register class across iterations; the last one
-  // or two stages are peeled after it.
-  dma_stage(st0, 0);
-  wait_dma();
-  __syncthreads();
-  // sched_barrier(0) pins each stage's load issue ahead of the MFMA block;
-  // left alone, the scheduler sinks the loads to just before the wait,
-  // which serializes load latency with compute.
-  int kt = 0;
-  for (; kt + 2 < nk; kt += 2) {
-    dma_stage(st1, kt + 1);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(st0);
-    wait_dma();
-    __syncthreads();
-    dma_stage(st0, kt + 2);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(st1);
-    wait_dma();
-    __syncthreads();
-  }
-  if (kt + 1 < nk) {
-    dma_stage(st1, kt + 1);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(st0);
-    wait_dma();
-    __syncthreads();
-    compute(st1);
+  // The MFMAs of one k-step.  B is the first operand, so the accumulators
+  // hold C transposed: lane (lrow, lg) of sub-tile (i, j) holds row lrow and
+  // the four consecutive columns 8*g + 4*lg + (0..3) in registers 4g..4g+3.
+  auto mfmas = [&](auto ksc) {
+    constexpr int ks = decltype(ksc)::value;
+    constexpr int s = ks & 1;
+    static_for<NB>([&](auto nbc) {
+      constexpr int nb = decltype(nbc)::value;
+      static_for<TN>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        v4i bj;
+        if constexpr (MODE != GM_W8) {
+          bj = fb[s][nb][j];
+        } else {
+          constexpr int jp = ks >> 1, h = ks & 1;
+          bj = __builtin_bit_cast(
+              v4i, i8x8_to_v8h((uint32_t)fb[jp][nb][j][2 * h], (uint32_t)fb[jp][nb][j][2 * h + 1]));
+        }
+        static_for<TM>([&](auto ic) {
+          constexpr int i = decltype(ic)::value;
+          if constexpr (MODE == GM_W8) acc[nb][i][j] = mfma32_f16(bj, fa[s][i], acc[nb][i][j]);
+          else acc[nb][i][j] = mfma32<MODE>(bj, fa[s][i], acc[nb][i][j]);
+        });
+      });
+    });
+  };
+
+  // One stage: the reads of step ks+1 are issued before the MFMAs of step
+  // ks.  Before the last step's MFMAs the workgroup meets at the barrier
+  // (every wave's loads of the next stage have landed, every wave is done
+  // reading this one), the loads of stage kt+2 go into this stage's buffer
+  // (DMA: 0 none, 1 a middle stage, 2 possibly the last stage) and step 0 of
+  // the next stage is read, so the MFMA pipe never waits on a barrier with
+  // an empty queue.  LAST: no next stage.
+  auto stage_body = [&](char* cur, char* nxt, int kt, auto dmac, auto lastc) {
+    constexpr int DMA = decltype(dmac)::value;
+    constexpr bool LAST = decltype(lastc)::value;
+    static_for<4>([&](auto ksc) {
+      constexpr int ks = decltype(ksc)::value;
+      if constexpr (ks < 3) {
+        read_frags(cur, std::integral_constant<int, ks + 1>{});
+      } else if constexpr (!LAST) {
+        wait_vm<0>();
+        lds_barrier();
+        if constexpr (DMA == 1) dma_stage(cur, kt + 2, std::false_type{});
+        if constexpr (DMA == 2) dma_stage(cur, kt + 2, std::true_type{});
+        read_frags(nxt, std::integral_constant<int, 0>{});
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(ksc);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+  typedef std::integral_constant<int, 0> NoDma;
+  typedef std::integral_constant<int, 2> LastDma;
+
+  // Stage buffers: stage kt lives in st0 when kt - (nk & 1) is even, so the
+  // final two stages are always (st0, st1) and the steady loop needs no
+  // remainder; with an odd stage count stage 0 goes to st1 and is peeled.
+  // (The fast path requires nk >= 2.)
+  const bool odd = nk & 1;
+  if (odd) {
+    dma_stage(st1, 0, std::true_type{});
+    dma_stage(st0, 1, std::true_type{});
   } else {
-    compute(st0);
+    dma_stage(st0, 0, std::true_type{});
+    dma_stage(st1, 1, std::true_type{});
   }
+  wait_vm<P>();
+  lds_barrier();
+  int kt = 0;
+  if (odd) {
+    read_frags(st1, std::integral_constant<int, 0>{});
+    stage_body(st1, st0, 0, LastDma{}, std::false_type{});
+    kt = 1;
+  } else {
+    read_frags(st0, std::integral_constant<int, 0>{});
+  }
+  // Steady state: straight-line pairs of stages (no conditional code, so
+  // the accumulators keep one register class across iterations).
+  for (; nk - kt > 2; kt += 2) {
+    stage_body(st0, st1, kt, LastDma{}, std::false_type{});
+    stage_body(st1, st0, kt + 1, LastDma{}, std::false_type{});
+  }
+  stage_body(st0, st1, kt, NoDma{}, std::false_type{});
+  stage_body(st1, st0, kt + 1, NoDma{}, std::true_type{});
 
   // ---- epilogue ----------------------------------------------------------
-  // Lane (lrow, lg) of sub-tile (i, j) holds column lrow and rows
-  // 8*(r/4) + 4*lg + (r%4) in accumulator register r.  All loops are
-  // compile-time (static_for), so the accumulators never leave registers;
-  // per-column scales are loaded once per sub-tile column, per-row scales
-  // once per sub-tile row.
-  const int64_t row_base = m0 + wm * WTM + 4 * lg;
-  const int64_t col_base = n0 + wn * WTN + lrow;
-  float cs[TN], cs2[TN];
-  static_for<TN>([&](auto jc) {
-    constexpr int j = decltype(jc)::value;
-    const int64_t col = col_base + j * 32;
-    cs[j] = (p.col_scale && col < p.N) ? p.col_scale[col] : 1.f;
-    cs2[j] = (NB == 2 && p.col_scale2 && col < p.N) ? p.col_scale2[col] : 1.f;
-  });
+  // Lane (lrow, lg) holds row m0 + wm*WTM + 32*i + lrow, columns
+  // n0 + wn*WTN + 32*j + 8*g + 4*lg + (0..3) in registers 4g..4g+3 of
+  // sub-tile (i, j): every store is four consecutive outputs.  For each
+  // sub-tile column j all its loads (scales, residual) are issued before any
+  // of its stores, so their latencies overlap instead of alternating with
+  // the stores they might alias.
+  const int64_t row0 = m0 + wm * WTM + lrow;
+  const int64_t col0 = n0 + wn * WTN + 4 * lg;
   const int odt = p.out_dtype;
+  float rs[TM];
   static_for<TM>([&](auto ic) {
     constexpr int i = decltype(ic)::value;
-    float rs[16];
-    static_for<16>([&](auto rc) {
-      constexpr int r = decltype(rc)::value;
-      const int64_t row = row_base + i * 32 + 8 * (r >> 2) + (r & 3);
-      rs[r] = (MODE == GM_I8 && p.row_scale && row < p.M) ? p.row_scale[row] : 1.f;
+    const int64_t row = row0 + i * 32;
+    rs[i] = (MODE == GM_I8 && p.row_scale && row < p.M) ? p.row_scale[row] : 1.f;
+  });
+  static_for<TN>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    v4f cs[4], cs2[4];
+    static_for<4>([&](auto gc) {
+      constexpr int g = decltype(gc)::value;
+      const int64_t col = col0 + j * 32 + 8 * g;
+      const bool in = col < p.N;
+      cs[g] = (p.col_scale && in) ? v4f{p.col_scale[col], p.col_scale[col + 1], p.col_scale[col + 2],
+                                         p.col_scale[col + 3]}
+                                  : v4f{1.f, 1.f, 1.f, 1.f};
+      if constexpr (NB == 2)
+        cs2[g] = (p.col_scale2 && in) ? v4f{p.col_scale2[col], p.col_scale2[col + 1],
+                                            p.col_scale2[col + 2], p.col_scale2[col + 3]}
+                                      : v4f{1.f, 1.f, 1.f, 1.f};
     });
-    static_for<TN>([&](auto jc) {
-      constexpr int j = decltype(jc)::value;
-      const int64_t col = col_base + j * 32;
-      if (col < p.N) {
-        static_for<16>([&](auto rc) {
-          constexpr int r = decltype(rc)::value;
-          const int64_t row = row_base + i * 32 + 8 * (r >> 2) + (r & 3);
-          if (row < p.M) {
+    v4f res[TM][4];
+    if constexpr (MODE != GM_I8 && EPI != GE_SWIGLU) {
+      if (p.res) {
+        static_for<TM>([&](auto ic) {
+          constexpr int i = decltype(ic)::value;
+          static_for<4>([&](auto gc) {
+            constexpr int g = decltype(gc)::value;
+            const int64_t row = row0 + i * 32, col = col0 + j * 32 + 8 * g;
+            res[i][g] = (row < p.M && col < p.N) ? load4(p.res, p.res_dtype, row * p.ldr + col)
+                                                 : v4f{0.f, 0.f, 0.f, 0.f};
+          });
+        });
+      }
+    }
+    static_for<TM>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      const int64_t row = row0 + i * 32;
+      if (row < p.M) {
+        static_for<4>([&](auto gc) {
+          constexpr int g = decltype(gc)::value;
+          const int64_t col = col0 + j * 32 + 8 * g;
+          if (col < p.N) {
             const int64_t idx = row * p.ldc + col;
+            float v[4];
             if constexpr (MODE == GM_I8) {
-              const int v = acc[0][i][j][r];
               if (odt == DT_I32) {
-                reinterpret_cast<int*>(p.c)[idx] = v;
-              } else {
-                float t = (float)v;
-                if (p.row_scale) t = t * rs[r];
-                if (p.col_scale) t = t * cs[j];
-                store_out(p.c, odt, idx, t);
+                *reinterpret_cast<v4i*>(reinterpret_cast<int*>(p.c) + idx) =
+                    v4i{acc[0][i][j][4 * g], acc[0][i][j][4 * g + 1], acc[0][i][j][4 * g + 2],
+                        acc[0][i][j][4 * g + 3]};
+                return;
               }
+              static_for<4>([&](auto qc) {
+                constexpr int q = decltype(qc)::value;
+                float t = (float)acc[0][i][j][4 * g + q];
+                if (p.row_scale) t = t * rs[i];
+                if (p.col_scale) t = t * cs[g][q];
+                v[q] = t;
+              });
             } else if constexpr (EPI == GE_SWIGLU) {
-              const float g = f16_bits_to_f32(f32_to_f16_bits(acc[0][i][j][r] * cs[j]));
-              const float u = f16_bits_to_f32(f32_to_f16_bits(acc[NB - 1][i][j][r] * cs2[j]));
-              const float sg = g / (1.0f + fast_exp(-g));
-              reinterpret_cast<uint16_t*>(p.c)[idx] = f32_to_f16_bits(sg * u);
+              static_for<4>([&](auto qc) {
+                constexpr int q = decltype(qc)::value;
+                const float gt = f16_bits_to_f32(f32_to_f16_bits(acc[0][i][j][4 * g + q] * cs[g][q]));
+                const float up = f16_bits_to_f32(f32_to_f16_bits(acc[NB - 1][i][j][4 * g + q] * cs2[g][q]));
+                const float sg = gt / (1.0f + fast_exp(-gt));
+                v[q] = sg * up;
+              });
             } else {
-              float t = acc[0][i][j][r];
-              if (p.col_scale) t = t * cs[j];
-              if (p.res) t = t + load_any(p.res, p.res_dtype, row * p.ldr + col);
-              store_out(p.c, odt, idx, t);
+              static_for<4>([&](auto qc) {
+                constexpr int q = decltype(qc)::value;
+                float t = acc[0][i][j][4 * g + q];
+                if (p.col_scale) t = t * cs[g][q];
+                if (p.res) t = t + res[i][g][q];
+                v[q] = t;
+              });
             }
+            store4(p.c, odt, idx, v[0], v[1], v[2], v[3]);
           }
         });
       }
@@ -590,6 +705,11 @@ bool gemm_fast_ok(int mode, const GemmArgs& a) {
   if ((int64_t)256 * a.lda * ea >= ((int64_t)1 << 31)) return false;
   if ((int64_t)256 * a.ldb * eb >= ((int64_t)1 << 31)) return false;
   if (a.M <= 0 || a.N <= 0 || a.K <= 0) return false;
+  // at least two K stages of 128 bytes of A per row
+  if (a.K * ea <= 128) return false;
+  // the epilogue stores (and reads the residual as) four consecutive outputs
+  if (a.N % 4 != 0 || a.ldc % 4 != 0 || !al16(a.c)) return false;
+  if (a.res && (a.ldr % 4 != 0 || !al16(a.res))) return false;
   return true;
 }
 
