@@ -202,6 +202,13 @@ gemm_kernel(GemmArgs p) {
   const int tiles_n = (int)((p.N + BN - 1) / BN);
   int tm, tn;
   tile_of(tiles_m, tiles_n, tm, tn);
+  // The tile coordinates are workgroup-uniform, but the integer divisions in
+  // tile_of run on the vector ALU; readfirstlane states the uniformity, so
+  // the buffer descriptors built from them stay scalar (a descriptor the
+  // compiler believes divergent turns every buffer load into a loop over
+  // lanes).
+  tm = __builtin_amdgcn_readfirstlane(tm);
+  tn = __builtin_amdgcn_readfirstlane(tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   const int64_t rows_a = min((int64_t)BM, p.M - m0);
   const int64_t rows_b = min((int64_t)BN, p.N - n0);
@@ -409,97 +416,147 @@ gemm_kernel(GemmArgs p) {
   stage_body(st1, st0, kt + 1, NoDma{}, std::true_type{});
 
   // ---- epilogue ----------------------------------------------------------
-  // Lane (lrow, lg) holds row m0 + wm*WTM + 32*i + lrow, columns
-  // n0 + wn*WTN + 32*j + 8*g + 4*lg + (0..3) in registers 4g..4g+3 of
-  // sub-tile (i, j): every store is four consecutive outputs.  For each
-  // sub-tile column j all its loads (scales, residual) are issued before any
-  // of its stores, so their latencies overlap instead of alternating with
-  // the stores they might alias.
-  const int64_t row0 = m0 + wm * WTM + lrow;
-  const int64_t col0 = n0 + wn * WTN + 4 * lg;
+  // Lane (lrow, lg) holds row wm*WTM + 32*i + lrow, columns
+  // wn*WTN + 32*j + 8*g + 4*lg + (0..3) of the tile in registers 4g..4g+3 of
+  // sub-tile (i, j).  Stored straight from that layout, every store
+  // instruction would write 16 bytes into each of 32 rows (32 partial-line
+  // requests).  Instead each wave converts its block to the output type in a
+  // private LDS region (the stage buffers are free now), row-major with the
+  // 16-byte chunk XOR-swizzled by row (conflict-free 8/16-byte writes and
+  // 16-byte reads), and reads it back so that every lane stores 16
+  // consecutive bytes and a wave store covers whole rows.  For each
+  // sub-tile column all loads (scales, residual) are issued before any
+  // store they might alias.
+  lds_barrier();  // every wave is done reading the stage buffers
+  const int64_t row0w = m0 + wm * WTM;
+  const int64_t col0w = n0 + wn * WTN;
   const int odt = p.out_dtype;
   float rs[TM];
   static_for<TM>([&](auto ic) {
     constexpr int i = decltype(ic)::value;
-    const int64_t row = row0 + i * 32;
+    const int64_t row = row0w + i * 32 + lrow;
     rs[i] = (MODE == GM_I8 && p.row_scale && row < p.M) ? p.row_scale[row] : 1.f;
   });
-  static_for<TN>([&](auto jc) {
-    constexpr int j = decltype(jc)::value;
-    v4f cs[4], cs2[4];
-    static_for<4>([&](auto gc) {
-      constexpr int g = decltype(gc)::value;
-      const int64_t col = col0 + j * 32 + 8 * g;
-      const bool in = col < p.N;
-      cs[g] = (p.col_scale && in) ? v4f{p.col_scale[col], p.col_scale[col + 1], p.col_scale[col + 2],
-                                         p.col_scale[col + 3]}
-                                  : v4f{1.f, 1.f, 1.f, 1.f};
-      if constexpr (NB == 2)
-        cs2[g] = (p.col_scale2 && in) ? v4f{p.col_scale2[col], p.col_scale2[col + 1],
-                                            p.col_scale2[col + 2], p.col_scale2[col + 3]}
-                                      : v4f{1.f, 1.f, 1.f, 1.f};
-    });
-    v4f res[TM][4];
-    if constexpr (MODE != GM_I8 && EPI != GE_SWIGLU) {
-      if (p.res) {
-        static_for<TM>([&](auto ic) {
-          constexpr int i = decltype(ic)::value;
-          static_for<4>([&](auto gc) {
-            constexpr int g = decltype(gc)::value;
-            const int64_t row = row0 + i * 32, col = col0 + j * 32 + 8 * g;
-            res[i][g] = (row < p.M && col < p.N) ? load4(p.res, p.res_dtype, row * p.ldr + col)
-                                                 : v4f{0.f, 0.f, 0.f, 0.f};
-          });
-        });
-      }
-    }
-    static_for<TM>([&](auto ic) {
-      constexpr int i = decltype(ic)::value;
-      const int64_t row = row0 + i * 32;
-      if (row < p.M) {
+
+  auto epilogue = [&](auto esc) {
+    constexpr int ES = decltype(esc)::value;     // output element bytes
+    constexpr int RB = WTN * ES;                 // bytes per row of the wave block
+    constexpr int PER_ARRAY = (NW + 1) / 2;      // wave regions per stage buffer
+    constexpr int REGION = STAGE / PER_ARRAY;
+    constexpr int TMP = (TM * 32 * RB <= REGION) ? TM : ((TM / 2) * 32 * RB <= REGION ? TM / 2 : 1);
+    static_assert(TMP >= 1 && TM % TMP == 0 && TMP * 32 * RB <= REGION, "epilogue region");
+    static_assert(RB >= 64 && (1024 % RB == 0 || RB % 1024 == 0), "epilogue row bytes");
+    auto swz_out = [](int row) -> int {
+      if constexpr (RB == 64) return (row >> 2) & 3;
+      else if constexpr (RB == 128) return (row >> 1) & 7;
+      else return row & 15;
+    };
+    char* region = (wave < PER_ARRAY ? st0 : st1) + (wave % PER_ARRAY) * (TMP * 32 * RB);
+    static_for<TM / TMP>([&](auto pc) {
+      constexpr int pp = decltype(pc)::value;
+      // 1) this pass's sub-tile rows -> LDS, in the output type
+      static_for<TN>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        v4f cs[4], cs2[4];
         static_for<4>([&](auto gc) {
           constexpr int g = decltype(gc)::value;
-          const int64_t col = col0 + j * 32 + 8 * g;
-          if (col < p.N) {
-            const int64_t idx = row * p.ldc + col;
-            float v[4];
+          const int64_t col = col0w + j * 32 + 8 * g + 4 * lg;
+          const bool in = col < p.N;
+          cs[g] = (p.col_scale && in) ? v4f{p.col_scale[col], p.col_scale[col + 1],
+                                             p.col_scale[col + 2], p.col_scale[col + 3]}
+                                      : v4f{1.f, 1.f, 1.f, 1.f};
+          if constexpr (NB == 2)
+            cs2[g] = (p.col_scale2 && in) ? v4f{p.col_scale2[col], p.col_scale2[col + 1],
+                                                p.col_scale2[col + 2], p.col_scale2[col + 3]}
+                                          : v4f{1.f, 1.f, 1.f, 1.f};
+        });
+        v4f res[TMP][4];
+        if constexpr (MODE != GM_I8 && EPI != GE_SWIGLU) {
+          if (p.res) {
+            static_for<TMP>([&](auto ic) {
+              constexpr int ii = decltype(ic)::value;
+              static_for<4>([&](auto gc) {
+                constexpr int g = decltype(gc)::value;
+                const int64_t row = row0w + (pp * TMP + ii) * 32 + lrow;
+                const int64_t col = col0w + j * 32 + 8 * g + 4 * lg;
+                res[ii][g] = (row < p.M && col < p.N) ? load4(p.res, p.res_dtype, row * p.ldr + col)
+                                                      : v4f{0.f, 0.f, 0.f, 0.f};
+              });
+            });
+          }
+        }
+        static_for<TMP>([&](auto ic) {
+          constexpr int ii = decltype(ic)::value;
+          constexpr int i = pp * TMP + ii;
+          const int rl = ii * 32 + lrow;
+          static_for<4>([&](auto gc) {
+            constexpr int g = decltype(gc)::value;
+            const int byte = (j * 32 + 8 * g + 4 * lg) * ES;
+            char* dst = region + rl * RB + (((byte >> 4) ^ swz_out(rl)) << 4) + (byte & 15);
             if constexpr (MODE == GM_I8) {
               if (odt == DT_I32) {
-                *reinterpret_cast<v4i*>(reinterpret_cast<int*>(p.c) + idx) =
-                    v4i{acc[0][i][j][4 * g], acc[0][i][j][4 * g + 1], acc[0][i][j][4 * g + 2],
-                        acc[0][i][j][4 * g + 3]};
+                *reinterpret_cast<v4i*>(dst) = v4i{acc[0][i][j][4 * g], acc[0][i][j][4 * g + 1],
+                                                   acc[0][i][j][4 * g + 2], acc[0][i][j][4 * g + 3]};
                 return;
               }
-              static_for<4>([&](auto qc) {
-                constexpr int q = decltype(qc)::value;
+            }
+            float v[4];
+            static_for<4>([&](auto qc) {
+              constexpr int q = decltype(qc)::value;
+              if constexpr (MODE == GM_I8) {
                 float t = (float)acc[0][i][j][4 * g + q];
                 if (p.row_scale) t = t * rs[i];
                 if (p.col_scale) t = t * cs[g][q];
                 v[q] = t;
-              });
-            } else if constexpr (EPI == GE_SWIGLU) {
-              static_for<4>([&](auto qc) {
-                constexpr int q = decltype(qc)::value;
+              } else if constexpr (EPI == GE_SWIGLU) {
                 const float gt = f16_bits_to_f32(f32_to_f16_bits(acc[0][i][j][4 * g + q] * cs[g][q]));
-                const float up = f16_bits_to_f32(f32_to_f16_bits(acc[NB - 1][i][j][4 * g + q] * cs2[g][q]));
+                const float up =
+                    f16_bits_to_f32(f32_to_f16_bits(acc[NB - 1][i][j][4 * g + q] * cs2[g][q]));
                 const float sg = gt / (1.0f + fast_exp(-gt));
                 v[q] = sg * up;
-              });
-            } else {
-              static_for<4>([&](auto qc) {
-                constexpr int q = decltype(qc)::value;
+              } else {
                 float t = acc[0][i][j][4 * g + q];
                 if (p.col_scale) t = t * cs[g][q];
-                if (p.res) t = t + res[i][g][q];
+                if (p.res) t = t + res[ii][g][q];
                 v[q] = t;
-              });
+              }
+            });
+            if constexpr (ES == 4) {
+              *reinterpret_cast<v4f*>(dst) = v4f{v[0], v[1], v[2], v[3]};
+            } else {
+              uint32_t lo, hi;
+              if (odt == DT_BF16) {
+                lo = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+                hi = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+              } else {
+                lo = (uint32_t)f32_to_f16_bits(v[0]) | ((uint32_t)f32_to_f16_bits(v[1]) << 16);
+                hi = (uint32_t)f32_to_f16_bits(v[2]) | ((uint32_t)f32_to_f16_bits(v[3]) << 16);
+              }
+              *reinterpret_cast<v2i*>(dst) = v2i{(int)lo, (int)hi};
             }
-            store4(p.c, odt, idx, v[0], v[1], v[2], v[3]);
-          }
+          });
         });
-      }
+      });
+      // 2) LDS -> global: 16 bytes per lane, whole rows per wave store
+      constexpr int NI = TMP * 32 * RB / 1024;
+      constexpr int EPC = 16 / ES;  // elements per 16-byte chunk
+      static_for<NI>([&](auto qc) {
+        constexpr int q = decltype(qc)::value;
+        const int byte = q * 1024 + lane * 16;
+        const int rl = byte / RB, c = (byte % RB) >> 4;
+        const v4i d = *reinterpret_cast<const v4i*>(region + rl * RB + ((c ^ swz_out(rl)) << 4));
+        const int64_t row = row0w + pp * TMP * 32 + rl;
+        const int64_t col = col0w + c * EPC;
+        if (row < p.M) {
+          char* out = reinterpret_cast<char*>(p.c) + (row * p.ldc + col) * ES;
+          if (col + EPC <= p.N) *reinterpret_cast<v4i*>(out) = d;
+          else if (ES == 2 && col < p.N) *reinterpret_cast<v2i*>(out) = v2i{d[0], d[1]};
+        }
+      });
     });
-  });
+  };
+  if (odt == DT_F32 || odt == DT_I32) epilogue(std::integral_constant<int, 4>{});
+  else epilogue(std::integral_constant<int, 2>{});
 }
 
 // ---------------------------------------------------------------------------
