@@ -66,9 +66,12 @@ def _sleep_cycles_per_ms() -> float:
 def event_timed(calls, iters: int):
     """Mean device time per launch of ``iters`` calls (cycling through
     ``calls``) issued back-to-back on the current stream, between one HIP
-    event pair.  A spin kernel holds the stream while the host queues the
-    launches, so host launch cost does not open gaps between them.  Returns
-    (ms per launch, whether the queue stayed ahead of the device)."""
+    event pair on that stream.  When the host issues a call in well under the
+    device time of one, the queue stays ahead of the device by itself and
+    nothing else runs.  Otherwise a bounded spin kernel holds the stream
+    while the host queues the launches (so host launch cost opens no gaps),
+    followed by a few untimed launches that bring the clocks back up.
+    Returns (ms per launch, whether the queue stayed ahead of the device)."""
     import torch
     s = torch.cuda.current_stream()
     torch.cuda.synchronize()
@@ -78,9 +81,20 @@ def event_timed(calls, iters: int):
         c()
     host_ms = (time.perf_counter() - t) * 1e3 / n
     torch.cuda.synchronize()
-    hold_ms = 1.0 + 2.0 * host_ms * iters
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda._sleep(int(hold_ms * _sleep_cycles_per_ms()))
+    a.record(s)
+    for c in calls[:n]:
+        c()
+    b.record(s)
+    torch.cuda.synchronize()
+    dev_ms = a.elapsed_time(b) / n
+    hot = max(3, iters // 8)
+    spin = host_ms > 0.5 * dev_ms
+    hold_ms = 1.0 + 2.0 * host_ms * (iters + hot)
+    if spin:
+        torch.cuda._sleep(int(hold_ms * _sleep_cycles_per_ms()))
+    for i in range(hot):
+        calls[i % len(calls)]()
     a.record(s)
     t0 = time.perf_counter()
     for i in range(iters):
@@ -88,7 +102,9 @@ def event_timed(calls, iters: int):
     queued_ms = (time.perf_counter() - t0) * 1e3
     b.record(s)
     torch.cuda.synchronize()
-    return a.elapsed_time(b) / iters, queued_ms < hold_ms
+    ms = a.elapsed_time(b) / iters
+    fed = (queued_ms < hold_ms) if spin else (queued_ms < ms * iters)
+    return ms, fed
 
 
 PROFILES = ROOT / "profiles"
@@ -145,8 +161,12 @@ def bench_gemm_i8(hx, steps: int, warmup: int, tune: bool = True):
     if tune:
         tune_report = tune_summary(hx.search.tune(1, M, N, K, step))
 
+    hx.manifest_clear()
+    hx.manifest_enable(True)
     for _ in range(warmup):
         step()
+    hx.manifest_enable(False)
+    plan = hx.manifest()["records"]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -170,7 +190,7 @@ def bench_gemm_i8(hx, steps: int, warmup: int, tune: bool = True):
     cfg = hx.config_get(1, cfg_idx)["name"] if cfg_idx >= 0 else "generic"
     return dict(ms_per_step=wall_ms, kernel_ms=ev_ms, tops=tops_wall, tops_kernel=tops_kernel,
                 parity_sampled_rows_bitexact=exact, kernel=cfg, inputs=(a, bt, sa, sb),
-                tune=tune_report, queue_fed=fed)
+                tune=tune_report, queue_fed=fed, plan=plan)
 
 
 def cpu_baseline_gemm_i8(inputs, reps: int = 5):
@@ -527,6 +547,7 @@ def main() -> int:
         "queue_fed": h["queue_fed"],
         "parity": {"int8_sampled_rows_bitexact": h["parity_sampled_rows_bitexact"]},
         "tune": h["tune"],
+        "plan": h["plan"],
         "cpu_baseline": cpu,
         "secondary": secondary,
     }

@@ -75,6 +75,9 @@ SIGNATURES = {
     "hx_config_get": ([_i, _i, ctypes.POINTER(KernelConfig)], _i),
     "hx_config_select": ([_i, _i64, _i64, _i64, _i], _i),
     "hx_config_lookup": ([_i, _i64, _i64, _i64, ctypes.POINTER(_i)], _i),
+    "hx_manifest_enable": ([_i], _i),
+    "hx_manifest_clear": ([], _i),
+    "hx_manifest_json": ([ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)], _i),
 }
 
 _lib = None

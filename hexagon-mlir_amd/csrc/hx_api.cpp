@@ -15,6 +15,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <set>
@@ -182,6 +183,74 @@ static int view1(const hx_memref1d* m, int dt, const char* name, int64_t expect,
 }
 
 // ---------------------------------------------------------------------------
+// Plan manifest
+// ---------------------------------------------------------------------------
+// When enabled, every matmul-family call records the plan it ran: the kernel
+// path, the tile configuration and whether it was pinned by the tuner or the
+// untuned default, why the fast path was or was not taken, and how the weight
+// was supplied.  One record per distinct decision, with a call count.  This
+// is the run-time counterpart of the reference's per-matmul kernel manifest
+// (plan + reason vocabulary, QHB/include/hexagon/Dialect/Hmx/Transforms/
+// HmxManifest.h:81-110; its JSON export, QHB/backend/utils.py:1055-1196).
+struct PlanCtx {
+  const char* entry;   // C entry point the caller used
+  const char* weight;  // "argument", "transposed-to-workspace", "resident-image", "resident-packed"
+  int a_dt, b_dt;
+};
+
+static std::atomic<int> g_manifest_on{0};
+static std::mutex g_manifest_mu;
+static std::vector<std::pair<std::string, uint64_t>> g_manifest;
+static std::map<std::string, size_t> g_manifest_index;
+
+static void note_plan(const PlanCtx& ctx, int64_t m, int64_t n, int64_t k, int c_dt, const char* plan,
+                      const char* config, const char* source, const char* reason) {
+  if (!g_manifest_on.load(std::memory_order_relaxed)) return;
+  char rec[512];
+  snprintf(rec, sizeof(rec),
+           "{\"entry\": \"%s\", \"m\": %lld, \"n\": %lld, \"k\": %lld, \"a\": \"%s\", \"b\": \"%s\", "
+           "\"c\": \"%s\", \"plan\": \"%s\", \"config\": \"%s\", \"config_source\": \"%s\", "
+           "\"reason\": \"%s\", \"weight\": \"%s\"",
+           ctx.entry, (long long)m, (long long)n, (long long)k, dt_name(ctx.a_dt), dt_name(ctx.b_dt),
+           dt_name(c_dt), plan, config, source, reason, ctx.weight);
+  std::lock_guard<std::mutex> lk(g_manifest_mu);
+  auto it = g_manifest_index.find(rec);
+  if (it != g_manifest_index.end()) {
+    ++g_manifest[it->second].second;
+    return;
+  }
+  g_manifest_index.emplace(rec, g_manifest.size());
+  g_manifest.emplace_back(rec, 1);
+}
+
+extern "C" int hx_manifest_enable(int on) { return g_manifest_on.exchange(on ? 1 : 0); }
+
+extern "C" int hx_manifest_clear(void) {
+  std::lock_guard<std::mutex> lk(g_manifest_mu);
+  g_manifest.clear();
+  g_manifest_index.clear();
+  return HX_OK;
+}
+
+extern "C" int hx_manifest_json(char* buf, size_t cap, size_t* needed) {
+  std::string out = "{\"schema\": \"hx.kernel_manifest/v1\", \"build\": \"" HX_BUILD_ID "\", \"records\": [";
+  {
+    std::lock_guard<std::mutex> lk(g_manifest_mu);
+    for (size_t i = 0; i < g_manifest.size(); ++i) {
+      if (i) out += ", ";
+      out += g_manifest[i].first;
+      out += ", \"calls\": " + std::to_string(g_manifest[i].second) + "}";
+    }
+  }
+  out += "]}";
+  if (needed) *needed = out.size() + 1;
+  if (!buf || cap < out.size() + 1)
+    return fail(HX_ERR_ARG, "hx_manifest_json: buffer of %zu bytes, %zu needed", cap, out.size() + 1);
+  memcpy(buf, out.c_str(), out.size() + 1);
+  return HX_OK;
+}
+
+// ---------------------------------------------------------------------------
 // Pinned configurations
 // ---------------------------------------------------------------------------
 static std::map<std::tuple<int, int, int64_t, int64_t, int64_t>, int> g_pins;
@@ -220,19 +289,25 @@ static int pinned(int op, int64_t m, int64_t n, int64_t k) {
   return it == g_pins.end() ? -1 : it->second;
 }
 
-// Mode-table index a call of family `op` runs with.
-static int resolve_gemm(int op, int64_t M, int64_t N, int64_t K) {
+// Mode-table index a call of family `op` runs with (*was_pinned: chosen by
+// the tuner rather than the untuned default).
+static int resolve_gemm(int op, int64_t M, int64_t N, int64_t K, bool* was_pinned = nullptr) {
   int mode, epi;
   op_gemm(op, &mode, &epi);
   const int pin = pinned(op, M, N, K);
+  if (was_pinned) *was_pinned = false;
   if (pin >= 0) {
     std::vector<int> idx = family_indices(op);
-    if (pin < (int)idx.size()) return idx[pin];
+    if (pin < (int)idx.size()) {
+      if (was_pinned) *was_pinned = true;
+      return idx[pin];
+    }
   }
   return gemm_default_config(mode, epi, M, N, K);
 }
-static int resolve_gemv(int64_t M, int64_t N, int64_t K) {
+static int resolve_gemv(int64_t M, int64_t N, int64_t K, bool* was_pinned = nullptr) {
   const int pin = pinned(HX_OP_GEMV_W8, M, N, K);
+  if (was_pinned) *was_pinned = pin >= 0 && pin < gemv_packed_config_count();
   if (pin >= 0 && pin < gemv_packed_config_count()) return pin;
   (void)N; (void)K;
   // untuned choice from the MI355X sweep: one column tile per workgroup for
@@ -240,18 +315,28 @@ static int resolve_gemv(int64_t M, int64_t N, int64_t K) {
   return M <= 8 ? 1 : 2;
 }
 
-static int run_gemm(int op, GemmArgs& a, hipStream_t s) {
+static int run_gemm(int op, GemmArgs& a, hipStream_t s, const PlanCtx& ctx) {
   int mode, epi;
   op_gemm(op, &mode, &epi);
   if (a.M == 0 || a.N == 0) return HX_OK;
-  if (gemm_fast_ok(mode, a)) {
-    const int cfg = resolve_gemm(op, a.M, a.N, a.K);
-    if (cfg >= 0) return map_internal(launch_gemm(mode, cfg, a, s), "gemm");
+  const char* refusal = gemm_fast_refusal(mode, a);
+  if (!refusal) {
+    bool pin = false;
+    const int cfg = resolve_gemm(op, a.M, a.N, a.K, &pin);
+    if (cfg >= 0) {
+      note_plan(ctx, a.M, a.N, a.K, a.out_dtype, "mfma-tiled", gemm_config(mode, cfg)->name,
+                pin ? "pinned" : "default", "selected-aligned");
+      return map_internal(launch_gemm(mode, cfg, a, s), "gemm");
+    }
+    refusal = "no-config";
   }
+  note_plan(ctx, a.M, a.N, a.K, a.out_dtype, "mfma-generic", "generic_32x32", "fixed", refusal);
   return map_internal(launch_gemm_generic(mode, a, s), "gemm_generic");
 }
 
-static int run_gemv(GemvArgs& a, hipStream_t s) {
+static int run_gemv(GemvArgs& a, hipStream_t s, const PlanCtx& ctx) {
+  static const char* const names[] = {"gemv_nk_ct1", "gemv_nk_ct2", "gemv_nk_ct4"};
+  note_plan(ctx, a.M, a.N, a.K, HX_F16, "gemv", names[gemv_raw_config(a)], "fixed", "min-rows");
   return map_internal(launch_gemv_w8a16(a, s), "gemv_w8a16");
 }
 
@@ -362,13 +447,15 @@ extern "C" int hx_matmul(const hx_memref2d* a, int a_dtype, const hx_memref2d* b
     return rc;
   if (residual) { g.res = vr.p; g.ldr = vr.ld; g.res_dtype = residual_dtype; }
 
+  const PlanCtx ctx{"hx_matmul", b_layout == HX_LAYOUT_KN ? "transposed-to-workspace" : "argument",
+                    a_dtype, b_dtype};
   if (op == HX_OP_MATMUL_W8 && M <= 16 && !residual && c_dtype == HX_F16) {
     GemvArgs v{};
     v.x = g.a; v.ldx = g.lda; v.w = (const int8_t*)g.b; v.ldw = g.ldb;
     v.scale = g.col_scale; v.y = g.c; v.ldy = g.ldc; v.M = M; v.N = N; v.K = K;
-    if (gemv_fast_ok(v)) return run_gemv(v, s);
+    if (gemv_fast_ok(v)) return run_gemv(v, s, ctx);
   }
-  return run_gemm(op, g, s);
+  return run_gemm(op, g, s, ctx);
 }
 
 extern "C" int hx_gemm_i8(const hx_memref2d* a, const hx_memref2d* b, int b_layout,
@@ -408,7 +495,9 @@ extern "C" int hx_gemm_i8(const hx_memref2d* a, const hx_memref2d* b, int b_layo
   g.out_dtype = c_dtype;
   g.row_scale = row_scale ? (const float*)vrs.p : nullptr;
   g.col_scale = col_scale ? (const float*)vcs.p : nullptr;
-  return run_gemm(HX_OP_GEMM_I8, g, s);
+  const PlanCtx ctx{"hx_gemm_i8", b_layout == HX_LAYOUT_KN ? "transposed-to-workspace" : "argument",
+                    HX_I8, HX_I8};
+  return run_gemm(HX_OP_GEMM_I8, g, s, ctx);
 }
 
 extern "C" int hx_gemv_w8a16(const hx_memref2d* x, const hx_memref2d* w, int w_layout,
@@ -638,7 +727,8 @@ extern "C" int hx_weight_info(hx_weight_t w, int64_t* k, int64_t* n, int* dtype,
 }
 
 static int matmul_resident_impl(const View2& vx, hx_weight* w, const View2* vr, int r_dt,
-                                const View2& vy, int y_dt, hipStream_t s) {
+                                const View2& vy, int y_dt, hipStream_t s, const char* entry) {
+  const int x_dt = w->dtype == HX_BF16 ? HX_BF16 : HX_F16;
   const int64_t M = vx.rows;
   if (M == 0) return HX_OK;
   // The packed GEMV reads activations as 8-element (16-byte) groups.
@@ -647,8 +737,11 @@ static int matmul_resident_impl(const View2& vx, hx_weight* w, const View2* vr, 
     GemvArgs v{};
     v.x = vx.p; v.ldx = vx.ld; v.w = nullptr; v.ldw = 0;
     v.scale = w->scale; v.y = vy.p; v.ldy = vy.ld; v.M = M; v.N = w->N; v.K = w->K;
-    return map_internal(launch_gemv_packed(resolve_gemv(M, w->N, w->K), v, w->packed, s),
-                        "gemv_packed");
+    bool pin = false;
+    const int cfg = resolve_gemv(M, w->N, w->K, &pin);
+    note_plan(PlanCtx{entry, "resident-packed", x_dt, w->dtype}, M, w->N, w->K, HX_F16, "gemv-packed",
+              gemv_packed_config(cfg)->name, pin ? "pinned" : "default", "min-rows");
+    return map_internal(launch_gemv_packed(cfg, v, w->packed, s), "gemv_packed");
   }
   GemmArgs g{};
   g.a = vx.p; g.lda = vx.ld;
@@ -659,7 +752,7 @@ static int matmul_resident_impl(const View2& vx, hx_weight* w, const View2* vr, 
   g.col_scale = w->scale;
   if (vr) { g.res = vr->p; g.ldr = vr->ld; g.res_dtype = r_dt; }
   const int op = w->dtype == HX_I8 ? HX_OP_MATMUL_W8 : w->dtype == HX_F16 ? HX_OP_MATMUL_F16 : HX_OP_MATMUL_BF16;
-  return run_gemm(op, g, s);
+  return run_gemm(op, g, s, PlanCtx{entry, "resident-image", x_dt, w->dtype});
 }
 
 extern "C" int hx_matmul_resident(const hx_memref2d* x, int x_dtype, hx_weight_t wt,
@@ -687,7 +780,7 @@ extern "C" int hx_matmul_resident(const hx_memref2d* x, int x_dtype, hx_weight_t
     if (vr.rows != vx.rows || vr.cols != w->N) return fail(HX_ERR_SHAPE, "hx_matmul_resident: residual shape");
   }
   return matmul_resident_impl(vx, w, residual ? &vr : nullptr, residual_dtype, vy, y_dtype,
-                              (hipStream_t)stream);
+                              (hipStream_t)stream, "hx_matmul_resident");
 }
 
 extern "C" int hx_swiglu_ffn(const hx_memref2d* x, const hx_memref1d* gamma, float eps, hx_weight_t w_gate,
@@ -728,8 +821,8 @@ extern "C" int hx_swiglu_ffn(const hx_memref2d* x, const hx_memref1d* gamma, flo
   View2 vh{h, T, H, H}, va{act, T, I, I};
   if (skinny) {
     View2 vgo{ws + off_g, T, I, I}, vuo{ws + off_u, T, I, I};
-    if ((rc = matmul_resident_impl(vh, wg, nullptr, 0, vgo, HX_F16, s))) return rc;
-    if ((rc = matmul_resident_impl(vh, wu, nullptr, 0, vuo, HX_F16, s))) return rc;
+    if ((rc = matmul_resident_impl(vh, wg, nullptr, 0, vgo, HX_F16, s, "hx_swiglu_ffn"))) return rc;
+    if ((rc = matmul_resident_impl(vh, wu, nullptr, 0, vuo, HX_F16, s, "hx_swiglu_ffn"))) return rc;
     rc = map_internal(launch_silu_mul_f16(vgo.p, I, vuo.p, I, act, I, T, I, s), "silu_mul");
     if (rc) return rc;
   } else {
@@ -740,9 +833,10 @@ extern "C" int hx_swiglu_ffn(const hx_memref2d* x, const hx_memref1d* gamma, flo
     g.M = T; g.N = I; g.K = H;
     g.out_dtype = HX_F16;
     g.col_scale = wg->scale; g.col_scale2 = wu->scale;
-    if ((rc = run_gemm(HX_OP_SWIGLU_W8, g, s))) return rc;
+    if ((rc = run_gemm(HX_OP_SWIGLU_W8, g, s, PlanCtx{"hx_swiglu_ffn", "resident-image", HX_F16, HX_I8})))
+      return rc;
   }
-  return matmul_resident_impl(va, wd, nullptr, 0, vy, HX_F16, s);
+  return matmul_resident_impl(va, wd, nullptr, 0, vy, HX_F16, s, "hx_swiglu_ffn");
 }
 
 // ---------------------------------------------------------------------------

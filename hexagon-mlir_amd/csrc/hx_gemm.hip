@@ -15,18 +15,20 @@
 // Design (MI355X-first, not a translation of the crouton scheme):
 //   * one workgroup per BMxBN output tile; a tile is split over WMxWN waves,
 //     each owning (BM/WM)x(BN/WN) = TMxTN MFMA 32x32 sub-tiles whose
-//     accumulators live in AGPRs for the whole K loop;
-//   * K is walked in stages of 128 bytes of A per row; each stage of A and B
-//     is loaded with 16-byte buffer loads (out-of-range rows and the K tail
-//     read as zero from the buffer descriptor's range) into registers one
-//     stage ahead and written to a double-buffered LDS ring, one barrier per
-//     stage;
+//     accumulators stay in registers for the whole K loop;
+//   * K is walked in stages of 128 bytes of A per row, double-buffered in
+//     LDS; each stage is fetched with direct-to-LDS 16-byte buffer loads
+//     (out-of-range rows and the K tail read as zero from the buffer
+//     descriptor's range), one LDS-only barrier per stage;
 //   * LDS rows are 128 (or 64) bytes with the 16-byte chunk index XOR-swizzled
 //     by the row so that the MFMA operand reads (16 bytes per lane, 32 rows)
 //     and the stage writes are bank-conflict free;
+//   * operand fragments are double-buffered in registers (the reads of k-step
+//     s+1 are in flight while the MFMAs of step s run);
 //   * B is consumed K-contiguous ([N][K]), i.e. the weight image the resident
 //     registry keeps -- the counterpart of the reference's pre-packed WH
 //     crouton image (QHB/backend/hmx_weight_prepack.py:171-212);
+//   * the epilogue converts each wave's block in LDS and writes whole rows;
 //   * workgroup ids are renumbered so that each XCD (workgroups are dealt to
 //     the 8 XCDs round robin) walks a compact block of tiles: the B strips of
 //     that block stay resident in the XCD's L2 while its M-tiles go by.
@@ -134,24 +136,6 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// Store four consecutive outputs (16-byte aligned for 4-byte types, 8-byte
-// aligned for 2-byte types).
-__device__ __forceinline__ void store4(void* c, int dt, int64_t idx, float v0, float v1, float v2,
-                                       float v3) {
-  if (dt == DT_F32) {
-    *reinterpret_cast<v4f*>(reinterpret_cast<float*>(c) + idx) = v4f{v0, v1, v2, v3};
-  } else {
-    uint32_t lo, hi;
-    if (dt == DT_F16) {
-      lo = (uint32_t)f32_to_f16_bits(v0) | ((uint32_t)f32_to_f16_bits(v1) << 16);
-      hi = (uint32_t)f32_to_f16_bits(v2) | ((uint32_t)f32_to_f16_bits(v3) << 16);
-    } else {
-      lo = (uint32_t)f32_to_bf16(v0) | ((uint32_t)f32_to_bf16(v1) << 16);
-      hi = (uint32_t)f32_to_bf16(v2) | ((uint32_t)f32_to_bf16(v3) << 16);
-    }
-    *reinterpret_cast<v2i*>(reinterpret_cast<uint16_t*>(c) + idx) = v2i{(int)lo, (int)hi};
-  }
-}
 __device__ __forceinline__ v4f load4(const void* p, int dt, int64_t idx) {
   if (dt == DT_F32) return *reinterpret_cast<const v4f*>(reinterpret_cast<const float*>(p) + idx);
   const v2i w = *reinterpret_cast<const v2i*>(reinterpret_cast<const uint16_t*>(p) + idx);
@@ -665,22 +649,26 @@ struct GemmEntry {
   GemmLaunch fn;
 };
 
-#define HX_GEMM_CFGS(MODE)                                                                 \
-  {{256, 256, 2, 2, GE_STORE, "256x256_w2x2"}, &launch_one<MODE, 256, 256, 2, 2, GE_STORE>}, \
-  {{256, 128, 2, 2, GE_STORE, "256x128_w2x2"}, &launch_one<MODE, 256, 128, 2, 2, GE_STORE>}, \
-  {{128, 256, 2, 2, GE_STORE, "128x256_w2x2"}, &launch_one<MODE, 128, 256, 2, 2, GE_STORE>}, \
-  {{128, 128, 2, 2, GE_STORE, "128x128_w2x2"}, &launch_one<MODE, 128, 128, 2, 2, GE_STORE>}, \
-  {{256, 256, 2, 4, GE_STORE, "256x256_w2x4"}, &launch_one<MODE, 256, 256, 2, 4, GE_STORE>}, \
-  {{64, 64, 2, 2, GE_STORE, "64x64_w2x2"}, &launch_one<MODE, 64, 64, 2, 2, GE_STORE>}
+// occ = workgroups a CU holds at once, rate = relative output throughput of
+// one CU at that occupancy, both measured on MI355X at 4096^3 (int8, fp16)
+// and 2048x11008x4096 (W8A16); they drive the untuned default choice.
+#define HX_GEMM_CFGS(MODE)                                                                         \
+  {{256, 256, 2, 2, GE_STORE, "256x256_w2x2", 1, 0.74f}, &launch_one<MODE, 256, 256, 2, 2, GE_STORE>}, \
+  {{256, 128, 2, 2, GE_STORE, "256x128_w2x2", 1, 0.77f}, &launch_one<MODE, 256, 128, 2, 2, GE_STORE>}, \
+  {{128, 256, 2, 2, GE_STORE, "128x256_w2x2", 1, 0.77f}, &launch_one<MODE, 128, 256, 2, 2, GE_STORE>}, \
+  {{128, 128, 2, 2, GE_STORE, "128x128_w2x2", 2, 0.89f}, &launch_one<MODE, 128, 128, 2, 2, GE_STORE>}, \
+  {{256, 256, 2, 4, GE_STORE, "256x256_w2x4", 1, 1.00f}, &launch_one<MODE, 256, 256, 2, 4, GE_STORE>}, \
+  {{64, 64, 2, 2, GE_STORE, "64x64_w2x2", 4, 0.61f}, &launch_one<MODE, 64, 64, 2, 2, GE_STORE>}
 
 static const GemmEntry kI8[] = {HX_GEMM_CFGS(GM_I8)};
 static const GemmEntry kF16[] = {HX_GEMM_CFGS(GM_F16)};
 static const GemmEntry kBF16[] = {HX_GEMM_CFGS(GM_BF16)};
 static const GemmEntry kW8[] = {
     HX_GEMM_CFGS(GM_W8),
-    {{256, 128, 2, 2, GE_SWIGLU, "swiglu_256x128_w2x2"}, &launch_one<GM_W8, 256, 128, 2, 2, GE_SWIGLU>},
-    {{128, 128, 2, 2, GE_SWIGLU, "swiglu_128x128_w2x2"}, &launch_one<GM_W8, 128, 128, 2, 2, GE_SWIGLU>},
-    {{128, 64, 2, 2, GE_SWIGLU, "swiglu_128x64_w2x2"}, &launch_one<GM_W8, 128, 64, 2, 2, GE_SWIGLU>},
+    {{256, 128, 2, 4, GE_SWIGLU, "swiglu_256x128_w2x4", 1, 0.95f}, &launch_one<GM_W8, 256, 128, 2, 4, GE_SWIGLU>},
+    {{256, 128, 2, 2, GE_SWIGLU, "swiglu_256x128_w2x2", 1, 0.77f}, &launch_one<GM_W8, 256, 128, 2, 2, GE_SWIGLU>},
+    {{128, 128, 2, 2, GE_SWIGLU, "swiglu_128x128_w2x2", 1, 0.80f}, &launch_one<GM_W8, 128, 128, 2, 2, GE_SWIGLU>},
+    {{128, 64, 2, 2, GE_SWIGLU, "swiglu_128x64_w2x2", 2, 0.80f}, &launch_one<GM_W8, 128, 64, 2, 2, GE_SWIGLU>},
 };
 
 static const GemmEntry* table(int mode, int& n) {
@@ -719,10 +707,9 @@ static int num_cus() {
   return g_num_cus;
 }
 
-// Untuned choice: estimated time = waves_of_tiles * tile_area / efficiency.
-// The efficiencies are relative throughputs measured on MI355X at 4096^3
-// (the 8-wave 256x256 tile is the fastest per MAC; 128x128 beats the
-// 4-wave 256-wide tiles); the autotuner replaces this guess per shape.
+// Untuned choice: estimated time = rounds * occ * tile_area / rate, where a
+// round is one workgroup in every resident slot (CUs x occ).  The autotuner
+// replaces this guess per shape.
 int gemm_default_config(int mode, int epi, int64_t M, int64_t N, int64_t K) {
   (void)K;
   int n;
@@ -735,14 +722,9 @@ int gemm_default_config(int mode, int epi, int64_t M, int64_t N, int64_t K) {
     const GemmConfig& c = t[i].cfg;
     if (c.epi != epi) continue;
     const double tiles = (double)((M + c.bm - 1) / c.bm) * (double)((N + c.bn - 1) / c.bn);
-    const double waves = (double)(int64_t)((tiles + cus - 1) / cus);
-    const double area = (double)c.bm * c.bn;
-    double eff;
-    if (area >= 65536) eff = (c.wm * c.wn == 8) ? 1.0 : 0.72;
-    else if (area >= 32768) eff = 0.68;
-    else if (area >= 16384) eff = 0.78;
-    else eff = 0.55;
-    const double cost = waves * area / eff;
+    const double slots = (double)cus * c.occ;
+    const double rounds = (double)(int64_t)((tiles + slots - 1) / slots);
+    const double cost = rounds * c.occ * (double)c.bm * c.bn / c.rate;
     if (best < 0 || cost < best_cost - 1e-9) {
       best = i;
       best_cost = cost;
@@ -751,24 +733,27 @@ int gemm_default_config(int mode, int epi, int64_t M, int64_t N, int64_t K) {
   return best;
 }
 
-bool gemm_fast_ok(int mode, const GemmArgs& a) {
+const char* gemm_fast_refusal(int mode, const GemmArgs& a) {
   const int ea = (mode == GM_I8) ? 1 : 2;
   const int eb = (mode == GM_I8 || mode == GM_W8) ? 1 : 2;
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
-  if (!al16(a.a) || !al16(a.b) || (a.b2 && !al16(a.b2))) return false;
-  if ((a.lda * ea) % 16 != 0 || (a.ldb * eb) % 16 != 0) return false;
-  if ((a.K * ea) % 16 != 0 || (a.K * eb) % 16 != 0) return false;
+  if (a.M <= 0 || a.N <= 0 || a.K <= 0) return "empty";
+  if (!al16(a.a) || !al16(a.b) || (a.b2 && !al16(a.b2))) return "unaligned-base";
+  if ((a.lda * ea) % 16 != 0 || (a.ldb * eb) % 16 != 0) return "row-stride";
+  if ((a.K * ea) % 16 != 0 || (a.K * eb) % 16 != 0) return "k-granularity";
   // 32-bit buffer offsets inside one tile's row range
-  if ((int64_t)256 * a.lda * ea >= ((int64_t)1 << 31)) return false;
-  if ((int64_t)256 * a.ldb * eb >= ((int64_t)1 << 31)) return false;
-  if (a.M <= 0 || a.N <= 0 || a.K <= 0) return false;
+  if ((int64_t)256 * a.lda * ea >= ((int64_t)1 << 31)) return "offset-range";
+  if ((int64_t)256 * a.ldb * eb >= ((int64_t)1 << 31)) return "offset-range";
   // at least two K stages of 128 bytes of A per row
-  if (a.K * ea <= 128) return false;
+  if (a.K * ea <= 128) return "shallow-k";
   // the epilogue stores (and reads the residual as) four consecutive outputs
-  if (a.N % 4 != 0 || a.ldc % 4 != 0 || !al16(a.c)) return false;
-  if (a.res && (a.ldr % 4 != 0 || !al16(a.res))) return false;
-  return true;
+  if (a.N % 4 != 0) return "n-granularity";
+  if (a.ldc % 4 != 0 || !al16(a.c)) return "output-layout";
+  if (a.res && (a.ldr % 4 != 0 || !al16(a.res))) return "residual-layout";
+  return nullptr;
 }
+
+bool gemm_fast_ok(int mode, const GemmArgs& a) { return gemm_fast_refusal(mode, a) == nullptr; }
 
 int launch_gemm(int mode, int cfg_idx, const GemmArgs& a, hipStream_t s) {
   int n;

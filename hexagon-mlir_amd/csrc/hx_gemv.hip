@@ -279,17 +279,20 @@ static void gemv_launch_one(const GemvArgs& a, hipStream_t s) {
 // image): 16*CT columns per workgroup, the four waves split K.
 static const GemvLaunch kGemvNK[] = {&gemv_launch_one<1>, &gemv_launch_one<2>, &gemv_launch_one<4>};
 
-bool gemv_fast_ok(const GemvArgs& a) {
+const char* gemv_fast_refusal(const GemvArgs& a) {
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
-  if (a.M < 1 || a.M > 16 || a.N < 1 || a.K < 1) return false;
-  if (a.K % 16 != 0 || a.ldw % 16 != 0 || (a.ldx * 2) % 16 != 0) return false;
-  if (!al16(a.x) || !al16(a.w)) return false;
-  if ((int64_t)64 * a.ldw >= ((int64_t)1 << 31)) return false;
-  if ((int64_t)a.M * a.ldx * 2 >= ((int64_t)1 << 31)) return false;
-  return true;
+  if (a.M < 1 || a.M > 16 || a.N < 1 || a.K < 1) return "row-count";
+  if (a.K % 16 != 0) return "k-granularity";
+  if (a.ldw % 16 != 0 || (a.ldx * 2) % 16 != 0) return "row-stride";
+  if (!al16(a.x) || !al16(a.w)) return "unaligned-base";
+  if ((int64_t)64 * a.ldw >= ((int64_t)1 << 31)) return "offset-range";
+  if ((int64_t)a.M * a.ldx * 2 >= ((int64_t)1 << 31)) return "offset-range";
+  return nullptr;
 }
+bool gemv_fast_ok(const GemvArgs& a) { return gemv_fast_refusal(a) == nullptr; }
+int gemv_raw_config(const GemvArgs& a) { return a.N >= 4096 ? 1 : 0; }
 int launch_gemv_w8a16(const GemvArgs& a, hipStream_t s) {
-  kGemvNK[a.N >= 4096 ? 1 : 0](a, s);
+  kGemvNK[gemv_raw_config(a)](a, s);
   return HXI_OK;
 }
 

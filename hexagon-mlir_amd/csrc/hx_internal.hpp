@@ -58,14 +58,18 @@ struct GemmConfig {
   int bm, bn, wm, wn;   // block tile and wave grid
   int epi;              // GemmEpi
   const char* name;
+  int occ;              // workgroups resident per CU (LDS / register limit)
+  float rate;           // measured output throughput of one CU, relative
 };
 
 int gemm_config_count(int mode);
 const GemmConfig* gemm_config(int mode, int idx);
 // Default (untuned) config index for a shape.
 int gemm_default_config(int mode, int epi, int64_t M, int64_t N, int64_t K);
-// True when the fast kernel's alignment preconditions hold for these args.
+// True when the fast kernel's alignment preconditions hold for these args;
+// otherwise gemm_fast_refusal names the first one that fails.
 bool gemm_fast_ok(int mode, const GemmArgs& a);
+const char* gemm_fast_refusal(int mode, const GemmArgs& a);
 int launch_gemm(int mode, int cfg_idx, const GemmArgs& a, hipStream_t s);
 // Any shape / alignment; simple tiled kernel, same arithmetic contract.
 int launch_gemm_generic(int mode, const GemmArgs& a, hipStream_t s);
@@ -80,6 +84,9 @@ struct GemvArgs {
 };
 struct GemvConfig { int ct, kw; const char* name; };
 bool gemv_fast_ok(const GemvArgs& a);
+const char* gemv_fast_refusal(const GemvArgs& a);
+// Column tiles per workgroup (1, 2 or 4 as index 0..2) of the [N][K] kernel.
+int gemv_raw_config(const GemvArgs& a);
 // [N][K] weight GEMV (unregistered weights).
 int launch_gemv_w8a16(const GemvArgs& a, hipStream_t s);
 // Fragment-packed resident image for the decode GEMV (see hx_gemv.hip).

@@ -291,6 +291,28 @@ def build_id() -> str:
     return load().hx_build_id().decode()
 
 
+def manifest_enable(on: bool = True) -> bool:
+    """Start (or stop) recording the plan of every matmul-family call;
+    returns the previous state."""
+    return bool(load().hx_manifest_enable(1 if on else 0))
+
+
+def manifest_clear() -> None:
+    load().hx_manifest_clear()
+
+
+def manifest() -> dict:
+    """The recorded plans: {"schema", "build", "records": [{entry, m, n, k,
+    a, b, c, plan, config, config_source, reason, weight, calls}, ...]}."""
+    import json
+    L = load()
+    need = ctypes.c_size_t(0)
+    L.hx_manifest_json(None, 0, ctypes.byref(need))
+    buf = ctypes.create_string_buffer(need.value + 4096)
+    check(L.hx_manifest_json(buf, len(buf), ctypes.byref(need)), "hx_manifest_json")
+    return json.loads(buf.value.decode())
+
+
 # --------------------------------------------------------------------------- #
 # Pre-bound calls: descriptors built once, so a repeated call costs one C-ABI
 # entry (for timing loops and serving loops; tensors must stay alive).

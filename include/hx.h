@@ -31,6 +31,7 @@
 #ifndef HX_H
 #define HX_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -255,6 +256,29 @@ int hx_config_select(int op, int64_t m, int64_t n, int64_t k, int index);
  * the untuned default.  *index = -1 means the generic (any-alignment)
  * kernel. */
 int hx_config_lookup(int op, int64_t m, int64_t n, int64_t k, int* index);
+
+/* ---------------------------------------------------------------------- */
+/* Plan manifest                                                           */
+/* ---------------------------------------------------------------------- */
+
+/* While enabled, every matmul-family call (hx_matmul, hx_gemm_i8,
+ * hx_gemv_w8a16, hx_matmul_resident, the GEMMs of hx_swiglu_ffn) records the
+ * plan it ran -- kernel path ("mfma-tiled", "mfma-generic", "gemv",
+ * "gemv-packed"), tile configuration and whether the tuner pinned it, the
+ * reason ("selected-aligned", "min-rows", or the fast-path precondition that
+ * failed), and how the weight was supplied -- one record per distinct
+ * decision with a call count.  Replaces the per-matmul semantic manifest
+ * `hmx.kernel_manifest` with its plan/reason vocabulary
+ * (QHB/include/hexagon/Dialect/Hmx/Transforms/HmxManifest.h:41, 81-110) and
+ * its JSON export (QHB/backend/utils.py:1055-1196); here the decisions are
+ * made per call at run time, so they are recorded at run time.
+ * hx_manifest_enable returns the previous state.  hx_manifest_json writes
+ * a NUL-terminated JSON document {"schema": "hx.kernel_manifest/v1",
+ * "build": ..., "records": [...]} into buf and sets *needed to its size;
+ * HX_ERR_ARG (with *needed set) when cap is too small. */
+int hx_manifest_enable(int on);
+int hx_manifest_clear(void);
+int hx_manifest_json(char* buf, size_t cap, size_t* needed);
 
 #ifdef __cplusplus
 }

@@ -84,3 +84,25 @@ def test_missing_library_fails_loudly(hx, monkeypatch, tmp_path):
     monkeypatch.setattr(hx._abi, "LIB_PATH", tmp_path / "libhxmi.so")
     with pytest.raises(ImportError, match="no fallback"):
         hx._abi.load()
+
+
+def test_manifest_without_device(hx):
+    """The manifest export needs no GPU: an empty manifest is valid JSON with
+    the schema tag, and a too-small buffer is an error that reports the size
+    needed."""
+    import ctypes
+    import json
+    L = hx.load()
+    prev = L.hx_manifest_enable(0)
+    L.hx_manifest_clear()
+    doc = hx.manifest()
+    assert doc["schema"] == "hx.kernel_manifest/v1" and doc["records"] == []
+    assert doc["build"] == hx.build_id()
+    need = ctypes.c_size_t(0)
+    buf = ctypes.create_string_buffer(8)
+    assert hx._abi.ERRORS[L.hx_manifest_json(buf, 8, ctypes.byref(need))] == "HX_ERR_ARG"
+    assert need.value > 8 and "needed" in hx._abi.last_error()
+    big = ctypes.create_string_buffer(need.value)
+    assert L.hx_manifest_json(big, need.value, ctypes.byref(need)) == 0
+    assert json.loads(big.value.decode())["records"] == []
+    L.hx_manifest_enable(prev)

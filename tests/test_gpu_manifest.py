@@ -1,0 +1,91 @@
+"""The plan manifest records, per matmul-family call, the kernel path, the
+tile configuration and who chose it, the reason, and how the weight was
+supplied (the run-time counterpart of the reference's hmx.kernel_manifest
+plan/reason records, QHB/include/hexagon/Dialect/Hmx/Transforms/
+HmxManifest.h:81-110)."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def records(hx):
+    return hx.manifest()["records"]
+
+
+def test_manifest_records_plans_and_reasons(hx, dev):
+    hx.manifest_clear()
+    prev = hx.manifest_enable(True)
+    try:
+        g = torch.Generator(device=dev).manual_seed(5)
+        a = torch.randint(-127, 128, (512, 512), dtype=torch.int8, device=dev, generator=g)
+        b = torch.randint(-127, 128, (512, 512), dtype=torch.int8, device=dev, generator=g)
+        for _ in range(3):
+            hx.gemm_i8(a, b, b_layout="nk")                      # aligned -> tiled
+        hx.gemm_i8(a, b, b_layout="kn")                          # KN -> transposed into workspace
+        hx.gemm_i8(a[:, :112], b[:, :112], b_layout="nk")        # K=112 bytes -> shallow-k, generic
+        hx.gemm_i8(a[:, :496], b[:36, :496].contiguous(), b_layout="nk")  # strided A, N=36: tiled
+        hx.gemm_i8(a[:, :504], b[:36, :504].contiguous(), b_layout="nk")  # ldb=504 -> row-stride
+        hx.gemm_i8(a, b[:38].contiguous(), b_layout="nk")         # N=38 -> n-granularity
+        x = torch.randn((4, 512), dtype=torch.float16, device=dev, generator=g)
+        w = torch.randint(-127, 128, (512, 512), dtype=torch.int8, device=dev, generator=g)
+        s = torch.rand(512, device=dev).half()
+        hx.gemv_w8a16(x, w, s, w_layout="nk")                    # raw decode GEMV
+        rw = hx.ResidentWeight(w, s, layout="nk")
+        try:
+            hx.matmul_resident(x, rw)                            # packed decode GEMV
+            hx.matmul_resident(torch.randn((64, 512), dtype=torch.float16, device=dev), rw)
+        finally:
+            rw.release()
+        torch.cuda.synchronize()
+        recs = records(hx)
+    finally:
+        hx.manifest_enable(prev)
+        hx.manifest_clear()
+
+    def find(**kw):
+        got = [r for r in recs if all(r[k] == v for k, v in kw.items())]
+        assert got, f"no record with {kw} in {recs}"
+        return got[0]
+
+    r = find(entry="hx_gemm_i8", m=512, n=512, k=512, weight="argument", plan="mfma-tiled")
+    assert r["calls"] == 3 and r["reason"] == "selected-aligned" and r["config_source"] == "default"
+    assert r["a"] == "i8" and r["c"] == "i32"
+    assert find(entry="hx_gemm_i8", weight="transposed-to-workspace")["plan"] == "mfma-tiled"
+    assert find(entry="hx_gemm_i8", k=112)["reason"] == "shallow-k"
+    assert find(entry="hx_gemm_i8", k=112)["plan"] == "mfma-generic"
+    assert find(entry="hx_gemm_i8", n=38)["reason"] == "n-granularity"
+    assert find(entry="hx_gemm_i8", n=36, k=496)["plan"] == "mfma-tiled"
+    assert find(entry="hx_gemm_i8", n=36, k=504)["reason"] == "row-stride"  # ldb = 504
+    assert find(entry="hx_matmul", m=4, plan="gemv")["reason"] == "min-rows"
+    assert find(entry="hx_matmul_resident", m=4)["plan"] == "gemv-packed"
+    r = find(entry="hx_matmul_resident", m=64)
+    assert r["plan"] == "mfma-tiled" and r["weight"] == "resident-image" and r["b"] == "i8"
+
+
+def test_manifest_reports_pinned_config(hx, dev):
+    M = N = K = 1024
+    a = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev)
+    b = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev)
+    hx.manifest_clear()
+    prev = hx.manifest_enable(True)
+    try:
+        hx.config_select(1, M, N, K, 3)
+        try:
+            hx.gemm_i8(a, b, b_layout="nk")
+        finally:
+            hx.config_select(1, M, N, K, -1)
+        hx.gemm_i8(a, b, b_layout="nk")
+        torch.cuda.synchronize()
+        recs = records(hx)
+    finally:
+        hx.manifest_enable(prev)
+        hx.manifest_clear()
+    pinned = [r for r in recs if r["config_source"] == "pinned"]
+    default = [r for r in recs if r["config_source"] == "default"]
+    assert len(pinned) == 1 and pinned[0]["config"] == hx.config_get(1, 3)["name"]
+    assert len(default) == 1
+    assert default[0]["config"] == hx.config_get(1, hx.config_lookup(1, M, N, K))["name"]
