@@ -360,6 +360,31 @@ def bench_ffn(hx, iters: int = 20, tune: bool = True):
             "roofline": roofline("mfma", tf, PEAK_F16_TFLOPS, "TFLOP/s"), "tune": tuned}
 
 
+def bench_attention(hx, iters: int = 20):
+    """Fused attention forward: the reference test's configuration
+    (test/python/triton/test_flash_attention.py: Z=H=1, N=1024, D=64, scale
+    0.5) and a multi-head one, plain and causal.  FLOP = 4*Z*H*Nq*Nk*D
+    (halved under the causal mask)."""
+    import torch
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(13)
+    out = []
+    for (Z, H, N, D, causal, scale) in ((1, 1, 1024, 64, False, 0.5), (4, 16, 2048, 128, False, None),
+                                        (4, 16, 2048, 128, True, None)):
+        q, k, v = (torch.rand((Z, H, N, D), dtype=torch.float16, device=dev, generator=g)
+                   for _ in range(3))
+        o = torch.empty_like(q)
+        call = lambda: hx.attention(q, k, v, scale=scale, causal=causal, out=o)  # noqa: E731
+        call()
+        ev_ms, fed = event_timed([call], iters)
+        fl = 4.0 * Z * H * N * N * D * (0.5 if causal else 1.0)
+        tf = fl / (ev_ms * 1e-3) / 1e12
+        out.append({"workload": f"attention Z={Z} H={H} N={N} D={D}{' causal' if causal else ''} fp16",
+                    "value": round(tf, 1), "unit": "TFLOP/s", "us_per_call": round(ev_ms * 1e3, 2),
+                    "roofline": roofline("mfma", tf, PEAK_F16_TFLOPS, "TFLOP/s"), "queue_fed": fed})
+    return out
+
+
 # --------------------------------------------------------------------------- #
 
 def pmc_workload(hx) -> None:
@@ -513,6 +538,8 @@ def main() -> int:
         secondary.append(bench_gemm_f16_small(hx))
         log("[bench] SwiGLU FFN")
         secondary.append(bench_ffn(hx, tune=tune))
+        log("[bench] attention")
+        secondary += bench_attention(hx)
         for s in secondary:
             log(f"[bench]   {s['workload']}: {s['value']} {s['unit']}")
     cpu = None

@@ -30,6 +30,12 @@ class MemRef2D(ctypes.Structure):
                 ("strides", ctypes.c_int64 * 2)]
 
 
+class MemRef4D(ctypes.Structure):
+    _fields_ = [("allocated", ctypes.c_void_p), ("aligned", ctypes.c_void_p),
+                ("offset", ctypes.c_int64), ("sizes", ctypes.c_int64 * 4),
+                ("strides", ctypes.c_int64 * 4)]
+
+
 class MemRef1D(ctypes.Structure):
     _fields_ = [("allocated", ctypes.c_void_p), ("aligned", ctypes.c_void_p),
                 ("offset", ctypes.c_int64), ("sizes", ctypes.c_int64 * 1),
@@ -75,6 +81,7 @@ SIGNATURES = {
     "hx_config_get": ([_i, _i, ctypes.POINTER(KernelConfig)], _i),
     "hx_config_select": ([_i, _i64, _i64, _i64, _i], _i),
     "hx_config_lookup": ([_i, _i64, _i64, _i64, ctypes.POINTER(_i)], _i),
+    "hx_attention": ([ctypes.POINTER(MemRef4D)] * 4 + [_f, _i, _i, _vp], _i),
     "hx_manifest_enable": ([_i], _i),
     "hx_manifest_clear": ([], _i),
     "hx_manifest_json": ([ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)], _i),

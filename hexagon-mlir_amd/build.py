@@ -21,7 +21,7 @@ OBJDIR = PKG / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["hx_rows.hip", "hx_gemm.hip", "hx_gemv.hip", "hx_pack.hip", "hx_api.cpp"]
+SOURCES = ["hx_rows.hip", "hx_gemm.hip", "hx_gemv.hip", "hx_pack.hip", "hx_attn.hip", "hx_api.cpp"]
 
 # Packed-FP32 VALU forms are disabled for all device code (they are not
 # needed: the hot loops are MFMA or memory bound).  Floating-point

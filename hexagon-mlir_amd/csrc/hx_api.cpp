@@ -578,6 +578,53 @@ extern "C" int hx_silu_mul(const hx_memref2d* g, const hx_memref2d* u, hx_memref
 }
 
 // ---------------------------------------------------------------------------
+// Attention
+// ---------------------------------------------------------------------------
+static int view4(const hx_memref4d* m, const char* name, const int64_t* expect, int64_t* strides,
+                 const char** base) {
+  if (!m) return fail(HX_ERR_ARG, "%s: null descriptor", name);
+  for (int i = 0; i < 4; ++i) {
+    if (m->sizes[i] < 0) return fail(HX_ERR_ARG, "%s: negative size", name);
+    if (expect[i] >= 0 && m->sizes[i] != expect[i])
+      return fail(HX_ERR_SHAPE, "%s: dim %d is %lld, expected %lld", name, i, (long long)m->sizes[i],
+                  (long long)expect[i]);
+  }
+  if (m->sizes[3] > 1 && m->strides[3] != 1)
+    return fail(HX_ERR_LAYOUT, "%s: innermost stride %lld != 1", name, (long long)m->strides[3]);
+  if (m->offset < 0) return fail(HX_ERR_ARG, "%s: negative offset", name);
+  const int64_t n = m->sizes[0] * m->sizes[1] * m->sizes[2] * m->sizes[3];
+  if (n > 0 && !m->aligned) return fail(HX_ERR_ARG, "%s: null data", name);
+  for (int i = 0; i < 3; ++i) strides[i] = m->strides[i];
+  *base = (const char*)m->aligned + m->offset * 2;
+  return HX_OK;
+}
+
+extern "C" int hx_attention(const hx_memref4d* q, const hx_memref4d* k, const hx_memref4d* v,
+                            hx_memref4d* o, float scale, int causal, int dtype, hx_stream_t stream) {
+  if (dtype != HX_F16 && dtype != HX_BF16)
+    return fail(HX_ERR_DTYPE, "hx_attention: dtype %s (f16 or bf16)", dt_name(dtype));
+  if (!q || !k) return fail(HX_ERR_ARG, "hx_attention: null descriptor");
+  const int64_t Z = q->sizes[0], H = q->sizes[1], Nq = q->sizes[2], D = q->sizes[3];
+  const int64_t Nk = k->sizes[2];
+  AttnArgs a{};
+  const char *bq, *bk, *bv, *bo;
+  int rc;
+  const int64_t eq[4] = {Z, H, Nq, D}, ek[4] = {Z, H, Nk, D};
+  if ((rc = view4(q, "q", eq, a.sq, &bq)) || (rc = view4(k, "k", ek, a.sk, &bk)) ||
+      (rc = view4(v, "v", ek, a.sv, &bv)) || (rc = view4(o, "o", eq, a.so, &bo)))
+    return rc;
+  a.q = bq; a.k = bk; a.v = bv; a.o = (void*)bo;
+  a.Z = Z; a.H = H; a.Nq = Nq; a.Nk = Nk; a.D = D;
+  a.scale = scale;
+  a.causal_offset = 0;
+  if (Z == 0 || H == 0 || Nq == 0) return HX_OK;
+  if (const char* why = attn_refusal(a))
+    return fail(HX_ERR_UNSUPPORTED, "hx_attention: %s (D=%lld; D must be 64 or 128, bases 16-byte "
+                "aligned, strides multiples of 8)", why, (long long)D);
+  return map_internal(launch_attention(dtype, causal != 0, a, (hipStream_t)stream), "attention");
+}
+
+// ---------------------------------------------------------------------------
 // Resident weights
 // ---------------------------------------------------------------------------
 struct hx_weight {

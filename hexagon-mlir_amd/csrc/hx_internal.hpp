@@ -96,6 +96,18 @@ int gemv_packed_config_count();
 const GemvConfig* gemv_packed_config(int idx);
 int launch_gemv_packed(int cfg_idx, const GemvArgs& a, const int8_t* packed, hipStream_t s);
 
+// ---- scaled-dot-product attention (hx_attn.hip) --------------------------
+struct AttnArgs {
+  const void* q; const void* k; const void* v; void* o;  // [Z][H][N][D], D contiguous
+  int64_t sq[3], sk[3], sv[3], so[3];                     // element strides of Z, H, N
+  int64_t Z, H, Nq, Nk, D;
+  float scale;
+  int64_t causal_offset;  // causal: key <= query + offset is visible
+};
+// Null when the fused kernel takes these args, else the first refusal.
+const char* attn_refusal(const AttnArgs& a);
+int launch_attention(int dtype, bool causal, const AttnArgs& a, hipStream_t s);
+
 // ---- layout utilities (hx_pack.hip) --------------------------------------
 // dst[c][r] = src[r][c] for a rows x cols matrix of 1/2/4-byte elements.
 int launch_transpose(const void* src, int64_t lds, void* dst, int64_t ldd, int64_t rows,

@@ -28,7 +28,7 @@ from typing import Optional
 import torch
 
 from . import _abi
-from ._abi import (BF16, F16, F32, I8, I32, LAYOUT_KN, LAYOUT_NK, MemRef1D, MemRef2D,
+from ._abi import (BF16, F16, F32, I8, I32, LAYOUT_KN, LAYOUT_NK, MemRef1D, MemRef2D, MemRef4D,
                    check, load)
 
 _DT = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32, torch.int8: I8,
@@ -72,6 +72,19 @@ def memref1d(t: torch.Tensor, name: str = "tensor") -> MemRef1D:
     m.offset = 0
     m.sizes[0] = t.shape[0]
     m.strides[0] = t.stride()[0]
+    return m
+
+
+def memref4d(t: torch.Tensor, name: str = "tensor") -> MemRef4D:
+    _dev(t, name)
+    if t.dim() != 4:
+        raise ValueError(f"{name}: expected 4-D [Z, H, N, D], got {tuple(t.shape)}")
+    m = MemRef4D()
+    m.allocated = m.aligned = t.data_ptr()
+    m.offset = 0
+    for i in range(4):
+        m.sizes[i] = t.shape[i]
+        m.strides[i] = t.stride()[i]
     return m
 
 
@@ -289,6 +302,23 @@ def config_lookup(op: int, m: int, n: int, k: int) -> int:
 
 def build_id() -> str:
     return load().hx_build_id().decode()
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Optional[float] = None,
+              causal: bool = False, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Fused O = softmax(Q K^T * scale) V for [Z, H, N, D] fp16/bf16 tensors
+    (D = 64 or 128); the arithmetic of the reference's FlashAttention test
+    (test/python/triton/test_flash_attention.py).  scale defaults to
+    1/sqrt(D) like torch.nn.functional.scaled_dot_product_attention."""
+    if scale is None:
+        scale = q.shape[-1] ** -0.5
+    if out is None:
+        out = torch.empty_like(q)
+    mq, mk, mv, mo = memref4d(q, "q"), memref4d(k, "k"), memref4d(v, "v"), memref4d(out, "out")
+    check(load().hx_attention(ctypes.byref(mq), ctypes.byref(mk), ctypes.byref(mv), ctypes.byref(mo),
+                              float(scale), 1 if causal else 0, dtype_code(q), _stream()),
+          "hx_attention")
+    return out
 
 
 def manifest_enable(on: bool = True) -> bool:

@@ -83,6 +83,15 @@ typedef struct hx_memref1d {
     int64_t strides[1];
 } hx_memref1d;
 
+/* Rank-4 descriptor ([Z][H][N][D] attention operands), same field meaning. */
+typedef struct hx_memref4d {
+    void* allocated;
+    void* aligned;
+    int64_t offset;
+    int64_t sizes[4];
+    int64_t strides[4];
+} hx_memref4d;
+
 /* ---------------------------------------------------------------------- */
 /* Library state                                                           */
 /* ---------------------------------------------------------------------- */
@@ -256,6 +265,22 @@ int hx_config_select(int op, int64_t m, int64_t n, int64_t k, int index);
  * the untuned default.  *index = -1 means the generic (any-alignment)
  * kernel. */
 int hx_config_lookup(int op, int64_t m, int64_t n, int64_t k, int* index);
+
+/* ---------------------------------------------------------------------- */
+/* Scaled-dot-product attention                                            */
+/* ---------------------------------------------------------------------- */
+
+/* O = softmax(Q K^T * scale [, causal]) V per (z, h): q, o [Z][H][Nq][D],
+ * k, v [Z][H][Nk][D] (innermost stride 1), dtype HX_F16 or HX_BF16, D 64 or
+ * 128.  Scores and accumulation in binary32, online softmax in the exp2
+ * domain (one pass over K/V, no Nq x Nk intermediate); causal masks key j
+ * for query i when j > i.  Replaces the FlashAttention forward the Triton
+ * front end compiles (test/python/triton/test_flash_attention.py:
+ * _attn_fwd_inner, attention_fwd_kernel) and its online-softmax recurrence
+ * (test/python/triton/test_online_softmax.py:28-78); same arithmetic
+ * (qk_scale = scale * log2 e, p = exp2(qk * qk_scale - m), O = acc / l). */
+int hx_attention(const hx_memref4d* q, const hx_memref4d* k, const hx_memref4d* v, hx_memref4d* o,
+                 float scale, int causal, int dtype, hx_stream_t stream);
 
 /* ---------------------------------------------------------------------- */
 /* Plan manifest                                                           */

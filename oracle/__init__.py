@@ -26,6 +26,10 @@ rmsnorm                numpy float64; scale invariance; torch-CPU rms_norm at
 layernorm              numpy float64 incl. mean/rstd; torch-CPU layer_norm at
                        the reference test's shape/atol
 silu_mul               numpy float64
+attention              numpy float64 softmax(QK^T s)V; V = 1 gives 1;
+                       one key returns its value row; causal row 0 is v[0];
+                       torch-CPU scaled_dot_product_attention at the reference
+                       test's shape and relative-error bound
 =====================  ======================================================
 """
 from __future__ import annotations
@@ -79,6 +83,7 @@ def lib():
         L.hxo_rmsnorm.argtypes = [vp, vp, f32, vp, i32, i64, i64, i64, i64]
         L.hxo_layernorm.argtypes = [vp, vp, vp, f32, vp, vp, vp, i32, i64, i64, i64, i64]
         L.hxo_silu_mul.argtypes = [vp, vp, vp, i32, i64, i64, i64, i64, i64]
+        L.hxo_attention.argtypes = [vp, vp, vp, vp, i32, i64, i64, i64, i64, f32, i32]
         _lib = L
     return _lib
 
@@ -212,6 +217,23 @@ def silu_mul(g: np.ndarray, u: np.ndarray, bf16: bool = False) -> np.ndarray:
     R, C = g.shape
     out = np.empty_like(g)
     lib().hxo_silu_mul(_p(g), _p(u), _p(out), _code(g, bf16), R, C, C, C, C)
+    return out
+
+
+def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, causal: bool = False,
+              bf16: bool = False) -> np.ndarray:
+    """O = softmax(Q K^T * scale) V over [..., N, D] arrays (fp16, or bf16
+    bits as uint16 with ``bf16``); binary32 throughout, one rounding of O."""
+    q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
+    lead = q.shape[:-2]
+    Nq, D = q.shape[-2:]
+    Nk = k.shape[-2]
+    if Nk > 16384:
+        raise ValueError("oracle attention: Nk <= 16384")
+    B = int(np.prod(lead)) if lead else 1
+    out = np.empty_like(q)
+    lib().hxo_attention(_p(q), _p(k), _p(v), _p(out), _code(q, bf16), B, Nq, Nk, D,
+                        ctypes.c_float(scale), 1 if causal else 0)
     return out
 
 

@@ -341,3 +341,50 @@ void hxo_silu_mul(const void* g, const void* u, void* out, int dtype,
         }
     }
 }
+
+/* ------------------------------------------------------------------------ */
+/* Scaled-dot-product attention                                              */
+/* ------------------------------------------------------------------------ */
+
+/* O = softmax(Q K^T * scale) V for one (z, h) slice per b < B:
+ * q, o [B][Nq][D], k, v [B][Nk][D] (dtype f16 or bf16, contiguous).
+ * Follows the FlashAttention test's arithmetic
+ * (test/python/triton/test_flash_attention.py, attention_fwd_kernel /
+ * _attn_fwd_inner): qk = sum_d q*k in binary32 (d ascending),
+ * t = qk * (scale * log2 e), m = max_j t, p = exp2(t - m), l = sum_j p,
+ * O = (sum_j p * v) / l.  The reference folds the blocks online; a single
+ * block holding the whole row is the same recurrence with alpha = 1.
+ * causal: key j is visible to query i iff j <= i. */
+void hxo_attention(const void* q, const void* k, const void* v, void* o, int dtype,
+                   int64_t B, int64_t Nq, int64_t Nk, int64_t D, float scale, int causal)
+{
+    const float qk_scale = scale * 1.44269504088896340736f;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int64_t b = 0; b < B; ++b) {
+        for (int64_t i = 0; i < Nq; ++i) {
+            float t[16384];  /* Nk <= 16384 (checked by the wrapper) */
+            const int64_t qo = (b * Nq + i) * D;
+            float m = -INFINITY;
+            for (int64_t j = 0; j < Nk; ++j) {
+                if (causal && j > i) { t[j] = -INFINITY; continue; }
+                const int64_t ko = (b * Nk + j) * D;
+                float acc = 0.0f;
+                for (int64_t d = 0; d < D; ++d)
+                    acc += load_elem(q, dtype, qo + d) * load_elem(k, dtype, ko + d);
+                t[j] = acc * qk_scale;
+                if (t[j] > m) m = t[j];
+            }
+            float l = 0.0f;
+            for (int64_t j = 0; j < Nk; ++j) {
+                t[j] = (t[j] == -INFINITY) ? 0.0f : exp2f(t[j] - m);
+                l += t[j];
+            }
+            for (int64_t d = 0; d < D; ++d) {
+                float acc = 0.0f;
+                for (int64_t j = 0; j < Nk; ++j)
+                    acc += t[j] * load_elem(v, dtype, (b * Nk + j) * D + d);
+                store_elem(o, dtype, qo + d, l > 0.0f ? acc / l : 0.0f);
+            }
+        }
+    }
+}

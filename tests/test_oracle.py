@@ -266,3 +266,60 @@ def test_golden_fixtures_reproduce():
     assert np.array_equal(oracle.rmsnorm(data["rms_x"], data["rms_g"], meta["rms_eps"]).view(np.uint16),
                           data["rms_y"])
     assert meta["seed"] == 20261201
+
+
+# --------------------------------------------------------------------------- #
+# Attention
+# --------------------------------------------------------------------------- #
+
+def _sdpa64(q, k, v, scale, causal=False):
+    s = np.einsum("bid,bjd->bij", q.astype(np.float64), k.astype(np.float64)) * scale
+    if causal:
+        nq, nk = s.shape[-2:]
+        s = np.where(np.arange(nk)[None, :] > np.arange(nq)[:, None], -np.inf, s)
+    s = s - s.max(-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(-1, keepdims=True)
+    return np.einsum("bij,bjd->bid", p, v.astype(np.float64))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_oracle_attention_fp64(causal):
+    r = rng(41)
+    q = r.uniform(-1, 1, (3, 37, 64)).astype(np.float16)
+    k = r.uniform(-1, 1, (3, 53, 64)).astype(np.float16)
+    v = r.normal(0, 1, (3, 53, 64)).astype(np.float16)
+    got = oracle.attention(q, k, v, 0.3, causal=causal).astype(np.float64)
+    want = _sdpa64(q, k, v, 0.3, causal)
+    assert np.abs(got - want).max() < 2e-3
+
+
+def test_oracle_attention_invariants():
+    r = rng(42)
+    q = r.uniform(0, 1, (2, 40, 64)).astype(np.float16)
+    k = r.uniform(0, 1, (2, 70, 64)).astype(np.float16)
+    ones = np.ones((2, 70, 64), np.float16)
+    assert np.array_equal(oracle.attention(q, k, ones, 0.5), np.ones((2, 40, 64), np.float16))
+    v1 = r.normal(0, 1, (2, 1, 64)).astype(np.float16)
+    got = oracle.attention(q, k[:, :1], v1, 0.5)
+    assert np.array_equal(got, np.broadcast_to(v1, got.shape))
+    v = r.normal(0, 1, (2, 70, 64)).astype(np.float16)
+    causal = oracle.attention(q, k, v, 0.5, causal=True)
+    assert np.array_equal(causal[:, 0], v[:, 0])          # row 0 sees only key 0
+    # scale 0: every key weighs the same, whatever the keys are
+    uniform = oracle.attention(q, k, v, 0.0)
+    assert np.array_equal(uniform, oracle.attention(q, k * 0, v, 0.0))
+    assert np.abs(uniform[:, 0].astype(np.float64) - v.astype(np.float64).mean(1)).max() < 1e-3
+
+
+def test_oracle_attention_matches_torch_at_reference_shape():
+    """test/python/triton/test_flash_attention.py: Z = H = 1, N_CTX = 1024,
+    D = 64, scale 0.5, torch.rand inputs, rel Frobenius error < 5e-3 against
+    scaled_dot_product_attention."""
+    import torch
+    torch.manual_seed(0)
+    q, k, v = (torch.rand(1, 1, 1024, 64) for _ in range(3))
+    ref = torch.nn.functional.scaled_dot_product_attention(q, k, v, scale=0.5)
+    got = oracle.attention(q.half().numpy(), k.half().numpy(), v.half().numpy(), 0.5)
+    rel = float(np.linalg.norm(got.astype(np.float64) - ref.numpy()) / np.linalg.norm(ref.numpy()))
+    assert rel < 5e-3, rel
