@@ -132,7 +132,13 @@ __global__ void __launch_bounds__(256) gemv_w8a16_kernel(GemvArgs p) {
 // issues its whole K slice (CT tiles x chunks) before the first MFMA: the
 // kernel is a single round trip to HBM.
 // ---------------------------------------------------------------------------
-template <int CT, int KW, int CPW>
+//
+// XL (M <= 4): the activations are staged once per workgroup in LDS ([M]
+// rows of kchunks*64, zero-padded) after the weight loads are issued, and
+// each MFMA step reads its operand from there; the registers that would
+// hold every step's activation fragment (2 x 16 bytes per chunk) are freed,
+// so more waves -- more weight bytes in flight -- fit on a CU.
+template <int CT, int KW, int CPW, bool XL>
 __global__ void __launch_bounds__(64 * KW) gemv_packed_kernel(GemvArgs p, const int8_t* packed,
                                                               int kchunks) {
   const int tid = threadIdx.x, lane = tid & 63;
@@ -142,6 +148,9 @@ __global__ void __launch_bounds__(64 * KW) gemv_packed_kernel(GemvArgs p, const 
   const int ntiles = (int)((p.N + 15) / 16);
   const bool xrow = col < p.M;
   const uint16_t* x = reinterpret_cast<const uint16_t*>(p.x);
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
+  const int64_t kp = (int64_t)kchunks * 64;
+  const int64_t kps = kp + 8;  // row pitch: 16 bytes of padding spread the rows over the banks
 
   v4f acc[CT];
 #pragma unroll
@@ -150,7 +159,7 @@ __global__ void __launch_bounds__(64 * KW) gemv_packed_kernel(GemvArgs p, const 
   // chunks [c0, c0 + CPW * KW) are split as wave w -> c0 + w + KW * u
   for (int c0 = 0; c0 < kchunks; c0 += CPW * KW) {
     v4u wq[CPW][CT];
-    v4u xq[CPW][2];
+    v4u xq[XL ? 1 : CPW][2];
 #pragma unroll
     for (int u = 0; u < CPW; ++u) {
       const int j = c0 + wave + KW * u;
@@ -163,19 +172,39 @@ __global__ void __launch_bounds__(64 * KW) gemv_packed_kernel(GemvArgs p, const 
                              packed + ((int64_t)t * kchunks + j) * 1024 + 16 * lane))
                        : v4u{0u, 0u, 0u, 0u};
       }
+      if constexpr (!XL) {
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int64_t k = (int64_t)j * 64 + 16 * g + 8 * e;
-        xq[u][e] = (jv && xrow && k < p.K)
-                       ? *reinterpret_cast<const v4u*>(x + (int64_t)col * p.ldx + k)
-                       : v4u{0u, 0u, 0u, 0u};
+        for (int e = 0; e < 2; ++e) {
+          const int64_t k = (int64_t)j * 64 + 16 * g + 8 * e;
+          xq[u][e] = (jv && xrow && k < p.K)
+                         ? *reinterpret_cast<const v4u*>(x + (int64_t)col * p.ldx + k)
+                         : v4u{0u, 0u, 0u, 0u};
+        }
+      }
+    }
+    if constexpr (XL) {
+      // stage X (rows < M, zero past K) while the weight loads are in flight
+      if (c0 == 0) {
+        const int64_t nch = (int64_t)p.M * kchunks * 8;  // 16-byte chunks
+        for (int64_t q = tid; q < nch; q += 64 * KW) {
+          const int64_t m = q / (kchunks * 8), k = (q - m * kchunks * 8) * 8;
+          *reinterpret_cast<v4u*>(xs + m * kps + k) =
+              k < p.K ? *reinterpret_cast<const v4u*>(x + m * p.ldx + k) : v4u{0u, 0u, 0u, 0u};
+        }
+        __syncthreads();
       }
     }
 #pragma unroll
     for (int u = 0; u < CPW; ++u)
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
-        const v8h xa = __builtin_bit_cast(v8h, xq[u][e]);
+        v8h xa;
+        if constexpr (XL) {
+          const int64_t k = (int64_t)(c0 + wave + KW * u) * 64 + 16 * g + 8 * e;
+          xa = (xrow && k < kp) ? *reinterpret_cast<const v8h*>(xs + col * kps + k) : v8h{};
+        } else {
+          xa = __builtin_bit_cast(v8h, xq[u][e]);
+        }
 #pragma unroll
         for (int c = 0; c < CT; ++c) {
           const v8h wb = i8x8_to_v8h(wq[u][c][2 * e], wq[u][c][2 * e + 1]);
@@ -238,22 +267,29 @@ int launch_gemv_pack(const int8_t* w, int64_t ldw, int64_t N, int64_t K, int8_t*
 }
 
 typedef void (*GemvPackedLaunch)(const GemvArgs&, const int8_t*, int, hipStream_t);
-template <int CT, int KW, int CPW>
+template <int CT, int KW, int CPW, bool XL>
 static void gemv_packed_one(const GemvArgs& a, const int8_t* packed, int kchunks, hipStream_t s) {
   const int64_t ntiles = (a.N + 15) / 16;
   const int64_t blocks = (ntiles + CT - 1) / CT;
-  gemv_packed_kernel<CT, KW, CPW><<<dim3((unsigned)blocks), dim3(64 * KW), 0, s>>>(a, packed, kchunks);
+  const size_t lds = XL ? (size_t)a.M * (kchunks * 64 + 8) * 2 : 0;
+  gemv_packed_kernel<CT, KW, CPW, XL><<<dim3((unsigned)blocks), dim3(64 * KW), lds, s>>>(a, packed, kchunks);
 }
 struct GemvPackedEntry {
   GemvConfig cfg;
   GemvPackedLaunch fn;
 };
+// xl configs (activations staged in LDS) take M <= 4 with the staged rows
+// within 64 KiB of LDS; outside that they run as their register-staged base
+// config (the `base` index).
 static const GemvPackedEntry kGemvPacked[] = {
-    {{2, 8, "packed_ct2_kw8"}, &gemv_packed_one<2, 8, 8>},
-    {{1, 8, "packed_ct1_kw8"}, &gemv_packed_one<1, 8, 8>},
-    {{4, 8, "packed_ct4_kw8"}, &gemv_packed_one<4, 8, 4>},
-    {{2, 4, "packed_ct2_kw4"}, &gemv_packed_one<2, 4, 8>},
-    {{1, 4, "packed_ct1_kw4"}, &gemv_packed_one<1, 4, 16>},
+    {{2, 8, "packed_ct2_kw8", 0, 0}, &gemv_packed_one<2, 8, 8, false>},
+    {{1, 8, "packed_ct1_kw8", 0, 1}, &gemv_packed_one<1, 8, 8, false>},
+    {{4, 8, "packed_ct4_kw8", 0, 2}, &gemv_packed_one<4, 8, 4, false>},
+    {{2, 4, "packed_ct2_kw4", 0, 3}, &gemv_packed_one<2, 4, 8, false>},
+    {{1, 4, "packed_ct1_kw4", 0, 4}, &gemv_packed_one<1, 4, 16, false>},
+    {{1, 8, "packed_ct1_kw8_xl", 1, 1}, &gemv_packed_one<1, 8, 8, true>},
+    {{2, 8, "packed_ct2_kw8_xl", 1, 0}, &gemv_packed_one<2, 8, 8, true>},
+    {{1, 16, "packed_ct1_kw16_xl", 1, 1}, &gemv_packed_one<1, 16, 4, true>},
 };
 int gemv_packed_config_count() { return (int)(sizeof(kGemvPacked) / sizeof(kGemvPacked[0])); }
 const GemvConfig* gemv_packed_config(int idx) {
@@ -263,6 +299,9 @@ const GemvConfig* gemv_packed_config(int idx) {
 int launch_gemv_packed(int cfg_idx, const GemvArgs& a, const int8_t* packed, hipStream_t s) {
   if (cfg_idx < 0 || cfg_idx >= gemv_packed_config_count()) return HXI_ERR_ARG;
   if (a.M < 1 || a.M > 16) return HXI_ERR_SHAPE;
+  const int64_t kchunks = (a.K + 63) / 64;
+  if (kGemvPacked[cfg_idx].cfg.xl && (a.M > 4 || a.M * (kchunks * 64 + 8) * 2 > 65536))
+    cfg_idx = kGemvPacked[cfg_idx].cfg.base;
   kGemvPacked[cfg_idx].fn(a, packed, (int)((a.K + 63) / 64), s);
   return HXI_OK;
 }

@@ -82,7 +82,12 @@ struct GemvArgs {
   void* y; int64_t ldy;         // f16 [M][N]
   int64_t M, N, K;
 };
-struct GemvConfig { int ct, kw; const char* name; };
+struct GemvConfig {
+  int ct, kw;        // 16-column tiles per workgroup, waves splitting K
+  const char* name;
+  int xl;            // activations staged in LDS (M <= 4, rows within 64 KiB)
+  int base;          // config that runs outside the xl limits
+};
 bool gemv_fast_ok(const GemvArgs& a);
 const char* gemv_fast_refusal(const GemvArgs& a);
 // Column tiles per workgroup (1, 2 or 4 as index 0..2) of the [N][K] kernel.

@@ -91,17 +91,27 @@ def test_gemv_resident_matches_raw(hx, dev, c3):
         rw.release()
 
 
-@pytest.mark.parametrize("shape", [(5, 1000, 4160), (16, 37, 200), (1, 11008, 64), (3, 20, 8)],
+@pytest.mark.parametrize("shape", [(5, 1000, 4160), (16, 37, 200), (1, 11008, 64), (3, 20, 8),
+                                   (4, 300, 8192), (2, 100, 16384)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_gemv_resident_ragged(hx, dev, shape):
     """Packed decode path with N not a multiple of 16 and K not a multiple of
-    64 (the image is zero-padded; K % 8 == 0 is required for this path)."""
+    64 (the image is zero-padded; K % 8 == 0 is required for this path), and
+    every config including the LDS-staged ones past their LDS limit (M = 4,
+    K = 8192 and M = 2, K = 16384 run as their base configs)."""
     M, N, K = shape
     x, w, s = case(M, N, K, seed=300)
     rw = hx.ResidentWeight(to_dev(w, dev), to_dev(s, dev))
+    want = oracle.matmul(x, w, scale_n=s.astype(np.float32))
+    xd = to_dev(x, dev)
     try:
-        y = to_np(hx.matmul_resident(to_dev(x, dev), rw))
+        for cfg in range(hx.config_count(6)):
+            hx.config_select(6, M, N, K, cfg)
+            try:
+                y = to_np(hx.matmul_resident(xd, rw))
+            finally:
+                hx.config_select(6, M, N, K, -1)
+            assert_close(y.astype(np.float32), want.astype(np.float32), 1e-2, 1e-3,
+                         f"packed ragged {shape} cfg {cfg}")
     finally:
         rw.release()
-    want = oracle.matmul(x, w, scale_n=s.astype(np.float32))
-    assert_close(y.astype(np.float32), want.astype(np.float32), 1e-2, 1e-3, f"packed ragged {shape}")
