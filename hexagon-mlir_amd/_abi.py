@@ -81,6 +81,8 @@ SIGNATURES = {
     "hx_config_get": ([_i, _i, ctypes.POINTER(KernelConfig)], _i),
     "hx_config_select": ([_i, _i64, _i64, _i64, _i], _i),
     "hx_config_lookup": ([_i, _i64, _i64, _i64, ctypes.POINTER(_i)], _i),
+    "hx_config_pins_save": ([ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)], _i),
+    "hx_config_pins_load": ([ctypes.c_char_p], _i),
     "hx_attention": ([ctypes.POINTER(MemRef4D)] * 4 + [_f, _i, _i, _vp], _i),
     "hx_manifest_enable": ([_i], _i),
     "hx_manifest_clear": ([], _i),

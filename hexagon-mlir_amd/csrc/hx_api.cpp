@@ -940,6 +940,72 @@ extern "C" int hx_config_select(int op, int64_t m, int64_t n, int64_t k, int ind
   return HX_OK;
 }
 
+static const char* config_name(int op, int index) {
+  std::vector<int> idx = family_indices(op);
+  if (index < 0 || index >= (int)idx.size()) return nullptr;
+  if (op == HX_OP_GEMV_W8) return gemv_packed_config(idx[index])->name;
+  int mode, epi;
+  op_gemm(op, &mode, &epi);
+  return gemm_config(mode, idx[index])->name;
+}
+
+extern "C" int hx_config_pins_save(char* buf, size_t cap, size_t* needed) {
+  int dev;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  std::string out = "hx-pins/v1 " HX_BUILD_ID "\n";
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    for (const auto& kv : g_pins) {
+      if (std::get<0>(kv.first) != dev) continue;
+      const int op = std::get<1>(kv.first);
+      char line[160];
+      snprintf(line, sizeof(line), "%d %lld %lld %lld %d %s\n", op, (long long)std::get<2>(kv.first),
+               (long long)std::get<3>(kv.first), (long long)std::get<4>(kv.first), kv.second,
+               config_name(op, kv.second));
+      out += line;
+    }
+  }
+  if (needed) *needed = out.size() + 1;
+  if (!buf || cap < out.size() + 1)
+    return fail(HX_ERR_ARG, "hx_config_pins_save: buffer of %zu bytes, %zu needed", cap, out.size() + 1);
+  memcpy(buf, out.c_str(), out.size() + 1);
+  return HX_OK;
+}
+
+extern "C" int hx_config_pins_load(const char* text) {
+  if (!text) return fail(HX_ERR_ARG, "hx_config_pins_load: null text");
+  int dev;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  const std::string header = "hx-pins/v1 " HX_BUILD_ID;
+  const char* nl = strchr(text, '\n');
+  const std::string first = nl ? std::string(text, nl - text) : std::string(text);
+  if (first != header)
+    return fail(HX_ERR_ARG, "hx_config_pins_load: pins are from '%s', this library is '%s'", first.c_str(),
+                header.c_str());
+  // parse everything before applying anything
+  std::vector<std::pair<std::tuple<int, int, int64_t, int64_t, int64_t>, int>> pins;
+  for (const char* line = nl ? nl + 1 : nullptr; line && *line;) {
+    const char* end = strchr(line, '\n');
+    const std::string l = end ? std::string(line, end - line) : std::string(line);
+    line = end ? end + 1 : nullptr;
+    if (l.empty()) continue;
+    int op, index;
+    long long m, n, k;
+    char name[64];
+    if (sscanf(l.c_str(), "%d %lld %lld %lld %d %63s", &op, &m, &n, &k, &index, name) != 6)
+      return fail(HX_ERR_ARG, "hx_config_pins_load: malformed line '%s'", l.c_str());
+    const char* have = config_name(op, index);
+    if (!have || strcmp(have, name) != 0)
+      return fail(HX_ERR_ARG, "hx_config_pins_load: op %d index %d is not config '%s'", op, index, name);
+    pins.emplace_back(std::make_tuple(dev, op, (int64_t)m, (int64_t)n, (int64_t)k), index);
+  }
+  std::lock_guard<std::mutex> lk(g_mu);
+  for (const auto& p : pins) g_pins[p.first] = p.second;
+  return HX_OK;
+}
+
 extern "C" int hx_config_lookup(int op, int64_t m, int64_t n, int64_t k, int* index) {
   if (!index) return fail(HX_ERR_ARG, "hx_config_lookup: null out");
   std::vector<int> idx = family_indices(op);

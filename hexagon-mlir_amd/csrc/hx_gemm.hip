@@ -63,10 +63,6 @@ template <> struct ModeTraits<GM_W8> {
 __device__ __forceinline__ int swz128(int row) { return (row ^ (row >> 3)) & 7; }
 __device__ __forceinline__ int swz64(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
 
-__device__ __forceinline__ v4i buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
-}
-
 template <int MODE>
 __device__ __forceinline__ typename ModeTraits<MODE>::Acc mfma32(v4i a, v4i b,
                                                                  typename ModeTraits<MODE>::Acc c) {

@@ -321,6 +321,20 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: Optional
     return out
 
 
+def config_pins_save() -> str:
+    """The current device's pinned configs as text (see hx_config_pins_save)."""
+    L = load()
+    need = ctypes.c_size_t(0)
+    L.hx_config_pins_save(None, 0, ctypes.byref(need))
+    buf = ctypes.create_string_buffer(need.value + 1024)
+    check(L.hx_config_pins_save(buf, len(buf), ctypes.byref(need)), "hx_config_pins_save")
+    return buf.value.decode()
+
+
+def config_pins_load(text: str) -> None:
+    check(load().hx_config_pins_load(text.encode()), "hx_config_pins_load")
+
+
 def manifest_enable(on: bool = True) -> bool:
     """Start (or stop) recording the plan of every matmul-family call;
     returns the previous state."""

@@ -265,6 +265,16 @@ int hx_config_select(int op, int64_t m, int64_t n, int64_t k, int index);
  * the untuned default.  *index = -1 means the generic (any-alignment)
  * kernel. */
 int hx_config_lookup(int op, int64_t m, int64_t n, int64_t k, int* index);
+/* Persist the tuner's champions: hx_config_pins_save writes the current
+ * device's pins as text ("hx-pins/v1 <build id>" then one "op m n k index
+ * name" line per pin; NUL-terminated, *needed = size; HX_ERR_ARG if cap is
+ * too small) and hx_config_pins_load pins them again in another process.
+ * Pins from another build are refused (a config index means nothing across
+ * builds), as is any line whose index does not name the same config.
+ * Replaces the tuned-config cache of QHB/backend/hmx_search.py (keyed by
+ * build fingerprints, tuning_key_int :416-452). */
+int hx_config_pins_save(char* buf, size_t cap, size_t* needed);
+int hx_config_pins_load(const char* text);
 
 /* ---------------------------------------------------------------------- */
 /* Scaled-dot-product attention                                            */

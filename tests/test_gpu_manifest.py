@@ -89,3 +89,32 @@ def test_manifest_reports_pinned_config(hx, dev):
     assert len(pinned) == 1 and pinned[0]["config"] == hx.config_get(1, 3)["name"]
     assert len(default) == 1
     assert default[0]["config"] == hx.config_get(1, hx.config_lookup(1, M, N, K))["name"]
+
+
+def test_config_pins_round_trip(hx, dev):
+    """Champions survive a save/load round trip; text from another build or
+    naming the wrong config is refused and pins nothing."""
+    shapes = [(1, 1000, 1000, 1000, 3), (2, 512, 768, 256, 1), (6, 4, 11008, 4096, 2)]
+    for op, m, n, k, i in shapes:
+        hx.config_select(op, m, n, k, i)
+    text = hx.config_pins_save()
+    assert text.startswith("hx-pins/v1 " + hx.build_id())
+    for op, m, n, k, i in shapes:
+        hx.config_select(op, m, n, k, -1)
+    try:
+        hx.config_pins_load(text)
+        for op, m, n, k, i in shapes:
+            assert hx.config_lookup(op, m, n, k) == i
+        for op, m, n, k, i in shapes:
+            hx.config_select(op, m, n, k, -1)
+        before = hx.config_pins_save()
+        other = text.replace(hx.build_id(), "hxmi-gfx950-0000000000000000-x", 1)
+        with pytest.raises(hx.HXError, match="pins are from"):
+            hx.config_pins_load(other)
+        wrong = text.splitlines()[0] + "\n1 1000 1000 1000 3 not_a_config\n"
+        with pytest.raises(hx.HXError, match="is not config"):
+            hx.config_pins_load(wrong)
+        assert hx.config_pins_save() == before, "a refused load must pin nothing"
+    finally:
+        for op, m, n, k, i in shapes:
+            hx.config_select(op, m, n, k, -1)
