@@ -11,7 +11,7 @@
 // online-softmax recurrence of test/python/triton/test_online_softmax.py.
 //
 // MI355X design: one workgroup of four waves per (batch*head, 128 query
-// rows); each wave owns 32 query rows.  K/V blocks of 64 keys are staged
+// rows); each wave owns 32 query rows.  K/V blocks of 64 or 128 keys are staged
 // through LDS, double-buffered, with the next block's global loads in flight
 // during the current block's MFMAs.  Scores are computed transposed
 // (S^T = K . Q^T with v_mfma_f32_32x32x16_{f16,bf16}) so that every lane
@@ -28,7 +28,6 @@ namespace hx {
 namespace {
 
 constexpr int ATT_BM = 128;  // query rows per workgroup
-constexpr int ATT_BN = 64;   // keys per block
 
 template <int DT>
 __device__ __forceinline__ v16f mfma_att(v4i a, v4i b, v16f c) {
@@ -48,22 +47,30 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
 }
 
 // 16-byte chunk swizzles.  K rows are D*2 bytes (D/8 chunks): the 32 rows an
-// operand read touches land on distinct bank groups.  V^T rows are 128 bytes
-// (64 keys): (d>>1 ^ d>>3) keeps both the transposing 2-byte writes (8 rows
-// 8 apart) and the 8-byte operand reads (16 consecutive rows) conflict-free.
+// operand read touches land on distinct bank groups.  V^T rows are BN*2
+// bytes: for 128-byte rows (64 keys) (d>>1 ^ d>>3), for 256-byte rows
+// (128 keys) (d ^ d>>3), keep both the transposing 2-byte writes (rows 8
+// apart) and the 8-byte operand reads (16 consecutive rows) conflict-free.
 template <int D>
 __device__ __forceinline__ int swz_k(int row) {
   if constexpr (D == 64) return (row ^ (row >> 3)) & 7;
   else return row & 15;
 }
-__device__ __forceinline__ int swz_vt(int d) { return ((d >> 1) ^ (d >> 3)) & 7; }
+template <int BN>
+__device__ __forceinline__ int swz_vt(int d) {
+  if constexpr (BN == 64) return ((d >> 1) ^ (d >> 3)) & 7;
+  else return (d ^ (d >> 3)) & 15;
+}
 
 }  // namespace
 
-template <int D, int DT, bool CAUSAL>
+template <int D, int DT, bool CAUSAL, int ATT_BN>
 __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
   constexpr int KS = D / 16;             // MFMA k-steps of the score product
   constexpr int DTILES = D / 32;         // 32-wide output column tiles
+  constexpr int JT = ATT_BN / 32;        // 32-key score tiles per block
+  constexpr int PS = ATT_BN / 16;        // 16-key steps of the P . V product
+  constexpr int VROW = ATT_BN * 2;       // bytes per V^T row
   constexpr int K_BYTES = ATT_BN * D * 2;
   constexpr int VT_BYTES = D * ATT_BN * 2;
   constexpr int CPR = D / 8;             // 16-byte chunks per K/V row
@@ -148,7 +155,7 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
         const int d = 8 * c + i;
         const uint16_t h = (uint16_t)(w[i >> 1] >> (16 * (i & 1)));
         *reinterpret_cast<uint16_t*>(
-            &svt[b][d * 128 + (((key >> 3) ^ swz_vt(d)) << 4) + (key & 7) * 2]) = h;
+            &svt[b][d * VROW + (((key >> 3) ^ swz_vt<ATT_BN>(d)) << 4) + (key & 7) * 2]) = h;
       });
     });
   };
@@ -164,25 +171,22 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
     if (blk + 1 < nblk) load_block(blk + 1);  // in flight during this block
 
     // S^T = K . Q^T: lane holds query q_row, keys 32*jt + 8*g + 4*lg + (0..3).
-    // All K fragment reads of the block are issued before the MFMAs.
-    v4i kf[2][KS];
-    static_for<2>([&](auto jc) {
+    // Per 32-key tile, its K fragment reads are issued before its MFMAs.
+    v16f s[JT];
+    static_for<JT>([&](auto jc) {
       constexpr int jt = decltype(jc)::value;
       const int krow = 32 * jt + lrow;
+      v4i kf[KS];
       static_for<KS>([&](auto kc) {
         constexpr int ks = decltype(kc)::value;
         const int c = 2 * ks + lg;
-        kf[jt][ks] = *reinterpret_cast<const v4i*>(&sk[b][krow * D * 2 + ((c ^ swz_k<D>(krow)) << 4)]);
+        kf[ks] = *reinterpret_cast<const v4i*>(&sk[b][krow * D * 2 + ((c ^ swz_k<D>(krow)) << 4)]);
       });
-    });
-    __builtin_amdgcn_sched_barrier(0);
-    v16f s[2];
-    static_for<2>([&](auto jc) {
-      constexpr int jt = decltype(jc)::value;
+      __builtin_amdgcn_sched_barrier(0);
       s[jt] = v16f{};
       static_for<KS>([&](auto kc) {
         constexpr int ks = decltype(kc)::value;
-        s[jt] = mfma_att<DT>(kf[jt][ks], qf[ks], s[jt]);
+        s[jt] = mfma_att<DT>(kf[ks], qf[ks], s[jt]);
       });
     });
     __builtin_amdgcn_sched_barrier(0);
@@ -195,7 +199,7 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
     bool full = key0 + ATT_BN <= p.Nk;
     if constexpr (CAUSAL) full = full && key0 + ATT_BN - 1 <= (int64_t)qb * ATT_BM + p.causal_offset;
     if (full) {
-      static_for<2>([&](auto jc) {
+      static_for<JT>([&](auto jc) {
         constexpr int jt = decltype(jc)::value;
         static_for<16>([&](auto rc) {
           constexpr int r = decltype(rc)::value;
@@ -205,7 +209,7 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
         });
       });
     } else {
-      static_for<2>([&](auto jc) {
+      static_for<JT>([&](auto jc) {
         constexpr int jt = decltype(jc)::value;
         static_for<16>([&](auto rc) {
           constexpr int r = decltype(rc)::value;
@@ -225,7 +229,7 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
     const float alpha = exp2_fast(m_i - m_use);
     float rs = 0.f;
-    static_for<2>([&](auto jc) {
+    static_for<JT>([&](auto jc) {
       constexpr int jt = decltype(jc)::value;
       static_for<16>([&](auto rc) {
         constexpr int r = decltype(rc)::value;
@@ -242,12 +246,12 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
       static_for<16>([&](auto rc) { oacc[dt][decltype(rc)::value] *= alpha; });
     });
 
-    // O^T += V^T . P^T over four 16-key steps.  Step t covers keys
+    // O^T += V^T . P^T over the block's 16-key steps.  Step t covers keys
     // 16t + 4*lg + (0..3) and 16t + 8 + 4*lg + (0..3) in this lane's k slots:
     // exactly the exponentials held in score registers 4g..4g+3, g = 2t' and
-    // 2t'+1 of tile t/2 -- and the matching V^T reads.
-    v4i pf[4];
-    static_for<4>([&](auto tc) {
+    // 2t'+1 (t' = t % 2) of tile t/2 -- and the matching V^T reads.
+    v4i pf[PS];
+    static_for<PS>([&](auto tc) {
       constexpr int t = decltype(tc)::value;
       constexpr int jt = t >> 1, g0 = 2 * (t & 1);
       pf[t] = v4i{(int)pack2<DT>(s[jt][4 * g0 + 0], s[jt][4 * g0 + 1]),
@@ -258,16 +262,16 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
     static_for<DTILES>([&](auto dc) {
       constexpr int dt = decltype(dc)::value;
       const int d = 32 * dt + lrow;
-      const char* row = &svt[b][d * 128];
-      v4i vf[4];
-      static_for<4>([&](auto tc) {
+      const char* row = &svt[b][d * VROW];
+      v4i vf[PS];
+      static_for<PS>([&](auto tc) {
         constexpr int t = decltype(tc)::value;
         const int ka = 16 * t + 4 * lg, kb = ka + 8;
-        const v2i lo = *reinterpret_cast<const v2i*>(row + (((ka >> 3) ^ swz_vt(d)) << 4) + (ka & 7) * 2);
-        const v2i hi = *reinterpret_cast<const v2i*>(row + (((kb >> 3) ^ swz_vt(d)) << 4) + (kb & 7) * 2);
+        const v2i lo = *reinterpret_cast<const v2i*>(row + (((ka >> 3) ^ swz_vt<ATT_BN>(d)) << 4) + (ka & 7) * 2);
+        const v2i hi = *reinterpret_cast<const v2i*>(row + (((kb >> 3) ^ swz_vt<ATT_BN>(d)) << 4) + (kb & 7) * 2);
         vf[t] = v4i{lo[0], lo[1], hi[0], hi[1]};
       });
-      static_for<4>([&](auto tc) {
+      static_for<PS>([&](auto tc) {
         constexpr int t = decltype(tc)::value;
         oacc[dt] = mfma_att<DT>(vf[t], pf[t], oacc[dt]);
       });
@@ -295,10 +299,10 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
   }
 }
 
-template <int D, int DT, bool CAUSAL>
+template <int D, int DT, bool CAUSAL, int BN>
 static void attn_launch(const AttnArgs& a, hipStream_t s) {
   const dim3 grid((unsigned)((a.Nq + ATT_BM - 1) / ATT_BM), (unsigned)(a.Z * a.H));
-  attn_fwd_kernel<D, DT, CAUSAL><<<grid, dim3(256), 0, s>>>(a);
+  attn_fwd_kernel<D, DT, CAUSAL, BN><<<grid, dim3(256), 0, s>>>(a);
 }
 
 const char* attn_refusal(const AttnArgs& a) {
@@ -314,16 +318,18 @@ const char* attn_refusal(const AttnArgs& a) {
 int launch_attention(int dtype, bool causal, const AttnArgs& a, hipStream_t s) {
   if (attn_refusal(a)) return HXI_ERR_UNSUPPORTED;
   if (a.Nq == 0 || a.Z * a.H == 0) return HXI_OK;
-#define HX_ATT(D_, DT_)                                          \
+  // keys per K/V block: 64 for D = 64 (two workgroups fit a CU), 128 for
+  // D = 128 (half the per-block softmax bookkeeping)
+#define HX_ATT(D_, DT_, BN_)                                     \
   if (a.D == D_ && dtype == DT_) {                               \
-    if (causal) attn_launch<D_, DT_, true>(a, s);                \
-    else attn_launch<D_, DT_, false>(a, s);                      \
+    if (causal) attn_launch<D_, DT_, true, BN_>(a, s);           \
+    else attn_launch<D_, DT_, false, BN_>(a, s);                 \
     return HXI_OK;                                               \
   }
-  HX_ATT(64, DT_F16)
-  HX_ATT(128, DT_F16)
-  HX_ATT(64, DT_BF16)
-  HX_ATT(128, DT_BF16)
+  HX_ATT(64, DT_F16, 64)
+  HX_ATT(128, DT_F16, 128)
+  HX_ATT(64, DT_BF16, 64)
+  HX_ATT(128, DT_BF16, 128)
 #undef HX_ATT
   return HXI_ERR_UNSUPPORTED;
 }
