@@ -187,6 +187,44 @@ def test_matmul_residual_scale_f32_out(hx, dev):
     assert not np.allclose(to_np(c), oracle.matmul(a, b, scale_n=s, out_dtype=np.float32), atol=1e-3)
 
 
+@pytest.mark.parametrize("segments", [2, 4])
+def test_matmul_k_looped_accumulator(hx, dev, segments):
+    """The K-looped form of test/python/triton/test_matmul_kloop.py:73-95:
+    M = N = 256, K = 512 walked in BLOCK_K segments with one f32 accumulator
+    carried across them.  Each segment is one hx_matmul whose residual and
+    output are the same f32 tensor (the read-out lands in the resident
+    accumulator, MatmulToHmxPass.cpp:1237-1305); the last segment writes the
+    f16 result directly.  Gate: rel < 2e-3 against the f64 product (:67), and
+    every segment must take the MFMA tile path with no fallback (:127-130)."""
+    import torch
+    M = N = 256
+    K = 512
+    bk = K // segments
+    g = torch.Generator().manual_seed(0)
+    a = torch.rand((M, K), generator=g).to(torch.float16)
+    b = torch.rand((K, N), generator=g).to(torch.float16)
+    ad, bd = a.to(dev), b.to(dev)
+    acc = torch.full((M, N), float("nan"), dtype=torch.float32, device=dev)
+    out = torch.empty((M, N), dtype=torch.float16, device=dev)
+    hx.manifest_clear()
+    hx.manifest_enable(True)
+    try:
+        for s in range(segments):
+            a_seg, b_seg = ad[:, s * bk:(s + 1) * bk], bd[s * bk:(s + 1) * bk, :]
+            last = s == segments - 1
+            hx.matmul(a_seg, b_seg, residual=acc if s else None, out=out if last else acc)
+        records = hx.manifest()["records"]
+    finally:
+        hx.manifest_enable(False)
+    exact = a.double().numpy() @ b.double().numpy()
+    assert rel_fro(to_np(out), exact) < 2e-3
+    assert sum(r["calls"] for r in records) == segments
+    assert {(r["plan"], r["reason"]) for r in records} == {("mfma-tiled", "selected-aligned")}
+    # the carried accumulator holds the f32 sum of all but the last segment
+    part = a[:, :K - bk].double().numpy() @ b[:K - bk, :].double().numpy()
+    assert rel_fro(to_np(acc), part) < 1e-5
+
+
 @pytest.mark.parametrize("shape", [(512, 1024, 512), (2048, 704, 4096), (40, 96, 64), (77, 130, 48)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_matmul_w8a16_gemm(hx, dev, shape):
