@@ -311,9 +311,9 @@ static int resolve_gemv(int64_t M, int64_t N, int64_t K, bool* was_pinned = null
   if (pin >= 0 && pin < gemv_packed_config_count()) return pin;
   (void)N; (void)K;
   // untuned choice from the MI355X sweep: LDS-staged activations and one
-  // column tile per workgroup for M <= 2, register-staged for M <= 8, four
-  // tiles (activation fragments reused 4x) for larger M
-  return M <= 2 && K <= 8192 ? 5 : M <= 8 ? 1 : 2;
+  // column tile per workgroup for M <= 2, register-staged for M <= 4, four
+  // tiles (activation fragments reused 4x) over 16 waves for larger M
+  return M <= 2 && K <= 8192 ? 5 : M <= 4 ? 1 : 8;
 }
 
 static int run_gemm(int op, GemmArgs& a, hipStream_t s, const PlanCtx& ctx) {

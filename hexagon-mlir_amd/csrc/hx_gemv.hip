@@ -290,6 +290,9 @@ static const GemvPackedEntry kGemvPacked[] = {
     {{1, 8, "packed_ct1_kw8_xl", 1, 1}, &gemv_packed_one<1, 8, 8, true>},
     {{2, 8, "packed_ct2_kw8_xl", 1, 0}, &gemv_packed_one<2, 8, 8, true>},
     {{1, 16, "packed_ct1_kw16_xl", 1, 1}, &gemv_packed_one<1, 16, 4, true>},
+    // 16 waves over K keep the 4-tile activation reuse of ct4 while putting
+    // 4x more waves (and weight bytes in flight) on the CUs it occupies
+    {{4, 16, "packed_ct4_kw16", 0, 8}, &gemv_packed_one<4, 16, 2, false>},
 };
 int gemv_packed_config_count() { return (int)(sizeof(kGemvPacked) / sizeof(kGemvPacked[0])); }
 const GemvConfig* gemv_packed_config(int idx) {
