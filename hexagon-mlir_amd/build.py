@@ -34,6 +34,14 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-ffp-contract
           "-Wno-unused-command-line-argument"]
 
 
+# Per-file device flags.  The attention kernel keeps MFMA operands and
+# results in architectural VGPRs (the score tiles feed VALU softmax code every
+# block; in accumulator registers each block would copy them back and forth).
+DEVICE_FLAGS = {
+    "hx_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def source_digest() -> str:
     h = hashlib.sha256()
     files = sorted(CSRC.glob("*")) + [ROOT / "include" / "hx.h", Path(__file__)]
@@ -62,7 +70,7 @@ def build(verbose: bool = False) -> Path:
 
     def compile_one(src: str) -> Path:
         obj = OBJDIR / (src + ".o")
-        cmd = [HIPCC, *COMMON, *defs, "-c", str(CSRC / src), "-o", str(obj)]
+        cmd = [HIPCC, *COMMON, *DEVICE_FLAGS.get(src, []), *defs, "-c", str(CSRC / src), "-o", str(obj)]
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode != 0:
             sys.stderr.write(r.stdout + r.stderr)

@@ -11,15 +11,18 @@
 // online-softmax recurrence of test/python/triton/test_online_softmax.py.
 //
 // MI355X design: one workgroup of four waves per (batch*head, 128 query
-// rows); each wave owns 32 query rows.  K/V blocks of 64 or 128 keys are staged
-// through LDS, double-buffered, with the next block's global loads in flight
-// during the current block's MFMAs.  Scores are computed transposed
-// (S^T = K . Q^T with v_mfma_f32_32x32x16_{f16,bf16}) so that every lane
-// holds one query row and 16 of its keys: row max and row sum are in-lane
-// plus one exchange with the partner lane (lane ^ 32), and the exponentials
-// are already in the operand layout of the P . V product -- no cross-lane
-// shuffle of P.  V is stored transposed in LDS (keys contiguous) so that the
-// P . V operand of a lane is two 8-byte reads.
+// rows); each wave owns 32 query rows.  K/V blocks of 64 or 128 keys are
+// staged row-major in LDS by direct-to-LDS buffer loads (no register
+// staging), double-buffered: the next block's loads are in flight during the
+// current block's MFMAs.  Scores are computed transposed (S^T = K . Q^T with
+// v_mfma_f32_32x32x16_{f16,bf16}) so that every lane holds one query row and
+// 16 of its keys: row max and row sum are in-lane plus one exchange with the
+// partner lane (lane ^ 32), and the exponentials are already in the operand
+// layout of the P . V product -- no cross-lane shuffle of P.  The V^T
+// operand of P . V is read from the row-major V block with gfx950's
+// transposing LDS read (ds_read_b64_tr_b16): within each 16-lane group,
+// lane 4a+b receives element b of the 8-byte chunks addressed by lanes
+// a, a+4, a+8, a+12, i.e. one column of V across four consecutive keys.
 #include "hx_device.hpp"
 #include "hx_internal.hpp"
 
@@ -40,27 +43,47 @@ __device__ __forceinline__ v16f mfma_att(v4i a, v4i b, v16f c) {
 // at binary32 accumulation precision anyway.
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// two binary32 values rounded to nearest-even and packed (v_cvt_pk_f16_f32 /
+// v_cvt_pk_bf16_f32: one instruction per pair)
 template <int DT>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
-  if constexpr (DT == DT_BF16) return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
-  else return (uint32_t)f32_to_f16_bits(a) | ((uint32_t)f32_to_f16_bits(b) << 16);
+  if constexpr (DT == DT_BF16) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, bf2{(__bf16)a, (__bf16)b});
+  } else {
+    typedef _Float16 hf2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, hf2{(_Float16)a, (_Float16)b});
+  }
 }
 
-// 16-byte chunk swizzles.  K rows are D*2 bytes (D/8 chunks): the 32 rows an
-// operand read touches land on distinct bank groups.  V^T rows are BN*2
-// bytes: for 128-byte rows (64 keys) (d>>1 ^ d>>3), for 256-byte rows
-// (128 keys) (d ^ d>>3), keep both the transposing 2-byte writes (rows 8
-// apart) and the 8-byte operand reads (16 consecutive rows) conflict-free.
+// Lazy rescaling: the running row maximum m is only moved (and the output
+// accumulator rescaled) when a block's maximum exceeds it by more than
+// RESCALE_MARGIN (log2 units); otherwise the block's probabilities are
+// exponentiated against the old m and may reach 2^RESCALE_MARGIN, which
+// fp16/bf16 P and the binary32 sums hold without loss (the final O = acc / l
+// is independent of which m was used).
+constexpr float RESCALE_MARGIN = 8.0f;
+
+// 16-byte chunk swizzles of the row-major K and V blocks (rows of D*2
+// bytes, D/8 chunks).  K: the 32 rows a score-operand read touches land on
+// distinct bank groups.  V: the transposing reads of a half wave cover 4
+// consecutive keys x 32 bytes (D = 64: 8 keys over two 128-byte rows per
+// bank period); XOR-ing the chunk with 4*(row & 3) (D = 128) or
+// 4*((row >> 1) & 1) (D = 64) spreads them over all 64 banks.  The direct
+// loads write whole KiB runs, conflict-free under any swizzle.
 template <int D>
 __device__ __forceinline__ int swz_k(int row) {
   if constexpr (D == 64) return (row ^ (row >> 3)) & 7;
   else return row & 15;
 }
-template <int BN>
-__device__ __forceinline__ int swz_vt(int d) {
-  if constexpr (BN == 64) return ((d >> 1) ^ (d >> 3)) & 7;
-  else return (d ^ (d >> 3)) & 15;
+template <int D>
+__device__ __forceinline__ int swz_v(int row) {
+  if constexpr (D == 64) return 4 * ((row >> 1) & 1);
+  else return 4 * (row & 3);
 }
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s* lds_v4s_ptr;
 
 }  // namespace
 
@@ -70,14 +93,19 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
   constexpr int DTILES = D / 32;         // 32-wide output column tiles
   constexpr int JT = ATT_BN / 32;        // 32-key score tiles per block
   constexpr int PS = ATT_BN / 16;        // 16-key steps of the P . V product
-  constexpr int VROW = ATT_BN * 2;       // bytes per V^T row
-  constexpr int K_BYTES = ATT_BN * D * 2;
-  constexpr int VT_BYTES = D * ATT_BN * 2;
-  constexpr int CPR = D / 8;             // 16-byte chunks per K/V row
-  constexpr int LOADS = ATT_BN * CPR / 256;  // 16-byte chunks per thread per block (each of K and V)
-  static_assert(LOADS >= 1 && ATT_BN * CPR % 256 == 0, "block split");
-  __shared__ __attribute__((aligned(16))) char sk[2][K_BYTES];
-  __shared__ __attribute__((aligned(16))) char svt[2][VT_BYTES];
+  constexpr int ROWB = D * 2;            // bytes per K or V row
+  constexpr int CPR = D / 8;             // 16-byte chunks per row
+  constexpr int RPK = 1024 / ROWB;       // rows per 1 KiB direct load
+  constexpr int BLK_BYTES = ATT_BN * ROWB;
+  constexpr int PER_W = BLK_BYTES / 4096;  // direct loads per wave per operand per block
+  static_assert(PER_W >= 1 && BLK_BYTES % 4096 == 0, "block split");
+  static_assert(2 * PER_W < 64, "vmcnt range");
+  // two buffers as distinct arrays, so the compiler can see that a direct
+  // load into one never aliases the reads of the other
+  __shared__ __attribute__((aligned(1024))) char sk0[BLK_BYTES];
+  __shared__ __attribute__((aligned(1024))) char sv0[BLK_BYTES];
+  __shared__ __attribute__((aligned(1024))) char sk1[BLK_BYTES];
+  __shared__ __attribute__((aligned(1024))) char sv1[BLK_BYTES];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -109,7 +137,16 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
   v16f oacc[DTILES];
   static_for<DTILES>([&](auto dc) { oacc[decltype(dc)::value] = v16f{}; });
   float m_i = -INFINITY, l_i = 0.f;
-  const float qk_scale = p.scale * 1.44269504088896340736f;
+  // exp2-domain scale; exponent arguments are fma(s, qk_scale, -m).  A
+  // negative scale is moved into Q (an exact sign flip of every element, so
+  // S flips sign exactly); a zero scale becomes a tiny positive one, which
+  // leaves every finite score at 2^0 and keeps masked (-inf) scores at 0.
+  float qk_scale = p.scale * 1.44269504088896340736f;
+  if (qk_scale < 0.f) {
+    static_for<KS>([&](auto kc) { qf[decltype(kc)::value] ^= (int)0x80008000u; });
+    qk_scale = -qk_scale;
+  }
+  qk_scale = fmaxf(qk_scale, 1e-30f);
 
   // Key blocks this workgroup visits (causal: up to its last query row).
   int64_t nk = p.Nk;
@@ -119,57 +156,39 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
   }
   const int nblk = nk > 0 ? (int)((nk + ATT_BN - 1) / ATT_BN) : 0;
 
-  // Global -> registers for one K/V block: thread chunk u = tid + 256*r is
-  // row u / CPR (key), 16-byte column chunk u % CPR.  Buffer loads: rows
-  // past Nk fall outside the descriptor's range and read as zero, with no
-  // branch.
+  // Direct loads of key block blk: load i of wave w fills the KiB of rows
+  // (w + 4i)*RPK + lane/CPR; the lane writes physical chunk lane % CPR and
+  // fetches the logical chunk the row's swizzle maps there.  Rows past Nk
+  // get an offset outside the buffer descriptor's range and read as zero.
+  const uint32_t sk_b = (uint32_t)(p.sk[2] * 2), sv_b = (uint32_t)(p.sv[2] * 2);
   const uint32_t k_bytes = (uint32_t)(((p.Nk - 1) * p.sk[2] + D) * 2);
   const uint32_t v_bytes = (uint32_t)(((p.Nk - 1) * p.sv[2] + D) * 2);
   const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)k, 0, (int)k_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)v, 0, (int)v_bytes, 0x00020000);
-  v4i kr[LOADS], vr[LOADS];
-  auto load_block = [&](int blk) {
-    static_for<LOADS>([&](auto rc) {
-      constexpr int r = decltype(rc)::value;
-      const int u = tid + 256 * r;
-      const int64_t key = (int64_t)blk * ATT_BN + u / CPR;
-      const int c = u % CPR;
+  auto dma_block = [&](char* dk, char* dv, int blk) {
+    static_for<PER_W>([&](auto ic) {
+      const int lb = wave + 4 * decltype(ic)::value;
+      const int row = lb * RPK + lane / CPR, pc = lane % CPR;
+      const int64_t key = (int64_t)blk * ATT_BN + row;
       const bool in = key < p.Nk;
-      const uint32_t ko = in ? (uint32_t)((key * p.sk[2] + 8 * c) * 2) : 0x80000000u;
-      const uint32_t vo = in ? (uint32_t)((key * p.sv[2] + 8 * c) * 2) : 0x80000000u;
-      kr[r] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rk, (int)ko, 0, 0));
-      vr[r] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rv, (int)vo, 0, 0));
-    });
-  };
-  // Registers -> LDS buffer b: K row-major (swizzled chunks), V transposed.
-  auto store_block = [&](int b) {
-    static_for<LOADS>([&](auto rc) {
-      constexpr int r = decltype(rc)::value;
-      const int u = tid + 256 * r;
-      const int key = u / CPR, c = u % CPR;
-      *reinterpret_cast<v4i*>(&sk[b][key * D * 2 + ((c ^ swz_k<D>(key)) << 4)]) = kr[r];
-      const uint32_t w[4] = {(uint32_t)vr[r][0], (uint32_t)vr[r][1], (uint32_t)vr[r][2],
-                             (uint32_t)vr[r][3]};
-      static_for<8>([&](auto ic) {
-        constexpr int i = decltype(ic)::value;
-        const int d = 8 * c + i;
-        const uint16_t h = (uint16_t)(w[i >> 1] >> (16 * (i & 1)));
-        *reinterpret_cast<uint16_t*>(
-            &svt[b][d * VROW + (((key >> 3) ^ swz_vt<ATT_BN>(d)) << 4) + (key & 7) * 2]) = h;
-      });
+      const uint32_t ko = in ? (uint32_t)key * sk_b + (uint32_t)((pc ^ swz_k<D>(row)) << 4) : 0x80000000u;
+      const uint32_t vo = in ? (uint32_t)key * sv_b + (uint32_t)((pc ^ swz_v<D>(row)) << 4) : 0x80000000u;
+      dma16(rk, dk + lb * 1024, ko, 0u);
+      dma16(rv, dv + lb * 1024, vo, 0u);
     });
   };
 
-  if (nblk > 0) {
-    load_block(0);
-    store_block(0);
-  }
-  __syncthreads();
+  // The V^T operand of 16-key step t, keys 16t + 8*half + 4*lg + (0..3) of
+  // column d = 32*dt + lrow: lane 16G + a + 4j addresses key
+  // 16t + 8*half + 4*(G/2) + j, columns 32*dt + 16*(G%2) + 4a + (0..3).
+  auto read_vt = [&](const char* cv, int dt, int t, int half) -> v2i {
+    const int row = 16 * t + 8 * half + 4 * (lane >> 5) + ((lane & 15) >> 2);
+    const int col = 32 * dt + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    const char* a = cv + row * ROWB + (((col >> 3) ^ swz_v<D>(row)) << 4) + ((col >> 2) & 1) * 8;
+    return __builtin_bit_cast(v2i, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_ptr)a));
+  };
 
-  for (int blk = 0; blk < nblk; ++blk) {
-    const int b = blk & 1;
-    if (blk + 1 < nblk) load_block(blk + 1);  // in flight during this block
-
+  auto block = [&](const char* ck, const char* cv, int blk) {
     // S^T = K . Q^T: lane holds query q_row, keys 32*jt + 8*g + 4*lg + (0..3).
     // Per 32-key tile, its K fragment reads are issued before its MFMAs.
     v16f s[JT];
@@ -180,12 +199,12 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
       static_for<KS>([&](auto kc) {
         constexpr int ks = decltype(kc)::value;
         const int c = 2 * ks + lg;
-        kf[ks] = *reinterpret_cast<const v4i*>(&sk[b][krow * D * 2 + ((c ^ swz_k<D>(krow)) << 4)]);
+        kf[ks] = *reinterpret_cast<const v4i*>(ck + krow * ROWB + ((c ^ swz_k<D>(krow)) << 4));
       });
       __builtin_amdgcn_sched_barrier(0);
-      s[jt] = v16f{};
-      static_for<KS>([&](auto kc) {
-        constexpr int ks = decltype(kc)::value;
+      s[jt] = mfma_att<DT>(kf[0], qf[0], v16f{});
+      static_for<KS - 1>([&](auto kc) {
+        constexpr int ks = decltype(kc)::value + 1;
         s[jt] = mfma_att<DT>(kf[ks], qf[ks], s[jt]);
       });
     });
@@ -195,56 +214,60 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
     const int64_t key0 = (int64_t)blk * ATT_BN;
     float mx = -INFINITY;
     // Only a block that reaches past Nk, or (causal) past the workgroup's
-    // first query row, needs the per-element mask.
+    // first query row, needs the per-element mask: keys key0 + rel with
+    // rel >= lim are masked to -inf.
     bool full = key0 + ATT_BN <= p.Nk;
     if constexpr (CAUSAL) full = full && key0 + ATT_BN - 1 <= (int64_t)qb * ATT_BM + p.causal_offset;
     if (full) {
       static_for<JT>([&](auto jc) {
         constexpr int jt = decltype(jc)::value;
-        static_for<16>([&](auto rc) {
-          constexpr int r = decltype(rc)::value;
-          const float t = s[jt][r] * qk_scale;
-          s[jt][r] = t;
-          mx = fmaxf(mx, t);
-        });
+        static_for<16>([&](auto rc) { mx = fmaxf(mx, s[jt][decltype(rc)::value]); });
       });
     } else {
+      int64_t lim64 = min((int64_t)ATT_BN, p.Nk - key0);
+      if constexpr (CAUSAL) lim64 = min(lim64, q_row + p.causal_offset - key0 + 1);
+      // this lane's keys are rel = c + 4*lg for compile-time c: compare c
+      // against lim - 4*lg (no per-element index registers)
+      const int lim_l = (int)max(lim64, (int64_t)0) - 4 * lg;
       static_for<JT>([&](auto jc) {
         constexpr int jt = decltype(jc)::value;
         static_for<16>([&](auto rc) {
           constexpr int r = decltype(rc)::value;
-          const int64_t key = key0 + 32 * jt + 8 * (r >> 2) + 4 * lg + (r & 3);
-          bool keep = key < p.Nk;
-          if constexpr (CAUSAL) keep = keep && key <= q_row + p.causal_offset;
-          const float t = keep ? s[jt][r] * qk_scale : -INFINITY;
+          constexpr int c = 32 * jt + 8 * (r >> 2) + (r & 3);
+          const float t = c < lim_l ? s[jt][r] : -INFINITY;
           s[jt][r] = t;
           mx = fmaxf(mx, t);
         });
       });
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_i, mx);
+    const float mxs = mx == -INFINITY ? -INFINITY : mx * qk_scale;
+    const bool grow = mxs > m_i + RESCALE_MARGIN;  // -inf + margin stays -inf
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+      const float m_new = grow ? mxs : m_i;
+      const float alpha = grow ? exp2_fast(m_i - m_new) : 1.f;
+      l_i *= alpha;
+      m_i = m_new;
+      static_for<DTILES>([&](auto dc) {
+        constexpr int dt = decltype(dc)::value;
+        static_for<16>([&](auto rc) { oacc[dt][decltype(rc)::value] *= alpha; });
+      });
+    }
     // a row with every key masked so far keeps m = -inf; exponentiate
-    // against 0 then so that p = 0 and alpha = 1 instead of NaN
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = exp2_fast(m_i - m_use);
+    // against 0 then so that p = 0 instead of NaN
+    const float mu = m_i == -INFINITY ? 0.f : m_i;
     float rs = 0.f;
     static_for<JT>([&](auto jc) {
       constexpr int jt = decltype(jc)::value;
       static_for<16>([&](auto rc) {
         constexpr int r = decltype(rc)::value;
-        const float e = exp2_fast(s[jt][r] - m_use);
+        const float e = exp2_fast(__builtin_fmaf(s[jt][r], qk_scale, -mu));
         s[jt][r] = e;
         rs += e;
       });
     });
     rs += __shfl_xor(rs, 32);
-    l_i = l_i * alpha + rs;
-    m_i = m_new;
-    static_for<DTILES>([&](auto dc) {
-      constexpr int dt = decltype(dc)::value;
-      static_for<16>([&](auto rc) { oacc[dt][decltype(rc)::value] *= alpha; });
-    });
+    l_i += rs;
 
     // O^T += V^T . P^T over the block's 16-key steps.  Step t covers keys
     // 16t + 4*lg + (0..3) and 16t + 8 + 4*lg + (0..3) in this lane's k slots:
@@ -261,14 +284,11 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
     });
     static_for<DTILES>([&](auto dc) {
       constexpr int dt = decltype(dc)::value;
-      const int d = 32 * dt + lrow;
-      const char* row = &svt[b][d * VROW];
       v4i vf[PS];
       static_for<PS>([&](auto tc) {
         constexpr int t = decltype(tc)::value;
-        const int ka = 16 * t + 4 * lg, kb = ka + 8;
-        const v2i lo = *reinterpret_cast<const v2i*>(row + (((ka >> 3) ^ swz_vt<ATT_BN>(d)) << 4) + (ka & 7) * 2);
-        const v2i hi = *reinterpret_cast<const v2i*>(row + (((kb >> 3) ^ swz_vt<ATT_BN>(d)) << 4) + (kb & 7) * 2);
+        const v2i lo = read_vt(cv, dt, t, 0);
+        const v2i hi = read_vt(cv, dt, t, 1);
         vf[t] = v4i{lo[0], lo[1], hi[0], hi[1]};
       });
       static_for<PS>([&](auto tc) {
@@ -276,12 +296,25 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
         oacc[dt] = mfma_att<DT>(vf[t], pf[t], oacc[dt]);
       });
     });
+  };
 
-    if (blk + 1 < nblk) {
-      store_block(b ^ 1);
-    }
-    __syncthreads();
+  // Blocks in pairs over the two buffers; each block's loads were issued
+  // one block earlier and are published by the barrier that ends it.
+  if (nblk > 0) dma_block(sk0, sv0, 0);
+  wait_vm<0>();
+  lds_barrier();
+  int blk = 0;
+  for (; blk + 2 <= nblk; blk += 2) {
+    dma_block(sk1, sv1, blk + 1);
+    block(sk0, sv0, blk);
+    wait_vm<0>();
+    lds_barrier();
+    if (blk + 2 < nblk) dma_block(sk0, sv0, blk + 2);
+    block(sk1, sv1, blk + 1);
+    wait_vm<0>();
+    lds_barrier();
   }
+  if (blk < nblk) block(sk0, sv0, blk);
 
   // O = acc / l: lane holds row q_row, columns 32*dt + 8*g + 4*lg + (0..3)
   if (q_in) {
@@ -312,14 +345,18 @@ const char* attn_refusal(const AttnArgs& a) {
   for (int i = 0; i < 3; ++i)
     if (a.sq[i] % 8 || a.sk[i] % 8 || a.sv[i] % 8 || a.so[i] % 8) return "row-stride";
   if (a.Z * a.H > 65535 || (a.Nq + ATT_BM - 1) / ATT_BM > 0x7fffffff) return "grid";
+  // K and V rows of one head are addressed with 32-bit byte offsets
+  if (a.Nk > 0 && (((a.Nk - 1) * a.sk[2] + a.D) * 2 >= ((int64_t)1 << 31) ||
+                   ((a.Nk - 1) * a.sv[2] + a.D) * 2 >= ((int64_t)1 << 31)))
+    return "offset-range";
   return nullptr;
 }
 
 int launch_attention(int dtype, bool causal, const AttnArgs& a, hipStream_t s) {
   if (attn_refusal(a)) return HXI_ERR_UNSUPPORTED;
   if (a.Nq == 0 || a.Z * a.H == 0) return HXI_OK;
-  // keys per K/V block: 64 for D = 64 (two workgroups fit a CU), 128 for
-  // D = 128 (half the per-block softmax bookkeeping)
+  // keys per K/V block: 64 (MI355X sweep over 32 / 64 / 128 keys; with
+  // 64 keys a D = 128 workgroup needs 64 KiB of LDS, two fit a CU)
 #define HX_ATT(D_, DT_, BN_)                                     \
   if (a.D == D_ && dtype == DT_) {                               \
     if (causal) attn_launch<D_, DT_, true, BN_>(a, s);           \
@@ -327,9 +364,9 @@ int launch_attention(int dtype, bool causal, const AttnArgs& a, hipStream_t s) {
     return HXI_OK;                                               \
   }
   HX_ATT(64, DT_F16, 64)
-  HX_ATT(128, DT_F16, 128)
+  HX_ATT(128, DT_F16, 64)
   HX_ATT(64, DT_BF16, 64)
-  HX_ATT(128, DT_BF16, 128)
+  HX_ATT(128, DT_BF16, 64)
 #undef HX_ATT
   return HXI_ERR_UNSUPPORTED;
 }

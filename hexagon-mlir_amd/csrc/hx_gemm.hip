@@ -99,39 +99,6 @@ __device__ __forceinline__ void tile_of(int tiles_m, int tiles_n, int& tm, int& 
   tn = in_group / gm;
 }
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-// One direct-to-LDS load: every lane fetches 16 bytes at voff + soff of the
-// buffer and the wave's 64 results land contiguously (lane order) at `lds`
-// (a wave-uniform address).  A plain function, not a template member: the
-// builtin inside a kernel template stops the host pass from emitting the
-// kernel's launch stub.
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* lds, uint32_t voff,
-                                      uint32_t soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voff, soff, 0, 0);
-}
-
-// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding):
-// all but this wave's N most recent direct-to-LDS loads have landed.
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// Workgroup barrier that orders LDS only.  __syncthreads() is a release
-// fence on all memory, which counts outstanding direct-to-LDS loads as
-// pending LDS writes and forces vmcnt(0); here every wave has already waited
-// for its own loads of the stage it is about to publish (wait_vm), so the
-// barrier needs only this wave's LDS reads retired (lgkmcnt(0)).  The
-// "memory" clobber keeps the compiler from moving memory operations across
-// it, the sched_barriers keep the machine scheduler from doing so.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_sched_barrier(0);
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
-}
-
 __device__ __forceinline__ v4f load4(const void* p, int dt, int64_t idx) {
   if (dt == DT_F32) return *reinterpret_cast<const v4f*>(reinterpret_cast<const float*>(p) + idx);
   const v2i w = *reinterpret_cast<const v2i*>(reinterpret_cast<const uint16_t*>(p) + idx);
