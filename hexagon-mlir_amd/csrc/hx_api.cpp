@@ -310,10 +310,12 @@ static int resolve_gemv(int64_t M, int64_t N, int64_t K, bool* was_pinned = null
   if (was_pinned) *was_pinned = pin >= 0 && pin < gemv_packed_config_count();
   if (pin >= 0 && pin < gemv_packed_config_count()) return pin;
   (void)N; (void)K;
-  // untuned choice from the MI355X sweep: LDS-staged activations and one
-  // column tile per workgroup for M <= 2, register-staged for M <= 4, four
-  // tiles (activation fragments reused 4x) over 16 waves for larger M
-  return M <= 2 && K <= 8192 ? 5 : M <= 4 ? 1 : 8;
+  // untuned choice from the MI355X sweep (N = 11008, K = 4096): LDS-staged
+  // activations and one column tile per workgroup for M <= 4 (the launcher
+  // falls back to the register-staged base config when the rows do not fit
+  // in LDS), four tiles (activation fragments reused 4x) over 8 waves for
+  // larger M
+  return M <= 4 ? 5 : 2;
 }
 
 static int run_gemm(int op, GemmArgs& a, hipStream_t s, const PlanCtx& ctx) {
@@ -779,9 +781,11 @@ static int matmul_resident_impl(const View2& vx, hx_weight* w, const View2* vr, 
   const int x_dt = w->dtype == HX_BF16 ? HX_BF16 : HX_F16;
   const int64_t M = vx.rows;
   if (M == 0) return HX_OK;
-  // The packed GEMV reads activations as 8-element (16-byte) groups.
+  // The packed GEMV reads activations as 8-element (16-byte) groups, with
+  // 32-bit buffer offsets into the activation rows and one workgroup's tiles.
   if (w->dtype == HX_I8 && w->packed && M <= 16 && !vr && y_dt == HX_F16 && w->K % 8 == 0 &&
-      ((uintptr_t)vx.p & 15u) == 0 && (vx.ld * 2) % 16 == 0) {
+      ((uintptr_t)vx.p & 15u) == 0 && (vx.ld * 2) % 16 == 0 && M * vx.ld * 2 < ((int64_t)1 << 31) &&
+      (w->K + 63) / 64 * 4 * 1024 < ((int64_t)1 << 31)) {
     GemvArgs v{};
     v.x = vx.p; v.ldx = vx.ld; v.w = nullptr; v.ldw = 0;
     v.scale = w->scale; v.y = vy.p; v.ldy = vy.ld; v.M = M; v.N = w->N; v.K = w->K;

@@ -128,6 +128,21 @@ __device__ __forceinline__ v8h i8x8_to_v8h(uint32_t w0, uint32_t w1) {
   return r;
 }
 
+// The same conversion for bytes already stored in excess-128 form
+// (u = b ^ 0x80, as the packed decode-GEMV weight image keeps them): the
+// XOR is done once when the image is built instead of on every load.
+__device__ __forceinline__ v8h x8x8_to_v8h(uint32_t u0, uint32_t u1) {
+  const v2h bias = {(f16)1152.0f, (f16)1152.0f};
+  v8h r;
+  const v2h a = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(0x64646464u, u0, 0x04010400u)) - bias;
+  const v2h b = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(0x64646464u, u0, 0x04030402u)) - bias;
+  const v2h c = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(0x64646464u, u1, 0x04010400u)) - bias;
+  const v2h d = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(0x64646464u, u1, 0x04030402u)) - bias;
+  r[0] = a[0]; r[1] = a[1]; r[2] = b[0]; r[3] = b[1];
+  r[4] = c[0]; r[5] = c[1]; r[6] = d[0]; r[7] = d[1];
+  return r;
+}
+
 // ---------------------------------------------------------------------------
 // MFMA wrappers.  All 32x32 variants take a 16-byte A and B operand per lane:
 // lane l supplies row (l % 32) and the 16-byte K slice (l / 32), and the 16

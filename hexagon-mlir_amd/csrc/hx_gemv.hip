@@ -123,8 +123,9 @@ __global__ void __launch_bounds__(256) gemv_w8a16_kernel(GemvArgs p) {
 // Fragment-packed variant (resident weights).  The weight image is stored in
 // MFMA B-fragment order: for column tile t (16 columns) and K chunk j (64 k)
 // one 1 KiB block at ((t * KC) + j) * 1024 (KC = K/64 chunks), in which byte
-// 256*g + 16*c + i holds W[64*j + 16*g + i][16*t + c] (g 0..3, c 0..15,
-// i 0..15).  Lane l of a wave then loads its operand as the 16 contiguous
+// 256*g + 16*c + i holds W[64*j + 16*g + i][16*t + c] ^ 0x80 (g 0..3,
+// c 0..15, i 0..15; excess-128, so the widening to f16 needs no XOR per
+// load).  Lane l of a wave then loads its operand as the 16 contiguous
 // bytes at 16*l: column l % 16, k = 64*j + 16*(l/16) + (0..15), which feeds
 // two v_mfma_f32_16x16x32_f16 steps (e = 0, 1: k = .. + 8*e + (0..7)); the
 // activation operand uses the same k mapping.  Every wave load is one
@@ -134,10 +135,14 @@ __global__ void __launch_bounds__(256) gemv_w8a16_kernel(GemvArgs p) {
 // ---------------------------------------------------------------------------
 //
 // XL (M <= 4): the activations are staged once per workgroup in LDS ([M]
-// rows of kchunks*64, zero-padded) after the weight loads are issued, and
-// each MFMA step reads its operand from there; the registers that would
-// hold every step's activation fragment (2 x 16 bytes per chunk) are freed,
-// so more waves -- more weight bytes in flight -- fit on a CU.
+// rows of kchunks*64, zero-padded), and each MFMA step reads its operand
+// from there; the registers that would hold every step's activation
+// fragment (2 x 16 bytes per chunk) are freed, so more waves -- more weight
+// bytes in flight -- fit on a CU.  The activation loads are issued before
+// the weight stream: loads complete in issue order, so an activation load
+// queued behind a wave's weight loads would hold back the whole
+// workgroup's compute (the LDS staging ends in a barrier) until its last
+// weight byte has arrived, leaving no overlap between compute and stream.
 template <int CT, int KW, int CPW, bool XL>
 __global__ void __launch_bounds__(64 * KW) gemv_packed_kernel(GemvArgs p, const int8_t* packed,
                                                               int kchunks) {
@@ -146,15 +151,52 @@ __global__ void __launch_bounds__(64 * KW) gemv_packed_kernel(GemvArgs p, const 
   const int col = lane & 15, g = lane >> 4;
   const int t0 = blockIdx.x * CT;                    // first column tile
   const int ntiles = (int)((p.N + 15) / 16);
+  const int tiles_here = min(CT, ntiles - t0);
   const bool xrow = col < p.M;
   const uint16_t* x = reinterpret_cast<const uint16_t*>(p.x);
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
   const int64_t kp = (int64_t)kchunks * 64;
   const int64_t kps = kp + 8;  // row pitch: 16 bytes of padding spread the rows over the banks
 
+  // Every global load below is a buffer load whose out-of-range offset
+  // (0x80000000) reads zero, so no load sits behind a branch: a conditional
+  // load makes the compiler wait for it at the join, or count outstanding
+  // loads conservatively.  The launcher keeps all offsets below 2^31.
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(packed + (int64_t)t0 * kchunks * 1024), 0, tiles_here * kchunks * 1024, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc((void*)x, 0, (int)(p.M * p.ldx * 2), 0x00020000);
+  constexpr int kNT = 2;  // cache policy: non-temporal (the weight is streamed once)
+
   v4f acc[CT];
 #pragma unroll
   for (int c = 0; c < CT; ++c) acc[c] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  // XL staging walks the [M][kp] activation block as (row m, column block
+  // b): step r = m * cb + b covers the 16-byte chunks c = b * T + tid of row m
+  // (T threads, cb = ceil(kchunks * 8 / T) blocks per row), so m and b are
+  // workgroup-uniform and no per-lane division is needed.  The first XR
+  // steps go through registers ahead of the weight loads; any further ones
+  // (large M * K) are loaded after them.
+  constexpr int NT = 64 * KW;
+  constexpr int XR = XL ? (2048 / NT > 0 ? 2048 / NT : 1) : 1;
+  const uint32_t row_ch = (uint32_t)kchunks * 8u;
+  const uint32_t cb = (row_ch + NT - 1) / NT;
+  const uint32_t nsteps = XL ? (uint32_t)p.M * cb : 0u;
+  auto x_load = [&](uint32_t r) -> v4u {  // step r; zero past K or past the last step
+    const uint32_t m = r / cb, k = ((r - m * cb) * NT + (uint32_t)tid) * 8u;
+    const uint32_t off = (r < nsteps && k < (uint32_t)p.K) ? (m * (uint32_t)p.ldx + k) * 2u : 0x80000000u;
+    return __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0));
+  };
+  auto x_store = [&](uint32_t r, const v4u& v) {  // step r into xs (chunks past kp skipped)
+    const uint32_t m = r / cb, c = (r - m * cb) * NT + (uint32_t)tid;
+    if (c < row_ch) *reinterpret_cast<v4u*>(xs + (int64_t)m * kps + c * 8u) = v;
+  };
+  v4u xr[XR];
+  if constexpr (XL) {
+#pragma unroll
+    for (int r = 0; r < XR; ++r) xr[r] = x_load((uint32_t)r);
+  }
 
   // chunks [c0, c0 + CPW * KW) are split as wave w -> c0 + w + KW * u
   for (int c0 = 0; c0 < kchunks; c0 += CPW * KW) {
@@ -166,31 +208,28 @@ __global__ void __launch_bounds__(64 * KW) gemv_packed_kernel(GemvArgs p, const 
       const bool jv = j < kchunks;
 #pragma unroll
       for (int c = 0; c < CT; ++c) {
-        const int t = t0 + c;
-        wq[u][c] = (jv && t < ntiles)
-                       ? __builtin_nontemporal_load(reinterpret_cast<const v4u*>(
-                             packed + ((int64_t)t * kchunks + j) * 1024 + 16 * lane))
-                       : v4u{0u, 0u, 0u, 0u};
+        const uint32_t off = (jv && c < tiles_here)
+                                 ? (uint32_t)(c * kchunks + j) * 1024u + 16u * (uint32_t)lane
+                                 : 0x80000000u;
+        wq[u][c] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)off, 0, kNT));
       }
       if constexpr (!XL) {
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-          const int64_t k = (int64_t)j * 64 + 16 * g + 8 * e;
-          xq[u][e] = (jv && xrow && k < p.K)
-                         ? *reinterpret_cast<const v4u*>(x + (int64_t)col * p.ldx + k)
-                         : v4u{0u, 0u, 0u, 0u};
+          const uint32_t k = (uint32_t)j * 64u + 16u * g + 8u * e;
+          const uint32_t off = (jv && xrow && k < (uint32_t)p.K)
+                                   ? ((uint32_t)col * (uint32_t)p.ldx + k) * 2u : 0x80000000u;
+          xq[u][e] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0));
         }
       }
     }
     if constexpr (XL) {
       // stage X (rows < M, zero past K) while the weight loads are in flight
       if (c0 == 0) {
-        const int64_t nch = (int64_t)p.M * kchunks * 8;  // 16-byte chunks
-        for (int64_t q = tid; q < nch; q += 64 * KW) {
-          const int64_t m = q / (kchunks * 8), k = (q - m * kchunks * 8) * 8;
-          *reinterpret_cast<v4u*>(xs + m * kps + k) =
-              k < p.K ? *reinterpret_cast<const v4u*>(x + m * p.ldx + k) : v4u{0u, 0u, 0u, 0u};
-        }
+#pragma unroll
+        for (int r = 0; r < XR; ++r)
+          if ((uint32_t)r < nsteps) x_store((uint32_t)r, xr[r]);
+        for (uint32_t r = XR; r < nsteps; ++r) x_store(r, x_load(r));
         __syncthreads();
       }
     }
@@ -200,14 +239,17 @@ __global__ void __launch_bounds__(64 * KW) gemv_packed_kernel(GemvArgs p, const 
       for (int e = 0; e < 2; ++e) {
         v8h xa;
         if constexpr (XL) {
+          // rows >= M read row 0 and are zeroed after the (unconditional) read
           const int64_t k = (int64_t)(c0 + wave + KW * u) * 64 + 16 * g + 8 * e;
-          xa = (xrow && k < kp) ? *reinterpret_cast<const v8h*>(xs + col * kps + k) : v8h{};
+          const bool in = xrow && k < kp;
+          const v8h t = *reinterpret_cast<const v8h*>(xs + (xrow ? col : 0) * kps + (in ? k : 0));
+          xa = in ? t : v8h{};
         } else {
           xa = __builtin_bit_cast(v8h, xq[u][e]);
         }
 #pragma unroll
         for (int c = 0; c < CT; ++c) {
-          const v8h wb = i8x8_to_v8h(wq[u][c][2 * e], wq[u][c][2 * e + 1]);
+          const v8h wb = x8x8_to_v8h(wq[u][c][2 * e], wq[u][c][2 * e + 1]);
           acc[c] = mfma16_f16(xa, wb, acc[c]);
         }
       }
@@ -235,7 +277,8 @@ __global__ void __launch_bounds__(64 * KW) gemv_packed_kernel(GemvArgs p, const 
 
 // Build the fragment-packed image from a K-contiguous [N][K] int8 weight:
 // packed block (t, j) byte 256*g + 16*c + i = W[n = 16t + c][k = 64j + 16g + i]
-// (zero beyond N or K).  One thread per 16-byte run (t, j, g, c).
+// ^ 0x80 (excess-128; 0x80, i.e. zero, beyond N or K).  One thread per
+// 16-byte run (t, j, g, c).
 __global__ void __launch_bounds__(256) gemv_pack_kernel(const int8_t* w, int64_t ldw, int64_t N,
                                                         int64_t K, int kchunks, int8_t* out) {
   const int64_t ntiles = (N + 15) / 16;
@@ -246,9 +289,10 @@ __global__ void __launch_bounds__(256) gemv_pack_kernel(const int8_t* w, int64_t
     const int64_t t = blk / kchunks, j = blk - t * kchunks;
     const int c = lane & 15, g = lane >> 4;
     const int64_t n = t * 16 + c, k0 = j * 64 + 16 * g;
-    int8_t v[16];
+    uint8_t v[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = (n < N && k0 + i < K) ? w[n * ldw + k0 + i] : (int8_t)0;
+    for (int i = 0; i < 16; ++i)
+      v[i] = (uint8_t)(((n < N && k0 + i < K) ? (uint8_t)w[n * ldw + k0 + i] : 0u) ^ 0x80u);
     *reinterpret_cast<v4u*>(out + blk * 1024 + 16 * lane) = *reinterpret_cast<const v4u*>(v);
   }
 }
@@ -303,6 +347,11 @@ int launch_gemv_packed(int cfg_idx, const GemvArgs& a, const int8_t* packed, hip
   if (cfg_idx < 0 || cfg_idx >= gemv_packed_config_count()) return HXI_ERR_ARG;
   if (a.M < 1 || a.M > 16) return HXI_ERR_SHAPE;
   const int64_t kchunks = (a.K + 63) / 64;
+  // 32-bit buffer offsets: one workgroup's tiles and the activation rows
+  if ((int64_t)kGemvPacked[cfg_idx].cfg.ct * kchunks * 1024 >= ((int64_t)1 << 31) ||
+      a.M * a.ldx * 2 >= ((int64_t)1 << 31))
+    return HXI_ERR_SHAPE;
+  // xl: staged rows within 64 KiB of LDS
   if (kGemvPacked[cfg_idx].cfg.xl && (a.M > 4 || a.M * (kchunks * 64 + 8) * 2 > 65536))
     cfg_idx = kGemvPacked[cfg_idx].cfg.base;
   kGemvPacked[cfg_idx].fn(a, packed, (int)((a.K + 63) / 64), s);

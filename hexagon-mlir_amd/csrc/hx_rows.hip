@@ -254,6 +254,21 @@ __global__ void __launch_bounds__(256) row_vec_kernel(RowArgs a) {
     raw[i] = ok[i] ? __builtin_nontemporal_load(reinterpret_cast<const v4u*>(xr + c0))
                    : v4u{0u, 0u, 0u, 0u};
   }
+  // gamma / beta are fetched with the row, so their latency hides under the
+  // row's own loads rather than stalling the write-back after the reduction
+  const S* wp = reinterpret_cast<const S*>(a.w);
+  const S* bp = reinterpret_cast<const S*>(a.b);
+  v4u wv[VPL], bv[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int64_t c0 = ((int64_t)(i * WPR + wave_in_row) * 64 + lane) * EV;
+    wv[i] = v4u{0u, 0u, 0u, 0u};
+    bv[i] = v4u{0u, 0u, 0u, 0u};
+    if constexpr (OP != ROW_SOFTMAX) {
+      if (wp && ok[i]) wv[i] = *reinterpret_cast<const v4u*>(wp + c0);
+      if (bp && ok[i]) bv[i] = *reinterpret_cast<const v4u*>(bp + c0);
+    }
+  }
 
   float scale = 1.f, shift = 0.f;
   if constexpr (OP == ROW_SOFTMAX) {
@@ -313,17 +328,10 @@ __global__ void __launch_bounds__(256) row_vec_kernel(RowArgs a) {
     }
   }
 
-  const S* wp = reinterpret_cast<const S*>(a.w);
-  const S* bp = reinterpret_cast<const S*>(a.b);
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     if (!ok[i]) continue;
     const int64_t c0 = ((int64_t)(i * WPR + wave_in_row) * 64 + lane) * EV;
-    v4u wv = {0u, 0u, 0u, 0u}, bv = {0u, 0u, 0u, 0u};
-    if constexpr (OP != ROW_SOFTMAX) {
-      if (wp) wv = *reinterpret_cast<const v4u*>(wp + c0);
-      if (bp) bv = *reinterpret_cast<const v4u*>(bp + c0);
-    }
     S out[EV];
 #pragma unroll
     for (int j = 0; j < EV; ++j) {
@@ -333,11 +341,11 @@ __global__ void __launch_bounds__(256) row_vec_kernel(RowArgs a) {
         r = fast_exp(x - shift) * scale;
       } else if constexpr (OP == ROW_RMSNORM) {
         r = x * scale;
-        if (wp) r = r * vec_elem<DT>(wv, j);
+        if (wp) r = r * vec_elem<DT>(wv[i], j);
       } else {
         r = (x - shift) * scale;
-        if (wp) r = r * vec_elem<DT>(wv, j);
-        if (bp) r = r + vec_elem<DT>(bv, j);
+        if (wp) r = r * vec_elem<DT>(wv[i], j);
+        if (bp) r = r + vec_elem<DT>(bv[i], j);
       }
       out[j] = Elem<DT>::store(r);
     }
