@@ -53,6 +53,10 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return (uint16_t)(x >> 16);
 }
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  // The empty asm makes f an opaque binary32 value: without it the backend
+  // folds a preceding multiply into the conversion (v_fma_mixlo_f16, one
+  // rounding instead of two) even with floating-point contraction off.
+  asm("" : "+v"(f));
   f16 h = (f16)f;
   return __builtin_bit_cast(uint16_t, h);
 }

@@ -371,22 +371,62 @@ gemm_kernel(GemmArgs p) {
   // private LDS region (the stage buffers are free now), row-major with the
   // 16-byte chunk XOR-swizzled by row (conflict-free 8/16-byte writes and
   // 16-byte reads), and reads it back so that every lane stores 16
-  // consecutive bytes and a wave store covers whole rows.  For each
-  // sub-tile column all loads (scales, residual) are issued before any
-  // store they might alias.
+  // consecutive bytes and a wave store covers whole rows.
+  //
+  // The epilogue is straight-line code: the output type is a compile-time
+  // variant chosen once, every scale is fetched up front with branch-free
+  // buffer loads (an absent scale reads as 1.0; multiplying by 1.0 is exact,
+  // so the result equals skipping the multiply), and residual reads use
+  // clamped in-bounds indices (values for rows/columns past the edge are
+  // never stored).  A per-element test of the output type or of an optional
+  // argument would put a branch, and a wait for every load behind it, on
+  // each element.  All loads of a pass (scales, residual) are issued before
+  // any store of that pass, so a residual that aliases C is read first.
   lds_barrier();  // every wave is done reading the stage buffers
   const int64_t row0w = m0 + wm * WTM;
   const int64_t col0w = n0 + wn * WTN;
-  const int odt = p.out_dtype;
+  auto f32_rsrc = [](const float* ptr, int64_t n) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)ptr, 0, ptr ? (int)(n * 4) : 0, 0x00020000);
+  };
+  const __amdgpu_buffer_rsrc_t r_rs = f32_rsrc(MODE == GM_I8 ? p.row_scale : nullptr, p.M);
+  const __amdgpu_buffer_rsrc_t r_cs = f32_rsrc(p.col_scale, p.N);
+  const __amdgpu_buffer_rsrc_t r_cs2 = f32_rsrc(NB == 2 ? p.col_scale2 : nullptr, p.N);
+  const bool has_rs = MODE == GM_I8 && p.row_scale != nullptr;
+  const bool has_cs = p.col_scale != nullptr;
+  const bool has_cs2 = NB == 2 && p.col_scale2 != nullptr;
   float rs[TM];
+  v4f cs[TN][4], cs2[TN][4];
   static_for<TM>([&](auto ic) {
     constexpr int i = decltype(ic)::value;
-    const int64_t row = row0w + i * 32 + lrow;
-    rs[i] = (MODE == GM_I8 && p.row_scale && row < p.M) ? p.row_scale[row] : 1.f;
+    const uint32_t row = (uint32_t)(row0w + i * 32 + lrow);
+    rs[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_rs, (int)(row * 4u), 0, 0));
   });
+  static_for<TN>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    static_for<4>([&](auto gc) {
+      constexpr int g = decltype(gc)::value;
+      const uint32_t col = (uint32_t)(col0w + j * 32 + 8 * g + 4 * lg);
+      cs[j][g] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(r_cs, (int)(col * 4u), 0, 0));
+      if constexpr (NB == 2)
+        cs2[j][g] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(r_cs2, (int)(col * 4u), 0, 0));
+    });
+  });
+  static_for<TM>([&](auto ic) { rs[decltype(ic)::value] = has_rs ? rs[decltype(ic)::value] : 1.f; });
+  static_for<TN>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    static_for<4>([&](auto gc) {
+      constexpr int g = decltype(gc)::value;
+      if (!has_cs) cs[j][g] = v4f{1.f, 1.f, 1.f, 1.f};
+      if constexpr (NB == 2)
+        if (!has_cs2) cs2[j][g] = v4f{1.f, 1.f, 1.f, 1.f};
+    });
+  });
+  const bool has_res = MODE != GM_I8 && EPI != GE_SWIGLU && p.res != nullptr;
 
-  auto epilogue = [&](auto esc) {
-    constexpr int ES = decltype(esc)::value;     // output element bytes
+  // OK: output kind (DT_I32 / DT_F32 / DT_F16 / DT_BF16), a compile-time value
+  auto epilogue = [&](auto okc) {
+    constexpr int OK = decltype(okc)::value;
+    constexpr int ES = (OK == DT_I32 || OK == DT_F32) ? 4 : 2;  // output element bytes
     constexpr int RB = WTN * ES;                 // bytes per row of the wave block
     constexpr int PER_ARRAY = (NW + 1) / 2;      // wave regions per stage buffer
     constexpr int REGION = STAGE / PER_ARRAY;
@@ -401,37 +441,35 @@ gemm_kernel(GemmArgs p) {
     char* region = (wave < PER_ARRAY ? st0 : st1) + (wave % PER_ARRAY) * (TMP * 32 * RB);
     static_for<TM / TMP>([&](auto pc) {
       constexpr int pp = decltype(pc)::value;
-      // 1) this pass's sub-tile rows -> LDS, in the output type
-      static_for<TN>([&](auto jc) {
-        constexpr int j = decltype(jc)::value;
-        v4f cs[4], cs2[4];
-        static_for<4>([&](auto gc) {
-          constexpr int g = decltype(gc)::value;
-          const int64_t col = col0w + j * 32 + 8 * g + 4 * lg;
-          const bool in = col < p.N;
-          cs[g] = (p.col_scale && in) ? v4f{p.col_scale[col], p.col_scale[col + 1],
-                                             p.col_scale[col + 2], p.col_scale[col + 3]}
-                                      : v4f{1.f, 1.f, 1.f, 1.f};
-          if constexpr (NB == 2)
-            cs2[g] = (p.col_scale2 && in) ? v4f{p.col_scale2[col], p.col_scale2[col + 1],
-                                                p.col_scale2[col + 2], p.col_scale2[col + 3]}
-                                          : v4f{1.f, 1.f, 1.f, 1.f};
-        });
-        v4f res[TMP][4];
-        if constexpr (MODE != GM_I8 && EPI != GE_SWIGLU) {
-          if (p.res) {
+      // residual of this pass (float GE_STORE only), all of it before any store
+      v4f res[TN][TMP][4];
+      if constexpr (MODE != GM_I8 && EPI != GE_SWIGLU) {
+        if (has_res) {
+          static_for<TN>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
             static_for<TMP>([&](auto ic) {
               constexpr int ii = decltype(ic)::value;
               static_for<4>([&](auto gc) {
                 constexpr int g = decltype(gc)::value;
-                const int64_t row = row0w + (pp * TMP + ii) * 32 + lrow;
-                const int64_t col = col0w + j * 32 + 8 * g + 4 * lg;
-                res[ii][g] = (row < p.M && col < p.N) ? load4(p.res, p.res_dtype, row * p.ldr + col)
-                                                      : v4f{0.f, 0.f, 0.f, 0.f};
+                const int64_t row = min(row0w + (pp * TMP + ii) * 32 + lrow, p.M - 1);
+                const int64_t col = min(col0w + j * 32 + 8 * g + 4 * lg, p.N - 4);
+                res[j][ii][g] = load4(p.res, p.res_dtype, row * p.ldr + col);
               });
             });
-          }
+          });
+        } else {
+          static_for<TN>([&](auto jc) {
+            static_for<TMP>([&](auto ic) {
+              static_for<4>([&](auto gc) {
+                res[decltype(jc)::value][decltype(ic)::value][decltype(gc)::value] = v4f{0.f, 0.f, 0.f, 0.f};
+              });
+            });
+          });
         }
+      }
+      // 1) this pass's sub-tile rows -> LDS, in the output type
+      static_for<TN>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
         static_for<TMP>([&](auto ic) {
           constexpr int ii = decltype(ic)::value;
           constexpr int i = pp * TMP + ii;
@@ -440,46 +478,41 @@ gemm_kernel(GemmArgs p) {
             constexpr int g = decltype(gc)::value;
             const int byte = (j * 32 + 8 * g + 4 * lg) * ES;
             char* dst = region + rl * RB + (((byte >> 4) ^ swz_out(rl)) << 4) + (byte & 15);
-            if constexpr (MODE == GM_I8) {
-              if (odt == DT_I32) {
-                *reinterpret_cast<v4i*>(dst) = v4i{acc[0][i][j][4 * g], acc[0][i][j][4 * g + 1],
-                                                   acc[0][i][j][4 * g + 2], acc[0][i][j][4 * g + 3]};
-                return;
-              }
-            }
-            float v[4];
-            static_for<4>([&](auto qc) {
-              constexpr int q = decltype(qc)::value;
-              if constexpr (MODE == GM_I8) {
-                float t = (float)acc[0][i][j][4 * g + q];
-                if (p.row_scale) t = t * rs[i];
-                if (p.col_scale) t = t * cs[g][q];
-                v[q] = t;
-              } else if constexpr (EPI == GE_SWIGLU) {
-                const float gt = f16_bits_to_f32(f32_to_f16_bits(acc[0][i][j][4 * g + q] * cs[g][q]));
-                const float up =
-                    f16_bits_to_f32(f32_to_f16_bits(acc[NB - 1][i][j][4 * g + q] * cs2[g][q]));
-                const float sg = gt / (1.0f + fast_exp(-gt));
-                v[q] = sg * up;
-              } else {
-                float t = acc[0][i][j][4 * g + q];
-                if (p.col_scale) t = t * cs[g][q];
-                if (p.res) t = t + res[ii][g][q];
-                v[q] = t;
-              }
-            });
-            if constexpr (ES == 4) {
-              *reinterpret_cast<v4f*>(dst) = v4f{v[0], v[1], v[2], v[3]};
+            if constexpr (MODE == GM_I8 && OK == DT_I32) {
+              *reinterpret_cast<v4i*>(dst) =
+                  v4i{(int)acc[0][i][j][4 * g], (int)acc[0][i][j][4 * g + 1],
+                      (int)acc[0][i][j][4 * g + 2], (int)acc[0][i][j][4 * g + 3]};
             } else {
-              uint32_t lo, hi;
-              if (odt == DT_BF16) {
-                lo = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
-                hi = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+              float v[4];
+              static_for<4>([&](auto qc) {
+                constexpr int q = decltype(qc)::value;
+                if constexpr (MODE == GM_I8) {
+                  v[q] = ((float)acc[0][i][j][4 * g + q] * rs[i]) * cs[j][g][q];
+                } else if constexpr (EPI == GE_SWIGLU) {
+                  const float gt =
+                      f16_bits_to_f32(f32_to_f16_bits(acc[0][i][j][4 * g + q] * cs[j][g][q]));
+                  const float up =
+                      f16_bits_to_f32(f32_to_f16_bits(acc[NB - 1][i][j][4 * g + q] * cs2[j][g][q]));
+                  const float sg = gt / (1.0f + fast_exp(-gt));
+                  v[q] = sg * up;
+                } else {
+                  const float t = acc[0][i][j][4 * g + q] * cs[j][g][q];
+                  v[q] = has_res ? t + res[j][ii][g][q] : t;
+                }
+              });
+              if constexpr (ES == 4) {
+                *reinterpret_cast<v4f*>(dst) = v4f{v[0], v[1], v[2], v[3]};
+              } else if constexpr (OK == DT_BF16) {
+                const uint32_t lo = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+                const uint32_t hi = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+                *reinterpret_cast<v2i*>(dst) = v2i{(int)lo, (int)hi};
               } else {
-                lo = (uint32_t)f32_to_f16_bits(v[0]) | ((uint32_t)f32_to_f16_bits(v[1]) << 16);
-                hi = (uint32_t)f32_to_f16_bits(v[2]) | ((uint32_t)f32_to_f16_bits(v[3]) << 16);
+                const uint32_t lo =
+                    (uint32_t)f32_to_f16_bits(v[0]) | ((uint32_t)f32_to_f16_bits(v[1]) << 16);
+                const uint32_t hi =
+                    (uint32_t)f32_to_f16_bits(v[2]) | ((uint32_t)f32_to_f16_bits(v[3]) << 16);
+                *reinterpret_cast<v2i*>(dst) = v2i{(int)lo, (int)hi};
               }
-              *reinterpret_cast<v2i*>(dst) = v2i{(int)lo, (int)hi};
             }
           });
         });
@@ -502,8 +535,12 @@ gemm_kernel(GemmArgs p) {
       });
     });
   };
-  if (odt == DT_F32 || odt == DT_I32) epilogue(std::integral_constant<int, 4>{});
-  else epilogue(std::integral_constant<int, 2>{});
+  switch (p.out_dtype) {
+    case DT_I32: if constexpr (MODE == GM_I8) epilogue(std::integral_constant<int, DT_I32>{}); break;
+    case DT_F32: if constexpr (EPI != GE_SWIGLU) epilogue(std::integral_constant<int, DT_F32>{}); break;
+    case DT_BF16: epilogue(std::integral_constant<int, DT_BF16>{}); break;
+    default: epilogue(std::integral_constant<int, DT_F16>{}); break;
+  }
 }
 
 // ---------------------------------------------------------------------------
