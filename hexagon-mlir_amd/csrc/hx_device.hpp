@@ -60,6 +60,14 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
   f16 h = (f16)f;
   return __builtin_bit_cast(uint16_t, h);
 }
+// Two binary32 values -> packed fp16 pair (low = a), each rounded to nearest
+// even: one v_cvt_pk_f16_f32.  The asm keeps a and b opaque for the same
+// reason as in f32_to_f16_bits.
+__device__ __forceinline__ uint32_t f32x2_to_f16x2(float a, float b) {
+  asm("" : "+v"(a), "+v"(b));
+  typedef _Float16 hf2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, hf2{(f16)a, (f16)b});
+}
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
   return (float)__builtin_bit_cast(f16, h);
 }

@@ -137,6 +137,10 @@ gemm_kernel(GemmArgs p) {
   // Two stages as two distinct arrays: the compiler can then see that a
   // direct load into one stage never aliases the reads of the other.
   __shared__ __attribute__((aligned(1024))) char st0[STAGE];
+  // per-row / per-column scales of this tile, fetched in the prologue
+  // (SC_ROWS floats each: one 1 KiB direct load covers 256)
+  constexpr int SC_ROWS = (BM > BN ? BM : BN) < 256 ? 256 : (BM > BN ? BM : BN);
+  __shared__ __attribute__((aligned(1024))) float scl[(1 + NB) * SC_ROWS];
   __shared__ __attribute__((aligned(1024))) char st1[STAGE];
 
   const int tid = threadIdx.x;
@@ -335,6 +339,22 @@ gemm_kernel(GemmArgs p) {
   // final two stages are always (st0, st1) and the steady loop needs no
   // remainder; with an odd stage count stage 0 goes to st1 and is peeled.
   // (The fast path requires nk >= 2.)
+  // The tile's scales go straight to LDS ahead of the first stage (wave 0:
+  // row scales, 1: column scales, 2: second column scales): issued first,
+  // they are covered by the prologue's wait for stage 0.  A null scale
+  // pointer gives an empty buffer range, so its slot reads as zeros.
+  {
+    static_assert(NW >= 2 + NB - 1, "one wave per scale vector");
+    auto sc_rsrc = [](const float* ptr, int64_t first, int64_t n) {
+      return __builtin_amdgcn_make_buffer_rsrc((void*)(ptr ? ptr + first : nullptr), 0,
+                                               ptr ? (int)((n - first) * 4) : 0, 0x00020000);
+    };
+    if (wave == 0)
+      dma16(sc_rsrc(MODE == GM_I8 ? p.row_scale : nullptr, m0, p.M), (char*)scl, lane * 16u, 0u);
+    if (wave == 1) dma16(sc_rsrc(p.col_scale, n0, p.N), (char*)(scl + SC_ROWS), lane * 16u, 0u);
+    if constexpr (NB == 2)
+      if (wave == 2) dma16(sc_rsrc(p.col_scale2, n0, p.N), (char*)(scl + 2 * SC_ROWS), lane * 16u, 0u);
+  }
   const bool odd = nk & 1;
   if (odd) {
     dma_stage(st1, 0, std::true_type{});
@@ -374,23 +394,22 @@ gemm_kernel(GemmArgs p) {
   // consecutive bytes and a wave store covers whole rows.
   //
   // The epilogue is straight-line code: the output type is a compile-time
-  // variant chosen once, every scale is fetched up front with branch-free
-  // buffer loads (an absent scale reads as 1.0; multiplying by 1.0 is exact,
-  // so the result equals skipping the multiply), and residual reads use
-  // clamped in-bounds indices (values for rows/columns past the edge are
-  // never stored).  A per-element test of the output type or of an optional
+  // variant chosen once, the scales come from LDS (fetched in the prologue;
+  // an absent scale reads as 1.0, and multiplying by 1.0 is exact, so the
+  // result equals skipping the multiply), and residual reads use clamped
+  // in-bounds indices (values for rows/columns past the edge are never
+  // stored).  A per-element test of the output type or of an optional
   // argument would put a branch, and a wait for every load behind it, on
-  // each element.  All loads of a pass (scales, residual) are issued before
-  // any store of that pass, so a residual that aliases C is read first.
+  // each element.  The block goes out in passes of 32 rows, so the
+  // conversion of one pass overlaps the stores of the previous one; all
+  // loads of a pass (residual) are issued before any store of that pass, so
+  // a residual that aliases C is read first.  The output stores are
+  // non-temporal: the tile is written once and not read back, and streamed
+  // stores drain to memory as they go instead of waiting in L2 for the
+  // end-of-kernel write-back.
   lds_barrier();  // every wave is done reading the stage buffers
   const int64_t row0w = m0 + wm * WTM;
   const int64_t col0w = n0 + wn * WTN;
-  auto f32_rsrc = [](const float* ptr, int64_t n) {
-    return __builtin_amdgcn_make_buffer_rsrc((void*)ptr, 0, ptr ? (int)(n * 4) : 0, 0x00020000);
-  };
-  const __amdgpu_buffer_rsrc_t r_rs = f32_rsrc(MODE == GM_I8 ? p.row_scale : nullptr, p.M);
-  const __amdgpu_buffer_rsrc_t r_cs = f32_rsrc(p.col_scale, p.N);
-  const __amdgpu_buffer_rsrc_t r_cs2 = f32_rsrc(NB == 2 ? p.col_scale2 : nullptr, p.N);
   const bool has_rs = MODE == GM_I8 && p.row_scale != nullptr;
   const bool has_cs = p.col_scale != nullptr;
   const bool has_cs2 = NB == 2 && p.col_scale2 != nullptr;
@@ -398,27 +417,16 @@ gemm_kernel(GemmArgs p) {
   v4f cs[TN][4], cs2[TN][4];
   static_for<TM>([&](auto ic) {
     constexpr int i = decltype(ic)::value;
-    const uint32_t row = (uint32_t)(row0w + i * 32 + lrow);
-    rs[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_rs, (int)(row * 4u), 0, 0));
+    rs[i] = has_rs ? scl[wm * WTM + i * 32 + lrow] : 1.f;
   });
   static_for<TN>([&](auto jc) {
     constexpr int j = decltype(jc)::value;
     static_for<4>([&](auto gc) {
       constexpr int g = decltype(gc)::value;
-      const uint32_t col = (uint32_t)(col0w + j * 32 + 8 * g + 4 * lg);
-      cs[j][g] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(r_cs, (int)(col * 4u), 0, 0));
+      const int c = wn * WTN + j * 32 + 8 * g + 4 * lg;
+      cs[j][g] = has_cs ? *reinterpret_cast<const v4f*>(scl + SC_ROWS + c) : v4f{1.f, 1.f, 1.f, 1.f};
       if constexpr (NB == 2)
-        cs2[j][g] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(r_cs2, (int)(col * 4u), 0, 0));
-    });
-  });
-  static_for<TM>([&](auto ic) { rs[decltype(ic)::value] = has_rs ? rs[decltype(ic)::value] : 1.f; });
-  static_for<TN>([&](auto jc) {
-    constexpr int j = decltype(jc)::value;
-    static_for<4>([&](auto gc) {
-      constexpr int g = decltype(gc)::value;
-      if (!has_cs) cs[j][g] = v4f{1.f, 1.f, 1.f, 1.f};
-      if constexpr (NB == 2)
-        if (!has_cs2) cs2[j][g] = v4f{1.f, 1.f, 1.f, 1.f};
+        cs2[j][g] = has_cs2 ? *reinterpret_cast<const v4f*>(scl + 2 * SC_ROWS + c) : v4f{1.f, 1.f, 1.f, 1.f};
     });
   });
   const bool has_res = MODE != GM_I8 && EPI != GE_SWIGLU && p.res != nullptr;
@@ -430,7 +438,7 @@ gemm_kernel(GemmArgs p) {
     constexpr int RB = WTN * ES;                 // bytes per row of the wave block
     constexpr int PER_ARRAY = (NW + 1) / 2;      // wave regions per stage buffer
     constexpr int REGION = STAGE / PER_ARRAY;
-    constexpr int TMP = (TM * 32 * RB <= REGION) ? TM : ((TM / 2) * 32 * RB <= REGION ? TM / 2 : 1);
+    constexpr int TMP = 1;  // 32-row passes
     static_assert(TMP >= 1 && TM % TMP == 0 && TMP * 32 * RB <= REGION, "epilogue region");
     static_assert(RB >= 64 && (1024 % RB == 0 || RB % 1024 == 0), "epilogue row bytes");
     auto swz_out = [](int row) -> int {
@@ -507,11 +515,8 @@ gemm_kernel(GemmArgs p) {
                 const uint32_t hi = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
                 *reinterpret_cast<v2i*>(dst) = v2i{(int)lo, (int)hi};
               } else {
-                const uint32_t lo =
-                    (uint32_t)f32_to_f16_bits(v[0]) | ((uint32_t)f32_to_f16_bits(v[1]) << 16);
-                const uint32_t hi =
-                    (uint32_t)f32_to_f16_bits(v[2]) | ((uint32_t)f32_to_f16_bits(v[3]) << 16);
-                *reinterpret_cast<v2i*>(dst) = v2i{(int)lo, (int)hi};
+                *reinterpret_cast<v2i*>(dst) =
+                    v2i{(int)f32x2_to_f16x2(v[0], v[1]), (int)f32x2_to_f16x2(v[2], v[3])};
               }
             }
           });
@@ -529,7 +534,7 @@ gemm_kernel(GemmArgs p) {
         const int64_t col = col0w + c * EPC;
         if (row < p.M) {
           char* out = reinterpret_cast<char*>(p.c) + (row * p.ldc + col) * ES;
-          if (col + EPC <= p.N) *reinterpret_cast<v4i*>(out) = d;
+          if (col + EPC <= p.N) __builtin_nontemporal_store(d, reinterpret_cast<v4i*>(out));
           else if (ES == 2 && col < p.N) *reinterpret_cast<v2i*>(out) = v2i{d[0], d[1]};
         }
       });
