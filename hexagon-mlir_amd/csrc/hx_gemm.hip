@@ -110,6 +110,18 @@ __device__ __forceinline__ v4f load4(const void* p, int dt, int64_t idx) {
              bf16_to_f32((uint16_t)(hi >> 16))};
 }
 
+// Scheduling recipe for the step that follows a stage barrier: NREAD LDS
+// reads first, then NMF MFMAs with the NVM direct loads spread after them.
+template <int NREAD, int NMF, int NVM>
+__device__ __forceinline__ void interleave_reads_mfma_vmem() {
+  constexpr int PER = (NVM + NMF - 1) / NMF;  // loads after each MFMA
+  __builtin_amdgcn_sched_group_barrier(0x100, NREAD, 0);  // DS reads
+  static_for<NMF>([](auto) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // one MFMA
+    __builtin_amdgcn_sched_group_barrier(0x020, PER, 0);  // its share of the direct loads
+  });
+}
+
 template <int MODE, int BM, int BN, int WM, int WN, int EPI>
 __global__ void __launch_bounds__(64 * WM * WN)
 gemm_kernel(GemmArgs p) {
@@ -318,18 +330,32 @@ gemm_kernel(GemmArgs p) {
     constexpr bool LAST = decltype(lastc)::value;
     static_for<4>([&](auto ksc) {
       constexpr int ks = decltype(ksc)::value;
-      if constexpr (ks < 3) {
-        read_frags(cur, std::integral_constant<int, ks + 1>{});
-      } else if constexpr (!LAST) {
+      if constexpr (ks == 3 && !LAST && DMA != 0) {
+        // After the barrier: the next stage's first fragment reads, then the
+        // direct loads of stage kt+2 alternating with this step's MFMAs, so
+        // the MFMA pipe keeps running while the loads are issued (issued as
+        // one burst, they stall the wave on the memory queue with its MFMAs
+        // stuck behind them).
         wait_vm<0>();
         lds_barrier();
+        read_frags(nxt, std::integral_constant<int, 0>{});
         if constexpr (DMA == 1) dma_stage(cur, kt + 2, std::false_type{});
         if constexpr (DMA == 2) dma_stage(cur, kt + 2, std::true_type{});
-        read_frags(nxt, std::integral_constant<int, 0>{});
+        mfmas(ksc);
+        interleave_reads_mfma_vmem<TM + NB * TN, NB * TN * TM, P>();
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+        if constexpr (ks < 3) {
+          read_frags(cur, std::integral_constant<int, ks + 1>{});
+        } else if constexpr (!LAST) {
+          wait_vm<0>();
+          lds_barrier();
+          read_frags(nxt, std::integral_constant<int, 0>{});
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(ksc);
+        __builtin_amdgcn_sched_barrier(0);
       }
-      __builtin_amdgcn_sched_barrier(0);
-      mfmas(ksc);
-      __builtin_amdgcn_sched_barrier(0);
     });
   };
   typedef std::integral_constant<int, 0> NoDma;
@@ -413,22 +439,15 @@ gemm_kernel(GemmArgs p) {
   const bool has_rs = MODE == GM_I8 && p.row_scale != nullptr;
   const bool has_cs = p.col_scale != nullptr;
   const bool has_cs2 = NB == 2 && p.col_scale2 != nullptr;
-  float rs[TM];
-  v4f cs[TN][4], cs2[TN][4];
-  static_for<TM>([&](auto ic) {
-    constexpr int i = decltype(ic)::value;
-    rs[i] = has_rs ? scl[wm * WTM + i * 32 + lrow] : 1.f;
-  });
-  static_for<TN>([&](auto jc) {
-    constexpr int j = decltype(jc)::value;
-    static_for<4>([&](auto gc) {
-      constexpr int g = decltype(gc)::value;
-      const int c = wn * WTN + j * 32 + 8 * g + 4 * lg;
-      cs[j][g] = has_cs ? *reinterpret_cast<const v4f*>(scl + SC_ROWS + c) : v4f{1.f, 1.f, 1.f, 1.f};
-      if constexpr (NB == 2)
-        cs2[j][g] = has_cs2 ? *reinterpret_cast<const v4f*>(scl + 2 * SC_ROWS + c) : v4f{1.f, 1.f, 1.f, 1.f};
-    });
-  });
+  // scale of sub-tile row i / columns (j, g) of this lane, read from LDS
+  // where it is used (holding a whole wave block's scales in registers
+  // would cost 16 registers per sub-tile column)
+  auto row_scale_of = [&](int i) -> float { return has_rs ? scl[wm * WTM + i * 32 + lrow] : 1.f; };
+  auto col_scale_of = [&](int j, int g, int which) -> v4f {
+    const bool has = which ? has_cs2 : has_cs;
+    const int c = wn * WTN + j * 32 + 8 * g + 4 * lg;
+    return has ? *reinterpret_cast<const v4f*>(scl + (1 + which) * SC_ROWS + c) : v4f{1.f, 1.f, 1.f, 1.f};
+  };
   const bool has_res = MODE != GM_I8 && EPI != GE_SWIGLU && p.res != nullptr;
 
   // OK: output kind (DT_I32 / DT_F32 / DT_F16 / DT_BF16), a compile-time value
@@ -449,39 +468,37 @@ gemm_kernel(GemmArgs p) {
     char* region = (wave < PER_ARRAY ? st0 : st1) + (wave % PER_ARRAY) * (TMP * 32 * RB);
     static_for<TM / TMP>([&](auto pc) {
       constexpr int pp = decltype(pc)::value;
-      // residual of this pass (float GE_STORE only), all of it before any store
-      v4f res[TN][TMP][4];
-      if constexpr (MODE != GM_I8 && EPI != GE_SWIGLU) {
-        if (has_res) {
-          static_for<TN>([&](auto jc) {
-            constexpr int j = decltype(jc)::value;
-            static_for<TMP>([&](auto ic) {
-              constexpr int ii = decltype(ic)::value;
-              static_for<4>([&](auto gc) {
-                constexpr int g = decltype(gc)::value;
-                const int64_t row = min(row0w + (pp * TMP + ii) * 32 + lrow, p.M - 1);
-                const int64_t col = min(col0w + j * 32 + 8 * g + 4 * lg, p.N - 4);
-                res[j][ii][g] = load4(p.res, p.res_dtype, row * p.ldr + col);
-              });
-            });
-          });
-        } else {
-          static_for<TN>([&](auto jc) {
-            static_for<TMP>([&](auto ic) {
-              static_for<4>([&](auto gc) {
-                res[decltype(jc)::value][decltype(ic)::value][decltype(gc)::value] = v4f{0.f, 0.f, 0.f, 0.f};
-              });
-            });
-          });
-        }
-      }
       // 1) this pass's sub-tile rows -> LDS, in the output type
       static_for<TN>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
+        // residual of sub-tile column j of this pass (float GE_STORE only)
+        v4f res[TMP][4];
+        if constexpr (MODE != GM_I8 && EPI != GE_SWIGLU) {
+          static_for<TMP>([&](auto ic) {
+            constexpr int ii = decltype(ic)::value;
+            static_for<4>([&](auto gc) {
+              constexpr int g = decltype(gc)::value;
+              if (has_res) {
+                const int64_t row = min(row0w + (pp * TMP + ii) * 32 + lrow, p.M - 1);
+                const int64_t col = min(col0w + j * 32 + 8 * g + 4 * lg, p.N - 4);
+                res[ii][g] = load4(p.res, p.res_dtype, row * p.ldr + col);
+              } else {
+                res[ii][g] = v4f{0.f, 0.f, 0.f, 0.f};
+              }
+            });
+          });
+        }
+        v4f cs[4], cs2[4];
+        static_for<4>([&](auto gc) {
+          constexpr int g = decltype(gc)::value;
+          cs[g] = col_scale_of(j, g, 0);
+          if constexpr (NB == 2) cs2[g] = col_scale_of(j, g, 1);
+        });
         static_for<TMP>([&](auto ic) {
           constexpr int ii = decltype(ic)::value;
           constexpr int i = pp * TMP + ii;
           const int rl = ii * 32 + lrow;
+          const float rs = row_scale_of(i);
           static_for<4>([&](auto gc) {
             constexpr int g = decltype(gc)::value;
             const int byte = (j * 32 + 8 * g + 4 * lg) * ES;
@@ -495,17 +512,17 @@ gemm_kernel(GemmArgs p) {
               static_for<4>([&](auto qc) {
                 constexpr int q = decltype(qc)::value;
                 if constexpr (MODE == GM_I8) {
-                  v[q] = ((float)acc[0][i][j][4 * g + q] * rs[i]) * cs[j][g][q];
+                  v[q] = ((float)acc[0][i][j][4 * g + q] * rs) * cs[g][q];
                 } else if constexpr (EPI == GE_SWIGLU) {
                   const float gt =
-                      f16_bits_to_f32(f32_to_f16_bits(acc[0][i][j][4 * g + q] * cs[j][g][q]));
+                      f16_bits_to_f32(f32_to_f16_bits(acc[0][i][j][4 * g + q] * cs[g][q]));
                   const float up =
-                      f16_bits_to_f32(f32_to_f16_bits(acc[NB - 1][i][j][4 * g + q] * cs2[j][g][q]));
+                      f16_bits_to_f32(f32_to_f16_bits(acc[NB - 1][i][j][4 * g + q] * cs2[g][q]));
                   const float sg = gt / (1.0f + fast_exp(-gt));
                   v[q] = sg * up;
                 } else {
-                  const float t = acc[0][i][j][4 * g + q] * cs[j][g][q];
-                  v[q] = has_res ? t + res[j][ii][g][q] : t;
+                  const float t = acc[0][i][j][4 * g + q] * cs[g][q];
+                  v[q] = has_res ? t + res[ii][g][q] : t;
                 }
               });
               if constexpr (ES == 4) {
