@@ -236,7 +236,9 @@ __global__ void __launch_bounds__(256) row_vec_kernel(RowArgs a) {
   __shared__ float red[4];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // wave index and row as provably uniform values: the row's buffer
+  // descriptors below are built from them and must live in scalar registers
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int rows_per_block = 4 / WPR;
   const int wave_in_row = (WPR == 1) ? 0 : wave;
   const int64_t row = (int64_t)blockIdx.x * rows_per_block + (WPR == 1 ? wave : 0);
@@ -245,28 +247,35 @@ __global__ void __launch_bounds__(256) row_vec_kernel(RowArgs a) {
   const S* xr = reinterpret_cast<const S*>(a.x) + row * a.ldx;
   S* yr = reinterpret_cast<S*>(a.y) + row * a.ldy;
 
-  v4u raw[VPL];
+  // Every load is a branch-free buffer load over the row (x) or over
+  // gamma / beta: chunks past the row end read zero from the descriptor's
+  // range.  A load behind a per-lane test would make the compiler wait for
+  // it at the join -- the row's loads and gamma's would then be serialised.
+  // Gamma / beta are fetched with the row, so their latency hides under the
+  // row's own loads rather than stalling the write-back after the reduction.
+  const S* wp = reinterpret_cast<const S*>(a.w);
+  const S* bp = reinterpret_cast<const S*>(a.b);
+  const int row_bytes = (int)(cols * (int64_t)sizeof(S));
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)xr, 0, row_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rw =
+      __builtin_amdgcn_make_buffer_rsrc((void*)wp, 0, wp ? row_bytes : 0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rb =
+      __builtin_amdgcn_make_buffer_rsrc((void*)bp, 0, bp ? row_bytes : 0, 0x00020000);
+  constexpr int kNT = 2;  // cache policy: non-temporal (each row is streamed once)
+  v4u raw[VPL], wv[VPL], bv[VPL];
   bool ok[VPL];
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int64_t c0 = ((int64_t)(i * WPR + wave_in_row) * 64 + lane) * EV;
     ok[i] = c0 < cols;
-    raw[i] = ok[i] ? __builtin_nontemporal_load(reinterpret_cast<const v4u*>(xr + c0))
-                   : v4u{0u, 0u, 0u, 0u};
-  }
-  // gamma / beta are fetched with the row, so their latency hides under the
-  // row's own loads rather than stalling the write-back after the reduction
-  const S* wp = reinterpret_cast<const S*>(a.w);
-  const S* bp = reinterpret_cast<const S*>(a.b);
-  v4u wv[VPL], bv[VPL];
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    const int64_t c0 = ((int64_t)(i * WPR + wave_in_row) * 64 + lane) * EV;
+    const int off = (int)(c0 * (int64_t)sizeof(S));
+    raw[i] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, kNT));
     wv[i] = v4u{0u, 0u, 0u, 0u};
     bv[i] = v4u{0u, 0u, 0u, 0u};
     if constexpr (OP != ROW_SOFTMAX) {
-      if (wp && ok[i]) wv[i] = *reinterpret_cast<const v4u*>(wp + c0);
-      if (bp && ok[i]) bv[i] = *reinterpret_cast<const v4u*>(bp + c0);
+      wv[i] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 0));
+      if constexpr (OP == ROW_LAYERNORM)
+        bv[i] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 0));
     }
   }
 
