@@ -8,12 +8,15 @@ hx_gemm_i8 on inputs already resident in HBM (B as the resident K-contiguous
 weight image).  value = 2*M*N*K / step time, in TOPS (10^12 int8 ops/s).
 
 Also reported (``secondary``), each against its roofline:
+  * the same int8 product with the exact int32 result stored (no dequant);
   * W8A16 decode GEMV, M in {1, 4, 16}, N=11008, K=4096, GB/s,
     rotating over >512 MB of weight copies so the 256 MB MALL cannot serve it;
   * softmax and RMSNorm on fp16 [8192 x 4096], GB/s, rotating
     over 6 input/output sets (768 MB);
   * fp16 GEMM 256^3 (configs[0]) latency;
-  * SwiGLU FFN tokens=2048, hidden=4096, inter=11008, TFLOP/s.
+  * SwiGLU FFN tokens=2048, hidden=4096, inter=11008 (configs[4]), TFLOP/s;
+  * the fused attention forward (the reference test's shape and a multi-head
+    one, plain and causal), TFLOP/s.
 
 The CPU baseline is the oracle's restatement of the reference's HVX lowering
 (the (i,k,j) int32 loop of ScheduleMatmulForHVX plus the dequant), timed on
@@ -311,6 +314,32 @@ def bench_rows(hx, iters: int = 60):
     return out
 
 
+def bench_gemm_i8_i32(hx, inputs, iters: int = 50):
+    """The headline product with the exact int32 result stored (C 67 MB, no
+    dequant): same operands and tile config as the headline, sampled rows
+    checked bit-exact against the oracle."""
+    import numpy as np
+    import torch
+    import oracle
+    a, bt, _, _ = inputs
+    M, K = a.shape
+    N = bt.shape[0]
+    c = torch.empty((M, N), dtype=torch.int32, device=a.device)
+    step = hx.bind_gemm_i8(a, bt, c, b_layout="nk")
+    step()
+    ev_ms, fed = event_timed([step], iters)
+    tops = 2.0 * M * N * K / (ev_ms * 1e-3) / 1e12
+    rows = np.array([0, 2047, 4095])
+    want = oracle.gemm_i8_i32(a[rows].cpu().numpy(), bt.cpu().numpy(), b_trans=True)
+    exact = bool(np.array_equal(c[rows].cpu().numpy(), want))
+    cfg_idx = hx.config_lookup(1, M, N, K)
+    return {"workload": f"int8 GEMM M=N=K={M}, exact int32 output (no dequant)",
+            "value": round(tops, 1), "unit": "TOPS", "us_per_call": round(ev_ms * 1e3, 3),
+            "kernel": hx.config_get(1, cfg_idx)["name"] if cfg_idx >= 0 else "generic",
+            "roofline": roofline("mfma", tops, PEAK_INT8_TOPS, "TFLOP/s"),
+            "parity": {"int32_sampled_rows_bitexact": exact}, "queue_fed": fed}
+
+
 def bench_gemm_f16_small(hx, iters: int = 200):
     import torch
     dev = torch.device("cuda:0")
@@ -530,6 +559,8 @@ def main() -> int:
         f"{h['kernel_ms']*1e3:.1f} us/launch, parity={h['parity_sampled_rows_bitexact']}")
     secondary = []
     if args.only == "all":
+        log("[bench] int8 GEMM 4096^3, int32 out")
+        secondary.append(bench_gemm_i8_i32(hx, h["inputs"]))
         log("[bench] W8A16 GEMV")
         secondary += bench_gemv(hx, tune=tune)
         log("[bench] row ops")
