@@ -62,6 +62,47 @@ def test_gemm_i8_dequant_f16_bitexact(hx, dev, shape):
         f"dequant differs in {int((got.view(np.uint16) != want.view(np.uint16)).sum())} elements"
 
 
+@pytest.mark.parametrize("which", ["row", "col", "none"])
+@pytest.mark.parametrize("shape", [(300, 260, 512), (256, 256, 256)], ids=lambda s: "x".join(map(str, s)))
+def test_gemm_i8_one_sided_scales(hx, dev, shape, which):
+    """Dequant with only the row scale, only the column scale, or neither: an
+    absent scale multiplies by nothing (the epilogue multiplies by 1.0, which is
+    exact), so each case is bit-exact against the oracle's own one-sided form."""
+    import torch
+    M, N, K = shape
+    a, b = i8((M, K), 31), i8((K, N), 32)
+    sa = rng(33).uniform(0.001, 0.02, M).astype(np.float32) if which == "row" else None
+    sb = rng(34).uniform(0.001, 0.02, N).astype(np.float32) if which == "col" else None
+    c = hx.gemm_i8(to_dev(a, dev), to_dev(b, dev),
+                   row_scale=None if sa is None else to_dev(sa, dev),
+                   col_scale=None if sb is None else to_dev(sb, dev), out_dtype=torch.float16)
+    want = oracle.dequant_i32_f16(oracle.gemm_i8_i32(a, b), sa, sb)
+    got = to_np(c)
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16)), \
+        f"{which}: {int((got.view(np.uint16) != want.view(np.uint16)).sum())} differ"
+
+
+@pytest.mark.parametrize("out", ["f32", "bf16"])
+def test_gemm_i8_dequant_wide_and_bf16_out(hx, dev, out):
+    """The dequant epilogue's other output types: ((float)acc * sa[i]) * sb[j]
+    in binary32 (numpy float32 products round the same way), stored as f32 or
+    rounded to bf16 (RNE) -- bit-exact either way."""
+    import torch
+    M, N, K = 272, 392, 640
+    a, b = i8((M, K), 35), i8((K, N), 36)
+    sa = rng(37).uniform(0.001, 0.02, M).astype(np.float32)
+    sb = rng(38).uniform(0.001, 0.02, N).astype(np.float32)
+    c = hx.gemm_i8(to_dev(a, dev), to_dev(b, dev), row_scale=to_dev(sa, dev), col_scale=to_dev(sb, dev),
+                   out_dtype=torch.float32 if out == "f32" else torch.bfloat16)
+    acc = oracle.gemm_i8_i32(a, b).astype(np.float32)
+    want32 = (acc * sa[:, None]) * sb[None, :]
+    got = to_np(c)
+    if out == "f32":
+        assert np.array_equal(got.view(np.uint32), want32.view(np.uint32))
+    else:
+        assert np.array_equal(got, bf16_from_f32(want32))
+
+
 def test_gemm_i8_extremes_closed_form(hx, dev):
     """All +127 times all -127: every entry is -K*127^2 (no int32 overflow
     at K=4096: 66,064,384 < 2^31); identity B reproduces A exactly."""
