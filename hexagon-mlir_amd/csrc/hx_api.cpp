@@ -313,9 +313,9 @@ static int resolve_gemv(int64_t M, int64_t N, int64_t K, bool* was_pinned = null
   // untuned choice from the MI355X sweep (N = 11008, K = 4096): LDS-staged
   // activations and one column tile per workgroup for M <= 4 (the launcher
   // falls back to the register-staged base config when the rows do not fit
-  // in LDS), four tiles (activation fragments reused 4x) over 8 waves for
-  // larger M
-  return M <= 4 ? 5 : 2;
+  // in LDS), four tiles (activation fragments reused 4x) over 8 waves with
+  // every K chunk in flight at once for larger M
+  return M <= 4 ? 5 : 10;
 }
 
 static int run_gemm(int op, GemmArgs& a, hipStream_t s, const PlanCtx& ctx) {

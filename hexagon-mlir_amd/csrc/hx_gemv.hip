@@ -337,6 +337,10 @@ static const GemvPackedEntry kGemvPacked[] = {
     // 16 waves over K keep the 4-tile activation reuse of ct4 while putting
     // 4x more waves (and weight bytes in flight) on the CUs it occupies
     {{4, 16, "packed_ct4_kw16", 0, 8}, &gemv_packed_one<4, 16, 2, false>},
+    // four tiles with every K chunk of K = 4096 in flight at once (one round
+    // trip to memory) over 16 or 8 waves
+    {{4, 16, "packed_ct4_kw16_c4", 0, 9}, &gemv_packed_one<4, 16, 4, false>},
+    {{4, 8, "packed_ct4_kw8_c8", 0, 10}, &gemv_packed_one<4, 8, 8, false>},
 };
 int gemv_packed_config_count() { return (int)(sizeof(kGemvPacked) / sizeof(kGemvPacked[0])); }
 const GemvConfig* gemv_packed_config(int idx) {
