@@ -40,15 +40,15 @@ namespace hx {
 
 template <int MODE> struct ModeTraits;
 template <> struct ModeTraits<GM_I8> {
-  static constexpr int EA = 1, EB = 1, BK = 128, BROW = 128;
+  static constexpr int EA = 1, EB = 1;  // operand element bytes
   typedef v16i Acc;
 };
 template <> struct ModeTraits<GM_F16> {
-  static constexpr int EA = 2, EB = 2, BK = 64, BROW = 128;
+  static constexpr int EA = 2, EB = 2;
   typedef v16f Acc;
 };
 template <> struct ModeTraits<GM_BF16> {
-  static constexpr int EA = 2, EB = 2, BK = 64, BROW = 128;
+  static constexpr int EA = 2, EB = 2;
   typedef v16f Acc;
 };
 template <> struct ModeTraits<GM_W8> {
@@ -122,20 +122,29 @@ __device__ __forceinline__ void interleave_reads_mfma_vmem() {
   });
 }
 
-template <int MODE, int BM, int BN, int WM, int WN, int EPI>
-__global__ void __launch_bounds__(64 * WM * WN)
+// SB: bytes of A per row in one K stage (128; 64 halves the LDS so that two
+// 4-wave workgroups share a CU with independent stage barriers -- measured
+// at 4096^3 as 76 us against 59 us for the 8-wave 256x256 tile, so no table
+// entry uses it).  MINW: waves per SIMD the register budget must allow (2
+// caps a wave at 256 registers).
+template <int MODE, int BM, int BN, int WM, int WN, int EPI, int SB = 128, int MINW = 1>
+__global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(MINW, 8)))
 gemm_kernel(GemmArgs p) {
   typedef ModeTraits<MODE> T;
   typedef typename T::Acc Acc;
+  static_assert(SB == 128 || (SB == 64 && MODE != GM_W8), "stage width");
   constexpr int NW = WM * WN;
   constexpr int NB = (EPI == GE_SWIGLU) ? 2 : 1;
-  constexpr int A_BYTES = BM * 128;
-  constexpr int B_BYTES = BN * T::BROW;
+  constexpr int BROW = (MODE == GM_W8) ? SB / 2 : SB;  // bytes of B per row in one stage
+  constexpr int KSTEPS = SB / 32;                      // MFMA k-steps per stage
+  constexpr int A_BYTES = BM * SB;
+  constexpr int B_BYTES = BN * BROW;
   constexpr int STAGE = A_BYTES + NB * B_BYTES;
   // 1 KiB direct-load blocks: 8 rows of a 128-byte row, or 16 of a 64-byte row
   constexpr int A_BLK = A_BYTES / 1024;
   constexpr int B_BLK = B_BYTES / 1024;
-  constexpr int B_RPB = 1024 / T::BROW;
+  constexpr int A_RPB = 1024 / SB;
+  constexpr int B_RPB = 1024 / BROW;
   constexpr int A_PER_W = A_BLK / NW;
   constexpr int B_PER_W = B_BLK / NW;
   constexpr int P = A_PER_W + NB * B_PER_W;  // direct loads per wave per stage
@@ -195,9 +204,10 @@ gemm_kernel(GemmArgs p) {
   // a wave-uniform offset (the instruction's scalar offset); the lane part
   // is a row offset plus the swizzled chunk, recomputed per block from the
   // block index rather than kept in registers.
-  const uint32_t a_lane_row = (uint32_t)(lane >> 3) * lda_b;
-  const uint32_t b_lane_row = (uint32_t)(T::BROW == 128 ? (lane >> 3) : (lane >> 2)) * ldb_b;
-  const int nk = (int)((p.K + T::BK - 1) / T::BK);
+  const uint32_t a_lane_row = (uint32_t)(SB == 128 ? (lane >> 3) : (lane >> 2)) * lda_b;
+  const uint32_t b_lane_row = (uint32_t)(BROW == 128 ? (lane >> 3) : (lane >> 2)) * ldb_b;
+  constexpr int BKE = SB / T::EA;  // elements of K per stage
+  const int nk = (int)((p.K + BKE - 1) / BKE);
   const uint32_t kb_bytes = (uint32_t)(p.K * T::EB);
 
   // Enqueue the direct loads of K-stage kt into `st`.  Only the last stage
@@ -205,23 +215,29 @@ gemm_kernel(GemmArgs p) {
   // MASK = false is for stages known not to be the last one.
   auto dma_stage = [&](char* st, int kt, auto maskc) {
     constexpr bool MASK = decltype(maskc)::value;
-    const uint32_t ka = (uint32_t)kt * 128u;
-    const uint32_t kb = (uint32_t)kt * T::BROW;
-    const bool tail = MASK && ka + 128u > ka_bytes;
+    const uint32_t ka = (uint32_t)kt * (uint32_t)SB;
+    const uint32_t kb = (uint32_t)kt * (uint32_t)BROW;
+    const bool tail = MASK && ka + (uint32_t)SB > ka_bytes;
     static_for<A_PER_W>([&](auto ic) {
       const int blk = wave + decltype(ic)::value * NW;
-      // row = 8*blk + lane/8, so swz128(row) = (lane/8 ^ blk) & 7
-      const uint32_t kc = (uint32_t)(((lane & 7) ^ (lane >> 3) ^ blk) & 7) * 16u;
+      uint32_t kc;
+      if constexpr (SB == 128) {
+        // row = 8*blk + lane/8, so swz128(row) = (lane/8 ^ blk) & 7
+        kc = (uint32_t)(((lane & 7) ^ (lane >> 3) ^ blk) & 7) * 16u;
+      } else {
+        const int row = blk * 16 + (lane >> 2);
+        kc = (uint32_t)((lane & 3) ^ swz64(row)) * 16u;
+      }
       uint32_t off = a_lane_row + kc + ka;
       if (tail && ka + kc >= ka_bytes) off = 0x80000000u;
-      dma16(ra, st + blk * 1024, off, (uint32_t)blk * 8u * lda_b);
+      dma16(ra, st + blk * 1024, off, (uint32_t)blk * (uint32_t)A_RPB * lda_b);
     });
     static_for<NB>([&](auto nbc) {
       constexpr int nb = decltype(nbc)::value;
       static_for<B_PER_W>([&](auto ic) {
         const int blk = wave + decltype(ic)::value * NW;
         uint32_t kc;
-        if constexpr (T::BROW == 128) {
+        if constexpr (BROW == 128) {
           kc = (uint32_t)(((lane & 7) ^ (lane >> 3) ^ blk) & 7) * 16u;
         } else {
           const int row = blk * 16 + (lane >> 2);
@@ -247,8 +263,8 @@ gemm_kernel(GemmArgs p) {
   const int lrow = lane & 31, lg = lane >> 5;
 
   // Operand fragments, double-buffered in registers: while the MFMAs of
-  // k-step ks run, the LDS reads of step ks+1 are in flight.  A stage is 4
-  // k-steps.  For W8 one 16-byte int8 B read covers two steps (it is widened
+  // k-step ks run, the LDS reads of step ks+1 are in flight.  A stage is
+  // KSTEPS k-steps.  For W8 one 16-byte int8 B read covers two steps (it is widened
   // to f16 half by half), so B is read on even steps into its own pair of
   // buffers, indexed by the step pair.
   v4i fa[2][TM];
@@ -261,10 +277,14 @@ gemm_kernel(GemmArgs p) {
     // k = 32*jp + 16*g + 8*h + (0..7) for lane group g, both operands, so
     // every k of the stage is summed exactly once)
     const int ca = (MODE != GM_W8) ? ks * 2 + lg : 4 * (ks >> 1) + 2 * lg + (ks & 1);
+    auto swz = [](int row) -> int {
+      if constexpr (SB == 128) return swz128(row);
+      else return swz64(row);
+    };
     static_for<TM>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
       const int row = wm * WTM + i * 32 + lrow;
-      fa[s][i] = *reinterpret_cast<const v4i*>(sa + row * 128 + ((ca ^ swz128(row)) << 4));
+      fa[s][i] = *reinterpret_cast<const v4i*>(sa + row * SB + ((ca ^ swz(row)) << 4));
     });
     if constexpr (MODE != GM_W8) {
       static_for<NB>([&](auto nbc) {
@@ -272,8 +292,8 @@ gemm_kernel(GemmArgs p) {
         static_for<TN>([&](auto jc) {
           constexpr int j = decltype(jc)::value;
           const int row = wn * WTN + j * 32 + lrow;
-          fb[s][nb][j] = *reinterpret_cast<const v4i*>(sa + A_BYTES + nb * B_BYTES + row * 128 +
-                                                       ((ca ^ swz128(row)) << 4));
+          fb[s][nb][j] = *reinterpret_cast<const v4i*>(sa + A_BYTES + nb * B_BYTES + row * SB +
+                                                       ((ca ^ swz(row)) << 4));
         });
       });
     } else if constexpr ((ks & 1) == 0) {
@@ -328,9 +348,9 @@ gemm_kernel(GemmArgs p) {
   auto stage_body = [&](char* cur, char* nxt, int kt, auto dmac, auto lastc) {
     constexpr int DMA = decltype(dmac)::value;
     constexpr bool LAST = decltype(lastc)::value;
-    static_for<4>([&](auto ksc) {
+    static_for<KSTEPS>([&](auto ksc) {
       constexpr int ks = decltype(ksc)::value;
-      if constexpr (ks == 3 && !LAST && DMA != 0) {
+      if constexpr (ks == KSTEPS - 1 && !LAST && DMA != 0) {
         // After the barrier: the next stage's first fragment reads, then the
         // direct loads of stage kt+2 alternating with this step's MFMAs, so
         // the MFMA pipe keeps running while the loads are issued (issued as
@@ -345,7 +365,7 @@ gemm_kernel(GemmArgs p) {
         interleave_reads_mfma_vmem<TM + NB * TN, NB * TN * TM, P>();
         __builtin_amdgcn_sched_barrier(0);
       } else {
-        if constexpr (ks < 3) {
+        if constexpr (ks < KSTEPS - 1) {
           read_frags(cur, std::integral_constant<int, ks + 1>{});
         } else if constexpr (!LAST) {
           wait_vm<0>();
@@ -660,10 +680,10 @@ __global__ void __launch_bounds__(256) gemm_generic_kernel(GemmArgs p) {
 // ---------------------------------------------------------------------------
 typedef void (*GemmLaunch)(const GemmArgs&, hipStream_t);
 
-template <int MODE, int BM, int BN, int WM, int WN, int EPI>
+template <int MODE, int BM, int BN, int WM, int WN, int EPI, int SB = 128, int MINW = 1>
 static void launch_one(const GemmArgs& a, hipStream_t s) {
   const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-  gemm_kernel<MODE, BM, BN, WM, WN, EPI><<<dim3((unsigned)tiles), dim3(64 * WM * WN), 0, s>>>(a);
+  gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW><<<dim3((unsigned)tiles), dim3(64 * WM * WN), 0, s>>>(a);
 }
 
 struct GemmEntry {
