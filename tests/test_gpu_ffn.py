@@ -43,3 +43,28 @@ def test_swiglu_ffn(hx, dev, T, H, I):
     assert_close(got, want, 2e-2, 2e-3, f"swiglu T={T}")
     rel = np.linalg.norm(got - want) / np.linalg.norm(want)
     assert rel < 2e-3, rel
+
+
+def test_swiglu_every_config(hx, dev):
+    """Every compiled configuration of the fused gate/up (SwiGLU epilogue)
+    GEMM family gives the oracle's FFN output (the autotuner may pick any)."""
+    T, H, I = 256, 512, 1376
+    wg, sg, wu, su, wd, sd = weights(H, I, 310)
+    x = rng(311).normal(0, 1, (T, H)).astype(np.float16)
+    gamma = rng(312).normal(1, 0.1, H).astype(np.float16)
+    want = oracle.swiglu_ffn(x, gamma, 1e-6, wg, sg, wu, su, wd, sd).astype(np.float32)
+    Wg = hx.ResidentWeight(to_dev(wg, dev), to_dev(sg, dev))
+    Wu = hx.ResidentWeight(to_dev(wu, dev), to_dev(su, dev))
+    Wd = hx.ResidentWeight(to_dev(wd, dev), to_dev(sd, dev))
+    n = hx.config_count(5)
+    assert n >= 2
+    try:
+        for cfg in range(n):
+            hx.config_select(5, T, I, H, cfg)
+            try:
+                got = to_np(hx.swiglu_ffn(to_dev(x, dev), to_dev(gamma, dev), 1e-6, Wg, Wu, Wd))
+            finally:
+                hx.config_select(5, T, I, H, -1)
+            assert_close(got.astype(np.float32), want, 2e-2, 2e-3, f"swiglu cfg {cfg}")
+    finally:
+        Wg.release(); Wu.release(); Wd.release()
