@@ -311,11 +311,12 @@ static int resolve_gemv(int64_t M, int64_t N, int64_t K, bool* was_pinned = null
   if (pin >= 0 && pin < gemv_packed_config_count()) return pin;
   (void)N; (void)K;
   // untuned choice from the MI355X sweep (N = 11008, K = 4096): LDS-staged
-  // activations and one column tile per workgroup for M <= 4 (the launcher
-  // falls back to the register-staged base config when the rows do not fit
-  // in LDS), four tiles (activation fragments reused 4x) over 8 waves with
-  // every K chunk in flight at once for larger M
-  return M <= 4 ? 5 : 10;
+  // activations and one column tile per workgroup for M <= 4 -- staged by
+  // direct-to-LDS loads for M <= 2, through registers for M = 3, 4 (the
+  // launcher falls back to the register-fragment base config when the rows
+  // do not fit in LDS) -- and four tiles (activation fragments reused 4x)
+  // over 8 waves with every K chunk in flight at once for larger M
+  return M <= 2 ? 11 : M <= 4 ? 5 : 10;
 }
 
 static int run_gemm(int op, GemmArgs& a, hipStream_t s, const PlanCtx& ctx) {

@@ -24,6 +24,10 @@
 
 namespace hx {
 
+// activation staging of the packed kernel: none (register fragments per
+// chunk), LDS filled through registers, LDS filled by direct-to-LDS loads
+enum GemvXStage : int { XS_NONE = 0, XS_REG = 1, XS_DMA = 2 };
+
 __device__ __forceinline__ v4i gv_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
@@ -143,9 +147,10 @@ __global__ void __launch_bounds__(256) gemv_w8a16_kernel(GemvArgs p) {
 // queued behind a wave's weight loads would hold back the whole
 // workgroup's compute (the LDS staging ends in a barrier) until its last
 // weight byte has arrived, leaving no overlap between compute and stream.
-template <int CT, int KW, int CPW, bool XL>
+template <int CT, int KW, int CPW, int XS>
 __global__ void __launch_bounds__(64 * KW) gemv_packed_kernel(GemvArgs p, const int8_t* packed,
                                                               int kchunks) {
+  constexpr bool XL = XS != XS_NONE;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, g = lane >> 4;
@@ -156,7 +161,6 @@ __global__ void __launch_bounds__(64 * KW) gemv_packed_kernel(GemvArgs p, const 
   const uint16_t* x = reinterpret_cast<const uint16_t*>(p.x);
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
   const int64_t kp = (int64_t)kchunks * 64;
-  const int64_t kps = kp + 8;  // row pitch: 16 bytes of padding spread the rows over the banks
 
   // Every global load below is a buffer load whose out-of-range offset
   // (0x80000000) reads zero, so no load sits behind a branch: a conditional
@@ -172,17 +176,27 @@ __global__ void __launch_bounds__(64 * KW) gemv_packed_kernel(GemvArgs p, const 
 #pragma unroll
   for (int c = 0; c < CT; ++c) acc[c] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  // XL staging walks the [M][kp] activation block as (row m, column block
-  // b): step r = m * cb + b covers the 16-byte chunks c = b * T + tid of row m
-  // (T threads, cb = ceil(kchunks * 8 / T) blocks per row), so m and b are
-  // workgroup-uniform and no per-lane division is needed.  The first XR
-  // steps go through registers ahead of the weight loads; any further ones
-  // (large M * K) are loaded after them.
+  // XL staging of the [M][kp] activation block into LDS, issued ahead of the
+  // weight stream.  Rows are XLP elements apart (kp rounded up to whole
+  // 1 KiB blocks, plus 8: a block never spills into the next row, and the
+  // 16-byte skew spreads the rows over the LDS banks); elements at or past K
+  // read zero.
+  //   XS_DMA: direct-to-LDS loads (no registers held, no copy); 1 KiB block
+  //     b = (row m, 512-element segment j) is loaded by wave b % KW.
+  //   XS_REG: the block is walked as (row m, column block b): step
+  //     r = m * cb + b covers the 16-byte chunks b * T + tid of row m (T
+  //     threads, cb blocks per row); the first XR steps go through registers
+  //     ahead of the weight loads, any further ones are loaded after them.
+  // Measured at N = 11008, K = 4096: DMA is faster for M = 1 (one load per
+  // wave), registers for M = 4 (the DMA's LDS writes delay the weight
+  // loads queued behind them).
+  const int bpr = (kchunks + 7) / 8;  // 1 KiB blocks per row
+  const int64_t xlp = (int64_t)bpr * 512 + 8;
   constexpr int NT = 64 * KW;
-  constexpr int XR = XL ? (2048 / NT > 0 ? 2048 / NT : 1) : 1;
+  constexpr int XR = XS == XS_REG ? (2048 / NT > 0 ? 2048 / NT : 1) : 1;
   const uint32_t row_ch = (uint32_t)kchunks * 8u;
   const uint32_t cb = (row_ch + NT - 1) / NT;
-  const uint32_t nsteps = XL ? (uint32_t)p.M * cb : 0u;
+  const uint32_t nsteps = XS == XS_REG ? (uint32_t)p.M * cb : 0u;
   auto x_load = [&](uint32_t r) -> v4u {  // step r; zero past K or past the last step
     const uint32_t m = r / cb, k = ((r - m * cb) * NT + (uint32_t)tid) * 8u;
     const uint32_t off = (r < nsteps && k < (uint32_t)p.K) ? (m * (uint32_t)p.ldx + k) * 2u : 0x80000000u;
@@ -190,12 +204,20 @@ __global__ void __launch_bounds__(64 * KW) gemv_packed_kernel(GemvArgs p, const 
   };
   auto x_store = [&](uint32_t r, const v4u& v) {  // step r into xs (chunks past kp skipped)
     const uint32_t m = r / cb, c = (r - m * cb) * NT + (uint32_t)tid;
-    if (c < row_ch) *reinterpret_cast<v4u*>(xs + (int64_t)m * kps + c * 8u) = v;
+    if (c < row_ch) *reinterpret_cast<v4u*>(xs + (int64_t)m * xlp + c * 8u) = v;
   };
   v4u xr[XR];
-  if constexpr (XL) {
+  if constexpr (XS == XS_REG) {
 #pragma unroll
     for (int r = 0; r < XR; ++r) xr[r] = x_load((uint32_t)r);
+  } else if constexpr (XS == XS_DMA) {
+    const int nblk = (int)p.M * bpr;
+    for (int blk = wave; blk < nblk; blk += KW) {
+      const int m = blk / bpr, j = blk - m * bpr;
+      const uint32_t k = (uint32_t)j * 512u + 8u * (uint32_t)lane;
+      const uint32_t off = k < (uint32_t)p.K ? ((uint32_t)m * (uint32_t)p.ldx + k) * 2u : 0x80000000u;
+      dma16(rx, reinterpret_cast<char*>(xs + (int64_t)m * xlp + (int64_t)j * 512), off, 0u);
+    }
   }
 
   // chunks [c0, c0 + CPW * KW) are split as wave w -> c0 + w + KW * u
@@ -224,13 +246,21 @@ __global__ void __launch_bounds__(64 * KW) gemv_packed_kernel(GemvArgs p, const 
       }
     }
     if constexpr (XL) {
-      // stage X (rows < M, zero past K) while the weight loads are in flight
+      // XS_DMA: the staged activations have landed (they were issued before
+      // this wave's weight loads, and loads complete in order); publish them
+      // with an LDS-only barrier (__syncthreads would also wait for every
+      // weight load still in flight).  XS_REG: copy them in, then barrier.
       if (c0 == 0) {
+        if constexpr (XS == XS_REG) {
 #pragma unroll
-        for (int r = 0; r < XR; ++r)
-          if ((uint32_t)r < nsteps) x_store((uint32_t)r, xr[r]);
-        for (uint32_t r = XR; r < nsteps; ++r) x_store(r, x_load(r));
-        __syncthreads();
+          for (int r = 0; r < XR; ++r)
+            if ((uint32_t)r < nsteps) x_store((uint32_t)r, xr[r]);
+          for (uint32_t r = XR; r < nsteps; ++r) x_store(r, x_load(r));
+          __syncthreads();
+        } else {
+          wait_vm<CPW * CT>();
+          lds_barrier();
+        }
       }
     }
 #pragma unroll
@@ -242,7 +272,7 @@ __global__ void __launch_bounds__(64 * KW) gemv_packed_kernel(GemvArgs p, const 
           // rows >= M read row 0 and are zeroed after the (unconditional) read
           const int64_t k = (int64_t)(c0 + wave + KW * u) * 64 + 16 * g + 8 * e;
           const bool in = xrow && k < kp;
-          const v8h t = *reinterpret_cast<const v8h*>(xs + (xrow ? col : 0) * kps + (in ? k : 0));
+          const v8h t = *reinterpret_cast<const v8h*>(xs + (xrow ? col : 0) * xlp + (in ? k : 0));
           xa = in ? t : v8h{};
         } else {
           xa = __builtin_bit_cast(v8h, xq[u][e]);
@@ -311,12 +341,12 @@ int launch_gemv_pack(const int8_t* w, int64_t ldw, int64_t N, int64_t K, int8_t*
 }
 
 typedef void (*GemvPackedLaunch)(const GemvArgs&, const int8_t*, int, hipStream_t);
-template <int CT, int KW, int CPW, bool XL>
+template <int CT, int KW, int CPW, int XS>
 static void gemv_packed_one(const GemvArgs& a, const int8_t* packed, int kchunks, hipStream_t s) {
   const int64_t ntiles = (a.N + 15) / 16;
   const int64_t blocks = (ntiles + CT - 1) / CT;
-  const size_t lds = XL ? (size_t)a.M * (kchunks * 64 + 8) * 2 : 0;
-  gemv_packed_kernel<CT, KW, CPW, XL><<<dim3((unsigned)blocks), dim3(64 * KW), lds, s>>>(a, packed, kchunks);
+  const size_t lds = XS != XS_NONE ? (size_t)a.M * (((kchunks + 7) / 8) * 512 + 8) * 2 : 0;
+  gemv_packed_kernel<CT, KW, CPW, XS><<<dim3((unsigned)blocks), dim3(64 * KW), lds, s>>>(a, packed, kchunks);
 }
 struct GemvPackedEntry {
   GemvConfig cfg;
@@ -326,21 +356,22 @@ struct GemvPackedEntry {
 // within 64 KiB of LDS; outside that they run as their register-staged base
 // config (the `base` index).
 static const GemvPackedEntry kGemvPacked[] = {
-    {{2, 8, "packed_ct2_kw8", 0, 0}, &gemv_packed_one<2, 8, 8, false>},
-    {{1, 8, "packed_ct1_kw8", 0, 1}, &gemv_packed_one<1, 8, 8, false>},
-    {{4, 8, "packed_ct4_kw8", 0, 2}, &gemv_packed_one<4, 8, 4, false>},
-    {{2, 4, "packed_ct2_kw4", 0, 3}, &gemv_packed_one<2, 4, 8, false>},
-    {{1, 4, "packed_ct1_kw4", 0, 4}, &gemv_packed_one<1, 4, 16, false>},
-    {{1, 8, "packed_ct1_kw8_xl", 1, 1}, &gemv_packed_one<1, 8, 8, true>},
-    {{2, 8, "packed_ct2_kw8_xl", 1, 0}, &gemv_packed_one<2, 8, 8, true>},
-    {{1, 16, "packed_ct1_kw16_xl", 1, 1}, &gemv_packed_one<1, 16, 4, true>},
+    {{2, 8, "packed_ct2_kw8", 0, 0}, &gemv_packed_one<2, 8, 8, XS_NONE>},
+    {{1, 8, "packed_ct1_kw8", 0, 1}, &gemv_packed_one<1, 8, 8, XS_NONE>},
+    {{4, 8, "packed_ct4_kw8", 0, 2}, &gemv_packed_one<4, 8, 4, XS_NONE>},
+    {{2, 4, "packed_ct2_kw4", 0, 3}, &gemv_packed_one<2, 4, 8, XS_NONE>},
+    {{1, 4, "packed_ct1_kw4", 0, 4}, &gemv_packed_one<1, 4, 16, XS_NONE>},
+    {{1, 8, "packed_ct1_kw8_xl", 1, 1}, &gemv_packed_one<1, 8, 8, XS_REG>},
+    {{2, 8, "packed_ct2_kw8_xl", 1, 0}, &gemv_packed_one<2, 8, 8, XS_REG>},
+    {{1, 16, "packed_ct1_kw16_xl", 1, 1}, &gemv_packed_one<1, 16, 4, XS_REG>},
     // 16 waves over K keep the 4-tile activation reuse of ct4 while putting
     // 4x more waves (and weight bytes in flight) on the CUs it occupies
-    {{4, 16, "packed_ct4_kw16", 0, 8}, &gemv_packed_one<4, 16, 2, false>},
+    {{4, 16, "packed_ct4_kw16", 0, 8}, &gemv_packed_one<4, 16, 2, XS_NONE>},
     // four tiles with every K chunk of K = 4096 in flight at once (one round
     // trip to memory) over 16 or 8 waves
-    {{4, 16, "packed_ct4_kw16_c4", 0, 9}, &gemv_packed_one<4, 16, 4, false>},
-    {{4, 8, "packed_ct4_kw8_c8", 0, 10}, &gemv_packed_one<4, 8, 8, false>},
+    {{4, 16, "packed_ct4_kw16_c4", 0, 9}, &gemv_packed_one<4, 16, 4, XS_NONE>},
+    {{4, 8, "packed_ct4_kw8_c8", 0, 10}, &gemv_packed_one<4, 8, 8, XS_NONE>},
+    {{1, 8, "packed_ct1_kw8_xd", 1, 1}, &gemv_packed_one<1, 8, 8, XS_DMA>},
 };
 int gemv_packed_config_count() { return (int)(sizeof(kGemvPacked) / sizeof(kGemvPacked[0])); }
 const GemvConfig* gemv_packed_config(int idx) {
@@ -356,7 +387,7 @@ int launch_gemv_packed(int cfg_idx, const GemvArgs& a, const int8_t* packed, hip
       a.M * a.ldx * 2 >= ((int64_t)1 << 31))
     return HXI_ERR_SHAPE;
   // xl: staged rows within 64 KiB of LDS
-  if (kGemvPacked[cfg_idx].cfg.xl && (a.M > 4 || a.M * (kchunks * 64 + 8) * 2 > 65536))
+  if (kGemvPacked[cfg_idx].cfg.xl && (a.M > 4 || a.M * (((kchunks + 7) / 8) * 512 + 8) * 2 > 65536))
     cfg_idx = kGemvPacked[cfg_idx].cfg.base;
   kGemvPacked[cfg_idx].fn(a, packed, (int)((a.K + 63) / 64), s);
   return HXI_OK;
