@@ -625,6 +625,15 @@ extern "C" int hx_attention(const hx_memref4d* q, const hx_memref4d* k, const hx
   if (const char* why = attn_refusal(a))
     return fail(HX_ERR_UNSUPPORTED, "hx_attention: %s (D=%lld; D must be 64 or 128, bases 16-byte "
                 "aligned, strides multiples of 8)", why, (long long)D);
+  // few (head, query block) workgroups: split the key range, partials in
+  // the stream's workspace
+  a.splits = attn_splits(a);
+  a.part = nullptr;
+  if (a.splits > 1) {
+    char* ws = nullptr;
+    if ((rc = ws_get((hipStream_t)stream, attn_part_bytes(a), &ws))) return rc;
+    a.part = reinterpret_cast<float*>(ws);
+  }
   return map_internal(launch_attention(dtype, causal != 0, a, (hipStream_t)stream), "attention");
 }
 

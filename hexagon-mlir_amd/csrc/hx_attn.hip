@@ -83,11 +83,19 @@ __device__ __forceinline__ int swz_v(int row) {
 }
 
 typedef short v4s __attribute__((ext_vector_type(4)));
+typedef float v2f __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) v4s* lds_v4s_ptr;
 
 }  // namespace
 
-template <int D, int DT, bool CAUSAL, int ATT_BN>
+// SPLIT: the workgroup covers key-block range `blockIdx.z` of `p.splits`
+// equal ranges of its query block's blocks, and instead of O it writes the
+// unnormalised binary32 accumulator with its row maximum m (exp2 domain) and
+// row sum l to `p.part`; attn_combine_kernel merges the ranges.  Partial
+// layout, for partial row r = (bh * splits + split) * Nq + query:
+//   acc at part[r * D + d], (m, l) at part[R * D + 2 * r + {0, 1}],
+//   R = Z * H * splits * Nq.
+template <int D, int DT, bool CAUSAL, int ATT_BN, bool SPLIT>
 __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
   constexpr int KS = D / 16;             // MFMA k-steps of the score product
   constexpr int DTILES = D / 32;         // 32-wide output column tiles
@@ -154,7 +162,14 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
     const int64_t last_q = min((int64_t)qb * ATT_BM + ATT_BM, p.Nq) - 1 + p.causal_offset;
     nk = min(nk, last_q + 1);
   }
-  const int nblk = nk > 0 ? (int)((nk + ATT_BN - 1) / ATT_BN) : 0;
+  const int nblk_all = nk > 0 ? (int)((nk + ATT_BN - 1) / ATT_BN) : 0;
+  // this workgroup's key blocks [b0, b0 + nblk)
+  int b0 = 0, nblk = nblk_all;
+  if constexpr (SPLIT) {
+    const int per = (nblk_all + p.splits - 1) / p.splits;
+    b0 = min((int)blockIdx.z * per, nblk_all);
+    nblk = min(per, nblk_all - b0);
+  }
 
   // Direct loads of key block blk: load i of wave w fills the KiB of rows
   // (w + 4i)*RPK + lane/CPR; the lane writes physical chunk lane % CPR and
@@ -300,21 +315,43 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
 
   // Blocks in pairs over the two buffers; each block's loads were issued
   // one block earlier and are published by the barrier that ends it.
-  if (nblk > 0) dma_block(sk0, sv0, 0);
+  if (nblk > 0) dma_block(sk0, sv0, b0);
   wait_vm<0>();
   lds_barrier();
-  int blk = 0;
-  for (; blk + 2 <= nblk; blk += 2) {
-    dma_block(sk1, sv1, blk + 1);
-    block(sk0, sv0, blk);
+  int i = 0;
+  for (; i + 2 <= nblk; i += 2) {
+    dma_block(sk1, sv1, b0 + i + 1);
+    block(sk0, sv0, b0 + i);
     wait_vm<0>();
     lds_barrier();
-    if (blk + 2 < nblk) dma_block(sk0, sv0, blk + 2);
-    block(sk1, sv1, blk + 1);
+    if (i + 2 < nblk) dma_block(sk0, sv0, b0 + i + 2);
+    block(sk1, sv1, b0 + i + 1);
     wait_vm<0>();
     lds_barrier();
   }
-  if (blk < nblk) block(sk0, sv0, blk);
+  if (i < nblk) block(sk0, sv0, b0 + i);
+
+  if constexpr (SPLIT) {
+    // lane holds accumulator columns 32*dt + 8*g + 4*lg + (0..3) of its row;
+    // both lanes of a row hold the same m and l
+    if (q_in) {
+      const int64_t r = ((int64_t)bh * p.splits + blockIdx.z) * p.Nq + q_row;
+      float* po = p.part + r * D;
+      static_for<DTILES>([&](auto dc) {
+        constexpr int dt = decltype(dc)::value;
+        static_for<4>([&](auto gc) {
+          constexpr int g = decltype(gc)::value;
+          *reinterpret_cast<v4f*>(po + 32 * dt + 8 * g + 4 * lg) =
+              v4f{oacc[dt][4 * g], oacc[dt][4 * g + 1], oacc[dt][4 * g + 2], oacc[dt][4 * g + 3]};
+        });
+      });
+      if (lg == 0) {
+        const int64_t R = p.Z * p.H * p.splits * p.Nq;
+        *reinterpret_cast<v2f*>(p.part + R * D + 2 * r) = v2f{m_i, l_i};
+      }
+    }
+    return;
+  }
 
   // O = acc / l: lane holds row q_row, columns 32*dt + 8*g + 4*lg + (0..3)
   if (q_in) {
@@ -332,10 +369,95 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
   }
 }
 
+// Merge of the key-range partials of attn_fwd_kernel<..., SPLIT = true>:
+// with M = max_s m_s and w_s = 2^(m_s - M),
+//   O = (sum_s w_s acc_s) / (sum_s w_s l_s),
+// the online-softmax recurrence applied once across the ranges.  A range
+// that saw only masked keys has m = -inf, l = 0, acc = 0 and weight 0; a
+// row with no visible key at all gets O = 0, as in the single pass.  Each
+// thread finalises four consecutive columns of one query row.  The loop
+// over ranges is unrolled to SMAX with the range index clamped to the last
+// one (its weight then forced to 0), so every partial load of the thread is
+// issued before the first is used: one round trip to memory, not one per
+// range.
+template <int D, int DT, int SMAX>
+__global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs p) {
+  constexpr int TPR = D / 4;  // threads per row
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t rows = p.Z * p.H * p.Nq;
+  if (t >= rows * TPR) return;
+  const int64_t row = t / TPR;  // bh * Nq + query
+  const int d = 4 * (int)(t - row * TPR);
+  const int64_t bh = row / p.Nq, qr = row - bh * p.Nq;
+  const int S = p.splits;
+  const float* ml = p.part + rows * S * D;
+  const int64_t r0 = bh * S * p.Nq + qr;  // partial row of range 0; range s adds s * Nq
+  v2f mls[SMAX];
+  v4f accs[SMAX];
+#pragma unroll
+  for (int s = 0; s < SMAX; ++s) {
+    const int64_t r = r0 + (int64_t)min(s, S - 1) * p.Nq;
+    mls[s] = *reinterpret_cast<const v2f*>(ml + 2 * r);
+    accs[s] = *reinterpret_cast<const v4f*>(p.part + r * D + d);
+  }
+  float M = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < SMAX; ++s) M = fmaxf(M, mls[s][0]);  // clamped copies repeat a real range
+  float L = 0.f;
+  v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < SMAX; ++s) {
+    const float w = (s < S && mls[s][0] != -INFINITY) ? exp2_fast(mls[s][0] - M) : 0.f;
+    L += w * mls[s][1];
+    acc += w * accs[s];
+  }
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  const int64_t zb = bh / p.H, hb = bh - zb * p.H;
+  char* o = reinterpret_cast<char*>(p.o) + 2 * (zb * p.so[0] + hb * p.so[1] + qr * p.so[2] + d);
+  *reinterpret_cast<v2i*>(o) = v2i{(int)pack2<DT>(acc[0] * inv, acc[1] * inv),
+                                   (int)pack2<DT>(acc[2] * inv, acc[3] * inv)};
+}
+
+// Split the key range when the (head, query block) workgroups would fill
+// less than half of the 256 CUs: enough ranges to bring the grid to about
+// 256 workgroups, each at least kMinSplitBlocks key blocks long, at most
+// kMaxSplits ranges.  Measured at Z = H = 1, N = 1024, D = 64: 8 ranges
+// 9.0 us, 16 ranges 9.7 us, 4 ranges 10.8 us, single pass 15.7 us.
+constexpr int kMinSplitBlocks = 2;
+constexpr int kMaxSplits = 8;
+
 template <int D, int DT, bool CAUSAL, int BN>
 static void attn_launch(const AttnArgs& a, hipStream_t s) {
-  const dim3 grid((unsigned)((a.Nq + ATT_BM - 1) / ATT_BM), (unsigned)(a.Z * a.H));
-  attn_fwd_kernel<D, DT, CAUSAL, BN><<<grid, dim3(256), 0, s>>>(a);
+  const unsigned qblocks = (unsigned)((a.Nq + ATT_BM - 1) / ATT_BM);
+  if (a.splits > 1) {
+    const dim3 grid(qblocks, (unsigned)(a.Z * a.H), (unsigned)a.splits);
+    attn_fwd_kernel<D, DT, CAUSAL, BN, true><<<grid, dim3(256), 0, s>>>(a);
+    const int64_t threads = a.Z * a.H * a.Nq * (D / 4);
+    const dim3 cgrid((unsigned)((threads + 255) / 256));
+    // the combine's unrolled range count: the smallest of 2, 4, 8 that holds
+    // every range (each unused slot costs a load per thread)
+    if (a.splits <= 2) attn_combine_kernel<D, DT, 2><<<cgrid, dim3(256), 0, s>>>(a);
+    else if (a.splits <= 4) attn_combine_kernel<D, DT, 4><<<cgrid, dim3(256), 0, s>>>(a);
+    else attn_combine_kernel<D, DT, kMaxSplits><<<cgrid, dim3(256), 0, s>>>(a);
+  } else {
+    attn_fwd_kernel<D, DT, CAUSAL, BN, false><<<dim3(qblocks, (unsigned)(a.Z * a.H)), dim3(256), 0, s>>>(a);
+  }
+}
+
+// Keys per block of the launched kernels (see launch_attention).
+constexpr int ATT_BN_ALL = 64;
+int attn_splits(const AttnArgs& a) {
+  const int64_t wgs = (a.Nq + ATT_BM - 1) / ATT_BM * a.Z * a.H;
+  const int64_t nblk = (a.Nk + ATT_BN_ALL - 1) / ATT_BN_ALL;
+  if (wgs <= 0 || wgs >= 128 || nblk < 2 * kMinSplitBlocks) return 1;
+  int64_t sp = (256 + wgs - 1) / wgs;
+  sp = std::min<int64_t>(sp, nblk / kMinSplitBlocks);
+  sp = std::min<int64_t>(sp, kMaxSplits);
+  return (int)std::max<int64_t>(sp, 1);
+}
+size_t attn_part_bytes(const AttnArgs& a) {
+  if (a.splits <= 1) return 0;
+  return (size_t)(a.Z * a.H * a.Nq) * (size_t)a.splits * (size_t)(a.D + 2) * sizeof(float);
 }
 
 const char* attn_refusal(const AttnArgs& a) {
@@ -355,6 +477,7 @@ const char* attn_refusal(const AttnArgs& a) {
 int launch_attention(int dtype, bool causal, const AttnArgs& a, hipStream_t s) {
   if (attn_refusal(a)) return HXI_ERR_UNSUPPORTED;
   if (a.Nq == 0 || a.Z * a.H == 0) return HXI_OK;
+  if (a.splits > 1 && (a.part == nullptr || a.splits > kMaxSplits)) return HXI_ERR_ARG;
   // keys per K/V block: 64 (MI355X sweep over 32 / 64 / 128 keys; with
   // 64 keys a D = 128 workgroup needs 64 KiB of LDS, two fit a CU)
 #define HX_ATT(D_, DT_, BN_)                                     \
@@ -363,6 +486,8 @@ int launch_attention(int dtype, bool causal, const AttnArgs& a, hipStream_t s) {
     else attn_launch<D_, DT_, false, BN_>(a, s);                 \
     return HXI_OK;                                               \
   }
+  static_assert(ATT_BN_ALL == 64, "attn_splits counts 64-key blocks");
+  static_assert(kMaxSplits == 8, "attn_launch instantiates the combine for 2, 4 and 8 ranges");
   HX_ATT(64, DT_F16, 64)
   HX_ATT(128, DT_F16, 64)
   HX_ATT(64, DT_BF16, 64)

@@ -108,9 +108,15 @@ struct AttnArgs {
   int64_t Z, H, Nq, Nk, D;
   float scale;
   int64_t causal_offset;  // causal: key <= query + offset is visible
+  int splits;             // key-range splits per (head, query block); 1 = single pass
+  float* part;            // split partials (attn_part_bytes), used when splits > 1
 };
 // Null when the fused kernel takes these args, else the first refusal.
 const char* attn_refusal(const AttnArgs& a);
+// Key-range splits for a launch of these args (1 when the heads and query
+// blocks alone occupy the chip), and the partial-result bytes they need.
+int attn_splits(const AttnArgs& a);
+size_t attn_part_bytes(const AttnArgs& a);
 int launch_attention(int dtype, bool causal, const AttnArgs& a, hipStream_t s);
 
 // ---- layout utilities (hx_pack.hip) --------------------------------------

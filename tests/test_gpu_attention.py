@@ -75,6 +75,24 @@ def test_attention_strided_heads_and_determinism(hx, dev):
     assert np.abs(got.astype(np.float32) - want.astype(np.float32)).max() < 1e-2
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_split_matches_single_pass(hx, dev, causal):
+    """One head alone occupies 8 workgroups, so its key range is split and
+    the partials merged; the same head repeated 128 times fills the chip and
+    runs in a single pass.  Both agree with each other and with the oracle."""
+    r = rng(91 + int(causal))
+    q, k, v = (r.normal(0, 1, (1, 1, 1024, 64)).astype(np.float16) for _ in range(3))
+    split = to_np(hx.attention(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), scale=0.125, causal=causal))
+    rep = [to_dev(a, dev).repeat(1, 128, 1, 1) for a in (q, k, v)]
+    single = to_np(hx.attention(*rep, scale=0.125, causal=causal))
+    assert all(np.array_equal(single[:, 0].view(np.uint16), single[:, h].view(np.uint16)) for h in range(128))
+    want = oracle.attention(q, k, v, 0.125, causal=causal).astype(np.float32)
+    s32, p32 = split.astype(np.float32), single[:, :1].astype(np.float32)
+    assert np.abs(s32 - p32).max() < 2e-3
+    assert np.abs(s32 - want).max() < 1e-2 and rel_err(s32, want) < 3e-3
+    assert np.abs(p32 - want).max() < 1e-2 and rel_err(p32, want) < 3e-3
+
+
 def test_attention_rejects_bad_head_dim(hx, dev):
     q = torch.zeros((1, 1, 64, 96), dtype=torch.float16, device=dev)
     with pytest.raises(hx.HXError, match="head-dim"):
