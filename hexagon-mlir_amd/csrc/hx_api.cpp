@@ -267,11 +267,16 @@ static bool op_gemm(int op, int* mode, int* epi) {
   }
 }
 
+// The decode GEMV families (int8, f16, bf16 weights) share one config table.
+static bool gemv_op(int op) {
+  return op == HX_OP_GEMV_W8 || op == HX_OP_GEMV_F16 || op == HX_OP_GEMV_BF16;
+}
+
 // Table indices (into the mode's table) of the configs of one family.
 static std::vector<int> family_indices(int op) {
   std::vector<int> out;
   int mode, epi;
-  if (op == HX_OP_GEMV_W8) {
+  if (gemv_op(op)) {
     for (int i = 0; i < gemv_packed_config_count(); ++i) out.push_back(i);
     return out;
   }
@@ -305,12 +310,21 @@ static int resolve_gemm(int op, int64_t M, int64_t N, int64_t K, bool* was_pinne
   }
   return gemm_default_config(mode, epi, M, N, K);
 }
-static int resolve_gemv(int64_t M, int64_t N, int64_t K, bool* was_pinned = nullptr) {
-  const int pin = pinned(HX_OP_GEMV_W8, M, N, K);
+static int resolve_gemv(int op, int64_t M, int64_t N, int64_t K, bool* was_pinned = nullptr) {
+  const int pin = pinned(op, M, N, K);
   if (was_pinned) *was_pinned = pin >= 0 && pin < gemv_packed_config_count();
   if (pin >= 0 && pin < gemv_packed_config_count()) return pin;
-  (void)N; (void)K;
-  // untuned choice from the MI355X sweep (N = 11008, K = 4096): LDS-staged
+  (void)N;
+  if (op != HX_OP_GEMV_W8) {
+    // f16 / bf16 weights, untuned choice from the MI355X sweep over
+    // N, K in {4096, 8192, 11008}: 16 waves with LDS-staged activations for
+    // M <= 2 (software pipelined once K spans several slices), 8 for M <= 4,
+    // one column tile per workgroup (two for K >= 8192) beyond
+    if (M <= 2) return K >= 8192 ? 12 : 7;
+    if (M <= 4) return 5;
+    return K >= 8192 ? 0 : 1;
+  }
+  // untuned choice from the MI355X sweep (int8, N = 11008, K = 4096): LDS-staged
   // activations and one column tile per workgroup for M <= 4 -- staged by
   // direct-to-LDS loads for M <= 2, through registers for M = 3, 4 (the
   // launcher falls back to the register-fragment base config when the rows
@@ -336,6 +350,16 @@ static int run_gemm(int op, GemmArgs& a, hipStream_t s, const PlanCtx& ctx) {
   }
   note_plan(ctx, a.M, a.N, a.K, a.out_dtype, "mfma-generic", "generic_32x32", "fixed", refusal);
   return map_internal(launch_gemm_generic(mode, a, s), "gemm_generic");
+}
+
+// f16 / bf16 weights read in place from [N][K] by the streaming GEMV.
+static int run_gemv_hw(GemvArgs& a, int dt, const void* w, int64_t ldw, hipStream_t s, const PlanCtx& ctx) {
+  const int op = dt == HX_BF16 ? HX_OP_GEMV_BF16 : HX_OP_GEMV_F16;
+  bool pin = false;
+  const int cfg = resolve_gemv(op, a.M, a.N, a.K, &pin);
+  note_plan(ctx, a.M, a.N, a.K, dt, "gemv-stream", gemv_packed_config(cfg)->name, pin ? "pinned" : "default",
+            "min-rows");
+  return map_internal(launch_gemv_hw(cfg, dt, a, w, ldw, s), "gemv_stream");
 }
 
 static int run_gemv(GemvArgs& a, hipStream_t s, const PlanCtx& ctx) {
@@ -458,6 +482,12 @@ extern "C" int hx_matmul(const hx_memref2d* a, int a_dtype, const hx_memref2d* b
     v.x = g.a; v.ldx = g.lda; v.w = (const int8_t*)g.b; v.ldw = g.ldb;
     v.scale = g.col_scale; v.y = g.c; v.ldy = g.ldc; v.M = M; v.N = N; v.K = K;
     if (gemv_fast_ok(v)) return run_gemv(v, s, ctx);
+  }
+  if (op != HX_OP_MATMUL_W8 && M <= 16 && !residual && c_dtype == a_dtype) {
+    GemvArgs v{};
+    v.x = g.a; v.ldx = g.lda; v.w = nullptr; v.ldw = 0;
+    v.scale = g.col_scale; v.y = g.c; v.ldy = g.ldc; v.M = M; v.N = N; v.K = K;
+    if (!gemv_hw_refusal(v, g.b, g.ldb)) return run_gemv_hw(v, a_dtype, g.b, g.ldb, s, ctx);
   }
   return run_gemm(op, g, s, ctx);
 }
@@ -800,10 +830,17 @@ static int matmul_resident_impl(const View2& vx, hx_weight* w, const View2* vr, 
     v.x = vx.p; v.ldx = vx.ld; v.w = nullptr; v.ldw = 0;
     v.scale = w->scale; v.y = vy.p; v.ldy = vy.ld; v.M = M; v.N = w->N; v.K = w->K;
     bool pin = false;
-    const int cfg = resolve_gemv(M, w->N, w->K, &pin);
+    const int cfg = resolve_gemv(HX_OP_GEMV_W8, M, w->N, w->K, &pin);
     note_plan(PlanCtx{entry, "resident-packed", x_dt, w->dtype}, M, w->N, w->K, HX_F16, "gemv-packed",
               gemv_packed_config(cfg)->name, pin ? "pinned" : "default", "min-rows");
     return map_internal(launch_gemv_packed(cfg, v, w->packed, s), "gemv_packed");
+  }
+  if (w->dtype != HX_I8 && M <= 16 && !vr && y_dt == x_dt) {
+    GemvArgs v{};
+    v.x = vx.p; v.ldx = vx.ld; v.w = nullptr; v.ldw = 0;
+    v.scale = w->scale; v.y = vy.p; v.ldy = vy.ld; v.M = M; v.N = w->N; v.K = w->K;
+    if (!gemv_hw_refusal(v, w->image, w->K)) return run_gemv_hw(v, x_dt, w->image, w->K, s,
+                                                                PlanCtx{entry, "resident-image", x_dt, w->dtype});
   }
   GemmArgs g{};
   g.a = vx.p; g.lda = vx.ld;
@@ -918,9 +955,9 @@ extern "C" int hx_config_get(int op, int index, hx_kernel_config* out) {
   memset(out, 0, sizeof(*out));
   out->op = op;
   out->index = index;
-  if (op == HX_OP_GEMV_W8) {
+  if (gemv_op(op)) {
     const GemvConfig* c = gemv_packed_config(idx[index]);
-    out->bm = 16; out->bn = 16 * c->ct; out->bk = 64;
+    out->bm = 16; out->bn = 16 * c->ct; out->bk = op == HX_OP_GEMV_W8 ? 64 : 32;
     out->waves_m = c->kw; out->waves_n = 1;
     out->lds_stages = 0; out->split_k = c->kw; out->col_tiles = c->ct;
     out->lds_bytes = c->kw * c->ct * 64 * 4 * 4;
@@ -957,7 +994,7 @@ extern "C" int hx_config_select(int op, int64_t m, int64_t n, int64_t k, int ind
 static const char* config_name(int op, int index) {
   std::vector<int> idx = family_indices(op);
   if (index < 0 || index >= (int)idx.size()) return nullptr;
-  if (op == HX_OP_GEMV_W8) return gemv_packed_config(idx[index])->name;
+  if (gemv_op(op)) return gemv_packed_config(idx[index])->name;
   int mode, epi;
   op_gemm(op, &mode, &epi);
   return gemm_config(mode, idx[index])->name;
@@ -1027,8 +1064,8 @@ extern "C" int hx_config_lookup(int op, int64_t m, int64_t n, int64_t k, int* in
   int dev;
   int rc = current_device(&dev);
   if (rc) return rc;
-  if (op == HX_OP_GEMV_W8) {
-    *index = resolve_gemv(m, n, k);
+  if (gemv_op(op)) {
+    *index = resolve_gemv(op, m, n, k);
     return HX_OK;
   }
   const int t = resolve_gemm(op, m, n, k);

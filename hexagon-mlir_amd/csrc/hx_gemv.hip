@@ -1,21 +1,24 @@
-// hx_gemv.hip -- W8A16 decode GEMM/GEMV for M <= 16:
-//   Y[m][n] = RNE_f16( (sum_k X[m][k] * W[k][n]) * s[n] ),  binary32 accumulate.
+// hx_gemv.hip -- decode GEMM/GEMV for M <= 16, int8 (W8A16), f16 or bf16
+// weights:
+//   Y[m][n] = RNE( (sum_k X[m][k] * W[k][n]) * s[n] ),  binary32 accumulate,
+// rounded to the activations' type.
 //
 // In hexagon-mlir the M <= 4 rows are refused by the HMX engine as
 // `min-rows` and M = 16 fails `tile-alignment` (QHB/include/hexagon/Dialect/
 // Hmx/Transforms/HmxTarget.h:100, 195-218), so these shapes run through the
 // HVX (i,k,j) generic of ScheduleMatmulForHVX
-// (QHB/lib/Transforms/ScheduleMatmulForHVXPass.cpp:169-196) with the
-// dequantised weight (sitofp, then the per-channel scale).
+// (QHB/lib/Transforms/ScheduleMatmulForHVXPass.cpp:169-196), for int8 with
+// the dequantised weight (sitofp, then the per-channel scale).
 //
-// MI355X design: an HBM stream over the int8 weight, read once, widened to
-// f16 exactly in registers and fed to v_mfma_f32_16x16x32_f16 with the
-// activations zero-padded to 16 rows.  Two kernels:
-//   * gemv_packed_kernel -- registered (resident) weights, stored in MFMA
-//     fragment order so that every wave load is one contiguous KiB and each
-//     wave issues its whole K slice before its first MFMA (below);
-//   * gemv_w8a16_kernel -- an unregistered K-contiguous [N][K] weight: per
-//     128-wide K window each lane loads 2 x 16 bytes of one column; lane
+// MI355X design: an HBM stream over the weight, read once, fed to
+// v_mfma_f32_16x16x32_{f16,bf16} with the activations zero-padded to 16
+// rows (int8 widened to f16 exactly in registers).  Two kernels:
+//   * gemv_stream_kernel -- registered int8 weights, stored in MFMA fragment
+//     order so that every wave load is one contiguous KiB, and f16/bf16
+//     weights read in place from [N][K]; each wave issues its K slice before
+//     its first MFMA (below);
+//   * gemv_w8a16_kernel -- an unregistered K-contiguous [N][K] int8 weight:
+//     per 128-wide K window each lane loads 2 x 16 bytes of one column; lane
 //     group g = lane/16 supplies k = 64*h + 16*g + 8*e + (0..7) in step
 //     s = 2h + e for both operands, so every k is summed exactly once; the
 //     four waves of a workgroup split K and reduce through LDS.
@@ -124,50 +127,77 @@ __global__ void __launch_bounds__(256) gemv_w8a16_kernel(GemvArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// Fragment-packed variant (resident weights).  The weight image is stored in
-// MFMA B-fragment order: for column tile t (16 columns) and K chunk j (64 k)
-// one 1 KiB block at ((t * KC) + j) * 1024 (KC = K/64 chunks), in which byte
-// 256*g + 16*c + i holds W[64*j + 16*g + i][16*t + c] ^ 0x80 (g 0..3,
-// c 0..15, i 0..15; excess-128, so the widening to f16 needs no XOR per
-// load).  Lane l of a wave then loads its operand as the 16 contiguous
-// bytes at 16*l: column l % 16, k = 64*j + 16*(l/16) + (0..15), which feeds
-// two v_mfma_f32_16x16x32_f16 steps (e = 0, 1: k = .. + 8*e + (0..7)); the
-// activation operand uses the same k mapping.  Every wave load is one
-// contiguous KiB, and a workgroup of KW waves splits K so that each wave
-// issues its whole K slice (CT tiles x chunks) before the first MFMA: the
-// kernel is a single round trip to HBM.
-// ---------------------------------------------------------------------------
+// Streaming kernel for registered int8 weights (fragment-packed image) and
+// for f16/bf16 weights read in place from a K-contiguous [N][K] matrix.
+//
+// A K chunk is the 1 KiB a wave loads per 16-column tile: 64 k of int8 or 32
+// k of f16/bf16.  Lane l = 16g + c of the wave loads the 16 bytes of column
+// c, k = KD*j + (KD/4)*g + (0..KD/4-1) of chunk j, which feed the
+// v_mfma_f32_16x16x32 steps e (k = .. + 8e + (0..7)): two steps for int8
+// (widened to f16 in registers), one for f16/bf16; the activation operand
+// uses the same k mapping.
+//   * int8, packed: for column tile t and chunk j one 1 KiB block at
+//     ((t * KC) + j) * 1024 (KC chunks per tile), in which byte
+//     256*g + 16*c + i holds W[64*j + 16*g + i][16*t + c] ^ 0x80 (g 0..3,
+//     c 0..15, i 0..15; excess-128, so the widening needs no XOR per load),
+//     so every wave load is one contiguous KiB;
+//   * f16/bf16, in place: lane l reads row 16t + c of the [N][K] weight at
+//     k = 32j + 8g: sixteen 64-byte runs per wave load.
+// A workgroup of KW waves splits K into slices of CPW * KW chunks; each wave
+// loads CPW chunks of each of its CT tiles per slice, ahead of the MFMAs
+// that use them (how far ahead is the compiler's schedule: for the wide
+// configs it interleaves loads and MFMAs with fewer live registers, which
+// measured faster than holding the whole slice).  With K = 4096 int8 and
+// CPW * KW = 64 a slice is all of K.  PIPE: two register sets, the next
+// slice's loads issued before the current slice's MFMAs.
 //
 // XL (M <= 4): the activations are staged once per workgroup in LDS ([M]
-// rows of kchunks*64, zero-padded), and each MFMA step reads its operand
+// rows of kchunks*KD, zero-padded), and each MFMA step reads its operand
 // from there; the registers that would hold every step's activation
-// fragment (2 x 16 bytes per chunk) are freed, so more waves -- more weight
-// bytes in flight -- fit on a CU.  The activation loads are issued before
-// the weight stream: loads complete in issue order, so an activation load
-// queued behind a wave's weight loads would hold back the whole
-// workgroup's compute (the LDS staging ends in a barrier) until its last
-// weight byte has arrived, leaving no overlap between compute and stream.
-template <int CT, int KW, int CPW, int XS>
-__global__ void __launch_bounds__(64 * KW) gemv_packed_kernel(GemvArgs p, const int8_t* packed,
+// fragment are freed, so more waves -- more weight bytes in flight -- fit
+// on a CU.  The activation loads are issued before the weight stream: loads
+// complete in issue order, so an activation load queued behind a wave's
+// weight loads would hold back the whole workgroup's compute (the LDS
+// staging ends in a barrier) until its last weight byte has arrived,
+// leaving no overlap between compute and stream.
+template <int WT>
+__device__ __forceinline__ v4f gv_mfma(v4u a, v4u b, v4f c) {
+  if constexpr (WT == DT_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b), c,
+                                                    0, 0, 0);
+  else
+    return mfma16_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c);
+}
+
+template <int CT, int KW, int CPW, int XS, int WT, bool PK, bool PIPE>
+__global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const void* wsrc, int64_t ldw,
                                                               int kchunks) {
+  static_assert(PK == (WT == DT_I8), "int8 weights stream from the packed image, f16/bf16 in place");
   constexpr bool XL = XS != XS_NONE;
+  constexpr int KD = WT == DT_I8 ? 64 : 32;  // k per chunk
+  constexpr int KG = KD / 4;                  // k per lane group within a chunk
+  constexpr int NE = WT == DT_I8 ? 2 : 1;     // MFMA steps per chunk
+  constexpr int ES = WT == DT_I8 ? 1 : 2;     // weight element bytes
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, g = lane >> 4;
   const int t0 = blockIdx.x * CT;                    // first column tile
   const int ntiles = (int)((p.N + 15) / 16);
   const int tiles_here = min(CT, ntiles - t0);
+  const int rows_here = (int)min((int64_t)16 * CT, p.N - (int64_t)16 * t0);
   const bool xrow = col < p.M;
   const uint16_t* x = reinterpret_cast<const uint16_t*>(p.x);
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
-  const int64_t kp = (int64_t)kchunks * 64;
+  const int64_t kp = (int64_t)kchunks * KD;
 
   // Every global load below is a buffer load whose out-of-range offset
   // (0x80000000) reads zero, so no load sits behind a branch: a conditional
   // load makes the compiler wait for it at the join, or count outstanding
   // loads conservatively.  The launcher keeps all offsets below 2^31.
-  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(packed + (int64_t)t0 * kchunks * 1024), 0, tiles_here * kchunks * 1024, 0x00020000);
+  const char* wbase = reinterpret_cast<const char*>(wsrc) +
+                      (PK ? (int64_t)t0 * kchunks * 1024 : (int64_t)16 * t0 * ldw * ES);
+  const int wbytes = PK ? tiles_here * kchunks * 1024 : (int)((int64_t)rows_here * ldw * ES);
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)wbase, 0, wbytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t rx =
       __builtin_amdgcn_make_buffer_rsrc((void*)x, 0, (int)(p.M * p.ldx * 2), 0x00020000);
   constexpr int kNT = 2;  // cache policy: non-temporal (the weight is streamed once)
@@ -187,14 +217,14 @@ __global__ void __launch_bounds__(64 * KW) gemv_packed_kernel(GemvArgs p, const 
   //     r = m * cb + b covers the 16-byte chunks b * T + tid of row m (T
   //     threads, cb blocks per row); the first XR steps go through registers
   //     ahead of the weight loads, any further ones are loaded after them.
-  // Measured at N = 11008, K = 4096: DMA is faster for M = 1 (one load per
-  // wave), registers for M = 4 (the DMA's LDS writes delay the weight
-  // loads queued behind them).
-  const int bpr = (kchunks + 7) / 8;  // 1 KiB blocks per row
+  // Measured at N = 11008, K = 4096 (int8): DMA is faster for M = 1 (one
+  // load per wave), registers for M = 4 (the DMA's LDS writes delay the
+  // weight loads queued behind them).
+  const int bpr = (int)((kp + 511) / 512);  // 1 KiB blocks per row
   const int64_t xlp = (int64_t)bpr * 512 + 8;
   constexpr int NT = 64 * KW;
   constexpr int XR = XS == XS_REG ? (2048 / NT > 0 ? 2048 / NT : 1) : 1;
-  const uint32_t row_ch = (uint32_t)kchunks * 8u;
+  const uint32_t row_ch = (uint32_t)(kp / 8);
   const uint32_t cb = (row_ch + NT - 1) / NT;
   const uint32_t nsteps = XS == XS_REG ? (uint32_t)p.M * cb : 0u;
   auto x_load = [&](uint32_t r) -> v4u {  // step r; zero past K or past the last step
@@ -221,72 +251,164 @@ __global__ void __launch_bounds__(64 * KW) gemv_packed_kernel(GemvArgs p, const 
   }
 
   // chunks [c0, c0 + CPW * KW) are split as wave w -> c0 + w + KW * u
-  for (int c0 = 0; c0 < kchunks; c0 += CPW * KW) {
-    v4u wq[CPW][CT];
-    v4u xq[XL ? 1 : CPW][2];
+  constexpr int STEP = CPW * KW;
+  // issue / compute of one K slice, for the pipelined path
+  typedef v4u WFrag[CPW][CT];
+  typedef v4u XFrag[XL ? 1 : CPW][NE];
+  auto issue = [&](int c0, WFrag& wq, XFrag& xq) {
 #pragma unroll
     for (int u = 0; u < CPW; ++u) {
       const int j = c0 + wave + KW * u;
       const bool jv = j < kchunks;
 #pragma unroll
       for (int c = 0; c < CT; ++c) {
-        const uint32_t off = (jv && c < tiles_here)
-                                 ? (uint32_t)(c * kchunks + j) * 1024u + 16u * (uint32_t)lane
-                                 : 0x80000000u;
+        uint32_t off;
+        if constexpr (PK) {
+          off = (jv && c < tiles_here) ? (uint32_t)(c * kchunks + j) * 1024u + 16u * (uint32_t)lane : 0x80000000u;
+        } else {
+          const uint32_t row = (uint32_t)(16 * c + col), k = (uint32_t)j * KD + KG * (uint32_t)g;
+          off = (jv && row < (uint32_t)rows_here && k < (uint32_t)p.K)
+                    ? (row * (uint32_t)ldw + k) * (uint32_t)ES : 0x80000000u;
+        }
         wq[u][c] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)off, 0, kNT));
       }
       if constexpr (!XL) {
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const uint32_t k = (uint32_t)j * 64u + 16u * g + 8u * e;
+        for (int e = 0; e < NE; ++e) {
+          const uint32_t k = (uint32_t)j * KD + KG * (uint32_t)g + 8u * e;
           const uint32_t off = (jv && xrow && k < (uint32_t)p.K)
                                    ? ((uint32_t)col * (uint32_t)p.ldx + k) * 2u : 0x80000000u;
           xq[u][e] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0));
         }
       }
     }
-    if constexpr (XL) {
-      // XS_DMA: the staged activations have landed (they were issued before
-      // this wave's weight loads, and loads complete in order); publish them
-      // with an LDS-only barrier (__syncthreads would also wait for every
-      // weight load still in flight).  XS_REG: copy them in, then barrier.
-      if (c0 == 0) {
-        if constexpr (XS == XS_REG) {
+  };
+  // XL: publish the staged activations.  XS_DMA: they have landed once no
+  // more than the `after` weight loads issued behind them are outstanding
+  // (loads complete in order); the LDS-only barrier does not wait for the
+  // weight loads still in flight, as __syncthreads would.  XS_REG: copy
+  // them in, then barrier.
+  auto publish = [&](auto after) {
+    if constexpr (XS == XS_REG) {
 #pragma unroll
-          for (int r = 0; r < XR; ++r)
-            if ((uint32_t)r < nsteps) x_store((uint32_t)r, xr[r]);
-          for (uint32_t r = XR; r < nsteps; ++r) x_store(r, x_load(r));
-          __syncthreads();
-        } else {
-          wait_vm<CPW * CT>();
-          lds_barrier();
-        }
-      }
+      for (int r = 0; r < XR; ++r)
+        if ((uint32_t)r < nsteps) x_store((uint32_t)r, xr[r]);
+      for (uint32_t r = XR; r < nsteps; ++r) x_store(r, x_load(r));
+      __syncthreads();
+    } else if constexpr (XS == XS_DMA) {
+      wait_vm<decltype(after)::value>();
+      lds_barrier();
     }
+  };
+  auto compute = [&](int c0, const WFrag& wq, const XFrag& xq) {
 #pragma unroll
     for (int u = 0; u < CPW; ++u)
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        v8h xa;
+      for (int e = 0; e < NE; ++e) {
+        v4u xa;
         if constexpr (XL) {
           // rows >= M read row 0 and are zeroed after the (unconditional) read
-          const int64_t k = (int64_t)(c0 + wave + KW * u) * 64 + 16 * g + 8 * e;
+          const int64_t k = (int64_t)(c0 + wave + KW * u) * KD + KG * g + 8 * e;
           const bool in = xrow && k < kp;
-          const v8h t = *reinterpret_cast<const v8h*>(xs + (xrow ? col : 0) * xlp + (in ? k : 0));
-          xa = in ? t : v8h{};
+          const v4u t = *reinterpret_cast<const v4u*>(xs + (xrow ? col : 0) * xlp + (in ? k : 0));
+          xa = in ? t : v4u{0u, 0u, 0u, 0u};
         } else {
-          xa = __builtin_bit_cast(v8h, xq[u][e]);
+          xa = xq[u][e];
         }
 #pragma unroll
         for (int c = 0; c < CT; ++c) {
-          const v8h wb = x8x8_to_v8h(wq[u][c][2 * e], wq[u][c][2 * e + 1]);
-          acc[c] = mfma16_f16(xa, wb, acc[c]);
+          v4u wb;
+          if constexpr (WT == DT_I8)
+            wb = __builtin_bit_cast(v4u, x8x8_to_v8h(wq[u][c][2 * e], wq[u][c][2 * e + 1]));
+          else
+            wb = wq[u][c];
+          acc[c] = gv_mfma<WT>(xa, wb, acc[c]);
         }
       }
+  };
+
+  if constexpr (!PIPE) {
+    // Each K slice of STEP chunks is one round trip: issue, then compute.
+    // Written out here rather than through issue/compute: the compiler then
+    // schedules the slice's loads among its MFMAs with fewer live registers,
+    // which measured up to 2x faster for the wide (CT >= 2, CPW = 8) configs.
+    for (int c0 = 0; c0 < kchunks; c0 += STEP) {
+      v4u wq[CPW][CT];
+      v4u xq[XL ? 1 : CPW][NE];
+#pragma unroll
+      for (int u = 0; u < CPW; ++u) {
+        const int j = c0 + wave + KW * u;
+        const bool jv = j < kchunks;
+#pragma unroll
+        for (int c = 0; c < CT; ++c) {
+          uint32_t off;
+          if constexpr (PK) {
+            off = (jv && c < tiles_here) ? (uint32_t)(c * kchunks + j) * 1024u + 16u * (uint32_t)lane
+                                         : 0x80000000u;
+          } else {
+            const uint32_t row = (uint32_t)(16 * c + col), k = (uint32_t)j * KD + KG * (uint32_t)g;
+            off = (jv && row < (uint32_t)rows_here && k < (uint32_t)p.K)
+                      ? (row * (uint32_t)ldw + k) * (uint32_t)ES : 0x80000000u;
+          }
+          wq[u][c] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)off, 0, kNT));
+        }
+        if constexpr (!XL) {
+#pragma unroll
+          for (int e = 0; e < NE; ++e) {
+            const uint32_t k = (uint32_t)j * KD + KG * (uint32_t)g + 8u * e;
+            const uint32_t off = (jv && xrow && k < (uint32_t)p.K)
+                                     ? ((uint32_t)col * (uint32_t)p.ldx + k) * 2u : 0x80000000u;
+            xq[u][e] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0));
+          }
+        }
+      }
+      if constexpr (XL)
+        if (c0 == 0) publish(std::integral_constant<int, CPW * CT>{});
+#pragma unroll
+      for (int u = 0; u < CPW; ++u)
+#pragma unroll
+        for (int e = 0; e < NE; ++e) {
+          v4u xa;
+          if constexpr (XL) {
+            // rows >= M read row 0 and are zeroed after the (unconditional) read
+            const int64_t k = (int64_t)(c0 + wave + KW * u) * KD + KG * g + 8 * e;
+            const bool in = xrow && k < kp;
+            const v4u t = *reinterpret_cast<const v4u*>(xs + (xrow ? col : 0) * xlp + (in ? k : 0));
+            xa = in ? t : v4u{0u, 0u, 0u, 0u};
+          } else {
+            xa = xq[u][e];
+          }
+#pragma unroll
+          for (int c = 0; c < CT; ++c) {
+            v4u wb;
+            if constexpr (WT == DT_I8)
+              wb = __builtin_bit_cast(v4u, x8x8_to_v8h(wq[u][c][2 * e], wq[u][c][2 * e + 1]));
+            else
+              wb = wq[u][c];
+            acc[c] = gv_mfma<WT>(xa, wb, acc[c]);
+          }
+        }
+    }
+  } else {
+    // software pipelined over two register sets: slice i + 1's loads are in
+    // flight while slice i is computed.  Loads past the last chunk read zero
+    // (no memory traffic); computes past it are skipped.
+    WFrag wa, wb;
+    XFrag xa, xb;
+    issue(0, wa, xa);
+    issue(STEP, wb, xb);
+    if constexpr (XL) publish(std::integral_constant<int, 2 * CPW * CT>{});
+    for (int c0 = 0; c0 < kchunks; c0 += 2 * STEP) {
+      compute(c0, wa, xa);
+      issue(c0 + 2 * STEP, wa, xa);
+      if (c0 + STEP < kchunks) compute(c0 + STEP, wb, xb);
+      issue(c0 + 3 * STEP, wb, xb);
+    }
   }
 
   // reduce the KW waves' partial tiles through LDS, thread t finalises
-  // (c, l, r) = (t / 256, (t / 4) % 64, t % 4)
+  // (c, l, r) = (t / 256, (t / 4) % 64, t % 4); the output has the
+  // activations' type (f16 for int8 and f16 weights, bf16 for bf16)
   __shared__ float red[KW][CT][64][4];
 #pragma unroll
   for (int c = 0; c < CT; ++c)
@@ -301,7 +423,10 @@ __global__ void __launch_bounds__(64 * KW) gemv_packed_kernel(GemvArgs p, const 
     for (int w = 0; w < KW; ++w) s += red[w][c][l][r];
     const int m = 4 * (l >> 4) + r;
     const int64_t n = (int64_t)(t0 + c) * 16 + (l & 15);
-    if (m < p.M && n < p.N) y[(int64_t)m * p.ldy + n] = f32_to_f16_bits(p.scale ? s * p.scale[n] : s);
+    if (m < p.M && n < p.N) {
+      const float v = p.scale ? s * p.scale[n] : s;
+      y[(int64_t)m * p.ldy + n] = WT == DT_BF16 ? f32_to_bf16(v) : f32_to_f16_bits(v);
+    }
   }
 }
 
@@ -340,57 +465,91 @@ int launch_gemv_pack(const int8_t* w, int64_t ldw, int64_t N, int64_t K, int8_t*
   return HXI_OK;
 }
 
-typedef void (*GemvPackedLaunch)(const GemvArgs&, const int8_t*, int, hipStream_t);
-template <int CT, int KW, int CPW, int XS>
-static void gemv_packed_one(const GemvArgs& a, const int8_t* packed, int kchunks, hipStream_t s) {
+typedef void (*GemvStreamLaunch)(const GemvArgs&, const void*, int64_t, int, hipStream_t);
+template <int CT, int KW, int CPW, int XS, bool PIPE, int WT>
+static void gemv_stream_one(const GemvArgs& a, const void* w, int64_t ldw, int kchunks, hipStream_t s) {
+  constexpr int KD = WT == DT_I8 ? 64 : 32;
   const int64_t ntiles = (a.N + 15) / 16;
   const int64_t blocks = (ntiles + CT - 1) / CT;
-  const size_t lds = XS != XS_NONE ? (size_t)a.M * (((kchunks + 7) / 8) * 512 + 8) * 2 : 0;
-  gemv_packed_kernel<CT, KW, CPW, XS><<<dim3((unsigned)blocks), dim3(64 * KW), lds, s>>>(a, packed, kchunks);
+  const size_t lds = XS != XS_NONE ? (size_t)a.M * (((int64_t)kchunks * KD + 511) / 512 * 512 + 8) * 2 : 0;
+  gemv_stream_kernel<CT, KW, CPW, XS, WT, WT == DT_I8, PIPE>
+      <<<dim3((unsigned)blocks), dim3(64 * KW), lds, s>>>(a, w, ldw, kchunks);
 }
-struct GemvPackedEntry {
+struct GemvStreamEntry {
   GemvConfig cfg;
-  GemvPackedLaunch fn;
+  GemvStreamLaunch fn[3];  // int8 (packed image), f16, bf16 (in place)
 };
+#define HX_GV(CT, KW, CPW, XS, PIPE)                                                                     \
+  {&gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_I8>, &gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_F16>, \
+   &gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_BF16>}
 // xl configs (activations staged in LDS) take M <= 4 with the staged rows
 // within 64 KiB of LDS; outside that they run as their register-staged base
-// config (the `base` index).
-static const GemvPackedEntry kGemvPacked[] = {
-    {{2, 8, "packed_ct2_kw8", 0, 0}, &gemv_packed_one<2, 8, 8, XS_NONE>},
-    {{1, 8, "packed_ct1_kw8", 0, 1}, &gemv_packed_one<1, 8, 8, XS_NONE>},
-    {{4, 8, "packed_ct4_kw8", 0, 2}, &gemv_packed_one<4, 8, 4, XS_NONE>},
-    {{2, 4, "packed_ct2_kw4", 0, 3}, &gemv_packed_one<2, 4, 8, XS_NONE>},
-    {{1, 4, "packed_ct1_kw4", 0, 4}, &gemv_packed_one<1, 4, 16, XS_NONE>},
-    {{1, 8, "packed_ct1_kw8_xl", 1, 1}, &gemv_packed_one<1, 8, 8, XS_REG>},
-    {{2, 8, "packed_ct2_kw8_xl", 1, 0}, &gemv_packed_one<2, 8, 8, XS_REG>},
-    {{1, 16, "packed_ct1_kw16_xl", 1, 1}, &gemv_packed_one<1, 16, 4, XS_REG>},
+// config (the `base` index).  The `_p` config is software pipelined over
+// two K slices.
+static const GemvStreamEntry kGemvStream[] = {
+    {{2, 8, "packed_ct2_kw8", 0, 0}, HX_GV(2, 8, 8, XS_NONE, false)},
+    {{1, 8, "packed_ct1_kw8", 0, 1}, HX_GV(1, 8, 8, XS_NONE, false)},
+    {{4, 8, "packed_ct4_kw8", 0, 2}, HX_GV(4, 8, 4, XS_NONE, false)},
+    {{2, 4, "packed_ct2_kw4", 0, 3}, HX_GV(2, 4, 8, XS_NONE, false)},
+    {{1, 4, "packed_ct1_kw4", 0, 4}, HX_GV(1, 4, 16, XS_NONE, false)},
+    {{1, 8, "packed_ct1_kw8_xl", 1, 1}, HX_GV(1, 8, 8, XS_REG, false)},
+    {{2, 8, "packed_ct2_kw8_xl", 1, 0}, HX_GV(2, 8, 8, XS_REG, false)},
+    {{1, 16, "packed_ct1_kw16_xl", 1, 1}, HX_GV(1, 16, 4, XS_REG, false)},
     // 16 waves over K keep the 4-tile activation reuse of ct4 while putting
     // 4x more waves (and weight bytes in flight) on the CUs it occupies
-    {{4, 16, "packed_ct4_kw16", 0, 8}, &gemv_packed_one<4, 16, 2, XS_NONE>},
-    // four tiles with every K chunk of K = 4096 in flight at once (one round
-    // trip to memory) over 16 or 8 waves
-    {{4, 16, "packed_ct4_kw16_c4", 0, 9}, &gemv_packed_one<4, 16, 4, XS_NONE>},
-    {{4, 8, "packed_ct4_kw8_c8", 0, 10}, &gemv_packed_one<4, 8, 8, XS_NONE>},
-    {{1, 8, "packed_ct1_kw8_xd", 1, 1}, &gemv_packed_one<1, 8, 8, XS_DMA>},
+    {{4, 16, "packed_ct4_kw16", 0, 8}, HX_GV(4, 16, 2, XS_NONE, false)},
+    // four tiles with every K chunk of K = 4096 int8 in flight at once (one
+    // round trip to memory) over 16 or 8 waves
+    {{4, 16, "packed_ct4_kw16_c4", 0, 9}, HX_GV(4, 16, 4, XS_NONE, false)},
+    {{4, 8, "packed_ct4_kw8_c8", 0, 10}, HX_GV(4, 8, 8, XS_NONE, false)},
+    {{1, 8, "packed_ct1_kw8_xd", 1, 1}, HX_GV(1, 8, 8, XS_DMA, false)},
+    // software pipelined: f16/bf16 weights with K spanning several slices
+    // (27.5 against 31.1 us at M = 1, N = K = 8192 f16); no int8 shape gains
+    {{1, 16, "packed_ct1_kw16_xl_p", 1, 1}, HX_GV(1, 16, 4, XS_REG, true)},
 };
-int gemv_packed_config_count() { return (int)(sizeof(kGemvPacked) / sizeof(kGemvPacked[0])); }
+#undef HX_GV
+int gemv_packed_config_count() { return (int)(sizeof(kGemvStream) / sizeof(kGemvStream[0])); }
 const GemvConfig* gemv_packed_config(int idx) {
   if (idx < 0 || idx >= gemv_packed_config_count()) return nullptr;
-  return &kGemvPacked[idx].cfg;
+  return &kGemvStream[idx].cfg;
 }
-int launch_gemv_packed(int cfg_idx, const GemvArgs& a, const int8_t* packed, hipStream_t s) {
+
+// Shared by the int8 (packed) and f16/bf16 (in place) launches.
+static int launch_gemv_stream(int cfg_idx, int wt, const GemvArgs& a, const void* w, int64_t ldw,
+                              hipStream_t s) {
   if (cfg_idx < 0 || cfg_idx >= gemv_packed_config_count()) return HXI_ERR_ARG;
   if (a.M < 1 || a.M > 16) return HXI_ERR_SHAPE;
-  const int64_t kchunks = (a.K + 63) / 64;
-  // 32-bit buffer offsets: one workgroup's tiles and the activation rows
-  if ((int64_t)kGemvPacked[cfg_idx].cfg.ct * kchunks * 1024 >= ((int64_t)1 << 31) ||
-      a.M * a.ldx * 2 >= ((int64_t)1 << 31))
-    return HXI_ERR_SHAPE;
+  const int slot = wt == DT_I8 ? 0 : wt == DT_F16 ? 1 : wt == DT_BF16 ? 2 : -1;
+  if (slot < 0) return HXI_ERR_ARG;
+  const int64_t kd = wt == DT_I8 ? 64 : 32;
+  const int64_t kchunks = (a.K + kd - 1) / kd;
+  const int64_t ct = kGemvStream[cfg_idx].cfg.ct;
+  // 32-bit buffer offsets: one workgroup's weight range and the activation rows
+  const int64_t wg_bytes = wt == DT_I8 ? ct * kchunks * 1024 : 16 * ct * ldw * 2;
+  if (wg_bytes >= ((int64_t)1 << 31) || a.M * a.ldx * 2 >= ((int64_t)1 << 31)) return HXI_ERR_SHAPE;
   // xl: staged rows within 64 KiB of LDS
-  if (kGemvPacked[cfg_idx].cfg.xl && (a.M > 4 || a.M * (((kchunks + 7) / 8) * 512 + 8) * 2 > 65536))
-    cfg_idx = kGemvPacked[cfg_idx].cfg.base;
-  kGemvPacked[cfg_idx].fn(a, packed, (int)((a.K + 63) / 64), s);
+  if (kGemvStream[cfg_idx].cfg.xl && (a.M > 4 || a.M * ((kchunks * kd + 511) / 512 * 512 + 8) * 2 > 65536))
+    cfg_idx = kGemvStream[cfg_idx].cfg.base;
+  kGemvStream[cfg_idx].fn[slot](a, w, ldw, (int)kchunks, s);
   return HXI_OK;
+}
+int launch_gemv_packed(int cfg_idx, const GemvArgs& a, const int8_t* packed, hipStream_t s) {
+  return launch_gemv_stream(cfg_idx, DT_I8, a, packed, 0, s);
+}
+const char* gemv_hw_refusal(const GemvArgs& a, const void* w, int64_t ldw) {
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  if (a.M < 1 || a.M > 16 || a.N < 1 || a.K < 1) return "row-count";
+  if (a.K % 8 != 0) return "k-granularity";
+  if ((ldw * 2) % 16 != 0 || (a.ldx * 2) % 16 != 0) return "row-stride";
+  if (!al16(a.x) || !al16(w)) return "unaligned-base";
+  if ((int64_t)64 * ldw * 2 >= ((int64_t)1 << 31) || a.M * a.ldx * 2 >= ((int64_t)1 << 31))
+    return "offset-range";
+  return nullptr;
+}
+int launch_gemv_hw(int cfg_idx, int wt, const GemvArgs& a, const void* w, int64_t ldw, hipStream_t s) {
+  if (wt != DT_F16 && wt != DT_BF16) return HXI_ERR_ARG;
+  if (gemv_hw_refusal(a, w, ldw)) return HXI_ERR_SHAPE;
+  return launch_gemv_stream(cfg_idx, wt, a, w, ldw, s);
 }
 
 typedef void (*GemvLaunch)(const GemvArgs&, hipStream_t);

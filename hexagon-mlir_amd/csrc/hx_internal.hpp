@@ -74,12 +74,12 @@ int launch_gemm(int mode, int cfg_idx, const GemmArgs& a, hipStream_t s);
 // Any shape / alignment; simple tiled kernel, same arithmetic contract.
 int launch_gemm_generic(int mode, const GemmArgs& a, hipStream_t s);
 
-// ---- W8A16 skinny GEMM / GEMV (hx_gemv.hip) ------------------------------
+// ---- decode GEMM / GEMV, M <= 16 (hx_gemv.hip) ---------------------------
 struct GemvArgs {
-  const void* x; int64_t ldx;   // f16 [M][K]
-  const int8_t* w; int64_t ldw; // int8 [N][K] (unregistered weights)
+  const void* x; int64_t ldx;   // f16 [M][K] (bf16 with bf16 weights)
+  const int8_t* w; int64_t ldw; // int8 [N][K] (unregistered int8 weights)
   const float* scale;           // [N], may be null (scale 1)
-  void* y; int64_t ldy;         // f16 [M][N]
+  void* y; int64_t ldy;         // [M][N], the activations' type
   int64_t M, N, K;
 };
 struct GemvConfig {
@@ -100,6 +100,12 @@ int launch_gemv_pack(const int8_t* w_nk, int64_t ldw, int64_t N, int64_t K, int8
 int gemv_packed_config_count();
 const GemvConfig* gemv_packed_config(int idx);
 int launch_gemv_packed(int cfg_idx, const GemvArgs& a, const int8_t* packed, hipStream_t s);
+// f16 / bf16 weights (wt = DT_F16 / DT_BF16) read in place from a
+// K-contiguous [N][K] matrix with row stride ldw (elements); the same config
+// table as the packed int8 kernel.  Null when the shape and layout are
+// taken, else the refusal.
+const char* gemv_hw_refusal(const GemvArgs& a, const void* w, int64_t ldw);
+int launch_gemv_hw(int cfg_idx, int wt, const GemvArgs& a, const void* w, int64_t ldw, hipStream_t s);
 
 // ---- scaled-dot-product attention (hx_attn.hip) --------------------------
 struct AttnArgs {

@@ -235,11 +235,13 @@ enum {
     HX_OP_MATMUL_BF16 = 3,  /* hx_matmul bf16 x bf16 */
     HX_OP_MATMUL_W8 = 4,    /* f16 x int8 GEMM (M > 16) */
     HX_OP_SWIGLU_W8 = 5,    /* fused gate/up GEMM of hx_swiglu_ffn */
-    HX_OP_GEMV_W8 = 6       /* W8A16 decode GEMV (M <= 16) */
+    HX_OP_GEMV_W8 = 6,      /* W8A16 decode GEMV (M <= 16) */
+    HX_OP_GEMV_F16 = 7,     /* f16 x f16 decode GEMV (M <= 16), same configs as 6 */
+    HX_OP_GEMV_BF16 = 8     /* bf16 x bf16 decode GEMV (M <= 16), same configs as 6 */
 };
 
 /* One compiled configuration.  GEMM families fill bm/bn/bk (K elements per
- * LDS stage)/waves_m/waves_n/lds_stages; the GEMV family fills col_tiles
+ * LDS stage)/waves_m/waves_n/lds_stages; the GEMV families fill col_tiles
  * (16-column tiles per wave) and split_k (workgroups per column tile).
  * Replaces the (BM, BN, BK) tile space of enumerate_tile_configs
  * (QHB/backend/hmx_search.py:246-332), widened to the knobs that matter on

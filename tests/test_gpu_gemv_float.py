@@ -1,0 +1,141 @@
+"""GPU parity for the f16 / bf16 decode GEMV (hx_matmul and hx_matmul_resident
+with M <= 16): the streaming kernel reads the K-contiguous [N][K] weight in
+place (argument weights in "nk" layout, "kn" ones after the transpose into
+the workspace, or the resident image).  Against the oracle's binary32
+(i,k,j) product within the float-matmul tolerances (f16: rtol 1e-2 / atol
+1e-3 and the reference's relative-Frobenius gate rel < 2e-3 against the f64
+product; bf16: 2e-2 / 1e-2, rel < 8e-3), for every compiled configuration,
+ragged N and K, the LDS-staged configs past their limit, and a column
+scale.  The plan manifest shows which kernel ran."""
+import numpy as np
+import pytest
+
+from conftest import assert_close, bf16_from_f32, rng, to_dev, to_np
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+OP = {"f16": 7, "bf16": 8}
+TOL = {"f16": (1e-2, 1e-3, 2e-3), "bf16": (2e-2, 1e-2, 8e-3)}
+
+
+def _fp(dtype, shape, seed):
+    x = rng(seed).uniform(-1.0, 1.0, shape).astype(np.float32)
+    return x.astype(np.float16) if dtype == "f16" else bf16_from_f32(x)
+
+
+def _vals(h, dtype):
+    return oracle.bf16_bits_to_f32(h) if dtype == "bf16" else np.asarray(h, np.float32)
+
+
+def _dev(h, dtype, dev):
+    import torch
+    t = to_dev(h.view(np.int16) if dtype == "bf16" else h, dev)
+    return t.view(torch.bfloat16) if dtype == "bf16" else t
+
+
+def _check(got, a, b_kn, dtype, what, scale=None):
+    bf = dtype == "bf16"
+    want = oracle.matmul(a, b_kn, a_bf16=bf, b_bf16=bf, out_bf16=bf,
+                         scale_n=None if scale is None else scale.astype(np.float32))
+    rtol, atol, gate = TOL[dtype]
+    g = _vals(got, dtype)
+    assert_close(g, _vals(want, dtype), rtol, atol, what)
+    exact = _vals(a, dtype).astype(np.float64) @ _vals(b_kn, dtype).astype(np.float64)
+    if scale is not None:
+        exact = exact * scale.astype(np.float64)
+    rel = np.linalg.norm(g - exact) / np.linalg.norm(exact)
+    assert rel < gate, (what, rel)
+
+
+def _plans(hx):
+    return [r["plan"] for r in hx.manifest()["records"]]
+
+
+SHAPES = [(1, 1000, 520), (3, 37, 72), (4, 4096, 4096), (5, 300, 1032), (16, 11008, 4096), (2, 100, 16384)]
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("layout", ["nk", "kn"])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_decode_float_argument(hx, dev, dtype, layout, shape):
+    M, N, K = shape
+    a = _fp(dtype, (M, K), 40)
+    b = _fp(dtype, (K, N), 41)
+    bb = b if layout == "kn" else np.ascontiguousarray(b.T)
+    hx.manifest_enable(True)
+    hx.manifest_clear()
+    try:
+        c = hx.matmul(_dev(a, dtype, dev), _dev(bb, dtype, dev), b_layout=layout)
+        plans = _plans(hx)
+    finally:
+        hx.manifest_enable(False)
+    assert plans == ["gemv-stream"], plans
+    _check(to_np(c), a, b, dtype, f"decode {dtype} {layout} {shape}")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("shape", [(1, 1000, 4160), (4, 300, 8192), (7, 37, 144), (16, 523, 1024)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_decode_float_resident_every_config(hx, dev, dtype, shape):
+    """Every config of the decode family on the resident image (LDS-staged
+    configs run as their base configs past M = 4 or their LDS limit), each
+    deterministic, with a per-column scale."""
+    M, N, K = shape
+    a = _fp(dtype, (M, K), 50)
+    b = _fp(dtype, (K, N), 51)
+    s = rng(52).uniform(0.5, 1.5, N).astype(np.float16)
+    rw = hx.ResidentWeight(_dev(b, dtype, dev), to_dev(s, dev), layout="kn")
+    ad = _dev(a, dtype, dev)
+    op = OP[dtype]
+    try:
+        n = hx.config_count(op)
+        assert n == hx.config_count(6)
+        for cfg in range(n):
+            hx.config_select(op, M, N, K, cfg)
+            try:
+                got = to_np(hx.matmul_resident(ad, rw))
+                again = to_np(hx.matmul_resident(ad, rw))
+            finally:
+                hx.config_select(op, M, N, K, -1)
+            _check(got, a, b, dtype, f"resident {dtype} {shape} cfg {cfg}", scale=s)
+            assert np.array_equal(got.view(np.uint16), again.view(np.uint16)), f"cfg {cfg}: not deterministic"
+    finally:
+        rw.release()
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_decode_float_tuner_shape(hx, dev, dtype):
+    """The reference tuner's decode shape (1, 8192, 8192): resident and
+    argument weights run the same kernel and agree bit for bit."""
+    M, N, K = 1, 8192, 8192
+    a = _fp(dtype, (M, K), 60)
+    b = _fp(dtype, (K, N), 61)
+    bt = _dev(np.ascontiguousarray(b.T), dtype, dev)
+    ad = _dev(a, dtype, dev)
+    rw = hx.ResidentWeight(bt, None, layout="nk")
+    try:
+        res = to_np(hx.matmul_resident(ad, rw))
+        arg = to_np(hx.matmul(ad, bt, b_layout="nk"))
+    finally:
+        rw.release()
+    assert np.array_equal(res.view(np.uint16), arg.view(np.uint16))
+    _check(res, a, b, dtype, f"tuner shape {dtype}")
+
+
+def test_decode_float_falls_back_off_grid(hx, dev):
+    """K not a multiple of 8 is refused by the streaming kernel; the call
+    still runs (the generic MFMA GEMM) and matches the oracle."""
+    M, N, K = 2, 64, 100
+    a = _fp("f16", (M, K), 70)
+    b = _fp("f16", (K, N), 71)
+    hx.manifest_enable(True)
+    hx.manifest_clear()
+    try:
+        c = hx.matmul(to_dev(a, dev), to_dev(b, dev), b_layout="kn")
+        plans = _plans(hx)
+    finally:
+        hx.manifest_enable(False)
+    assert "gemv-stream" not in plans, plans
+    _check(to_np(c), a, b, "f16", "off-grid decode")
