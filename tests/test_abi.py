@@ -68,7 +68,7 @@ def test_dtype_errors_are_reported_before_any_launch(hx):
 
 def test_config_surface(hx):
     total = 0
-    for op in range(1, 7):
+    for op in range(1, 9):
         n = hx.config_count(op)
         assert n >= 3
         for i in range(n):
@@ -77,6 +77,12 @@ def test_config_surface(hx):
             assert c["lds_bytes"] <= 160 * 1024, c
             total += 1
     assert total >= 30
+    # the three decode-GEMV families (int8, f16, bf16 weights) share one table
+    names = [[hx.config_get(op, i)["name"] for i in range(hx.config_count(op))] for op in (6, 7, 8)]
+    assert names[0] == names[1] == names[2]
+    assert hx.config_get(6, 0)["bk"] == 64 and hx.config_get(7, 0)["bk"] == 32
+    with pytest.raises(hx.HXError):
+        hx.config_count(9)
 
 
 def test_missing_library_fails_loudly(hx, monkeypatch, tmp_path):
