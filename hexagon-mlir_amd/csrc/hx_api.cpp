@@ -194,7 +194,8 @@ static int view1(const hx_memref1d* m, int dt, const char* name, int64_t expect,
 // HmxManifest.h:81-110; its JSON export, QHB/backend/utils.py:1055-1196).
 struct PlanCtx {
   const char* entry;   // C entry point the caller used
-  const char* weight;  // "argument", "transposed-to-workspace", "resident-image", "resident-packed"
+  const char* weight;  // "argument", "transposed-to-workspace", "resident-image", "resident-packed",
+                       // "swapped-a-streamed" (N = 1: A streamed as the GEMV weight)
   int a_dt, b_dt;
 };
 
@@ -353,12 +354,13 @@ static int run_gemm(int op, GemmArgs& a, hipStream_t s, const PlanCtx& ctx) {
 }
 
 // f16 / bf16 weights read in place from [N][K] by the streaming GEMV.
-static int run_gemv_hw(GemvArgs& a, int dt, const void* w, int64_t ldw, hipStream_t s, const PlanCtx& ctx) {
+static int run_gemv_hw(GemvArgs& a, int dt, const void* w, int64_t ldw, hipStream_t s, const PlanCtx& ctx,
+                       const char* reason = "min-rows") {
   const int op = dt == HX_BF16 ? HX_OP_GEMV_BF16 : HX_OP_GEMV_F16;
   bool pin = false;
   const int cfg = resolve_gemv(op, a.M, a.N, a.K, &pin);
   note_plan(ctx, a.M, a.N, a.K, dt, "gemv-stream", gemv_packed_config(cfg)->name, pin ? "pinned" : "default",
-            "min-rows");
+            reason);
   return map_internal(launch_gemv_hw(cfg, dt, a, w, ldw, s), "gemv_stream");
 }
 
@@ -456,6 +458,20 @@ extern "C" int hx_matmul(const hx_memref2d* a, int a_dtype, const hx_memref2d* b
     if (vr.rows != M || vr.cols != N) return fail(HX_ERR_SHAPE, "hx_matmul: residual shape");
   }
   if (M == 0 || N == 0) return HX_OK;
+
+  // N = 1 (a matrix-vector product, the reference tuner's (M, K, 1) rows):
+  // C^T = b^T . A^T is the decode GEMV with the [M][K] operand A streamed as
+  // its K-contiguous weight and b as the single activation row, when b and C
+  // are contiguous vectors.  The tiled GEMM would pad N to 32.
+  if (N == 1 && M > 16 && op != HX_OP_MATMUL_W8 && !residual && !col_scale && c_dtype == a_dtype &&
+      (b_layout == HX_LAYOUT_NK || vb.ld == 1) && vc.ld == 1) {
+    GemvArgs v{};
+    v.x = vb.p; v.ldx = K; v.w = nullptr; v.ldw = 0;
+    v.scale = nullptr; v.y = vc.p; v.ldy = M; v.M = 1; v.N = M; v.K = K;
+    if (!gemv_hw_refusal(v, va.p, va.ld))
+      return run_gemv_hw(v, a_dtype, va.p, va.ld, s, PlanCtx{"hx_matmul", "swapped-a-streamed", a_dtype, b_dtype},
+                         "n-is-one");
+  }
 
   const size_t eb = dt_size(b_dtype);
   Carver cv;

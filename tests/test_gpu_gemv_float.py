@@ -139,3 +139,47 @@ def test_decode_float_falls_back_off_grid(hx, dev):
         hx.manifest_enable(False)
     assert "gemv-stream" not in plans, plans
     _check(to_np(c), a, b, "f16", "off-grid decode")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+@pytest.mark.parametrize("mk", [(8192, 4096), (300, 520), (17, 64)], ids=lambda s: "x".join(map(str, s)))
+def test_matvec_n_is_one(hx, dev, dtype, layout, mk):
+    """N = 1 (the reference tuner's (M, K, 1) rows): A [M][K] is streamed as
+    the decode GEMV's weight with b as the single activation row."""
+    M, K = mk
+    a = _fp(dtype, (M, K), 80)
+    b = _fp(dtype, (K, 1), 81)
+    bb = b if layout == "kn" else np.ascontiguousarray(b.T)
+    hx.manifest_enable(True)
+    hx.manifest_clear()
+    try:
+        c = hx.matmul(_dev(a, dtype, dev), _dev(bb, dtype, dev), b_layout=layout)
+        recs = hx.manifest()["records"]
+    finally:
+        hx.manifest_enable(False)
+    assert [(r["plan"], r["weight"], r["reason"]) for r in recs] == [("gemv-stream", "swapped-a-streamed", "n-is-one")]
+    _check(to_np(c), a, b, dtype, f"matvec {dtype} {layout} {mk}")
+
+
+def test_matvec_n_is_one_fallbacks(hx, dev):
+    """A column scale, or an output column that is not contiguous, keeps the
+    N = 1 product on the GEMM path; the result is unchanged."""
+    import torch
+    M, K = 256, 512
+    a = _fp("f16", (M, K), 90)
+    b = _fp("f16", (K, 1), 91)
+    s = rng(92).uniform(0.5, 1.5, 1).astype(np.float16)
+    out = torch.zeros((M, 2), dtype=torch.float16, device=dev)
+    hx.manifest_enable(True)
+    hx.manifest_clear()
+    try:
+        c1 = hx.matmul(to_dev(a, dev), to_dev(b, dev), col_scale=to_dev(s, dev))
+        hx.matmul(to_dev(a, dev), to_dev(b, dev), out=out[:, :1])
+        recs = hx.manifest()["records"]
+    finally:
+        hx.manifest_enable(False)
+    assert all(r["plan"] != "gemv-stream" for r in recs), recs
+    _check(to_np(c1), a, b, "f16", "matvec scaled", scale=s)
+    _check(to_np(out[:, :1].contiguous()), a, b, "f16", "matvec strided out")
+    assert not to_np(out[:, 1:].contiguous()).any()
