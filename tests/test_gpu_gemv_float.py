@@ -71,8 +71,37 @@ def test_decode_float_argument(hx, dev, dtype, layout, shape):
         plans = _plans(hx)
     finally:
         hx.manifest_enable(False)
-    assert plans == ["gemv-stream"], plans
+    # [K][N] weights stream in place when N % 8 == 0, else after the transpose
+    assert plans == ["gemv-kn" if layout == "kn" and N % 8 == 0 else "gemv-stream"], plans
     _check(to_np(c), a, b, dtype, f"decode {dtype} {layout} {shape}")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("shape", [(1, 8192, 8192), (3, 4096, 1032), (16, 128, 4096), (1, 136, 24), (7, 11008, 256)],
+                         ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("scale", [None, "f16", "f32"])
+def test_decode_kn_in_place(hx, dev, dtype, shape, scale):
+    """[K][N] weights read in place (no transpose): one K part or several
+    with the binary32 partial merge, with an f16 or f32 column scale, and a
+    row stride wider than N."""
+    import torch
+    M, N, K = shape
+    a = _fp(dtype, (M, K), 100)
+    b = _fp(dtype, (K, N), 101)
+    s = None if scale is None else rng(102).uniform(0.5, 1.5, N).astype(np.float16)
+    wide = _dev(np.zeros((K, N + 24), b.dtype), dtype, dev)
+    wide[:, :N] = _dev(b, dtype, dev)
+    sd = None if s is None else (to_dev(s, dev) if scale == "f16" else to_dev(s.astype(np.float32), dev))
+    hx.manifest_enable(True)
+    hx.manifest_clear()
+    try:
+        c = hx.matmul(_dev(a, dtype, dev), wide[:, :N], b_layout="kn", col_scale=sd)
+        recs = hx.manifest()["records"]
+    finally:
+        hx.manifest_enable(False)
+    assert [(r["plan"], r["weight"]) for r in recs] == [("gemv-kn", "argument-kn")], recs
+    torch.cuda.synchronize()
+    _check(to_np(c), a, b, dtype, f"kn {dtype} {shape} {scale}", scale=s)
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
