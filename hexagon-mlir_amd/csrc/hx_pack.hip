@@ -35,14 +35,75 @@ __global__ void __launch_bounds__(256) transpose_kernel(const E* __restrict__ sr
   }
 }
 
+// The same 64 x 64 tile with 16-byte global accesses: a row of the tile is
+// 64 * sizeof(E) bytes = 4 * sizeof(E) chunks, so the 256 threads load it in
+// sizeof(E) passes of one chunk each and store the transposed tile the same
+// way, each thread gathering the 16 / sizeof(E) elements of its output chunk
+// from LDS.  The LDS row pitch is 16 bytes longer than the tile row (chunk
+// stores stay 16-byte aligned).  Chunks that reach past the matrix edge move
+// element by element.  Needs 16-byte aligned bases and row strides.
+template <typename E>
+__global__ void __launch_bounds__(256) transpose_vec_kernel(const E* __restrict__ src, int64_t lds,
+                                                            E* __restrict__ dst, int64_t ldd,
+                                                            int64_t rows, int64_t cols) {
+  constexpr int VE = 16 / sizeof(E);     // elements per chunk
+  constexpr int CPR = 64 / VE;           // chunks per tile row
+  constexpr int PITCH = 64 + VE;         // LDS row pitch, elements
+  __shared__ __attribute__((aligned(16))) E tile[64 * PITCH];
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int pass = 0; pass < (int)sizeof(E); ++pass) {
+    const int q = t + 256 * pass;
+    const int r = q / CPR, ch = q % CPR;
+    const int64_t gr = r0 + r, gc = c0 + (int64_t)ch * VE;
+    E* lt = tile + r * PITCH + ch * VE;
+    if (gr < rows && gc + VE <= cols) {
+      *reinterpret_cast<v4u*>(lt) = *reinterpret_cast<const v4u*>(src + gr * lds + gc);
+    } else {
+#pragma unroll
+      for (int i = 0; i < VE; ++i) lt[i] = (gr < rows && gc + i < cols) ? src[gr * lds + gc + i] : E(0);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int pass = 0; pass < (int)sizeof(E); ++pass) {
+    const int q = t + 256 * pass;
+    const int oc = q / CPR, ch = q % CPR;  // output row = input column c0 + oc
+    const int64_t gc = c0 + oc, gr = r0 + (int64_t)ch * VE;
+    if (gc >= cols) continue;
+    E v[VE];
+#pragma unroll
+    for (int i = 0; i < VE; ++i) v[i] = tile[(ch * VE + i) * PITCH + oc];
+    if (gr + VE <= rows) {
+      *reinterpret_cast<v4u*>(dst + gc * ldd + gr) = *reinterpret_cast<const v4u*>(v);
+    } else {
+#pragma unroll
+      for (int i = 0; i < VE; ++i)
+        if (gr + i < rows) dst[gc * ldd + gr + i] = v[i];
+    }
+  }
+}
+
 int launch_transpose(const void* src, int64_t lds, void* dst, int64_t ldd, int64_t rows,
                      int64_t cols, int elem_bytes, hipStream_t s) {
   if (rows <= 0 || cols <= 0) return HXI_OK;
   const dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  const bool vec = al16(src) && al16(dst) && (lds * elem_bytes) % 16 == 0 && (ldd * elem_bytes) % 16 == 0;
   switch (elem_bytes) {
-    case 1: transpose_kernel<uint8_t><<<grid, dim3(256), 0, s>>>((const uint8_t*)src, lds, (uint8_t*)dst, ldd, rows, cols); break;
-    case 2: transpose_kernel<uint16_t><<<grid, dim3(256), 0, s>>>((const uint16_t*)src, lds, (uint16_t*)dst, ldd, rows, cols); break;
-    case 4: transpose_kernel<uint32_t><<<grid, dim3(256), 0, s>>>((const uint32_t*)src, lds, (uint32_t*)dst, ldd, rows, cols); break;
+    case 1:
+      if (vec) transpose_vec_kernel<uint8_t><<<grid, dim3(256), 0, s>>>((const uint8_t*)src, lds, (uint8_t*)dst, ldd, rows, cols);
+      else transpose_kernel<uint8_t><<<grid, dim3(256), 0, s>>>((const uint8_t*)src, lds, (uint8_t*)dst, ldd, rows, cols);
+      break;
+    case 2:
+      if (vec) transpose_vec_kernel<uint16_t><<<grid, dim3(256), 0, s>>>((const uint16_t*)src, lds, (uint16_t*)dst, ldd, rows, cols);
+      else transpose_kernel<uint16_t><<<grid, dim3(256), 0, s>>>((const uint16_t*)src, lds, (uint16_t*)dst, ldd, rows, cols);
+      break;
+    case 4:
+      if (vec) transpose_vec_kernel<uint32_t><<<grid, dim3(256), 0, s>>>((const uint32_t*)src, lds, (uint32_t*)dst, ldd, rows, cols);
+      else transpose_kernel<uint32_t><<<grid, dim3(256), 0, s>>>((const uint32_t*)src, lds, (uint32_t*)dst, ldd, rows, cols);
+      break;
     default: return HXI_ERR_ARG;
   }
   return HXI_OK;
