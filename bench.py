@@ -485,7 +485,7 @@ def traffic_from_pmc(fetch_csv: str, write_csv: str, hx) -> str:
     cw = [v for k, v in write if k == "__amd_rocclr_copyBuffer"][:3]
     f_scale = copy / 1024 / statistics.median(cf)   # counter unit is KiB
     w_scale = copy / 1024 / statistics.median(cw)
-    measured = re.compile(r"void hx::(gemm_kernel|gemm_generic_kernel|gemv_packed_kernel|row_vec_kernel|"
+    measured = re.compile(r"void hx::(gemm_kernel|gemm_generic_kernel|gemv_stream_kernel|row_vec_kernel|"
                           r"row_kernel)<")
     seq = [(k, f * f_scale * 1024 + w * w_scale * 1024) for (k, f), (_, w) in zip(fetch, write)
            if measured.match(k)]
@@ -531,7 +531,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the multi-GPU sharding is design-only, see DESIGN.md)", file=sys.stderr)
+              "(multi-GPU sharding is designed, not built: one GPU's shard is what this bench measures)", file=sys.stderr)
         return 2
 
     import torch
