@@ -316,7 +316,7 @@ static int resolve_gemv(int op, int64_t M, int64_t N, int64_t K, bool* was_pinne
   const int pin = pinned(op, M, N, K);
   if (was_pinned) *was_pinned = pin >= 0 && pin < gemv_packed_config_count();
   if (pin >= 0 && pin < gemv_packed_config_count()) return pin;
-  (void)N;
+  if (M > 16) return gemv_rows_default(M, N);
   if (op != HX_OP_GEMV_W8) {
     // f16 / bf16 weights, untuned choice from the MI355X sweep over
     // N, K in {4096, 8192, 11008}: 16 waves with LDS-staged activations for
@@ -356,7 +356,8 @@ static int run_gemm(int op, GemmArgs& a, hipStream_t s, const PlanCtx& ctx) {
 
 // f16 / bf16 weights read in place from [N][K] by the streaming GEMV.
 static int run_gemv_hw(GemvArgs& a, int dt, const void* w, int64_t ldw, hipStream_t s, const PlanCtx& ctx,
-                       const char* reason = "min-rows") {
+                       const char* reason = nullptr) {
+  if (!reason) reason = a.M <= 16 ? "min-rows" : "few-rows";  // 16 < M <= 64: row-block configs
   const int op = dt == HX_BF16 ? HX_OP_GEMV_BF16 : HX_OP_GEMV_F16;
   bool pin = false;
   const int cfg = resolve_gemv(op, a.M, a.N, a.K, &pin);
@@ -521,7 +522,7 @@ extern "C" int hx_matmul(const hx_memref2d* a, int a_dtype, const hx_memref2d* b
     v.scale = g.col_scale; v.y = g.c; v.ldy = g.ldc; v.M = M; v.N = N; v.K = K;
     if (gemv_fast_ok(v)) return run_gemv(v, s, ctx);
   }
-  if (op != HX_OP_MATMUL_W8 && M <= 16 && !residual && c_dtype == a_dtype) {
+  if (op != HX_OP_MATMUL_W8 && M <= kGemvMaxRows && !residual && c_dtype == a_dtype) {
     GemvArgs v{};
     v.x = g.a; v.ldx = g.lda; v.w = nullptr; v.ldw = 0;
     v.scale = g.col_scale; v.y = g.c; v.ldy = g.ldc; v.M = M; v.N = N; v.K = K;
@@ -861,7 +862,7 @@ static int matmul_resident_impl(const View2& vx, hx_weight* w, const View2* vr, 
   if (M == 0) return HX_OK;
   // The packed GEMV reads activations as 8-element (16-byte) groups, with
   // 32-bit buffer offsets into the activation rows and one workgroup's tiles.
-  if (w->dtype == HX_I8 && w->packed && M <= 16 && !vr && y_dt == HX_F16 && w->K % 8 == 0 &&
+  if (w->dtype == HX_I8 && w->packed && M <= kGemvMaxRows && !vr && y_dt == HX_F16 && w->K % 8 == 0 &&
       ((uintptr_t)vx.p & 15u) == 0 && (vx.ld * 2) % 16 == 0 && M * vx.ld * 2 < ((int64_t)1 << 31) &&
       (w->K + 63) / 64 * 4 * 1024 < ((int64_t)1 << 31)) {
     GemvArgs v{};
@@ -870,10 +871,10 @@ static int matmul_resident_impl(const View2& vx, hx_weight* w, const View2* vr, 
     bool pin = false;
     const int cfg = resolve_gemv(HX_OP_GEMV_W8, M, w->N, w->K, &pin);
     note_plan(PlanCtx{entry, "resident-packed", x_dt, w->dtype}, M, w->N, w->K, HX_F16, "gemv-packed",
-              gemv_packed_config(cfg)->name, pin ? "pinned" : "default", "min-rows");
+              gemv_packed_config(cfg)->name, pin ? "pinned" : "default", M <= 16 ? "min-rows" : "few-rows");
     return map_internal(launch_gemv_packed(cfg, v, w->packed, s), "gemv_packed");
   }
-  if (w->dtype != HX_I8 && M <= 16 && !vr && y_dt == x_dt) {
+  if (w->dtype != HX_I8 && M <= kGemvMaxRows && !vr && y_dt == x_dt) {
     GemvArgs v{};
     v.x = vx.p; v.ldx = vx.ld; v.w = nullptr; v.ldw = 0;
     v.scale = w->scale; v.y = vy.p; v.ldy = vy.ld; v.M = M; v.N = w->N; v.K = w->K;
@@ -943,7 +944,9 @@ extern "C" int hx_swiglu_ffn(const hx_memref2d* x, const hx_memref1d* gamma, flo
   if (gamma && (rc = view1(gamma, HX_F16, "gamma", H, &vg))) return rc;
   if (T == 0) return HX_OK;
 
-  const bool skinny = T <= 16;
+  // up to 64 tokens: the row-block decode GEMVs (T = 17 / 64: 68.9 / 113.4 us
+  // against 78.1 / 119.2 with the fused gate/up GEMM at H = 4096, I = 11008)
+  const bool skinny = T <= kGemvMaxRows;
   Carver cv;
   const size_t off_h = cv.take((size_t)T * H * 2);
   const size_t off_a = cv.take((size_t)T * I * 2);

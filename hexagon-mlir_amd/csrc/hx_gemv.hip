@@ -169,10 +169,13 @@ __device__ __forceinline__ v4f gv_mfma(v4u a, v4u b, v4f c) {
     return mfma16_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c);
 }
 
-template <int CT, int KW, int CPW, int XS, int WT, bool PK, bool PIPE>
+// MB > 1 (16 < M <= 16 MB): MB blocks of 16 activation rows; every weight
+// fragment feeds MB MFMAs, so the weight is still streamed once.
+template <int CT, int KW, int CPW, int XS, int WT, bool PK, bool PIPE, int MB = 1>
 __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const void* wsrc, int64_t ldw,
                                                               int kchunks) {
   static_assert(PK == (WT == DT_I8), "int8 weights stream from the packed image, f16/bf16 in place");
+  static_assert(MB == 1 || (XS == XS_NONE && !PIPE), "row blocks: register-fragment configs only");
   constexpr bool XL = XS != XS_NONE;
   constexpr int KD = WT == DT_I8 ? 64 : 32;  // k per chunk
   constexpr int KG = KD / 4;                  // k per lane group within a chunk
@@ -202,9 +205,11 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
       __builtin_amdgcn_make_buffer_rsrc((void*)x, 0, (int)(p.M * p.ldx * 2), 0x00020000);
   constexpr int kNT = 2;  // cache policy: non-temporal (the weight is streamed once)
 
-  v4f acc[CT];
+  v4f acc[MB][CT];
 #pragma unroll
-  for (int c = 0; c < CT; ++c) acc[c] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int b = 0; b < MB; ++b)
+#pragma unroll
+    for (int c = 0; c < CT; ++c) acc[b][c] = v4f{0.f, 0.f, 0.f, 0.f};
 
   // XL staging of the [M][kp] activation block into LDS, issued ahead of the
   // weight stream.  Rows are XLP elements apart (kp rounded up to whole
@@ -322,7 +327,7 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
             wb = __builtin_bit_cast(v4u, x8x8_to_v8h(wq[u][c][2 * e], wq[u][c][2 * e + 1]));
           else
             wb = wq[u][c];
-          acc[c] = gv_mfma<WT>(xa, wb, acc[c]);
+          acc[0][c] = gv_mfma<WT>(xa, wb, acc[0][c]);
         }
       }
   };
@@ -334,7 +339,7 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
     // which measured up to 2x faster for the wide (CT >= 2, CPW = 8) configs.
     for (int c0 = 0; c0 < kchunks; c0 += STEP) {
       v4u wq[CPW][CT];
-      v4u xq[XL ? 1 : CPW][NE];
+      v4u xq[XL ? 1 : CPW][NE][MB];
 #pragma unroll
       for (int u = 0; u < CPW; ++u) {
         const int j = c0 + wave + KW * u;
@@ -354,12 +359,15 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
         }
         if constexpr (!XL) {
 #pragma unroll
-          for (int e = 0; e < NE; ++e) {
-            const uint32_t k = (uint32_t)j * KD + KG * (uint32_t)g + 8u * e;
-            const uint32_t off = (jv && xrow && k < (uint32_t)p.K)
-                                     ? ((uint32_t)col * (uint32_t)p.ldx + k) * 2u : 0x80000000u;
-            xq[u][e] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0));
-          }
+          for (int e = 0; e < NE; ++e)
+#pragma unroll
+            for (int b = 0; b < MB; ++b) {
+              const uint32_t k = (uint32_t)j * KD + KG * (uint32_t)g + 8u * e;
+              const uint32_t row = (uint32_t)(16 * b + col);
+              const uint32_t off = (jv && row < (uint32_t)p.M && k < (uint32_t)p.K)
+                                       ? (row * (uint32_t)p.ldx + k) * 2u : 0x80000000u;
+              xq[u][e][b] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0));
+            }
         }
       }
       if constexpr (XL)
@@ -368,15 +376,16 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
       for (int u = 0; u < CPW; ++u)
 #pragma unroll
         for (int e = 0; e < NE; ++e) {
-          v4u xa;
+          v4u xa[MB];
           if constexpr (XL) {
             // rows >= M read row 0 and are zeroed after the (unconditional) read
             const int64_t k = (int64_t)(c0 + wave + KW * u) * KD + KG * g + 8 * e;
             const bool in = xrow && k < kp;
             const v4u t = *reinterpret_cast<const v4u*>(xs + (xrow ? col : 0) * xlp + (in ? k : 0));
-            xa = in ? t : v4u{0u, 0u, 0u, 0u};
+            xa[0] = in ? t : v4u{0u, 0u, 0u, 0u};
           } else {
-            xa = xq[u][e];
+#pragma unroll
+            for (int b = 0; b < MB; ++b) xa[b] = xq[u][e][b];
           }
 #pragma unroll
           for (int c = 0; c < CT; ++c) {
@@ -385,7 +394,8 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
               wb = __builtin_bit_cast(v4u, x8x8_to_v8h(wq[u][c][2 * e], wq[u][c][2 * e + 1]));
             else
               wb = wq[u][c];
-            acc[c] = gv_mfma<WT>(xa, wb, acc[c]);
+#pragma unroll
+            for (int b = 0; b < MB; ++b) acc[b][c] = gv_mfma<WT>(xa[b], wb, acc[b][c]);
           }
         }
     }
@@ -406,26 +416,31 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
     }
   }
 
-  // reduce the KW waves' partial tiles through LDS, thread t finalises
-  // (c, l, r) = (t / 256, (t / 4) % 64, t % 4); the output has the
-  // activations' type (f16 for int8 and f16 weights, bf16 for bf16)
+  // reduce the KW waves' partial tiles through LDS, one row block at a
+  // time; thread t finalises (c, l, r) = (t / 256, (t / 4) % 64, t % 4).
+  // The output has the activations' type (f16 for int8 and f16 weights,
+  // bf16 for bf16).
   __shared__ float red[KW][CT][64][4];
-#pragma unroll
-  for (int c = 0; c < CT; ++c)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) red[wave][c][lane][r] = acc[c][r];
-  __syncthreads();
   uint16_t* y = reinterpret_cast<uint16_t*>(p.y);
-  for (int e = tid; e < CT * 256; e += 64 * KW) {
-    const int c = e >> 8, l = (e >> 2) & 63, r = e & 3;
-    float s = 0.f;
 #pragma unroll
-    for (int w = 0; w < KW; ++w) s += red[w][c][l][r];
-    const int m = 4 * (l >> 4) + r;
-    const int64_t n = (int64_t)(t0 + c) * 16 + (l & 15);
-    if (m < p.M && n < p.N) {
-      const float v = p.scale ? s * p.scale[n] : s;
-      y[(int64_t)m * p.ldy + n] = WT == DT_BF16 ? f32_to_bf16(v) : f32_to_f16_bits(v);
+  for (int b = 0; b < MB; ++b) {
+    if (b > 0) __syncthreads();  // the previous block's sums are read
+#pragma unroll
+    for (int c = 0; c < CT; ++c)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wave][c][lane][r] = acc[b][c][r];
+    __syncthreads();
+    for (int e = tid; e < CT * 256; e += 64 * KW) {
+      const int c = e >> 8, l = (e >> 2) & 63, r = e & 3;
+      float s = 0.f;
+#pragma unroll
+      for (int w = 0; w < KW; ++w) s += red[w][c][l][r];
+      const int m = 16 * b + 4 * (l >> 4) + r;
+      const int64_t n = (int64_t)(t0 + c) * 16 + (l & 15);
+      if (m < p.M && n < p.N) {
+        const float v = p.scale ? s * p.scale[n] : s;
+        y[(int64_t)m * p.ldy + n] = WT == DT_BF16 ? f32_to_bf16(v) : f32_to_f16_bits(v);
+      }
     }
   }
 }
@@ -466,13 +481,13 @@ int launch_gemv_pack(const int8_t* w, int64_t ldw, int64_t N, int64_t K, int8_t*
 }
 
 typedef void (*GemvStreamLaunch)(const GemvArgs&, const void*, int64_t, int, hipStream_t);
-template <int CT, int KW, int CPW, int XS, bool PIPE, int WT>
+template <int CT, int KW, int CPW, int XS, bool PIPE, int WT, int MB = 1>
 static void gemv_stream_one(const GemvArgs& a, const void* w, int64_t ldw, int kchunks, hipStream_t s) {
   constexpr int KD = WT == DT_I8 ? 64 : 32;
   const int64_t ntiles = (a.N + 15) / 16;
   const int64_t blocks = (ntiles + CT - 1) / CT;
   const size_t lds = XS != XS_NONE ? (size_t)a.M * (((int64_t)kchunks * KD + 511) / 512 * 512 + 8) * 2 : 0;
-  gemv_stream_kernel<CT, KW, CPW, XS, WT, WT == DT_I8, PIPE>
+  gemv_stream_kernel<CT, KW, CPW, XS, WT, WT == DT_I8, PIPE, MB>
       <<<dim3((unsigned)blocks), dim3(64 * KW), lds, s>>>(a, w, ldw, kchunks);
 }
 struct GemvStreamEntry {
@@ -482,31 +497,43 @@ struct GemvStreamEntry {
 #define HX_GV(CT, KW, CPW, XS, PIPE)                                                                     \
   {&gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_I8>, &gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_F16>, \
    &gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_BF16>}
+#define HX_GR(CT, KW, CPW, MB)                                                                      \
+  {&gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_I8, MB>,                                        \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_F16, MB>,                                       \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_BF16, MB>}
 // xl configs (activations staged in LDS) take M <= 4 with the staged rows
 // within 64 KiB of LDS; outside that they run as their register-staged base
 // config (the `base` index).  The `_p` config is software pipelined over
-// two K slices.
+// two K slices.  `rows` configs hold mb blocks of 16 activation rows; a
+// config whose blocks cannot hold M runs as the row-block default.
 static const GemvStreamEntry kGemvStream[] = {
-    {{2, 8, "packed_ct2_kw8", 0, 0}, HX_GV(2, 8, 8, XS_NONE, false)},
-    {{1, 8, "packed_ct1_kw8", 0, 1}, HX_GV(1, 8, 8, XS_NONE, false)},
-    {{4, 8, "packed_ct4_kw8", 0, 2}, HX_GV(4, 8, 4, XS_NONE, false)},
-    {{2, 4, "packed_ct2_kw4", 0, 3}, HX_GV(2, 4, 8, XS_NONE, false)},
-    {{1, 4, "packed_ct1_kw4", 0, 4}, HX_GV(1, 4, 16, XS_NONE, false)},
-    {{1, 8, "packed_ct1_kw8_xl", 1, 1}, HX_GV(1, 8, 8, XS_REG, false)},
-    {{2, 8, "packed_ct2_kw8_xl", 1, 0}, HX_GV(2, 8, 8, XS_REG, false)},
-    {{1, 16, "packed_ct1_kw16_xl", 1, 1}, HX_GV(1, 16, 4, XS_REG, false)},
+    {{2, 8, "packed_ct2_kw8", 0, 0, 1}, HX_GV(2, 8, 8, XS_NONE, false)},
+    {{1, 8, "packed_ct1_kw8", 0, 1, 1}, HX_GV(1, 8, 8, XS_NONE, false)},
+    {{4, 8, "packed_ct4_kw8", 0, 2, 1}, HX_GV(4, 8, 4, XS_NONE, false)},
+    {{2, 4, "packed_ct2_kw4", 0, 3, 1}, HX_GV(2, 4, 8, XS_NONE, false)},
+    {{1, 4, "packed_ct1_kw4", 0, 4, 1}, HX_GV(1, 4, 16, XS_NONE, false)},
+    {{1, 8, "packed_ct1_kw8_xl", 1, 1, 1}, HX_GV(1, 8, 8, XS_REG, false)},
+    {{2, 8, "packed_ct2_kw8_xl", 1, 0, 1}, HX_GV(2, 8, 8, XS_REG, false)},
+    {{1, 16, "packed_ct1_kw16_xl", 1, 1, 1}, HX_GV(1, 16, 4, XS_REG, false)},
     // 16 waves over K keep the 4-tile activation reuse of ct4 while putting
     // 4x more waves (and weight bytes in flight) on the CUs it occupies
-    {{4, 16, "packed_ct4_kw16", 0, 8}, HX_GV(4, 16, 2, XS_NONE, false)},
+    {{4, 16, "packed_ct4_kw16", 0, 8, 1}, HX_GV(4, 16, 2, XS_NONE, false)},
     // four tiles with every K chunk of K = 4096 int8 in flight at once (one
     // round trip to memory) over 16 or 8 waves
-    {{4, 16, "packed_ct4_kw16_c4", 0, 9}, HX_GV(4, 16, 4, XS_NONE, false)},
-    {{4, 8, "packed_ct4_kw8_c8", 0, 10}, HX_GV(4, 8, 8, XS_NONE, false)},
-    {{1, 8, "packed_ct1_kw8_xd", 1, 1}, HX_GV(1, 8, 8, XS_DMA, false)},
+    {{4, 16, "packed_ct4_kw16_c4", 0, 9, 1}, HX_GV(4, 16, 4, XS_NONE, false)},
+    {{4, 8, "packed_ct4_kw8_c8", 0, 10, 1}, HX_GV(4, 8, 8, XS_NONE, false)},
+    {{1, 8, "packed_ct1_kw8_xd", 1, 1, 1}, HX_GV(1, 8, 8, XS_DMA, false)},
     // software pipelined: f16/bf16 weights with K spanning several slices
     // (27.5 against 31.1 us at M = 1, N = K = 8192 f16); no int8 shape gains
-    {{1, 16, "packed_ct1_kw16_xl_p", 1, 1}, HX_GV(1, 16, 4, XS_REG, true)},
+    {{1, 16, "packed_ct1_kw16_xl_p", 1, 1, 1}, HX_GV(1, 16, 4, XS_REG, true)},
+    {{1, 8, "rows2_ct1_kw8", 0, 13, 2}, HX_GR(1, 8, 8, 2)},
+    {{2, 8, "rows2_ct2_kw8", 0, 14, 2}, HX_GR(2, 8, 4, 2)},
+    {{1, 8, "rows4_ct1_kw8", 0, 15, 4}, HX_GR(1, 8, 4, 4)},
+    {{2, 8, "rows4_ct2_kw8", 0, 16, 4}, HX_GR(2, 8, 4, 4)},
+    {{4, 8, "rows4_ct4_kw8", 0, 17, 4}, HX_GR(4, 8, 2, 4)},
+    {{1, 4, "rows4_ct1_kw4", 0, 18, 4}, HX_GR(1, 4, 8, 4)},
 };
+#undef HX_GR
 #undef HX_GV
 int gemv_packed_config_count() { return (int)(sizeof(kGemvStream) / sizeof(kGemvStream[0])); }
 const GemvConfig* gemv_packed_config(int idx) {
@@ -518,7 +545,9 @@ const GemvConfig* gemv_packed_config(int idx) {
 static int launch_gemv_stream(int cfg_idx, int wt, const GemvArgs& a, const void* w, int64_t ldw,
                               hipStream_t s) {
   if (cfg_idx < 0 || cfg_idx >= gemv_packed_config_count()) return HXI_ERR_ARG;
-  if (a.M < 1 || a.M > 16) return HXI_ERR_SHAPE;
+  if (a.M < 1 || a.M > kGemvMaxRows) return HXI_ERR_SHAPE;
+  // a config whose row blocks cannot hold M runs as the row-block default
+  if (a.M > 16 * kGemvStream[cfg_idx].cfg.mb) cfg_idx = gemv_rows_default(a.M, a.N);
   const int slot = wt == DT_I8 ? 0 : wt == DT_F16 ? 1 : wt == DT_BF16 ? 2 : -1;
   if (slot < 0) return HXI_ERR_ARG;
   const int64_t kd = wt == DT_I8 ? 64 : 32;
@@ -533,12 +562,19 @@ static int launch_gemv_stream(int cfg_idx, int wt, const GemvArgs& a, const void
   kGemvStream[cfg_idx].fn[slot](a, w, ldw, (int)kchunks, s);
   return HXI_OK;
 }
+// Measured at M = 17..64 (rotating resident weights): four tiles and four
+// row blocks when N leaves >= 160 such workgroups (int8 and f16,
+// N = 11008), else one tile with two or four row blocks (f16, N = 4096).
+int gemv_rows_default(int64_t M, int64_t N) {
+  if (N >= 160 * 64) return 17;
+  return M <= 32 ? 13 : 15;
+}
 int launch_gemv_packed(int cfg_idx, const GemvArgs& a, const int8_t* packed, hipStream_t s) {
   return launch_gemv_stream(cfg_idx, DT_I8, a, packed, 0, s);
 }
 const char* gemv_hw_refusal(const GemvArgs& a, const void* w, int64_t ldw) {
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
-  if (a.M < 1 || a.M > 16 || a.N < 1 || a.K < 1) return "row-count";
+  if (a.M < 1 || a.M > kGemvMaxRows || a.N < 1 || a.K < 1) return "row-count";
   if (a.K % 8 != 0) return "k-granularity";
   if ((ldw * 2) % 16 != 0 || (a.ldx * 2) % 16 != 0) return "row-stride";
   if (!al16(a.x) || !al16(w)) return "unaligned-base";

@@ -87,7 +87,12 @@ struct GemvConfig {
   const char* name;
   int xl;            // activations staged in LDS (M <= 4, rows within 64 KiB)
   int base;          // config that runs outside the xl limits
+  int mb;            // 16-row activation blocks (M <= 16 mb)
 };
+// Largest M the decode GEMV takes (row-block configs).
+constexpr int kGemvMaxRows = 64;
+// Untuned row-block config for 16 < M <= kGemvMaxRows.
+int gemv_rows_default(int64_t M, int64_t N);
 bool gemv_fast_ok(const GemvArgs& a);
 const char* gemv_fast_refusal(const GemvArgs& a);
 // Column tiles per workgroup (1, 2 or 4 as index 0..2) of the [N][K] kernel.

@@ -212,3 +212,66 @@ def test_matvec_n_is_one_fallbacks(hx, dev):
     _check(to_np(c1), a, b, "f16", "matvec scaled", scale=s)
     _check(to_np(out[:, :1].contiguous()), a, b, "f16", "matvec strided out")
     assert not to_np(out[:, 1:].contiguous()).any()
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("shape", [(17, 1000, 520), (32, 4096, 4096), (48, 11008, 1024), (64, 300, 8192), (63, 37, 72)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_decode_float_row_blocks(hx, dev, dtype, shape):
+    """16 < M <= 64: the streaming kernel with 2 or 4 blocks of 16 activation
+    rows (each weight fragment feeds every block), argument and resident."""
+    M, N, K = shape
+    a = _fp(dtype, (M, K), 110)
+    b = _fp(dtype, (K, N), 111)
+    bt = _dev(np.ascontiguousarray(b.T), dtype, dev)
+    hx.manifest_enable(True)
+    hx.manifest_clear()
+    try:
+        c = hx.matmul(_dev(a, dtype, dev), bt, b_layout="nk")
+        recs = hx.manifest()["records"]
+    finally:
+        hx.manifest_enable(False)
+    assert [r["plan"] for r in recs] == ["gemv-stream"] and recs[0]["config"].startswith("rows"), recs
+    _check(to_np(c), a, b, dtype, f"rows {dtype} {shape}")
+    rw = hx.ResidentWeight(bt, None, layout="nk")
+    try:
+        _check(to_np(hx.matmul_resident(_dev(a, dtype, dev), rw)), a, b, dtype, f"rows resident {dtype} {shape}")
+    finally:
+        rw.release()
+
+
+def test_decode_row_blocks_every_config(hx, dev):
+    """Every config of the shared table at M = 40 (f16) and M = 24 (int8):
+    configs with too few row blocks run as the row-block default."""
+    M, N, K = 40, 523, 1024
+    a = _fp("f16", (M, K), 120)
+    b = _fp("f16", (K, N), 121)
+    rw = hx.ResidentWeight(_dev(b, "f16", dev), None, layout="kn")
+    ad = _dev(a, "f16", dev)
+    try:
+        for cfg in range(hx.config_count(7)):
+            hx.config_select(7, M, N, K, cfg)
+            try:
+                got = to_np(hx.matmul_resident(ad, rw))
+            finally:
+                hx.config_select(7, M, N, K, -1)
+            _check(got, a, b, "f16", f"rows every config {cfg}")
+    finally:
+        rw.release()
+    M = 24
+    x = rng(122).normal(0, 1, (M, K)).astype(np.float16)
+    w = rng(123).integers(-127, 128, (K, N), dtype=np.int8)
+    s = rng(124).uniform(0.001, 0.02, N).astype(np.float16)
+    want = oracle.matmul(x, w, scale_n=s.astype(np.float32)).astype(np.float32)
+    rw = hx.ResidentWeight(to_dev(w, dev), to_dev(s, dev))
+    xd = to_dev(x, dev)
+    try:
+        for cfg in range(hx.config_count(6)):
+            hx.config_select(6, M, N, K, cfg)
+            try:
+                got = to_np(hx.matmul_resident(xd, rw)).astype(np.float32)
+            finally:
+                hx.config_select(6, M, N, K, -1)
+            assert_close(got, want, 1e-2, 1e-3, f"int8 rows cfg {cfg}")
+    finally:
+        rw.release()

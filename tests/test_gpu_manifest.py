@@ -37,7 +37,8 @@ def test_manifest_records_plans_and_reasons(hx, dev):
         rw = hx.ResidentWeight(w, s, layout="nk")
         try:
             hx.matmul_resident(x, rw)                            # packed decode GEMV
-            hx.matmul_resident(torch.randn((64, 512), dtype=torch.float16, device=dev), rw)
+            hx.matmul_resident(torch.randn((64, 512), dtype=torch.float16, device=dev), rw)   # row blocks
+            hx.matmul_resident(torch.randn((128, 512), dtype=torch.float16, device=dev), rw)  # tiled
         finally:
             rw.release()
         torch.cuda.synchronize()
@@ -63,6 +64,8 @@ def test_manifest_records_plans_and_reasons(hx, dev):
     assert find(entry="hx_matmul", m=4, plan="gemv")["reason"] == "min-rows"
     assert find(entry="hx_matmul_resident", m=4)["plan"] == "gemv-packed"
     r = find(entry="hx_matmul_resident", m=64)
+    assert r["plan"] == "gemv-packed" and r["reason"] == "few-rows" and r["config"].startswith("rows")
+    r = find(entry="hx_matmul_resident", m=128)
     assert r["plan"] == "mfma-tiled" and r["weight"] == "resident-image" and r["b"] == "i8"
 
 
