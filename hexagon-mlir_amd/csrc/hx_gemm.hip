@@ -1,589 +1,10 @@
-// hx_gemm.hip -- MFMA GEMM family for gfx950: int8 x int8 -> int32,
-// f16/bf16 x f16/bf16 -> f32, and f16 x int8 (W8A16, weights widened to f16
-// in registers) -> f32, with fused epilogues (int32 store, per-row/per-column
-// dequant to fp16, per-channel scale + residual, SwiGLU gate*up).
-//
-// What it replaces in hexagon-mlir (QHB = qcom_hexagon_backend):
-//   * the HMX tile loop -- hmx-partition's (m,n) loop with K batches of up to
-//     32 croutons per hmx_mma_f16 and a staged activation ring
-//     (QHB/lib/Dialect/Hmx/Transforms/HmxPartitionPass.cpp:783-866, 2001-2066)
-//     and the leaf itself (QHB/bin/runtime/hmx/src/HMXAPI.c:47-55);
-//   * the HVX (i,k,j) generic that int8 and skinny matmuls fall back to
-//     (QHB/lib/Transforms/ScheduleMatmulForHVXPass.cpp:169-196);
-//   * the fused read-out (HMXAPI.c:30-44, HMXLayout.c:692-999).
-//
-// Design (MI355X-first, not a translation of the crouton scheme):
-//   * one workgroup per BMxBN output tile; a tile is split over WMxWN waves,
-//     each owning (BM/WM)x(BN/WN) = TMxTN MFMA 32x32 sub-tiles whose
-//     accumulators stay in registers for the whole K loop;
-//   * K is walked in stages of 128 bytes of A per row, double-buffered in
-//     LDS; each stage is fetched with direct-to-LDS 16-byte buffer loads
-//     (out-of-range rows and the K tail read as zero from the buffer
-//     descriptor's range), one LDS-only barrier per stage;
-//   * LDS rows are 128 (or 64) bytes with the 16-byte chunk index XOR-swizzled
-//     by the row so that the MFMA operand reads (16 bytes per lane, 32 rows)
-//     and the stage writes are bank-conflict free;
-//   * operand fragments are double-buffered in registers (the reads of k-step
-//     s+1 are in flight while the MFMAs of step s run);
-//   * B is consumed K-contiguous ([N][K]), i.e. the weight image the resident
-//     registry keeps -- the counterpart of the reference's pre-packed WH
-//     crouton image (QHB/backend/hmx_weight_prepack.py:171-212);
-//   * the epilogue converts each wave's block in LDS and writes whole rows;
-//   * workgroup ids are renumbered so that each XCD (workgroups are dealt to
-//     the 8 XCDs round robin) walks a compact block of tiles: the B strips of
-//     that block stay resident in the XCD's L2 while its M-tiles go by.
-#include "hx_device.hpp"
-#include "hx_internal.hpp"
-#include <type_traits>
+// hx_gemm.hip -- dispatch of the MFMA GEMM family (config tables, untuned
+// default choice, fast-path preconditions) and the generic any-shape kernel.
+// The tiled kernel template is in hx_gemm_kernel.hpp; its per-mode config
+// tables are in hx_gemm_{i8,f16,bf16,w8}.hip.
+#include "hx_gemm_kernel.hpp"
 
 namespace hx {
-
-template <int MODE> struct ModeTraits;
-template <> struct ModeTraits<GM_I8> {
-  static constexpr int EA = 1, EB = 1;  // operand element bytes
-  typedef v16i Acc;
-};
-template <> struct ModeTraits<GM_F16> {
-  static constexpr int EA = 2, EB = 2;
-  typedef v16f Acc;
-};
-template <> struct ModeTraits<GM_BF16> {
-  static constexpr int EA = 2, EB = 2;
-  typedef v16f Acc;
-};
-template <> struct ModeTraits<GM_W8> {
-  static constexpr int EA = 2, EB = 1, BK = 64, BROW = 64;
-  typedef v16f Acc;
-};
-
-// Chunk swizzles.  For 128-byte rows, (row ^ row>>3) & 7 makes any 8 and any
-// 16 consecutive rows reading the same logical chunk hit distinct bank groups
-// (both the 32-bank/8-lane and the 64-bank/16-lane service patterns).  The
-// 64-byte variant does the same for the int8 W8 weight rows.
-__device__ __forceinline__ int swz128(int row) { return (row ^ (row >> 3)) & 7; }
-__device__ __forceinline__ int swz64(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
-
-template <int MODE>
-__device__ __forceinline__ typename ModeTraits<MODE>::Acc mfma32(v4i a, v4i b,
-                                                                 typename ModeTraits<MODE>::Acc c) {
-  if constexpr (MODE == GM_I8) return mfma32_i8(a, b, c);
-  else if constexpr (MODE == GM_BF16) return mfma32_bf16(a, b, c);
-  else return mfma32_f16(a, b, c);
-}
-
-__device__ __forceinline__ void store_out(void* c, int dt, int64_t idx, float v) {
-  if (dt == DT_F16) reinterpret_cast<uint16_t*>(c)[idx] = f32_to_f16_bits(v);
-  else if (dt == DT_BF16) reinterpret_cast<uint16_t*>(c)[idx] = f32_to_bf16(v);
-  else reinterpret_cast<float*>(c)[idx] = v;
-}
-__device__ __forceinline__ float load_any(const void* p, int dt, int64_t idx) {
-  if (dt == DT_F16) return f16_bits_to_f32(reinterpret_cast<const uint16_t*>(p)[idx]);
-  if (dt == DT_BF16) return bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[idx]);
-  return reinterpret_cast<const float*>(p)[idx];
-}
-
-// Map a workgroup to its output tile.  Workgroup b runs on XCD b % 8; the
-// renumbering makes the tiles of one XCD a contiguous run of `lin`, and the
-// grouped order turns that run into a GROUP_M x k block of tiles.
-__device__ __forceinline__ void tile_of(int tiles_m, int tiles_n, int& tm, int& tn) {
-  const int ntiles = tiles_m * tiles_n;
-  int lin = blockIdx.x;
-  if ((ntiles & 7) == 0) lin = (blockIdx.x & 7) * (ntiles >> 3) + (blockIdx.x >> 3);
-  constexpr int GROUP_M = 4;
-  const int per_group = GROUP_M * tiles_n;
-  const int group = lin / per_group;
-  const int first_m = group * GROUP_M;
-  const int gm = min(tiles_m - first_m, GROUP_M);
-  const int in_group = lin - group * per_group;
-  tm = first_m + in_group % gm;
-  tn = in_group / gm;
-}
-
-__device__ __forceinline__ v4f load4(const void* p, int dt, int64_t idx) {
-  if (dt == DT_F32) return *reinterpret_cast<const v4f*>(reinterpret_cast<const float*>(p) + idx);
-  const v2i w = *reinterpret_cast<const v2i*>(reinterpret_cast<const uint16_t*>(p) + idx);
-  const uint32_t lo = (uint32_t)w[0], hi = (uint32_t)w[1];
-  if (dt == DT_F16)
-    return v4f{f16_bits_to_f32((uint16_t)lo), f16_bits_to_f32((uint16_t)(lo >> 16)),
-               f16_bits_to_f32((uint16_t)hi), f16_bits_to_f32((uint16_t)(hi >> 16))};
-  return v4f{bf16_to_f32((uint16_t)lo), bf16_to_f32((uint16_t)(lo >> 16)), bf16_to_f32((uint16_t)hi),
-             bf16_to_f32((uint16_t)(hi >> 16))};
-}
-
-// Scheduling recipe for the step that follows a stage barrier: NREAD LDS
-// reads first, then NMF MFMAs with the NVM direct loads spread after them.
-template <int NREAD, int NMF, int NVM>
-__device__ __forceinline__ void interleave_reads_mfma_vmem() {
-  constexpr int PER = (NVM + NMF - 1) / NMF;  // loads after each MFMA
-  __builtin_amdgcn_sched_group_barrier(0x100, NREAD, 0);  // DS reads
-  static_for<NMF>([](auto) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // one MFMA
-    __builtin_amdgcn_sched_group_barrier(0x020, PER, 0);  // its share of the direct loads
-  });
-}
-
-// SB: bytes of A per row in one K stage (128; 64 halves the LDS so that two
-// 4-wave workgroups share a CU with independent stage barriers -- measured
-// at 4096^3 as 76 us against 59 us for the 8-wave 256x256 tile, so no table
-// entry uses it).  MINW: waves per SIMD the register budget must allow (2
-// caps a wave at 256 registers).
-template <int MODE, int BM, int BN, int WM, int WN, int EPI, int SB = 128, int MINW = 1>
-__global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(MINW, 8)))
-gemm_kernel(GemmArgs p) {
-  typedef ModeTraits<MODE> T;
-  typedef typename T::Acc Acc;
-  static_assert(SB == 128 || (SB == 64 && MODE != GM_W8), "stage width");
-  constexpr int NW = WM * WN;
-  constexpr int NB = (EPI == GE_SWIGLU) ? 2 : 1;
-  constexpr int BROW = (MODE == GM_W8) ? SB / 2 : SB;  // bytes of B per row in one stage
-  constexpr int KSTEPS = SB / 32;                      // MFMA k-steps per stage
-  constexpr int A_BYTES = BM * SB;
-  constexpr int B_BYTES = BN * BROW;
-  constexpr int STAGE = A_BYTES + NB * B_BYTES;
-  // 1 KiB direct-load blocks: 8 rows of a 128-byte row, or 16 of a 64-byte row
-  constexpr int A_BLK = A_BYTES / 1024;
-  constexpr int B_BLK = B_BYTES / 1024;
-  constexpr int A_RPB = 1024 / SB;
-  constexpr int B_RPB = 1024 / BROW;
-  constexpr int A_PER_W = A_BLK / NW;
-  constexpr int B_PER_W = B_BLK / NW;
-  constexpr int P = A_PER_W + NB * B_PER_W;  // direct loads per wave per stage
-  static_assert(A_BLK % NW == 0 && B_BLK % NW == 0, "block split");
-  constexpr int WTM = BM / WM, WTN = BN / WN;
-  constexpr int TM = WTM / 32, TN = WTN / 32;
-  static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
-  static_assert(2 * STAGE <= 160 * 1024, "LDS budget");
-  static_assert(2 * P < 64, "vmcnt range");
-
-  // Two stages as two distinct arrays: the compiler can then see that a
-  // direct load into one stage never aliases the reads of the other.
-  __shared__ __attribute__((aligned(1024))) char st0[STAGE];
-  // per-row / per-column scales of this tile, fetched in the prologue
-  // (SC_ROWS floats each: one 1 KiB direct load covers 256)
-  constexpr int SC_ROWS = (BM > BN ? BM : BN) < 256 ? 256 : (BM > BN ? BM : BN);
-  __shared__ __attribute__((aligned(1024))) float scl[(1 + NB) * SC_ROWS];
-  __shared__ __attribute__((aligned(1024))) char st1[STAGE];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  // wave index as a provably uniform (scalar) value: the direct-load LDS
-  // address and scalar offset derive from it and must live in SGPRs
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave / WN, wn = wave % WN;
-  const int tiles_m = (int)((p.M + BM - 1) / BM);
-  const int tiles_n = (int)((p.N + BN - 1) / BN);
-  int tm, tn;
-  tile_of(tiles_m, tiles_n, tm, tn);
-  // The tile coordinates are workgroup-uniform, but the integer divisions in
-  // tile_of run on the vector ALU; readfirstlane states the uniformity, so
-  // the buffer descriptors built from them stay scalar (a descriptor the
-  // compiler believes divergent turns every buffer load into a loop over
-  // lanes).
-  tm = __builtin_amdgcn_readfirstlane(tm);
-  tn = __builtin_amdgcn_readfirstlane(tn);
-  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-  const int64_t rows_a = min((int64_t)BM, p.M - m0);
-  const int64_t rows_b = min((int64_t)BN, p.N - n0);
-  const uint32_t lda_b = (uint32_t)(p.lda * T::EA);
-  const uint32_t ldb_b = (uint32_t)(p.ldb * T::EB);
-  const uint32_t ka_bytes = (uint32_t)(p.K * T::EA);
-
-  __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(reinterpret_cast<const char*>(p.a) + m0 * lda_b), 0, (int)(rows_a * lda_b), 0x00020000);
-  __amdgpu_buffer_rsrc_t rb[NB];
-  rb[0] = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(reinterpret_cast<const char*>(p.b) + n0 * ldb_b), 0, (int)(rows_b * ldb_b), 0x00020000);
-  if constexpr (NB == 2)
-    rb[1] = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(reinterpret_cast<const char*>(p.b2) + n0 * ldb_b), 0, (int)(rows_b * ldb_b),
-        0x00020000);
-
-  // Direct-load addressing.  Lane L of a 1 KiB block fills physical chunk
-  // L % cpr of block row L / cpr (cpr = 16-byte chunks per row) and fetches
-  // the logical chunk the XOR swizzle maps there.  The block's first row is
-  // a wave-uniform offset (the instruction's scalar offset); the lane part
-  // is a row offset plus the swizzled chunk, recomputed per block from the
-  // block index rather than kept in registers.
-  const uint32_t a_lane_row = (uint32_t)(SB == 128 ? (lane >> 3) : (lane >> 2)) * lda_b;
-  const uint32_t b_lane_row = (uint32_t)(BROW == 128 ? (lane >> 3) : (lane >> 2)) * ldb_b;
-  constexpr int BKE = SB / T::EA;  // elements of K per stage
-  const int nk = (int)((p.K + BKE - 1) / BKE);
-  const uint32_t kb_bytes = (uint32_t)(p.K * T::EB);
-
-  // Enqueue the direct loads of K-stage kt into `st`.  Only the last stage
-  // can overhang K; its chunks past K read as zero (offset out of range).
-  // MASK = false is for stages known not to be the last one.
-  auto dma_stage = [&](char* st, int kt, auto maskc) {
-    constexpr bool MASK = decltype(maskc)::value;
-    const uint32_t ka = (uint32_t)kt * (uint32_t)SB;
-    const uint32_t kb = (uint32_t)kt * (uint32_t)BROW;
-    const bool tail = MASK && ka + (uint32_t)SB > ka_bytes;
-    static_for<A_PER_W>([&](auto ic) {
-      const int blk = wave + decltype(ic)::value * NW;
-      uint32_t kc;
-      if constexpr (SB == 128) {
-        // row = 8*blk + lane/8, so swz128(row) = (lane/8 ^ blk) & 7
-        kc = (uint32_t)(((lane & 7) ^ (lane >> 3) ^ blk) & 7) * 16u;
-      } else {
-        const int row = blk * 16 + (lane >> 2);
-        kc = (uint32_t)((lane & 3) ^ swz64(row)) * 16u;
-      }
-      uint32_t off = a_lane_row + kc + ka;
-      if (tail && ka + kc >= ka_bytes) off = 0x80000000u;
-      dma16(ra, st + blk * 1024, off, (uint32_t)blk * (uint32_t)A_RPB * lda_b);
-    });
-    static_for<NB>([&](auto nbc) {
-      constexpr int nb = decltype(nbc)::value;
-      static_for<B_PER_W>([&](auto ic) {
-        const int blk = wave + decltype(ic)::value * NW;
-        uint32_t kc;
-        if constexpr (BROW == 128) {
-          kc = (uint32_t)(((lane & 7) ^ (lane >> 3) ^ blk) & 7) * 16u;
-        } else {
-          const int row = blk * 16 + (lane >> 2);
-          kc = (uint32_t)((lane & 3) ^ swz64(row)) * 16u;
-        }
-        uint32_t off = b_lane_row + kc + kb;
-        if (tail && kb + kc >= kb_bytes) off = 0x80000000u;
-        dma16(rb[nb], st + A_BYTES + nb * B_BYTES + blk * 1024, off,
-              (uint32_t)blk * (uint32_t)B_RPB * ldb_b);
-      });
-    });
-  };
-
-  Acc acc[NB][TM][TN];
-  static_for<NB>([&](auto nbc) {
-    static_for<TM>([&](auto ic) {
-      static_for<TN>([&](auto jc) {
-        acc[decltype(nbc)::value][decltype(ic)::value][decltype(jc)::value] = Acc{};
-      });
-    });
-  });
-
-  const int lrow = lane & 31, lg = lane >> 5;
-
-  // Operand fragments, double-buffered in registers: while the MFMAs of
-  // k-step ks run, the LDS reads of step ks+1 are in flight.  A stage is
-  // KSTEPS k-steps.  For W8 one 16-byte int8 B read covers two steps (it is widened
-  // to f16 half by half), so B is read on even steps into its own pair of
-  // buffers, indexed by the step pair.
-  v4i fa[2][TM];
-  v4i fb[2][NB][TN];
-
-  auto read_frags = [&](const char* sa, auto ksc) {
-    constexpr int ks = decltype(ksc)::value;
-    constexpr int s = ks & 1;
-    // step ks reads A chunk ca (W8: A is f16, step ks = 2*jp + h covers
-    // k = 32*jp + 16*g + 8*h + (0..7) for lane group g, both operands, so
-    // every k of the stage is summed exactly once)
-    const int ca = (MODE != GM_W8) ? ks * 2 + lg : 4 * (ks >> 1) + 2 * lg + (ks & 1);
-    auto swz = [](int row) -> int {
-      if constexpr (SB == 128) return swz128(row);
-      else return swz64(row);
-    };
-    static_for<TM>([&](auto ic) {
-      constexpr int i = decltype(ic)::value;
-      const int row = wm * WTM + i * 32 + lrow;
-      fa[s][i] = *reinterpret_cast<const v4i*>(sa + row * SB + ((ca ^ swz(row)) << 4));
-    });
-    if constexpr (MODE != GM_W8) {
-      static_for<NB>([&](auto nbc) {
-        constexpr int nb = decltype(nbc)::value;
-        static_for<TN>([&](auto jc) {
-          constexpr int j = decltype(jc)::value;
-          const int row = wn * WTN + j * 32 + lrow;
-          fb[s][nb][j] = *reinterpret_cast<const v4i*>(sa + A_BYTES + nb * B_BYTES + row * SB +
-                                                       ((ca ^ swz(row)) << 4));
-        });
-      });
-    } else if constexpr ((ks & 1) == 0) {
-      constexpr int jp = ks >> 1;
-      const int cb = 2 * jp + lg;
-      static_for<NB>([&](auto nbc) {
-        constexpr int nb = decltype(nbc)::value;
-        static_for<TN>([&](auto jc) {
-          constexpr int j = decltype(jc)::value;
-          const int row = wn * WTN + j * 32 + lrow;
-          fb[jp][nb][j] = *reinterpret_cast<const v4i*>(sa + A_BYTES + nb * B_BYTES + row * 64 +
-                                                        ((cb ^ swz64(row)) << 4));
-        });
-      });
-    }
-  };
-
-  // The MFMAs of one k-step.  B is the first operand, so the accumulators
-  // hold C transposed: lane (lrow, lg) of sub-tile (i, j) holds row lrow and
-  // the four consecutive columns 8*g + 4*lg + (0..3) in registers 4g..4g+3.
-  auto mfmas = [&](auto ksc) {
-    constexpr int ks = decltype(ksc)::value;
-    constexpr int s = ks & 1;
-    static_for<NB>([&](auto nbc) {
-      constexpr int nb = decltype(nbc)::value;
-      static_for<TN>([&](auto jc) {
-        constexpr int j = decltype(jc)::value;
-        v4i bj;
-        if constexpr (MODE != GM_W8) {
-          bj = fb[s][nb][j];
-        } else {
-          constexpr int jp = ks >> 1, h = ks & 1;
-          bj = __builtin_bit_cast(
-              v4i, i8x8_to_v8h((uint32_t)fb[jp][nb][j][2 * h], (uint32_t)fb[jp][nb][j][2 * h + 1]));
-        }
-        static_for<TM>([&](auto ic) {
-          constexpr int i = decltype(ic)::value;
-          if constexpr (MODE == GM_W8) acc[nb][i][j] = mfma32_f16(bj, fa[s][i], acc[nb][i][j]);
-          else acc[nb][i][j] = mfma32<MODE>(bj, fa[s][i], acc[nb][i][j]);
-        });
-      });
-    });
-  };
-
-  // One stage: the reads of step ks+1 are issued before the MFMAs of step
-  // ks.  Before the last step's MFMAs the workgroup meets at the barrier
-  // (every wave's loads of the next stage have landed, every wave is done
-  // reading this one), the loads of stage kt+2 go into this stage's buffer
-  // (DMA: 0 none, 1 a middle stage, 2 possibly the last stage) and step 0 of
-  // the next stage is read, so the MFMA pipe never waits on a barrier with
-  // an empty queue.  LAST: no next stage.
-  auto stage_body = [&](char* cur, char* nxt, int kt, auto dmac, auto lastc) {
-    constexpr int DMA = decltype(dmac)::value;
-    constexpr bool LAST = decltype(lastc)::value;
-    static_for<KSTEPS>([&](auto ksc) {
-      constexpr int ks = decltype(ksc)::value;
-      if constexpr (ks == KSTEPS - 1 && !LAST && DMA != 0) {
-        // After the barrier: the next stage's first fragment reads, then the
-        // direct loads of stage kt+2 alternating with this step's MFMAs, so
-        // the MFMA pipe keeps running while the loads are issued (issued as
-        // one burst, they stall the wave on the memory queue with its MFMAs
-        // stuck behind them).
-        wait_vm<0>();
-        lds_barrier();
-        read_frags(nxt, std::integral_constant<int, 0>{});
-        if constexpr (DMA == 1) dma_stage(cur, kt + 2, std::false_type{});
-        if constexpr (DMA == 2) dma_stage(cur, kt + 2, std::true_type{});
-        mfmas(ksc);
-        interleave_reads_mfma_vmem<TM + NB * TN, NB * TN * TM, P>();
-        __builtin_amdgcn_sched_barrier(0);
-      } else {
-        if constexpr (ks < KSTEPS - 1) {
-          read_frags(cur, std::integral_constant<int, ks + 1>{});
-        } else if constexpr (!LAST) {
-          wait_vm<0>();
-          lds_barrier();
-          read_frags(nxt, std::integral_constant<int, 0>{});
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        mfmas(ksc);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    });
-  };
-  typedef std::integral_constant<int, 0> NoDma;
-  typedef std::integral_constant<int, 2> LastDma;
-
-  // Stage buffers: stage kt lives in st0 when kt - (nk & 1) is even, so the
-  // final two stages are always (st0, st1) and the steady loop needs no
-  // remainder; with an odd stage count stage 0 goes to st1 and is peeled.
-  // (The fast path requires nk >= 2.)
-  // The tile's scales go straight to LDS ahead of the first stage (wave 0:
-  // row scales, 1: column scales, 2: second column scales): issued first,
-  // they are covered by the prologue's wait for stage 0.  A null scale
-  // pointer gives an empty buffer range, so its slot reads as zeros.
-  {
-    static_assert(NW >= 2 + NB - 1, "one wave per scale vector");
-    auto sc_rsrc = [](const float* ptr, int64_t first, int64_t n) {
-      return __builtin_amdgcn_make_buffer_rsrc((void*)(ptr ? ptr + first : nullptr), 0,
-                                               ptr ? (int)((n - first) * 4) : 0, 0x00020000);
-    };
-    if (wave == 0)
-      dma16(sc_rsrc(MODE == GM_I8 ? p.row_scale : nullptr, m0, p.M), (char*)scl, lane * 16u, 0u);
-    if (wave == 1) dma16(sc_rsrc(p.col_scale, n0, p.N), (char*)(scl + SC_ROWS), lane * 16u, 0u);
-    if constexpr (NB == 2)
-      if (wave == 2) dma16(sc_rsrc(p.col_scale2, n0, p.N), (char*)(scl + 2 * SC_ROWS), lane * 16u, 0u);
-  }
-  const bool odd = nk & 1;
-  if (odd) {
-    dma_stage(st1, 0, std::true_type{});
-    dma_stage(st0, 1, std::true_type{});
-  } else {
-    dma_stage(st0, 0, std::true_type{});
-    dma_stage(st1, 1, std::true_type{});
-  }
-  wait_vm<P>();
-  lds_barrier();
-  int kt = 0;
-  if (odd) {
-    read_frags(st1, std::integral_constant<int, 0>{});
-    stage_body(st1, st0, 0, LastDma{}, std::false_type{});
-    kt = 1;
-  } else {
-    read_frags(st0, std::integral_constant<int, 0>{});
-  }
-  // Steady state: straight-line pairs of stages (no conditional code, so
-  // the accumulators keep one register class across iterations).
-  for (; nk - kt > 2; kt += 2) {
-    stage_body(st0, st1, kt, LastDma{}, std::false_type{});
-    stage_body(st1, st0, kt + 1, LastDma{}, std::false_type{});
-  }
-  stage_body(st0, st1, kt, NoDma{}, std::false_type{});
-  stage_body(st1, st0, kt + 1, NoDma{}, std::true_type{});
-
-  // ---- epilogue ----------------------------------------------------------
-  // Lane (lrow, lg) holds row wm*WTM + 32*i + lrow, columns
-  // wn*WTN + 32*j + 8*g + 4*lg + (0..3) of the tile in registers 4g..4g+3 of
-  // sub-tile (i, j).  Stored straight from that layout, every store
-  // instruction would write 16 bytes into each of 32 rows (32 partial-line
-  // requests).  Instead each wave converts its block to the output type in a
-  // private LDS region (the stage buffers are free now), row-major with the
-  // 16-byte chunk XOR-swizzled by row (conflict-free 8/16-byte writes and
-  // 16-byte reads), and reads it back so that every lane stores 16
-  // consecutive bytes and a wave store covers whole rows.
-  //
-  // The epilogue is straight-line code: the output type is a compile-time
-  // variant chosen once, the scales come from LDS (fetched in the prologue;
-  // an absent scale reads as 1.0, and multiplying by 1.0 is exact, so the
-  // result equals skipping the multiply), and residual reads use clamped
-  // in-bounds indices (values for rows/columns past the edge are never
-  // stored).  A per-element test of the output type or of an optional
-  // argument would put a branch, and a wait for every load behind it, on
-  // each element.  The block goes out in passes of 32 rows, so the
-  // conversion of one pass overlaps the stores of the previous one; all
-  // loads of a pass (residual) are issued before any store of that pass, so
-  // a residual that aliases C is read first.  The output stores are
-  // non-temporal: the tile is written once and not read back, and streamed
-  // stores drain to memory as they go instead of waiting in L2 for the
-  // end-of-kernel write-back.
-  lds_barrier();  // every wave is done reading the stage buffers
-  const int64_t row0w = m0 + wm * WTM;
-  const int64_t col0w = n0 + wn * WTN;
-  const bool has_rs = MODE == GM_I8 && p.row_scale != nullptr;
-  const bool has_cs = p.col_scale != nullptr;
-  const bool has_cs2 = NB == 2 && p.col_scale2 != nullptr;
-  // scale of sub-tile row i / columns (j, g) of this lane, read from LDS
-  // where it is used (holding a whole wave block's scales in registers
-  // would cost 16 registers per sub-tile column)
-  auto row_scale_of = [&](int i) -> float { return has_rs ? scl[wm * WTM + i * 32 + lrow] : 1.f; };
-  auto col_scale_of = [&](int j, int g, int which) -> v4f {
-    const bool has = which ? has_cs2 : has_cs;
-    const int c = wn * WTN + j * 32 + 8 * g + 4 * lg;
-    return has ? *reinterpret_cast<const v4f*>(scl + (1 + which) * SC_ROWS + c) : v4f{1.f, 1.f, 1.f, 1.f};
-  };
-  const bool has_res = MODE != GM_I8 && EPI != GE_SWIGLU && p.res != nullptr;
-
-  // OK: output kind (DT_I32 / DT_F32 / DT_F16 / DT_BF16), a compile-time value
-  auto epilogue = [&](auto okc) {
-    constexpr int OK = decltype(okc)::value;
-    constexpr int ES = (OK == DT_I32 || OK == DT_F32) ? 4 : 2;  // output element bytes
-    constexpr int RB = WTN * ES;                 // bytes per row of the wave block
-    constexpr int PER_ARRAY = (NW + 1) / 2;      // wave regions per stage buffer
-    constexpr int REGION = STAGE / PER_ARRAY;
-    constexpr int TMP = 1;  // 32-row passes
-    static_assert(TMP >= 1 && TM % TMP == 0 && TMP * 32 * RB <= REGION, "epilogue region");
-    static_assert(RB >= 64 && (1024 % RB == 0 || RB % 1024 == 0), "epilogue row bytes");
-    auto swz_out = [](int row) -> int {
-      if constexpr (RB == 64) return (row >> 2) & 3;
-      else if constexpr (RB == 128) return (row >> 1) & 7;
-      else return row & 15;
-    };
-    char* region = (wave < PER_ARRAY ? st0 : st1) + (wave % PER_ARRAY) * (TMP * 32 * RB);
-    static_for<TM / TMP>([&](auto pc) {
-      constexpr int pp = decltype(pc)::value;
-      // 1) this pass's sub-tile rows -> LDS, in the output type
-      static_for<TN>([&](auto jc) {
-        constexpr int j = decltype(jc)::value;
-        // residual of sub-tile column j of this pass (float GE_STORE only)
-        v4f res[TMP][4];
-        if constexpr (MODE != GM_I8 && EPI != GE_SWIGLU) {
-          static_for<TMP>([&](auto ic) {
-            constexpr int ii = decltype(ic)::value;
-            static_for<4>([&](auto gc) {
-              constexpr int g = decltype(gc)::value;
-              if (has_res) {
-                const int64_t row = min(row0w + (pp * TMP + ii) * 32 + lrow, p.M - 1);
-                const int64_t col = min(col0w + j * 32 + 8 * g + 4 * lg, p.N - 4);
-                res[ii][g] = load4(p.res, p.res_dtype, row * p.ldr + col);
-              } else {
-                res[ii][g] = v4f{0.f, 0.f, 0.f, 0.f};
-              }
-            });
-          });
-        }
-        v4f cs[4], cs2[4];
-        static_for<4>([&](auto gc) {
-          constexpr int g = decltype(gc)::value;
-          cs[g] = col_scale_of(j, g, 0);
-          if constexpr (NB == 2) cs2[g] = col_scale_of(j, g, 1);
-        });
-        static_for<TMP>([&](auto ic) {
-          constexpr int ii = decltype(ic)::value;
-          constexpr int i = pp * TMP + ii;
-          const int rl = ii * 32 + lrow;
-          const float rs = row_scale_of(i);
-          static_for<4>([&](auto gc) {
-            constexpr int g = decltype(gc)::value;
-            const int byte = (j * 32 + 8 * g + 4 * lg) * ES;
-            char* dst = region + rl * RB + (((byte >> 4) ^ swz_out(rl)) << 4) + (byte & 15);
-            if constexpr (MODE == GM_I8 && OK == DT_I32) {
-              *reinterpret_cast<v4i*>(dst) =
-                  v4i{(int)acc[0][i][j][4 * g], (int)acc[0][i][j][4 * g + 1],
-                      (int)acc[0][i][j][4 * g + 2], (int)acc[0][i][j][4 * g + 3]};
-            } else {
-              float v[4];
-              static_for<4>([&](auto qc) {
-                constexpr int q = decltype(qc)::value;
-                if constexpr (MODE == GM_I8) {
-                  v[q] = ((float)acc[0][i][j][4 * g + q] * rs) * cs[g][q];
-                } else if constexpr (EPI == GE_SWIGLU) {
-                  const float gt =
-                      f16_bits_to_f32(f32_to_f16_bits(acc[0][i][j][4 * g + q] * cs[g][q]));
-                  const float up =
-                      f16_bits_to_f32(f32_to_f16_bits(acc[NB - 1][i][j][4 * g + q] * cs2[g][q]));
-                  const float sg = gt / (1.0f + fast_exp(-gt));
-                  v[q] = sg * up;
-                } else {
-                  const float t = acc[0][i][j][4 * g + q] * cs[g][q];
-                  v[q] = has_res ? t + res[ii][g][q] : t;
-                }
-              });
-              if constexpr (ES == 4) {
-                *reinterpret_cast<v4f*>(dst) = v4f{v[0], v[1], v[2], v[3]};
-              } else if constexpr (OK == DT_BF16) {
-                const uint32_t lo = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
-                const uint32_t hi = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
-                *reinterpret_cast<v2i*>(dst) = v2i{(int)lo, (int)hi};
-              } else {
-                *reinterpret_cast<v2i*>(dst) =
-                    v2i{(int)f32x2_to_f16x2(v[0], v[1]), (int)f32x2_to_f16x2(v[2], v[3])};
-              }
-            }
-          });
-        });
-      });
-      // 2) LDS -> global: 16 bytes per lane, whole rows per wave store
-      constexpr int NI = TMP * 32 * RB / 1024;
-      constexpr int EPC = 16 / ES;  // elements per 16-byte chunk
-      static_for<NI>([&](auto qc) {
-        constexpr int q = decltype(qc)::value;
-        const int byte = q * 1024 + lane * 16;
-        const int rl = byte / RB, c = (byte % RB) >> 4;
-        const v4i d = *reinterpret_cast<const v4i*>(region + rl * RB + ((c ^ swz_out(rl)) << 4));
-        const int64_t row = row0w + pp * TMP * 32 + rl;
-        const int64_t col = col0w + c * EPC;
-        if (row < p.M) {
-          char* out = reinterpret_cast<char*>(p.c) + (row * p.ldc + col) * ES;
-          if (col + EPC <= p.N) __builtin_nontemporal_store(d, reinterpret_cast<v4i*>(out));
-          else if (ES == 2 && col < p.N) *reinterpret_cast<v2i*>(out) = v2i{d[0], d[1]};
-        }
-      });
-    });
-  };
-  switch (p.out_dtype) {
-    case DT_I32: if constexpr (MODE == GM_I8) epilogue(std::integral_constant<int, DT_I32>{}); break;
-    case DT_F32: if constexpr (EPI != GE_SWIGLU) epilogue(std::integral_constant<int, DT_F32>{}); break;
-    case DT_BF16: epilogue(std::integral_constant<int, DT_BF16>{}); break;
-    default: epilogue(std::integral_constant<int, DT_F16>{}); break;
-  }
-}
 
 // ---------------------------------------------------------------------------
 // Generic kernel: any shape, any alignment, same arithmetic contract (int32
@@ -675,50 +96,12 @@ __global__ void __launch_bounds__(256) gemm_generic_kernel(GemmArgs p) {
   }
 }
 
-// ---------------------------------------------------------------------------
-// Config table.  The autotuner searches over these instantiations.
-// ---------------------------------------------------------------------------
-typedef void (*GemmLaunch)(const GemmArgs&, hipStream_t);
-
-template <int MODE, int BM, int BN, int WM, int WN, int EPI, int SB = 128, int MINW = 1>
-static void launch_one(const GemmArgs& a, hipStream_t s) {
-  const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-  gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW><<<dim3((unsigned)tiles), dim3(64 * WM * WN), 0, s>>>(a);
-}
-
-struct GemmEntry {
-  GemmConfig cfg;
-  GemmLaunch fn;
-};
-
-// occ = workgroups a CU holds at once, rate = relative output throughput of
-// one CU at that occupancy, both measured on MI355X at 4096^3 (int8, fp16)
-// and 2048x11008x4096 (W8A16); they drive the untuned default choice.
-#define HX_GEMM_CFGS(MODE)                                                                         \
-  {{256, 256, 2, 2, GE_STORE, "256x256_w2x2", 1, 0.74f}, &launch_one<MODE, 256, 256, 2, 2, GE_STORE>}, \
-  {{256, 128, 2, 2, GE_STORE, "256x128_w2x2", 1, 0.77f}, &launch_one<MODE, 256, 128, 2, 2, GE_STORE>}, \
-  {{128, 256, 2, 2, GE_STORE, "128x256_w2x2", 1, 0.77f}, &launch_one<MODE, 128, 256, 2, 2, GE_STORE>}, \
-  {{128, 128, 2, 2, GE_STORE, "128x128_w2x2", 2, 0.89f}, &launch_one<MODE, 128, 128, 2, 2, GE_STORE>}, \
-  {{256, 256, 2, 4, GE_STORE, "256x256_w2x4", 1, 1.00f}, &launch_one<MODE, 256, 256, 2, 4, GE_STORE>}, \
-  {{64, 64, 2, 2, GE_STORE, "64x64_w2x2", 4, 0.61f}, &launch_one<MODE, 64, 64, 2, 2, GE_STORE>}
-
-static const GemmEntry kI8[] = {HX_GEMM_CFGS(GM_I8)};
-static const GemmEntry kF16[] = {HX_GEMM_CFGS(GM_F16)};
-static const GemmEntry kBF16[] = {HX_GEMM_CFGS(GM_BF16)};
-static const GemmEntry kW8[] = {
-    HX_GEMM_CFGS(GM_W8),
-    {{256, 128, 2, 4, GE_SWIGLU, "swiglu_256x128_w2x4", 1, 0.95f}, &launch_one<GM_W8, 256, 128, 2, 4, GE_SWIGLU>},
-    {{256, 128, 2, 2, GE_SWIGLU, "swiglu_256x128_w2x2", 1, 0.77f}, &launch_one<GM_W8, 256, 128, 2, 2, GE_SWIGLU>},
-    {{128, 128, 2, 2, GE_SWIGLU, "swiglu_128x128_w2x2", 1, 0.80f}, &launch_one<GM_W8, 128, 128, 2, 2, GE_SWIGLU>},
-    {{128, 64, 2, 2, GE_SWIGLU, "swiglu_128x64_w2x2", 2, 0.80f}, &launch_one<GM_W8, 128, 64, 2, 2, GE_SWIGLU>},
-};
-
 static const GemmEntry* table(int mode, int& n) {
   switch (mode) {
-    case GM_I8: n = (int)(sizeof(kI8) / sizeof(kI8[0])); return kI8;
-    case GM_F16: n = (int)(sizeof(kF16) / sizeof(kF16[0])); return kF16;
-    case GM_BF16: n = (int)(sizeof(kBF16) / sizeof(kBF16[0])); return kBF16;
-    case GM_W8: n = (int)(sizeof(kW8) / sizeof(kW8[0])); return kW8;
+    case GM_I8: return gemm_table_i8(n);
+    case GM_F16: return gemm_table_f16(n);
+    case GM_BF16: return gemm_table_bf16(n);
+    case GM_W8: return gemm_table_w8(n);
     default: n = 0; return nullptr;
   }
 }

@@ -1,0 +1,15 @@
+// hx_gemm_bf16.hip -- the bf16 x bf16 config table of the MFMA GEMM family
+// (kernel template in hx_gemm_kernel.hpp, dispatch in hx_gemm.hip).
+#include "hx_gemm_kernel.hpp"
+
+namespace hx {
+
+// A host function holding the table: a namespace-scope array of host
+// function pointers would also be emitted by the device compilation.
+const GemmEntry* gemm_table_bf16(int& n) {
+  static const GemmEntry t[] = {HX_GEMM_CFGS(GM_BF16)};
+  n = (int)(sizeof(t) / sizeof(t[0]));
+  return t;
+}
+
+}  // namespace hx

@@ -1,0 +1,21 @@
+// hx_gemm_w8.hip -- the f16 x int8 (W8A16, incl. SwiGLU) config table of the MFMA GEMM family
+// (kernel template in hx_gemm_kernel.hpp, dispatch in hx_gemm.hip).
+#include "hx_gemm_kernel.hpp"
+
+namespace hx {
+
+// A host function holding the table: a namespace-scope array of host
+// function pointers would also be emitted by the device compilation.
+const GemmEntry* gemm_table_w8(int& n) {
+  static const GemmEntry t[] = {
+    HX_GEMM_CFGS(GM_W8),
+    {{256, 128, 2, 4, GE_SWIGLU, "swiglu_256x128_w2x4", 1, 0.95f}, &launch_one<GM_W8, 256, 128, 2, 4, GE_SWIGLU>},
+    {{256, 128, 2, 2, GE_SWIGLU, "swiglu_256x128_w2x2", 1, 0.77f}, &launch_one<GM_W8, 256, 128, 2, 2, GE_SWIGLU>},
+    {{128, 128, 2, 2, GE_SWIGLU, "swiglu_128x128_w2x2", 1, 0.80f}, &launch_one<GM_W8, 128, 128, 2, 2, GE_SWIGLU>},
+    {{128, 64, 2, 2, GE_SWIGLU, "swiglu_128x64_w2x2", 2, 0.80f}, &launch_one<GM_W8, 128, 64, 2, 2, GE_SWIGLU>},
+};
+  n = (int)(sizeof(t) / sizeof(t[0]));
+  return t;
+}
+
+}  // namespace hx
