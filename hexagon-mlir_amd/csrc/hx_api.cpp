@@ -477,12 +477,12 @@ extern "C" int hx_matmul(const hx_memref2d* a, int a_dtype, const hx_memref2d* b
 
   // Decode shapes with f16/bf16 weights in the [K][N] orientation: stream
   // the weight in place rather than transposing it into the workspace.
-  if (op != HX_OP_MATMUL_W8 && b_layout == HX_LAYOUT_KN && M <= 16 && !residual && c_dtype == a_dtype) {
+  if (b_layout == HX_LAYOUT_KN && M <= 16 && !residual && c_dtype == a_dtype) {
     GemvArgs v{};
     v.x = va.p; v.ldx = va.ld; v.w = nullptr; v.ldw = 0;
     v.y = vc.p; v.ldy = vc.ld; v.M = M; v.N = N; v.K = K;
-    if (!gemv_kn_refusal(v, vb.p, vb.ld)) {
-      const int parts = gemv_kn_parts(v);
+    if (!gemv_kn_refusal(b_dtype, v, vb.p, vb.ld)) {
+      const int parts = gemv_kn_parts(b_dtype, v);
       Carver kv;
       const size_t off_part = kv.take(gemv_kn_part_bytes(v, parts));
       const size_t off_sc = (col_scale && scale_dtype == HX_F16) ? kv.take((size_t)N * 4) : 0;
@@ -491,7 +491,7 @@ extern "C" int hx_matmul(const hx_memref2d* a, int a_dtype, const hx_memref2d* b
       if ((rc = scale_f32(col_scale, scale_dtype, N, "col_scale", (float*)(ws + off_sc), &v.scale, s))) return rc;
       note_plan(PlanCtx{"hx_matmul", "argument-kn", a_dtype, b_dtype}, M, N, K, c_dtype, "gemv-kn",
                 parts > 1 ? "kn_split" : "kn", "fixed", "min-rows");
-      return map_internal(launch_gemv_kn(a_dtype, v, vb.p, vb.ld, parts, parts > 1 ? (float*)(ws + off_part) : nullptr, s),
+      return map_internal(launch_gemv_kn(b_dtype, v, vb.p, vb.ld, parts, parts > 1 ? (float*)(ws + off_part) : nullptr, s),
                           "gemv_kn");
     }
   }

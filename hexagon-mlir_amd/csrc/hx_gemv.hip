@@ -589,19 +589,25 @@ int launch_gemv_hw(int cfg_idx, int wt, const GemvArgs& a, const void* w, int64_
 }
 
 // ---------------------------------------------------------------------------
-// f16 / bf16 weights in the linalg [K][N] orientation (N contiguous), read in
-// place: no transpose of the weight.
+// Weights in the linalg [K][N] orientation (N contiguous), read in place: no
+// transpose of the weight.  f16 / bf16 weights, or int8 (W8A16, f16
+// activations).
 //
-// Workgroup (column block b, K part s) covers columns 128b .. 128b + 127.
-// Lane l = 16g + c of a wave loads, for K chunk j (32 k), the eight 16-byte
-// rows W[32j + 8g + r][128b + 8c + (0..7)], r = 0..7 (a wave load is four
-// 256-byte runs), and transposes that 8 x 8 block of halves in registers
-// (32 v_perm_b32): for each q = 0..7 it then holds column 128b + 8c + q at
-// k = 32j + 8g + (0..7), which is the v_mfma_f32_16x16x32 B operand of lane
-// l for the "tile" of the 16 columns {128b + 8c' + q : c' = 0..15}.  The
-// activation operand is the row-fragment x[c][32j + 8g + (0..7)] (rows >= M
-// read zero), shared by the eight tiles.  Accumulator register i of tile q
-// in lane l is Y[4g + i][128b + 8c + q].
+// A lane load is 16 bytes of one row: NQ = 8 (f16/bf16) or 16 (int8)
+// consecutive columns.  Workgroup (column block b, K part s) covers the
+// CB = 16 NQ columns CB*b .. CB*b + CB - 1.  Lane l = 16g + c of a wave
+// loads, for K chunk j (32 k), the eight rows W[32j + 8g + r][CB*b + NQ*c +
+// (0..NQ-1)], r = 0..7 (a wave load is four runs of 16 x 16 bytes), and
+// transposes that block in registers: for each q < NQ it then holds column
+// CB*b + NQ*c + q at k = 32j + 8g + (0..7), which is the
+// v_mfma_f32_16x16x32 B operand of lane l for the "tile" of the 16 columns
+// {CB*b + NQ*c' + q : c' = 0..15}.  f16/bf16: 32 v_perm_b32 per chunk move
+// halves; int8: one v_perm_b32 per pair of rows puts the two bytes of a
+// column into the low bytes of two halves, the XOR with 0x64806480 makes
+// them 1024 + (b ^ 128) exactly, and subtracting 1152 leaves the signed
+// value.  The activation operand is the row-fragment x[c][32j + 8g +
+// (0..7)] (rows >= M read zero), shared by the NQ tiles.  Accumulator
+// register i of tile q in lane l is Y[4g + i][CB*b + NQ*c + q].
 // The KW waves of a workgroup and the S K parts split the chunks (wave w of
 // part s takes chunks j = s*KW + w + S*KW*t); the waves reduce through LDS,
 // and with S > 1 each part writes binary32 partials [S][M][N] that
@@ -609,26 +615,29 @@ int launch_gemv_hw(int cfg_idx, int wt, const GemvArgs& a, const void* w, int64_
 template <int WT, int KW, int U>
 __global__ void __launch_bounds__(64 * KW) gemv_kn_kernel(GemvArgs p, const void* wsrc, int64_t ldw, int kchunks,
                                                           float* part) {
+  constexpr int ES = WT == DT_I8 ? 1 : 2;  // weight element bytes
+  constexpr int NQ = 16 / ES;              // columns per lane load
+  constexpr int CB = 16 * NQ;              // columns per workgroup
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 15, g = lane >> 4;
-  const int64_t n0 = (int64_t)blockIdx.x * 128;
+  const int64_t n0 = (int64_t)blockIdx.x * CB;
   const int S = gridDim.y, sp = blockIdx.y;
   const int P = S * KW;  // chunk stride
-  // the weight rows of this column block: byte offset (k * ldw + 8c + q) * 2
-  const char* wb = reinterpret_cast<const char*>(wsrc) + n0 * 2;
-  const int64_t wbytes = (p.K - 1) * ldw * 2 + (p.N - n0) * 2;  // to the last element of the block's range
+  // the weight rows of this column block: byte offset (k * ldw + NQ c + q) * ES
+  const char* wb = reinterpret_cast<const char*>(wsrc) + n0 * ES;
+  const int64_t wbytes = ((p.K - 1) * ldw + (p.N - n0)) * ES;  // to the last element of the block's range
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
       (void*)wb, 0, (int)min(wbytes, (int64_t)0x7fffffff), 0x00020000);
   const __amdgpu_buffer_rsrc_t rx =
       __builtin_amdgcn_make_buffer_rsrc((void*)p.x, 0, (int)(p.M * p.ldx * 2), 0x00020000);
   const bool xrow = c < p.M;
-  const bool cin = n0 + 8 * c < p.N;  // this lane's column octet starts inside N
+  const bool cin = n0 + NQ * c < p.N;  // this lane's column run starts inside N
   constexpr int kNT = 2;
 
-  v4f acc[8];
+  v4f acc[NQ];
 #pragma unroll
-  for (int q = 0; q < 8; ++q) acc[q] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int q = 0; q < NQ; ++q) acc[q] = v4f{0.f, 0.f, 0.f, 0.f};
 
   for (int j0 = sp * KW + wave; j0 < kchunks; j0 += P * U) {
     v4u wr[U][8];
@@ -640,7 +649,7 @@ __global__ void __launch_bounds__(64 * KW) gemv_kn_kernel(GemvArgs p, const void
       for (int r = 0; r < 8; ++r) {
         const uint32_t k = (uint32_t)j * 32u + 8u * g + r;
         const uint32_t off = (j < kchunks && cin && k < (uint32_t)p.K)
-                                 ? (k * (uint32_t)ldw + 8u * c) * 2u : 0x80000000u;
+                                 ? (k * (uint32_t)ldw + (uint32_t)NQ * c) * (uint32_t)ES : 0x80000000u;
         wr[u][r] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)off, 0, kNT));
       }
       const uint32_t kx = (uint32_t)j * 32u + 8u * g;
@@ -650,36 +659,55 @@ __global__ void __launch_bounds__(64 * KW) gemv_kn_kernel(GemvArgs p, const void
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      // 8 x 8 transpose of halves: dword d of rows 2p, 2p+1 -> columns 2d, 2d+1
-      v4u t[8];
+      if constexpr (WT == DT_I8) {
+        typedef _Float16 hf2 __attribute__((ext_vector_type(2)));
+        const hf2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
 #pragma unroll
-      for (int pr = 0; pr < 4; ++pr)
+        for (int q = 0; q < 16; ++q) {
+          // byte q & 3 of dword q >> 2 of rows 2pr (low half) and 2pr + 1 (high half)
+          constexpr uint32_t Z = 0x0cu;  // selector of a zero byte
+          const uint32_t bq = (uint32_t)(q & 3);
+          const uint32_t sel = (Z << 24) | ((4u + bq) << 16) | (Z << 8) | bq;
+          v4u t;
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const uint32_t a = wr[u][2 * pr][d], b = wr[u][2 * pr + 1][d];
-          t[2 * d][pr] = __builtin_amdgcn_perm(b, a, 0x05040100u);      // low halves
-          t[2 * d + 1][pr] = __builtin_amdgcn_perm(b, a, 0x07060302u);  // high halves
+          for (int pr = 0; pr < 4; ++pr) {
+            const uint32_t d = __builtin_amdgcn_perm(wr[u][2 * pr + 1][q >> 2], wr[u][2 * pr][q >> 2], sel) ^ 0x64806480u;
+            t[pr] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(hf2, d) - bias);
+          }
+          acc[q] = gv_mfma<DT_F16>(xa[u], t, acc[q]);
         }
+      } else {
+        // 8 x 8 transpose of halves: dword d of rows 2p, 2p+1 -> columns 2d, 2d+1
+        v4u t[8];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) acc[q] = gv_mfma<WT>(xa[u], t[q], acc[q]);
+        for (int pr = 0; pr < 4; ++pr)
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            const uint32_t a = wr[u][2 * pr][d], b = wr[u][2 * pr + 1][d];
+            t[2 * d][pr] = __builtin_amdgcn_perm(b, a, 0x05040100u);      // low halves
+            t[2 * d + 1][pr] = __builtin_amdgcn_perm(b, a, 0x07060302u);  // high halves
+          }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc[q] = gv_mfma<WT>(xa[u], t[q], acc[q]);
+      }
     }
   }
 
   // reduce the KW waves through LDS; thread t finalises (q, l, i) =
   // (e / 256, (e / 4) % 64, e % 4) for e = t, t + 64 KW, ...
-  __shared__ float red[KW][8][64][4];
+  __shared__ float red[KW][NQ][64][4];
 #pragma unroll
-  for (int q = 0; q < 8; ++q)
+  for (int q = 0; q < NQ; ++q)
 #pragma unroll
     for (int i = 0; i < 4; ++i) red[wave][q][lane][i] = acc[q][i];
   __syncthreads();
-  for (int e = tid; e < 8 * 256; e += 64 * KW) {
+  for (int e = tid; e < NQ * 256; e += 64 * KW) {
     const int q = e >> 8, l = (e >> 2) & 63, i = e & 3;
     float sum = 0.f;
 #pragma unroll
     for (int w = 0; w < KW; ++w) sum += red[w][q][l][i];
     const int m = 4 * (l >> 4) + i;
-    const int64_t n = n0 + 8 * (l & 15) + q;
+    const int64_t n = n0 + NQ * (l & 15) + q;
     if (m < p.M && n < p.N) {
       if (S > 1) {
         part[((int64_t)sp * p.M + m) * p.N + n] = sum;
@@ -705,22 +733,27 @@ __global__ void __launch_bounds__(256) gemv_kn_combine_kernel(GemvArgs p, const 
 
 namespace {
 constexpr int kKnWaves = 4, kKnUnroll = 2;
+int kn_elem_bytes(int wt) { return wt == DT_I8 ? 1 : 2; }
 }
-const char* gemv_kn_refusal(const GemvArgs& a, const void* w, int64_t ldw) {
+const char* gemv_kn_refusal(int wt, const GemvArgs& a, const void* w, int64_t ldw) {
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  const int es = kn_elem_bytes(wt);
   if (a.M < 1 || a.M > 16 || a.N < 1 || a.K < 1) return "row-count";
-  if ((ldw * 2) % 16 != 0 || (a.ldx * 2) % 16 != 0 || a.K % 8 != 0) return "row-stride";
-  // whole 16-byte column octets: a load never straddles the end of a row
-  if (a.N % 8 != 0) return "n-granularity";
+  if ((ldw * es) % 16 != 0 || (a.ldx * 2) % 16 != 0 || a.K % 8 != 0) return "row-stride";
+  // whole 16-byte column runs: a load never straddles the end of a row
+  if (a.N % (16 / es) != 0) return "n-granularity";
   if (!al16(a.x) || !al16(w)) return "unaligned-base";
-  if (a.K * ldw * 2 >= ((int64_t)1 << 31) || a.M * a.ldx * 2 >= ((int64_t)1 << 31)) return "offset-range";
+  if (a.K * ldw * es >= ((int64_t)1 << 31) || a.M * a.ldx * 2 >= ((int64_t)1 << 31)) return "offset-range";
   return nullptr;
 }
-int gemv_kn_parts(const GemvArgs& a) {
-  // about 512 workgroups, each wave with at least kKnUnroll chunks per part
-  const int64_t blocks = (a.N + 127) / 128;
+int gemv_kn_parts(int wt, const GemvArgs& a) {
+  // about 256 workgroups (measured against 128 and 512: int8 11008x4096
+  // 19.9 / 20.0 / 21.6 us, f16 4096^2 12.8 / 13.5 / 14.9 us at M = 1), each
+  // wave with at least kKnUnroll chunks per part
+  const int64_t cb = 16 * (16 / kn_elem_bytes(wt));
+  const int64_t blocks = (a.N + cb - 1) / cb;
   const int64_t kchunks = (a.K + 31) / 32;
-  int64_t S = (512 + blocks - 1) / blocks;
+  int64_t S = (256 + blocks - 1) / blocks;
   S = std::min<int64_t>(S, kchunks / (kKnWaves * kKnUnroll));
   S = std::min<int64_t>(S, 64);
   return (int)std::max<int64_t>(S, 1);
@@ -728,18 +761,21 @@ int gemv_kn_parts(const GemvArgs& a) {
 size_t gemv_kn_part_bytes(const GemvArgs& a, int parts) {
   return parts > 1 ? (size_t)parts * (size_t)(a.M * a.N) * sizeof(float) : 0;
 }
-int launch_gemv_kn(int wt, const GemvArgs& a, const void* w, int64_t ldw, int parts, float* part, hipStream_t s) {
-  if (wt != DT_F16 && wt != DT_BF16) return HXI_ERR_ARG;
-  if (gemv_kn_refusal(a, w, ldw) || parts < 1 || parts > 64 || (parts > 1 && !part)) return HXI_ERR_SHAPE;
+template <int WT>
+static void gemv_kn_launch(const GemvArgs& a, const void* w, int64_t ldw, int parts, float* part, hipStream_t s) {
+  constexpr int CB = 16 * (16 / (WT == DT_I8 ? 1 : 2));
   const int kchunks = (int)((a.K + 31) / 32);
-  const dim3 grid((unsigned)((a.N + 127) / 128), (unsigned)parts);
-  if (wt == DT_F16) gemv_kn_kernel<DT_F16, kKnWaves, kKnUnroll><<<grid, dim3(64 * kKnWaves), 0, s>>>(a, w, ldw, kchunks, part);
-  else gemv_kn_kernel<DT_BF16, kKnWaves, kKnUnroll><<<grid, dim3(64 * kKnWaves), 0, s>>>(a, w, ldw, kchunks, part);
-  if (parts > 1) {
-    const dim3 cg((unsigned)((a.M * a.N + 255) / 256));
-    if (wt == DT_F16) gemv_kn_combine_kernel<DT_F16><<<cg, dim3(256), 0, s>>>(a, part, parts);
-    else gemv_kn_combine_kernel<DT_BF16><<<cg, dim3(256), 0, s>>>(a, part, parts);
-  }
+  const dim3 grid((unsigned)((a.N + CB - 1) / CB), (unsigned)parts);
+  gemv_kn_kernel<WT, kKnWaves, kKnUnroll><<<grid, dim3(64 * kKnWaves), 0, s>>>(a, w, ldw, kchunks, part);
+  if (parts > 1)
+    gemv_kn_combine_kernel<WT><<<dim3((unsigned)((a.M * a.N + 255) / 256)), dim3(256), 0, s>>>(a, part, parts);
+}
+int launch_gemv_kn(int wt, const GemvArgs& a, const void* w, int64_t ldw, int parts, float* part, hipStream_t s) {
+  if (wt != DT_F16 && wt != DT_BF16 && wt != DT_I8) return HXI_ERR_ARG;
+  if (gemv_kn_refusal(wt, a, w, ldw) || parts < 1 || parts > 64 || (parts > 1 && !part)) return HXI_ERR_SHAPE;
+  if (wt == DT_F16) gemv_kn_launch<DT_F16>(a, w, ldw, parts, part, s);
+  else if (wt == DT_BF16) gemv_kn_launch<DT_BF16>(a, w, ldw, parts, part, s);
+  else gemv_kn_launch<DT_I8>(a, w, ldw, parts, part, s);
   return HXI_OK;
 }
 

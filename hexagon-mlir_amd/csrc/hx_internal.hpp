@@ -111,11 +111,12 @@ int launch_gemv_packed(int cfg_idx, const GemvArgs& a, const int8_t* packed, hip
 // taken, else the refusal.
 const char* gemv_hw_refusal(const GemvArgs& a, const void* w, int64_t ldw);
 int launch_gemv_hw(int cfg_idx, int wt, const GemvArgs& a, const void* w, int64_t ldw, hipStream_t s);
-// f16 / bf16 weights in the [K][N] orientation (row stride ldw), read in
-// place; K split over `parts` workgroups per column block, whose binary32
-// partials (gemv_kn_part_bytes) are summed by a second kernel when > 1.
-const char* gemv_kn_refusal(const GemvArgs& a, const void* w, int64_t ldw);
-int gemv_kn_parts(const GemvArgs& a);
+// Weights in the [K][N] orientation (row stride ldw), read in place: f16 /
+// bf16, or int8 (wt = DT_I8) with f16 activations.  K is split over `parts`
+// workgroups per column block, whose binary32 partials (gemv_kn_part_bytes)
+// are summed by a second kernel when > 1.
+const char* gemv_kn_refusal(int wt, const GemvArgs& a, const void* w, int64_t ldw);
+int gemv_kn_parts(int wt, const GemvArgs& a);
 size_t gemv_kn_part_bytes(const GemvArgs& a, int parts);
 int launch_gemv_kn(int wt, const GemvArgs& a, const void* w, int64_t ldw, int parts, float* part, hipStream_t s);
 

@@ -115,3 +115,26 @@ def test_gemv_resident_ragged(hx, dev, shape):
                          f"packed ragged {shape} cfg {cfg}")
     finally:
         rw.release()
+
+
+@pytest.mark.parametrize("shape", [(1, 11008, 4096), (4, 4096, 1032), (16, 256, 8192), (2, 16, 24)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_gemv_kn_in_place(hx, dev, shape):
+    """int8 weights in the linalg [K][N] orientation are streamed in place
+    (no transpose): bytes transposed and widened in registers, one K part or
+    several with the binary32 partial merge; a row stride wider than N."""
+    import torch
+    M, N, K = shape
+    x, w, s = case(M, N, K, seed=400)
+    wide = torch.zeros((K, N + 32), dtype=torch.int8, device=dev)
+    wide[:, :N] = to_dev(w, dev)
+    hx.manifest_enable(True)
+    hx.manifest_clear()
+    try:
+        y = hx.gemv_w8a16(to_dev(x, dev), wide[:, :N], to_dev(s, dev), w_layout="kn")
+        recs = hx.manifest()["records"]
+    finally:
+        hx.manifest_enable(False)
+    assert [(r["plan"], r["weight"], r["b"]) for r in recs] == [("gemv-kn", "argument-kn", "i8")], recs
+    want = oracle.matmul(x, w, scale_n=s.astype(np.float32))
+    assert_close(to_np(y).astype(np.float32), want.astype(np.float32), 1e-2, 1e-3, f"kn in place {shape}")
