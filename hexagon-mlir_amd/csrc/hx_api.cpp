@@ -355,14 +355,16 @@ static int run_gemm(int op, GemmArgs& a, hipStream_t s, const PlanCtx& ctx) {
 }
 
 // f16 / bf16 weights read in place from [N][K] by the streaming GEMV.
+// dt: the weight's type (the output has the activations' type: bf16 for
+// bf16 weights, else f16).
 static int run_gemv_hw(GemvArgs& a, int dt, const void* w, int64_t ldw, hipStream_t s, const PlanCtx& ctx,
                        const char* reason = nullptr) {
   if (!reason) reason = a.M <= 16 ? "min-rows" : "few-rows";  // 16 < M <= 64: row-block configs
-  const int op = dt == HX_BF16 ? HX_OP_GEMV_BF16 : HX_OP_GEMV_F16;
+  const int op = dt == HX_BF16 ? HX_OP_GEMV_BF16 : dt == HX_I8 ? HX_OP_GEMV_W8 : HX_OP_GEMV_F16;
   bool pin = false;
   const int cfg = resolve_gemv(op, a.M, a.N, a.K, &pin);
-  note_plan(ctx, a.M, a.N, a.K, dt, "gemv-stream", gemv_packed_config(cfg)->name, pin ? "pinned" : "default",
-            reason);
+  note_plan(ctx, a.M, a.N, a.K, dt == HX_BF16 ? HX_BF16 : HX_F16, "gemv-stream", gemv_packed_config(cfg)->name,
+            pin ? "pinned" : "default", reason);
   return map_internal(launch_gemv_hw(cfg, dt, a, w, ldw, s), "gemv_stream");
 }
 
@@ -470,7 +472,7 @@ extern "C" int hx_matmul(const hx_memref2d* a, int a_dtype, const hx_memref2d* b
     GemvArgs v{};
     v.x = vb.p; v.ldx = K; v.w = nullptr; v.ldw = 0;
     v.scale = nullptr; v.y = vc.p; v.ldy = M; v.M = 1; v.N = M; v.K = K;
-    if (!gemv_hw_refusal(v, va.p, va.ld))
+    if (!gemv_hw_refusal(a_dtype, v, va.p, va.ld))
       return run_gemv_hw(v, a_dtype, va.p, va.ld, s, PlanCtx{"hx_matmul", "swapped-a-streamed", a_dtype, b_dtype},
                          "n-is-one");
   }
@@ -516,17 +518,20 @@ extern "C" int hx_matmul(const hx_memref2d* a, int a_dtype, const hx_memref2d* b
 
   const PlanCtx ctx{"hx_matmul", b_layout == HX_LAYOUT_KN ? "transposed-to-workspace" : "argument",
                     a_dtype, b_dtype};
-  if (op == HX_OP_MATMUL_W8 && M <= 16 && !residual && c_dtype == HX_F16) {
+  if (op == HX_OP_MATMUL_W8 && M <= kGemvMaxRows && !residual && c_dtype == HX_F16) {
     GemvArgs v{};
     v.x = g.a; v.ldx = g.lda; v.w = (const int8_t*)g.b; v.ldw = g.ldb;
     v.scale = g.col_scale; v.y = g.c; v.ldy = g.ldc; v.M = M; v.N = N; v.K = K;
-    if (gemv_fast_ok(v)) return run_gemv(v, s, ctx);
+    // the streaming kernel reads the [N][K] int8 weight in place; the older
+    // 4-wave kernel covers what it refuses (M <= 16)
+    if (!gemv_hw_refusal(HX_I8, v, g.b, g.ldb)) return run_gemv_hw(v, HX_I8, g.b, g.ldb, s, ctx);
+    if (M <= 16 && gemv_fast_ok(v)) return run_gemv(v, s, ctx);
   }
   if (op != HX_OP_MATMUL_W8 && M <= kGemvMaxRows && !residual && c_dtype == a_dtype) {
     GemvArgs v{};
     v.x = g.a; v.ldx = g.lda; v.w = nullptr; v.ldw = 0;
     v.scale = g.col_scale; v.y = g.c; v.ldy = g.ldc; v.M = M; v.N = N; v.K = K;
-    if (!gemv_hw_refusal(v, g.b, g.ldb)) return run_gemv_hw(v, a_dtype, g.b, g.ldb, s, ctx);
+    if (!gemv_hw_refusal(a_dtype, v, g.b, g.ldb)) return run_gemv_hw(v, a_dtype, g.b, g.ldb, s, ctx);
   }
   return run_gemm(op, g, s, ctx);
 }
@@ -878,7 +883,7 @@ static int matmul_resident_impl(const View2& vx, hx_weight* w, const View2* vr, 
     GemvArgs v{};
     v.x = vx.p; v.ldx = vx.ld; v.w = nullptr; v.ldw = 0;
     v.scale = w->scale; v.y = vy.p; v.ldy = vy.ld; v.M = M; v.N = w->N; v.K = w->K;
-    if (!gemv_hw_refusal(v, w->image, w->K)) return run_gemv_hw(v, x_dt, w->image, w->K, s,
+    if (!gemv_hw_refusal(w->dtype, v, w->image, w->K)) return run_gemv_hw(v, w->dtype, w->image, w->K, s,
                                                                 PlanCtx{entry, "resident-image", x_dt, w->dtype});
   }
   GemmArgs g{};

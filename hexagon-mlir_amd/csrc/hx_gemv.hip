@@ -174,7 +174,7 @@ __device__ __forceinline__ v4f gv_mfma(v4u a, v4u b, v4f c) {
 template <int CT, int KW, int CPW, int XS, int WT, bool PK, bool PIPE, int MB = 1>
 __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const void* wsrc, int64_t ldw,
                                                               int kchunks) {
-  static_assert(PK == (WT == DT_I8), "int8 weights stream from the packed image, f16/bf16 in place");
+  static_assert(!PK || WT == DT_I8, "only int8 weights have a packed image");
   static_assert(MB == 1 || (XS == XS_NONE && !PIPE), "row blocks: register-fragment configs only");
   constexpr bool XL = XS != XS_NONE;
   constexpr int KD = WT == DT_I8 ? 64 : 32;  // k per chunk
@@ -324,7 +324,8 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
         for (int c = 0; c < CT; ++c) {
           v4u wb;
           if constexpr (WT == DT_I8)
-            wb = __builtin_bit_cast(v4u, x8x8_to_v8h(wq[u][c][2 * e], wq[u][c][2 * e + 1]));
+            wb = __builtin_bit_cast(v4u, PK ? x8x8_to_v8h(wq[u][c][2 * e], wq[u][c][2 * e + 1])
+                                         : i8x8_to_v8h(wq[u][c][2 * e], wq[u][c][2 * e + 1]));
           else
             wb = wq[u][c];
           acc[0][c] = gv_mfma<WT>(xa, wb, acc[0][c]);
@@ -391,7 +392,8 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
           for (int c = 0; c < CT; ++c) {
             v4u wb;
             if constexpr (WT == DT_I8)
-              wb = __builtin_bit_cast(v4u, x8x8_to_v8h(wq[u][c][2 * e], wq[u][c][2 * e + 1]));
+              wb = __builtin_bit_cast(v4u, PK ? x8x8_to_v8h(wq[u][c][2 * e], wq[u][c][2 * e + 1])
+                                           : i8x8_to_v8h(wq[u][c][2 * e], wq[u][c][2 * e + 1]));
             else
               wb = wq[u][c];
 #pragma unroll
@@ -481,26 +483,27 @@ int launch_gemv_pack(const int8_t* w, int64_t ldw, int64_t N, int64_t K, int8_t*
 }
 
 typedef void (*GemvStreamLaunch)(const GemvArgs&, const void*, int64_t, int, hipStream_t);
-template <int CT, int KW, int CPW, int XS, bool PIPE, int WT, int MB = 1>
+template <int CT, int KW, int CPW, int XS, bool PIPE, int WT, int MB = 1, bool PK = (WT == DT_I8)>
 static void gemv_stream_one(const GemvArgs& a, const void* w, int64_t ldw, int kchunks, hipStream_t s) {
   constexpr int KD = WT == DT_I8 ? 64 : 32;
   const int64_t ntiles = (a.N + 15) / 16;
   const int64_t blocks = (ntiles + CT - 1) / CT;
   const size_t lds = XS != XS_NONE ? (size_t)a.M * (((int64_t)kchunks * KD + 511) / 512 * 512 + 8) * 2 : 0;
-  gemv_stream_kernel<CT, KW, CPW, XS, WT, WT == DT_I8, PIPE, MB>
+  gemv_stream_kernel<CT, KW, CPW, XS, WT, PK, PIPE, MB>
       <<<dim3((unsigned)blocks), dim3(64 * KW), lds, s>>>(a, w, ldw, kchunks);
 }
 struct GemvStreamEntry {
   GemvConfig cfg;
-  GemvStreamLaunch fn[3];  // int8 (packed image), f16, bf16 (in place)
+  GemvStreamLaunch fn[4];  // int8 (packed image), f16, bf16, int8 (in place)
 };
 #define HX_GV(CT, KW, CPW, XS, PIPE)                                                                     \
   {&gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_I8>, &gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_F16>, \
-   &gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_BF16>}
+   &gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_BF16>, &gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_I8, 1, false>}
 #define HX_GR(CT, KW, CPW, MB)                                                                      \
   {&gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_I8, MB>,                                        \
    &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_F16, MB>,                                       \
-   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_BF16, MB>}
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_BF16, MB>,                                      \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_I8, MB, false>}
 // xl configs (activations staged in LDS) take M <= 4 with the staged rows
 // within 64 KiB of LDS; outside that they run as their register-staged base
 // config (the `base` index).  The `_p` config is software pipelined over
@@ -542,19 +545,19 @@ const GemvConfig* gemv_packed_config(int idx) {
 }
 
 // Shared by the int8 (packed) and f16/bf16 (in place) launches.
-static int launch_gemv_stream(int cfg_idx, int wt, const GemvArgs& a, const void* w, int64_t ldw,
-                              hipStream_t s) {
+static int launch_gemv_stream(int cfg_idx, int wt, bool packed, const GemvArgs& a, const void* w,
+                              int64_t ldw, hipStream_t s) {
   if (cfg_idx < 0 || cfg_idx >= gemv_packed_config_count()) return HXI_ERR_ARG;
   if (a.M < 1 || a.M > kGemvMaxRows) return HXI_ERR_SHAPE;
   // a config whose row blocks cannot hold M runs as the row-block default
   if (a.M > 16 * kGemvStream[cfg_idx].cfg.mb) cfg_idx = gemv_rows_default(a.M, a.N);
-  const int slot = wt == DT_I8 ? 0 : wt == DT_F16 ? 1 : wt == DT_BF16 ? 2 : -1;
+  const int slot = wt == DT_I8 ? (packed ? 0 : 3) : wt == DT_F16 ? 1 : wt == DT_BF16 ? 2 : -1;
   if (slot < 0) return HXI_ERR_ARG;
   const int64_t kd = wt == DT_I8 ? 64 : 32;
   const int64_t kchunks = (a.K + kd - 1) / kd;
   const int64_t ct = kGemvStream[cfg_idx].cfg.ct;
   // 32-bit buffer offsets: one workgroup's weight range and the activation rows
-  const int64_t wg_bytes = wt == DT_I8 ? ct * kchunks * 1024 : 16 * ct * ldw * 2;
+  const int64_t wg_bytes = packed ? ct * kchunks * 1024 : 16 * ct * ldw * (wt == DT_I8 ? 1 : 2);
   if (wg_bytes >= ((int64_t)1 << 31) || a.M * a.ldx * 2 >= ((int64_t)1 << 31)) return HXI_ERR_SHAPE;
   // xl: staged rows within 64 KiB of LDS
   if (kGemvStream[cfg_idx].cfg.xl && (a.M > 4 || a.M * ((kchunks * kd + 511) / 512 * 512 + 8) * 2 > 65536))
@@ -570,22 +573,23 @@ int gemv_rows_default(int64_t M, int64_t N) {
   return M <= 32 ? 13 : 15;
 }
 int launch_gemv_packed(int cfg_idx, const GemvArgs& a, const int8_t* packed, hipStream_t s) {
-  return launch_gemv_stream(cfg_idx, DT_I8, a, packed, 0, s);
+  return launch_gemv_stream(cfg_idx, DT_I8, true, a, packed, 0, s);
 }
-const char* gemv_hw_refusal(const GemvArgs& a, const void* w, int64_t ldw) {
+const char* gemv_hw_refusal(int wt, const GemvArgs& a, const void* w, int64_t ldw) {
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  const int64_t es = wt == DT_I8 ? 1 : 2;
   if (a.M < 1 || a.M > kGemvMaxRows || a.N < 1 || a.K < 1) return "row-count";
   if (a.K % 8 != 0) return "k-granularity";
-  if ((ldw * 2) % 16 != 0 || (a.ldx * 2) % 16 != 0) return "row-stride";
+  if ((ldw * es) % 16 != 0 || (a.ldx * 2) % 16 != 0) return "row-stride";
   if (!al16(a.x) || !al16(w)) return "unaligned-base";
-  if ((int64_t)64 * ldw * 2 >= ((int64_t)1 << 31) || a.M * a.ldx * 2 >= ((int64_t)1 << 31))
+  if ((int64_t)64 * ldw * es >= ((int64_t)1 << 31) || a.M * a.ldx * 2 >= ((int64_t)1 << 31))
     return "offset-range";
   return nullptr;
 }
 int launch_gemv_hw(int cfg_idx, int wt, const GemvArgs& a, const void* w, int64_t ldw, hipStream_t s) {
-  if (wt != DT_F16 && wt != DT_BF16) return HXI_ERR_ARG;
-  if (gemv_hw_refusal(a, w, ldw)) return HXI_ERR_SHAPE;
-  return launch_gemv_stream(cfg_idx, wt, a, w, ldw, s);
+  if (wt != DT_F16 && wt != DT_BF16 && wt != DT_I8) return HXI_ERR_ARG;
+  if (gemv_hw_refusal(wt, a, w, ldw)) return HXI_ERR_SHAPE;
+  return launch_gemv_stream(cfg_idx, wt, false, a, w, ldw, s);
 }
 
 // ---------------------------------------------------------------------------

@@ -105,11 +105,11 @@ int launch_gemv_pack(const int8_t* w_nk, int64_t ldw, int64_t N, int64_t K, int8
 int gemv_packed_config_count();
 const GemvConfig* gemv_packed_config(int idx);
 int launch_gemv_packed(int cfg_idx, const GemvArgs& a, const int8_t* packed, hipStream_t s);
-// f16 / bf16 weights (wt = DT_F16 / DT_BF16) read in place from a
-// K-contiguous [N][K] matrix with row stride ldw (elements); the same config
-// table as the packed int8 kernel.  Null when the shape and layout are
-// taken, else the refusal.
-const char* gemv_hw_refusal(const GemvArgs& a, const void* w, int64_t ldw);
+// Weights read in place from a K-contiguous [N][K] matrix with row stride
+// ldw (elements): f16 / bf16 (wt = DT_F16 / DT_BF16), or int8 (DT_I8, f16
+// activations); the same config table as the packed int8 kernel.  Null when
+// the shape and layout are taken, else the refusal.
+const char* gemv_hw_refusal(int wt, const GemvArgs& a, const void* w, int64_t ldw);
 int launch_gemv_hw(int cfg_idx, int wt, const GemvArgs& a, const void* w, int64_t ldw, hipStream_t s);
 // Weights in the [K][N] orientation (row stride ldw), read in place: f16 /
 // bf16, or int8 (wt = DT_I8) with f16 activations.  K is split over `parts`

@@ -33,7 +33,7 @@ def test_manifest_records_plans_and_reasons(hx, dev):
         x = torch.randn((4, 512), dtype=torch.float16, device=dev, generator=g)
         w = torch.randint(-127, 128, (512, 512), dtype=torch.int8, device=dev, generator=g)
         s = torch.rand(512, device=dev).half()
-        hx.gemv_w8a16(x, w, s, w_layout="nk")                    # raw decode GEMV
+        hx.gemv_w8a16(x, w, s, w_layout="nk")                    # decode GEMV, weight read in place
         rw = hx.ResidentWeight(w, s, layout="nk")
         try:
             hx.matmul_resident(x, rw)                            # packed decode GEMV
@@ -61,7 +61,7 @@ def test_manifest_records_plans_and_reasons(hx, dev):
     assert find(entry="hx_gemm_i8", n=38)["reason"] == "n-granularity"
     assert find(entry="hx_gemm_i8", n=36, k=496)["plan"] == "mfma-tiled"
     assert find(entry="hx_gemm_i8", n=36, k=504)["reason"] == "row-stride"  # ldb = 504
-    assert find(entry="hx_matmul", m=4, plan="gemv")["reason"] == "min-rows"
+    assert find(entry="hx_matmul", m=4, plan="gemv-stream")["reason"] == "min-rows"
     assert find(entry="hx_matmul_resident", m=4)["plan"] == "gemv-packed"
     r = find(entry="hx_matmul_resident", m=64)
     assert r["plan"] == "gemv-packed" and r["reason"] == "few-rows" and r["config"].startswith("rows")
