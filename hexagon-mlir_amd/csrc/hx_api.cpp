@@ -477,25 +477,49 @@ extern "C" int hx_matmul(const hx_memref2d* a, int a_dtype, const hx_memref2d* b
                          "n-is-one");
   }
 
-  // Decode shapes with f16/bf16 weights in the [K][N] orientation: stream
-  // the weight in place rather than transposing it into the workspace.
-  if (b_layout == HX_LAYOUT_KN && M <= 16 && !residual && c_dtype == a_dtype) {
+  // The decode GEMV epilogues read an f16 or f32 column scale directly (the
+  // GEMM path widens an f16 scale into the workspace first).
+  const float* sc32 = nullptr;
+  const uint16_t* sc16 = nullptr;
+  if (col_scale) {
+    if (scale_dtype != HX_F16 && scale_dtype != HX_F32)
+      return fail(HX_ERR_DTYPE, "col_scale: dtype %s (f16 or f32)", dt_name(scale_dtype));
+    View1 vs;
+    if ((rc = view1(col_scale, scale_dtype, "col_scale", N, &vs))) return rc;
+    if (scale_dtype == HX_F16) sc16 = (const uint16_t*)vs.p;
+    else sc32 = (const float*)vs.p;
+  }
+  const bool gemv_rows = M <= kGemvMaxRows && !residual && c_dtype == (op == HX_OP_MATMUL_W8 ? HX_F16 : a_dtype);
+
+  // Decode shapes with weights in the [K][N] orientation: stream the weight
+  // in place rather than transposing it into the workspace.
+  if (b_layout == HX_LAYOUT_KN && M <= 16 && gemv_rows) {
     GemvArgs v{};
     v.x = va.p; v.ldx = va.ld; v.w = nullptr; v.ldw = 0;
     v.y = vc.p; v.ldy = vc.ld; v.M = M; v.N = N; v.K = K;
+    v.scale = sc32; v.scale16 = sc16;
     if (!gemv_kn_refusal(b_dtype, v, vb.p, vb.ld)) {
       const int parts = gemv_kn_parts(b_dtype, v);
       Carver kv;
       const size_t off_part = kv.take(gemv_kn_part_bytes(v, parts));
-      const size_t off_sc = (col_scale && scale_dtype == HX_F16) ? kv.take((size_t)N * 4) : 0;
       char* ws = nullptr;
       if (kv.used && (rc = ws_get(s, kv.used, &ws))) return rc;
-      if ((rc = scale_f32(col_scale, scale_dtype, N, "col_scale", (float*)(ws + off_sc), &v.scale, s))) return rc;
       note_plan(PlanCtx{"hx_matmul", "argument-kn", a_dtype, b_dtype}, M, N, K, c_dtype, "gemv-kn",
                 parts > 1 ? "kn_split" : "kn", "fixed", "min-rows");
       return map_internal(launch_gemv_kn(b_dtype, v, vb.p, vb.ld, parts, parts > 1 ? (float*)(ws + off_part) : nullptr, s),
                           "gemv_kn");
     }
+  }
+
+  // Decode shapes with a K-contiguous [N][K] weight: the streaming GEMV reads
+  // it in place (the older 4-wave int8 kernel covers what it refuses).
+  if (b_layout == HX_LAYOUT_NK && gemv_rows) {
+    const PlanCtx nctx{"hx_matmul", "argument", a_dtype, b_dtype};
+    GemvArgs v{};
+    v.x = va.p; v.ldx = va.ld; v.w = (const int8_t*)vb.p; v.ldw = vb.ld;
+    v.scale = sc32; v.scale16 = sc16; v.y = vc.p; v.ldy = vc.ld; v.M = M; v.N = N; v.K = K;
+    if (!gemv_hw_refusal(b_dtype, v, vb.p, vb.ld)) return run_gemv_hw(v, b_dtype, vb.p, vb.ld, s, nctx);
+    if (op == HX_OP_MATMUL_W8 && M <= 16 && gemv_fast_ok(v)) return run_gemv(v, s, nctx);
   }
 
   const size_t eb = dt_size(b_dtype);
@@ -518,20 +542,13 @@ extern "C" int hx_matmul(const hx_memref2d* a, int a_dtype, const hx_memref2d* b
 
   const PlanCtx ctx{"hx_matmul", b_layout == HX_LAYOUT_KN ? "transposed-to-workspace" : "argument",
                     a_dtype, b_dtype};
-  if (op == HX_OP_MATMUL_W8 && M <= kGemvMaxRows && !residual && c_dtype == HX_F16) {
+  // [K][N] weights the in-place GEMV refused: the transposed copy
+  if (b_layout == HX_LAYOUT_KN && gemv_rows) {
     GemvArgs v{};
     v.x = g.a; v.ldx = g.lda; v.w = (const int8_t*)g.b; v.ldw = g.ldb;
     v.scale = g.col_scale; v.y = g.c; v.ldy = g.ldc; v.M = M; v.N = N; v.K = K;
-    // the streaming kernel reads the [N][K] int8 weight in place; the older
-    // 4-wave kernel covers what it refuses (M <= 16)
-    if (!gemv_hw_refusal(HX_I8, v, g.b, g.ldb)) return run_gemv_hw(v, HX_I8, g.b, g.ldb, s, ctx);
-    if (M <= 16 && gemv_fast_ok(v)) return run_gemv(v, s, ctx);
-  }
-  if (op != HX_OP_MATMUL_W8 && M <= kGemvMaxRows && !residual && c_dtype == a_dtype) {
-    GemvArgs v{};
-    v.x = g.a; v.ldx = g.lda; v.w = nullptr; v.ldw = 0;
-    v.scale = g.col_scale; v.y = g.c; v.ldy = g.ldc; v.M = M; v.N = N; v.K = K;
-    if (!gemv_hw_refusal(a_dtype, v, g.b, g.ldb)) return run_gemv_hw(v, a_dtype, g.b, g.ldb, s, ctx);
+    if (!gemv_hw_refusal(b_dtype, v, g.b, g.ldb)) return run_gemv_hw(v, b_dtype, g.b, g.ldb, s, ctx);
+    if (op == HX_OP_MATMUL_W8 && M <= 16 && gemv_fast_ok(v)) return run_gemv(v, s, ctx);
   }
   return run_gemm(op, g, s, ctx);
 }

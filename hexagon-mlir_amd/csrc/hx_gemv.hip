@@ -27,6 +27,14 @@
 
 namespace hx {
 
+// s * scale[n] in binary32 (an f16 scale is widened exactly), or s without
+// a scale.
+__device__ __forceinline__ float gv_scaled(const GemvArgs& p, int64_t n, float s) {
+  if (p.scale) return s * p.scale[n];
+  if (p.scale16) return s * f16_bits_to_f32(p.scale16[n]);
+  return s;
+}
+
 // activation staging of the packed kernel: none (register fragments per
 // chunk), LDS filled through registers, LDS filled by direct-to-LDS loads
 enum GemvXStage : int { XS_NONE = 0, XS_REG = 1, XS_DMA = 2 };
@@ -122,7 +130,7 @@ __global__ void __launch_bounds__(256) gemv_w8a16_kernel(GemvArgs p) {
   for (int c = 0; c < CT; ++c) {
     const int64_t n = n0 + 16 * c + (fl & 15);
     if (fm < p.M && n < p.N)
-      y[(int64_t)fm * p.ldy + n] = f32_to_f16_bits(p.scale ? sum[c] * p.scale[n] : sum[c]);
+      y[(int64_t)fm * p.ldy + n] = f32_to_f16_bits(gv_scaled(p, n, sum[c]));
   }
 }
 
@@ -440,7 +448,7 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
       const int m = 16 * b + 4 * (l >> 4) + r;
       const int64_t n = (int64_t)(t0 + c) * 16 + (l & 15);
       if (m < p.M && n < p.N) {
-        const float v = p.scale ? s * p.scale[n] : s;
+        const float v = gv_scaled(p, n, s);
         y[(int64_t)m * p.ldy + n] = WT == DT_BF16 ? f32_to_bf16(v) : f32_to_f16_bits(v);
       }
     }
@@ -716,7 +724,7 @@ __global__ void __launch_bounds__(64 * KW) gemv_kn_kernel(GemvArgs p, const void
       if (S > 1) {
         part[((int64_t)sp * p.M + m) * p.N + n] = sum;
       } else {
-        const float v = p.scale ? sum * p.scale[n] : sum;
+        const float v = gv_scaled(p, n, sum);
         reinterpret_cast<uint16_t*>(p.y)[(int64_t)m * p.ldy + n] = WT == DT_BF16 ? f32_to_bf16(v) : f32_to_f16_bits(v);
       }
     }
@@ -731,7 +739,7 @@ __global__ void __launch_bounds__(256) gemv_kn_combine_kernel(GemvArgs p, const 
   const int64_t m = t / p.N, n = t - m * p.N;
   float sum = 0.f;
   for (int s = 0; s < S; ++s) sum += part[(int64_t)s * p.M * p.N + t];
-  const float v = p.scale ? sum * p.scale[n] : sum;
+  const float v = gv_scaled(p, n, sum);
   reinterpret_cast<uint16_t*>(p.y)[m * p.ldy + n] = WT == DT_BF16 ? f32_to_bf16(v) : f32_to_f16_bits(v);
 }
 

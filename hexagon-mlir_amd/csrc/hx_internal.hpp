@@ -79,6 +79,7 @@ struct GemvArgs {
   const void* x; int64_t ldx;   // f16 [M][K] (bf16 with bf16 weights)
   const int8_t* w; int64_t ldw; // int8 [N][K] (unregistered int8 weights)
   const float* scale;           // [N], may be null (scale 1)
+  const uint16_t* scale16;      // [N] f16 scale, used when `scale` is null
   void* y; int64_t ldy;         // [M][N], the activations' type
   int64_t M, N, K;
 };
