@@ -350,6 +350,9 @@ static int run_gemm(int op, GemmArgs& a, hipStream_t s, const PlanCtx& ctx) {
     }
     refusal = "no-config";
   }
+  // the generic kernel reads B K-contiguous only (callers check the fast
+  // path before passing a [K][N] B)
+  if (a.b_kn) return fail(HX_ERR_UNSUPPORTED, "matmul: [K][N] B refused by the tiled kernel (%s)", refusal);
   note_plan(ctx, a.M, a.N, a.K, a.out_dtype, "mfma-generic", "generic_32x32", "fixed", refusal);
   return map_internal(launch_gemm_generic(mode, a, s), "gemm_generic");
 }
@@ -522,17 +525,35 @@ extern "C" int hx_matmul(const hx_memref2d* a, int a_dtype, const hx_memref2d* b
     if (op == HX_OP_MATMUL_W8 && M <= 16 && gemv_fast_ok(v)) return run_gemv(v, s, nctx);
   }
 
+  // [K][N] f16 / bf16 operands beyond the decode GEMV's rows: the tiled
+  // kernel reads B in place (transposing LDS reads) when its fast path takes
+  // the shape; otherwise B is transposed into the workspace.
+  bool kn_native = false;
+  if (b_layout == HX_LAYOUT_KN && (op == HX_OP_MATMUL_F16 || op == HX_OP_MATMUL_BF16) && !gemv_rows) {
+    int mode, epi;
+    op_gemm(op, &mode, &epi);
+    GemmArgs t{};
+    t.a = va.p; t.lda = va.ld; t.b = vb.p; t.ldb = vb.ld; t.c = vc.p; t.ldc = vc.ld;
+    t.M = M; t.N = N; t.K = K; t.b_kn = 1;
+    if (residual) { t.res = vr.p; t.ldr = vr.ld; t.res_dtype = residual_dtype; }
+    kn_native = gemm_fast_refusal(mode, t) == nullptr;
+  }
+
   const size_t eb = dt_size(b_dtype);
   Carver cv;
-  const size_t off_bt = b_layout == HX_LAYOUT_KN ? cv.take((size_t)N * K * eb) : 0;
+  const size_t off_bt = (b_layout == HX_LAYOUT_KN && !kn_native) ? cv.take((size_t)N * K * eb) : 0;
   const size_t off_sc = (col_scale && scale_dtype == HX_F16) ? cv.take((size_t)N * 4) : 0;
   char* ws = nullptr;
   if (cv.used && (rc = ws_get(s, cv.used, &ws))) return rc;
 
   GemmArgs g{};
   g.a = va.p; g.lda = va.ld;
-  g.b = b_as_nk(vb, b_layout, eb, ws + off_bt, &g.ldb, s, &rc);
-  if (rc) return rc;
+  if (kn_native) {
+    g.b = vb.p; g.ldb = vb.ld; g.b_kn = 1;
+  } else {
+    g.b = b_as_nk(vb, b_layout, eb, ws + off_bt, &g.ldb, s, &rc);
+    if (rc) return rc;
+  }
   g.c = vc.p; g.ldc = vc.ld;
   g.M = M; g.N = N; g.K = K;
   g.out_dtype = c_dtype;
@@ -540,10 +561,11 @@ extern "C" int hx_matmul(const hx_memref2d* a, int a_dtype, const hx_memref2d* b
     return rc;
   if (residual) { g.res = vr.p; g.ldr = vr.ld; g.res_dtype = residual_dtype; }
 
-  const PlanCtx ctx{"hx_matmul", b_layout == HX_LAYOUT_KN ? "transposed-to-workspace" : "argument",
+  const PlanCtx ctx{"hx_matmul",
+                    kn_native ? "argument-kn" : b_layout == HX_LAYOUT_KN ? "transposed-to-workspace" : "argument",
                     a_dtype, b_dtype};
   // [K][N] weights the in-place GEMV refused: the transposed copy
-  if (b_layout == HX_LAYOUT_KN && gemv_rows) {
+  if (b_layout == HX_LAYOUT_KN && gemv_rows && !kn_native) {
     GemvArgs v{};
     v.x = g.a; v.ldx = g.lda; v.w = (const int8_t*)g.b; v.ldw = g.ldb;
     v.scale = g.col_scale; v.y = g.c; v.ldy = g.ldc; v.M = M; v.N = N; v.K = K;

@@ -129,12 +129,23 @@ __device__ __forceinline__ void interleave_reads_mfma_vmem() {
 // at 4096^3 as 76 us against 59 us for the 8-wave 256x256 tile, so no table
 // entry uses it).  MINW: waves per SIMD the register budget must allow (2
 // caps a wave at 256 registers).
-template <int MODE, int BM, int BN, int WM, int WN, int EPI, int SB = 128, int MINW = 1, bool EDGE = false>
+// BKN (f16 / bf16): B is [K][N], N contiguous.  A stage then holds BKE rows
+// of k, each BN elements, with 64-byte segments XOR-swizzled by the row; the
+// B operand of each MFMA step comes from two transposing LDS reads
+// (ds_read_b64_tr_b16: within each 16-lane group, lane 4a+b receives
+// element b of the 8-byte chunks addressed by lanes a, a+4, a+8, a+12), so
+// lane l = 16G + i, addressing row 16ks + 8(G/2) + 4h + i/4 at column
+// 16(G%2) + 4(i%4) of its 32-column sub-tile, receives column l % 32 at
+// k = 16ks + 8(l/32) + 4h + (0..3) -- the K-contiguous operand without a
+// transpose of B in memory.
+template <int MODE, int BM, int BN, int WM, int WN, int EPI, int SB = 128, int MINW = 1, bool EDGE = false,
+          bool BKN = false>
 __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(MINW, 8)))
 gemm_kernel(GemmArgs p) {
   typedef ModeTraits<MODE> T;
   typedef typename T::Acc Acc;
   static_assert(SB == 128 || (SB == 64 && MODE != GM_W8), "stage width");
+  static_assert(!BKN || ((MODE == GM_F16 || MODE == GM_BF16) && SB == 128 && EPI == GE_STORE), "[K][N] B");
   constexpr int NW = WM * WN;
   constexpr int NB = (EPI == GE_SWIGLU) ? 2 : 1;
   constexpr int BROW = (MODE == GM_W8) ? SB / 2 : SB;  // bytes of B per row in one stage
@@ -193,8 +204,15 @@ gemm_kernel(GemmArgs p) {
   __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(reinterpret_cast<const char*>(p.a) + m0 * lda_b), 0, (int)(rows_a * lda_b), 0x00020000);
   __amdgpu_buffer_rsrc_t rb[NB];
-  rb[0] = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(reinterpret_cast<const char*>(p.b) + n0 * ldb_b), 0, (int)(rows_b * ldb_b), 0x00020000);
+  if constexpr (BKN) {
+    // columns n0.. of every row of k, up to the matrix's last element
+    rb[0] = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(reinterpret_cast<const char*>(p.b) + n0 * T::EB), 0,
+        (int)(((p.K - 1) * p.ldb + (p.N - n0)) * T::EB), 0x00020000);
+  } else {
+    rb[0] = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(reinterpret_cast<const char*>(p.b) + n0 * ldb_b), 0, (int)(rows_b * ldb_b), 0x00020000);
+  }
   if constexpr (NB == 2)
     rb[1] = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(reinterpret_cast<const char*>(p.b2) + n0 * ldb_b), 0, (int)(rows_b * ldb_b),
@@ -217,6 +235,18 @@ gemm_kernel(GemmArgs p) {
   const int a_lim = (int)rows_a - (SB == 128 ? (lane >> 3) : (lane >> 2));
   const int b_lim = (int)rows_b - (BROW == 128 ? (lane >> 3) : (lane >> 2));
   constexpr int BKE = SB / T::EA;  // elements of K per stage
+  // BKN stage layout: BKE rows of k, KROWB bytes each, 64-byte segments
+  // XOR-swizzled so that the 8 rows one transposing read touches (4 + 4,
+  // 8 apart) spread over the four 64-byte bank groups
+  constexpr int KROWB = BN * T::EB;
+  constexpr int KCPR = KROWB / 16;
+  constexpr int KRPB = KROWB >= 1024 ? 1 : 1024 / KROWB;
+  constexpr int KNSEG = KROWB / 64;
+  auto swz_kn = [](int row) -> int {
+    if constexpr (KNSEG >= 4) return row & 3;
+    else if constexpr (KNSEG == 2) return (row >> 1) & 1;
+    else return 0;
+  };
   const int nk = (int)((p.K + BKE - 1) / BKE);
   const uint32_t kb_bytes = (uint32_t)(p.K * T::EB);
 
@@ -244,6 +274,21 @@ gemm_kernel(GemmArgs p) {
         if (blk * A_RPB >= a_lim) off = 0x80000000u;
       dma16(ra, st + blk * 1024, off, (uint32_t)blk * (uint32_t)A_RPB * lda_b);
     });
+    if constexpr (BKN) {
+      // block blk holds k rows blk*KRPB .. of the stage, 16-byte chunk
+      // lane % KCPR of row lane / KCPR; the lane fetches the logical
+      // segment the row's swizzle maps to its physical one
+      static_for<B_PER_W>([&](auto ic) {
+        const int blk = wave + decltype(ic)::value * NW;
+        const int row = blk * KRPB + lane / KCPR, pc = lane % KCPR;
+        const int lcol = (((pc >> 2) ^ swz_kn(row)) << 2) | (pc & 3);  // logical chunk
+        const uint32_t k = (uint32_t)kt * (uint32_t)BKE + (uint32_t)row;
+        uint32_t off = k * ldb_b + (uint32_t)lcol * 16u;
+        if (k >= (uint32_t)p.K) off = 0x80000000u;
+        dma16(rb[0], st + A_BYTES + blk * 1024, off, 0u);
+      });
+      return;
+    }
     static_for<NB>([&](auto nbc) {
       constexpr int nb = decltype(nbc)::value;
       static_for<B_PER_W>([&](auto ic) {
@@ -287,6 +332,8 @@ gemm_kernel(GemmArgs p) {
   auto read_frags = [&](const char* sa, auto ksc) {
     constexpr int ks = decltype(ksc)::value;
     constexpr int s = ks & 1;
+    typedef short v4s_t __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) v4s_t* lds_v4s_t;
     // step ks reads A chunk ca (W8: A is f16, step ks = 2*jp + h covers
     // k = 32*jp + 16*g + 8*h + (0..7) for lane group g, both operands, so
     // every k of the stage is summed exactly once)
@@ -300,7 +347,21 @@ gemm_kernel(GemmArgs p) {
       const int row = wm * WTM + i * 32 + lrow;
       fa[s][i] = *reinterpret_cast<const v4i*>(sa + row * SB + ((ca ^ swz(row)) << 4));
     });
-    if constexpr (MODE != GM_W8) {
+    if constexpr (BKN) {
+      const int G = lane >> 4, i = lane & 15;
+      static_for<TN>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        const int colb = (wn * WTN + 32 * j + 16 * (G & 1) + 4 * (i & 3)) * T::EB;  // byte in the row
+        v2i hv[2];
+        static_for<2>([&](auto hc) {
+          constexpr int h = decltype(hc)::value;
+          const int row = 16 * ks + 8 * (G >> 1) + 4 * h + (i >> 2);
+          const char* a = sa + A_BYTES + row * KROWB + (((colb >> 6) ^ swz_kn(row)) << 6) + (colb & 63);
+          hv[h] = __builtin_bit_cast(v2i, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_t)a));
+        });
+        fb[s][0][j] = v4i{hv[0][0], hv[0][1], hv[1][0], hv[1][1]};
+      });
+    } else if constexpr (MODE != GM_W8) {
       static_for<NB>([&](auto nbc) {
         constexpr int nb = decltype(nbc)::value;
         static_for<TN>([&](auto jc) {
@@ -607,10 +668,17 @@ typedef void (*GemmLaunch)(const GemmArgs&, hipStream_t);
 template <int MODE, int BM, int BN, int WM, int WN, int EPI, int SB = 128, int MINW = 1>
 static void launch_one(const GemmArgs& a, hipStream_t s) {
   const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-  if (a.M % BM == 0 && a.N % BN == 0)
-    gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, false><<<dim3((unsigned)tiles), dim3(64 * WM * WN), 0, s>>>(a);
-  else
-    gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, true><<<dim3((unsigned)tiles), dim3(64 * WM * WN), 0, s>>>(a);
+  const dim3 grid((unsigned)tiles), block(64 * WM * WN);
+  const bool edge = a.M % BM != 0 || a.N % BN != 0;
+  if constexpr ((MODE == GM_F16 || MODE == GM_BF16) && EPI == GE_STORE && SB == 128) {
+    if (a.b_kn) {
+      if (edge) gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, true, true><<<grid, block, 0, s>>>(a);
+      else gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, false, true><<<grid, block, 0, s>>>(a);
+      return;
+    }
+  }
+  if (edge) gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, true><<<grid, block, 0, s>>>(a);
+  else gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, false><<<grid, block, 0, s>>>(a);
 }
 
 struct GemmEntry {

@@ -43,7 +43,7 @@ enum GemmEpi : int { GE_STORE = 0, GE_SWIGLU = 1 };
 
 struct GemmArgs {
   const void* a; int64_t lda;   // [M][K], elements
-  const void* b; int64_t ldb;   // [N][K], elements
+  const void* b; int64_t ldb;   // [N][K], elements ([K][N] when b_kn)
   const void* b2;               // second weight for GE_SWIGLU (same ldb)
   void* c; int64_t ldc;         // [M][N]
   int64_t M, N, K;
@@ -52,6 +52,7 @@ struct GemmArgs {
   const float* col_scale;       // [N], may be null
   const float* col_scale2;      // [N] scale of b2 (GE_SWIGLU)
   const void* res; int64_t ldr; int res_dtype;  // residual, may be null
+  int b_kn;                     // f16 / bf16 only: b is [K][N] (N contiguous)
 };
 
 struct GemmConfig {

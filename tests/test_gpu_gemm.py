@@ -297,3 +297,41 @@ def test_float_every_config(hx, dev, op):
         finally:
             hx.config_select(op, M, N, K, -1)
         assert_close(got.astype(np.float32), want.astype(np.float32), 1e-2, 1e-3, f"op {op} cfg {cfg}")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("shape", [(320, 448, 512), (200, 136, 264), (96, 1024, 192)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_matmul_kn_in_place_every_config(hx, dev, dtype, shape):
+    """[K][N] (linalg orientation) f16 / bf16 B read in place by the tiled
+    kernel (transposing LDS reads, no transposed copy), every config, edge
+    tiles included; with a column scale and an f32 residual once."""
+    import torch
+    M, N, K = shape
+    a = _fp(dtype, (M, K), 130)
+    b = _fp(dtype, (K, N), 131)
+    bf = dtype == "bf16"
+    want = oracle.matmul(a, b, a_bf16=bf, b_bf16=bf, out_bf16=bf)
+    rtol, atol = (1e-2, 1e-3) if dtype == "f16" else (2e-2, 1e-2)
+    op = 2 if dtype == "f16" else 3
+    ad, bd = _torch(a, dtype, dev), _torch(b, dtype, dev)
+    hx.manifest_enable(True)
+    hx.manifest_clear()
+    try:
+        for cfg in range(hx.config_count(op)):
+            hx.config_select(op, M, N, K, cfg)
+            try:
+                got = _vals(to_np(hx.matmul(ad, bd, b_layout="kn")), dtype)
+            finally:
+                hx.config_select(op, M, N, K, -1)
+            assert_close(got, _vals(want, dtype), rtol, atol, f"kn {dtype} {shape} cfg {cfg}")
+        recs = hx.manifest()["records"]
+    finally:
+        hx.manifest_enable(False)
+    assert recs and all(r["weight"] == "argument-kn" and r["plan"] == "mfma-tiled" for r in recs), recs
+    s = rng(132).uniform(0.5, 1.5, N).astype(np.float32)
+    r = rng(133).normal(0, 1, (M, N)).astype(np.float32)
+    c = hx.matmul(ad, bd, b_layout="kn", col_scale=to_dev(s, dev), residual=to_dev(r, dev),
+                  out_dtype=torch.float32)
+    want32 = oracle.matmul(a, b, a_bf16=bf, b_bf16=bf, scale_n=s, residual=r, out_dtype=np.float32)
+    assert_close(to_np(c), want32, 1e-4, 1e-4, f"kn scaled residual {dtype} {shape}")
