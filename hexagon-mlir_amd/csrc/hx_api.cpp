@@ -110,6 +110,28 @@ static int ws_get(hipStream_t s, size_t bytes, char** out) {
   return HX_OK;
 }
 
+// The binary32 partials of a K-split GEMM: a second per-stream region, so
+// that growing it never moves the workspace a caller has already carved.
+static std::map<std::pair<int, hipStream_t>, Workspace> g_part;
+static int part_get(hipStream_t s, size_t bytes, float** out) {
+  int dev;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(g_mu);
+  Workspace& w = g_part[{dev, s}];
+  if (w.bytes < bytes) {
+    size_t nb = (bytes + 4095) & ~(size_t)4095;
+    HX_HIP_TRY(hipStreamSynchronize(s));
+    if (w.buf) HX_HIP_TRY(hipFree(w.buf));
+    w.buf = nullptr;
+    w.bytes = 0;
+    if (hipMalloc(&w.buf, nb) != hipSuccess) return fail(HX_ERR_NOMEM, "split-K partials of %zu bytes", nb);
+    w.bytes = nb;
+  }
+  *out = reinterpret_cast<float*>(w.buf);
+  return HX_OK;
+}
+
 // Carve 256-byte aligned sub-buffers out of one workspace region.
 struct Carver {
   size_t used = 0;
@@ -346,6 +368,10 @@ static int run_gemm(int op, GemmArgs& a, hipStream_t s, const PlanCtx& ctx) {
     if (cfg >= 0) {
       note_plan(ctx, a.M, a.N, a.K, a.out_dtype, "mfma-tiled", gemm_config(mode, cfg)->name,
                 pin ? "pinned" : "default", "selected-aligned");
+      if (const size_t pb = gemm_part_bytes(mode, cfg, a)) {
+        int rc = part_get(s, pb, &a.part);
+        if (rc) return rc;
+      }
       return map_internal(launch_gemm(mode, cfg, a, s), "gemm");
     }
     refusal = "no-config";

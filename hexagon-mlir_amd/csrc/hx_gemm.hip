@@ -136,7 +136,6 @@ static int num_cus() {
 // round is one workgroup in every resident slot (CUs x occ).  The autotuner
 // replaces this guess per shape.
 int gemm_default_config(int mode, int epi, int64_t M, int64_t N, int64_t K) {
-  (void)K;
   int n;
   const GemmEntry* t = table(mode, n);
   if (!t) return -1;
@@ -150,9 +149,13 @@ int gemm_default_config(int mode, int epi, int64_t M, int64_t N, int64_t K) {
   for (int i = 0; i < n; ++i) {
     const GemmConfig& c = t[i].cfg;
     if (c.epi != epi) continue;
-    const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
+    // a K split runs ksplit workgroups per tile on 1/ksplit of K each, plus
+    // a merge; it needs at least 2048 k per part
+    const int ks = c.ksplit > 1 ? c.ksplit : 1;
+    if (ks > 1 && K / ks < 2048) continue;
+    const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * ks;
     const double per_cu = (double)((tiles + cus - 1) / cus);
-    const double cost = per_cu * (double)c.bm * c.bn / c.rate;
+    const double cost = per_cu * (double)c.bm * c.bn / c.rate / ks * (ks > 1 ? 1.05 : 1.0);
     if (best < 0 || cost < best_cost - 1e-9) {
       best = i;
       best_cost = cost;
@@ -191,14 +194,69 @@ const char* gemm_fast_refusal(int mode, const GemmArgs& a) {
 
 bool gemm_fast_ok(int mode, const GemmArgs& a) { return gemm_fast_refusal(mode, a) == nullptr; }
 
+// Merge of a K split: y[m][n] = RNE((sum_s part[s][m][n]) * col_scale[n]
+// (+ residual[m][n])), parts summed in order; four columns per thread
+// (N % 4 == 0 on the tiled path).
+__global__ void __launch_bounds__(256) splitk_merge_kernel(GemmArgs a, const float* part, int parts) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t n4 = a.N / 4;
+  if (q >= a.M * n4) return;
+  const int64_t m = q / n4, n = 4 * (q - m * n4);
+  v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < parts; ++s)
+    acc += *reinterpret_cast<const v4f*>(part + ((int64_t)s * a.M + m) * a.N + n);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float v = acc[i];
+    if (a.col_scale) v = v * a.col_scale[n + i];
+    if (a.res) v = v + load_any(a.res, a.res_dtype, m * a.ldr + n + i);
+    store_out(a.c, a.out_dtype, m * a.ldc + n + i, v);
+  }
+}
+
+static int64_t split_k_elems(const GemmConfig& c, const GemmArgs& a) {
+  // whole 128-byte stages of A per part
+  const int64_t bke = 64;  // f16 / bf16 A: 64 k per stage
+  const int64_t per = (a.K + c.ksplit - 1) / c.ksplit;
+  return (per + bke - 1) / bke * bke;
+}
+
+size_t gemm_part_bytes(int mode, int cfg_idx, const GemmArgs& a) {
+  int n;
+  const GemmEntry* t = table(mode, n);
+  if (!t || cfg_idx < 0 || cfg_idx >= n || t[cfg_idx].cfg.ksplit <= 1) return 0;
+  const int64_t ks = split_k_elems(t[cfg_idx].cfg, a);
+  const int64_t parts = (a.K + ks - 1) / ks;
+  return (size_t)parts * (size_t)(a.M * a.N) * sizeof(float);
+}
+
 int launch_gemm(int mode, int cfg_idx, const GemmArgs& a, hipStream_t s) {
   int n;
   const GemmEntry* t = table(mode, n);
   if (!t || cfg_idx < 0 || cfg_idx >= n) return HXI_ERR_ARG;
-  const int64_t tiles = ((a.M + t[cfg_idx].cfg.bm - 1) / t[cfg_idx].cfg.bm) *
-                        ((a.N + t[cfg_idx].cfg.bn - 1) / t[cfg_idx].cfg.bn);
+  const GemmConfig& c = t[cfg_idx].cfg;
+  const int64_t tiles = ((a.M + c.bm - 1) / c.bm) * ((a.N + c.bn - 1) / c.bn);
   if (tiles <= 0 || tiles > 0x7fffffff) return HXI_ERR_SHAPE;
-  t[cfg_idx].fn(a, s);
+  if (c.ksplit <= 1) {
+    GemmArgs q = a;
+    q.k_split = 0;
+    t[cfg_idx].fn(q, s);
+    return HXI_OK;
+  }
+  // K split: binary32 partials into a.part, then the merge applies the
+  // epilogue (column scale, residual, rounding)
+  if (mode == GM_I8 || a.b2 || !a.part || a.row_scale) return HXI_ERR_ARG;
+  GemmArgs q = a;
+  q.k_split = split_k_elems(c, a);
+  q.c = a.part;
+  q.ldc = a.N;
+  q.out_dtype = DT_F32;
+  q.col_scale = nullptr;
+  q.res = nullptr;
+  const int parts = (int)((a.K + q.k_split - 1) / q.k_split);
+  t[cfg_idx].fn(q, s);
+  const int64_t threads = a.M * (a.N / 4);
+  splitk_merge_kernel<<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s>>>(a, a.part, parts);
   return HXI_OK;
 }
 

@@ -7,7 +7,12 @@ namespace hx {
 // A host function holding the table: a namespace-scope array of host
 // function pointers would also be emitted by the device compilation.
 const GemmEntry* gemm_table_bf16(int& n) {
-  static const GemmEntry t[] = {HX_GEMM_CFGS(GM_BF16)};
+  static const GemmEntry t[] = {
+      HX_GEMM_CFGS(GM_BF16),
+      // K in two parts (binary32 partials and a merge): fills the chip when
+      // the 256x256 tiles of a long-K product are fewer than the CUs
+      {{256, 256, 2, 4, GE_STORE, "256x256_w2x4_k2", 1, 1.00f, 2}, &launch_one<GM_BF16, 256, 256, 2, 4, GE_STORE>},
+  };
   n = (int)(sizeof(t) / sizeof(t[0]));
   return t;
 }

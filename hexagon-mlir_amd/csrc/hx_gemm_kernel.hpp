@@ -177,6 +177,16 @@ gemm_kernel(GemmArgs p) {
   __shared__ __attribute__((aligned(1024))) float scl[(1 + NB) * SC_ROWS];
   __shared__ __attribute__((aligned(1024))) char st1[STAGE];
 
+  // K split: workgroup row blockIdx.y sums k in [y k_split, (y+1) k_split)
+  // into the binary32 slice y of c (launch_gemm merges the slices)
+  if (gridDim.y > 1) {
+    const int64_t k0 = (int64_t)blockIdx.y * p.k_split;
+    p.a = reinterpret_cast<const char*>(p.a) + k0 * T::EA;
+    p.b = reinterpret_cast<const char*>(p.b) + k0 * (BKN ? p.ldb : 1) * T::EB;
+    p.K = min(p.k_split, p.K - k0);
+    p.c = reinterpret_cast<char*>(p.c) + (int64_t)blockIdx.y * p.M * p.ldc * 4;
+  }
+
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   // wave index as a provably uniform (scalar) value: the direct-load LDS
@@ -668,7 +678,8 @@ typedef void (*GemmLaunch)(const GemmArgs&, hipStream_t);
 template <int MODE, int BM, int BN, int WM, int WN, int EPI, int SB = 128, int MINW = 1>
 static void launch_one(const GemmArgs& a, hipStream_t s) {
   const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-  const dim3 grid((unsigned)tiles), block(64 * WM * WN);
+  const unsigned parts = a.k_split > 0 ? (unsigned)((a.K + a.k_split - 1) / a.k_split) : 1u;
+  const dim3 grid((unsigned)tiles, parts), block(64 * WM * WN);
   const bool edge = a.M % BM != 0 || a.N % BN != 0;
   if constexpr ((MODE == GM_F16 || MODE == GM_BF16) && EPI == GE_STORE && SB == 128) {
     if (a.b_kn) {

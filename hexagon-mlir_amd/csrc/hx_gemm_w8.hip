@@ -13,6 +13,9 @@ const GemmEntry* gemm_table_w8(int& n) {
     {{256, 128, 2, 2, GE_SWIGLU, "swiglu_256x128_w2x2", 1, 0.77f}, &launch_one<GM_W8, 256, 128, 2, 2, GE_SWIGLU>},
     {{128, 128, 2, 2, GE_SWIGLU, "swiglu_128x128_w2x2", 1, 0.80f}, &launch_one<GM_W8, 128, 128, 2, 2, GE_SWIGLU>},
     {{128, 64, 2, 2, GE_SWIGLU, "swiglu_128x64_w2x2", 2, 0.80f}, &launch_one<GM_W8, 128, 64, 2, 2, GE_SWIGLU>},
+    // K in two parts (binary32 partials and a merge): the FFN down
+    // projection's 2048x4096 output is 128 tiles of 256x256 for 256 CUs
+    {{256, 256, 2, 4, GE_STORE, "256x256_w2x4_k2", 1, 1.00f, 2}, &launch_one<GM_W8, 256, 256, 2, 4, GE_STORE>},
 };
   n = (int)(sizeof(t) / sizeof(t[0]));
   return t;

@@ -53,6 +53,11 @@ struct GemmArgs {
   const float* col_scale2;      // [N] scale of b2 (GE_SWIGLU)
   const void* res; int64_t ldr; int res_dtype;  // residual, may be null
   int b_kn;                     // f16 / bf16 only: b is [K][N] (N contiguous)
+  // K split (float modes): the kernel runs gridDim.y parts of k_split
+  // elements, each writing binary32 partials to its [M][N] slice of c;
+  // `part` is the partial buffer launch_gemm uses for a split config
+  int64_t k_split;
+  float* part;
 };
 
 struct GemmConfig {
@@ -61,7 +66,10 @@ struct GemmConfig {
   const char* name;
   int occ;              // workgroups resident per CU (LDS / register limit)
   float rate;           // measured output throughput of one CU, relative
+  int ksplit;           // K parts (0 or 1: none); partials merged by a second kernel
 };
+// Partial-buffer bytes a launch of config cfg_idx needs (0 without a K split).
+size_t gemm_part_bytes(int mode, int cfg_idx, const GemmArgs& a);
 
 int gemm_config_count(int mode);
 const GemmConfig* gemm_config(int mode, int idx);

@@ -335,3 +335,39 @@ def test_matmul_kn_in_place_every_config(hx, dev, dtype, shape):
                   out_dtype=torch.float32)
     want32 = oracle.matmul(a, b, a_bf16=bf, b_bf16=bf, scale_n=s, residual=r, out_dtype=np.float32)
     assert_close(to_np(c), want32, 1e-4, 1e-4, f"kn scaled residual {dtype} {shape}")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("layout", ["nk", "kn"])
+def test_matmul_split_k_scale_residual(hx, dev, dtype, layout):
+    """The K-split config (binary32 partials over two K parts, merged with
+    the column scale and the residual) against the oracle, with K not a
+    multiple of the part size and an edge tile."""
+    import torch
+    M, N, K = 272, 200, 1000
+    a = _fp(dtype, (M, K), 140)
+    b = _fp(dtype, (K, N), 141)
+    bf = dtype == "bf16"
+    s = rng(142).uniform(0.5, 1.5, N).astype(np.float32)
+    r = rng(143).normal(0, 1, (M, N)).astype(np.float32)
+    op = 2 if dtype == "f16" else 3
+    names = [hx.config_get(op, i)["name"] for i in range(hx.config_count(op))]
+    cfg = names.index("256x256_w2x4_k2")
+    bb = b if layout == "kn" else np.ascontiguousarray(b.T)
+    hx.config_select(op, M, N, K, cfg)
+    hx.manifest_enable(True)
+    hx.manifest_clear()
+    try:
+        c = hx.matmul(_torch(a, dtype, dev), _torch(bb, dtype, dev), b_layout=layout,
+                      col_scale=to_dev(s, dev), residual=to_dev(r, dev), out_dtype=torch.float32)
+        plain = hx.matmul(_torch(a, dtype, dev), _torch(bb, dtype, dev), b_layout=layout)
+        recs = hx.manifest()["records"]
+    finally:
+        hx.manifest_enable(False)
+        hx.config_select(op, M, N, K, -1)
+    assert all(rc["config"] == "256x256_w2x4_k2" for rc in recs), recs
+    want = oracle.matmul(a, b, a_bf16=bf, b_bf16=bf, scale_n=s, residual=r, out_dtype=np.float32)
+    assert_close(to_np(c), want, 1e-4, 1e-4, f"split-K {dtype} {layout}")
+    want16 = oracle.matmul(a, b, a_bf16=bf, b_bf16=bf, out_bf16=bf)
+    rtol, atol = (1e-2, 1e-3) if dtype == "f16" else (2e-2, 1e-2)
+    assert_close(_vals(to_np(plain), dtype), _vals(want16, dtype), rtol, atol, f"split-K plain {dtype} {layout}")
