@@ -143,19 +143,24 @@ int gemm_default_config(int mode, int epi, int64_t M, int64_t N, int64_t K) {
   int best = -1;
   double best_cost = 0;
   // Cost: the tiles of the busiest CU times one tile's area over the
-  // config's relative per-CU rate (tiles sharing a CU split its rate).
-  // Counting occupancy-limited rounds instead picked 64x64 at 2048^3, where
-  // 128x128 measured 1.2-1.4x faster (f16 and int8).
+  // config's relative per-CU rate (tiles sharing a CU split its rate),
+  // divided by an occupancy efficiency sqrt(resident / occ): a CU holding
+  // fewer workgroups than it can is latency-bound (one 64x64 tile per CU ran
+  // at half speed).  A K split runs ksplit workgroups per tile on 1/ksplit
+  // of K each, plus a merge (x1.5), and needs >= 512 k per part.  Counting
+  // occupancy-limited rounds instead picked 64x64 at 2048^3, where 128x128
+  // measured 1.2-1.4x faster (f16 and int8).
   for (int i = 0; i < n; ++i) {
     const GemmConfig& c = t[i].cfg;
     if (c.epi != epi) continue;
-    // a K split runs ksplit workgroups per tile on 1/ksplit of K each, plus
-    // a merge; it needs at least 2048 k per part
     const int ks = c.ksplit > 1 ? c.ksplit : 1;
-    if (ks > 1 && K / ks < 2048) continue;
+    if (ks > 1 && K / ks < 512) continue;
     const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * ks;
-    const double per_cu = (double)((tiles + cus - 1) / cus);
-    const double cost = per_cu * (double)c.bm * c.bn / c.rate / ks * (ks > 1 ? 1.05 : 1.0);
+    const int64_t per_cu_i = (tiles + cus - 1) / cus;
+    const double per_cu = (double)per_cu_i;
+    const double resident = (double)(per_cu_i < c.occ ? per_cu_i : c.occ);
+    const double eff = sqrt(resident / (double)c.occ);
+    const double cost = per_cu * (double)c.bm * c.bn / c.rate / ks / eff * (ks > 1 ? 1.5 : 1.0);
     if (best < 0 || cost < best_cost - 1e-9) {
       best = i;
       best_cost = cost;

@@ -12,6 +12,9 @@ const GemmEntry* gemm_table_bf16(int& n) {
       // K in two parts (binary32 partials and a merge): fills the chip when
       // the 256x256 tiles of a long-K product are fewer than the CUs
       {{256, 256, 2, 4, GE_STORE, "256x256_w2x4_k2", 1, 1.00f, 2}, &launch_one<GM_BF16, 256, 256, 2, 4, GE_STORE>},
+      // small tiles with K in parts: more workgroups per CU for skinny M
+      {{128, 128, 2, 2, GE_STORE, "128x128_w2x2_k2", 2, 0.89f, 2}, &launch_one<GM_BF16, 128, 128, 2, 2, GE_STORE>},
+      {{64, 64, 2, 2, GE_STORE, "64x64_w2x2_k4", 4, 0.61f, 4}, &launch_one<GM_BF16, 64, 64, 2, 2, GE_STORE>},
   };
   n = (int)(sizeof(t) / sizeof(t[0]));
   return t;
