@@ -147,7 +147,8 @@ int gemm_default_config(int mode, int epi, int64_t M, int64_t N, int64_t K) {
   // divided by an occupancy efficiency sqrt(resident / occ): a CU holding
   // fewer workgroups than it can is latency-bound (one 64x64 tile per CU ran
   // at half speed).  A K split runs ksplit workgroups per tile on 1/ksplit
-  // of K each, plus a merge (x1.5), and needs >= 512 k per part.  Counting
+  // of K each, plus a merge (x1.5, x1.05 from K = 8192 on, where the merge
+  // is small against the product), and needs >= 512 k per part.  Counting
   // occupancy-limited rounds instead picked 64x64 at 2048^3, where 128x128
   // measured 1.2-1.4x faster (f16 and int8).
   for (int i = 0; i < n; ++i) {
@@ -160,7 +161,8 @@ int gemm_default_config(int mode, int epi, int64_t M, int64_t N, int64_t K) {
     const double per_cu = (double)per_cu_i;
     const double resident = (double)(per_cu_i < c.occ ? per_cu_i : c.occ);
     const double eff = sqrt(resident / (double)c.occ);
-    const double cost = per_cu * (double)c.bm * c.bn / c.rate / ks / eff * (ks > 1 ? 1.5 : 1.0);
+    const double merge = ks > 1 ? (K >= 8192 ? 1.05 : 1.5) : 1.0;
+    const double cost = per_cu * (double)c.bm * c.bn / c.rate / ks / eff * merge;
     if (best < 0 || cost < best_cost - 1e-9) {
       best = i;
       best_cost = cost;
