@@ -204,6 +204,62 @@ bool gemm_fast_ok(int mode, const GemmArgs& a) { return gemm_fast_refusal(mode, 
 // Merge of a K split: y[m][n] = RNE((sum_s part[s][m][n]) * col_scale[n]
 // (+ residual[m][n])), parts summed in order; four columns per thread
 // (N % 4 == 0 on the tiled path).
+// Eight columns per thread with 16-byte loads and stores (N, ldc and ldr
+// multiples of 8, 16-byte aligned column scales): OUT is the output type,
+// the residual's type is a uniform branch.
+template <int OUT>
+__global__ void __launch_bounds__(256) splitk_merge8_kernel(GemmArgs a, const float* part, int parts) {
+  const uint32_t q = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t n8 = (uint32_t)(a.N >> 3);
+  if (q >= (uint32_t)a.M * n8) return;
+  const uint32_t m = q / n8;
+  const int64_t n = 8 * (int64_t)(q - m * n8);
+  const int64_t mn = a.M * a.N;
+  const float* p = part + (int64_t)m * a.N + n;
+  v4f lo = v4f{0.f, 0.f, 0.f, 0.f}, hi = lo;
+  for (int s = 0; s < parts; ++s) {
+    lo += *reinterpret_cast<const v4f*>(p + s * mn);
+    hi += *reinterpret_cast<const v4f*>(p + s * mn + 4);
+  }
+  float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  if (a.col_scale) {
+    const v4f s0 = *reinterpret_cast<const v4f*>(a.col_scale + n);
+    const v4f s1 = *reinterpret_cast<const v4f*>(a.col_scale + n + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { v[i] = v[i] * s0[i]; v[i + 4] = v[i + 4] * s1[i]; }
+  }
+  if (a.res) {
+    const int64_t r = (int64_t)m * a.ldr + n;
+    if (a.res_dtype == DT_F32) {
+      const v4f r0 = *reinterpret_cast<const v4f*>(reinterpret_cast<const float*>(a.res) + r);
+      const v4f r1 = *reinterpret_cast<const v4f*>(reinterpret_cast<const float*>(a.res) + r + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { v[i] = v[i] + r0[i]; v[i + 4] = v[i + 4] + r1[i]; }
+    } else {
+      const v4i rr = *reinterpret_cast<const v4i*>(reinterpret_cast<const uint16_t*>(a.res) + r);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint16_t h = (uint16_t)((uint32_t)rr[i >> 1] >> (16 * (i & 1)));
+        v[i] = v[i] + (a.res_dtype == DT_F16 ? f16_bits_to_f32(h) : bf16_to_f32(h));
+      }
+    }
+  }
+  const int64_t o = (int64_t)m * a.ldc + n;
+  if constexpr (OUT == DT_F32) {
+    *reinterpret_cast<v4f*>(reinterpret_cast<float*>(a.c) + o) = v4f{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<v4f*>(reinterpret_cast<float*>(a.c) + o + 4) = v4f{v[4], v[5], v[6], v[7]};
+  } else {
+    v4i w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t l = OUT == DT_F16 ? f32_to_f16_bits(v[2 * i]) : f32_to_bf16(v[2 * i]);
+      const uint32_t h = OUT == DT_F16 ? f32_to_f16_bits(v[2 * i + 1]) : f32_to_bf16(v[2 * i + 1]);
+      w[i] = (int)(l | (h << 16));
+    }
+    *reinterpret_cast<v4i*>(reinterpret_cast<uint16_t*>(a.c) + o) = w;
+  }
+}
+
 __global__ void __launch_bounds__(256) splitk_merge_kernel(GemmArgs a, const float* part, int parts) {
   const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t n4 = a.N / 4;
@@ -262,6 +318,17 @@ int launch_gemm(int mode, int cfg_idx, const GemmArgs& a, hipStream_t s) {
   q.res = nullptr;
   const int parts = (int)((a.K + q.k_split - 1) / q.k_split);
   t[cfg_idx].fn(q, s);
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  const bool v8 = a.N % 8 == 0 && a.ldc % 8 == 0 && (!a.res || a.ldr % 8 == 0) &&
+                  (!a.col_scale || al16(a.col_scale)) && a.M * (a.N / 8) < ((int64_t)1 << 31) &&
+                  (a.out_dtype == DT_F16 || a.out_dtype == DT_BF16 || a.out_dtype == DT_F32);
+  if (v8) {
+    const dim3 grid((unsigned)((a.M * (a.N / 8) + 255) / 256));
+    if (a.out_dtype == DT_F16) splitk_merge8_kernel<DT_F16><<<grid, dim3(256), 0, s>>>(a, a.part, parts);
+    else if (a.out_dtype == DT_BF16) splitk_merge8_kernel<DT_BF16><<<grid, dim3(256), 0, s>>>(a, a.part, parts);
+    else splitk_merge8_kernel<DT_F32><<<grid, dim3(256), 0, s>>>(a, a.part, parts);
+    return HXI_OK;
+  }
   const int64_t threads = a.M * (a.N / 4);
   splitk_merge_kernel<<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s>>>(a, a.part, parts);
   return HXI_OK;

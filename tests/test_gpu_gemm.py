@@ -371,3 +371,45 @@ def test_matmul_split_k_scale_residual(hx, dev, dtype, layout):
     want16 = oracle.matmul(a, b, a_bf16=bf, b_bf16=bf, out_bf16=bf)
     rtol, atol = (1e-2, 1e-3) if dtype == "f16" else (2e-2, 1e-2)
     assert_close(_vals(to_np(plain), dtype), _vals(want16, dtype), rtol, atol, f"split-K plain {dtype} {layout}")
+
+
+@pytest.mark.parametrize("dtype,res_dtype", [("f16", "f16"), ("bf16", "bf16"), ("f16", "f32"), ("bf16", "f16")])
+def test_matmul_split_k_merge_widths_agree(hx, dev, dtype, res_dtype):
+    """The K-split merge runs eight columns per thread when the output and
+    residual row strides are multiples of 8 and four otherwise.  The same
+    partials merged both ways (outputs with row strides 200 and 204) agree
+    bit for bit, with the column scale, a residual of another type and a
+    rounded 16-bit output, and match the oracle."""
+    import torch
+    M, N, K = 272, 200, 1000
+    a = _fp(dtype, (M, K), 150)
+    b = _fp(dtype, (N, K), 151)
+    bf = dtype == "bf16"
+    s = rng(152).uniform(0.5, 1.5, N).astype(np.float32)
+    r = rng(153).normal(0, 1, (M, N)).astype(np.float32)
+    tdt = torch.bfloat16 if bf else torch.float16
+    rt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[res_dtype]
+    op = 2 if dtype == "f16" else 3
+    names = [hx.config_get(op, i)["name"] for i in range(hx.config_count(op))]
+    hx.config_select(op, M, N, K, names.index("256x256_w2x4_k2"))
+    try:
+        A, B = _torch(a, dtype, dev), _torch(b, dtype, dev)
+        res8 = torch.from_numpy(r).to(dev).to(rt)
+        res4 = torch.zeros((M, 204), dtype=rt, device=dev)[:, :N]
+        res4.copy_(res8)
+        outs = []
+        for ld, res in ((200, res8), (204, res4)):
+            out = torch.full((M, ld), 7.0, dtype=tdt, device=dev)[:, :N]
+            hx.matmul(A, B, b_layout="nk", col_scale=to_dev(s, dev), residual=res, out=out)
+            outs.append(out.contiguous().view(torch.int16).cpu())
+        torch.cuda.synchronize()
+    finally:
+        hx.config_select(op, M, N, K, -1)
+    assert torch.equal(outs[0], outs[1])
+    rq = res8.float().cpu().numpy()
+    want = oracle.matmul(a, np.ascontiguousarray(b.T), a_bf16=bf, b_bf16=bf, scale_n=s, residual=rq,
+                         out_dtype=np.float32)
+    got = outs[0].numpy().view(np.uint16)
+    got = oracle.bf16_bits_to_f32(got) if bf else got.view(np.float16).astype(np.float32)
+    rtol, atol = (1e-2, 1e-2) if not bf else (2e-2, 5e-2)
+    assert_close(got, want, rtol, atol, f"split-K merge {dtype} res {res_dtype}")
