@@ -180,17 +180,36 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
   const uint32_t v_bytes = (uint32_t)(((p.Nk - 1) * p.sv[2] + D) * 2);
   const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)k, 0, (int)k_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)v, 0, (int)v_bytes, 0x00020000);
+  // The lane's part of each offset (its row within the block and swizzled
+  // chunk) is fixed; the block's first key enters as the uniform scalar
+  // offset.  Only a block that reaches past Nk selects per row.
+  uint32_t k_lane[PER_W], v_lane[PER_W];
+  int row_l[PER_W];
+  static_for<PER_W>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    const int row = (wave + 4 * i) * RPK + lane / CPR, pc = lane % CPR;
+    row_l[i] = row;
+    k_lane[i] = (uint32_t)row * sk_b + (uint32_t)((pc ^ swz_k<D>(row)) << 4);
+    v_lane[i] = (uint32_t)row * sv_b + (uint32_t)((pc ^ swz_v<D>(row)) << 4);
+  });
   auto dma_block = [&](char* dk, char* dv, int blk) {
-    static_for<PER_W>([&](auto ic) {
-      const int lb = wave + 4 * decltype(ic)::value;
-      const int row = lb * RPK + lane / CPR, pc = lane % CPR;
-      const int64_t key = (int64_t)blk * ATT_BN + row;
-      const bool in = key < p.Nk;
-      const uint32_t ko = in ? (uint32_t)key * sk_b + (uint32_t)((pc ^ swz_k<D>(row)) << 4) : 0x80000000u;
-      const uint32_t vo = in ? (uint32_t)key * sv_b + (uint32_t)((pc ^ swz_v<D>(row)) << 4) : 0x80000000u;
-      dma16(rk, dk + lb * 1024, ko, 0u);
-      dma16(rv, dv + lb * 1024, vo, 0u);
-    });
+    const int64_t key0 = (int64_t)blk * ATT_BN;
+    const uint32_t ks = (uint32_t)key0 * sk_b, vs = (uint32_t)key0 * sv_b;
+    if (key0 + ATT_BN <= p.Nk) {
+      static_for<PER_W>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        dma16(rk, dk + (wave + 4 * i) * 1024, k_lane[i], ks);
+        dma16(rv, dv + (wave + 4 * i) * 1024, v_lane[i], vs);
+      });
+    } else {
+      const int lim = (int)(p.Nk - key0);
+      static_for<PER_W>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        const bool in = row_l[i] < lim;
+        dma16(rk, dk + (wave + 4 * i) * 1024, in ? k_lane[i] : 0x80000000u, ks);
+        dma16(rv, dv + (wave + 4 * i) * 1024, in ? v_lane[i] : 0x80000000u, vs);
+      });
+    }
   };
 
   // The V^T operand of 16-key step t, keys 16t + 8*half + 4*lg + (0..3) of
