@@ -69,3 +69,34 @@ def test_swiglu_every_config(hx, dev):
             assert_close(got.astype(np.float32), want, 2e-2, 2e-3, f"swiglu cfg {cfg}")
     finally:
         Wg.release(); Wu.release(); Wd.release()
+
+
+def test_swiglu_down_projection_split_k(hx, dev):
+    """The down projection through the K-split config (the untuned default at
+    the full 2048 x 4096 x 11008 shape): binary32 partials over two halves of
+    the intermediate dimension, merged with the down scale, against the
+    oracle's composition."""
+    T, H, I = 256, 512, 1376
+    wg, sg, wu, su, wd, sd = weights(H, I, 320)
+    x = rng(321).normal(0, 1, (T, H)).astype(np.float16)
+    gamma = rng(322).normal(1, 0.1, H).astype(np.float16)
+    want = oracle.swiglu_ffn(x, gamma, 1e-6, wg, sg, wu, su, wd, sd).astype(np.float32)
+    Wg = hx.ResidentWeight(to_dev(wg, dev), to_dev(sg, dev))
+    Wu = hx.ResidentWeight(to_dev(wu, dev), to_dev(su, dev))
+    Wd = hx.ResidentWeight(to_dev(wd, dev), to_dev(sd, dev))
+    names = [hx.config_get(4, i)["name"] for i in range(hx.config_count(4))]
+    hx.config_select(4, T, H, I, names.index("256x256_w2x4_k2"))
+    hx.manifest_enable(True)
+    hx.manifest_clear()
+    try:
+        got = to_np(hx.swiglu_ffn(to_dev(x, dev), to_dev(gamma, dev), 1e-6, Wg, Wu, Wd)).astype(np.float32)
+        recs = hx.manifest()["records"]
+    finally:
+        hx.manifest_enable(False)
+        hx.config_select(4, T, H, I, -1)
+        Wg.release(); Wu.release(); Wd.release()
+    assert any(rc["config"] == "256x256_w2x4_k2" for rc in recs), \
+        [(rc["plan"], rc["config"], rc["reason"]) for rc in recs]
+    assert_close(got, want, 2e-2, 2e-3, "swiglu split down projection")
+    rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+    assert rel < 2e-3, rel

@@ -413,3 +413,33 @@ def test_matmul_split_k_merge_widths_agree(hx, dev, dtype, res_dtype):
     got = oracle.bf16_bits_to_f32(got) if bf else got.view(np.float16).astype(np.float32)
     rtol, atol = (1e-2, 1e-2) if not bf else (2e-2, 5e-2)
     assert_close(got, want, rtol, atol, f"split-K merge {dtype} res {res_dtype}")
+
+
+@pytest.mark.parametrize("cfg_name", ["256x256_w2x4_k2", "128x128_w2x2_k2", "64x64_w2x2_k4"])
+def test_matmul_w8a16_split_k_scale_residual(hx, dev, cfg_name):
+    """W8A16 (f16 activations, int8 [N][K] weights) through each K-split
+    config, with the per-channel f16 scale and an f16 residual merged after
+    the partial sums: an edge tile in M and N, and K not a multiple of the
+    part size."""
+    import torch
+    M, N, K = 200, 328, 1168
+    x = rng(160).normal(0, 1, (M, K)).astype(np.float16)
+    w = i8((N, K), 161)
+    s = rng(162).uniform(0.001, 0.02, N).astype(np.float16)
+    r = rng(163).normal(0, 1, (M, N)).astype(np.float16)
+    names = [hx.config_get(4, i)["name"] for i in range(hx.config_count(4))]
+    hx.config_select(4, M, N, K, names.index(cfg_name))
+    hx.manifest_enable(True)
+    hx.manifest_clear()
+    try:
+        y = hx.matmul(to_dev(x, dev), to_dev(w, dev), b_layout="nk", col_scale=to_dev(s, dev),
+                      residual=to_dev(r, dev))
+        torch.cuda.synchronize()
+        recs = hx.manifest()["records"]
+    finally:
+        hx.manifest_enable(False)
+        hx.config_select(4, M, N, K, -1)
+    assert recs and all(rc["config"] == cfg_name for rc in recs), \
+        [(rc["plan"], rc["config"], rc["reason"]) for rc in recs]
+    want = oracle.matmul(x, w, b_trans=True, scale_n=s.astype(np.float32), residual=r)
+    assert_close(to_np(y).astype(np.float32), want.astype(np.float32), 1e-2, 2e-3, f"w8a16 split {cfg_name}")
