@@ -30,6 +30,11 @@ attention              numpy float64 softmax(QK^T s)V; V = 1 gives 1;
                        one key returns its value row; causal row 0 is v[0];
                        torch-CPU scaled_dot_product_attention at the reference
                        test's shape and relative-error bound
+swiglu_ffn             an independent float64 composition (numpy matmuls, no
+                       fp16 stages) within the bound of five fp16 roundings;
+                       negative controls: gate/up swapped, per-channel scales
+                       on the wrong channels, gamma dropped, silu on the up
+                       branch; row independence (a row subset is bit-equal)
 =====================  ======================================================
 """
 from __future__ import annotations
@@ -65,12 +70,39 @@ def build(force: bool = True) -> Path:
     return LIB
 
 
-def lib():
+def use_native_build() -> str:
+    """Compile the C restatement for the host it runs on (-march=native,
+    the CPU baseline's build) into a temporary directory and make it the
+    library every function below calls.  The in-tree build targets
+    x86-64-v3 so that it loads on any x86 host; this one uses every vector
+    extension the host has.  Returns the -march flags gcc resolved."""
     global _lib
+    import tempfile
+    d = Path(tempfile.mkdtemp(prefix="hx_oracle_native_"))
+    out = d / "liboracle_native.so"
+    subprocess.run(["gcc", "-O3", "-march=native", "-fopenmp", "-ffp-contract=off", "-fno-math-errno",
+                    "-fPIC", "-shared", str(SRC), "-o", str(out), "-lm"], check=True)
+    _lib = None
+    _bind(ctypes.CDLL(str(out)))
+    r = subprocess.run(["gcc", "-march=native", "-Q", "--help=target"], capture_output=True, text=True)
+    for line in r.stdout.splitlines():
+        if line.strip().startswith("-march="):
+            return line.split()[-1]
+    return "native"
+
+
+def lib():
     if _lib is None:
         if not LIB.exists():
             build()
-        L = ctypes.CDLL(str(LIB))
+        _bind(ctypes.CDLL(str(LIB)))
+    return _lib
+
+
+def _bind(L):
+    """Declare the C signatures on a loaded copy and make it the active one."""
+    global _lib
+    if True:  # noqa: SIM108 -- one block of declarations
         vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
         L.hxo_f32_to_f16_array.argtypes = [vp, vp, i64]
         L.hxo_f16_to_f32_array.argtypes = [vp, vp, i64]
@@ -85,7 +117,6 @@ def lib():
         L.hxo_silu_mul.argtypes = [vp, vp, vp, i32, i64, i64, i64, i64, i64]
         L.hxo_attention.argtypes = [vp, vp, vp, vp, i32, i64, i64, i64, i64, f32, i32]
         _lib = L
-    return _lib
 
 
 # --------------------------------------------------------------------------- #

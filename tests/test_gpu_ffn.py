@@ -100,3 +100,38 @@ def test_swiglu_down_projection_split_k(hx, dev):
     assert_close(got, want, 2e-2, 2e-3, "swiglu split down projection")
     rel = np.linalg.norm(got - want) / np.linalg.norm(want)
     assert rel < 2e-3, rel
+
+
+def test_swiglu_ffn_c5_full_size(hx, dev):
+    """BASELINE config C5 at its own shape: tokens 2048, hidden 4096,
+    intermediate 11008, seeded int8 weights with per-channel fp16 scales,
+    gamma N(1, 0.1).  This runs the fused gate/up GEMM over its 688 output
+    tiles and the down projection's K = 11008 (split into two binary32 halves
+    by the untuned default), checked against the oracle on sampled token rows
+    (tokens are independent rows; the first and last are included)."""
+    T, H, I = 2048, 4096, 11008
+    wg, sg, wu, su, wd, sd = weights(H, I, 330)
+    x = rng(331).normal(0, 1, (T, H)).astype(np.float16)
+    gamma = rng(332).normal(1, 0.1, H).astype(np.float16)
+    Wg = hx.ResidentWeight(to_dev(wg, dev), to_dev(sg, dev))
+    Wu = hx.ResidentWeight(to_dev(wu, dev), to_dev(su, dev))
+    Wd = hx.ResidentWeight(to_dev(wd, dev), to_dev(sd, dev))
+    hx.manifest_clear()
+    hx.manifest_enable(True)
+    try:
+        y = to_np(hx.swiglu_ffn(to_dev(x, dev), to_dev(gamma, dev), 1e-6, Wg, Wu, Wd)).astype(np.float32)
+        recs = hx.manifest()["records"]
+    finally:
+        hx.manifest_enable(False)
+        Wg.release(); Wu.release(); Wd.release()
+    plans = {(rc["m"], rc["n"], rc["k"]): rc for rc in recs}
+    assert plans[(T, I, H)]["plan"] == "mfma-tiled", plans
+    assert plans[(T, H, I)]["plan"] == "mfma-tiled", plans
+    rows = np.unique(np.concatenate([[0, 1, 255, 256, 1023, 1024, 2046, 2047],
+                                     rng(333).integers(0, T, 8)]))
+    want = oracle.swiglu_ffn(np.ascontiguousarray(x[rows]), gamma, 1e-6, wg, sg, wu, su, wd, sd)
+    got = y[rows]
+    assert np.isfinite(y).all()
+    assert_close(got, want.astype(np.float32), 2e-2, 2e-3, "swiglu C5 sampled rows")
+    rel = np.linalg.norm(got - want) / np.linalg.norm(want.astype(np.float32))
+    assert rel < 2e-3, rel

@@ -117,3 +117,29 @@ def test_silu_mul(hx, dev):
     # odd width takes the element path
     y2 = hx.silu_mul(to_dev(g[:, :1001].copy(), dev), to_dev(u[:, :1001].copy(), dev))
     assert_close(to_np(y2).astype(np.float32), want[:, :1001].astype(np.float32), 1e-2, 1e-3, "silu_mul odd")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_softmax_c4_relative(hx, dev, dtype):
+    """C4 softmax (8192 x 4096, N(0, 2)) checked in relative terms: most
+    outputs are ~1e-4 or smaller, where the absolute gate above says little.
+    Every output in the normal range of the type must agree with the oracle
+    to a few ulps of relative error, subnormal fp16 outputs to two subnormal
+    ulps, and the whole matrix to a relative Frobenius error of 1e-3 (a 1%
+    error in exp, or a row sum off by 1%, fails all three)."""
+    xh, _ = make(dtype, (8192, 4096), seed=11)
+    got = values(to_np(hx.softmax(to_torch(xh, dtype, dev))), dtype).astype(np.float64)
+    want = values(oracle.softmax(xh, bf16=(dtype == "bf16")), dtype).astype(np.float64)
+    tiny = 2.0 ** -14 if dtype == "f16" else 2.0 ** -126   # smallest normal of the type
+    ulp_rel = 2.0 ** -10 if dtype == "f16" else 2.0 ** -7  # one ulp, relative, at worst
+    normal = want >= tiny
+    assert normal.mean() > 0.3, normal.mean()  # ~38% of fp16 outputs are normal numbers
+    err = np.abs(got - want)
+    assert (err[normal] <= 2 * ulp_rel * want[normal]).all(), float((err[normal] / want[normal]).max())
+    if dtype == "f16":
+        assert (err[~normal] <= 2.0 ** -23).all(), float(err[~normal].max())
+    rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+    assert rel < 1e-3, rel
+    # each row's mass is 1 to within the outputs' own rounding
+    assert np.abs(got.sum(axis=1) - 1.0).max() < (2e-3 if dtype == "f16" else 2e-2)
+

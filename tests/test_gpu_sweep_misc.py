@@ -18,7 +18,8 @@ def _attn_case(i):
     D = int(r.choice([64, 128]))
     Nq = int(r.integers(1, 700))
     causal = bool(r.random() < 0.4)
-    Nk = Nq if causal else int(r.integers(1, 700))
+    # causal cases are square half of the time, else any key count
+    Nk = Nq if (causal and r.random() < 0.5) else int(r.integers(1, 700))
     return int(r.integers(1, 3)), int(r.integers(1, 5)), Nq, Nk, D, causal, ["f16", "bf16"][i % 2]
 
 

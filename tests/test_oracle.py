@@ -323,3 +323,105 @@ def test_oracle_attention_matches_torch_at_reference_shape():
     got = oracle.attention(q.half().numpy(), k.half().numpy(), v.half().numpy(), 0.5)
     rel = float(np.linalg.norm(got.astype(np.float64) - ref.numpy()) / np.linalg.norm(ref.numpy()))
     assert rel < 5e-3, rel
+
+
+# --------------------------------------------------------------------------- #
+# SwiGLU FFN composition
+# --------------------------------------------------------------------------- #
+
+def _ffn_float64(x, gamma, eps, wg, sg, wu, su, wd, sd):
+    """The block written out in float64 with no intermediate rounding:
+    y = (silu(h Wg sg) * (h Wu su)) Wd sd, h = x / sqrt(mean(x^2) + eps) * gamma.
+    Shares no code with the oracle (numpy matmuls, no fp16 steps)."""
+    x = x.astype(np.float64)
+    h = x / np.sqrt((x * x).mean(axis=1, keepdims=True) + eps) * gamma.astype(np.float64)
+    g = (h @ wg.astype(np.float64)) * sg.astype(np.float64)
+    u = (h @ wu.astype(np.float64)) * su.astype(np.float64)
+    a = g / (1.0 + np.exp(-g)) * u
+    return (a @ wd.astype(np.float64)) * sd.astype(np.float64)
+
+
+def _ffn_case(T=48, H=256, I=704, seed=40):
+    r = rng(seed)
+    wg = r.integers(-127, 128, (H, I), dtype=np.int8)
+    wu = r.integers(-127, 128, (H, I), dtype=np.int8)
+    wd = r.integers(-127, 128, (I, H), dtype=np.int8)
+    sg = (r.uniform(0.5, 1.5, I) / (127 * np.sqrt(H / 3))).astype(np.float16)
+    su = (r.uniform(0.5, 1.5, I) / (127 * np.sqrt(H / 3))).astype(np.float16)
+    sd = (r.uniform(0.5, 1.5, H) / (127 * np.sqrt(I / 3))).astype(np.float16)
+    x = r.normal(0, 1, (T, H)).astype(np.float16)
+    gamma = r.normal(1, 0.1, H).astype(np.float16)
+    return x, gamma, wg, sg, wu, su, wd, sd
+
+
+def _rel(got, want):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    return float(np.linalg.norm(got - want) / np.linalg.norm(want))
+
+
+def test_swiglu_ffn_vs_float64_composition():
+    """oracle.swiglu_ffn rounds to fp16 after each of its five stages; the
+    float64 composition does not, so they differ by a few fp16 roundings
+    (relative 2^-11 each) and nothing more."""
+    x, gamma, wg, sg, wu, su, wd, sd = _ffn_case()
+    got = oracle.swiglu_ffn(x, gamma, 1e-6, wg, sg, wu, su, wd, sd).astype(np.float64)
+    want = _ffn_float64(x, gamma, 1e-6, wg, sg, wu, su, wd, sd)
+    assert _rel(got, want) < 2e-3
+    assert_close(got, want, 2e-2, 3e-3, "swiglu oracle vs float64")
+
+
+def test_swiglu_ffn_negative_controls():
+    """A swap of the gate and up weights (with their scales), per-channel
+    scales applied to the wrong channels (reversed order), a dropped gamma,
+    and silu applied to the up branch each move the result far outside the
+    bound the oracle meets."""
+    x, gamma, wg, sg, wu, su, wd, sd = _ffn_case(seed=41)
+    want = _ffn_float64(x, gamma, 1e-6, wg, sg, wu, su, wd, sd)
+    bad = {
+        "gate/up swapped": oracle.swiglu_ffn(x, gamma, 1e-6, wu, su, wg, sg, wd, sd),
+        "down scale on the wrong channels": oracle.swiglu_ffn(x, gamma, 1e-6, wg, sg, wu, su, wd,
+                                                              np.ascontiguousarray(sd[::-1])),
+        "gate scale on the wrong channels": oracle.swiglu_ffn(x, gamma, 1e-6, wg,
+                                                              np.ascontiguousarray(sg[::-1]), wu, su, wd, sd),
+        "gamma dropped": oracle.swiglu_ffn(x, np.ones_like(gamma), 1e-6, wg, sg, wu, su, wd, sd),
+    }
+    for what, y in bad.items():
+        assert _rel(y, want) > 5e-2, what
+    # silu on the wrong branch, computed from the float64 stages directly
+    xf = x.astype(np.float64)
+    h = xf / np.sqrt((xf * xf).mean(axis=1, keepdims=True) + 1e-6) * gamma.astype(np.float64)
+    g = (h @ wg.astype(np.float64)) * sg.astype(np.float64)
+    u = (h @ wu.astype(np.float64)) * su.astype(np.float64)
+    wrong = ((u / (1.0 + np.exp(-u)) * g) @ wd.astype(np.float64)) * sd.astype(np.float64)
+    got = oracle.swiglu_ffn(x, gamma, 1e-6, wg, sg, wu, su, wd, sd)
+    assert _rel(got, wrong) > 5e-2
+
+
+def test_swiglu_ffn_rows_are_independent():
+    """Tokens are independent rows: the block on a row subset equals those
+    rows of the block on all rows, bit for bit (what the full-size GPU test
+    relies on when it checks sampled token rows)."""
+    x, gamma, wg, sg, wu, su, wd, sd = _ffn_case(T=40, seed=42)
+    full = oracle.swiglu_ffn(x, gamma, 1e-6, wg, sg, wu, su, wd, sd)
+    rows = np.array([0, 7, 39])
+    part = oracle.swiglu_ffn(np.ascontiguousarray(x[rows]), gamma, 1e-6, wg, sg, wu, su, wd, sd)
+    assert np.array_equal(full[rows].view(np.uint16), part.view(np.uint16))
+
+
+def test_softmax_relative_gate_catches_a_one_percent_exp_error():
+    """The relative gate the C4 softmax GPU test applies (two ulps relative on
+    every normal-range fp16 output) accepts a float64 softmax rounded once to
+    fp16 and rejects one with a 1% error planted in exp."""
+    x16 = rng(12).normal(0, 2, (64, 4096)).astype(np.float16)
+    x = x16.astype(np.float64)
+    e = np.exp(x - x.max(axis=1, keepdims=True))
+    good = (e / e.sum(axis=1, keepdims=True)).astype(np.float16).astype(np.float64)
+    # exp 1% high on every other column (a uniform error would cancel in
+    # the normalisation)
+    e_bad = e * np.where(np.arange(x.shape[1]) % 2 == 0, 1.01, 1.0)
+    bad = (e_bad / e_bad.sum(axis=1, keepdims=True)).astype(np.float16).astype(np.float64)
+    want = oracle.softmax(x16).astype(np.float64)
+    normal = want >= 2.0 ** -14
+    ok = lambda y: bool((np.abs(y - want)[normal] <= 2 * 2.0 ** -10 * want[normal]).all())  # noqa: E731
+    assert ok(good)
+    assert not ok(bad)
