@@ -138,16 +138,28 @@ def roofline(bound, achieved, peak, unit, traffic=None):
 # Headline: int8 GEMM 4096^3 + dequant
 # --------------------------------------------------------------------------- #
 
+#: the native tuner's protocol on the bench path: 3 repetitions of about
+#: 50 ms of device time each (the reference's 2 s per repetition would make
+#: the default bench run take many minutes)
+BENCH_TUNE = dict(reps=3, budget_us=50_000.0, min_iters=5, max_iters=200)
+
+
 def tune_summary(report):
-    """The autotuner's verdict, trimmed for the bench line."""
-    return {"champion": report.get("champion"), "round_verdict": report.get("round_verdict"),
-            "default": next((r["cfg"] for r in report.get("measurements", [])
-                             if r.get("index") == report.get("default_index")), None),
-            "q50_us": {r["cfg"]: (round(r["q50_us"], 2) if r.get("q50_us") is not None else None)
-                       for r in report.get("measurements", [])}}
+    """The autotuner's verdict (hx_tune's report), trimmed for the bench line."""
+    return {"champion": report.get("champion"), "control": report.get("control"),
+            "best": report.get("best"), "margin": round(report.get("margin", 0.0), 4),
+            "gate": round(report.get("gate", 0.0), 4), "round_valid": report.get("round_valid"),
+            "pinned": report.get("pinned"),
+            "canary": {k: report["canary"][k] for k in ("status", "q50_us", "reference_us", "shift")},
+            "q50_us": {e["cfg"]: (round(e["q50_us"], 2) if e.get("q50_us") is not None else e["reason"])
+                       for e in report.get("entries", [])}}
 
 
-def bench_gemm_i8(hx, steps: int, warmup: int, tune: bool = True):
+def tune(hx, op, m, n, k):
+    return tune_summary(hx.search.tune(op, m, n, k, **BENCH_TUNE))
+
+
+def bench_gemm_i8(hx, steps: int, warmup: int, tune_on: bool = True):
     import numpy as np
     import torch
     import oracle
@@ -161,8 +173,8 @@ def bench_gemm_i8(hx, steps: int, warmup: int, tune: bool = True):
     c = torch.empty((M, N), dtype=torch.float16, device=dev)
     step = hx.bind_gemm_i8(a, bt, c, b_layout="nk", row_scale=sa, col_scale=sb)
     tune_report = None
-    if tune:
-        tune_report = tune_summary(hx.search.tune(1, M, N, K, step))
+    if tune_on:
+        tune_report = tune(hx, 1, M, N, K)
 
     hx.manifest_clear()
     hx.manifest_enable(True)
@@ -196,11 +208,39 @@ def bench_gemm_i8(hx, steps: int, warmup: int, tune: bool = True):
                 tune=tune_report, queue_fed=fed, plan=plan)
 
 
-def cpu_baseline_gemm_i8(inputs, reps: int = 5):
+def _host_threads():
+    try:
+        gomp = ctypes.CDLL("libgomp.so.1")
+        return gomp, int(gomp.omp_get_max_threads())
+    except OSError:
+        return None, os.cpu_count() or 1
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_time(fn, reps: int) -> float:
+    import statistics
+    fn()  # warm-up (thread pool, page-in)
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    return statistics.median(times)
+
+
+def cpu_baseline_gemm_i8(inputs, march: str, reps: int = 5):
     """The oracle's (i,k,j) int32 loop + dequant over the same inputs: one
     warm-up, then the median of ``reps`` runs of the full 4096^3 product on
     all host threads (OpenMP), plus a 256-row sample on one thread."""
-    import statistics
     import numpy as np
     import oracle
     a, bt, sa, sb = inputs
@@ -211,46 +251,90 @@ def cpu_baseline_gemm_i8(inputs, reps: int = 5):
     M = a_h.shape[0]
 
     def run(rows):
-        t = time.perf_counter()
         acc = oracle.gemm_i8_i32(np.ascontiguousarray(a_h[:rows]), b_kn)
         oracle.dequant_i32_f16(acc, sa_h[:rows], sb_h)
-        return time.perf_counter() - t
 
-    try:
-        gomp = ctypes.CDLL("libgomp.so.1")
-        threads = gomp.omp_get_max_threads()
-    except OSError:
-        gomp, threads = None, os.cpu_count()
-    run(64)  # warm-up (thread pool, page-in)
-    times = [run(M) for _ in range(reps)]
-    med = statistics.median(times)
+    gomp, threads = _host_threads()
+    med = _median_time(lambda: run(M), reps)
     one_core = None
     if gomp is not None:
         gomp.omp_set_num_threads(1)
-        t1 = run(256)
+        t1 = _median_time(lambda: run(256), 1)
         gomp.omp_set_num_threads(threads)
         one_core = round(2.0 * 256 * N * K / t1 / 1e12, 5)
-    cpu = "unknown"
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
     return {"value": round(2.0 * M * N * K / med / 1e12, 5), "unit": "TOPS", "cores": int(threads),
             "kind": "port",
             "sample": f"full int8 4096^3 GEMM + dequant, oracle/hx_oracle.c hxo_gemm_i8_i32 "
                       f"(i,k,j) loop, median of {reps} runs ({med:.3f} s each) after a warm-up",
             "one_core_tops": one_core, "one_core_sample": "256 of 4096 rows on 1 thread",
-            "cpu_model": cpu}
+            "cpu_model": _cpu_model(), "build": f"gcc -O3 -march=native ({march}) -fopenmp"}
+
+
+def cpu_baselines_secondary(march: str) -> dict:
+    """The oracle's restatement of the reference's linalg path for every
+    secondary workload, timed on this host on seeded inputs of the same shape
+    (medians after a warm-up; samples bounded so the whole leg stays within
+    about a minute).  Keys match the secondary workloads' names."""
+    import numpy as np
+    import oracle
+    gomp, threads = _host_threads()
+    r = np.random.default_rng(2024)
+    out = {}
+    base = {"kind": "port", "cpu_model": _cpu_model(), "build": f"gcc -O3 -march=native ({march}) -fopenmp"}
+    # C3: W8A16 decode GEMV, the oracle's dequant matmul ((i,k,j), rows over threads)
+    N, K = 11008, 4096
+    w = r.integers(-127, 128, (K, N), dtype=np.int8)
+    sc = r.uniform(0.001, 0.02, N).astype(np.float32)
+    for M in (1, 4, 16):
+        x = r.normal(0, 1, (M, K)).astype(np.float16)
+        t = _median_time(lambda: oracle.matmul(x, w, scale_n=sc), 3)
+        nbytes = N * K + 2 * N + 2 * M * K + 2 * M * N
+        out[f"gemv_m{M}"] = dict(base, value=round(nbytes / t / 1e9, 3), unit="GB/s",
+                                 cores=min(M, threads), us_per_call=round(t * 1e6, 1),
+                                 sample=f"full W8A16 GEMV M={M} N={N} K={K}, hxo_matmul (i,k,j) loop, "
+                                        f"median of 3 after a warm-up (rows over threads)")
+    del w
+    # C4: softmax / RMSNorm on the full 8192 x 4096 fp16 matrix
+    R, C = 8192, 4096
+    xr = (r.normal(0, 2, (R, C))).astype(np.float16)
+    gam = r.normal(1, 0.1, C).astype(np.float16)
+    for name, fn in (("softmax", lambda: oracle.softmax(xr)), ("rmsnorm", lambda: oracle.rmsnorm(xr, gam, 1e-6))):
+        t = _median_time(fn, 3)
+        nbytes = 2 * R * C * 2 + (2 * C if name == "rmsnorm" else 0)
+        out[name] = dict(base, value=round(nbytes / t / 1e9, 3), unit="GB/s", cores=threads,
+                         us_per_call=round(t * 1e6, 1),
+                         sample=f"full {name} fp16 [{R} x {C}], oracle row loop, median of 3 after a warm-up")
+    del xr
+    # C1: fp16 256^3
+    a = r.uniform(-1, 1, (256, 256)).astype(np.float16)
+    b = r.uniform(-1, 1, (256, 256)).astype(np.float16)
+    t = _median_time(lambda: oracle.matmul(a, b), 5)
+    out["gemm_f16_256"] = dict(base, value=round(t * 1e6, 2), unit="us", cores=threads,
+                               tflops=round(2 * 256 ** 3 / t / 1e12, 5),
+                               sample="full fp16 256^3 matmul, hxo_matmul, median of 5 after a warm-up")
+    # C5: the FFN block on a 64-token sample (tokens are independent rows)
+    T, H, I = 64, 4096, 11008
+    wg = r.integers(-127, 128, (H, I), dtype=np.int8)
+    wu = r.integers(-127, 128, (H, I), dtype=np.int8)
+    wd = r.integers(-127, 128, (I, H), dtype=np.int8)
+    sg = (r.uniform(0.5, 1.5, I) / (127 * np.sqrt(H / 3))).astype(np.float16)
+    su = (r.uniform(0.5, 1.5, I) / (127 * np.sqrt(H / 3))).astype(np.float16)
+    sd = (r.uniform(0.5, 1.5, H) / (127 * np.sqrt(I / 3))).astype(np.float16)
+    xf = r.normal(0, 1, (T, H)).astype(np.float16)
+    g1 = r.normal(1, 0.1, H).astype(np.float16)
+    t = _median_time(lambda: oracle.swiglu_ffn(xf, g1, 1e-6, wg, sg, wu, su, wd, sd), 1)
+    out["ffn"] = dict(base, value=round(3 * 2.0 * T * H * I / t / 1e12, 5), unit="TFLOP/s", cores=min(T, threads),
+                      us_per_call=round(t * 1e6, 1),
+                      sample=f"{T} of 2048 tokens through the full block (RMSNorm, gate/up/down W8A16 "
+                             "matmuls, SiLU*mul), oracle composition, one run after a warm-up")
+    return out
 
 
 # --------------------------------------------------------------------------- #
 # Secondary workloads
 # --------------------------------------------------------------------------- #
 
-def bench_gemv(hx, iters: int = 200, tune: bool = True):
+def bench_gemv(hx, iters: int = 200, tune_on: bool = True, tune_fn=tune):
     import torch
     N, K = 11008, 4096
     dev = torch.device("cuda:0")
@@ -270,9 +354,7 @@ def bench_gemv(hx, iters: int = 200, tune: bool = True):
             calls = [hx.bind_matmul_resident(x, w, y) for w in weights]
             for c in calls:
                 c()
-            rot = iter(range(1 << 30))
-            tuned = (tune_summary(hx.search.tune(6, M, N, K, lambda: calls[next(rot) % copies]()))
-                     if tune else None)
+            tuned = tune_fn(hx, 6, M, N, K) if tune_on else None
             ev_ms, fed = event_timed(calls, iters)
             nbytes = N * K + 2 * N + 2 * M * K + 2 * M * N
             gbs = nbytes / (ev_ms * 1e-3) / 1e9
@@ -356,7 +438,7 @@ def bench_gemm_f16_small(hx, iters: int = 200):
             "roofline": roofline("mfma", tf, PEAK_F16_TFLOPS, "TFLOP/s")}
 
 
-def bench_ffn(hx, iters: int = 20, tune: bool = True):
+def bench_ffn(hx, iters: int = 20, tune_on: bool = True, tune_fn=tune):
     import torch
     T, H, I = 2048, 4096, 11008
     dev = torch.device("cuda:0")
@@ -375,10 +457,9 @@ def bench_ffn(hx, iters: int = 20, tune: bool = True):
         call = lambda: hx.swiglu_ffn(x, gamma, 1e-6, Wg, Wu, Wd, out=y)  # noqa: E731
         call()
         tuned = None
-        if tune:
+        if tune_on:
             # gate/up stage (fused SwiGLU epilogue), then the down projection
-            tuned = {"swiglu": tune_summary(hx.search.tune(5, T, I, H, call)),
-                     "down": tune_summary(hx.search.tune(4, T, H, I, call))}
+            tuned = {"swiglu": tune_fn(hx, 5, T, I, H), "down": tune_fn(hx, 4, T, H, I)}
         ev_ms, _ = event_timed([call], iters)
     finally:
         Wg.release(); Wu.release(); Wd.release()
@@ -553,8 +634,8 @@ def main() -> int:
         return 0
 
     log("[bench] int8 GEMM 4096^3 + dequant")
-    tune = not args.no_tune
-    h = bench_gemm_i8(hx, args.steps, args.warmup, tune=tune)
+    tune_on = not args.no_tune
+    h = bench_gemm_i8(hx, args.steps, args.warmup, tune_on=tune_on)
     log(f"[bench] int8 GEMM: {h['tops']:.1f} TOPS wall, {h['tops_kernel']:.1f} TOPS kernel, "
         f"{h['kernel_ms']*1e3:.1f} us/launch, parity={h['parity_sampled_rows_bitexact']}")
     secondary = []
@@ -562,22 +643,34 @@ def main() -> int:
         log("[bench] int8 GEMM 4096^3, int32 out")
         secondary.append(bench_gemm_i8_i32(hx, h["inputs"]))
         log("[bench] W8A16 GEMV")
-        secondary += bench_gemv(hx, tune=tune)
+        secondary += bench_gemv(hx, tune_on=tune_on)
         log("[bench] row ops")
         secondary += bench_rows(hx)
         log("[bench] fp16 GEMM 256^3")
         secondary.append(bench_gemm_f16_small(hx))
         log("[bench] SwiGLU FFN")
-        secondary.append(bench_ffn(hx, tune=tune))
+        secondary.append(bench_ffn(hx, tune_on=tune_on))
         log("[bench] attention")
         secondary += bench_attention(hx)
         for s in secondary:
             log(f"[bench]   {s['workload']}: {s['value']} {s['unit']}")
     cpu = None
     if not args.no_cpu:
-        log("[bench] CPU baseline (oracle port)")
-        cpu = cpu_baseline_gemm_i8(h["inputs"])
+        import oracle
+        march = oracle.use_native_build()
+        log(f"[bench] CPU baseline (oracle port, -march=native = {march})")
+        cpu = cpu_baseline_gemm_i8(h["inputs"], march)
         log(f"[bench] CPU: {cpu['value']} TOPS on {cpu['cores']} threads")
+        if secondary:
+            sec_cpu = cpu_baselines_secondary(march)
+            keys = {"W8A16 GEMV M=1 ": "gemv_m1", "W8A16 GEMV M=4 ": "gemv_m4", "W8A16 GEMV M=16 ": "gemv_m16",
+                    "softmax fp16": "softmax", "rmsnorm fp16": "rmsnorm", "fp16 GEMM 256^3": "gemm_f16_256",
+                    "SwiGLU FFN": "ffn"}
+            for sec in secondary:
+                for prefix, key in keys.items():
+                    if sec["workload"].startswith(prefix):
+                        sec["cpu_baseline"] = sec_cpu[key]
+            log("[bench] CPU secondary baselines done")
 
     line = {
         "metric": METRIC,

@@ -52,6 +52,39 @@ class KernelConfig(ctypes.Structure):
                 ("lds_bytes", ctypes.c_int32), ("name", ctypes.c_char * 40)]
 
 
+class TuneOptions(ctypes.Structure):
+    _fields_ = [("reps", ctypes.c_int32), ("min_iters", ctypes.c_int32), ("max_iters", ctypes.c_int32),
+                ("budget_us", ctypes.c_double), ("canary_reference_us", ctypes.c_double),
+                ("pin", ctypes.c_int32), ("seed", ctypes.c_uint64)]
+
+
+class TuneEntry(ctypes.Structure):
+    _fields_ = [("index", ctypes.c_int32), ("status", ctypes.c_int32), ("q50_us", ctypes.c_double),
+                ("q20_us", ctypes.c_double), ("q80_us", ctypes.c_double), ("reason", ctypes.c_char * 24)]
+
+
+TUNE_MAX_ENTRIES = 64
+
+
+class TuneReport(ctypes.Structure):
+    _fields_ = [("op", ctypes.c_int32), ("m", ctypes.c_int64), ("n", ctypes.c_int64), ("k", ctypes.c_int64),
+                ("iters", ctypes.c_int32), ("control_index", ctypes.c_int32), ("best_index", ctypes.c_int32),
+                ("champion_index", ctypes.c_int32), ("control_q50_us", ctypes.c_double),
+                ("best_q50_us", ctypes.c_double), ("margin", ctypes.c_double), ("gate", ctypes.c_double),
+                ("canary_index", ctypes.c_int32), ("canary_m", ctypes.c_int64), ("canary_n", ctypes.c_int64),
+                ("canary_k", ctypes.c_int64), ("canary_status", ctypes.c_int32),
+                ("canary_q50_us", ctypes.c_double), ("canary_reference_us", ctypes.c_double),
+                ("canary_shift", ctypes.c_double), ("canary_gate", ctypes.c_double),
+                ("round_valid", ctypes.c_int32), ("pinned", ctypes.c_int32), ("n_entries", ctypes.c_int32),
+                ("entries", TuneEntry * TUNE_MAX_ENTRIES)]
+
+
+TUNE_TIMED, TUNE_REFUSED, TUNE_LAUNCH_FAILED, TUNE_WRONG = 0, 1, 2, 3
+TUNE_STATUS = {0: "timed", 1: "refused", 2: "launch-failed", 3: "wrong"}
+CANARY_BASELINE, CANARY_STEADY, CANARY_DRIFT, CANARY_FAILED = 0, 1, 2, 3
+CANARY_STATUS = {0: "baseline", 1: "steady", 2: "drift", 3: "failed"}
+
+
 class HXError(RuntimeError):
     def __init__(self, code: int, message: str):
         super().__init__(f"{ERRORS.get(code, code)}: {message}")
@@ -86,6 +119,9 @@ SIGNATURES = {
     "hx_config_pins_save": ([ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)], _i),
     "hx_config_pins_load": ([ctypes.c_char_p], _i),
     "hx_attention": ([ctypes.POINTER(MemRef4D)] * 4 + [_f, _i, _i, _vp], _i),
+    "hx_tune": ([_i, _i64, _i64, _i64, ctypes.POINTER(TuneOptions), ctypes.POINTER(TuneReport), _vp], _i),
+    "hx_tune_decide": ([ctypes.POINTER(TuneEntry), _i, _i, ctypes.POINTER(TuneEntry), ctypes.c_double,
+                        ctypes.POINTER(TuneReport)], _i),
     "hx_manifest_enable": ([_i], _i),
     "hx_manifest_clear": ([], _i),
     "hx_manifest_json": ([ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)], _i),

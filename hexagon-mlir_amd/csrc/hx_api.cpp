@@ -14,6 +14,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cmath>
 #include <cstring>
 #include <atomic>
 #include <map>
@@ -24,6 +25,7 @@
 #include <vector>
 
 #include "../../include/hx.h"
+#include "hx_api_internal.hpp"
 #include "hx_device.hpp"
 #include "hx_internal.hpp"
 
@@ -39,6 +41,16 @@ using namespace hx;
 static thread_local std::string g_err;
 
 static int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hx::api_fail(int code, const char* fmt, ...) {
   char buf[512];
   va_list ap;
   va_start(ap, fmt);
@@ -280,7 +292,7 @@ extern "C" int hx_manifest_json(char* buf, size_t cap, size_t* needed) {
 static std::map<std::tuple<int, int, int64_t, int64_t, int64_t>, int> g_pins;
 
 // (gemm mode, epilogue) of each GEMM family
-static bool op_gemm(int op, int* mode, int* epi) {
+bool hx::op_gemm(int op, int* mode, int* epi) {
   switch (op) {
     case HX_OP_GEMM_I8: *mode = GM_I8; *epi = GE_STORE; return true;
     case HX_OP_MATMUL_F16: *mode = GM_F16; *epi = GE_STORE; return true;
@@ -292,12 +304,12 @@ static bool op_gemm(int op, int* mode, int* epi) {
 }
 
 // The decode GEMV families (int8, f16, bf16 weights) share one config table.
-static bool gemv_op(int op) {
+bool hx::gemv_op(int op) {
   return op == HX_OP_GEMV_W8 || op == HX_OP_GEMV_F16 || op == HX_OP_GEMV_BF16;
 }
 
 // Table indices (into the mode's table) of the configs of one family.
-static std::vector<int> family_indices(int op) {
+std::vector<int> hx::family_indices(int op) {
   std::vector<int> out;
   int mode, epi;
   if (gemv_op(op)) {
@@ -334,10 +346,8 @@ static int resolve_gemm(int op, int64_t M, int64_t N, int64_t K, bool* was_pinne
   }
   return gemm_default_config(mode, epi, M, N, K);
 }
-static int resolve_gemv(int op, int64_t M, int64_t N, int64_t K, bool* was_pinned = nullptr) {
-  const int pin = pinned(op, M, N, K);
-  if (was_pinned) *was_pinned = pin >= 0 && pin < gemv_packed_config_count();
-  if (pin >= 0 && pin < gemv_packed_config_count()) return pin;
+// Untuned GEMV config (table index = family index) for a shape.
+static int gemv_untuned(int op, int64_t M, int64_t N, int64_t K) {
   if (M > 16) return gemv_rows_default(M, N);
   if (op != HX_OP_GEMV_W8) {
     // f16 / bf16 weights, untuned choice from the MI355X sweep over
@@ -357,7 +367,69 @@ static int resolve_gemv(int op, int64_t M, int64_t N, int64_t K, bool* was_pinne
   return M <= 2 ? 11 : M <= 4 ? 5 : 10;
 }
 
-static int run_gemm(int op, GemmArgs& a, hipStream_t s, const PlanCtx& ctx) {
+static int resolve_gemv(int op, int64_t M, int64_t N, int64_t K, bool* was_pinned = nullptr) {
+  const int pin = pinned(op, M, N, K);
+  if (was_pinned) *was_pinned = pin >= 0 && pin < gemv_packed_config_count();
+  if (pin >= 0 && pin < gemv_packed_config_count()) return pin;
+  return gemv_untuned(op, M, N, K);
+}
+
+int hx::untuned_family_index(int op, int64_t m, int64_t n, int64_t k) {
+  if (gemv_op(op)) return gemv_untuned(op, m, n, k);
+  int mode, epi;
+  if (!op_gemm(op, &mode, &epi)) return -1;
+  const int t = gemm_default_config(mode, epi, m, n, k);
+  const std::vector<int> idx = family_indices(op);
+  for (size_t i = 0; i < idx.size(); ++i)
+    if (idx[i] == t) return (int)i;
+  return -1;
+}
+
+// Canary references of the tuner, per (device, family).
+static std::map<std::pair<int, int>, double> g_canary;
+
+bool hx::canary_reference_get(int dev, int op, double* q50_us) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_canary.find({dev, op});
+  if (it == g_canary.end()) return false;
+  *q50_us = it->second;
+  return true;
+}
+
+void hx::canary_reference_set(int dev, int op, double q50_us) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_canary[{dev, op}] = q50_us;
+}
+
+std::vector<std::pair<int, double>> hx::canary_references(int dev) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  std::vector<std::pair<int, double>> out;
+  for (const auto& kv : g_canary)
+    if (kv.first.first == dev) out.emplace_back(kv.first.second, kv.second);
+  return out;
+}
+
+// Where a K-split GEMM's binary32 partials go: the per-stream partials
+// region (allocated on demand), or a caller-supplied buffer of `cap` bytes
+// when the call must not allocate.
+struct PartialsTarget {
+  float* buf = nullptr;
+  size_t cap = 0;
+  bool fixed = false;
+};
+
+// Partial bytes a run_gemm call of these args would need (0: no K split or
+// not the tiled path).
+static size_t gemm_partials_needed(int op, const GemmArgs& a) {
+  int mode, epi;
+  op_gemm(op, &mode, &epi);
+  if (a.M == 0 || a.N == 0 || gemm_fast_refusal(mode, a)) return 0;
+  const int cfg = resolve_gemm(op, a.M, a.N, a.K);
+  return cfg >= 0 ? gemm_part_bytes(mode, cfg, a) : 0;
+}
+
+static int run_gemm(int op, GemmArgs& a, hipStream_t s, const PlanCtx& ctx,
+                    const PartialsTarget& pt = PartialsTarget{}) {
   int mode, epi;
   op_gemm(op, &mode, &epi);
   if (a.M == 0 || a.N == 0) return HX_OK;
@@ -369,8 +441,15 @@ static int run_gemm(int op, GemmArgs& a, hipStream_t s, const PlanCtx& ctx) {
       note_plan(ctx, a.M, a.N, a.K, a.out_dtype, "mfma-tiled", gemm_config(mode, cfg)->name,
                 pin ? "pinned" : "default", "selected-aligned");
       if (const size_t pb = gemm_part_bytes(mode, cfg, a)) {
-        int rc = part_get(s, pb, &a.part);
-        if (rc) return rc;
+        if (pt.fixed) {
+          if (pb > pt.cap)
+            return fail(HX_ERR_UNSUPPORTED, "%s: config %s needs %zu bytes of K-split partials, %zu reserved",
+                        ctx.entry, gemm_config(mode, cfg)->name, pb, pt.cap);
+          a.part = pt.buf;
+        } else {
+          int rc = part_get(s, pb, &a.part);
+          if (rc) return rc;
+        }
       }
       return map_internal(launch_gemm(mode, cfg, a, s), "gemm");
     }
@@ -787,15 +866,80 @@ struct hx_weight {
   int8_t* packed;  // int8 only: MFMA-fragment-ordered copy for the decode GEMV
   float* scale;    // [N] or null
   uint64_t hash;
-  int refcount;
+  int refcount;    // registrations not yet released
+  int inuse;       // entry-point calls currently holding the weight
 };
 static std::set<hx_weight*> g_weights;
+
+// Free a weight no registration and no call holds any more.  The
+// synchronization makes sure no enqueued kernel still reads the image.
+static void weight_free(hx_weight* x) {
+  int cur = 0;
+  (void)hipGetDevice(&cur);
+  (void)hipSetDevice(x->device);
+  (void)hipDeviceSynchronize();
+  (void)hipFree(x->image);
+  if (x->packed) (void)hipFree(x->packed);
+  if (x->scale) (void)hipFree(x->scale);
+  (void)hipSetDevice(cur);
+  delete x;
+}
+
+// Weights whose last holder was a call that may not free device memory
+// (the no-allocation entry points); the next registration or release frees
+// them.
+static std::vector<hx_weight*> g_deferred;
+
+static void free_deferred() {
+  std::vector<hx_weight*> dead;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    dead.swap(g_deferred);
+  }
+  for (hx_weight* x : dead) weight_free(x);
+}
+
+// A weight held for the duration of one entry-point call: a release on
+// another thread in the meantime only drops the registration, and the
+// memory goes when the last holder lets go (or, for a call that may not
+// free, at the next registration or release).
+class WeightUse {
+ public:
+  explicit WeightUse(hx_weight_t w, bool may_free = true) : may_free_(may_free) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (w && g_weights.count(w) && w->refcount > 0) {
+      ++w->inuse;
+      w_ = w;
+    }
+  }
+  ~WeightUse() {
+    if (!w_) return;
+    bool last;
+    {
+      std::lock_guard<std::mutex> lk(g_mu);
+      last = --w_->inuse == 0 && w_->refcount == 0;
+      if (last) {
+        g_weights.erase(w_);
+        if (!may_free_) g_deferred.push_back(w_);
+      }
+    }
+    if (last && may_free_) weight_free(w_);
+  }
+  WeightUse(const WeightUse&) = delete;
+  WeightUse& operator=(const WeightUse&) = delete;
+  hx_weight* get() const { return w_; }
+
+ private:
+  hx_weight* w_ = nullptr;
+  bool may_free_;
+};
 
 extern "C" int hx_weight_register(const hx_memref2d* w, int w_dtype, int w_layout,
                                   const hx_memref1d* scale, int scale_dtype, hx_stream_t stream,
                                   hx_weight_t* out) {
   hipStream_t s = (hipStream_t)stream;
   if (!out) return fail(HX_ERR_ARG, "hx_weight_register: null out");
+  free_deferred();
   *out = nullptr;
   if (w_dtype != HX_I8 && w_dtype != HX_F16 && w_dtype != HX_BF16)
     return fail(HX_ERR_DTYPE, "hx_weight_register: dtype %s", dt_name(w_dtype));
@@ -859,8 +1003,25 @@ extern "C" int hx_weight_register(const hx_memref2d* w, int w_dtype, int w_layou
 
   std::lock_guard<std::mutex> lk(g_mu);
   for (hx_weight* x : g_weights) {
-    if (x->device == dev && x->hash == key && x->K == K && x->N == N && x->dtype == w_dtype &&
-        (x->scale != nullptr) == (scale != nullptr)) {
+    if (x->refcount > 0 && x->device == dev && x->hash == key && x->K == K && x->N == N &&
+        x->dtype == w_dtype && (x->scale != nullptr) == (scale != nullptr)) {
+      // A 64-bit key can collide: share the image only when the bytes
+      // (image and scales) are equal, compared on the device.
+      unsigned* cnt = nullptr;
+      unsigned diff = 1;
+      if (hipMalloc((void**)&cnt, sizeof(unsigned)) == hipSuccess) {
+        bool ok = hipMemsetAsync(cnt, 0, sizeof(unsigned), s) == hipSuccess;
+        ok = ok && launch_diff_bytes(image, x->image, N * K * (int64_t)es, cnt, s) == HXI_OK;
+        if (ok && scale) ok = launch_diff_bytes(sc, x->scale, N * 4, cnt, s) == HXI_OK;
+        ok = ok && hipMemcpyAsync(&diff, cnt, sizeof(unsigned), hipMemcpyDeviceToHost, s) == hipSuccess &&
+             hipStreamSynchronize(s) == hipSuccess;
+        (void)hipFree(cnt);
+        if (!ok) {
+          cleanup();
+          return fail(HX_ERR_HIP, "hx_weight_register: content comparison failed");
+        }
+      }
+      if (diff != 0) continue;  // same key, different content: a registration of its own
       ++x->refcount;
       cleanup();
       *out = x;
@@ -881,42 +1042,28 @@ extern "C" int hx_weight_register(const hx_memref2d* w, int w_dtype, int w_layou
       return rc ? rc : fail(HX_ERR_HIP, "gemv pack: %s", hipGetErrorString(se));
     }
   }
-  hx_weight* x = new hx_weight{dev, K, N, w_dtype, image, packed, sc, key, 1};
+  hx_weight* x = new hx_weight{dev, K, N, w_dtype, image, packed, sc, key, 1, 0};
   g_weights.insert(x);
   *out = x;
   return HX_OK;
 }
 
-static hx_weight* lookup(hx_weight_t w) {
-  std::lock_guard<std::mutex> lk(g_mu);
-  return g_weights.count(w) ? w : nullptr;
-}
-
 extern "C" int hx_weight_release(hx_weight_t w) {
-  hx_weight* x = nullptr;
+  free_deferred();
   {
     std::lock_guard<std::mutex> lk(g_mu);
-    if (!g_weights.count(w)) return fail(HX_ERR_HANDLE, "hx_weight_release: unknown handle");
-    if (--w->refcount > 0) return HX_OK;
+    if (!g_weights.count(w) || w->refcount <= 0) return fail(HX_ERR_HANDLE, "hx_weight_release: unknown handle");
+    if (--w->refcount > 0 || w->inuse > 0) return HX_OK;  // a running call frees it when it returns
     g_weights.erase(w);
-    x = w;
   }
-  int cur = 0;
-  (void)hipGetDevice(&cur);
-  (void)hipSetDevice(x->device);
-  (void)hipDeviceSynchronize();  // no kernel may still read the image
-  (void)hipFree(x->image);
-  if (x->packed) (void)hipFree(x->packed);
-  if (x->scale) (void)hipFree(x->scale);
-  (void)hipSetDevice(cur);
-  delete x;
+  weight_free(w);
   return HX_OK;
 }
 
 extern "C" int hx_weight_info(hx_weight_t w, int64_t* k, int64_t* n, int* dtype, uint64_t* content_hash,
                               int* refcount) {
   std::lock_guard<std::mutex> lk(g_mu);
-  if (!g_weights.count(w)) return fail(HX_ERR_HANDLE, "hx_weight_info: unknown handle");
+  if (!g_weights.count(w) || w->refcount <= 0) return fail(HX_ERR_HANDLE, "hx_weight_info: unknown handle");
   if (k) *k = w->K;
   if (n) *n = w->N;
   if (dtype) *dtype = w->dtype;
@@ -926,7 +1073,8 @@ extern "C" int hx_weight_info(hx_weight_t w, int64_t* k, int64_t* n, int* dtype,
 }
 
 static int matmul_resident_impl(const View2& vx, hx_weight* w, const View2* vr, int r_dt,
-                                const View2& vy, int y_dt, hipStream_t s, const char* entry) {
+                                const View2& vy, int y_dt, hipStream_t s, const char* entry,
+                                const PartialsTarget& pt = PartialsTarget{}) {
   const int x_dt = w->dtype == HX_BF16 ? HX_BF16 : HX_F16;
   const int64_t M = vx.rows;
   if (M == 0) return HX_OK;
@@ -960,13 +1108,14 @@ static int matmul_resident_impl(const View2& vx, hx_weight* w, const View2* vr, 
   g.col_scale = w->scale;
   if (vr) { g.res = vr->p; g.ldr = vr->ld; g.res_dtype = r_dt; }
   const int op = w->dtype == HX_I8 ? HX_OP_MATMUL_W8 : w->dtype == HX_F16 ? HX_OP_MATMUL_F16 : HX_OP_MATMUL_BF16;
-  return run_gemm(op, g, s, PlanCtx{entry, "resident-image", x_dt, w->dtype});
+  return run_gemm(op, g, s, PlanCtx{entry, "resident-image", x_dt, w->dtype}, pt);
 }
 
 extern "C" int hx_matmul_resident(const hx_memref2d* x, int x_dtype, hx_weight_t wt,
                                   const hx_memref2d* residual, int residual_dtype, hx_memref2d* y,
                                   int y_dtype, hx_stream_t stream) {
-  hx_weight* w = lookup(wt);
+  WeightUse use(wt);
+  hx_weight* w = use.get();
   if (!w) return fail(HX_ERR_HANDLE, "hx_matmul_resident: unknown weight handle");
   const int want_x = w->dtype == HX_BF16 ? HX_BF16 : HX_F16;
   if (x_dtype != want_x)
@@ -991,26 +1140,32 @@ extern "C" int hx_matmul_resident(const hx_memref2d* x, int x_dtype, hx_weight_t
                               (hipStream_t)stream, "hx_matmul_resident");
 }
 
-extern "C" int hx_swiglu_ffn(const hx_memref2d* x, const hx_memref1d* gamma, float eps, hx_weight_t w_gate,
-                             hx_weight_t w_up, hx_weight_t w_down, hx_memref2d* y, hx_stream_t stream) {
+// The FFN block.  `fixed` (may be null) is caller-supplied device memory of
+// fixed->cap bytes that holds every intermediate and K-split partial; then
+// the call allocates nothing and refuses shapes that do not fit.  Without
+// it the intermediates live in the stream's workspace.
+int hx::swiglu_ffn_impl(const hx_memref2d* x, const hx_memref1d* gamma, float eps, hx_weight_t w_gate,
+                        hx_weight_t w_up, hx_weight_t w_down, hx_memref2d* y, hx_stream_t stream,
+                        const FixedScratch* fixed, const char* entry) {
   hipStream_t s = (hipStream_t)stream;
-  hx_weight *wg = lookup(w_gate), *wu = lookup(w_up), *wd = lookup(w_down);
-  if (!wg || !wu || !wd) return fail(HX_ERR_HANDLE, "hx_swiglu_ffn: unknown weight handle");
+  WeightUse ug(w_gate, !fixed), uu(w_up, !fixed), ud(w_down, !fixed);
+  hx_weight *wg = ug.get(), *wu = uu.get(), *wd = ud.get();
+  if (!wg || !wu || !wd) return fail(HX_ERR_HANDLE, "%s: unknown weight handle", entry);
   if (wg->dtype != HX_I8 || wu->dtype != HX_I8 || wd->dtype != HX_I8)
-    return fail(HX_ERR_DTYPE, "hx_swiglu_ffn: int8 weights expected");
+    return fail(HX_ERR_DTYPE, "%s: int8 weights expected", entry);
   int rc, dev;
   if ((rc = current_device(&dev))) return rc;
   if (wg->device != dev || wu->device != dev || wd->device != dev)
-    return fail(HX_ERR_HANDLE, "hx_swiglu_ffn: weights live on another device");
+    return fail(HX_ERR_HANDLE, "%s: weights live on another device", entry);
   View2 vx, vy;
   View1 vg{};
   if ((rc = view2(x, HX_F16, "x", &vx)) || (rc = view2(y, HX_F16, "y", &vy))) return rc;
   const int64_t T = vx.rows, H = vx.cols, I = wg->N;
   if (wg->K != H || wu->K != H || wu->N != I || wd->K != I || wd->N != H)
-    return fail(HX_ERR_SHAPE, "hx_swiglu_ffn: weights [%lld,%lld] [%lld,%lld] [%lld,%lld] vs hidden %lld",
+    return fail(HX_ERR_SHAPE, "%s: weights [%lld,%lld] [%lld,%lld] [%lld,%lld] vs hidden %lld", entry,
                 (long long)wg->K, (long long)wg->N, (long long)wu->K, (long long)wu->N, (long long)wd->K,
                 (long long)wd->N, (long long)H);
-  if (vy.rows != T || vy.cols != H) return fail(HX_ERR_SHAPE, "hx_swiglu_ffn: y shape");
+  if (vy.rows != T || vy.cols != H) return fail(HX_ERR_SHAPE, "%s: y shape", entry);
   if (gamma && (rc = view1(gamma, HX_F16, "gamma", H, &vg))) return rc;
   if (T == 0) return HX_OK;
 
@@ -1023,7 +1178,32 @@ extern "C" int hx_swiglu_ffn(const hx_memref2d* x, const hx_memref1d* gamma, flo
   const size_t off_g = skinny ? cv.take((size_t)T * I * 2) : 0;
   const size_t off_u = skinny ? cv.take((size_t)T * I * 2) : 0;
   char* ws;
-  if ((rc = ws_get(s, cv.used, &ws))) return rc;
+  PartialsTarget pt;
+  if (fixed) {
+    // the down projection's K-split partials (if its config splits) go in
+    // the same scratch, after the intermediates
+    ws = fixed->base;
+    size_t part = 0;
+    if (!skinny) {
+      GemmArgs d{};
+      d.a = ws + off_a; d.lda = I;
+      d.b = wd->image; d.ldb = I;
+      d.c = vy.p; d.ldc = vy.ld;
+      d.M = T; d.N = H; d.K = I;
+      d.out_dtype = HX_F16;
+      d.col_scale = wd->scale;
+      part = gemm_partials_needed(HX_OP_MATMUL_W8, d);
+    }
+    const size_t off_p = part ? cv.take(part) : 0;
+    if (cv.used > fixed->cap)
+      return fail(HX_ERR_UNSUPPORTED, "%s: %lld tokens need %zu bytes of scratch; the fixed scratch holds %zu",
+                  entry, (long long)T, cv.used, fixed->cap);
+    pt.fixed = true;
+    pt.buf = part ? reinterpret_cast<float*>(ws + off_p) : nullptr;
+    pt.cap = part;
+  } else if ((rc = ws_get(s, cv.used, &ws))) {
+    return rc;
+  }
   char* h = ws + off_h;
   char* act = ws + off_a;
   rc = map_internal(launch_rmsnorm(HX_F16, vx.p, vx.ld, gamma ? vg.p : nullptr, eps, h, H, T, H, s), "rmsnorm");
@@ -1031,8 +1211,8 @@ extern "C" int hx_swiglu_ffn(const hx_memref2d* x, const hx_memref1d* gamma, flo
   View2 vh{h, T, H, H}, va{act, T, I, I};
   if (skinny) {
     View2 vgo{ws + off_g, T, I, I}, vuo{ws + off_u, T, I, I};
-    if ((rc = matmul_resident_impl(vh, wg, nullptr, 0, vgo, HX_F16, s, "hx_swiglu_ffn"))) return rc;
-    if ((rc = matmul_resident_impl(vh, wu, nullptr, 0, vuo, HX_F16, s, "hx_swiglu_ffn"))) return rc;
+    if ((rc = matmul_resident_impl(vh, wg, nullptr, 0, vgo, HX_F16, s, entry, pt))) return rc;
+    if ((rc = matmul_resident_impl(vh, wu, nullptr, 0, vuo, HX_F16, s, entry, pt))) return rc;
     rc = map_internal(launch_silu_mul_f16(vgo.p, I, vuo.p, I, act, I, T, I, s), "silu_mul");
     if (rc) return rc;
   } else {
@@ -1043,10 +1223,14 @@ extern "C" int hx_swiglu_ffn(const hx_memref2d* x, const hx_memref1d* gamma, flo
     g.M = T; g.N = I; g.K = H;
     g.out_dtype = HX_F16;
     g.col_scale = wg->scale; g.col_scale2 = wu->scale;
-    if ((rc = run_gemm(HX_OP_SWIGLU_W8, g, s, PlanCtx{"hx_swiglu_ffn", "resident-image", HX_F16, HX_I8})))
-      return rc;
+    if ((rc = run_gemm(HX_OP_SWIGLU_W8, g, s, PlanCtx{entry, "resident-image", HX_F16, HX_I8}, pt))) return rc;
   }
-  return matmul_resident_impl(va, wd, nullptr, 0, vy, HX_F16, s, "hx_swiglu_ffn");
+  return matmul_resident_impl(va, wd, nullptr, 0, vy, HX_F16, s, entry, pt);
+}
+
+extern "C" int hx_swiglu_ffn(const hx_memref2d* x, const hx_memref1d* gamma, float eps, hx_weight_t w_gate,
+                             hx_weight_t w_up, hx_weight_t w_down, hx_memref2d* y, hx_stream_t stream) {
+  return swiglu_ffn_impl(x, gamma, eps, w_gate, w_up, w_down, y, stream, nullptr, "hx_swiglu_ffn");
 }
 
 // ---------------------------------------------------------------------------
@@ -1068,10 +1252,13 @@ extern "C" int hx_config_get(int op, int index, hx_kernel_config* out) {
   out->index = index;
   if (gemv_op(op)) {
     const GemvConfig* c = gemv_packed_config(idx[index]);
-    out->bm = 16; out->bn = 16 * c->ct; out->bk = op == HX_OP_GEMV_W8 ? 64 : 32;
+    // bm: activation rows one launch covers (16-row blocks); lds_bytes: the
+    // cross-wave reduction buffer (reused per row block) plus, for configs
+    // that stage the activation rows in LDS, the 64 KiB staging limit
+    out->bm = 16 * c->mb; out->bn = 16 * c->ct; out->bk = op == HX_OP_GEMV_W8 ? 64 : 32;
     out->waves_m = c->kw; out->waves_n = 1;
     out->lds_stages = 0; out->split_k = c->kw; out->col_tiles = c->ct;
-    out->lds_bytes = c->kw * c->ct * 64 * 4 * 4;
+    out->lds_bytes = c->kw * c->ct * 64 * 4 * 4 + (c->xl ? 65536 : 0);
     snprintf(out->name, sizeof(out->name), "gemv_%s", c->name);
     return HX_OK;
   }
@@ -1115,18 +1302,24 @@ extern "C" int hx_config_pins_save(char* buf, size_t cap, size_t* needed) {
   int dev;
   int rc = current_device(&dev);
   if (rc) return rc;
-  std::string out = "hx-pins/v1 " HX_BUILD_ID "\n";
+  std::string out = "hx-pins/v2 " HX_BUILD_ID "\n";
+  std::vector<std::pair<int, double>> canaries = canary_references(dev);
   {
     std::lock_guard<std::mutex> lk(g_mu);
     for (const auto& kv : g_pins) {
       if (std::get<0>(kv.first) != dev) continue;
       const int op = std::get<1>(kv.first);
-      char line[160];
-      snprintf(line, sizeof(line), "%d %lld %lld %lld %d %s\n", op, (long long)std::get<2>(kv.first),
+      char line[192];
+      snprintf(line, sizeof(line), "pin %d %lld %lld %lld %d %s\n", op, (long long)std::get<2>(kv.first),
                (long long)std::get<3>(kv.first), (long long)std::get<4>(kv.first), kv.second,
                config_name(op, kv.second));
       out += line;
     }
+  }
+  for (const auto& c : canaries) {
+    char line[96];
+    snprintf(line, sizeof(line), "canary %d %.6g\n", c.first, c.second);
+    out += line;
   }
   if (needed) *needed = out.size() + 1;
   if (!buf || cap < out.size() + 1)
@@ -1140,7 +1333,7 @@ extern "C" int hx_config_pins_load(const char* text) {
   int dev;
   int rc = current_device(&dev);
   if (rc) return rc;
-  const std::string header = "hx-pins/v1 " HX_BUILD_ID;
+  const std::string header = "hx-pins/v2 " HX_BUILD_ID;
   const char* nl = strchr(text, '\n');
   const std::string first = nl ? std::string(text, nl - text) : std::string(text);
   if (first != header)
@@ -1148,6 +1341,7 @@ extern "C" int hx_config_pins_load(const char* text) {
                 header.c_str());
   // parse everything before applying anything
   std::vector<std::pair<std::tuple<int, int, int64_t, int64_t, int64_t>, int>> pins;
+  std::vector<std::pair<int, double>> canaries;
   for (const char* line = nl ? nl + 1 : nullptr; line && *line;) {
     const char* end = strchr(line, '\n');
     const std::string l = end ? std::string(line, end - line) : std::string(line);
@@ -1156,15 +1350,25 @@ extern "C" int hx_config_pins_load(const char* text) {
     int op, index;
     long long m, n, k;
     char name[64];
-    if (sscanf(l.c_str(), "%d %lld %lld %lld %d %63s", &op, &m, &n, &k, &index, name) != 6)
+    double q50;
+    if (sscanf(l.c_str(), "pin %d %lld %lld %lld %d %63s", &op, &m, &n, &k, &index, name) == 6) {
+      const char* have = config_name(op, index);
+      if (!have || strcmp(have, name) != 0)
+        return fail(HX_ERR_ARG, "hx_config_pins_load: op %d index %d is not config '%s'", op, index, name);
+      pins.emplace_back(std::make_tuple(dev, op, (int64_t)m, (int64_t)n, (int64_t)k), index);
+    } else if (sscanf(l.c_str(), "canary %d %lf", &op, &q50) == 2) {
+      if (family_indices(op).empty() || !(q50 > 0.0) || !std::isfinite(q50))
+        return fail(HX_ERR_ARG, "hx_config_pins_load: bad canary line '%s'", l.c_str());
+      canaries.emplace_back(op, q50);
+    } else {
       return fail(HX_ERR_ARG, "hx_config_pins_load: malformed line '%s'", l.c_str());
-    const char* have = config_name(op, index);
-    if (!have || strcmp(have, name) != 0)
-      return fail(HX_ERR_ARG, "hx_config_pins_load: op %d index %d is not config '%s'", op, index, name);
-    pins.emplace_back(std::make_tuple(dev, op, (int64_t)m, (int64_t)n, (int64_t)k), index);
+    }
   }
-  std::lock_guard<std::mutex> lk(g_mu);
-  for (const auto& p : pins) g_pins[p.first] = p.second;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    for (const auto& p : pins) g_pins[p.first] = p.second;
+  }
+  for (const auto& c : canaries) canary_reference_set(dev, c.first, c.second);
   return HX_OK;
 }
 

@@ -156,5 +156,15 @@ int launch_transpose(const void* src, int64_t lds, void* dst, int64_t ldd, int64
 int launch_f16_to_f32(const void* src, float* dst, int64_t n, hipStream_t s);
 // 64-bit content hash of a byte range (order-dependent, deterministic).
 int launch_hash64(const void* src, int64_t bytes, uint64_t* out_dev, hipStream_t s);
+// Adds to *count_dev the number of 4-byte words (and tail bytes) in which
+// two 16-byte aligned ranges differ.
+int launch_diff_bytes(const void* a, const void* b, int64_t bytes, unsigned* count_dev, hipStream_t s);
+// Seeded uniform fill of n elements of type dt: integers in [lo, hi] for
+// DT_I8, U[lo, hi) rounded to the type otherwise.
+int launch_fill_uniform(void* dst, int64_t n, int dt, float lo, float hi, uint64_t seed, hipStream_t s);
+// Adds to *count_dev the elements where |got - want| > atol + rtol |want|
+// (or either is not finite), for DT_F16 / DT_BF16 / DT_F32 arrays.
+int launch_count_far(const void* got, const void* want, int64_t n, int dt, float rtol, float atol,
+                     unsigned* count_dev, hipStream_t s);
 
 }  // namespace hx

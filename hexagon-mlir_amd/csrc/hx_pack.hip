@@ -7,7 +7,11 @@
 //     171-212; QHB/lib/Dialect/Hmx/Transforms/WeightResidentPass.cpp:1-60);
 //   * f16 -> f32 widening of per-channel scales (exact);
 //   * a 64-bit content hash used to key registered weights by content, as
-//     the reference keys its prepack cache (hmx_weight_prepack.py:155-168).
+//     the reference keys its prepack cache (hmx_weight_prepack.py:155-168),
+//     and a byte-wise comparison that confirms a hash hit before two
+//     registrations share one image;
+//   * a seeded uniform fill and a mismatch count, the synthetic operands and
+//     the first-repetition check of the native autotuner.
 #include "hx_device.hpp"
 #include "hx_internal.hpp"
 
@@ -159,6 +163,115 @@ int launch_hash64(const void* src, int64_t bytes, uint64_t* out_dev, hipStream_t
   if (blocks > 2048) blocks = 2048;
   if (blocks < 1) blocks = 1;
   hash64_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>((const uint8_t*)src, bytes, out_dev);
+  return HXI_OK;
+}
+
+// Number of 4-byte words (and tail bytes) in which a and b differ (added to
+// *count).
+__global__ void __launch_bounds__(256) diff_bytes_kernel(const uint8_t* a, const uint8_t* b, int64_t bytes,
+                                                         unsigned* count) {
+  unsigned bad = 0;
+  const int64_t words = bytes / 16;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < words; i += (int64_t)gridDim.x * 256) {
+    const v4i x = *reinterpret_cast<const v4i*>(a + 16 * i);
+    const v4i y = *reinterpret_cast<const v4i*>(b + 16 * i);
+    bad += (x[0] != y[0]) + (x[1] != y[1]) + (x[2] != y[2]) + (x[3] != y[3]);
+  }
+  if (blockIdx.x == 0)
+    for (int64_t j = 16 * words + threadIdx.x; j < bytes; j += 256) bad += a[j] != b[j];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) bad += __shfl_xor(bad, o, 64);
+  __shared__ unsigned part[4];
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = bad;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned t = part[0] + part[1] + part[2] + part[3];
+    if (t) atomicAdd(count, t);
+  }
+}
+
+int launch_diff_bytes(const void* a, const void* b, int64_t bytes, unsigned* count_dev, hipStream_t s) {
+  if ((((uintptr_t)a | (uintptr_t)b) & 15u) != 0) return HXI_ERR_ARG;
+  int64_t blocks = (bytes / 16 + 255) / 256;
+  if (blocks > 2048) blocks = 2048;
+  if (blocks < 1) blocks = 1;
+  diff_bytes_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>((const uint8_t*)a, (const uint8_t*)b, bytes,
+                                                                  count_dev);
+  return HXI_OK;
+}
+
+// Element i of a seeded stream: a 64-bit mix of (seed, i), mapped to
+// integers in [lo, hi] (DT_I8) or to U[lo, hi) rounded to the element type.
+__device__ __forceinline__ uint64_t fill_mix(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+__global__ void __launch_bounds__(256) fill_uniform_kernel(void* dst, int64_t n, int dt, float lo, float hi,
+                                                           uint64_t seed) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const uint64_t r = fill_mix(seed * 0x9e3779b97f4a7c15ull + (uint64_t)i);
+    if (dt == DT_I8) {
+      const int span = (int)hi - (int)lo + 1;
+      reinterpret_cast<int8_t*>(dst)[i] = (int8_t)((int)lo + (int)((r >> 32) % (uint64_t)span));
+      continue;
+    }
+    const float u = (float)(r >> 40) * (1.0f / 16777216.0f);  // [0, 1), 24 bits
+    const float v = lo + (hi - lo) * u;
+    if (dt == DT_F16) reinterpret_cast<uint16_t*>(dst)[i] = f32_to_f16_bits(v);
+    else if (dt == DT_BF16) reinterpret_cast<uint16_t*>(dst)[i] = f32_to_bf16(v);
+    else reinterpret_cast<float*>(dst)[i] = v;
+  }
+}
+
+int launch_fill_uniform(void* dst, int64_t n, int dt, float lo, float hi, uint64_t seed, hipStream_t s) {
+  if (dt != DT_I8 && dt != DT_F16 && dt != DT_BF16 && dt != DT_F32) return HXI_ERR_DTYPE;
+  if (n <= 0) return HXI_OK;
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  fill_uniform_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(dst, n, dt, lo, hi, seed);
+  return HXI_OK;
+}
+
+// Elements of a float matrix (f16 / bf16 / f32) where |got - want| >
+// atol + rtol |want|, or either is not finite (added to *count).
+__global__ void __launch_bounds__(256) count_far_kernel(const void* got, const void* want, int64_t n, int dt,
+                                                        float rtol, float atol, unsigned* count) {
+  unsigned bad = 0;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    float g, w;
+    if (dt == DT_F32) {
+      g = reinterpret_cast<const float*>(got)[i];
+      w = reinterpret_cast<const float*>(want)[i];
+    } else if (dt == DT_BF16) {
+      g = bf16_to_f32(reinterpret_cast<const uint16_t*>(got)[i]);
+      w = bf16_to_f32(reinterpret_cast<const uint16_t*>(want)[i]);
+    } else {
+      g = f16_bits_to_f32(reinterpret_cast<const uint16_t*>(got)[i]);
+      w = f16_bits_to_f32(reinterpret_cast<const uint16_t*>(want)[i]);
+    }
+    const float d = fabsf(g - w);
+    bad += !(d <= atol + rtol * fabsf(w));  // NaN / inf count as far
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) bad += __shfl_xor(bad, o, 64);
+  __shared__ unsigned part[4];
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = bad;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned t = part[0] + part[1] + part[2] + part[3];
+    if (t) atomicAdd(count, t);
+  }
+}
+
+int launch_count_far(const void* got, const void* want, int64_t n, int dt, float rtol, float atol,
+                     unsigned* count_dev, hipStream_t s) {
+  if (dt != DT_F16 && dt != DT_BF16 && dt != DT_F32) return HXI_ERR_DTYPE;
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 2048) blocks = 2048;
+  if (blocks < 1) blocks = 1;
+  count_far_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(got, want, n, dt, rtol, atol, count_dev);
   return HXI_OK;
 }
 

@@ -20,7 +20,8 @@
  *   - Data pointers are device pointers.  The caller owns every tensor; the
  *     library owns registered weights and a per-stream workspace.
  *   - Work is enqueued on `stream` (NULL = the null stream); no entry point
- *     synchronizes the device except hx_weight_register.
+ *     synchronizes the device except hx_weight_register, hx_weight_release
+ *     (of the last reference) and hx_tune.
  *   - Return value: HX_OK or a negative HX_ERR_*; hx_last_error() returns a
  *     thread-local message for the last failure.  Failures are closed: there
  *     is no silent fallback to another arithmetic path (the reference aborts
@@ -270,16 +271,116 @@ int hx_config_select(int op, int64_t m, int64_t n, int64_t k, int index);
  * the untuned default.  *index = -1 means the generic (any-alignment)
  * kernel. */
 int hx_config_lookup(int op, int64_t m, int64_t n, int64_t k, int* index);
-/* Persist the tuner's champions: hx_config_pins_save writes the current
- * device's pins as text ("hx-pins/v1 <build id>" then one "op m n k index
- * name" line per pin; NUL-terminated, *needed = size; HX_ERR_ARG if cap is
- * too small) and hx_config_pins_load pins them again in another process.
- * Pins from another build are refused (a config index means nothing across
- * builds), as is any line whose index does not name the same config.
- * Replaces the tuned-config cache of QHB/backend/hmx_search.py (keyed by
- * build fingerprints, tuning_key_int :416-452). */
+/* Persist the tuner's state: hx_config_pins_save writes the current
+ * device's pins and canary references as text ("hx-pins/v2 <build id>",
+ * then one "pin op m n k index name" line per pin and one "canary op q50_us"
+ * line per family with a canary reference; NUL-terminated, *needed = size;
+ * HX_ERR_ARG if cap is too small) and hx_config_pins_load restores them in
+ * another process.  Text from another build is refused (a config index
+ * means nothing across builds), as is any line whose index does not name
+ * the same config; a refused load changes nothing.  Replaces the
+ * tuned-config cache of QHB/backend/hmx_search.py (keyed by build
+ * fingerprints, tuning_key_int :416-452) and the canary record the next
+ * round is judged against (:1292-1368). */
 int hx_config_pins_save(char* buf, size_t cap, size_t* needed);
 int hx_config_pins_load(const char* text);
+
+/* ---------------------------------------------------------------------- */
+/* Autotuning                                                              */
+/* ---------------------------------------------------------------------- */
+
+/* Status of one configuration in a tuning round. */
+enum {
+    HX_TUNE_TIMED = 0,          /* timed; q50/q20/q80 hold its per-launch times */
+    HX_TUNE_REFUSED = 1,        /* not legal at this shape; `reason` says why */
+    HX_TUNE_LAUNCH_FAILED = 2,  /* a launch or its timing failed: scored infinite */
+    HX_TUNE_WRONG = 3           /* its first launch disagreed with the reference
+                                   kernel: scored infinite after one launch */
+};
+
+/* The canary: the family's untuned default on a small fixed shape, timed
+ * after the sweep and judged against the family's previous valid round. */
+enum {
+    HX_CANARY_BASELINE = 0,     /* no earlier reading: this one becomes the reference */
+    HX_CANARY_STEADY = 1,       /* within its gate of the reference */
+    HX_CANARY_DRIFT = 2,        /* moved by more than its gate: the round is void */
+    HX_CANARY_FAILED = 3        /* could not be timed: the round is void */
+};
+
+typedef struct hx_tune_options {
+    int32_t reps;               /* repetitions per configuration; 0 = 3 */
+    int32_t min_iters;          /* launches per repetition = clamp(budget / one */
+    int32_t max_iters;          /*   launch, min, max); 0 = 5 and 1000 */
+    double budget_us;           /* device time aimed at per repetition; 0 = 2e6 */
+    double canary_reference_us; /* > 0: judge the canary against this median;
+                                   0: against the family's held reference (the
+                                   last valid round, or hx_config_pins_load);
+                                   < 0: no reference (the round sets one) */
+    int32_t pin;                /* pin the champion when the round is valid */
+    uint64_t seed;              /* synthetic operand seed; 0 = a fixed default */
+} hx_tune_options;
+
+typedef struct hx_tune_entry {
+    int32_t index;              /* family configuration index (hx_config_get) */
+    int32_t status;             /* HX_TUNE_* */
+    double q50_us, q20_us, q80_us;  /* quantiles over the repetitions of the
+                                       mean per-launch device time (inf unless
+                                       timed) */
+    char reason[24];            /* "timed", or the refusal / failure */
+} hx_tune_entry;
+
+#define HX_TUNE_MAX_ENTRIES 64
+
+typedef struct hx_tune_report {
+    int32_t op;
+    int64_t m, n, k;
+    int32_t iters;              /* launches per repetition (largest used) */
+    int32_t control_index;      /* the untuned default: the control arm */
+    int32_t best_index;         /* the fastest timed configuration, or -1 */
+    int32_t champion_index;     /* best when it beats the control by more than
+                                   the gate (or no control was timed), else the
+                                   control; -1 when nothing was timed */
+    double control_q50_us, best_q50_us;
+    double margin;              /* (control - best) / control */
+    double gate;                /* max(3 * CV, 0.15), CV = (q80 - q20) / q50 of
+                                   the noisier of the two arms */
+    int32_t canary_index;
+    int64_t canary_m, canary_n, canary_k;
+    int32_t canary_status;      /* HX_CANARY_* */
+    double canary_q50_us, canary_reference_us;
+    double canary_shift;        /* (canary - reference) / reference */
+    double canary_gate;         /* max(3 * CV_canary, 0.15) */
+    int32_t round_valid;        /* canary BASELINE or STEADY */
+    int32_t pinned;             /* this call pinned the champion */
+    int32_t n_entries;
+    hx_tune_entry entries[HX_TUNE_MAX_ENTRIES];
+} hx_tune_report;
+
+/* Autotune family `op` at (m, n, k) on the current device: every compiled
+ * configuration runs on synthetic seeded operands the call allocates
+ * (weights of the decode families rotated over copies larger than the
+ * 256 MB MALL), its first launch is checked against the generic kernel
+ * (bit-equal for int8, within 1e-2 relative for floats), and it is timed
+ * with HIP events on `stream` for `reps` repetitions.  The champion is the
+ * fastest configuration if it beats the untuned default by more than the
+ * gate, else the default.  The round is void when the canary drifted or
+ * failed; a void round pins nothing and leaves every earlier pin in place.
+ * A valid round becomes the family's canary reference.  Synchronizes
+ * `stream`; allocates and frees device memory.  Replaces the tile search of
+ * QHB/backend/hmx_search.py: enumerate_tile_configs / tile_verdict
+ * (:246-332), hexagon_bench (:1109-1156), calibration_iters (:1159-1177),
+ * quantile_spread_cv / champion_gate (:1254-1289) and the canary
+ * (:1292-1368). */
+int hx_tune(int op, int64_t m, int64_t n, int64_t k, const hx_tune_options* opt,
+            hx_tune_report* out, hx_stream_t stream);
+
+/* The decision of hx_tune alone, with no device work: from timed entries,
+ * the control's configuration index, the canary's entry and a reference
+ * median (<= 0: none), fill best/champion/margin/gate and the canary and
+ * round fields of `out`. */
+int hx_tune_decide(const hx_tune_entry* entries, int n, int control_index,
+                   const hx_tune_entry* canary, double canary_reference_us,
+                   hx_tune_report* out);
 
 /* ---------------------------------------------------------------------- */
 /* Scaled-dot-product attention                                            */

@@ -101,7 +101,7 @@ def test_config_pins_round_trip(hx, dev):
     for op, m, n, k, i in shapes:
         hx.config_select(op, m, n, k, i)
     text = hx.config_pins_save()
-    assert text.startswith("hx-pins/v1 " + hx.build_id())
+    assert text.startswith("hx-pins/v2 " + hx.build_id())
     for op, m, n, k, i in shapes:
         hx.config_select(op, m, n, k, -1)
     try:
@@ -114,7 +114,7 @@ def test_config_pins_round_trip(hx, dev):
         other = text.replace(hx.build_id(), "hxmi-gfx950-0000000000000000-x", 1)
         with pytest.raises(hx.HXError, match="pins are from"):
             hx.config_pins_load(other)
-        wrong = text.splitlines()[0] + "\n1 1000 1000 1000 3 not_a_config\n"
+        wrong = text.splitlines()[0] + "\npin 1 1000 1000 1000 3 not_a_config\n"
         with pytest.raises(hx.HXError, match="is not config"):
             hx.config_pins_load(wrong)
         assert hx.config_pins_save() == before, "a refused load must pin nothing"

@@ -1,9 +1,19 @@
-"""The autotune protocol, pinned on the host with the known answers of the
-reference's own contract tests (qcom_hexagon_backend/test/
-test_hmx_champion_criterion_contract.py and test_hmx_search_loop_contract.py):
-the gate max(3xCV, 15%) with ties to the incumbent, the defended walk, the
-canary verdicts, inf on failure, the first-rep correctness gate, and the
-calibration box.  Plus the gfx950 legality rules over the compiled configs."""
+"""The native autotuner's decision rule (hx_tune_decide, the decision half of
+hx_tune), checked on the CPU through the C ABI with hand-computed cases:
+
+* the gate is max(3 CV, 15%), CV = (q80 - q20) / q50 of the noisier of the
+  fastest configuration and the untuned default (the protocol constant of
+  QHB/backend/hmx_search.py champion_gate, :1280-1289);
+* the fastest timed configuration replaces the default only when it is
+  faster by more than the gate; a margin equal to the gate keeps the
+  default;
+* configurations that failed, were refused or were wrong never win;
+* with no timed default, the fastest configuration is the champion;
+* the canary: no reference sets one (baseline, valid); a shift within its
+  own gate is steady (valid); beyond it, drift voids the round; an untimed
+  canary voids the round.
+
+A GPU test (tests/test_gpu_tune.py) drives the whole of hx_tune."""
 import math
 
 import pytest
@@ -16,150 +26,96 @@ def S(hx):
     return hx.search
 
 
-def row(cfg, tiles, q50, spread=None):
-    if spread is None:
-        spread = 0.02 * q50
-    return dict(cfg=cfg, tiles=list(tiles), q50_us=q50, q20_us=q50 - spread, q80_us=q50 + spread)
+def e(index, q50, spread=0.0, status=0):
+    """An entry with quantiles q50 -/+ spread/2 (CV = spread / q50)."""
+    return dict(index=index, q50=q50, q20=None if q50 is None else q50 - spread / 2,
+                q80=None if q50 is None else q50 + spread / 2, status=status)
 
 
-def canary(q50=5000.0, spread=100.0):
-    return row("canary", (32, 32, 32), q50, spread)
+def test_gate_floor_and_cv_factor(S):
+    # quiet arms: the gate is its 15% floor
+    r = S.decide([e(0, 100.0), e(1, 80.0)], control_index=0, canary=e(0, 5.0))
+    assert r["gate"] == pytest.approx(0.15)
+    assert r["margin"] == pytest.approx(0.20)
+    assert r["champion_index"] == 1 and r["best_index"] == 1
+    # a noisy control (CV 0.1) lifts the gate to 30%: a 20% win is not enough
+    r = S.decide([e(0, 100.0, spread=10.0), e(1, 80.0)], control_index=0, canary=e(0, 5.0))
+    assert r["gate"] == pytest.approx(0.30)
+    assert r["champion_index"] == 0 and r["best_index"] == 1
+    # the noisier arm sets it: CV of the challenger 0.125 -> gate 0.375
+    r = S.decide([e(0, 100.0, spread=1.0), e(1, 80.0, spread=10.0)], control_index=0, canary=e(0, 5.0))
+    assert r["gate"] == pytest.approx(0.375)
 
 
-def test_gate_and_cv(S):
-    assert (S.CHAMPION_CV_FACTOR, S.CHAMPION_MARGIN_FLOOR) == (3.0, 0.15)
-    assert S.champion_gate(0.0) == 0.15
-    assert abs(S.champion_gate(0.05) - 0.15) < 1e-12
-    assert abs(S.champion_gate(0.10) - 0.30) < 1e-12
-    assert abs(S.champion_gate(1.0) - 3.0) < 1e-12
-    assert S.champion_gate(None) == 0.15
-    assert S.quantile_spread_cv(980, 1000, 1020) == 0.04
-    assert S.quantile_spread_cv(None, 1000, 1020) == 0.0
-    assert S.quantile_spread_cv(980, INF, 1020) == 0.0
-    assert S.quantile_spread_cv(0, 0, 0) == 0.0
+def test_margin_equal_to_gate_keeps_the_default(S):
+    # 85 against 100 is exactly the 15% floor: not more than the gate
+    r = S.decide([e(0, 100.0), e(3, 85.0)], control_index=0, canary=e(0, 5.0))
+    assert r["margin"] == pytest.approx(0.15)
+    assert r["champion_index"] == 0
+    r = S.decide([e(0, 100.0), e(3, 84.9)], control_index=0, canary=e(0, 5.0))
+    assert r["champion_index"] == 3
 
 
-def test_tie_goes_to_incumbent(S):
-    rep = S.judge_champion_round([row("ctrl", (32, 32, 32), 1000.0), row("edge", (64, 32, 32), 850.0)],
-                                 control="ctrl", canary=canary())
-    assert rep["champion"] == "ctrl" and rep["changes"] == []
-    assert rep["comparisons"][0]["outcome"] == "kept"
+def test_fastest_is_compared_not_the_walk_order(S):
+    # only the fastest candidate is judged against the default, wherever it
+    # sits in the list
+    rows = [e(2, 90.0), e(0, 100.0), e(5, 70.0), e(1, 88.0)]
+    for order in (rows, rows[::-1]):
+        r = S.decide(order, control_index=0, canary=e(0, 5.0))
+        assert r["best_index"] == 5 and r["champion_index"] == 5
+        assert r["margin"] == pytest.approx(0.30)
 
 
-def test_crown_is_defended(S):
-    rows = [row("ctrl", (32, 32, 32), 1000.0), row("A", (64, 32, 32), 700.0),
-            row("B", (32, 64, 32), 900.0), row("C", (128, 32, 32), 640.0)]
-    rep = S.judge_champion_round(rows, control="ctrl", iters=300, canary=canary())
-    assert rep["round_verdict"] == S.ROUND_VALID
-    assert rep["champion"] == "A" and rep["champion_tiles"] == [64, 32, 32]
-    assert [c["challenger"] for c in rep["changes"]] == ["A"]
-    t = rep["changes"][0]
-    assert t["incumbent"] == "ctrl" and abs(t["delta_pct"] - 30.0) < 1e-9 and abs(t["gate_pct"] - 15.0) < 1e-9
-    assert {c["challenger"]: c["outcome"] for c in rep["comparisons"]} == {"B": "kept", "A": "takeover", "C": "kept"}
-    assert rep["beats_control"]["significant"] is True and rep["champion_significant"] is True
-    assert rep["iters"] == 300
-    noisy = [row("ctrl", (32, 32, 32), 1000.0, spread=50.0), row("A", (64, 32, 32), 700.0, spread=35.0)]
-    assert abs(S.quantile_spread_cv(950, 1000, 1050) - 0.10) < 1e-12
-    rep = S.judge_champion_round(noisy, control="ctrl", canary=canary())
-    assert rep["champion"] == "ctrl" and abs(rep["comparisons"][0]["gate_pct"] - 30.0) < 1e-9
+def test_failures_never_win(S):
+    rows = [e(0, 100.0), e(1, 10.0, status=1), e(2, 5.0, status=2), e(3, 1.0, status=3), e(4, 95.0)]
+    r = S.decide(rows, control_index=0, canary=e(0, 5.0))
+    assert r["best_index"] == 4
+    assert r["champion_index"] == 0  # 5% is inside the gate
+    # an infinite (unmeasured) time is not timed either
+    r = S.decide([e(0, 100.0), e(1, INF)], control_index=0, canary=e(0, 5.0))
+    assert r["best_index"] == 0 and r["champion_index"] == 0
 
 
-def test_no_control_is_not_proven(S):
-    rows = [row("x", (32, 32, 32), 900.0), row("y", (64, 32, 32), 500.0)]
-    rep = S.judge_champion_round(rows, canary=canary())
-    assert rep["champion"] == "y" and rep["beats_control"] is None
-    assert rep["champion_significant"] is False and "NOT-PROVEN" in rep["significance_note"]
-    dead = rows + [row("ctrl", (128, 128, 128), INF)]
-    rep = S.judge_champion_round(dead, control=(128, 128, 128), canary=canary())
-    assert rep["control"] is None and rep["beats_control"] is None
-    assert "never measured" in rep["walk_note"]
+def test_no_timed_control(S):
+    # the default failed: the fastest configuration is the only evidence
+    r = S.decide([e(0, 100.0, status=2), e(1, 60.0), e(2, 50.0)], control_index=0, canary=e(0, 5.0))
+    assert r["champion_index"] == 2 and r["control_q50_us"] is None
+    # the default is not among the entries at all (generic kernel)
+    r = S.decide([e(1, 60.0), e(2, 50.0)], control_index=-1, canary=e(0, 5.0))
+    assert r["champion_index"] == 2
+    # nothing timed: no champion
+    r = S.decide([e(0, None, status=1), e(1, None, status=1)], control_index=0, canary=e(0, 5.0))
+    assert r["champion_index"] == -1 and r["best_index"] == -1
 
 
-def test_unmeasured_is_per_config(S):
-    rows = [row("ctrl", (32, 32, 32), 1000.0), row("dead", (64, 64, 64), INF), row("alive", (128, 32, 32), 700.0)]
-    rep = S.judge_champion_round(rows, control="ctrl", canary=canary())
-    assert rep["unmeasured"] == ["dead"] and rep["champion"] == "alive"
-    assert rep["round_verdict"] == S.ROUND_VALID and rep["champion_significant"] is True
-    empty = S.judge_champion_round([row("only", (32, 32, 32), INF)], canary=canary())
-    assert empty["champion"] is None and empty["unmeasured"] == ["only"]
+def test_canary_rules(S):
+    rows = [e(0, 100.0), e(1, 50.0)]
+    # no reference: the round establishes one
+    r = S.decide(rows, 0, canary=e(0, 5.0, spread=0.1), canary_reference_us=0.0)
+    assert r["canary"]["status"] == "baseline" and r["round_valid"]
+    # within the gate (4% shift, quiet canary: gate 15%)
+    r = S.decide(rows, 0, canary=e(0, 5.2, spread=0.05), canary_reference_us=5.0)
+    assert r["canary"]["status"] == "steady" and r["round_valid"]
+    assert r["canary"]["shift"] == pytest.approx(0.04)
+    # beyond it, either way
+    for q in (6.0, 4.0):
+        r = S.decide(rows, 0, canary=e(0, q, spread=0.05), canary_reference_us=5.0)
+        assert r["canary"]["status"] == "drift" and not r["round_valid"]
+    # a noisy canary (CV 0.2) widens its own gate to 60%: a 20% shift is steady
+    r = S.decide(rows, 0, canary=e(0, 6.0, spread=1.2), canary_reference_us=5.0)
+    assert r["canary"]["gate"] == pytest.approx(0.6)
+    assert r["canary"]["status"] == "steady"
+    # untimed canary, or none at all: void
+    r = S.decide(rows, 0, canary=e(0, None, status=2), canary_reference_us=5.0)
+    assert r["canary"]["status"] == "failed" and not r["round_valid"]
+    r = S.decide(rows, 0, canary=None, canary_reference_us=5.0)
+    assert r["canary"]["status"] == "failed" and not r["round_valid"]
+    # the champion is still reported in a void round (it is not pinned)
+    assert r["champion_index"] == 1
 
 
-def test_canary_verdicts(S):
-    rows = [row("ctrl", (32, 32, 32), 1000.0), row("A", (64, 32, 32), 700.0)]
-    good = S.judge_champion_round(rows, control="ctrl", canary=canary())
-    assert good["canary"]["status"] == S.CANARY_REFERENCE and good["champion_significant"]
-    judged = S.judge_champion_round(rows, control="ctrl", canary=canary(), canary_reference=canary())
-    assert judged["canary"]["status"] == S.CANARY_OK
-    for c in (row("canary", (32, 32, 32), INF), None):
-        rep = S.judge_champion_round(rows, control="ctrl", canary=c)
-        assert rep["round_verdict"] == S.ROUND_INVALID_CANARY
-        assert rep["champion"] == "A" and rep["champion_significant"] is False
-        assert rep["beats_control"]["significant"] is False and "void" in rep["significance_note"]
-    drift = S.judge_champion_round(rows, control="ctrl", canary=canary(8000.0), canary_reference=canary(5000.0))
-    assert drift["canary"]["status"] == S.CANARY_DRIFT and "device state moved" in drift["canary"]["reason"]
-    assert S.canary_verdict(canary(3000.0), canary(5000.0))["status"] == S.CANARY_DRIFT
-    steady = S.canary_verdict(canary(5400.0), canary(5000.0))
-    assert steady["status"] == S.CANARY_OK and abs(steady["delta_pct"] - 8.0) < 1e-9
-    assert S.canary_verdict(canary(), row("ref", (32, 32, 32), INF))["status"] == S.CANARY_REFERENCE
-
-
-def test_bench_inf_rules_and_first_rep_gate(S):
-    def boom():
-        raise RuntimeError("launch failed")
-    assert S.bench(boom) == [INF] * 3
-    assert S.bench(lambda: (_ for _ in ()).throw(SystemExit(1))) == [INF] * 3
-    assert S.bench(lambda: float("nan")) == [INF] * 3
-    assert S.bench(lambda: None) == [INF] * 3
-    calls = []
-
-    def launch():
-        calls.append(1)
-        return 10.0
-    assert S.bench(launch, reps=3, verify=lambda: False) == [INF] * 3
-    assert len(calls) == 1, "a wrong config costs one launch"
-
-    def bad_verify():
-        raise FileNotFoundError
-    assert S.bench(launch, verify=bad_verify) == [INF] * 3
-    n = {"i": 0}
-
-    def drifting():
-        n["i"] += 1
-        return 1000.0 * n["i"]
-    assert S.bench(drifting, reps=3, verify=lambda: True) == [2000.0, 1400.0, 2600.0]
-
-
-def test_calibration_box(S):
-    assert S.calibration_iters(10.0) == 1000
-    assert S.calibration_iters(2_600_000.0) == 5
-    assert S.calibration_iters(0.0) == 1000
-    assert S.calibration_iters(float("nan")) == 1000
-
-
-def test_gfx950_legality(S, hx):
-    gemv = hx.config_get(6, 0)
-    assert S.config_verdict(gemv, 16, 11008, 4096) == S.REASON_OK
-    assert S.config_verdict(gemv, 17, 11008, 4096) == S.REASON_FAMILY_SHAPE
-    big = hx.config_get(1, 0)  # 256x256
-    assert (big["bm"], big["bn"]) == (256, 256)
-    assert S.config_verdict(big, 4096, 4096, 4096) == S.REASON_OK
-    assert S.config_verdict(big, 64, 4096, 4096) == S.REASON_TILE_EXCEEDS_EXTENT
-    assert S.config_verdict(dict(big, lds_bytes=200_000), 4096, 4096, 4096) == S.REASON_LDS_BUDGET
-    cands = S.enumerate_configs(1, 4096, 4096, 4096)
-    assert [c["tiles"] for c in cands] == sorted(c["tiles"] for c in cands)
-    assert all(c["verdict"] == S.REASON_OK for c in cands)
-    small = S.enumerate_configs(1, 16, 16, 256)
-    assert any(c["verdict"] == S.REASON_TILE_EXCEEDS_EXTENT for c in small)
-    assert any(c["verdict"] == S.REASON_OK for c in small)
-
-
-def test_cache_key_and_roundtrip(S, tmp_path):
-    k = S.cache_key("b1", "MI355X", "gfx950", 256, 1, 4096, 4096, 4096)
-    assert "b1" in k and "4096x4096x4096" in k
-    assert k != S.cache_key("b2", "MI355X", "gfx950", 256, 1, 4096, 4096, 4096)
-    c = S.TuneCache(tmp_path / "tune.json")
-    c.put(k, {"champion": "x", "champion_index": 2, "round_verdict": S.ROUND_VALID})
-    c.save()
-    c2 = S.TuneCache(tmp_path / "tune.json")
-    assert c2.get(k)["champion_index"] == 2
-    assert math.isfinite(S.quantile([3.0, 1.0, 2.0], 0.5))
+def test_cv_of_degenerate_quantiles(S):
+    # a single repetition has q20 = q50 = q80: CV 0, gate on its floor
+    r = S.decide([dict(index=0, q50=100.0), dict(index=1, q50=80.0)], control_index=0, canary=e(0, 5.0))
+    assert r["gate"] == pytest.approx(0.15)
+    assert math.isfinite(r["margin"])
