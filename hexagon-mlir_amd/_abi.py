@@ -112,6 +112,7 @@ SIGNATURES = {
                         ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(_i)], _i),
     "hx_matmul_resident": ([_P2, _i, _vp, _P2, _i, _P2, _i, _vp], _i),
     "hx_swiglu_ffn": ([_P2, _P1, _f, _vp, _vp, _vp, _P2, _vp], _i),
+    "hx_swiglu_ffn_noalloc": ([_P2, _P1, _f, _vp, _vp, _vp, _P2, _vp], _i),
     "hx_config_count": ([_i], _i),
     "hx_config_get": ([_i, _i, ctypes.POINTER(KernelConfig)], _i),
     "hx_config_select": ([_i, _i64, _i64, _i64, _i], _i),

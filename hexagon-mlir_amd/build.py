@@ -24,7 +24,8 @@ ARCH = "gfx950"
 # the GEMM tables are split per operand mode so that their kernel
 # instantiations compile in parallel (each takes minutes)
 SOURCES = ["hx_gemm_i8.hip", "hx_gemm_w8.hip", "hx_gemm_f16.hip", "hx_gemm_bf16.hip", "hx_gemm.hip",
-           "hx_rows.hip", "hx_gemv.hip", "hx_pack.hip", "hx_attn.hip", "hx_api.cpp", "hx_tune.cpp"]
+           "hx_rows.hip", "hx_gemv.hip", "hx_pack.hip", "hx_attn.hip", "hx_api.cpp", "hx_tune.cpp",
+           "hx_noalloc.cpp"]
 
 # Packed-FP32 VALU forms are disabled for all device code (they are not
 # needed: the hot loops are MFMA or memory bound).  Floating-point

@@ -494,7 +494,8 @@ extern "C" int hx_init(void) {
   if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
     return fail(HX_ERR_UNSUPPORTED, "device %d is %s; libhxmi is built for gfx950 only", dev,
                 prop.gcnArchName);
-  return HX_OK;
+  // the no-allocation entry point's scratch address on this device
+  return noalloc_setup(nullptr);
 }
 
 extern "C" const char* hx_last_error(void) { return g_err.c_str(); }

@@ -40,6 +40,10 @@ struct FixedScratch {
   size_t cap;
 };
 
+// The current device's fixed scratch (hx_noalloc.cpp), resolved once per
+// device; *out (may be null) receives its address.
+int noalloc_setup(char** out);
+
 // The SwiGLU FFN block (hx_swiglu_ffn); with `fixed` every intermediate and
 // K-split partial lives in that memory and the call allocates nothing.
 int swiglu_ffn_impl(const hx_memref2d* x, const hx_memref1d* gamma, float eps, hx_weight_t w_gate,

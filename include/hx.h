@@ -228,6 +228,27 @@ int hx_swiglu_ffn(const hx_memref2d* x, const hx_memref1d* gamma, float eps,
                   hx_weight_t w_gate, hx_weight_t w_up, hx_weight_t w_down,
                   hx_memref2d* y, hx_stream_t stream);
 
+/* Size of the fixed per-GPU scratch of hx_swiglu_ffn_noalloc (32 MiB). */
+#define HX_NOALLOC_SCRATCH_BYTES (32 << 20)
+
+/* hx_swiglu_ffn that allocates nothing.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments and bit-identical result as hx_swiglu_ffn; the RMSNorm
+ * output, the gate/up/SiLU*mul intermediates and the down projection's
+ * K-split partials live in a fixed device array of HX_NOALLOC_SCRATCH_BYTES
+ * that each GPU the library runs on holds until the process ends, instead
+ * of the stream workspace.  The call makes no hipMalloc or hipFree.  It
+ * needs T*(H + I)*2 bytes for T > 64 tokens (T*(H + 3 I)*2 for T <= 64, the
+ * decode path), plus T*H*4 per K part when the down projection's
+ * configuration splits K (256-byte aligned each); a shape that needs more
+ * than the array returns HX_ERR_UNSUPPORTED before anything is enqueued.
+ * Every call on one GPU shares its array: calls that overlap on one GPU
+ * race. */
+int hx_swiglu_ffn_noalloc(const hx_memref2d* x, const hx_memref1d* gamma, float eps,
+                          hx_weight_t w_gate, hx_weight_t w_up, hx_weight_t w_down,
+                          hx_memref2d* y, hx_stream_t stream);
+
 /* ---------------------------------------------------------------------- */
 /* Kernel configurations (the autotuner's search space)                    */
 /* ---------------------------------------------------------------------- */

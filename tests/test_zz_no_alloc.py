@@ -1,0 +1,96 @@
+"""hx_swiglu_ffn_noalloc through the C ABI: the FFN block with its
+intermediates in the library's fixed per-GPU scratch.  Its output must equal
+hx_swiglu_ffn's bit for bit (the same kernels and configurations run), on two
+calls in a row, the second with fewer tokens; it must allocate no device
+memory; and a shape whose intermediates exceed the scratch is refused
+before anything runs."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import rng, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+H, I = 4096, 11008
+
+
+def _weights(hx, dev, seed):
+    r = rng(seed)
+    wg = r.integers(-127, 128, (H, I), dtype=np.int8)
+    wu = r.integers(-127, 128, (H, I), dtype=np.int8)
+    wd = r.integers(-127, 128, (I, H), dtype=np.int8)
+    sg = (r.uniform(0.5, 1.5, I) / (127 * np.sqrt(H / 3))).astype(np.float16)
+    su = (r.uniform(0.5, 1.5, I) / (127 * np.sqrt(H / 3))).astype(np.float16)
+    sd = (r.uniform(0.5, 1.5, H) / (127 * np.sqrt(I / 3))).astype(np.float16)
+    return (hx.ResidentWeight(to_dev(wg, dev), to_dev(sg, dev)), hx.ResidentWeight(to_dev(wu, dev), to_dev(su, dev)),
+            hx.ResidentWeight(to_dev(wd, dev), to_dev(sd, dev)))
+
+
+def _noalloc(hx, x, gamma, eps, Wg, Wu, Wd, y, stream):
+    from hexagon_mlir_amd import ops
+    fn = hx._abi.load().hx_swiglu_ffn_noalloc
+    mx, mg, my = ops.memref2d(x, "x"), ops.memref1d(gamma, "gamma"), ops.memref2d(y, "y")
+    return fn(ctypes.byref(mx), ctypes.byref(mg), eps, Wg.handle, Wu.handle, Wd.handle, ctypes.byref(my),
+              ctypes.c_void_p(stream.cuda_stream))
+
+
+def test_noalloc_matches_and_allocates_nothing(hx, dev):
+    """Two no-allocation calls in a row (256 tokens: the fused gate/up GEMM and
+    the K-split down projection; then 40 tokens: the decode GEMVs) leave the
+    device's free memory unchanged and equal hx_swiglu_ffn bit for bit.  A
+    warm-up pass first lets the HIP runtime load the kernels' code objects
+    and set up the stream (its own lazy allocations, not the call's)."""
+    import torch
+    Wg, Wu, Wd = _weights(hx, dev, 500)
+    stream = torch.cuda.Stream()  # a stream the workspace path has never seen
+    # set-up: hx_init resolves this device's scratch (and loads the code
+    # object that holds it)
+    assert hx._abi.load().hx_init() == 0, hx._abi.last_error()
+    try:
+        gamma = to_dev(rng(501).normal(1, 0.1, H).astype(np.float16), dev)
+        shapes = (256, 40)
+        xs = {T: to_dev(rng(502 + T).normal(0, 1, (T, H)).astype(np.float16), dev) for T in shapes}
+        ys = {T: torch.full((T, H), 7.0, dtype=torch.float16, device=dev) for T in shapes}
+        refs = {T: torch.full((T, H), 3.0, dtype=torch.float16, device=dev) for T in shapes}
+        for T in shapes:  # warm-up
+            with torch.cuda.stream(stream):
+                assert _noalloc(hx, xs[T], gamma, 1e-6, Wg, Wu, Wd, ys[T], stream) == 0, hx._abi.last_error()
+            stream.synchronize()
+            ys[T].fill_(7.0)
+        torch.cuda.synchronize()
+        free_before = torch.cuda.mem_get_info()[0]
+        for T in shapes:  # the measured calls: 256 tokens, then 40
+            with torch.cuda.stream(stream):
+                rc = _noalloc(hx, xs[T], gamma, 1e-6, Wg, Wu, Wd, ys[T], stream)
+            assert rc == 0, hx._abi.last_error()
+            stream.synchronize()
+        assert torch.cuda.mem_get_info()[0] == free_before, "the no-allocation calls allocated"
+        for T in shapes:
+            with torch.cuda.stream(stream):
+                hx.swiglu_ffn(xs[T], gamma, 1e-6, Wg, Wu, Wd, out=refs[T])
+            stream.synchronize()
+            a, b = to_np(refs[T]), to_np(ys[T])
+            assert np.isfinite(a.astype(np.float32)).all()
+            assert np.array_equal(a.view(np.uint16), b.view(np.uint16)), f"T={T}"
+    finally:
+        Wg.release(); Wu.release(); Wd.release()
+
+
+def test_noalloc_refuses_what_does_not_fit(hx, dev):
+    import torch
+    Wg, Wu, Wd = _weights(hx, dev, 510)
+    try:
+        T = 2048  # 16.8 MB + 45 MB of intermediates alone
+        x = torch.zeros((T, H), dtype=torch.float16, device=dev)
+        gamma = torch.ones(H, dtype=torch.float16, device=dev)
+        y = torch.full((T, H), 5.0, dtype=torch.float16, device=dev)
+        stream = torch.cuda.current_stream()
+        rc = _noalloc(hx, x, gamma, 1e-6, Wg, Wu, Wd, y, stream)
+        assert rc == -7, rc  # HX_ERR_UNSUPPORTED
+        assert "scratch" in hx._abi.last_error()
+        torch.cuda.synchronize()
+        assert bool((y == 5.0).all()), "a refused call must launch nothing"
+    finally:
+        Wg.release(); Wu.release(); Wd.release()
