@@ -497,12 +497,14 @@ def bench_attention(hx, iters: int = 20):
 
 # --------------------------------------------------------------------------- #
 
-def pmc_workload(hx) -> None:
+def pmc_workload(hx, keys_path=None) -> None:
     """A few launches of every benchmarked kernel -- every compiled config of
     the headline GEMM and of the decode GEMV, so whichever one the tuner
-    picks has a reading -- plus a plain 64 MiB copy of known size, for
-    ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` runs (the copy's readings
-    give the scale factor from counter to bytes)."""
+    picks has a reading, the headline with its int32 output, the row ops and
+    the FFN block -- plus a plain 64 MiB copy of known size, for the
+    ``rocprofv3 --pmc`` runs (FETCH_SIZE, WRITE_SIZE, the MFMA / LDS / clock
+    counters; the copy's readings give the scale from counter to bytes).
+    The order is the one ``pmc_sequence`` lists."""
     import torch
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(3)
@@ -521,6 +523,10 @@ def pmc_workload(hx) -> None:
         for _ in range(3):
             hx.gemm_i8(a, bt, b_layout="nk", row_scale=sa, col_scale=sb, out=c)
     hx.config_select(1, M, N, K, -1)
+    c32 = torch.empty((M, N), dtype=torch.int32, device=dev)
+    for _ in range(3):
+        hx.gemm_i8(a, bt, b_layout="nk", out=c32)
+    del c32, a, bt, c
     w = torch.randint(-127, 128, (11008, 4096), dtype=torch.int8, device=dev, generator=g)
     rw = hx.ResidentWeight(w, torch.rand(11008, device=dev).half() * 0.02, layout="nk")
     for m in (1, 4, 16):
@@ -538,62 +544,211 @@ def pmc_workload(hx) -> None:
         hx.softmax(xr, out=yr)
     for _ in range(3):
         hx.rms_norm(xr, gam, 1e-6, out=yr)
+    del xr, yr
+    T, H, I = 2048, 4096, 11008
+
+    def wt(k, n):
+        m = torch.randint(-127, 128, (k, n), dtype=torch.int8, device=dev, generator=g)
+        s = (torch.rand(n, device=dev) + 0.5) / (127 * (k / 3) ** 0.5)
+        return hx.ResidentWeight(m, s.half(), layout="kn")
+
+    Wg, Wu, Wd = wt(H, I), wt(H, I), wt(I, H)
+    x = torch.randn((T, H), dtype=torch.float16, device=dev, generator=g)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        hx.swiglu_ffn(x, gam, 1e-6, Wg, Wu, Wd, out=y)
+    Wg.release(); Wu.release(); Wd.release()
     torch.cuda.synchronize()
+    if keys_path:
+        Path(keys_path).write_text(json.dumps(pmc_sequence(hx)))
     print("pmc workload done", flush=True)
 
 
-def traffic_from_pmc(fetch_csv: str, write_csv: str, hx) -> str:
-    """Turn the two counter-collection CSVs of ``--pmc-workload`` runs into
-    the key=value lines of profiles/traffic.txt (bytes per launch).  Launch
-    order follows pmc_workload; each counter is scaled by its reading on the
-    64 MiB copies (bytes / counter value)."""
-    import csv
-    import re
-    import statistics
+#: kernels the counter parsers read, in pmc_workload's launch order
+MEASURED_KERNELS = r"void hx::(gemm_kernel|gemm_generic_kernel|gemv_stream_kernel|row_vec_kernel|row_kernel)<"
 
-    def per_dispatch(path):
-        rows = {}
-        for r in csv.DictReader(open(path)):
-            d = int(r["Dispatch_Id"])
-            rows.setdefault(d, [r["Kernel_Name"], 0.0])
-            rows[d][1] += float(r["Counter_Value"])
-        return [rows[d] for d in sorted(rows)]
 
-    fetch, write = per_dispatch(fetch_csv), per_dispatch(write_csv)
-    assert [k for k, _ in fetch] == [k for k, _ in write], "the two runs launched different kernels"
-    copy = 64 << 20
-    cf = [v for k, v in fetch if k == "__amd_rocclr_copyBuffer"][:3]
-    cw = [v for k, v in write if k == "__amd_rocclr_copyBuffer"][:3]
-    f_scale = copy / 1024 / statistics.median(cf)   # counter unit is KiB
-    w_scale = copy / 1024 / statistics.median(cw)
-    measured = re.compile(r"void hx::(gemm_kernel|gemm_generic_kernel|gemv_stream_kernel|row_vec_kernel|"
-                          r"row_kernel)<")
-    seq = [(k, f * f_scale * 1024 + w * w_scale * 1024) for (k, f), (_, w) in zip(fetch, write)
-           if measured.match(k)]
-    lines = [f"# HBM bytes per launch = FETCH_SIZE*{f_scale:.4f} + WRITE_SIZE*{w_scale:.4f} (KiB -> bytes)",
-             f"# scale factors: 64 MiB copy read FETCH_SIZE {statistics.median(cf):.1f} KiB, "
-             f"WRITE_SIZE {statistics.median(cw):.1f} KiB"]
-    pos = 0
-
-    def take(n):
-        nonlocal pos
-        vals = seq[pos:pos + n]
-        pos += n
-        return vals
-
-    def fill(key, vals):
-        assert len({k for k, _ in vals}) == 1, f"{key}: mixed kernels {vals}"
-        lines.append(f"{key}={int(statistics.median(v for _, v in vals))}  # {vals[0][0].split('(')[0]}")
-
+def pmc_sequence(hx):
+    """(key, launches) of the measured kernels in pmc_workload's order; a
+    key repeated across an interleaved group (the FFN block's three kernels
+    per call) is listed per call."""
+    seq = []
     for idx in range(hx.config_count(1)):
-        fill(f"gemm_i8_4096_dequant_f16:{hx.config_get(1, idx)['name']}", take(3))
+        seq.append((f"gemm_i8_4096_dequant_f16:{hx.config_get(1, idx)['name']}", 3))
+    head = hx.config_get(1, hx.config_lookup(1, 4096, 4096, 4096))["name"]
+    seq.append((f"gemm_i8_4096_i32:{head}", 3))
     for m in (1, 4, 16):
         for idx in range(hx.config_count(6)):
-            fill(f"gemv_w8a16_m{m}:{hx.config_get(6, idx)['name']}", take(3))
-    fill("softmax_f16_8192x4096", take(3))
-    fill("rmsnorm_f16_8192x4096", take(3))
+            seq.append((f"gemv_w8a16_m{m}:{hx.config_get(6, idx)['name']}", 3))
+    seq += [("softmax_f16_8192x4096", 3), ("rmsnorm_f16_8192x4096", 3)]
+    gu = hx.config_get(5, hx.config_lookup(5, 2048, 11008, 4096))["name"]
+    dn = hx.config_get(4, hx.config_lookup(4, 2048, 4096, 11008))["name"]
+    for _ in range(3):
+        seq += [("ffn_rmsnorm_2048x4096", 1), (f"ffn_gate_up:{gu}", 1), (f"ffn_down:{dn}", 1)]
+    return seq
+
+
+def _per_dispatch(path):
+    """{dispatch id: (kernel name, {counter: summed value}, row)} of a
+    rocprofv3 counter-collection CSV (values summed over dimensions)."""
+    import csv
+    rows = {}
+    for r in csv.DictReader(open(path)):
+        d = int(r["Dispatch_Id"])
+        ent = rows.setdefault(d, [r["Kernel_Name"], {}, r])
+        ent[1][r["Counter_Name"]] = ent[1].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    return [rows[d] for d in sorted(rows)]
+
+
+def _group(keys, dispatches):
+    """Map the measured dispatches onto the (key, launches) sequence that
+    pmc_workload recorded."""
+    import re
+    measured = re.compile(MEASURED_KERNELS)
+    seq = [d for d in dispatches if measured.match(d[0])]
+    out, pos = {}, 0
+    for key, n in keys:
+        vals = seq[pos:pos + n]
+        pos += n
+        assert len(vals) == n and len({v[0] for v in vals}) == 1, f"{key}: {[v[0][:60] for v in vals]}"
+        out.setdefault(key, []).extend(vals)
     assert pos == len(seq), f"{len(seq) - pos} unmatched launches"
+    return out
+
+
+def traffic_from_pmc(fetch_csv: str, write_csv: str, keys_json: str) -> str:
+    """Turn the two counter-collection CSVs of ``--pmc-workload`` runs into
+    the key=value lines of profiles/traffic.txt (bytes per launch).  Each
+    counter is scaled by its reading on the 64 MiB copies (bytes / counter
+    value)."""
+    import statistics
+    fetch, write = _per_dispatch(fetch_csv), _per_dispatch(write_csv)
+    assert [k for k, _, _ in fetch] == [k for k, _, _ in write], "the two runs launched different kernels"
+    copy = 64 << 20
+    cf = [v["FETCH_SIZE"] for k, v, _ in fetch if k == "__amd_rocclr_copyBuffer"][:3]
+    cw = [v["WRITE_SIZE"] for k, v, _ in write if k == "__amd_rocclr_copyBuffer"][:3]
+    f_scale = copy / 1024 / statistics.median(cf)   # counter unit is KiB
+    w_scale = copy / 1024 / statistics.median(cw)
+    merged = [(k, {"bytes": f["FETCH_SIZE"] * f_scale * 1024 + w["WRITE_SIZE"] * w_scale * 1024}, r)
+              for (k, f, r), (_, w, _) in zip(fetch, write)]
+    lines = ["# Commands: rocprofv3 --pmc FETCH_SIZE -d F -o run --output-format csv -- python3 bench.py "
+             "--pmc-workload --pmc-keys K; the same with WRITE_SIZE into W; then python bench.py --traffic-from "
+             "F/run_counter_collection.csv W/run_counter_collection.csv K",
+             f"# HBM bytes per launch = FETCH_SIZE*{f_scale:.4f} + WRITE_SIZE*{w_scale:.4f} (KiB -> bytes)",
+             f"# scale factors: 64 MiB copy read FETCH_SIZE {statistics.median(cf):.1f} KiB, "
+             f"WRITE_SIZE {statistics.median(cw):.1f} KiB"]
+    for key, vals in _group(json.loads(Path(keys_json).read_text()), merged).items():
+        lines.append(f"{key}={int(statistics.median(v[1]['bytes'] for v in vals))}  # {vals[0][0].split('(')[0]}")
     return "\n".join(lines) + "\n"
+
+
+def mfma_from_pmc(pmc_csv: str, keys_json: str, command: str) -> str:
+    """Markdown summary of the MFMA / LDS / clock counters of a
+    ``--pmc-workload`` run: per kernel, the MFMA-busy fraction of all SIMD
+    cycles (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE per XCC times the
+    SIMD count), the mean engine clock (GRBM_GUI_ACTIVE per XCC over the
+    dispatch's duration), MFMA ops counted by the hardware against the
+    algorithmic count, and LDS bank-conflict cycles over LDS-active
+    cycles."""
+    import statistics
+    disp = _per_dispatch(pmc_csv)
+    xcc, simds = 8, 256 * 4
+    algo = {"gemm_i8_4096": 2.0 * 4096 ** 3, "ffn_gate_up": 2 * 2.0 * 2048 * 4096 * 11008,
+            "ffn_down": 2.0 * 2048 * 4096 * 11008}
+    lines = ["# MFMA utilisation, clock and LDS conflicts per kernel (rocprofv3 --pmc)", "",
+             f"Command: `{command}`", "",
+             "Per kernel, the median over its launches. MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / "
+             "(GRBM_GUI_ACTIVE / 8 XCDs x 1024 SIMDs); clock = GRBM_GUI_ACTIVE / 8 / duration; "
+             "MOPS x 512 = the operations the MFMA units counted (I8 or F16 MOPS); LDS conflict = "
+             "SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE.", "",
+             "| kernel (workload:config) | duration us | clock GHz | MFMA busy | counted ops / algorithmic | "
+             "LDS conflict |", "|---|---:|---:|---:|---:|---:|"]
+    for key, vals in _group(json.loads(Path(keys_json).read_text()), disp).items():
+        if not (key.startswith("gemm_i8_4096") or key.startswith("ffn_gate") or key.startswith("ffn_down")):
+            continue
+        rec = []
+        for name, c, row in vals:
+            d_ns = int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
+            gui = c.get("GRBM_GUI_ACTIVE", 0.0) / xcc
+            busy = c.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / (gui * simds) if gui else float("nan")
+            ops = 512.0 * (c.get("SQ_INSTS_VALU_MFMA_MOPS_I8", 0.0) + c.get("SQ_INSTS_VALU_MFMA_MOPS_F16", 0.0))
+            lds = (c.get("SQ_LDS_BANK_CONFLICT", 0.0) / c["SQ_LDS_IDX_ACTIVE"]
+                   if c.get("SQ_LDS_IDX_ACTIVE") else float("nan"))
+            rec.append((d_ns / 1e3 if d_ns else float("nan"), gui / d_ns if d_ns else float("nan"), busy, ops, lds))
+        med = [statistics.median(r[i] for r in rec) for i in range(5)]
+        base = next((v for k, v in algo.items() if key.startswith(k)), None)
+        ratio = f"{med[3] / base:.3f}" if base else "-"
+        lines.append(f"| {key} | {med[0]:.1f} | {med[1]:.3f} | {100 * med[2]:.1f}% | {ratio} | {100 * med[4]:.2f}% |")
+    return "\n".join(lines) + "\n"
+
+
+def ceilings() -> dict:
+    """What this box sustains, timed with HIP events over back-to-back
+    launches (the way every kernel of the bench line is timed) using the
+    probes of libhxprobe.so: the launch period of an empty kernel, a
+    streaming read and a copy (rotating over copies larger than the 256 MB
+    MALL, best of a sweep of grid sizes), and int8 MFMA issue on register
+    operands with LDS reads (6 per 8 MFMAs is the GEMM's 128x64 wave tile)
+    and L2-resident global loads beside it."""
+    import torch
+    lib = ctypes.CDLL(str(ROOT / "hexagon-mlir_amd" / "libhxprobe.so"))
+    vp, i64, ci = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    lib.hxp_empty.argtypes = [vp]
+    lib.hxp_read.argtypes = [vp, i64, ci, vp, vp]
+    lib.hxp_copy.argtypes = [vp, vp, i64, ci, vp]
+    lib.hxp_mfma_i8.argtypes = [ci, ci, ci, ci, vp, vp, ctypes.POINTER(ctypes.c_double), vp]
+    dev = torch.device("cuda:0")
+    stream = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)  # noqa: E731
+    out = {}
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device=dev)
+    ms, _ = event_timed([lambda: lib.hxp_empty(stream())], 2000)
+    out["empty_launch_period_us"] = round(ms * 1e3, 3)
+
+    def sweep(label, nbytes, fn_of):
+        best = None
+        for blocks in (512, 1024, 2048, 4096, 8192):
+            calls = fn_of(blocks)
+            ms, _ = event_timed(calls, 200)
+            if best is None or ms < best[0]:
+                best = (ms, blocks)
+        ms, blocks = best
+        out[label] = {"bytes": nbytes, "us_per_launch": round(ms * 1e3, 3),
+                      "GB_s": round(nbytes / (ms * 1e-3) / 1e9, 1), "blocks": blocks}
+
+    for mb in (45, 64, 256):
+        nbytes = (45_140_992 if mb == 45 else mb << 20)
+        copies = max(1, min(16, -(-(600 << 20) // nbytes)))
+        bufs = [torch.ones(nbytes // 4, dtype=torch.int32, device=dev) for _ in range(copies)]
+        sweep(f"read_{mb}MB", nbytes, lambda blocks, bufs=bufs, nbytes=nbytes: [
+            (lambda b=b: lib.hxp_read(ctypes.c_void_p(b.data_ptr()), nbytes, blocks,
+                                      ctypes.c_void_p(sink.data_ptr()), stream())) for b in bufs])
+        del bufs
+    nbytes = 64 << 20
+    pairs = [(torch.ones(nbytes // 4, dtype=torch.int32, device=dev), torch.empty(nbytes // 4, dtype=torch.int32, device=dev))
+             for _ in range(6)]
+    sweep("copy_64MiB_in_64MiB_out", 2 * nbytes, lambda blocks: [
+        (lambda s_=s_, d_=d_: lib.hxp_copy(ctypes.c_void_p(s_.data_ptr()), ctypes.c_void_p(d_.data_ptr()), nbytes,
+                                           blocks, stream())) for s_, d_ in pairs])
+    del pairs
+    ops = ctypes.c_double()
+    gbuf = torch.ones(1 << 18, dtype=torch.int32, device=dev)  # 1 MiB, L2-resident
+    for nr, ng in ((0, 0), (2, 0), (4, 0), (6, 0), (0, 2), (0, 4), (0, 6), (4, 2), (2, 4)):
+        call = lambda nr=nr, ng=ng: lib.hxp_mfma_i8(  # noqa: E731
+            256, 4000, nr, ng, ctypes.c_void_p(gbuf.data_ptr()), ctypes.c_void_p(sink.data_ptr()),
+            ctypes.byref(ops), stream())
+        ms, _ = event_timed([call], 20)
+        out[f"mfma_i8_{nr}_lds_{ng}_vmem_per_8"] = {
+            "us_per_launch": round(ms * 1e3, 2), "TOPS": round(ops.value / (ms * 1e-3) / 1e12, 1),
+            "frac_of_5000": round(ops.value / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
+    lib.hxp_mfma4_i8.argtypes = [ci, ci, ci, vp, ctypes.POINTER(ctypes.c_double), vp]
+    for nr in (0, 4, 8):
+        call = lambda nr=nr: lib.hxp_mfma4_i8(256, 4000, nr, ctypes.c_void_p(sink.data_ptr()),  # noqa: E731
+                                              ctypes.byref(ops), stream())
+        ms, _ = event_timed([call], 20)
+        out[f"mfma_i8_4waves_{nr}_lds_per_16"] = {
+            "us_per_launch": round(ms * 1e3, 2), "TOPS": round(ops.value / (ms * 1e-3) / 1e12, 1),
+            "frac_of_5000": round(ops.value / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
+    return out
 
 
 def main() -> int:
@@ -607,21 +762,30 @@ def main() -> int:
                     help="time the untuned default configs (skip the tile search)")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="launch each benchmarked kernel a few times for rocprofv3 --pmc")
-    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
-                    help="write profiles/traffic.txt from two --pmc-workload counter CSVs and exit")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="time the libhxprobe probes (launch gap, read, copy, MFMA issue), print JSON, exit")
+    ap.add_argument("--pmc-keys", metavar="JSON",
+                    help="with --pmc-workload: write the launch sequence the counter parsers read")
+    ap.add_argument("--traffic-from", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "KEYS_JSON"),
+                    help="print the traffic.txt lines of two --pmc-workload counter CSVs and exit")
+    ap.add_argument("--mfma-from", nargs=3, metavar=("PMC_CSV", "KEYS_JSON", "COMMAND"),
+                    help="print the MFMA counter summary of a --pmc-workload counter CSV (and the "
+                         "command that made it) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(multi-GPU sharding is designed, not built: one GPU's shard is what this bench measures)", file=sys.stderr)
         return 2
 
+    if args.traffic_from:
+        print(traffic_from_pmc(*args.traffic_from), end="")
+        return 0
+    if args.mfma_from:
+        print(mfma_from_pmc(*args.mfma_from), end="")
+        return 0
     import torch
     from __graft_entry__ import load_package
     hx = load_package()
-    if args.traffic_from:
-        (PROFILES / "traffic.txt").write_text(traffic_from_pmc(*args.traffic_from, hx))
-        print((PROFILES / "traffic.txt").read_text())
-        return 0
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
@@ -629,8 +793,11 @@ def main() -> int:
     if rc != 0:
         print(f"bench.py: hx_init failed: {hx._abi.last_error()}", file=sys.stderr)
         return 1
+    if args.ceilings:
+        print(json.dumps(ceilings()), flush=True)
+        return 0
     if args.pmc_workload:
-        pmc_workload(hx)
+        pmc_workload(hx, args.pmc_keys)
         return 0
 
     log("[bench] int8 GEMM 4096^3 + dequant")

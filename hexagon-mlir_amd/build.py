@@ -96,7 +96,25 @@ def build(verbose: bool = False) -> Path:
         sys.stderr.write(r.stdout + r.stderr)
         raise RuntimeError("link of libhxmi.so failed")
     os.replace(tmp, OUT)
+    build_probe()
     return OUT
+
+
+PROBE_SRC = CSRC / "probe" / "hx_probe.hip"
+PROBE_OUT = PKG / "libhxprobe.so"
+
+
+def build_probe() -> Path:
+    """libhxprobe.so: the measurement probes bench.py --ceilings times
+    (empty launch, streaming read, copy, MFMA issue); not part of the hx ABI."""
+    tmp = PROBE_OUT.with_suffix(".so.tmp")
+    cmd = [HIPCC, *COMMON, "-shared", str(PROBE_SRC), "-o", str(tmp)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError("hipcc failed on the probes")
+    os.replace(tmp, PROBE_OUT)
+    return PROBE_OUT
 
 
 if __name__ == "__main__":

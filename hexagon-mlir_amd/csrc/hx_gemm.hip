@@ -179,8 +179,9 @@ const char* gemm_fast_refusal(int mode, const GemmArgs& a) {
   if (!al16(a.a) || !al16(a.b) || (a.b2 && !al16(a.b2))) return "unaligned-base";
   if ((a.lda * ea) % 16 != 0 || (a.ldb * eb) % 16 != 0) return "row-stride";
   if ((a.K * ea) % 16 != 0 || (a.K * eb) % 16 != 0) return "k-granularity";
-  // 32-bit buffer offsets inside one tile's row range
+  // 32-bit buffer offsets inside one tile's row range (operands and output)
   if ((int64_t)256 * a.lda * ea >= ((int64_t)1 << 31)) return "offset-range";
+  if ((int64_t)256 * a.ldc * 4 >= ((int64_t)1 << 31)) return "offset-range";
   if (a.b_kn) {
     // [K][N] B (f16 / bf16): whole 16-byte chunks of a row, every row of k
     // addressed with 32-bit offsets

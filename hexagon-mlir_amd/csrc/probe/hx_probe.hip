@@ -1,0 +1,156 @@
+// hx_probe.hip -- measurement probes for bench.py's --ceilings mode (built
+// into libhxprobe.so, not part of the hx ABI).  They measure what this box
+// sustains, as the denominators the kernels' rooflines are read against:
+//   * the period of back-to-back launches of an empty kernel (the launch
+//     gap every short kernel pays when timed back to back);
+//   * a streaming read and a copy of a given size (16-byte non-temporal
+//     loads, grid-stride), the HBM ceiling of the GEMV and the row ops;
+//   * v_mfma_i32_32x32x32_i8 issued back to back on register operands (the
+//     MFMA ceiling at the clock the chip holds under that load), alone and
+//     with the LDS operand reads of the GEMM's 128x64 wave tile beside it.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+__global__ void probe_empty_kernel() {}
+
+// Streaming read: XOR of every 16-byte word; one word per block reaches
+// memory only if the XOR hits a magic value (it never does for the fills
+// used), so the loads cannot be dropped.
+__global__ void __launch_bounds__(256) probe_read_kernel(const v4i* __restrict__ p, int64_t n16, int* sink) {
+  v4i acc = v4i{0, 0, 0, 0};
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (int64_t)gridDim.x * 256)
+    acc ^= __builtin_nontemporal_load(p + i);
+  const int x = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+  if (x == 0x5eed1234) sink[blockIdx.x] = x;
+}
+
+__global__ void __launch_bounds__(256) probe_copy_kernel(const v4i* __restrict__ s, v4i* __restrict__ d,
+                                                         int64_t n16) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (int64_t)gridDim.x * 256)
+    __builtin_nontemporal_store(__builtin_nontemporal_load(s + i), d + i);
+}
+
+// 8 independent int8 MFMA chains per wave, `iters` rounds of 8 MFMAs; NR
+// 16-byte LDS reads per round beside them (6 is the GEMM's 128x64 wave
+// tile), and NG coalesced 16-byte-per-lane loads of an L2-resident 1 MiB
+// buffer (operands that bypass LDS).  The reads' results feed the next
+// round's operands, so they cannot be dropped; LDS lanes read 16 bytes at an
+// 80-byte stride (conflict-free).
+template <int NR, int NG>
+__global__ void __launch_bounds__(512) probe_mfma_kernel(int iters, const v4i* __restrict__ g, int* out) {
+  __shared__ v4i tile[NR ? 4096 : 1];
+  const int lane = threadIdx.x & 63;
+  v4i a[2], b[4];
+  for (int i = 0; i < 2; ++i) a[i] = v4i{lane + i, 1, 2, 3};
+  for (int j = 0; j < 4; ++j) b[j] = v4i{j, lane, 5, 7};
+  if constexpr (NR > 0) {
+    for (int i = threadIdx.x; i < 4096; i += 512) tile[i] = v4i{i, i + 1, i + 2, i + 3};
+    __syncthreads();
+  }
+  v16i acc[8];
+  for (int t = 0; t < 8; ++t) acc[t] = v16i{};
+  const int base = (threadIdx.x * 5) & 4095;
+  const int gw = (int)(blockIdx.x * 8 + (threadIdx.x >> 6)) * 97;
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[4 * i + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[4 * i + j], 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const v4i t = tile[(base + 64 * r + it) & 4095];
+      if (r % 6 < 2) a[r % 6] ^= t;
+      else b[r % 6 - 2] ^= t;
+    }
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+      const v4i t = g[((gw + it * NG + q) * 64 + lane) & 65535];
+      b[(q + 2) & 3] ^= t;
+    }
+  }
+  int s = 0;
+  for (int t = 0; t < 8; ++t)
+    for (int r = 0; r < 16; ++r) s += acc[t][r];
+  if (s == 0x5eed1234) out[blockIdx.x] = s;
+}
+
+// One wave per SIMD (4 per CU) with a 128x128 wave tile: 16 independent
+// MFMA chains (256 accumulator registers), `iters` rounds of 16 MFMAs with NR
+// LDS reads per round (8 is the tile's operand traffic: 4 A + 4 B).
+template <int NR>
+__global__ void __launch_bounds__(256) probe_mfma4_kernel(int iters, int* out) {
+  __shared__ v4i tile[4096];
+  const int lane = threadIdx.x & 63;
+  v4i a[4], b[4];
+  for (int i = 0; i < 4; ++i) a[i] = v4i{lane + i, 1, 2, 3};
+  for (int j = 0; j < 4; ++j) b[j] = v4i{j, lane, 5, 7};
+  for (int i = threadIdx.x; i < 4096; i += 256) tile[i] = v4i{i, i + 1, i + 2, i + 3};
+  __syncthreads();
+  v16i acc[16];
+  for (int t = 0; t < 16; ++t) acc[t] = v16i{};
+  const int base = (threadIdx.x * 5) & 4095;
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[4 * i + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[4 * i + j], 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const v4i t = tile[(base + 64 * r + it) & 4095];
+      if (r < 4) a[r] ^= t;
+      else b[r - 4] ^= t;
+    }
+  }
+  int s = 0;
+  for (int t = 0; t < 16; ++t)
+    for (int r = 0; r < 16; ++r) s += acc[t][r];
+  if (s == 0x5eed1234) out[blockIdx.x] = s;
+}
+
+extern "C" {
+// blocks x 256 threads (4 waves, 128x128 wave tiles), 0, 4 or 8 LDS reads
+// per 16 MFMAs
+int hxp_mfma4_i8(int blocks, int iters, int lds_reads, int* out, double* ops, hipStream_t s) {
+  if (lds_reads == 0) probe_mfma4_kernel<0><<<blocks, 256, 0, s>>>(iters, out);
+  else if (lds_reads == 4) probe_mfma4_kernel<4><<<blocks, 256, 0, s>>>(iters, out);
+  else if (lds_reads == 8) probe_mfma4_kernel<8><<<blocks, 256, 0, s>>>(iters, out);
+  else return -1;
+  *ops = (double)blocks * 4 /*waves*/ * iters * 16 /*mfma*/ * 65536.0;
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int hxp_empty(hipStream_t s) {
+  probe_empty_kernel<<<1, 64, 0, s>>>();
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+int hxp_read(const void* p, int64_t bytes, int blocks, int* sink, hipStream_t s) {
+  probe_read_kernel<<<blocks, 256, 0, s>>>((const v4i*)p, bytes / 16, sink);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+int hxp_copy(const void* src, void* dst, int64_t bytes, int blocks, hipStream_t s) {
+  probe_copy_kernel<<<blocks, 256, 0, s>>>((const v4i*)src, (v4i*)dst, bytes / 16);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+// blocks x 512 threads (8 waves): `lds_reads` LDS reads and `global_loads`
+// buffer loads (of `g`, 1 MiB) per 8 MFMAs, for the combinations below;
+// returns int8 ops per launch in *ops
+int hxp_mfma_i8(int blocks, int iters, int lds_reads, int global_loads, const void* g, int* out, double* ops,
+                hipStream_t s) {
+  const v4i* gv = (const v4i*)g;
+#define HXP_CASE(R, G)                                                            \
+  if (lds_reads == R && global_loads == G) {                                      \
+    probe_mfma_kernel<R, G><<<blocks, 512, 0, s>>>(iters, gv, out);               \
+    *ops = (double)blocks * 8 /*waves*/ * iters * 8 /*mfma*/ * 65536.0;           \
+    return hipGetLastError() == hipSuccess ? 0 : -1;                              \
+  }
+  HXP_CASE(0, 0) HXP_CASE(2, 0) HXP_CASE(4, 0) HXP_CASE(6, 0)
+  HXP_CASE(0, 2) HXP_CASE(0, 4) HXP_CASE(0, 6) HXP_CASE(4, 2) HXP_CASE(2, 4)
+#undef HXP_CASE
+  return -1;
+}
+}
