@@ -144,6 +144,28 @@ static int part_get(hipStream_t s, size_t bytes, float** out) {
   return HX_OK;
 }
 
+// f32 operands quantised to f16 (hx_matmul): a third per-stream region, so
+// that the workspace the f16 call then carves can grow without moving them.
+static std::map<std::pair<int, hipStream_t>, Workspace> g_quant;
+static int quant_get(hipStream_t s, size_t bytes, char** out) {
+  int dev;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(g_mu);
+  Workspace& w = g_quant[{dev, s}];
+  if (w.bytes < bytes) {
+    size_t nb = (bytes + 4095) & ~(size_t)4095;
+    HX_HIP_TRY(hipStreamSynchronize(s));
+    if (w.buf) HX_HIP_TRY(hipFree(w.buf));
+    w.buf = nullptr;
+    w.bytes = 0;
+    if (hipMalloc(&w.buf, nb) != hipSuccess) return fail(HX_ERR_NOMEM, "f32 operand quantisation of %zu bytes", nb);
+    w.bytes = nb;
+  }
+  *out = w.buf;
+  return HX_OK;
+}
+
 // Carve 256-byte aligned sub-buffers out of one workspace region.
 struct Carver {
   size_t used = 0;
@@ -543,11 +565,43 @@ extern "C" int hx_matmul(const hx_memref2d* a, int a_dtype, const hx_memref2d* b
                          const hx_memref2d* residual, int residual_dtype, hx_memref2d* c,
                          int c_dtype, hx_stream_t stream) {
   hipStream_t s = (hipStream_t)stream;
+  if (a_dtype == HX_F32 || (b_dtype == HX_F32 && (a_dtype == HX_F16 || a_dtype == HX_F32))) {
+    // f32 operands are quantised to f16 as the reference's f32 pack does
+    // ((x + 0) rounded to nearest even, -0 -> +0; QHB/bin/runtime/hmx/src/
+    // HMXLayout.c:257-340), then multiplied on the f16 path with binary32
+    // accumulation.  f32 A goes with an f16, f32 or int8 B; f32 B with f16
+    // or f32 A.
+    if (a_dtype == HX_F32 && b_dtype != HX_F32 && b_dtype != HX_F16 && b_dtype != HX_I8)
+      return fail(HX_ERR_DTYPE, "hx_matmul: a=f32 with b=%s (f32, f16 or i8)", dt_name(b_dtype));
+    View2 qa, qb;
+    int rc;
+    if ((rc = view2(a, a_dtype, "a", &qa)) || (rc = view2(b, b_dtype, "b", &qb))) return rc;
+    Carver cv;
+    const size_t off_qa = a_dtype == HX_F32 ? cv.take((size_t)qa.rows * qa.cols * 2) : 0;
+    const size_t off_qb = b_dtype == HX_F32 ? cv.take((size_t)qb.rows * qb.cols * 2) : 0;
+    char* q = nullptr;
+    if (cv.used && (rc = quant_get(s, cv.used, &q))) return rc;
+    hx_memref2d a16 = *a, b16 = *b;
+    if (a_dtype == HX_F32) {
+      rc = map_internal(launch_f32_to_f16_rne((const float*)qa.p, qa.ld, (uint16_t*)(q + off_qa), qa.rows, qa.cols, s),
+                        "f32 quantisation");
+      if (rc) return rc;
+      a16 = hx_memref2d{q + off_qa, q + off_qa, 0, {qa.rows, qa.cols}, {qa.cols, 1}};
+    }
+    if (b_dtype == HX_F32) {
+      rc = map_internal(launch_f32_to_f16_rne((const float*)qb.p, qb.ld, (uint16_t*)(q + off_qb), qb.rows, qb.cols, s),
+                        "f32 quantisation");
+      if (rc) return rc;
+      b16 = hx_memref2d{q + off_qb, q + off_qb, 0, {qb.rows, qb.cols}, {qb.cols, 1}};
+    }
+    return hx_matmul(&a16, a_dtype == HX_F32 ? HX_F16 : a_dtype, &b16, b_dtype == HX_F32 ? HX_F16 : b_dtype,
+                     b_layout, col_scale, scale_dtype, residual, residual_dtype, c, c_dtype, stream);
+  }
   int op;
   if (a_dtype == HX_F16 && b_dtype == HX_F16) op = HX_OP_MATMUL_F16;
   else if (a_dtype == HX_BF16 && b_dtype == HX_BF16) op = HX_OP_MATMUL_BF16;
   else if (a_dtype == HX_F16 && b_dtype == HX_I8) op = HX_OP_MATMUL_W8;
-  else return fail(HX_ERR_DTYPE, "hx_matmul: a=%s b=%s (f16.f16, bf16.bf16 or f16.i8)",
+  else return fail(HX_ERR_DTYPE, "hx_matmul: a=%s b=%s (f16.f16, bf16.bf16, f16.i8, or f32 with f16/f32/i8)",
                    dt_name(a_dtype), dt_name(b_dtype));
   if (c_dtype != HX_F16 && c_dtype != HX_BF16 && c_dtype != HX_F32)
     return fail(HX_ERR_DTYPE, "hx_matmul: c dtype %s", dt_name(c_dtype));
@@ -942,6 +996,26 @@ extern "C" int hx_weight_register(const hx_memref2d* w, int w_dtype, int w_layou
   if (!out) return fail(HX_ERR_ARG, "hx_weight_register: null out");
   free_deferred();
   *out = nullptr;
+  if (w_dtype == HX_F32) {
+    // an f32 weight is quantised to f16 first, as the reference's host
+    // prepack does ((w + 0) rounded to nearest even, -0 -> +0;
+    // QHB/backend/hmx_weight_prepack.py:185-212), and registered as f16
+    View2 v;
+    int rc = view2(w, HX_F32, "w", &v);
+    if (rc) return rc;
+    uint16_t* tmp = nullptr;
+    if (v.rows * v.cols > 0 && hipMalloc((void**)&tmp, (size_t)v.rows * v.cols * 2) != hipSuccess)
+      return fail(HX_ERR_NOMEM, "hx_weight_register: f32 quantisation buffer");
+    rc = map_internal(launch_f32_to_f16_rne((const float*)v.p, v.ld, tmp, v.rows, v.cols, s), "f32 quantisation");
+    if (!rc) {
+      hx_memref2d w16{tmp, tmp, 0, {v.rows, v.cols}, {v.cols, 1}};
+      rc = hx_weight_register(&w16, HX_F16, w_layout, scale, scale_dtype, stream, out);
+    }
+    // registration synchronized the stream: the f16 copy is no longer read
+    (void)hipStreamSynchronize(s);
+    if (tmp) (void)hipFree(tmp);
+    return rc;
+  }
   if (w_dtype != HX_I8 && w_dtype != HX_F16 && w_dtype != HX_BF16)
     return fail(HX_ERR_DTYPE, "hx_weight_register: dtype %s", dt_name(w_dtype));
   if (w_layout != HX_LAYOUT_KN && w_layout != HX_LAYOUT_NK) return fail(HX_ERR_ARG, "hx_weight_register: layout");

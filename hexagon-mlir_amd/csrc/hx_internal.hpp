@@ -152,6 +152,10 @@ int launch_attention(int dtype, bool causal, const AttnArgs& a, hipStream_t s);
 // dst[c][r] = src[r][c] for a rows x cols matrix of 1/2/4-byte elements.
 int launch_transpose(const void* src, int64_t lds, void* dst, int64_t ldd, int64_t rows,
                      int64_t cols, int elem_bytes, hipStream_t s);
+// f32 [rows][cols] (row stride lds) -> dense f16, (x + 0) rounded to
+// nearest even (-0 becomes +0): the reference's f32 pack quantisation.
+int launch_f32_to_f16_rne(const float* src, int64_t lds, uint16_t* dst, int64_t rows, int64_t cols,
+                          hipStream_t s);
 // f16 -> f32 widening of a vector (scales).
 int launch_f16_to_f32(const void* src, float* dst, int64_t n, hipStream_t s);
 // 64-bit content hash of a byte range (order-dependent, deterministic).

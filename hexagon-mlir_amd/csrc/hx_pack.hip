@@ -126,6 +126,32 @@ int launch_f16_to_f32(const void* src, float* dst, int64_t n, hipStream_t s) {
   return HXI_OK;
 }
 
+// f32 -> f16 quantisation of a [rows][cols] matrix (row stride lds) into a
+// dense [rows][cols] f16 matrix: (x + 0) rounded to nearest even, so -0
+// becomes +0 and values beyond the f16 range become infinities.  This is
+// the quantisation the reference's f32 pack applies to activations and
+// weights before the fp16 engine sees them (QHB/bin/runtime/hmx/src/
+// HMXLayout.c:257-340, the qf32 add of zero then the RNE narrowing;
+// QHB/backend/hmx_weight_prepack.py:185-212 states the same rule).
+__global__ void __launch_bounds__(256) f32_to_f16_rne_kernel(const float* __restrict__ src, int64_t lds,
+                                                             uint16_t* __restrict__ dst, int64_t rows,
+                                                             int64_t cols) {
+  const int64_t total = rows * cols;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / cols, c = i - r * cols;
+    dst[i] = f32_to_f16_bits(src[r * lds + c] + 0.0f);
+  }
+}
+
+int launch_f32_to_f16_rne(const float* src, int64_t lds, uint16_t* dst, int64_t rows, int64_t cols,
+                          hipStream_t s) {
+  if (rows <= 0 || cols <= 0) return HXI_OK;
+  int64_t blocks = (rows * cols + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  f32_to_f16_rne_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(src, lds, dst, rows, cols);
+  return HXI_OK;
+}
+
 // Content hash: H = sum over 8-byte words i of mix(word_i + (i+1)*phi), plus
 // the tail bytes folded into one last word.  The per-word mix includes the
 // position, so permutations change H; the sum is order-free, so the result

@@ -106,7 +106,10 @@ def matmul(a: torch.Tensor, b: torch.Tensor, *, b_layout: str = "kn",
     """C = A . B (* col_scale) (+ residual), binary32 accumulation.
 
     a: [M, K] f16/bf16.  b: [K, N] ("kn") or [N, K] ("nk"), same dtype as a,
-    or int8 with an f16 a (W8A16).  out dtype defaults to a's dtype."""
+    or int8 with an f16 a (W8A16).  f32 operands (with f16 / f32 partners,
+    or an f32 a with an int8 b) are quantised to f16 first ((x + 0) rounded
+    to nearest even), as the reference's f32 pack does.  out dtype defaults
+    to a's dtype."""
     lay = _LAYOUT[b_layout]
     M = a.shape[0]
     N = b.shape[1] if lay == LAYOUT_KN else b.shape[0]
@@ -222,7 +225,8 @@ class ResidentWeight:
                                         dtype_code(scale) if scale is not None else 0, _stream(),
                                         ctypes.byref(handle)), "hx_weight_register")
         self.handle = handle.value
-        self.dtype = w.dtype
+        # an f32 weight is held as its f16 quantisation
+        self.dtype = torch.float16 if w.dtype == torch.float32 else w.dtype
 
     def info(self) -> dict:
         k, n, dt, rc = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int(), ctypes.c_int()

@@ -443,3 +443,67 @@ def test_matmul_w8a16_split_k_scale_residual(hx, dev, cfg_name):
         [(rc["plan"], rc["config"], rc["reason"]) for rc in recs]
     want = oracle.matmul(x, w, b_trans=True, scale_n=s.astype(np.float32), residual=r)
     assert_close(to_np(y).astype(np.float32), want.astype(np.float32), 1e-2, 2e-3, f"w8a16 split {cfg_name}")
+
+
+def _quant16(x):
+    """The reference's f32 pack quantisation: (x + 0) rounded to nearest even."""
+    return (np.asarray(x, np.float32) + np.float32(0.0)).astype(np.float16)
+
+
+@pytest.mark.parametrize("a_dt,b_dt,layout", [("f32", "f32", "kn"), ("f32", "f16", "nk"), ("f16", "f32", "kn"),
+                                              ("f32", "f32", "nk")])
+def test_matmul_f32_operands_quantised_at_the_pack(hx, dev, a_dt, b_dt, layout):
+    """f32 operands are quantised to f16 ((x + 0), RNE) and multiplied on the
+    f16 path: the result equals the oracle's product of the quantised
+    operands within the f16 path's tolerance, on shapes that take the tiled
+    kernel (M = 300) and the decode GEMV (M = 7)."""
+    import torch
+    for M in (300, 7):
+        K, N = 512, 384
+        a32 = rng(80 + M).normal(0, 1, (M, K)).astype(np.float32)
+        b32 = rng(81 + M).normal(0, 1, (K, N) if layout == "kn" else (N, K)).astype(np.float32)
+        a = a32 if a_dt == "f32" else _quant16(a32)
+        b = b32 if b_dt == "f32" else _quant16(b32)
+        got = to_np(hx.matmul(to_dev(a, dev), to_dev(b, dev), b_layout=layout, out_dtype=torch.float32))
+        want = oracle.matmul(_quant16(a32), _quant16(b32), b_trans=(layout == "nk"), out_dtype=np.float32)
+        assert_close(got, want, 1e-3, 1e-3, f"f32 operands {a_dt}.{b_dt} {layout} M={M}")
+
+
+def test_f32_quantisation_special_values(hx, dev):
+    """The quantisation itself, read back through an identity product (each
+    value alone in its row, on the diagonal): ties round to even, values past
+    65504 become infinities of their sign, and tiny values land on the f16
+    subnormals or flush to zero.  (A -0 operand is not observable through a
+    product: the binary32 accumulator starts at +0.)"""
+    import torch
+    K = 256
+    vals = np.array([1.0 + 2 ** -11, 1.0 + 3 * 2 ** -11, 65504.0, 65520.0, -70000.0, 2 ** -24, 2 ** -26,
+                     3 * 2 ** -25, 0.1, -1 / 3], np.float32)
+    a = np.zeros((len(vals), K), np.float32)
+    a[np.arange(len(vals)), np.arange(len(vals))] = vals
+    eye = np.eye(K, dtype=np.float32)
+    got = to_np(hx.matmul(to_dev(a, dev), to_dev(eye, dev), b_layout="kn", out_dtype=torch.float32))
+    diag = got[np.arange(len(vals)), np.arange(len(vals))]
+    want = _quant16(vals).astype(np.float32)
+    np.testing.assert_array_equal(diag, want)
+    assert diag[3] == np.inf and diag[4] == -np.inf and diag[0] == 1.0 and diag[1] == 1.0 + 4 * 2 ** -11
+    assert diag[6] == 0.0 and diag[7] == 2 ** -24 * 2
+
+
+def test_resident_f32_weight(hx, dev):
+    """An f32 weight registers as its f16 quantisation: the resident product
+    equals the argument product of the quantised weight bit for bit, and an
+    identical f16 registration shares its handle."""
+    import torch
+    K, N = 384, 512
+    w32 = rng(85).normal(0, 0.5, (K, N)).astype(np.float32)
+    x = rng(86).normal(0, 1, (40, K)).astype(np.float16)
+    W = hx.ResidentWeight(to_dev(w32, dev), layout="kn")
+    W16 = hx.ResidentWeight(to_dev(_quant16(w32), dev), layout="kn")
+    try:
+        assert W.info()["dtype"] == 1 and W.handle == W16.handle and W.info()["refcount"] == 2
+        got = to_np(hx.matmul_resident(to_dev(x, dev), W))
+        ref = to_np(hx.matmul(to_dev(x, dev), to_dev(_quant16(w32), dev), b_layout="kn"))
+        assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+    finally:
+        W.release(); W16.release()
