@@ -80,30 +80,39 @@ __global__ void __launch_bounds__(512) probe_mfma_kernel(int iters, const v4i* _
 
 // One wave per SIMD (4 per CU) with a 128x128 wave tile: 16 independent
 // MFMA chains (256 accumulator registers), `iters` rounds of 16 MFMAs with NR
-// LDS reads per round (8 is the tile's operand traffic: 4 A + 4 B).
+// LDS reads per round (8 is the tile's operand traffic: 4 A + 4 B).  The
+// operands are double-buffered as a GEMM would hold them: a round's reads
+// land in the other register set and feed the round after the next one.
 template <int NR>
 __global__ void __launch_bounds__(256) probe_mfma4_kernel(int iters, int* out) {
   __shared__ v4i tile[4096];
   const int lane = threadIdx.x & 63;
-  v4i a[4], b[4];
-  for (int i = 0; i < 4; ++i) a[i] = v4i{lane + i, 1, 2, 3};
-  for (int j = 0; j < 4; ++j) b[j] = v4i{j, lane, 5, 7};
+  v4i a[2][4], b[2][4];
+  for (int s = 0; s < 2; ++s) {
+    for (int i = 0; i < 4; ++i) a[s][i] = v4i{lane + i + s, 1, 2, 3};
+    for (int j = 0; j < 4; ++j) b[s][j] = v4i{j + s, lane, 5, 7};
+  }
   for (int i = threadIdx.x; i < 4096; i += 256) tile[i] = v4i{i, i + 1, i + 2, i + 3};
   __syncthreads();
   v16i acc[16];
   for (int t = 0; t < 16; ++t) acc[t] = v16i{};
   const int base = (threadIdx.x * 5) & 4095;
-  for (int it = 0; it < iters; ++it) {
+  for (int it = 0; it < iters; it += 2) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int s = 0; s < 2; ++s) {
+      // reads for the other set, spread between this set's MFMAs
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[4 * i + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[4 * i + j], 0, 0, 0);
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      const v4i t = tile[(base + 64 * r + it) & 4095];
-      if (r < 4) a[r] ^= t;
-      else b[r - 4] ^= t;
+        for (int j = 0; j < 4; ++j) {
+          acc[4 * i + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[s][i], b[s][j], acc[4 * i + j], 0, 0, 0);
+          const int r = 4 * i + j;
+          if (r < NR) {
+            const v4i t = tile[(base + 64 * r + it + s) & 4095];
+            if (r < 4) a[s ^ 1][r] ^= t;
+            else b[s ^ 1][r - 4] ^= t;
+          }
+        }
     }
   }
   int s = 0;
