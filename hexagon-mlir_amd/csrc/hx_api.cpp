@@ -1340,12 +1340,14 @@ extern "C" int hx_config_get(int op, int index, hx_kernel_config* out) {
   int mode, epi;
   op_gemm(op, &mode, &epi);
   const GemmConfig* c = gemm_config(mode, idx[index]);
-  const int bk = mode == GM_I8 ? 128 : 64;
-  const int brow = mode == GM_F16 || mode == GM_BF16 || mode == GM_I8 ? 128 : 64;
+  // bk: K elements per stage (sb bytes of A per row); brow: bytes of B per
+  // row in one stage (the W8 weights are int8 beside f16 activations)
+  const int bk = mode == GM_I8 ? c->sb : c->sb / 2;
+  const int brow = mode == GM_W8 ? c->sb / 2 : c->sb;
   out->bm = c->bm; out->bn = c->bn; out->bk = bk;
   out->waves_m = c->wm; out->waves_n = c->wn;
-  out->lds_stages = 2; out->split_k = 1; out->col_tiles = 0;
-  out->lds_bytes = 2 * (c->bm * 128 + (epi == GE_SWIGLU ? 2 : 1) * c->bn * brow);
+  out->lds_stages = c->stages; out->split_k = c->ksplit > 1 ? c->ksplit : 1; out->col_tiles = 0;
+  out->lds_bytes = c->stages * (c->bm * c->sb + (epi == GE_SWIGLU ? 2 : 1) * c->bn * brow);
   snprintf(out->name, sizeof(out->name), "%s", c->name);
   return HX_OK;
 }

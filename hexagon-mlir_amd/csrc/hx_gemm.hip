@@ -151,11 +151,15 @@ int gemm_default_config(int mode, int epi, int64_t M, int64_t N, int64_t K) {
   // is small against the product), and needs >= 512 k per part.  Counting
   // occupancy-limited rounds instead picked 64x64 at 2048^3, where 128x128
   // measured 1.2-1.4x faster (f16 and int8).
+  const int64_t ea = mode == GM_I8 ? 1 : 2;
   for (int i = 0; i < n; ++i) {
     const GemmConfig& c = t[i].cfg;
     if (c.epi != epi) continue;
     const int ks = c.ksplit > 1 ? c.ksplit : 1;
     if (ks > 1 && K / ks < 512) continue;
+    // at least as many K stages (per part, the last one partial) as the
+    // LDS ring holds
+    if ((K / ks * ea + c.sb - 1) / c.sb < c.stages) continue;
     const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * ks;
     const int64_t per_cu_i = (tiles + cus - 1) / cus;
     const double per_cu = (double)per_cu_i;
@@ -278,9 +282,56 @@ __global__ void __launch_bounds__(256) splitk_merge_kernel(GemmArgs a, const flo
   }
 }
 
-static int64_t split_k_elems(const GemmConfig& c, const GemmArgs& a) {
-  // whole 128-byte stages of A per part
-  const int64_t bke = 64;  // f16 / bf16 A: 64 k per stage
+// Merge of an int8 K split: the int32 partials summed in order with
+// two's-complement wrap-around (integer addition is associative, so the sum
+// equals the unsplit accumulator bit for bit), then the fused epilogue's
+// dequant ((float)acc * row_scale) * col_scale, an absent scale reading as
+// 1.0, rounded to the output type; DT_I32 stores the sum.  Four columns per
+// thread with 16-byte partial loads (N % 4 == 0 on the tiled path).
+template <int OUT>
+__global__ void __launch_bounds__(256) splitk_merge_i8_kernel(GemmArgs a, const int* part, int parts) {
+  const uint32_t q = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t n4 = (uint32_t)(a.N >> 2);
+  if (q >= (uint32_t)a.M * n4) return;
+  const uint32_t m = q / n4;
+  const int64_t n = 4 * (int64_t)(q - m * n4);
+  const int64_t mn = a.M * a.N;
+  const int* p = part + (int64_t)m * a.N + n;
+  uint32_t acc[4] = {0u, 0u, 0u, 0u};
+  for (int s = 0; s < parts; ++s) {
+    const v4i v = *reinterpret_cast<const v4i*>(p + s * mn);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] += (uint32_t)v[i];
+  }
+  const int64_t o = (int64_t)m * a.ldc + n;
+  if constexpr (OUT == DT_I32) {
+    *reinterpret_cast<v4i*>(reinterpret_cast<int*>(a.c) + o) =
+        v4i{(int)acc[0], (int)acc[1], (int)acc[2], (int)acc[3]};
+  } else {
+    const float rs = a.row_scale ? a.row_scale[m] : 1.f;
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float cs = a.col_scale ? a.col_scale[n + i] : 1.f;
+      v[i] = ((float)(int)acc[i] * rs) * cs;
+    }
+    if constexpr (OUT == DT_F32) {
+      *reinterpret_cast<v4f*>(reinterpret_cast<float*>(a.c) + o) = v4f{v[0], v[1], v[2], v[3]};
+    } else if constexpr (OUT == DT_BF16) {
+      const uint32_t lo = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+      const uint32_t hi = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+      *reinterpret_cast<v2i*>(reinterpret_cast<uint16_t*>(a.c) + o) = v2i{(int)lo, (int)hi};
+    } else {
+      *reinterpret_cast<v2i*>(reinterpret_cast<uint16_t*>(a.c) + o) =
+          v2i{(int)f32x2_to_f16x2(v[0], v[1]), (int)f32x2_to_f16x2(v[2], v[3])};
+    }
+  }
+}
+
+// K elements of one part of a split: whole K stages of the config's width
+// per part (an int8 stage is sb elements, a 16-bit one sb / 2).
+static int64_t split_k_elems(int mode, const GemmConfig& c, const GemmArgs& a) {
+  const int64_t bke = mode == GM_I8 ? c.sb : c.sb / 2;
   const int64_t per = (a.K + c.ksplit - 1) / c.ksplit;
   return (per + bke - 1) / bke * bke;
 }
@@ -289,9 +340,9 @@ size_t gemm_part_bytes(int mode, int cfg_idx, const GemmArgs& a) {
   int n;
   const GemmEntry* t = table(mode, n);
   if (!t || cfg_idx < 0 || cfg_idx >= n || t[cfg_idx].cfg.ksplit <= 1) return 0;
-  const int64_t ks = split_k_elems(t[cfg_idx].cfg, a);
+  const int64_t ks = split_k_elems(mode, t[cfg_idx].cfg, a);
   const int64_t parts = (a.K + ks - 1) / ks;
-  return (size_t)parts * (size_t)(a.M * a.N) * sizeof(float);
+  return (size_t)parts * (size_t)(a.M * a.N) * sizeof(float);  // binary32 or int32 partials
 }
 
 int launch_gemm(int mode, int cfg_idx, const GemmArgs& a, hipStream_t s) {
@@ -307,18 +358,31 @@ int launch_gemm(int mode, int cfg_idx, const GemmArgs& a, hipStream_t s) {
     t[cfg_idx].fn(q, s);
     return HXI_OK;
   }
-  // K split: binary32 partials into a.part, then the merge applies the
-  // epilogue (column scale, residual, rounding)
-  if (mode == GM_I8 || a.b2 || !a.part || a.row_scale) return HXI_ERR_ARG;
+  // K split: binary32 (int8: int32) partials into a.part, then the merge
+  // applies the epilogue (scales, residual, rounding)
+  if (a.b2 || !a.part || (mode != GM_I8 && a.row_scale)) return HXI_ERR_ARG;
   GemmArgs q = a;
-  q.k_split = split_k_elems(c, a);
+  q.k_split = split_k_elems(mode, c, a);
   q.c = a.part;
   q.ldc = a.N;
-  q.out_dtype = DT_F32;
+  q.out_dtype = mode == GM_I8 ? DT_I32 : DT_F32;
+  q.row_scale = nullptr;
   q.col_scale = nullptr;
   q.res = nullptr;
   const int parts = (int)((a.K + q.k_split - 1) / q.k_split);
   t[cfg_idx].fn(q, s);
+  if (mode == GM_I8) {
+    if ((uint64_t)a.M * (uint64_t)(a.N / 4) >= ((uint64_t)1 << 32)) return HXI_ERR_SHAPE;
+    const dim3 grid((unsigned)((a.M * (a.N / 4) + 255) / 256));
+    const int* ip = reinterpret_cast<const int*>(a.part);
+    switch (a.out_dtype) {
+      case DT_I32: splitk_merge_i8_kernel<DT_I32><<<grid, dim3(256), 0, s>>>(a, ip, parts); break;
+      case DT_F32: splitk_merge_i8_kernel<DT_F32><<<grid, dim3(256), 0, s>>>(a, ip, parts); break;
+      case DT_BF16: splitk_merge_i8_kernel<DT_BF16><<<grid, dim3(256), 0, s>>>(a, ip, parts); break;
+      default: splitk_merge_i8_kernel<DT_F16><<<grid, dim3(256), 0, s>>>(a, ip, parts); break;
+    }
+    return HXI_OK;
+  }
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
   const bool v8 = a.N % 8 == 0 && a.ldc % 8 == 0 && (!a.res || a.ldr % 8 == 0) &&
                   (!a.col_scale || al16(a.col_scale)) && a.M * (a.N / 8) < ((int64_t)1 << 31) &&

@@ -15,6 +15,13 @@ const GemmEntry* gemm_table_f16(int& n) {
       // small tiles with K in parts: more workgroups per CU for skinny M
       {{128, 128, 2, 2, GE_STORE, "128x128_w2x2_k2", 2, 0.89f, 2}, &launch_one<GM_F16, 128, 128, 2, 2, GE_STORE>},
       {{64, 64, 2, 2, GE_STORE, "64x64_w2x2_k4", 4, 0.61f, 4}, &launch_one<GM_F16, 64, 64, 2, 2, GE_STORE>},
+      // K stage width and depth (a 128-byte stage is 64 k): 256-byte stages
+      // halve the barriers per K of a deep product; three 64-byte stages
+      // keep two stages of loads in flight
+      {{128, 128, 2, 2, GE_STORE, "128x128_w2x2_bk256", 1, 0.67f, 0, 256, 2},
+       &launch_one<GM_F16, 128, 128, 2, 2, GE_STORE, 256, 2>},
+      {{128, 128, 2, 2, GE_STORE, "128x128_w2x2_bk64_s3", 2, 0.68f, 0, 64, 3},
+       &launch_one<GM_F16, 128, 128, 2, 2, GE_STORE, 64, 3>},
   };
   n = (int)(sizeof(t) / sizeof(t[0]));
   return t;

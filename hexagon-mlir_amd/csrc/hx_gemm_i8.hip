@@ -7,7 +7,29 @@ namespace hx {
 // A host function holding the table: a namespace-scope array of host
 // function pointers would also be emitted by the device compilation.
 const GemmEntry* gemm_table_i8(int& n) {
-  static const GemmEntry t[] = {HX_GEMM_CFGS(GM_I8)};
+  static const GemmEntry t[] = {
+      HX_GEMM_CFGS(GM_I8),
+      // K stage width and depth: 64-byte stages halve the LDS per stage
+      // (room for a third stage, or more workgroups per CU), 256-byte stages
+      // halve the barriers per K
+      {{256, 256, 2, 4, GE_STORE, "256x256_w2x4_bk64", 1, 0.86f, 0, 64, 2},
+       &launch_one<GM_I8, 256, 256, 2, 4, GE_STORE, 64, 2>},
+      {{256, 256, 2, 4, GE_STORE, "256x256_w2x4_bk64_s3", 1, 0.92f, 0, 64, 3},
+       &launch_one<GM_I8, 256, 256, 2, 4, GE_STORE, 64, 3>},
+      {{128, 128, 2, 2, GE_STORE, "128x128_w2x2_bk64", 2, 0.71f, 0, 64, 2},
+       &launch_one<GM_I8, 128, 128, 2, 2, GE_STORE, 64, 2>},
+      {{128, 128, 2, 2, GE_STORE, "128x128_w2x2_bk64_s3", 2, 0.68f, 0, 64, 3},
+       &launch_one<GM_I8, 128, 128, 2, 2, GE_STORE, 64, 3>},
+      {{128, 128, 2, 2, GE_STORE, "128x128_w2x2_bk256", 1, 0.67f, 0, 256, 2},
+       &launch_one<GM_I8, 128, 128, 2, 2, GE_STORE, 256, 2>},
+      {{64, 64, 2, 2, GE_STORE, "64x64_w2x2_bk256", 2, 0.51f, 0, 256, 2},
+       &launch_one<GM_I8, 64, 64, 2, 2, GE_STORE, 256, 2>},
+      // K in parts (int32 partials, exact, and a merge that dequantises):
+      // fills the chip when the output tiles are fewer than the CUs
+      {{256, 256, 2, 4, GE_STORE, "256x256_w2x4_k2", 1, 1.00f, 2}, &launch_one<GM_I8, 256, 256, 2, 4, GE_STORE>},
+      {{128, 128, 2, 2, GE_STORE, "128x128_w2x2_k2", 2, 0.89f, 2}, &launch_one<GM_I8, 128, 128, 2, 2, GE_STORE>},
+      {{64, 64, 2, 2, GE_STORE, "64x64_w2x2_k4", 4, 0.61f, 4}, &launch_one<GM_I8, 64, 64, 2, 2, GE_STORE>},
+  };
   n = (int)(sizeof(t) / sizeof(t[0]));
   return t;
 }

@@ -68,6 +68,15 @@ __device__ __forceinline__ int swz128(int row) { return (row ^ (row >> 3)) & 7; 
 // coherent, i.e. written through to memory).
 constexpr int kStoreWriteThrough = 1 | 16;
 __device__ __forceinline__ int swz64(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+// 256-byte rows: 16 consecutive rows (one 16-lane service group of a
+// 16-byte read) reading the same logical chunk cover all 16 chunk slots.
+__device__ __forceinline__ int swz256(int row) { return (row ^ (row >> 4)) & 15; }
+template <int RB>
+__device__ __forceinline__ int swz_rows(int row) {
+  if constexpr (RB == 256) return swz256(row);
+  else if constexpr (RB == 128) return swz128(row);
+  else return swz64(row);
+}
 
 template <int MODE>
 __device__ __forceinline__ typename ModeTraits<MODE>::Acc mfma32(v4i a, v4i b,
@@ -132,11 +141,13 @@ __device__ __forceinline__ void interleave_reads_mfma_vmem() {
   });
 }
 
-// SB: bytes of A per row in one K stage (128; 64 halves the LDS so that two
-// 4-wave workgroups share a CU with independent stage barriers -- measured
-// at 4096^3 as 76 us against 59 us for the 8-wave 256x256 tile, so no table
-// entry uses it).  MINW: waves per SIMD the register budget must allow (2
-// caps a wave at 256 registers).
+// SB: bytes of A per row in one K stage (64, 128 or 256; the W8 mode takes
+// 128 only).  Smaller stages cut the LDS a workgroup holds
+// (more workgroups per CU, or a third stage), larger ones halve the
+// barriers per K.  STAGES: K stages held in LDS at once (2: double buffer,
+// 3: the loads of stage kt+2 are in flight while stage kt is consumed).
+// MINW: waves per SIMD the register budget must allow (2 caps a wave at 256
+// registers).
 // BKN (f16 / bf16): B is [K][N], N contiguous.  A stage then holds BKE rows
 // of k, each BN elements, with 64-byte segments XOR-swizzled by the row; the
 // B operand of each MFMA step comes from two transposing LDS reads
@@ -147,13 +158,14 @@ __device__ __forceinline__ void interleave_reads_mfma_vmem() {
 // k = 16ks + 8(l/32) + 4h + (0..3) -- the K-contiguous operand without a
 // transpose of B in memory.
 template <int MODE, int BM, int BN, int WM, int WN, int EPI, int SB = 128, int MINW = 1, bool EDGE = false,
-          bool BKN = false>
+          bool BKN = false, int STAGES = 2>
 __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(MINW, 8)))
 gemm_kernel(GemmArgs p) {
   typedef ModeTraits<MODE> T;
   typedef typename T::Acc Acc;
-  static_assert(SB == 128 || (SB == 64 && MODE != GM_W8), "stage width");
-  static_assert(!BKN || ((MODE == GM_F16 || MODE == GM_BF16) && SB == 128 && EPI == GE_STORE), "[K][N] B");
+  static_assert(SB == 128 || ((SB == 64 || SB == 256) && MODE != GM_W8), "stage width");
+  static_assert(STAGES == 2 || STAGES == 3, "stage count");
+  static_assert(!BKN || ((MODE == GM_F16 || MODE == GM_BF16) && EPI == GE_STORE), "[K][N] B");
   constexpr int NW = WM * WN;
   constexpr int NB = (EPI == GE_SWIGLU) ? 2 : 1;
   constexpr int BROW = (MODE == GM_W8) ? SB / 2 : SB;  // bytes of B per row in one stage
@@ -166,6 +178,7 @@ gemm_kernel(GemmArgs p) {
   constexpr int B_BLK = B_BYTES / 1024;
   constexpr int A_RPB = 1024 / SB;
   constexpr int B_RPB = 1024 / BROW;
+  constexpr int A_CPR = SB / 16, B_CPR = BROW / 16;  // 16-byte chunks per row
   constexpr int A_PER_W = A_BLK / NW;
   constexpr int B_PER_W = B_BLK / NW;
   constexpr int P = A_PER_W + NB * B_PER_W;  // direct loads per wave per stage
@@ -173,17 +186,18 @@ gemm_kernel(GemmArgs p) {
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
   static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
-  static_assert(2 * STAGE <= 160 * 1024, "LDS budget");
-  static_assert(2 * P < 64, "vmcnt range");
-
-  // Two stages as two distinct arrays: the compiler can then see that a
-  // direct load into one stage never aliases the reads of the other.
-  __shared__ __attribute__((aligned(1024))) char st0[STAGE];
   // per-row / per-column scales of this tile, fetched in the prologue
   // (SC_ROWS floats each: one 1 KiB direct load covers 256)
   constexpr int SC_ROWS = (BM > BN ? BM : BN) < 256 ? 256 : (BM > BN ? BM : BN);
+  static_assert(STAGES * STAGE + (1 + NB) * SC_ROWS * 4 <= 160 * 1024, "LDS budget");
+  static_assert(STAGES * P < 64, "vmcnt range");
+
+  // The stages as distinct arrays: the compiler can then see that a direct
+  // load into one stage never aliases the reads of another.
+  __shared__ __attribute__((aligned(1024))) char st0[STAGE];
   __shared__ __attribute__((aligned(1024))) float scl[(1 + NB) * SC_ROWS];
   __shared__ __attribute__((aligned(1024))) char st1[STAGE];
+  __shared__ __attribute__((aligned(1024))) char st2[STAGES == 3 ? STAGE : 16];
 
   // K split: workgroup row blockIdx.y sums k in [y k_split, (y+1) k_split)
   // into the binary32 slice y of c (launch_gemm merges the slices)
@@ -242,16 +256,16 @@ gemm_kernel(GemmArgs p) {
   // a wave-uniform offset (the instruction's scalar offset); the lane part
   // is a row offset plus the swizzled chunk, recomputed per block from the
   // block index rather than kept in registers.
-  const uint32_t a_lane_row = (uint32_t)(SB == 128 ? (lane >> 3) : (lane >> 2)) * lda_b;
-  const uint32_t b_lane_row = (uint32_t)(BROW == 128 ? (lane >> 3) : (lane >> 2)) * ldb_b;
+  const uint32_t a_lane_row = (uint32_t)(lane / A_CPR) * lda_b;
+  const uint32_t b_lane_row = (uint32_t)(lane / B_CPR) * ldb_b;
   // EDGE (M or N not a multiple of the tile): lanes whose row lies past the
   // tile's last row get an out-of-range vector offset.  The block's row
   // offset travels in the scalar offset, and the zero fill must not depend
   // on whether the range check includes it.  Block blk's lane row is past
   // the edge when blk * RPB >= lim.  Interior shapes skip the test (it costs
   // ~1% at 4096^3).
-  const int a_lim = (int)rows_a - (SB == 128 ? (lane >> 3) : (lane >> 2));
-  const int b_lim = (int)rows_b - (BROW == 128 ? (lane >> 3) : (lane >> 2));
+  const int a_lim = (int)rows_a - lane / A_CPR;
+  const int b_lim = (int)rows_b - lane / B_CPR;
   constexpr int BKE = SB / T::EA;  // elements of K per stage
   // BKN stage layout: BKE rows of k, KROWB bytes each, 64-byte segments
   // XOR-swizzled so that the 8 rows one transposing read touches (4 + 4,
@@ -283,8 +297,8 @@ gemm_kernel(GemmArgs p) {
         // row = 8*blk + lane/8, so swz128(row) = (lane/8 ^ blk) & 7
         kc = (uint32_t)(((lane & 7) ^ (lane >> 3) ^ blk) & 7) * 16u;
       } else {
-        const int row = blk * 16 + (lane >> 2);
-        kc = (uint32_t)((lane & 3) ^ swz64(row)) * 16u;
+        const int row = blk * A_RPB + lane / A_CPR;
+        kc = (uint32_t)((lane % A_CPR) ^ swz_rows<SB>(row)) * 16u;
       }
       uint32_t off = a_lane_row + kc + ka;
       if (tail && ka + kc >= ka_bytes) off = 0x80000000u;
@@ -315,8 +329,8 @@ gemm_kernel(GemmArgs p) {
         if constexpr (BROW == 128) {
           kc = (uint32_t)(((lane & 7) ^ (lane >> 3) ^ blk) & 7) * 16u;
         } else {
-          const int row = blk * 16 + (lane >> 2);
-          kc = (uint32_t)((lane & 3) ^ swz64(row)) * 16u;
+          const int row = blk * B_RPB + lane / B_CPR;
+          kc = (uint32_t)((lane % B_CPR) ^ swz_rows<BROW>(row)) * 16u;
         }
         uint32_t off = b_lane_row + kc + kb;
         if (tail && kb + kc >= kb_bytes) off = 0x80000000u;
@@ -356,10 +370,7 @@ gemm_kernel(GemmArgs p) {
     // k = 32*jp + 16*g + 8*h + (0..7) for lane group g, both operands, so
     // every k of the stage is summed exactly once)
     const int ca = (MODE != GM_W8) ? ks * 2 + lg : 4 * (ks >> 1) + 2 * lg + (ks & 1);
-    auto swz = [](int row) -> int {
-      if constexpr (SB == 128) return swz128(row);
-      else return swz64(row);
-    };
+    auto swz = [](int row) -> int { return swz_rows<SB>(row); };
     static_for<TM>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
       const int row = wm * WTM + i * 32 + lrow;
@@ -434,13 +445,16 @@ gemm_kernel(GemmArgs p) {
   // One stage: the reads of step ks+1 are issued before the MFMAs of step
   // ks.  Before the last step's MFMAs the workgroup meets at the barrier
   // (every wave's loads of the next stage have landed, every wave is done
-  // reading this one), the loads of stage kt+2 go into this stage's buffer
-  // (DMA: 0 none, 1 a middle stage, 2 possibly the last stage) and step 0 of
-  // the next stage is read, so the MFMA pipe never waits on a barrier with
-  // an empty queue.  LAST: no next stage.
-  auto stage_body = [&](char* cur, char* nxt, int kt, auto dmac, auto lastc) {
+  // reading this one), the loads of stage kt+STAGES go into this stage's
+  // buffer (DMA: 0 none, 1 a middle stage, 2 possibly the last stage) and
+  // step 0 of the next stage is read, so the MFMA pipe never waits on a
+  // barrier with an empty queue.  LAST: no next stage.  WAITN: direct loads
+  // (per wave) that may still be in flight at the barrier -- those of the
+  // stages after the next one.
+  auto stage_body = [&](char* cur, char* nxt, int kt, auto dmac, auto lastc, auto waitc) {
     constexpr int DMA = decltype(dmac)::value;
     constexpr bool LAST = decltype(lastc)::value;
+    constexpr int WAITN = decltype(waitc)::value;
     static_for<KSTEPS>([&](auto ksc) {
       constexpr int ks = decltype(ksc)::value;
       if constexpr (ks == KSTEPS - 1 && !LAST && DMA != 0) {
@@ -449,11 +463,11 @@ gemm_kernel(GemmArgs p) {
         // the MFMA pipe keeps running while the loads are issued (issued as
         // one burst, they stall the wave on the memory queue with its MFMAs
         // stuck behind them).
-        wait_vm<0>();
+        wait_vm<WAITN>();
         lds_barrier();
         read_frags(nxt, std::integral_constant<int, 0>{});
-        if constexpr (DMA == 1) dma_stage(cur, kt + 2, std::false_type{});
-        if constexpr (DMA == 2) dma_stage(cur, kt + 2, std::true_type{});
+        if constexpr (DMA == 1) dma_stage(cur, kt + STAGES, std::false_type{});
+        if constexpr (DMA == 2) dma_stage(cur, kt + STAGES, std::true_type{});
         mfmas(ksc);
         interleave_reads_mfma_vmem<TM + NB * TN, NB * TN * TM, P>();
         __builtin_amdgcn_sched_barrier(0);
@@ -466,7 +480,7 @@ gemm_kernel(GemmArgs p) {
           __builtin_amdgcn_sched_barrier(0);
         } else {
           if constexpr (!LAST) {
-            wait_vm<0>();
+            wait_vm<WAITN>();
             lds_barrier();
             read_frags(nxt, std::integral_constant<int, 0>{});
           }
@@ -480,10 +494,11 @@ gemm_kernel(GemmArgs p) {
   typedef std::integral_constant<int, 0> NoDma;
   typedef std::integral_constant<int, 2> LastDma;
 
-  // Stage buffers: stage kt lives in st0 when kt - (nk & 1) is even, so the
-  // final two stages are always (st0, st1) and the steady loop needs no
-  // remainder; with an odd stage count stage 0 goes to st1 and is peeled.
-  // (The fast path requires nk >= 2.)
+  // Stage buffers (two stages): stage kt lives in st0 when kt - (nk & 1) is
+  // even, so the final two stages are always (st0, st1) and the steady loop
+  // needs no remainder; with an odd stage count stage 0 goes to st1 and is
+  // peeled.  A single stage of K runs as three, the later two reading as
+  // zeros (their loads are masked like any K tail).
   // The tile's scales go straight to LDS ahead of the first stage (wave 0:
   // row scales, 1: column scales, 2: second column scales): issued first,
   // they are covered by the prologue's wait for stage 0.  A null scale
@@ -500,32 +515,81 @@ gemm_kernel(GemmArgs p) {
     if constexpr (NB == 2)
       if (wave == 2) dma16(sc_rsrc(p.col_scale2, n0, p.N), (char*)(scl + 2 * SC_ROWS), lane * 16u, 0u);
   }
-  const bool odd = nk & 1;
-  if (odd) {
-    dma_stage(st1, 0, std::true_type{});
-    dma_stage(st0, 1, std::true_type{});
+  typedef std::integral_constant<int, 0> Wait0;
+  typedef std::integral_constant<int, P> Wait1;  // one later stage's loads may be in flight
+  typedef std::false_type More;
+  auto first = [&](char* st) { read_frags(st, std::integral_constant<int, 0>{}); };
+  if constexpr (STAGES == 2) {
+    const bool odd = nk & 1;
+    if (odd) {
+      dma_stage(st1, 0, std::true_type{});
+      dma_stage(st0, 1, std::true_type{});
+    } else {
+      dma_stage(st0, 0, std::true_type{});
+      dma_stage(st1, 1, std::true_type{});
+    }
+    wait_vm<P>();
+    lds_barrier();
+    int kt = 0;
+    if (odd) {
+      first(st1);
+      stage_body(st1, st0, 0, LastDma{}, More{}, Wait0{});
+      kt = 1;
+    } else {
+      first(st0);
+    }
+    // Steady state: straight-line pairs of stages (no conditional code, so
+    // the accumulators keep one register class across iterations).
+    for (; nk - kt > 2; kt += 2) {
+      stage_body(st0, st1, kt, LastDma{}, More{}, Wait0{});
+      stage_body(st1, st0, kt + 1, LastDma{}, More{}, Wait0{});
+    }
+    stage_body(st0, st1, kt, NoDma{}, More{}, Wait0{});
+    stage_body(st1, st0, kt + 1, NoDma{}, std::true_type{}, Wait0{});
   } else {
-    dma_stage(st0, 0, std::true_type{});
-    dma_stage(st1, 1, std::true_type{});
+    // Three-stage ring.  Stage kt lives in buffer (kt + 3 - nk3 % 3) % 3, so
+    // the final three stages are always (st0, st1, st2); the first nk3 % 3
+    // stages are peeled.  Fewer than three stages of K run as three, the
+    // stages past K reading as zeros.
+    const int nk3 = nk < 3 ? 3 : nk;
+    const int r = nk3 % 3;
+    if (r == 0) {
+      dma_stage(st0, 0, std::true_type{});
+      dma_stage(st1, 1, std::true_type{});
+      dma_stage(st2, 2, std::true_type{});
+    } else if (r == 1) {
+      dma_stage(st2, 0, std::true_type{});
+      dma_stage(st0, 1, std::true_type{});
+      dma_stage(st1, 2, std::true_type{});
+    } else {
+      dma_stage(st1, 0, std::true_type{});
+      dma_stage(st2, 1, std::true_type{});
+      dma_stage(st0, 2, std::true_type{});
+    }
+    wait_vm<2 * P>();
+    lds_barrier();
+    int kt = 0;
+    if (r == 1) {
+      first(st2);
+      stage_body(st2, st0, 0, LastDma{}, More{}, Wait1{});
+      kt = 1;
+    } else if (r == 2) {
+      first(st1);
+      stage_body(st1, st2, 0, LastDma{}, More{}, Wait1{});
+      stage_body(st2, st0, 1, LastDma{}, More{}, Wait1{});
+      kt = 2;
+    } else {
+      first(st0);
+    }
+    for (; nk3 - kt > 3; kt += 3) {
+      stage_body(st0, st1, kt, LastDma{}, More{}, Wait1{});
+      stage_body(st1, st2, kt + 1, LastDma{}, More{}, Wait1{});
+      stage_body(st2, st0, kt + 2, LastDma{}, More{}, Wait1{});
+    }
+    stage_body(st0, st1, kt, NoDma{}, More{}, Wait1{});
+    stage_body(st1, st2, kt + 1, NoDma{}, More{}, Wait0{});
+    stage_body(st2, st0, kt + 2, NoDma{}, std::true_type{}, Wait0{});
   }
-  wait_vm<P>();
-  lds_barrier();
-  int kt = 0;
-  if (odd) {
-    read_frags(st1, std::integral_constant<int, 0>{});
-    stage_body(st1, st0, 0, LastDma{}, std::false_type{});
-    kt = 1;
-  } else {
-    read_frags(st0, std::integral_constant<int, 0>{});
-  }
-  // Steady state: straight-line pairs of stages (no conditional code, so
-  // the accumulators keep one register class across iterations).
-  for (; nk - kt > 2; kt += 2) {
-    stage_body(st0, st1, kt, LastDma{}, std::false_type{});
-    stage_body(st1, st0, kt + 1, LastDma{}, std::false_type{});
-  }
-  stage_body(st0, st1, kt, NoDma{}, std::false_type{});
-  stage_body(st1, st0, kt + 1, NoDma{}, std::true_type{});
 
   // ---- epilogue ----------------------------------------------------------
   // Lane (lrow, lg) holds row wm*WTM + 32*i + lrow, columns
@@ -706,21 +770,21 @@ gemm_kernel(GemmArgs p) {
 // ---------------------------------------------------------------------------
 typedef void (*GemmLaunch)(const GemmArgs&, hipStream_t);
 
-template <int MODE, int BM, int BN, int WM, int WN, int EPI, int SB = 128, int MINW = 1>
+template <int MODE, int BM, int BN, int WM, int WN, int EPI, int SB = 128, int STAGES = 2, int MINW = 1>
 static void launch_one(const GemmArgs& a, hipStream_t s) {
   const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   const unsigned parts = a.k_split > 0 ? (unsigned)((a.K + a.k_split - 1) / a.k_split) : 1u;
   const dim3 grid((unsigned)tiles, parts), block(64 * WM * WN);
   const bool edge = a.M % BM != 0 || a.N % BN != 0;
-  if constexpr ((MODE == GM_F16 || MODE == GM_BF16) && EPI == GE_STORE && SB == 128) {
+  if constexpr ((MODE == GM_F16 || MODE == GM_BF16) && EPI == GE_STORE) {
     if (a.b_kn) {
-      if (edge) gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, true, true><<<grid, block, 0, s>>>(a);
-      else gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, false, true><<<grid, block, 0, s>>>(a);
+      if (edge) gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, true, true, STAGES><<<grid, block, 0, s>>>(a);
+      else gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, false, true, STAGES><<<grid, block, 0, s>>>(a);
       return;
     }
   }
-  if (edge) gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, true><<<grid, block, 0, s>>>(a);
-  else gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, false><<<grid, block, 0, s>>>(a);
+  if (edge) gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, true, false, STAGES><<<grid, block, 0, s>>>(a);
+  else gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, false, false, STAGES><<<grid, block, 0, s>>>(a);
 }
 
 struct GemmEntry {

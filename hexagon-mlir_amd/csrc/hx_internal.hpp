@@ -53,8 +53,8 @@ struct GemmArgs {
   const float* col_scale2;      // [N] scale of b2 (GE_SWIGLU)
   const void* res; int64_t ldr; int res_dtype;  // residual, may be null
   int b_kn;                     // f16 / bf16 only: b is [K][N] (N contiguous)
-  // K split (float modes): the kernel runs gridDim.y parts of k_split
-  // elements, each writing binary32 partials to its [M][N] slice of c;
+  // K split: the kernel runs gridDim.y parts of k_split elements, each
+  // writing binary32 (int8: int32) partials to its [M][N] slice of c;
   // `part` is the partial buffer launch_gemm uses for a split config
   int64_t k_split;
   float* part;
@@ -66,7 +66,9 @@ struct GemmConfig {
   const char* name;
   int occ;              // workgroups resident per CU (LDS / register limit)
   float rate;           // measured output throughput of one CU, relative
-  int ksplit;           // K parts (0 or 1: none); partials merged by a second kernel
+  int ksplit = 0;       // K parts (0 or 1: none); partials merged by a second kernel
+  int sb = 128;         // bytes of A per row in one K stage (64, 128, 256)
+  int stages = 2;       // K stages resident in LDS at once (2 or 3)
 };
 // Partial-buffer bytes a launch of config cfg_idx needs (0 without a K split).
 size_t gemm_part_bytes(int mode, int cfg_idx, const GemmArgs& a);

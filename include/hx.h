@@ -274,8 +274,10 @@ enum {
 };
 
 /* One compiled configuration.  GEMM families fill bm/bn/bk (K elements per
- * LDS stage)/waves_m/waves_n/lds_stages; the GEMV families fill col_tiles
- * (16-column tiles per wave) and split_k (workgroups per column tile).
+ * LDS stage)/waves_m/waves_n/lds_stages (K stages resident in LDS: 2 or 3)/
+ * split_k (K parts, partials merged by a second kernel; 1: none); the GEMV
+ * families fill col_tiles (16-column tiles per wave) and split_k
+ * (workgroups per column tile).
  * Replaces the (BM, BN, BK) tile space of enumerate_tile_configs
  * (QHB/backend/hmx_search.py:246-332), widened to the knobs that matter on
  * gfx950. */

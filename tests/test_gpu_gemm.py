@@ -143,18 +143,73 @@ def test_gemm_i8_4096_cube(hx, dev):
     assert np.array_equal(to_np(c16).view(np.uint16), want16.view(np.uint16))
 
 
-@pytest.mark.parametrize("cfg", range(6))
-def test_gemm_i8_every_config(hx, dev, cfg):
-    assert hx.config_count(1) == 6, "new int8 configs: extend this test's range"
-    """Every compiled int8 configuration is exact (the autotuner may pick any)."""
-    M, N, K = 384, 640, 1024
+N_I8_CONFIGS = 15
+
+
+@pytest.mark.parametrize("K", [1024, 1072, 1152, 208, 144])
+@pytest.mark.parametrize("cfg", range(N_I8_CONFIGS))
+def test_gemm_i8_every_config(hx, dev, cfg, K):
+    """Every compiled int8 configuration is exact (the autotuner may pick
+    any): edge tiles in M and N, K stage counts that leave each remainder of
+    the three-stage ring (1072 = 16.75 stages of 64 bytes, 1152 = 18), K
+    shorter than the stage ring (208, 144) and, for the split configs, parts
+    of unequal length."""
+    assert hx.config_count(1) == N_I8_CONFIGS, "new int8 configs: extend this test's range"
+    M, N = 384, 640
     a, b = i8((M, K), 20), i8((K, N), 21)
     hx.config_select(1, M, N, K, cfg)
     try:
         got = to_np(hx.gemm_i8(to_dev(a, dev), to_dev(np.ascontiguousarray(b.T), dev), b_layout="nk"))
     finally:
         hx.config_select(1, M, N, K, -1)
-    assert np.array_equal(got, oracle.gemm_i8_i32(a, b))
+    assert np.array_equal(got, oracle.gemm_i8_i32(a, b)), hx.config_get(1, cfg)["name"]
+
+
+@pytest.mark.parametrize("out", ["i32", "f16", "bf16", "f32"])
+@pytest.mark.parametrize("name", ["256x256_w2x4_k2", "128x128_w2x2_k2", "64x64_w2x2_k4"])
+def test_gemm_i8_split_k_dequant_bitexact(hx, dev, name, out):
+    """int8 K split: int32 partials summed with wrap-around equal the
+    unsplit accumulator, and the merge's dequant ((acc * row) * col, one
+    rounding to the output type) equals the fused epilogue's bit for bit;
+    one-sided and two-sided scales, K not a multiple of the part size."""
+    import torch
+    M, N, K = 272, 200, 1936
+    a, bt = i8((M, K), 150), i8((N, K), 151)
+    sa = rng(152).uniform(0.001, 0.02, M).astype(np.float32)
+    sb = rng(153).uniform(0.001, 0.02, N).astype(np.float32)
+    names = [hx.config_get(1, i)["name"] for i in range(hx.config_count(1))]
+    cfg = names.index(name)
+    assert hx.config_get(1, cfg)["split_k"] > 1
+    acc = oracle.gemm_i8_i32(a, bt, b_trans=True)
+    tdt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}
+    hx.config_select(1, M, N, K, cfg)
+    hx.manifest_enable(True)
+    hx.manifest_clear()
+    try:
+        ad, bd = to_dev(a, dev), to_dev(bt, dev)
+        if out == "i32":
+            got = to_np(hx.gemm_i8(ad, bd, b_layout="nk"))
+            assert np.array_equal(got, acc)
+        else:
+            for rs, cs in ((sa, sb), (sa, None), (None, sb)):
+                c = hx.gemm_i8(ad, bd, b_layout="nk", row_scale=None if rs is None else to_dev(rs, dev),
+                               col_scale=None if cs is None else to_dev(cs, dev), out_dtype=tdt[out])
+                ones_m, ones_n = np.ones(M, np.float32), np.ones(N, np.float32)
+                v = (acc.astype(np.float32) * (ones_m if rs is None else rs)[:, None]) * \
+                    (ones_n if cs is None else cs)[None, :]
+                if out == "f16":
+                    want = oracle.dequant_i32_f16(acc, rs, cs)
+                    assert np.array_equal(to_np(c).view(np.uint16), want.view(np.uint16))
+                elif out == "bf16":
+                    got = to_np(c.view(torch.int16)).view(np.uint16)
+                    assert np.array_equal(got, bf16_from_f32(v).view(np.uint16))
+                else:
+                    assert np.array_equal(to_np(c).view(np.uint32), v.view(np.uint32))
+        recs = hx.manifest()["records"]
+    finally:
+        hx.manifest_enable(False)
+        hx.config_select(1, M, N, K, -1)
+    assert recs and all(r["config"] == name for r in recs), recs
 
 
 def _fp(dtype, shape, seed, lo=-1.0, hi=1.0):
