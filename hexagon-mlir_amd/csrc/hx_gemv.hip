@@ -200,6 +200,39 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
   const uint16_t* x = reinterpret_cast<const uint16_t*>(p.x);
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
   const int64_t kp = (int64_t)kchunks * KD;
+  constexpr int NT = 64 * KW;                     // threads
+  constexpr int NSC = (CT * 256 + NT - 1) / NT;  // outputs per row block this thread finalises
+
+  // The column scales this thread applies at the end, loaded first: issued
+  // after the reduction, the load of a cold scale line would add its whole
+  // memory latency to every launch.  Thread t finalises element
+  // e = t + NT * i of each row block, column (t0 + e / 256) * 16 + (e / 4) % 16
+  // (the reduction below); with M <= 4 (one row block, rows in lanes 0..15)
+  // thread t < 64 CT finalises column (t0 + t / 64) * 16 + (t / 4) % 16.
+  // Out-of-range offsets read zero and are never used.
+  const bool few_rows = MB == 1 && p.M <= 4;
+  float sc[NSC];
+  {
+    const bool s32 = p.scale != nullptr;
+    const __amdgpu_buffer_rsrc_t rsc = __builtin_amdgcn_make_buffer_rsrc(
+        s32 ? (void*)p.scale : (void*)p.scale16, 0,
+        (s32 || p.scale16) ? (int)(p.N * (s32 ? 4 : 2)) : 0, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < NSC; ++i) {
+      const int e = tid + NT * i;
+      const int64_t n = few_rows ? (int64_t)(t0 + (tid >> 6)) * 16 + ((tid >> 2) & 15)
+                                 : (int64_t)(t0 + (e >> 8)) * 16 + ((e >> 2) & 15);
+      const bool in = (few_rows ? (i == 0 && tid < 64 * CT) : e < CT * 256) && n < p.N;
+      if (s32) {
+        sc[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                              rsc, in ? (int)(n * 4) : (int)0x80000000, 0, 0));
+      } else {
+        const uint16_t h = __builtin_amdgcn_raw_buffer_load_b16(rsc, in ? (int)(n * 2) : (int)0x80000000, 0, 0);
+        sc[i] = f16_bits_to_f32(h);
+      }
+    }
+  }
+  const bool has_scale = p.scale != nullptr || p.scale16 != nullptr;
 
   // Every global load below is a buffer load whose out-of-range offset
   // (0x80000000) reads zero, so no load sits behind a branch: a conditional
@@ -235,7 +268,6 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
   // weight loads queued behind them).
   const int bpr = (int)((kp + 511) / 512);  // 1 KiB blocks per row
   const int64_t xlp = (int64_t)bpr * 512 + 8;
-  constexpr int NT = 64 * KW;
   constexpr int XR = XS == XS_REG ? (2048 / NT > 0 ? 2048 / NT : 1) : 1;
   const uint32_t row_ch = (uint32_t)(kp / 8);
   const uint32_t cb = (row_ch + NT - 1) / NT;
@@ -320,11 +352,11 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
       for (int e = 0; e < NE; ++e) {
         v4u xa;
         if constexpr (XL) {
-          // rows >= M read row 0 and are zeroed after the (unconditional) read
+          // only the lanes of rows < M read (the others hold zeros): with
+          // M = 1 a read moves 4 lanes' bytes instead of 64
           const int64_t k = (int64_t)(c0 + wave + KW * u) * KD + KG * g + 8 * e;
-          const bool in = xrow && k < kp;
-          const v4u t = *reinterpret_cast<const v4u*>(xs + (xrow ? col : 0) * xlp + (in ? k : 0));
-          xa = in ? t : v4u{0u, 0u, 0u, 0u};
+          xa = v4u{0u, 0u, 0u, 0u};
+          if (xrow && k < kp) xa = *reinterpret_cast<const v4u*>(xs + col * xlp + k);
         } else {
           xa = xq[u][e];
         }
@@ -387,11 +419,10 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
         for (int e = 0; e < NE; ++e) {
           v4u xa[MB];
           if constexpr (XL) {
-            // rows >= M read row 0 and are zeroed after the (unconditional) read
+            // only the lanes of rows < M read (the others hold zeros)
             const int64_t k = (int64_t)(c0 + wave + KW * u) * KD + KG * g + 8 * e;
-            const bool in = xrow && k < kp;
-            const v4u t = *reinterpret_cast<const v4u*>(xs + (xrow ? col : 0) * xlp + (in ? k : 0));
-            xa[0] = in ? t : v4u{0u, 0u, 0u, 0u};
+            xa[0] = v4u{0u, 0u, 0u, 0u};
+            if (xrow && k < kp) xa[0] = *reinterpret_cast<const v4u*>(xs + col * xlp + k);
           } else {
 #pragma unroll
             for (int b = 0; b < MB; ++b) xa[b] = xq[u][e][b];
@@ -432,6 +463,31 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
   // bf16 for bf16).
   __shared__ float red[KW][CT][64][4];
   uint16_t* y = reinterpret_cast<uint16_t*>(p.y);
+  if (few_rows) {
+    // rows 0..3 of a 16-row block are lanes 0..15 of every tile: only those
+    // go through LDS, and the first 64 CT threads finalise (c, l, r) =
+    // (t / 64, (t / 4) % 16, t % 4), summing the waves in the same order as
+    // the full reduction (identical results).
+    float(*red4)[CT][16][4] = reinterpret_cast<float(*)[CT][16][4]>(&red[0][0][0][0]);
+    if (lane < 16)
+#pragma unroll
+      for (int c = 0; c < CT; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red4[wave][c][lane][r] = acc[0][c][r];
+    __syncthreads();
+    if (tid < 64 * CT) {
+      const int c = tid >> 6, l = (tid >> 2) & 15, r = tid & 3;
+      float s = 0.f;
+#pragma unroll
+      for (int w = 0; w < KW; ++w) s += red4[w][c][l][r];
+      const int64_t n = (int64_t)(t0 + c) * 16 + l;
+      if (r < p.M && n < p.N) {
+        const float v = has_scale ? s * sc[0] : s;
+        y[(int64_t)r * p.ldy + n] = WT == DT_BF16 ? f32_to_bf16(v) : f32_to_f16_bits(v);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int b = 0; b < MB; ++b) {
     if (b > 0) __syncthreads();  // the previous block's sums are read
@@ -440,7 +496,10 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
 #pragma unroll
       for (int r = 0; r < 4; ++r) red[wave][c][lane][r] = acc[b][c][r];
     __syncthreads();
-    for (int e = tid; e < CT * 256; e += 64 * KW) {
+#pragma unroll
+    for (int i = 0; i < NSC; ++i) {
+      const int e = tid + NT * i;
+      if (e >= CT * 256) break;
       const int c = e >> 8, l = (e >> 2) & 63, r = e & 3;
       float s = 0.f;
 #pragma unroll
@@ -448,7 +507,8 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
       const int m = 16 * b + 4 * (l >> 4) + r;
       const int64_t n = (int64_t)(t0 + c) * 16 + (l & 15);
       if (m < p.M && n < p.N) {
-        const float v = gv_scaled(p, n, s);
+        // s * scale[n] in binary32 (an f16 scale widened exactly)
+        const float v = has_scale ? s * sc[i] : s;
         y[(int64_t)m * p.ldy + n] = WT == DT_BF16 ? f32_to_bf16(v) : f32_to_f16_bits(v);
       }
     }
