@@ -187,10 +187,10 @@ const char* gemm_fast_refusal(int mode, const GemmArgs& a) {
   if ((int64_t)256 * a.lda * ea >= ((int64_t)1 << 31)) return "offset-range";
   if ((int64_t)256 * a.ldc * 4 >= ((int64_t)1 << 31)) return "offset-range";
   if (a.b_kn) {
-    // [K][N] B (f16 / bf16): whole 16-byte chunks of a row, every row of k
-    // addressed with 32-bit offsets
-    if (mode != GM_F16 && mode != GM_BF16) return "b-layout";
-    if (a.N % 8 != 0) return "n-granularity";
+    // [K][N] B (int8, f16, bf16): whole 16-byte chunks of a row, every row
+    // of k addressed with 32-bit offsets
+    if (mode != GM_F16 && mode != GM_BF16 && mode != GM_I8) return "b-layout";
+    if ((a.N * eb) % 16 != 0) return "n-granularity";
     if (a.K * a.ldb * eb >= ((int64_t)1 << 31)) return "offset-range";
   } else if ((int64_t)256 * a.ldb * eb >= ((int64_t)1 << 31)) {
     return "offset-range";

@@ -157,6 +157,14 @@ __device__ __forceinline__ void interleave_reads_mfma_vmem() {
 // 16(G%2) + 4(i%4) of its 32-column sub-tile, receives column l % 32 at
 // k = 16ks + 8(l/32) + 4h + (0..3) -- the K-contiguous operand without a
 // transpose of B in memory.
+// BKN int8: the same with ds_read_b64_tr_b8 (within each 16-lane group,
+// lane 8a+b receives element b of the 8-byte chunks addressed by lanes a,
+// a+2, ..., a+14) and the 16-byte chunks of a k row XOR-swizzled so that the
+// 8 consecutive rows x 2 adjacent chunks that a half-wave reads cover 16
+// distinct bank groups: lane
+// l = 16G + i, addressing row 32ks + 16(G/2) + 8h + i/2 at column
+// 16(G%2) + 8(i%2) of its 32-column sub-tile, receives column l % 32 at
+// k = 32ks + 16(l/32) + 8h + (0..7).
 template <int MODE, int BM, int BN, int WM, int WN, int EPI, int SB = 128, int MINW = 1, bool EDGE = false,
           bool BKN = false, int STAGES = 2>
 __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(MINW, 8)))
@@ -165,7 +173,7 @@ gemm_kernel(GemmArgs p) {
   typedef typename T::Acc Acc;
   static_assert(SB == 128 || ((SB == 64 || SB == 256) && MODE != GM_W8), "stage width");
   static_assert(STAGES == 2 || STAGES == 3, "stage count");
-  static_assert(!BKN || ((MODE == GM_F16 || MODE == GM_BF16) && EPI == GE_STORE), "[K][N] B");
+  static_assert(!BKN || ((MODE == GM_F16 || MODE == GM_BF16 || MODE == GM_I8) && EPI == GE_STORE), "[K][N] B");
   constexpr int NW = WM * WN;
   constexpr int NB = (EPI == GE_SWIGLU) ? 2 : 1;
   constexpr int BROW = (MODE == GM_W8) ? SB / 2 : SB;  // bytes of B per row in one stage
@@ -279,6 +287,11 @@ gemm_kernel(GemmArgs p) {
     else if constexpr (KNSEG == 2) return (row >> 1) & 1;
     else return 0;
   };
+  // int8: 16-byte chunks, KRW rows per 256-byte bank window; the chunk is
+  // XORed with twice the row's window index among 8 consecutive rows, so an
+  // even chunk and its odd neighbour (read together) never collide
+  constexpr int KRW = KCPR >= 16 ? 1 : 16 / KCPR;
+  auto swz_kn8 = [](int row) -> int { return ((row / KRW) & (8 / KRW - 1)) << 1; };
   const int nk = (int)((p.K + BKE - 1) / BKE);
   const uint32_t kb_bytes = (uint32_t)(p.K * T::EB);
 
@@ -313,7 +326,8 @@ gemm_kernel(GemmArgs p) {
       static_for<B_PER_W>([&](auto ic) {
         const int blk = wave + decltype(ic)::value * NW;
         const int row = blk * KRPB + lane / KCPR, pc = lane % KCPR;
-        const int lcol = (((pc >> 2) ^ swz_kn(row)) << 2) | (pc & 3);  // logical chunk
+        const int lcol = MODE == GM_I8 ? (pc ^ swz_kn8(row))                    // logical chunk
+                                       : ((((pc >> 2) ^ swz_kn(row)) << 2) | (pc & 3));
         const uint32_t k = (uint32_t)kt * (uint32_t)BKE + (uint32_t)row;
         uint32_t off = k * ldb_b + (uint32_t)lcol * 16u;
         if (k >= (uint32_t)p.K) off = 0x80000000u;
@@ -376,7 +390,22 @@ gemm_kernel(GemmArgs p) {
       const int row = wm * WTM + i * 32 + lrow;
       fa[s][i] = *reinterpret_cast<const v4i*>(sa + row * SB + ((ca ^ swz(row)) << 4));
     });
-    if constexpr (BKN) {
+    if constexpr (BKN && MODE == GM_I8) {
+      const int G = lane >> 4, i = lane & 15;
+      typedef __attribute__((address_space(3))) v2i* lds_v2i_t;
+      static_for<TN>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        const int colb = wn * WTN + 32 * j + 16 * (G & 1) + 8 * (i & 1);  // byte (column) in the row
+        v2i hv[2];
+        static_for<2>([&](auto hc) {
+          constexpr int h = decltype(hc)::value;
+          const int row = 32 * ks + 16 * (G >> 1) + 8 * h + (i >> 1);
+          const char* a = sa + A_BYTES + row * KROWB + (((colb >> 4) ^ swz_kn8(row)) << 4) + (colb & 15);
+          hv[h] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_t)a);
+        });
+        fb[s][0][j] = v4i{hv[0][0], hv[0][1], hv[1][0], hv[1][1]};
+      });
+    } else if constexpr (BKN) {
       const int G = lane >> 4, i = lane & 15;
       static_for<TN>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
@@ -776,7 +805,7 @@ static void launch_one(const GemmArgs& a, hipStream_t s) {
   const unsigned parts = a.k_split > 0 ? (unsigned)((a.K + a.k_split - 1) / a.k_split) : 1u;
   const dim3 grid((unsigned)tiles, parts), block(64 * WM * WN);
   const bool edge = a.M % BM != 0 || a.N % BN != 0;
-  if constexpr ((MODE == GM_F16 || MODE == GM_BF16) && EPI == GE_STORE) {
+  if constexpr ((MODE == GM_F16 || MODE == GM_BF16 || MODE == GM_I8) && EPI == GE_STORE) {
     if (a.b_kn) {
       if (edge) gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, true, true, STAGES><<<grid, block, 0, s>>>(a);
       else gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, false, true, STAGES><<<grid, block, 0, s>>>(a);

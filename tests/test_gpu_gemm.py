@@ -165,6 +165,38 @@ def test_gemm_i8_every_config(hx, dev, cfg, K):
     assert np.array_equal(got, oracle.gemm_i8_i32(a, b)), hx.config_get(1, cfg)["name"]
 
 
+@pytest.mark.parametrize("shape", [(384, 640, 1024), (200, 144, 272), (64, 2048, 4096)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_gemm_i8_kn_in_place_every_config(hx, dev, shape):
+    """int8 B in the linalg [K][N] orientation read in place by the tiled
+    kernel (transposing 8-bit LDS reads, no transposed copy): every config
+    bit-exact, edge tiles and a K tail included, and the fused dequant."""
+    import torch
+    M, N, K = shape
+    a, b = i8((M, K), 160), i8((K, N), 161)
+    want = oracle.gemm_i8_i32(a, b)
+    ad, bd = to_dev(a, dev), to_dev(b, dev)
+    hx.manifest_enable(True)
+    hx.manifest_clear()
+    try:
+        for cfg in range(hx.config_count(1)):
+            hx.config_select(1, M, N, K, cfg)
+            try:
+                got = to_np(hx.gemm_i8(ad, bd, b_layout="kn"))
+            finally:
+                hx.config_select(1, M, N, K, -1)
+            assert np.array_equal(got, want), hx.config_get(1, cfg)["name"]
+        recs = hx.manifest()["records"]
+    finally:
+        hx.manifest_enable(False)
+    assert recs and all(r["weight"] == "argument-kn" and r["plan"] == "mfma-tiled" for r in recs), recs
+    sa = rng(162).uniform(0.001, 0.02, M).astype(np.float32)
+    sb = rng(163).uniform(0.001, 0.02, N).astype(np.float32)
+    c = hx.gemm_i8(ad, bd, b_layout="kn", row_scale=to_dev(sa, dev), col_scale=to_dev(sb, dev),
+                   out_dtype=torch.float16)
+    assert np.array_equal(to_np(c).view(np.uint16), oracle.dequant_i32_f16(want, sa, sb).view(np.uint16))
+
+
 @pytest.mark.parametrize("out", ["i32", "f16", "bf16", "f32"])
 @pytest.mark.parametrize("name", ["256x256_w2x4_k2", "128x128_w2x2_k2", "64x64_w2x2_k4"])
 def test_gemm_i8_split_k_dequant_bitexact(hx, dev, name, out):

@@ -25,7 +25,10 @@ def test_manifest_records_plans_and_reasons(hx, dev):
         b = torch.randint(-127, 128, (512, 512), dtype=torch.int8, device=dev, generator=g)
         for _ in range(3):
             hx.gemm_i8(a, b, b_layout="nk")                      # aligned -> tiled
-        hx.gemm_i8(a, b, b_layout="kn")                          # KN -> transposed into workspace
+        hx.gemm_i8(a, b, b_layout="kn")                          # KN -> read in place (tiled)
+        hx.gemm_i8(a, b[:, :504].contiguous(), b_layout="kn")    # KN, N = 504 -> transposed into workspace
+        a_tall = torch.randint(-127, 128, (2056, 512), dtype=torch.int8, device=dev, generator=g)
+        hx.gemm_i8(a_tall, b, b_layout="kn")                     # KN, M = 2056 -> read in place
         hx.gemm_i8(a[:, :112], b[:, :112], b_layout="nk")        # K=112 bytes -> shallow-k, generic
         hx.gemm_i8(a[:, :496], b[:36, :496].contiguous(), b_layout="nk")  # strided A, N=36: tiled
         hx.gemm_i8(a[:, :504], b[:36, :504].contiguous(), b_layout="nk")  # ldb=504 -> row-stride
@@ -55,7 +58,9 @@ def test_manifest_records_plans_and_reasons(hx, dev):
     r = find(entry="hx_gemm_i8", m=512, n=512, k=512, weight="argument", plan="mfma-tiled")
     assert r["calls"] == 3 and r["reason"] == "selected-aligned" and r["config_source"] == "default"
     assert r["a"] == "i8" and r["c"] == "i32"
-    assert find(entry="hx_gemm_i8", weight="transposed-to-workspace")["plan"] == "mfma-tiled"
+    assert find(entry="hx_gemm_i8", weight="argument-kn", n=512)["plan"] == "mfma-tiled"
+    assert find(entry="hx_gemm_i8", weight="transposed-to-workspace", n=504)["plan"] == "mfma-tiled"
+    assert find(entry="hx_gemm_i8", weight="argument-kn", m=2056)["plan"] == "mfma-tiled"
     assert find(entry="hx_gemm_i8", k=112)["reason"] == "shallow-k"
     assert find(entry="hx_gemm_i8", k=112)["plan"] == "mfma-generic"
     assert find(entry="hx_gemm_i8", n=38)["reason"] == "n-granularity"
