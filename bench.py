@@ -731,6 +731,59 @@ def mfma_from_pmc(pmc_csv: str, keys_json: str, command: str) -> str:
     return "\n".join(lines) + "\n"
 
 
+def stats_from_trace(stats_csv: str, trace_csv: str, bench_json: str, command: str) -> str:
+    """Markdown summary of a ``rocprofv3 --kernel-trace --stats`` run of
+    the bench: the hx kernels of the stats CSV, the phases of the trace
+    (consecutive dispatches of one kernel with one grid, >= 20 of them) and,
+    beside the bench line's own live timing, the trace's mean for the
+    headline kernel over its last phase of at least ``steps`` dispatches."""
+    import csv
+    import statistics
+    rows = [r for r in csv.DictReader(open(stats_csv)) if "hx::" in r.get("Name", "")]
+    lines = ["# Kernel durations, default `bench.py` run (rocprofv3 kernel trace)", "",
+             f"Command: `{command}`", "",
+             "The run includes the tile search (every compiled config of each tuned family is "
+             "timed, so each config appears) and then the timed steps with the champion config.", "",
+             "## Kernel statistics (hx kernels; durations in us)", "",
+             "| kernel | calls | avg | min | max | % of GPU time |", "|---|---:|---:|---:|---:|---:|"]
+    rows.sort(key=lambda r: -float(r["Percentage"]))
+    for r in rows[:60]:
+        lines.append(f"| `{r['Name']}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                     f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.2f} |")
+    trace = list(csv.DictReader(open(trace_csv)))
+    trace.sort(key=lambda r: int(r["Start_Timestamp"]))
+    phases = []
+    for r in trace:
+        name = r["Kernel_Name"]
+        if "hx::" not in name:
+            continue
+        key = (name, r.get("Grid_Size", ""))
+        d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        if phases and phases[-1][0] == key:
+            phases[-1][1].append(d)
+        else:
+            phases.append((key, [d]))
+    lines += ["", "## Phases of the trace (>= 20 consecutive dispatches; us)", "",
+              "| kernel | grid (work-items) | dispatches | mean | median |", "|---|---:|---:|---:|---:|"]
+    for (name, grid), ds in phases:
+        if len(ds) >= 20:
+            lines.append(f"| `{name.replace('void ', '')}` | {grid} | {len(ds)} | {statistics.mean(ds):.2f} | "
+                         f"{statistics.median(ds):.2f} |")
+    line = json.loads(Path(bench_json).read_text().strip().splitlines()[-1])
+    head = line["config"]["kernel"]
+    steps = int(line["steps"])
+    cand = [(k, ds) for k, ds in phases if k[0].startswith("void hx::gemm_kernel<0, 256, 256") and len(ds) >= steps]
+    lines += ["", "## Agreement with the bench line", "",
+              f"The bench line (same process, under the profiler) reports {line['kernel_us']} us per launch for "
+              f"the headline kernel ({head}), from one HIP event pair on the launch stream."]
+    if cand:
+        (name, grid), ds = cand[-1]
+        lines.append(f"The trace's last phase of that kernel with >= {steps} dispatches ({len(ds)} dispatches, "
+                     f"`{name.replace('void ', '')}`) has mean {statistics.mean(ds):.2f} us, median "
+                     f"{statistics.median(ds):.2f} us.")
+    return "\n".join(lines) + "\n"
+
+
 def ceilings() -> dict:
     """What this box sustains, timed with HIP events over back-to-back
     launches (the way every kernel of the bench line is timed) using the
@@ -817,6 +870,8 @@ def main() -> int:
                     help="with --pmc-workload: write the launch sequence the counter parsers read")
     ap.add_argument("--traffic-from", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "KEYS_JSON"),
                     help="print the traffic.txt lines of two --pmc-workload counter CSVs and exit")
+    ap.add_argument("--stats-from", nargs=4, metavar=("STATS_CSV", "TRACE_CSV", "BENCH_JSON", "COMMAND"),
+                    help="markdown summary of a rocprofv3 --kernel-trace --stats run of the bench")
     ap.add_argument("--mfma-from", nargs=3, metavar=("PMC_CSV", "KEYS_JSON", "COMMAND"),
                     help="print the MFMA counter summary of a --pmc-workload counter CSV (and the "
                          "command that made it) and exit")
@@ -828,6 +883,9 @@ def main() -> int:
 
     if args.traffic_from:
         print(traffic_from_pmc(*args.traffic_from), end="")
+        return 0
+    if args.stats_from:
+        print(stats_from_trace(*args.stats_from), end="")
         return 0
     if args.mfma_from:
         print(mfma_from_pmc(*args.mfma_from), end="")
