@@ -757,7 +757,10 @@ def stats_from_trace(stats_csv: str, trace_csv: str, bench_json: str, command: s
         name = r["Kernel_Name"]
         if "hx::" not in name:
             continue
-        key = (name, r.get("Grid_Size", ""))
+        grid = r.get("Grid_Size") or ""
+        if not grid and r.get("Grid_Size_X"):
+            grid = str(int(r["Grid_Size_X"]) * int(r.get("Grid_Size_Y") or 1) * int(r.get("Grid_Size_Z") or 1))
+        key = (name, grid)
         d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
         if phases and phases[-1][0] == key:
             phases[-1][1].append(d)
@@ -772,7 +775,12 @@ def stats_from_trace(stats_csv: str, trace_csv: str, bench_json: str, command: s
     line = json.loads(Path(bench_json).read_text().strip().splitlines()[-1])
     head = line["config"]["kernel"]
     steps = int(line["steps"])
-    cand = [(k, ds) for k, ds in phases if k[0].startswith("void hx::gemm_kernel<0, 256, 256") and len(ds) >= steps]
+    # the headline config's kernel with no edge tiles and a [N][K] B
+    import re
+    m = re.match(r"(\d+)x(\d+)_w(\d+)x(\d+)", head)
+    prefix = f"hx::gemm_kernel<0, {m[1]}, {m[2]}, {m[3]}, {m[4]}, 0, " if m else "hx::gemm_kernel<0, "
+    cand = [(k, ds) for k, ds in phases
+            if k[0].replace("void ", "").startswith(prefix) and ", false, false," in k[0] and len(ds) >= steps]
     lines += ["", "## Agreement with the bench line", "",
               f"The bench line (same process, under the profiler) reports {line['kernel_us']} us per launch for "
               f"the headline kernel ({head}), from one HIP event pair on the launch stream."]

@@ -380,12 +380,18 @@ static int gemv_untuned(int op, int64_t M, int64_t N, int64_t K) {
     if (M <= 4) return 5;
     return K >= 8192 ? 0 : 1;
   }
-  // untuned choice from the MI355X sweep (int8, N = 11008, K = 4096): LDS-staged
-  // activations and one column tile per workgroup for M <= 4 -- staged by
-  // direct-to-LDS loads for M <= 2, through registers for M = 3, 4 (the
-  // launcher falls back to the register-fragment base config when the rows
-  // do not fit in LDS) -- and four tiles (activation fragments reused 4x)
-  // over 8 waves with every K chunk in flight at once for larger M
+  // untuned choice from the MI355X sweep (int8, K = 4096).  When the
+  // 16-column tiles need three per workgroup to fit one workgroup per CU
+  // (N = 11008: 688 tiles, 230 workgroups), the three-tile configs: 16
+  // waves for M <= 4, 8 for larger M (9.24 / 9.35 / 10.08 us at M = 1 / 4 /
+  // 16 against 9.43 / 10.14 / 11.07 for the configs below).  Otherwise
+  // LDS-staged activations and one column tile per workgroup for M <= 4 --
+  // staged by direct-to-LDS loads for M <= 2, through registers for M = 3, 4
+  // (the launcher falls back to the register-fragment base config when the
+  // rows do not fit in LDS) -- and four tiles (activation fragments reused
+  // 4x) over 8 waves with every K chunk in flight at once for larger M.
+  const int64_t tiles = (N + 15) / 16;
+  if ((tiles + 255) / 256 == 3) return M <= 4 ? 20 : 19;
   return M <= 2 ? 11 : M <= 4 ? 5 : 10;
 }
 

@@ -603,6 +603,10 @@ static const GemvStreamEntry kGemvStream[] = {
     {{2, 8, "rows4_ct2_kw8", 0, 16, 4}, HX_GR(2, 8, 4, 4)},
     {{4, 8, "rows4_ct4_kw8", 0, 17, 4}, HX_GR(4, 8, 2, 4)},
     {{1, 4, "rows4_ct1_kw4", 0, 18, 4}, HX_GR(1, 4, 8, 4)},
+    // three tiles: 230 workgroups at N = 11008 (four tiles leave 172 of 256
+    // CUs busy, two re-read the activation fragments twice as often)
+    {{3, 8, "packed_ct3_kw8", 0, 19, 1}, HX_GV(3, 8, 8, XS_NONE, false)},
+    {{3, 16, "packed_ct3_kw16", 0, 20, 1}, HX_GV(3, 16, 4, XS_NONE, false)},
 };
 #undef HX_GR
 #undef HX_GV
