@@ -792,7 +792,7 @@ def stats_from_trace(stats_csv: str, trace_csv: str, bench_json: str, command: s
     return "\n".join(lines) + "\n"
 
 
-def ceilings() -> dict:
+def ceilings(hx=None) -> dict:
     """What this box sustains, timed with HIP events over back-to-back
     launches (the way every kernel of the bench line is timed) using the
     probes of libhxprobe.so: the launch period of an empty kernel, a
@@ -858,7 +858,57 @@ def ceilings() -> dict:
         out[f"mfma_i8_4waves_{nr}_lds_per_16"] = {
             "us_per_launch": round(ms * 1e3, 2), "TOPS": round(ops.value / (ms * 1e-3) / 1e12, 1),
             "frac_of_5000": round(ops.value / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
+    if hx is not None:
+        out.update(operand_data_ceiling(hx))
     return out
+
+
+def operand_data_ceiling(hx) -> dict:
+    """The headline product (hx_gemm_i8, 4096^3, fp16 dequant, the same
+    config and binary as the bench line) timed on operands of different
+    value ranges.  The arithmetic and every memory access are identical;
+    only the bits the MFMA arrays switch differ, so the spread is the chip's
+    power and current management reacting to the data."""
+    import torch
+    M = N = K = 4096
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(99)
+    sa = torch.empty(M, dtype=torch.float32, device=dev).uniform_(0.001, 0.02, generator=g)
+    sb = torch.empty(N, dtype=torch.float32, device=dev).uniform_(0.001, 0.02, generator=g)
+    c = torch.empty((M, N), dtype=torch.float16, device=dev)
+    cfg_idx = hx.config_lookup(1, M, N, K)
+    res = {}
+    for label, lo, hi in (("zero", 0, 0), ("one", 1, 1), ("uniform_-1_1", -1, 1), ("uniform_-15_15", -15, 15),
+                          ("uniform_-127_127", -127, 127)):
+        a = torch.randint(lo, hi + 1, (M, K), dtype=torch.int8, device=dev, generator=g)
+        bt = torch.randint(lo, hi + 1, (N, K), dtype=torch.int8, device=dev, generator=g)
+        step = hx.bind_gemm_i8(a, bt, c, b_layout="nk", row_scale=sa, col_scale=sb)
+        ms, _ = event_timed([step], 200)
+        tops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+        res[f"gemm_i8_4096_dequant_operands_{label}"] = {
+            "us_per_launch": round(ms * 1e3, 2), "TOPS": round(tops, 1),
+            "frac_of_5000": round(tops / PEAK_INT8_TOPS, 4),
+            "config": hx.config_get(1, cfg_idx)["name"] if cfg_idx >= 0 else "default"}
+        del a, bt
+    # the W8A16 product of the FFN's gate projection (f16 MFMA on int8 weights
+    # widened in registers): activations and weights zero, or as configs[4]
+    Mw, Nw, Kw = 2048, 11008, 4096
+    s16 = torch.empty(Nw, dtype=torch.float16, device=dev).uniform_(0.001, 0.02, generator=g)
+    y = torch.empty((Mw, Nw), dtype=torch.float16, device=dev)
+    for label, zero in (("zero", True), ("ffn_data", False)):
+        x = torch.zeros((Mw, Kw), dtype=torch.float16, device=dev) if zero else \
+            torch.randn((Mw, Kw), dtype=torch.float16, device=dev, generator=g)
+        w = torch.zeros((Kw, Nw), dtype=torch.int8, device=dev) if zero else \
+            torch.randint(-127, 128, (Kw, Nw), dtype=torch.int8, device=dev, generator=g)
+        rw = hx.ResidentWeight(w, s16, layout="kn")
+        ms, _ = event_timed([hx.bind_matmul_resident(x, rw, y)], 50)
+        tf = 2.0 * Mw * Nw * Kw / (ms * 1e-3) / 1e12
+        res[f"gemm_w8a16_2048x11008x4096_operands_{label}"] = {
+            "us_per_launch": round(ms * 1e3, 2), "TFLOPS": round(tf, 1),
+            "frac_of_2500": round(tf / PEAK_F16_TFLOPS, 4)}
+        rw.release()
+        del x, w
+    return res
 
 
 def main() -> int:
@@ -909,7 +959,7 @@ def main() -> int:
         print(f"bench.py: hx_init failed: {hx._abi.last_error()}", file=sys.stderr)
         return 1
     if args.ceilings:
-        print(json.dumps(ceilings()), flush=True)
+        print(json.dumps(ceilings(hx)), flush=True)
         return 0
     if args.pmc_workload:
         pmc_workload(hx, args.pmc_keys)
