@@ -16,6 +16,10 @@ const GemmEntry* gemm_table_w8(int& n) {
     // K in two parts (binary32 partials and a merge): the FFN down
     // projection's 2048x4096 output is 128 tiles of 256x256 for 256 CUs
     {{256, 256, 2, 4, GE_STORE, "256x256_w2x4_k2", 1, 1.00f, 2}, &launch_one<GM_W8, 256, 256, 2, 4, GE_STORE>},
+    // the same output as 256 tiles of half the width, eight waves of 64x64
+    // each: the chip is full without a K split, so no partials and no merge
+    {{256, 128, 4, 2, GE_STORE, "256x128_w4x2", 1, 0.90f}, &launch_one<GM_W8, 256, 128, 4, 2, GE_STORE>},
+    {{128, 256, 2, 4, GE_STORE, "128x256_w2x4", 1, 0.90f}, &launch_one<GM_W8, 128, 256, 2, 4, GE_STORE>},
     // small tiles with K in parts: more workgroups per CU for skinny M
     {{128, 128, 2, 2, GE_STORE, "128x128_w2x2_k2", 2, 0.89f, 2}, &launch_one<GM_W8, 128, 128, 2, 2, GE_STORE>},
     {{64, 64, 2, 2, GE_STORE, "64x64_w2x2_k4", 4, 0.61f, 4}, &launch_one<GM_W8, 64, 64, 2, 2, GE_STORE>},
