@@ -182,13 +182,21 @@ def bench_gemm_i8(hx, steps: int, warmup: int, tune_on: bool = True):
         step()
     hx.manifest_enable(False)
     plan = hx.manifest()["records"]
+    # the timed region: K back-to-back steps between one HIP event pair on
+    # the launch stream, inside the host-clock bracket (both synchronized)
+    s = torch.cuda.current_stream()
+    ev_a, ev_b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    ev_a.record(s)
     for _ in range(steps):
         step()
+    queued_ms = (time.perf_counter() - t0) * 1e3
+    ev_b.record(s)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    ev_ms, fed = event_timed([step], steps)
+    ev_ms = ev_a.elapsed_time(ev_b) / steps
+    fed = queued_ms < ev_ms * steps  # the host stayed ahead of the device
     ops = 2.0 * M * N * K
     tops_wall = ops / (wall_ms * 1e-3) / 1e12
     tops_kernel = ops / (ev_ms * 1e-3) / 1e12
