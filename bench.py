@@ -933,6 +933,28 @@ def operand_data_ceiling(hx) -> dict:
             "frac_of_2500": round(tf / PEAK_F16_TFLOPS, 4)}
         rw.release()
         del x, w
+    # the whole SwiGLU FFN block with zero operands and with the
+    # bench line's data (the same untuned configurations in both)
+    T, H, I = 2048, 4096, 11008
+    for label, zero in (("zero", True), ("ffn_data", False)):
+        def wt(k, n):
+            w = torch.zeros((k, n), dtype=torch.int8, device=dev) if zero else \
+                torch.randint(-127, 128, (k, n), dtype=torch.int8, device=dev, generator=g)
+            s = torch.empty(n, dtype=torch.float16, device=dev).uniform_(0.5, 1.5, generator=g) / (127 * (k / 3) ** 0.5)
+            return hx.ResidentWeight(w, s.half(), layout="kn")
+        ws = [wt(H, I), wt(H, I), wt(I, H)]
+        x = torch.zeros((T, H), dtype=torch.float16, device=dev) if zero else \
+            torch.randn((T, H), dtype=torch.float16, device=dev, generator=g)
+        gamma = torch.randn(H, dtype=torch.float16, device=dev, generator=g) * 0.1 + 1.0
+        y = torch.empty_like(x)
+        ms, _ = event_timed([lambda: hx.swiglu_ffn(x, gamma, 1e-6, *ws, out=y)], 20)
+        tf = 3 * 2.0 * T * H * I / (ms * 1e-3) / 1e12
+        res[f"swiglu_ffn_2048x4096x11008_operands_{label}"] = {
+            "us_per_launch": round(ms * 1e3, 1), "TFLOPS": round(tf, 1),
+            "frac_of_2500": round(tf / PEAK_F16_TFLOPS, 4)}
+        for w in ws:
+            w.release()
+        del x, y
     return res
 
 
