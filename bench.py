@@ -176,6 +176,12 @@ def bench_gemm_i8(hx, steps: int, warmup: int, tune_on: bool = True):
     if tune_on:
         tune_report = tune(hx, 1, M, N, K)
 
+    # a one-row softmax before the warmup and after the timed steps: other
+    # hx kernels around them make the headline's launches one phase of a
+    # kernel trace (bench.py --stats-from finds it by its length)
+    marker_x = torch.zeros((1, 64), dtype=torch.float16, device=dev)
+    marker = lambda: hx.softmax(marker_x)  # noqa: E731
+    marker()
     hx.manifest_clear()
     hx.manifest_enable(True)
     for _ in range(warmup):
@@ -197,6 +203,7 @@ def bench_gemm_i8(hx, steps: int, warmup: int, tune_on: bool = True):
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
     ev_ms = ev_a.elapsed_time(ev_b) / steps
     fed = queued_ms < ev_ms * steps  # the host stayed ahead of the device
+    marker()
     ops = 2.0 * M * N * K
     tops_wall = ops / (wall_ms * 1e-3) / 1e12
     tops_kernel = ops / (ev_ms * 1e-3) / 1e12
@@ -804,12 +811,24 @@ def stats_from_trace(stats_csv: str, trace_csv: str, bench_json: str, command: s
     import re
     m = re.match(r"(\d+)x(\d+)_w(\d+)x(\d+)", head)
     prefix = f"hx::gemm_kernel<0, {m[1]}, {m[2]}, {m[3]}, {m[4]}, 0, " if m else "hx::gemm_kernel<0, "
+    warm = int(line.get("warmup", 0))
     cand = [(k, ds) for k, ds in phases
             if k[0].replace("void ", "").startswith(prefix) and ", false, false," in k[0] and len(ds) >= steps]
+    # the headline's own phase: its warmup and timed steps between the two
+    # marker launches (exactly warmup + steps dispatches); else the last
+    # long enough phase of that kernel
+    exact = [(k, ds) for k, ds in cand if len(ds) == warm + steps]
     lines += ["", "## Agreement with the bench line", "",
               f"The bench line (same process, under the profiler) reports {line['kernel_us']} us per launch for "
-              f"the headline kernel ({head}), from one HIP event pair on the launch stream."]
-    if cand:
+              f"the headline kernel ({head}), from one HIP event pair around its {steps} timed steps on the "
+              f"launch stream."]
+    if exact:
+        (name, grid), ds = exact[0]
+        timed = ds[-steps:]
+        lines.append(f"The trace's phase of that kernel with the bench's {warm} warmup and {steps} timed dispatches "
+                     f"(`{name.replace('void ', '')}`): the timed {steps} have mean {statistics.mean(timed):.2f} us, "
+                     f"median {statistics.median(timed):.2f} us.")
+    elif cand:
         (name, grid), ds = cand[-1]
         lines.append(f"The trace's last phase of that kernel with >= {steps} dispatches ({len(ds)} dispatches, "
                      f"`{name.replace('void ', '')}`) has mean {statistics.mean(ds):.2f} us, median "
