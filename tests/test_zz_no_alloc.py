@@ -2,8 +2,8 @@
 intermediates in the library's fixed per-GPU scratch.  Its output must equal
 hx_swiglu_ffn's bit for bit (the same kernels and configurations run), on two
 calls in a row, the second with fewer tokens; it must allocate no device
-memory; and a shape whose intermediates exceed the scratch is refused
-before anything runs."""
+memory; it can be captured into a HIP graph and replayed; and a shape whose
+intermediates exceed the scratch is refused before anything runs."""
 import ctypes
 
 import numpy as np
@@ -74,6 +74,43 @@ def test_noalloc_matches_and_allocates_nothing(hx, dev):
             a, b = to_np(refs[T]), to_np(ys[T])
             assert np.isfinite(a.astype(np.float32)).all()
             assert np.array_equal(a.view(np.uint16), b.view(np.uint16)), f"T={T}"
+    finally:
+        Wg.release(); Wu.release(); Wd.release()
+
+
+@pytest.mark.parametrize("T", [256, 40])
+def test_noalloc_in_a_hip_graph(hx, dev, T):
+    """The call captured into a HIP graph (256 tokens: the GEMM path; 40: the
+    decode GEMVs), then three replays, each after eager work that rewrites
+    the activations and a synchronization, each equal bit for bit to the
+    eager hx_swiglu_ffn on the same activations."""
+    import torch
+    Wg, Wu, Wd = _weights(hx, dev, 520)
+    assert hx._abi.load().hx_init() == 0, hx._abi.last_error()
+    try:
+        gamma = to_dev(rng(521).normal(1, 0.1, H).astype(np.float16), dev)
+        x = to_dev(rng(522).normal(0, 1, (T, H)).astype(np.float16), dev)
+        y = torch.zeros((T, H), dtype=torch.float16, device=dev)
+        ref = torch.zeros((T, H), dtype=torch.float16, device=dev)
+        side = torch.cuda.Stream()
+        with torch.cuda.stream(side):  # warm-up outside the capture
+            assert _noalloc(hx, x, gamma, 1e-6, Wg, Wu, Wd, y, side) == 0, hx._abi.last_error()
+        side.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            rc = _noalloc(hx, x, gamma, 1e-6, Wg, Wu, Wd, y, torch.cuda.current_stream())
+        assert rc == 0, hx._abi.last_error()
+        for i in range(3):
+            x.copy_(to_dev(rng(530 + i).normal(0, 1, (T, H)).astype(np.float16), dev))
+            y.fill_(9.0)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            hx.swiglu_ffn(x, gamma, 1e-6, Wg, Wu, Wd, out=ref)
+            a, b = to_np(ref), to_np(y)
+            assert np.isfinite(a.astype(np.float32)).all()
+            assert np.array_equal(a.view(np.uint16), b.view(np.uint16)), f"T={T} replay {i}"
+        del g
     finally:
         Wg.release(); Wu.release(); Wd.release()
 
