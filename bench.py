@@ -327,6 +327,14 @@ def cpu_baselines_secondary(march: str) -> dict:
     out["gemm_f16_256"] = dict(base, value=round(t * 1e6, 2), unit="us", cores=threads,
                                tflops=round(2 * 256 ** 3 / t / 1e12, 5),
                                sample="full fp16 256^3 matmul, hxo_matmul, median of 5 after a warm-up")
+    # the reference's published fp16 matmul shapes (S1, S2, S3)
+    for (M, N, K) in REF_SHAPES:
+        a = r.uniform(-1, 1, (M, K)).astype(np.float16)
+        b = r.uniform(-1, 1, (K, N)).astype(np.float16)
+        t = _median_time(lambda: oracle.matmul(a, b), 5)
+        out[f"ref_{M}x{N}x{K}"] = dict(base, value=round(t * 1e6, 2), unit="us", cores=threads,
+                                       tflops=round(2.0 * M * N * K / t / 1e12, 5),
+                                       sample=f"full fp16 {M}x{N}x{K} matmul, hxo_matmul, median of 5 after a warm-up")
     # C5: the FFN block on a 64-token sample (tokens are independent rows)
     T, H, I = 64, 4096, 11008
     wg = r.integers(-127, 128, (H, I), dtype=np.int8)
@@ -517,6 +525,45 @@ def bench_gemm_f16_small(hx, iters: int = 200):
     return {"workload": "fp16 GEMM 256^3 (configs[0], latency-bound plumbing case)",
             "value": round(ev_ms * 1e3, 3), "unit": "us", "tflops": round(tf, 2),
             "roofline": roofline("mfma", tf, PEAK_F16_TFLOPS, "TFLOP/s")}
+
+
+#: the fp16 matmul shapes the reference publishes timings for (M, N, K;
+#: ROADMAP.md:98-100, M, N, K = 1024, 512, 64 in QHB/test/
+#: test_hmx_vector_readout_object_gate.py:94), with its frozen-build
+#: zero-knob medians on a Hexagon v79 NPU (us)
+REF_SHAPES = [(1024, 512, 64), (256, 64, 2048), (128, 128, 128)]
+REF_PUBLISHED_US = {(1024, 512, 64): 37.0, (256, 64, 2048): 32.0, (128, 128, 128): 3.0}
+
+
+def bench_reference_shapes(hx, iters: int = 200):
+    """fp16 C = A.B at the three shapes the reference publishes timings for
+    (A, B uniform [-1, 1], B in linalg [K][N], fp16 out), beside its numbers.
+    Different hardware (a phone NPU): context, not a baseline ratio."""
+    import torch
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(6)
+    res = []
+    for (M, N, K) in REF_SHAPES:
+        a = torch.empty((M, K), dtype=torch.float16, device=dev).uniform_(-1, 1, generator=g)
+        b = torch.empty((K, N), dtype=torch.float16, device=dev).uniform_(-1, 1, generator=g)
+        c = torch.empty((M, N), dtype=torch.float16, device=dev)
+        call = lambda a=a, b=b, c=c: hx.matmul(a, b, b_layout="kn", out=c)  # noqa: E731
+        hx.manifest_clear()
+        hx.manifest_enable(True)
+        call()
+        hx.manifest_enable(False)
+        plan = hx.manifest()["records"]
+        ev_ms, fed = event_timed([call], iters)
+        tf = 2.0 * M * N * K / (ev_ms * 1e-3) / 1e12
+        res.append({"workload": f"fp16 matmul {M}x{N}x{K} (the reference's published shape)",
+                    "value": round(ev_ms * 1e3, 3), "unit": "us", "tflops": round(tf, 3),
+                    "roofline": roofline("mfma", tf, PEAK_F16_TFLOPS, "TFLOP/s"),
+                    "kernel": f"{plan[0]['plan']}:{plan[0]['config']}" if plan else None,
+                    "reference_published_us": REF_PUBLISHED_US[(M, N, K)],
+                    "reference_hardware": "Hexagon v79 NPU (ROADMAP.md:98-100, frozen build, zero-knob "
+                                          "default); not comparable hardware",
+                    "queue_fed": fed})
+    return res
 
 
 def bench_ffn(hx, iters: int = 20, tune_on: bool = True, tune_fn=tune):
@@ -1053,6 +1100,8 @@ def main() -> int:
         secondary += bench_rows(hx)
         log("[bench] fp16 GEMM 256^3")
         secondary.append(bench_gemm_f16_small(hx))
+        log("[bench] fp16 matmul at the reference's published shapes")
+        secondary += bench_reference_shapes(hx)
         log("[bench] SwiGLU FFN")
         secondary.append(bench_ffn(hx, tune_on=tune_on))
         log("[bench] attention")
@@ -1071,6 +1120,7 @@ def main() -> int:
             keys = {"W8A16 GEMV M=1 ": "gemv_m1", "W8A16 GEMV M=4 ": "gemv_m4", "W8A16 GEMV M=16 ": "gemv_m16",
                     "softmax fp16": "softmax", "rmsnorm fp16": "rmsnorm", "fp16 GEMM 256^3": "gemm_f16_256",
                     "SwiGLU FFN": "ffn"}
+            keys.update({f"fp16 matmul {M}x{N}x{K} ": f"ref_{M}x{N}x{K}" for (M, N, K) in REF_SHAPES})
             for sec in secondary:
                 for prefix, key in keys.items():
                     if sec["workload"].startswith(prefix):

@@ -152,14 +152,16 @@ int gemm_default_config(int mode, int epi, int64_t M, int64_t N, int64_t K) {
   // occupancy-limited rounds instead picked 64x64 at 2048^3, where 128x128
   // measured 1.2-1.4x faster (f16 and int8).
   const int64_t ea = mode == GM_I8 ? 1 : 2;
+  // first pass: configs whose LDS ring K fills (at least as many K stages
+  // per part, the last one partial, as the ring holds); when K is shorter
+  // than every ring, a second pass takes any unsplit config
+  for (int pass = 0; pass < 2 && best < 0; ++pass)
   for (int i = 0; i < n; ++i) {
     const GemmConfig& c = t[i].cfg;
     if (c.epi != epi) continue;
     const int ks = c.ksplit > 1 ? c.ksplit : 1;
-    if (ks > 1 && K / ks < 512) continue;
-    // at least as many K stages (per part, the last one partial) as the
-    // LDS ring holds
-    if ((K / ks * ea + c.sb - 1) / c.sb < c.stages) continue;
+    if (ks > 1 && (pass == 1 || K / ks < 512)) continue;
+    if (pass == 0 && (K / ks * ea + c.sb - 1) / c.sb < c.stages) continue;
     const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * ks;
     const int64_t per_cu_i = (tiles + cus - 1) / cus;
     const double per_cu = (double)per_cu_i;
@@ -195,8 +197,11 @@ const char* gemm_fast_refusal(int mode, const GemmArgs& a) {
   } else if ((int64_t)256 * a.ldb * eb >= ((int64_t)1 << 31)) {
     return "offset-range";
   }
-  // at least two K stages of 128 bytes of A per row
-  if (a.K * ea <= 128) return "shallow-k";
+  // at least one 32-byte MFMA k-step of A per row.  K shorter than a
+  // config's stage ring is fine: the ring's extra stages load zeros through
+  // the buffer range (every config is tested exact at K below its ring),
+  // which for small K still beats the generic kernel by 3x.
+  if (a.K * ea < 32) return "shallow-k";
   // the epilogue stores (and reads the residual as) four consecutive outputs
   if (a.N % 4 != 0) return "n-granularity";
   if (a.ldc % 4 != 0 || !al16(a.c)) return "output-layout";

@@ -137,10 +137,8 @@ class Probe {
     if (c->bm > std::max<int64_t>(64, pad_pow2(m_)) || c->bn > std::max<int64_t>(64, pad_pow2(n_)))
       return "tile-exceeds-extent";
     if (c->ksplit > 1 && (k_ / c->ksplit) * es_of(ea_dt_) < 256) return "split-too-short";
-    // fewer K stages (the last one partial) than the ring holds: the extra
-    // stages would only load zeros
-    if (((c->ksplit > 1 ? k_ / c->ksplit : k_) * es_of(ea_dt_) + c->sb - 1) / c->sb < c->stages)
-      return "stages-exceed-k";
+    // a stage ring deeper than K runs (its extra stages load zeros): it is
+    // timed like any other config
     return nullptr;
   }
 

@@ -146,14 +146,15 @@ def test_gemm_i8_4096_cube(hx, dev):
 N_I8_CONFIGS = 15
 
 
-@pytest.mark.parametrize("K", [1024, 1072, 1152, 208, 144])
+@pytest.mark.parametrize("K", [1024, 1072, 1152, 208, 144, 112, 32])
 @pytest.mark.parametrize("cfg", range(N_I8_CONFIGS))
 def test_gemm_i8_every_config(hx, dev, cfg, K):
     """Every compiled int8 configuration is exact (the autotuner may pick
     any): edge tiles in M and N, K stage counts that leave each remainder of
     the three-stage ring (1072 = 16.75 stages of 64 bytes, 1152 = 18), K
-    shorter than the stage ring (208, 144) and, for the split configs, parts
-    of unequal length."""
+    shorter than the stage ring (208, 144), shorter than one stage (112, and
+    32: a single MFMA k-step) and, for the split configs, parts of unequal
+    length."""
     assert hx.config_count(1) == N_I8_CONFIGS, "new int8 configs: extend this test's range"
     M, N = 384, 640
     a, b = i8((M, K), 20), i8((K, N), 21)
@@ -262,7 +263,8 @@ def _vals(h, dtype):
     return oracle.bf16_bits_to_f32(h) if dtype == "bf16" else np.asarray(h, np.float32)
 
 
-F_SHAPES = [(256, 256, 256), (256, 256, 512), (1024, 512, 64), (100, 200, 72), (33, 65, 17), (512, 384, 1024)]
+F_SHAPES = [(256, 256, 256), (256, 256, 512), (1024, 512, 64), (256, 64, 2048), (128, 128, 128), (100, 200, 72),
+            (33, 65, 17), (512, 384, 1024)]
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
@@ -367,9 +369,12 @@ def test_matmul_w8a16_gemm(hx, dev, shape):
     assert_close(to_np(y).astype(np.float32), want.astype(np.float32), 1e-2, 1e-3, f"w8a16 {shape}")
 
 
+@pytest.mark.parametrize("K", [512, 64, 16])
 @pytest.mark.parametrize("op", [2, 4])
-def test_float_every_config(hx, dev, op):
-    M, N, K = 320, 448, 512
+def test_float_every_config(hx, dev, op, K):
+    """Every f16 and W8A16 configuration, incl. K shorter than one stage
+    (64) and equal to one k-step (16); the ring runs its extra stages on zero fill."""
+    M, N = 320, 448
     a = _fp("f16", (M, K), 70)
     if op == 2:
         b = _fp("f16", (N, K), 71)

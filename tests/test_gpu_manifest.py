@@ -29,7 +29,8 @@ def test_manifest_records_plans_and_reasons(hx, dev):
         hx.gemm_i8(a, b[:, :504].contiguous(), b_layout="kn")    # KN, N = 504 -> transposed into workspace
         a_tall = torch.randint(-127, 128, (2056, 512), dtype=torch.int8, device=dev, generator=g)
         hx.gemm_i8(a_tall, b, b_layout="kn")                     # KN, M = 2056 -> read in place
-        hx.gemm_i8(a[:, :112], b[:, :112], b_layout="nk")        # K=112 bytes -> shallow-k, generic
+        hx.gemm_i8(a[:, :16], b[:, :16], b_layout="nk")          # K=16 bytes -> shallow-k, generic
+        hx.gemm_i8(a[:, :112], b[:, :112], b_layout="nk")        # K=112 bytes, shorter than any ring: tiled
         hx.gemm_i8(a[:, :496], b[:36, :496].contiguous(), b_layout="nk")  # strided A, N=36: tiled
         hx.gemm_i8(a[:, :504], b[:36, :504].contiguous(), b_layout="nk")  # ldb=504 -> row-stride
         hx.gemm_i8(a, b[:38].contiguous(), b_layout="nk")         # N=38 -> n-granularity
@@ -61,8 +62,9 @@ def test_manifest_records_plans_and_reasons(hx, dev):
     assert find(entry="hx_gemm_i8", weight="argument-kn", n=512)["plan"] == "mfma-tiled"
     assert find(entry="hx_gemm_i8", weight="transposed-to-workspace", n=504)["plan"] == "mfma-tiled"
     assert find(entry="hx_gemm_i8", weight="argument-kn", m=2056)["plan"] == "mfma-tiled"
-    assert find(entry="hx_gemm_i8", k=112)["reason"] == "shallow-k"
-    assert find(entry="hx_gemm_i8", k=112)["plan"] == "mfma-generic"
+    assert find(entry="hx_gemm_i8", k=16)["reason"] == "shallow-k"
+    assert find(entry="hx_gemm_i8", k=16)["plan"] == "mfma-generic"
+    assert find(entry="hx_gemm_i8", k=112)["plan"] == "mfma-tiled"
     assert find(entry="hx_gemm_i8", n=38)["reason"] == "n-granularity"
     assert find(entry="hx_gemm_i8", n=36, k=496)["plan"] == "mfma-tiled"
     assert find(entry="hx_gemm_i8", n=36, k=504)["reason"] == "row-stride"  # ldb = 504

@@ -95,12 +95,12 @@ def test_drifted_canary_voids_the_round_and_keeps_earlier_pins(hx, dev):
 
 
 def test_refused_shape_pins_nothing(hx, dev):
-    # K = 112 int8 bytes is below the tiled kernel's two 128-byte stages:
-    # every configuration is refused, there is no champion
-    r = hx.search.tune(1, 112, 112, 112, canary_reference_us=-1.0, **FAST)
+    # K = 16 int8 bytes is below one 32-byte MFMA k-step: every
+    # configuration is refused, there is no champion
+    r = hx.search.tune(1, 112, 112, 16, canary_reference_us=-1.0, **FAST)
     assert all(e["status"] == "refused" and e["reason"] == "shallow-k" for e in r["entries"]), r["entries"]
     assert r["champion_index"] == -1 and not r["pinned"]
-    assert hx.config_lookup(1, 112, 112, 112) == r["control_index"]
+    assert hx.config_lookup(1, 112, 112, 16) == r["control_index"]
     # K = 100: the tuner's A rows (stride K) are not whole 16-byte chunks
     r = hx.search.tune(1, 100, 100, 100, canary_reference_us=-1.0, **FAST)
     reasons = [(e["status"], e["reason"]) for e in r["entries"]]
