@@ -658,7 +658,18 @@ extern "C" int hx_matmul(const hx_memref2d* a, int a_dtype, const hx_memref2d* b
     if (scale_dtype == HX_F16) sc16 = (const uint16_t*)vs.p;
     else sc32 = (const float*)vs.p;
   }
-  const bool gemv_rows = M <= kGemvMaxRows && !residual && c_dtype == (op == HX_OP_MATMUL_W8 ? HX_F16 : a_dtype);
+  // Argument weights: the decode GEMV for M <= 16, its row blocks up to
+  // kGemvRowsMaxM rows for a K-contiguous weight with enough column tiles;
+  // the tiled GEMM (K split) beyond.  Measured with argument weights (f16 /
+  // W8A16, K = 4096): at M = 17 the row blocks win with an [N][K] weight
+  // (f16 N = 4096: 11.1 against 13.8 us; W8A16 N = 2048: 8.6 against 13.7)
+  // and lose with a [K][N] one (transposed first: 25.1 against 14.0); at
+  // M = 32..64 the tiled GEMM wins (64 x 11008 f16: 20.7 against 36.5 us),
+  // and at N < 2048 by up to 3x (64 x 256 x 8192 f16: 14.2 against 37.1).
+  // Registered weights keep the row blocks to 64 rows (the FFN's decode path
+  // sizes its scratch for them).
+  const bool gemv_rows = (M <= 16 || (gemv_rows_route(M, N) && b_layout == HX_LAYOUT_NK)) &&
+                         M <= kGemvMaxRows && !residual && c_dtype == (op == HX_OP_MATMUL_W8 ? HX_F16 : a_dtype);
 
   // Decode shapes with weights in the [K][N] orientation: stream the weight
   // in place rather than transposing it into the workspace.
@@ -1190,7 +1201,10 @@ static int matmul_resident_impl(const View2& vx, hx_weight* w, const View2* vr, 
               gemv_packed_config(cfg)->name, pin ? "pinned" : "default", M <= 16 ? "min-rows" : "few-rows");
     return map_internal(launch_gemv_packed(cfg, v, w->packed, s), "gemv_packed");
   }
-  if (w->dtype != HX_I8 && M <= kGemvMaxRows && !vr && y_dt == x_dt) {
+  // An f16 / bf16 image is a [N][K] weight: the argument products' rule
+  // for the row blocks applies as it stands (the packed int8 weight above
+  // keeps them to kGemvMaxRows rows: its tiles read half the bytes).
+  if (w->dtype != HX_I8 && gemv_rows_route(M, w->N) && !vr && y_dt == x_dt) {
     GemvArgs v{};
     v.x = vx.p; v.ldx = vx.ld; v.w = nullptr; v.ldw = 0;
     v.scale = w->scale; v.y = vy.p; v.ldy = vy.ld; v.M = M; v.N = w->N; v.K = w->K;

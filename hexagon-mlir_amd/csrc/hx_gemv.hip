@@ -637,11 +637,13 @@ static int launch_gemv_stream(int cfg_idx, int wt, bool packed, const GemvArgs& 
   kGemvStream[cfg_idx].fn[slot](a, w, ldw, (int)kchunks, s);
   return HXI_OK;
 }
-// Measured at M = 17..64 (rotating resident weights): four tiles and four
-// row blocks when N leaves >= 160 such workgroups (int8 and f16,
-// N = 11008), else one tile with two or four row blocks (f16, N = 4096).
+// Measured at M = 17..64 (rotating resident weights): when N leaves >= 160
+// workgroups of four tiles (int8 and f16, N = 11008), two tiles and two row
+// blocks up to 32 rows (int8 M = 17 / 24: 16.9 / 19.7 us against 21.7 / 22.2
+// for four and four) and four tiles and four row blocks beyond; else one
+// tile with two or four row blocks (f16, N = 4096).
 int gemv_rows_default(int64_t M, int64_t N) {
-  if (N >= 160 * 64) return 17;
+  if (N >= 160 * 64) return M <= 32 ? 14 : 17;
   return M <= 32 ? 13 : 15;
 }
 int launch_gemv_packed(int cfg_idx, const GemvArgs& a, const int8_t* packed, hipStream_t s) {

@@ -103,6 +103,14 @@ struct GemvConfig {
 };
 // Largest M the decode GEMV takes (row-block configs).
 constexpr int kGemvMaxRows = 64;
+// hx_matmul with argument weights: 16 < M <= kGemvRowsMaxM rows take the
+// decode GEMV's row blocks when N >= kGemvRowsMinN (fewer 16-column tiles
+// leave most CUs idle); other skinny shapes take the tiled GEMM.
+constexpr int64_t kGemvRowsMaxM = 24;
+constexpr int64_t kGemvRowsMinN = 2048;
+// The decode GEMV's routing for an f16 / bf16 weight (argument or
+// registered) and an argument int8 one, both read as [N][K].
+inline bool gemv_rows_route(int64_t M, int64_t N) { return M <= 16 || (M <= kGemvRowsMaxM && N >= kGemvRowsMinN); }
 // Untuned row-block config for 16 < M <= kGemvMaxRows.
 int gemv_rows_default(int64_t M, int64_t N);
 bool gemv_fast_ok(const GemvArgs& a);

@@ -289,7 +289,9 @@ class Probe {
     const int xt = op_ == HX_OP_GEMV_BF16 ? DT_BF16 : DT_F16;
     out_dt_ = xt;
     exact_ = false;
-    if (m_ > kGemvMaxRows) family_reason_ = "family-shape";
+    // the shapes the products run on this family: the packed int8 weight's
+    // row blocks to kGemvMaxRows rows, the f16 / bf16 image's by the routing
+    if (m_ > kGemvMaxRows || (op_ != HX_OP_GEMV_W8 && !gemv_rows_route(m_, n_))) family_reason_ = "family-shape";
     const int64_t mm = std::min<int64_t>(m_, kGemvMaxRows);
     const size_t eb = es_of(wt_);
     const size_t img = op_ == HX_OP_GEMV_W8 ? (size_t)gemv_packed_bytes(n_, k_) : (size_t)n_ * k_ * eb;

@@ -582,20 +582,25 @@ def test_f32_quantisation_special_values(hx, dev):
     assert diag[6] == 0.0 and diag[7] == 2 ** -24 * 2
 
 
-def test_resident_f32_weight(hx, dev):
+@pytest.mark.parametrize("M,N", [(8, 512), (20, 2048), (40, 512)])
+def test_resident_f32_weight(hx, dev, M, N):
     """An f32 weight registers as its f16 quantisation: the resident product
-    equals the argument product of the quantised weight bit for bit, and an
-    identical f16 registration shares its handle."""
+    equals the argument product of the quantised weight in the same [N][K]
+    orientation bit for bit (the decode GEMV, its row blocks, and the tiled
+    GEMM), and an identical f16 registration shares its handle."""
     import torch
-    K, N = 384, 512
+    K = 384
     w32 = rng(85).normal(0, 0.5, (K, N)).astype(np.float32)
-    x = rng(86).normal(0, 1, (40, K)).astype(np.float16)
+    x = rng(86).normal(0, 1, (M, K)).astype(np.float16)
     W = hx.ResidentWeight(to_dev(w32, dev), layout="kn")
     W16 = hx.ResidentWeight(to_dev(_quant16(w32), dev), layout="kn")
     try:
         assert W.info()["dtype"] == 1 and W.handle == W16.handle and W.info()["refcount"] == 2
         got = to_np(hx.matmul_resident(to_dev(x, dev), W))
-        ref = to_np(hx.matmul(to_dev(x, dev), to_dev(_quant16(w32), dev), b_layout="kn"))
+        wq = np.ascontiguousarray(_quant16(w32).T)
+        ref = to_np(hx.matmul(to_dev(x, dev), to_dev(wq, dev), b_layout="nk"))
         assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+        want = x.astype(np.float64) @ _quant16(w32).astype(np.float64)
+        assert np.abs(got.astype(np.float64) - want).max() <= 2e-3 * np.abs(want).max()
     finally:
         W.release(); W16.release()

@@ -215,12 +215,15 @@ def test_matvec_n_is_one_fallbacks(hx, dev):
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
-@pytest.mark.parametrize("shape", [(17, 1000, 520), (32, 4096, 4096), (48, 11008, 1024), (64, 300, 8192), (63, 37, 72)],
+@pytest.mark.parametrize("shape", [(17, 2048, 520), (24, 4096, 4096), (20, 11008, 1024), (23, 2053, 72),
+                                   (17, 1000, 520), (25, 4096, 4096), (48, 11008, 1024), (64, 300, 8192), (63, 37, 72)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_decode_float_row_blocks(hx, dev, dtype, shape):
-    """16 < M <= 64: the streaming kernel with 2 or 4 blocks of 16 activation
-    rows (each weight fragment feeds every block), argument and resident."""
+    """16 < M <= 24 with N >= 2048: the streaming kernel with 2 blocks of 16
+    activation rows (each weight fragment feeds every block); fewer columns
+    or more rows: the tiled GEMM.  Argument and resident, same numerics."""
     M, N, K = shape
+    rows = M <= 24 and N >= 2048
     a = _fp(dtype, (M, K), 110)
     b = _fp(dtype, (K, N), 111)
     bt = _dev(np.ascontiguousarray(b.T), dtype, dev)
@@ -231,7 +234,10 @@ def test_decode_float_row_blocks(hx, dev, dtype, shape):
         recs = hx.manifest()["records"]
     finally:
         hx.manifest_enable(False)
-    assert [r["plan"] for r in recs] == ["gemv-stream"] and recs[0]["config"].startswith("rows"), recs
+    if rows:
+        assert [r["plan"] for r in recs] == ["gemv-stream"] and recs[0]["config"].startswith("rows"), recs
+    else:
+        assert [r["plan"] for r in recs] in (["mfma-tiled"], ["mfma-generic"]), recs  # N = 37: generic
     _check(to_np(c), a, b, dtype, f"rows {dtype} {shape}")
     rw = hx.ResidentWeight(bt, None, layout="nk")
     try:
@@ -241,9 +247,9 @@ def test_decode_float_row_blocks(hx, dev, dtype, shape):
 
 
 def test_decode_row_blocks_every_config(hx, dev):
-    """Every config of the shared table at M = 40 (f16) and M = 24 (int8):
-    configs with too few row blocks run as the row-block default."""
-    M, N, K = 40, 523, 1024
+    """Every config of the shared table at M = 24 (f16, N = 2059; int8,
+    N = 523): configs with too few row blocks run as the row-block default."""
+    M, N, K = 24, 2059, 1024
     a = _fp("f16", (M, K), 120)
     b = _fp("f16", (K, N), 121)
     rw = hx.ResidentWeight(_dev(b, "f16", dev), None, layout="kn")
@@ -258,7 +264,7 @@ def test_decode_row_blocks_every_config(hx, dev):
             _check(got, a, b, "f16", f"rows every config {cfg}")
     finally:
         rw.release()
-    M = 24
+    M, N = 24, 523
     x = rng(122).normal(0, 1, (M, K)).astype(np.float16)
     w = rng(123).integers(-127, 128, (K, N), dtype=np.int8)
     s = rng(124).uniform(0.001, 0.02, N).astype(np.float16)

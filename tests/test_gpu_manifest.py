@@ -45,6 +45,14 @@ def test_manifest_records_plans_and_reasons(hx, dev):
             hx.matmul_resident(torch.randn((128, 512), dtype=torch.float16, device=dev), rw)  # tiled
         finally:
             rw.release()
+        # argument f16 weights past 16 rows: row blocks only for a [N][K]
+        # weight of >= 2048 columns and <= 24 rows, else the tiled GEMM
+        wf = torch.randn((2048, 512), dtype=torch.float16, device=dev, generator=g)
+        x20 = torch.randn((20, 512), dtype=torch.float16, device=dev, generator=g)
+        hx.matmul(x20, wf, b_layout="nk")                        # row blocks
+        hx.matmul(x20, wf.t().contiguous(), b_layout="kn")       # tiled, B read in place
+        hx.matmul(x20, wf[:1024], b_layout="nk")                 # N = 1024: tiled
+        hx.matmul(torch.randn((40, 512), dtype=torch.float16, device=dev, generator=g), wf, b_layout="nk")
         torch.cuda.synchronize()
         recs = records(hx)
     finally:
@@ -74,6 +82,11 @@ def test_manifest_records_plans_and_reasons(hx, dev):
     assert r["plan"] == "gemv-packed" and r["reason"] == "few-rows" and r["config"].startswith("rows")
     r = find(entry="hx_matmul_resident", m=128)
     assert r["plan"] == "mfma-tiled" and r["weight"] == "resident-image" and r["b"] == "i8"
+    r = find(entry="hx_matmul", m=20, n=2048, weight="argument")
+    assert r["plan"] == "gemv-stream" and r["reason"] == "few-rows" and r["config"].startswith("rows")
+    assert find(entry="hx_matmul", m=20, n=2048, weight="argument-kn")["plan"] == "mfma-tiled"
+    assert find(entry="hx_matmul", m=20, n=1024)["plan"] == "mfma-tiled"
+    assert find(entry="hx_matmul", m=40, n=2048)["plan"] == "mfma-tiled"
 
 
 def test_manifest_reports_pinned_config(hx, dev):

@@ -105,6 +105,10 @@ def test_refused_shape_pins_nothing(hx, dev):
     r = hx.search.tune(1, 100, 100, 100, canary_reference_us=-1.0, **FAST)
     reasons = [(e["status"], e["reason"]) for e in r["entries"]]
     assert all(x == ("refused", "row-stride") for x in reasons), reasons
+    # f16 decode family at 40 rows: the products run the tiled GEMM there
+    r = hx.search.tune(7, 40, 2048, 512, canary_reference_us=-1.0, **FAST)
+    reasons = {(e["status"], e["reason"]) for e in r["entries"]}
+    assert reasons == {("refused", "family-shape")} and not r["pinned"], reasons
 
 
 def test_canary_reference_survives_pins_round_trip(hx, dev):
