@@ -335,6 +335,17 @@ def cpu_baselines_secondary(march: str) -> dict:
         out[f"ref_{M}x{N}x{K}"] = dict(base, value=round(t * 1e6, 2), unit="us", cores=threads,
                                        tflops=round(2.0 * M * N * K / t / 1e12, 5),
                                        sample=f"full fp16 {M}x{N}x{K} matmul, hxo_matmul, median of 5 after a warm-up")
+    # fp16 decode at the reference tuner's decode shapes (one row: one thread)
+    for (M, N, K) in ((1, 8192, 8192), (1, 4096, 16384)):
+        x = r.uniform(-1, 1, (M, K)).astype(np.float16)
+        wk = r.uniform(-1, 1, (K, N)).astype(np.float16)
+        t = _median_time(lambda: oracle.matmul(x, wk), 3)
+        nbytes = N * K * 2 + 2 * M * K + 2 * M * N
+        out[f"dec_{M}x{N}x{K}"] = dict(base, value=round(nbytes / t / 1e9, 3), unit="GB/s", cores=min(M, threads),
+                                       us_per_call=round(t * 1e6, 1),
+                                       sample=f"full fp16 decode {M}x{N}x{K}, hxo_matmul (i,k,j) loop, "
+                                              f"median of 3 after a warm-up")
+        del wk
     # C5: the FFN block on a 64-token sample (tokens are independent rows)
     T, H, I = 64, 4096, 11008
     wg = r.integers(-127, 128, (H, I), dtype=np.int8)
@@ -563,6 +574,47 @@ def bench_reference_shapes(hx, iters: int = 200):
                     "reference_hardware": "Hexagon v79 NPU (ROADMAP.md:98-100, frozen build, zero-knob "
                                           "default); not comparable hardware",
                     "queue_fed": fed})
+    return res
+
+
+def bench_f16_decode(hx, iters: int = 300):
+    """fp16 decode products at the reference tuner's decode shapes
+    (QHB/test/test_hmx_search_loop_contract.py:100-113: (1, 8192, 8192) and
+    (1, 4096, 16384)): a registered f16 weight (its packed decode image),
+    rotating over copies larger than twice the 256 MB MALL, each copy
+    writing its own output; torch (hipBLASLt) on the same weights beside."""
+    import torch
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(12)
+    res = []
+    for (M, N, K) in ((1, 8192, 8192), (1, 4096, 16384)):
+        nbytes = N * K * 2
+        copies = max(2, -(-(600 << 20) // nbytes))
+        wts = [torch.empty((N, K), dtype=torch.float16, device=dev).uniform_(-1, 1, generator=g) for _ in range(copies)]
+        rws = [hx.ResidentWeight(w, None, layout="nk") for w in wts]
+        try:
+            x = torch.randn((M, K), dtype=torch.float16, device=dev, generator=g)
+            ys = [torch.empty((M, N), dtype=torch.float16, device=dev) for _ in rws]
+            calls = [hx.bind_matmul_resident(x, w, y) for w, y in zip(rws, ys)]
+            hx.manifest_clear()
+            hx.manifest_enable(True)
+            calls[0]()
+            hx.manifest_enable(False)
+            plan = hx.manifest()["records"]
+            ev_ms, fed = event_timed(calls, iters)
+            t_ms, _ = event_timed([(lambda w=w, y=y: torch.matmul(x, w.t(), out=y)) for w, y in zip(wts, ys)], iters)
+        finally:
+            for w in rws:
+                w.release()
+        alg = nbytes + 2 * M * K + 2 * M * N
+        gbs = alg / (ev_ms * 1e-3) / 1e9
+        res.append({"workload": f"fp16 decode {M}x{N}x{K}, registered weight (the reference tuner's decode shape)",
+                    "value": round(gbs, 1), "unit": "GB/s", "us_per_call": round(ev_ms * 1e3, 2),
+                    "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s"),
+                    "kernel": f"{plan[0]['plan']}:{plan[0]['config']}" if plan else None,
+                    "torch_us_same_weights": round(t_ms * 1e3, 2), "weight_copies": copies, "queue_fed": fed})
+        del wts, rws, ys, calls
+        torch.cuda.empty_cache()
     return res
 
 
@@ -1102,6 +1154,8 @@ def main() -> int:
         secondary.append(bench_gemm_f16_small(hx))
         log("[bench] fp16 matmul at the reference's published shapes")
         secondary += bench_reference_shapes(hx)
+        log("[bench] fp16 decode at the reference tuner's decode shapes")
+        secondary += bench_f16_decode(hx)
         log("[bench] SwiGLU FFN")
         secondary.append(bench_ffn(hx, tune_on=tune_on))
         log("[bench] attention")
@@ -1121,6 +1175,8 @@ def main() -> int:
                     "softmax fp16": "softmax", "rmsnorm fp16": "rmsnorm", "fp16 GEMM 256^3": "gemm_f16_256",
                     "SwiGLU FFN": "ffn"}
             keys.update({f"fp16 matmul {M}x{N}x{K} ": f"ref_{M}x{N}x{K}" for (M, N, K) in REF_SHAPES})
+            keys.update({f"fp16 decode {M}x{N}x{K},": f"dec_{M}x{N}x{K}" for (M, N, K) in ((1, 8192, 8192),
+                                                                                       (1, 4096, 16384))})
             for sec in secondary:
                 for prefix, key in keys.items():
                     if sec["workload"].startswith(prefix):

@@ -369,16 +369,32 @@ static int resolve_gemm(int op, int64_t M, int64_t N, int64_t K, bool* was_pinne
   return gemm_default_config(mode, epi, M, N, K);
 }
 // Untuned GEMV config (table index = family index) for a shape.
-static int gemv_untuned(int op, int64_t M, int64_t N, int64_t K) {
+// in_place: an f16 / bf16 [N][K] weight read where it lies (argument
+// weights); otherwise a registered weight's packed image.
+static int gemv_untuned(int op, int64_t M, int64_t N, int64_t K, bool in_place = false) {
   if (M > 16) return gemv_rows_default(M, N);
-  if (op != HX_OP_GEMV_W8) {
-    // f16 / bf16 weights, untuned choice from the MI355X sweep over
+  const int64_t tiles = (N + 15) / 16;
+  const bool three_tiles = (tiles + 255) / 256 == 3;  // N = 11008: 688 tiles, 230 workgroups
+  if (op != HX_OP_GEMV_W8 && in_place) {
+    // f16 / bf16 weights in place, untuned choice from the MI355X sweep over
     // N, K in {4096, 8192, 11008}: 16 waves with LDS-staged activations for
     // M <= 2 (software pipelined once K spans several slices), 8 for M <= 4,
     // one column tile per workgroup (two for K >= 8192) beyond
     if (M <= 2) return K >= 8192 ? 12 : 7;
     if (M <= 4) return 5;
     return K >= 8192 ? 0 : 1;
+  }
+  if (op != HX_OP_GEMV_W8) {
+    // the packed f16 / bf16 image (tuner medians, rotating copies): 16 waves
+    // with staged activations for M <= 2 (1 x 8192 x 8192: 22.8 us, within
+    // 4% of the best at N, K in {4096, 8192, 11008, 16384}), 8 for M <= 4;
+    // beyond, three tiles over 16 waves where they give one workgroup per
+    // CU (16 x 11008 x 4096: 16.9 against 24.7 us for one tile), two tiles
+    // from 512 tiles (16 x 8192 x 8192: 24.4 against 33.4) and one below
+    // (16 x 4096 x 16384: 30.6 against 39.5 for two)
+    if (M <= 2) return 7;
+    if (M <= 4) return 5;
+    return three_tiles ? 20 : tiles >= 512 ? 0 : 1;
   }
   // untuned choice from the MI355X sweep (int8, K = 4096).  When the
   // 16-column tiles need three per workgroup to fit one workgroup per CU
@@ -390,16 +406,16 @@ static int gemv_untuned(int op, int64_t M, int64_t N, int64_t K) {
   // (the launcher falls back to the register-fragment base config when the
   // rows do not fit in LDS) -- and four tiles (activation fragments reused
   // 4x) over 8 waves with every K chunk in flight at once for larger M.
-  const int64_t tiles = (N + 15) / 16;
-  if ((tiles + 255) / 256 == 3) return M <= 4 ? 20 : 19;
+  if (three_tiles) return M <= 4 ? 20 : 19;
   return M <= 2 ? 11 : M <= 4 ? 5 : 10;
 }
 
-static int resolve_gemv(int op, int64_t M, int64_t N, int64_t K, bool* was_pinned = nullptr) {
+static int resolve_gemv(int op, int64_t M, int64_t N, int64_t K, bool* was_pinned = nullptr,
+                        bool in_place = false) {
   const int pin = pinned(op, M, N, K);
   if (was_pinned) *was_pinned = pin >= 0 && pin < gemv_packed_config_count();
   if (pin >= 0 && pin < gemv_packed_config_count()) return pin;
-  return gemv_untuned(op, M, N, K);
+  return gemv_untuned(op, M, N, K, in_place);
 }
 
 int hx::untuned_family_index(int op, int64_t m, int64_t n, int64_t k) {
@@ -498,7 +514,7 @@ static int run_gemv_hw(GemvArgs& a, int dt, const void* w, int64_t ldw, hipStrea
   if (!reason) reason = a.M <= 16 ? "min-rows" : "few-rows";  // 16 < M <= 64: row-block configs
   const int op = dt == HX_BF16 ? HX_OP_GEMV_BF16 : dt == HX_I8 ? HX_OP_GEMV_W8 : HX_OP_GEMV_F16;
   bool pin = false;
-  const int cfg = resolve_gemv(op, a.M, a.N, a.K, &pin);
+  const int cfg = resolve_gemv(op, a.M, a.N, a.K, &pin, dt != HX_I8);
   note_plan(ctx, a.M, a.N, a.K, dt == HX_BF16 ? HX_BF16 : HX_F16, "gemv-stream", gemv_packed_config(cfg)->name,
             pin ? "pinned" : "default", reason);
   return map_internal(launch_gemv_hw(cfg, dt, a, w, ldw, s), "gemv_stream");
@@ -659,16 +675,15 @@ extern "C" int hx_matmul(const hx_memref2d* a, int a_dtype, const hx_memref2d* b
     else sc32 = (const float*)vs.p;
   }
   // Argument weights: the decode GEMV for M <= 16, its row blocks up to
-  // kGemvRowsMaxM rows for a K-contiguous weight with enough column tiles;
-  // the tiled GEMM (K split) beyond.  Measured with argument weights (f16 /
-  // W8A16, K = 4096): at M = 17 the row blocks win with an [N][K] weight
-  // (f16 N = 4096: 11.1 against 13.8 us; W8A16 N = 2048: 8.6 against 13.7)
-  // and lose with a [K][N] one (transposed first: 25.1 against 14.0); at
-  // M = 32..64 the tiled GEMM wins (64 x 11008 f16: 20.7 against 36.5 us),
-  // and at N < 2048 by up to 3x (64 x 256 x 8192 f16: 14.2 against 37.1).
-  // Registered weights keep the row blocks to 64 rows (the FFN's decode path
-  // sizes its scratch for them).
-  const bool gemv_rows = (M <= 16 || (gemv_rows_route(M, N) && b_layout == HX_LAYOUT_NK)) &&
+  // kGemvRowsMaxM rows for a K-contiguous weight of 2048..4096 columns; the
+  // tiled GEMM (K split) beyond.  Measured with argument f16 weights
+  // (K = 4096, rotating copies): at M = 17 / 32 the row blocks take 12.2 /
+  // 15.8 us at N = 4096 against 18.4 tiled, and 29.7 / 29.8 at N = 11008
+  // against 23.0 / 23.5 (the in-place read streams slower than a packed
+  // image); with a [K][N] weight they lose (transposed first: 25.1 against
+  // 14.0 at M = 17); below N = 2048 the tiled GEMM wins by up to 3x (64 x
+  // 256 x 8192: 14.2 against 37.1).
+  const bool gemv_rows = (M <= 16 || (gemv_rows_route(M, N, false) && b_layout == HX_LAYOUT_NK)) &&
                          M <= kGemvMaxRows && !residual && c_dtype == (op == HX_OP_MATMUL_W8 ? HX_F16 : a_dtype);
 
   // Decode shapes with weights in the [K][N] orientation: stream the weight
@@ -952,7 +967,8 @@ struct hx_weight {
   int64_t K, N;
   int dtype;
   void* image;     // [N][K], K-contiguous (the GEMM operand)
-  int8_t* packed;  // int8 only: MFMA-fragment-ordered copy for the decode GEMV
+  void* packed;    // MFMA-fragment-ordered copy for the decode GEMV (int8: 16 x 64 bytes
+                   // per KiB block, f16 / bf16: 16 x 32 halves)
   float* scale;    // [N] or null
   uint64_t hash;
   int refcount;    // registrations not yet released
@@ -1137,13 +1153,19 @@ extern "C" int hx_weight_register(const hx_memref2d* w, int w_dtype, int w_layou
       return HX_OK;
     }
   }
-  int8_t* packed = nullptr;
-  if (w_dtype == HX_I8) {
-    if (hipMalloc((void**)&packed, (size_t)gemv_packed_bytes(N, K)) != hipSuccess) {
+  // the decode GEMV's image: every wave load one contiguous KiB (the [N][K]
+  // image read in place gives sixteen 64-byte runs per load, about 1.4x
+  // slower to stream)
+  void* packed = nullptr;
+  {
+    const bool i8 = w_dtype == HX_I8;
+    if (hipMalloc(&packed, (size_t)(i8 ? gemv_packed_bytes(N, K) : gemv_packed16_bytes(N, K))) != hipSuccess) {
       cleanup();
       return fail(HX_ERR_NOMEM, "packed weight image");
     }
-    rc = map_internal(launch_gemv_pack((const int8_t*)image, K, N, K, packed, s), "gemv pack");
+    rc = map_internal(i8 ? launch_gemv_pack((const int8_t*)image, K, N, K, (int8_t*)packed, s)
+                         : launch_gemv_pack16((const uint16_t*)image, K, N, K, (uint16_t*)packed, s),
+                      "gemv pack");
     hipError_t se = hipStreamSynchronize(s);
     if (rc || se != hipSuccess) {
       (void)hipFree(packed);
@@ -1199,15 +1221,25 @@ static int matmul_resident_impl(const View2& vx, hx_weight* w, const View2* vr, 
     const int cfg = resolve_gemv(HX_OP_GEMV_W8, M, w->N, w->K, &pin);
     note_plan(PlanCtx{entry, "resident-packed", x_dt, w->dtype}, M, w->N, w->K, HX_F16, "gemv-packed",
               gemv_packed_config(cfg)->name, pin ? "pinned" : "default", M <= 16 ? "min-rows" : "few-rows");
-    return map_internal(launch_gemv_packed(cfg, v, w->packed, s), "gemv_packed");
+    return map_internal(launch_gemv_packed(cfg, v, (const int8_t*)w->packed, s), "gemv_packed");
   }
   // An f16 / bf16 image is a [N][K] weight: the argument products' rule
   // for the row blocks applies as it stands (the packed int8 weight above
   // keeps them to kGemvMaxRows rows: its tiles read half the bytes).
-  if (w->dtype != HX_I8 && gemv_rows_route(M, w->N) && !vr && y_dt == x_dt) {
+  if (w->dtype != HX_I8 && gemv_rows_route(M, w->N, w->packed != nullptr) && !vr && y_dt == x_dt) {
     GemvArgs v{};
     v.x = vx.p; v.ldx = vx.ld; v.w = nullptr; v.ldw = 0;
     v.scale = w->scale; v.y = vy.p; v.ldy = vy.ld; v.M = M; v.N = w->N; v.K = w->K;
+    // the packed image: activations as 16-byte groups, 32-bit offsets into
+    // the activation rows and one workgroup's tiles (at most four)
+    if (w->packed && !gemv_hw_refusal(w->dtype, v, w->image, w->K) && (w->K + 31) / 32 * 4 * 1024 < ((int64_t)1 << 31)) {
+      const int op = w->dtype == HX_BF16 ? HX_OP_GEMV_BF16 : HX_OP_GEMV_F16;
+      bool pin = false;
+      const int cfg = resolve_gemv(op, M, w->N, w->K, &pin);
+      note_plan(PlanCtx{entry, "resident-packed", x_dt, w->dtype}, M, w->N, w->K, x_dt, "gemv-packed",
+                gemv_packed_config(cfg)->name, pin ? "pinned" : "default", M <= 16 ? "min-rows" : "few-rows");
+      return map_internal(launch_gemv_packed16(cfg, w->dtype, v, w->packed, s), "gemv_packed");
+    }
     if (!gemv_hw_refusal(w->dtype, v, w->image, w->K)) return run_gemv_hw(v, w->dtype, w->image, w->K, s,
                                                                 PlanCtx{entry, "resident-image", x_dt, w->dtype});
   }

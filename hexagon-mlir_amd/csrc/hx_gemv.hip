@@ -149,8 +149,14 @@ __global__ void __launch_bounds__(256) gemv_w8a16_kernel(GemvArgs p) {
 //     256*g + 16*c + i holds W[64*j + 16*g + i][16*t + c] ^ 0x80 (g 0..3,
 //     c 0..15, i 0..15; excess-128, so the widening needs no XOR per load),
 //     so every wave load is one contiguous KiB;
+//   * f16/bf16, packed (registered weights): block (t, j) at ((t * KC) + j)
+//     * 1024, in which bytes 256*g + 16*c .. + 15 hold W[32*j + 8*g + (0..7)]
+//     [16*t + c] (zero beyond N and K);
 //   * f16/bf16, in place: lane l reads row 16t + c of the [N][K] weight at
-//     k = 32j + 8g: sixteen 64-byte runs per wave load.
+//     k = 32j + 8g: sixteen 64-byte runs per wave load.  A pure read of
+//     134 MB in that pattern takes 31 us against 21-22 us in contiguous
+//     KiBs (N = K = 8192, 512 workgroups), which is what the packed image
+//     buys.
 // A workgroup of KW waves splits K into slices of CPW * KW chunks; each wave
 // loads CPW chunks of each of its CT tiles per slice, ahead of the MFMAs
 // that use them (how far ahead is the compiler's schedule: for the wide
@@ -182,7 +188,6 @@ __device__ __forceinline__ v4f gv_mfma(v4u a, v4u b, v4f c) {
 template <int CT, int KW, int CPW, int XS, int WT, bool PK, bool PIPE, int MB = 1>
 __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const void* wsrc, int64_t ldw,
                                                               int kchunks) {
-  static_assert(!PK || WT == DT_I8, "only int8 weights have a packed image");
   static_assert(MB == 1 || (XS == XS_NONE && !PIPE), "row blocks: register-fragment configs only");
   constexpr bool XL = XS != XS_NONE;
   constexpr int KD = WT == DT_I8 ? 64 : 32;  // k per chunk
@@ -541,6 +546,39 @@ int64_t gemv_packed_bytes(int64_t N, int64_t K) {
   return ((N + 15) / 16) * ((K + 63) / 64) * 1024;
 }
 
+// The 16-bit (f16 / bf16) fragment-packed image from a K-contiguous [N][K]
+// weight: block (t, j) bytes 256*g + 16*c .. + 15 = W[n = 16t + c][k = 32j +
+// 8g + (0..7)], zero beyond N or K.  One thread per 16-byte run.
+__global__ void __launch_bounds__(256) gemv_pack16_kernel(const uint16_t* w, int64_t ldw, int64_t N,
+                                                          int64_t K, int kchunks, uint16_t* out) {
+  const int64_t ntiles = (N + 15) / 16;
+  const int64_t runs = ntiles * kchunks * 64;
+  for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < runs; q += (int64_t)gridDim.x * 256) {
+    const int64_t blk = q >> 6;
+    const int lane = (int)(q & 63);
+    const int64_t t = blk / kchunks, j = blk - t * kchunks;
+    const int c = lane & 15, g = lane >> 4;
+    const int64_t n = t * 16 + c, k0 = j * 32 + 8 * g;
+    uint16_t v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (n < N && k0 + i < K) ? w[n * ldw + k0 + i] : (uint16_t)0;
+    *reinterpret_cast<v4u*>(out + blk * 512 + 8 * lane) = *reinterpret_cast<const v4u*>(v);
+  }
+}
+
+int64_t gemv_packed16_bytes(int64_t N, int64_t K) {
+  return ((N + 15) / 16) * ((K + 31) / 32) * 1024;
+}
+
+int launch_gemv_pack16(const uint16_t* w, int64_t ldw, int64_t N, int64_t K, uint16_t* out, hipStream_t s) {
+  const int kchunks = (int)((K + 31) / 32);
+  const int64_t runs = ((N + 15) / 16) * kchunks * 64;
+  int64_t blocks = (runs + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  gemv_pack16_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(w, ldw, N, K, kchunks, out);
+  return HXI_OK;
+}
+
 int launch_gemv_pack(const int8_t* w, int64_t ldw, int64_t N, int64_t K, int8_t* out, hipStream_t s) {
   const int kchunks = (int)((K + 63) / 64);
   const int64_t runs = ((N + 15) / 16) * kchunks * 64;
@@ -562,16 +600,19 @@ static void gemv_stream_one(const GemvArgs& a, const void* w, int64_t ldw, int k
 }
 struct GemvStreamEntry {
   GemvConfig cfg;
-  GemvStreamLaunch fn[4];  // int8 (packed image), f16, bf16, int8 (in place)
+  GemvStreamLaunch fn[6];  // int8 (packed image), f16, bf16, int8 (in place), f16 / bf16 (packed image)
 };
 #define HX_GV(CT, KW, CPW, XS, PIPE)                                                                     \
   {&gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_I8>, &gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_F16>, \
-   &gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_BF16>, &gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_I8, 1, false>}
+   &gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_BF16>, &gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_I8, 1, false>, \
+   &gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_F16, 1, true>, &gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_BF16, 1, true>}
 #define HX_GR(CT, KW, CPW, MB)                                                                      \
   {&gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_I8, MB>,                                        \
    &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_F16, MB>,                                       \
    &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_BF16, MB>,                                      \
-   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_I8, MB, false>}
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_I8, MB, false>,                                 \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_F16, MB, true>,                                 \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_BF16, MB, true>}
 // xl configs (activations staged in LDS) take M <= 4 with the staged rows
 // within 64 KiB of LDS; outside that they run as their register-staged base
 // config (the `base` index).  The `_p` config is software pipelined over
@@ -607,6 +648,10 @@ static const GemvStreamEntry kGemvStream[] = {
     // CUs busy, two re-read the activation fragments twice as often)
     {{3, 8, "packed_ct3_kw8", 0, 19, 1}, HX_GV(3, 8, 8, XS_NONE, false)},
     {{3, 16, "packed_ct3_kw16", 0, 20, 1}, HX_GV(3, 16, 4, XS_NONE, false)},
+    // three tiles with two or four row blocks: one workgroup per CU at
+    // N = 11008 for 16 < M <= 64
+    {{3, 8, "rows2_ct3_kw8", 0, 21, 2}, HX_GR(3, 8, 4, 2)},
+    {{3, 8, "rows4_ct3_kw8", 0, 22, 4}, HX_GR(3, 8, 2, 4)},
 };
 #undef HX_GR
 #undef HX_GV
@@ -616,14 +661,14 @@ const GemvConfig* gemv_packed_config(int idx) {
   return &kGemvStream[idx].cfg;
 }
 
-// Shared by the int8 (packed) and f16/bf16 (in place) launches.
+// Shared by the packed-image and in-place launches.
 static int launch_gemv_stream(int cfg_idx, int wt, bool packed, const GemvArgs& a, const void* w,
                               int64_t ldw, hipStream_t s) {
   if (cfg_idx < 0 || cfg_idx >= gemv_packed_config_count()) return HXI_ERR_ARG;
   if (a.M < 1 || a.M > kGemvMaxRows) return HXI_ERR_SHAPE;
   // a config whose row blocks cannot hold M runs as the row-block default
   if (a.M > 16 * kGemvStream[cfg_idx].cfg.mb) cfg_idx = gemv_rows_default(a.M, a.N);
-  const int slot = wt == DT_I8 ? (packed ? 0 : 3) : wt == DT_F16 ? 1 : wt == DT_BF16 ? 2 : -1;
+  const int slot = wt == DT_I8 ? (packed ? 0 : 3) : wt == DT_F16 ? (packed ? 4 : 1) : wt == DT_BF16 ? (packed ? 5 : 2) : -1;
   if (slot < 0) return HXI_ERR_ARG;
   const int64_t kd = wt == DT_I8 ? 64 : 32;
   const int64_t kchunks = (a.K + kd - 1) / kd;
@@ -643,11 +688,16 @@ static int launch_gemv_stream(int cfg_idx, int wt, bool packed, const GemvArgs& 
 // for four and four) and four tiles and four row blocks beyond; else one
 // tile with two or four row blocks (f16, N = 4096).
 int gemv_rows_default(int64_t M, int64_t N) {
-  if (N >= 160 * 64) return M <= 32 ? 14 : 17;
-  return M <= 32 ? 13 : 15;
+  const int64_t tiles = (N + 15) / 16;
+  if (M <= 32) return (tiles + 255) / 256 == 3 ? 21 : tiles > 256 ? 14 : 13;
+  return N >= 160 * 64 ? 17 : 15;
 }
 int launch_gemv_packed(int cfg_idx, const GemvArgs& a, const int8_t* packed, hipStream_t s) {
   return launch_gemv_stream(cfg_idx, DT_I8, true, a, packed, 0, s);
+}
+int launch_gemv_packed16(int cfg_idx, int wt, const GemvArgs& a, const void* packed, hipStream_t s) {
+  if (wt != DT_F16 && wt != DT_BF16) return HXI_ERR_ARG;
+  return launch_gemv_stream(cfg_idx, wt, true, a, packed, 0, s);
 }
 const char* gemv_hw_refusal(int wt, const GemvArgs& a, const void* w, int64_t ldw) {
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };

@@ -103,14 +103,20 @@ struct GemvConfig {
 };
 // Largest M the decode GEMV takes (row-block configs).
 constexpr int kGemvMaxRows = 64;
-// hx_matmul with argument weights: 16 < M <= kGemvRowsMaxM rows take the
-// decode GEMV's row blocks when N >= kGemvRowsMinN (fewer 16-column tiles
-// leave most CUs idle); other skinny shapes take the tiled GEMM.
-constexpr int64_t kGemvRowsMaxM = 24;
+// Where 16 < M <= kGemvRowsMaxM rows of an f16 / bf16 weight (registered or
+// argument) or an argument int8 weight take the decode GEMV's row blocks
+// rather than the tiled GEMM: N >= kGemvRowsMinN (fewer 16-column tiles
+// leave most CUs idle), and for a [N][K] weight read in place (sixteen
+// 64-byte runs per wave load, not one contiguous KiB) N <= kGemvRowsInPlaceMaxN.
+// A registered int8 weight's packed image takes them to kGemvMaxRows rows.
+constexpr int64_t kGemvRowsMaxM = 32;
 constexpr int64_t kGemvRowsMinN = 2048;
-// The decode GEMV's routing for an f16 / bf16 weight (argument or
-// registered) and an argument int8 one, both read as [N][K].
-inline bool gemv_rows_route(int64_t M, int64_t N) { return M <= 16 || (M <= kGemvRowsMaxM && N >= kGemvRowsMinN); }
+constexpr int64_t kGemvRowsInPlaceMaxN = 4096;
+inline bool gemv_rows_route(int64_t M, int64_t N, bool packed) {
+  if (M <= 16) return true;
+  if (M > kGemvRowsMaxM || N < kGemvRowsMinN) return false;
+  return packed || N <= kGemvRowsInPlaceMaxN;
+}
 // Untuned row-block config for 16 < M <= kGemvMaxRows.
 int gemv_rows_default(int64_t M, int64_t N);
 bool gemv_fast_ok(const GemvArgs& a);
@@ -125,6 +131,11 @@ int launch_gemv_pack(const int8_t* w_nk, int64_t ldw, int64_t N, int64_t K, int8
 int gemv_packed_config_count();
 const GemvConfig* gemv_packed_config(int idx);
 int launch_gemv_packed(int cfg_idx, const GemvArgs& a, const int8_t* packed, hipStream_t s);
+// f16 / bf16 weights: the 16-bit fragment-packed image (16 columns x 32 k per
+// KiB block) of a registered weight, and the decode GEMV over it.
+int64_t gemv_packed16_bytes(int64_t N, int64_t K);
+int launch_gemv_pack16(const uint16_t* w_nk, int64_t ldw, int64_t N, int64_t K, uint16_t* out, hipStream_t s);
+int launch_gemv_packed16(int cfg_idx, int wt, const GemvArgs& a, const void* packed, hipStream_t s);
 // Weights read in place from a K-contiguous [N][K] matrix with row stride
 // ldw (elements): f16 / bf16 (wt = DT_F16 / DT_BF16), or int8 (DT_I8, f16
 // activations); the same config table as the packed int8 kernel.  Null when

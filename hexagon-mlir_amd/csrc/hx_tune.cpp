@@ -151,7 +151,7 @@ class Probe {
     } else if (op_ == HX_OP_GEMV_W8) {
       rc = launch_gemv_packed(t, v_[copy], (const int8_t*)w_[copy], s_);
     } else {
-      rc = launch_gemv_hw(t, wt_, v_[copy], w_[copy], k_, s_);
+      rc = launch_gemv_packed16(t, wt_, v_[copy], w_[copy], s_);
     }
     if (rc != HXI_OK) return HX_ERR_UNSUPPORTED;
     return hipGetLastError() == hipSuccess ? HX_OK : HX_ERR_HIP;
@@ -291,21 +291,24 @@ class Probe {
     exact_ = false;
     // the shapes the products run on this family: the packed int8 weight's
     // row blocks to kGemvMaxRows rows, the f16 / bf16 image's by the routing
-    if (m_ > kGemvMaxRows || (op_ != HX_OP_GEMV_W8 && !gemv_rows_route(m_, n_))) family_reason_ = "family-shape";
+    if (m_ > kGemvMaxRows || (op_ != HX_OP_GEMV_W8 && !gemv_rows_route(m_, n_, true))) family_reason_ = "family-shape";
     const int64_t mm = std::min<int64_t>(m_, kGemvMaxRows);
     const size_t eb = es_of(wt_);
-    const size_t img = op_ == HX_OP_GEMV_W8 ? (size_t)gemv_packed_bytes(n_, k_) : (size_t)n_ * k_ * eb;
+    // every family times the registered weight's packed image, the form a
+    // resident decode reads (a pin applies to an argument [N][K] weight
+    // read in place as well)
+    const size_t img = op_ == HX_OP_GEMV_W8 ? (size_t)gemv_packed_bytes(n_, k_) : (size_t)gemv_packed16_bytes(n_, k_);
     copies_ = copies_for(img, true);
     void* x = ar_.get((size_t)mm * k_ * 2);
     out_bytes_ = (size_t)mm * n_ * 2;
     out_ = ar_.get(out_bytes_);
     ref_ = ar_.get(out_bytes_);
-    // [N][K] image of copy 0: the reference's operand (and, for int8, the
-    // source of copy 0's packed image); int8 copies >= 1 are generated into
-    // a scratch image and packed from there
+    // [N][K] image of copy 0: the reference's operand and the source of
+    // copy 0's packed image; copies >= 1 are generated into a scratch image
+    // and packed from there
     void* w0 = ar_.get((size_t)n_ * k_ * eb);
-    void* scratch = (wt_ == DT_I8 && copies_ > 1) ? ar_.get((size_t)n_ * k_) : nullptr;
-    if (!x || !out_ || !ref_ || !w0 || (wt_ == DT_I8 && copies_ > 1 && !scratch))
+    void* scratch = copies_ > 1 ? ar_.get((size_t)n_ * k_ * eb) : nullptr;
+    if (!x || !out_ || !ref_ || !w0 || (copies_ > 1 && !scratch))
       return api_fail(HX_ERR_NOMEM, "hx_tune: operands");
     if (fill(x, mm * k_, xt, -1.f, 1.f, 1)) return api_fail(HX_ERR_HIP, "hx_tune: fill");
     float* sc = nullptr;
@@ -316,19 +319,15 @@ class Probe {
     const float lo = wt_ == DT_I8 ? -127.f : -1.f, hi = -lo;
     ref_nk_ = w0;
     for (int c = 0; c < copies_; ++c) {
-      void* nk = c == 0 ? w0 : (wt_ == DT_I8 ? scratch : ar_.get((size_t)n_ * k_ * eb));
-      if (!nk) return api_fail(HX_ERR_NOMEM, "hx_tune: weight copy %d", c);
+      void* nk = c == 0 ? w0 : scratch;
       if (fill(nk, n_ * k_, wt_, lo, hi, 10 + c)) return api_fail(HX_ERR_HIP, "hx_tune: fill");
-      const void* w = nk;
-      if (wt_ == DT_I8) {
-        // the registered (resident) form the int8 decode GEMV reads
-        void* packed = ar_.get(img);
-        if (!packed) return api_fail(HX_ERR_NOMEM, "hx_tune: packed copy %d", c);
-        if (launch_gemv_pack((const int8_t*)nk, k_, n_, k_, (int8_t*)packed, s_) != HXI_OK)
-          return api_fail(HX_ERR_HIP, "hx_tune: pack");
-        w = packed;
-      }
-      w_.push_back(w);
+      // the registered (resident) form the decode GEMV reads
+      void* packed = ar_.get(img);
+      if (!packed) return api_fail(HX_ERR_NOMEM, "hx_tune: packed copy %d", c);
+      const int prc = wt_ == DT_I8 ? launch_gemv_pack((const int8_t*)nk, k_, n_, k_, (int8_t*)packed, s_)
+                                   : launch_gemv_pack16((const uint16_t*)nk, k_, n_, k_, (uint16_t*)packed, s_);
+      if (prc != HXI_OK) return api_fail(HX_ERR_HIP, "hx_tune: pack");
+      w_.push_back(packed);
       GemvArgs v{};
       v.x = x; v.ldx = k_;
       v.scale = sc;
@@ -336,8 +335,10 @@ class Probe {
       v.M = mm; v.N = n_; v.K = k_;
       v_.push_back(v);
     }
-    if (family_reason_.empty() && wt_ != DT_I8)
+    if (family_reason_.empty() && wt_ != DT_I8) {
       if (const char* why = gemv_hw_refusal(wt_, v_[0], w_[0], k_)) family_reason_ = why;
+      else if ((k_ + 31) / 32 * 4 * 1024 >= ((int64_t)1 << 31)) family_reason_ = "offset-range";
+    }
     if (family_reason_.empty() && wt_ == DT_I8 && k_ % 8 != 0) family_reason_ = "k-granularity";
     return reference_gemv();
   }

@@ -216,14 +216,18 @@ def test_matvec_n_is_one_fallbacks(hx, dev):
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 @pytest.mark.parametrize("shape", [(17, 2048, 520), (24, 4096, 4096), (20, 11008, 1024), (23, 2053, 72),
-                                   (17, 1000, 520), (25, 4096, 4096), (48, 11008, 1024), (64, 300, 8192), (63, 37, 72)],
+                                   (32, 4096, 1024), (17, 1000, 520), (33, 4096, 4096), (48, 11008, 1024),
+                                   (64, 300, 8192), (63, 37, 72)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_decode_float_row_blocks(hx, dev, dtype, shape):
-    """16 < M <= 24 with N >= 2048: the streaming kernel with 2 blocks of 16
-    activation rows (each weight fragment feeds every block); fewer columns
-    or more rows: the tiled GEMM.  Argument and resident, same numerics."""
+    """16 < M <= 32 with N >= 2048: the streaming kernel with 2 blocks of 16
+    activation rows (each weight fragment feeds every block), on a registered
+    weight's packed image, and on an argument [N][K] weight read in place up
+    to N = 4096; fewer columns or more rows: the tiled GEMM.  Same numerics
+    either way."""
     M, N, K = shape
-    rows = M <= 24 and N >= 2048
+    rows = 16 < M <= 32 and 2048 <= N <= 4096
+    rows_resident = 16 < M <= 32 and N >= 2048
     a = _fp(dtype, (M, K), 110)
     b = _fp(dtype, (K, N), 111)
     bt = _dev(np.ascontiguousarray(b.T), dtype, dev)
@@ -240,8 +244,47 @@ def test_decode_float_row_blocks(hx, dev, dtype, shape):
         assert [r["plan"] for r in recs] in (["mfma-tiled"], ["mfma-generic"]), recs  # N = 37: generic
     _check(to_np(c), a, b, dtype, f"rows {dtype} {shape}")
     rw = hx.ResidentWeight(bt, None, layout="nk")
+    hx.manifest_enable(True)
+    hx.manifest_clear()
     try:
-        _check(to_np(hx.matmul_resident(_dev(a, dtype, dev), rw)), a, b, dtype, f"rows resident {dtype} {shape}")
+        got = to_np(hx.matmul_resident(_dev(a, dtype, dev), rw))
+        recs = hx.manifest()["records"]
+    finally:
+        hx.manifest_enable(False)
+        rw.release()
+    if rows_resident:
+        assert [(r["plan"], r["weight"]) for r in recs] == [("gemv-packed", "resident-packed")], recs
+        assert recs[0]["config"].startswith("rows"), recs
+    else:
+        assert [r["plan"] for r in recs] in (["mfma-tiled"], ["mfma-generic"]), recs
+    _check(got, a, b, dtype, f"rows resident {dtype} {shape}")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("shape", [(3, 523, 1064), (16, 700, 264), (20, 2053, 264)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_packed_image_matches_in_place(hx, dev, dtype, shape):
+    """A registered f16 / bf16 weight's packed image holds, in every lane of
+    every wave load, the same 16 bytes the in-place read of the [N][K] weight
+    gives that lane: under every config of the family the resident product
+    equals the argument product bit for bit (ragged N, K not a multiple of
+    the 32-deep chunk)."""
+    M, N, K = shape
+    a = _fp(dtype, (M, K), 130)
+    bt = _fp(dtype, (N, K), 131)
+    ad, bd = _dev(a, dtype, dev), _dev(bt, dtype, dev)
+    rw = hx.ResidentWeight(bd, None, layout="nk")
+    op = OP[dtype]
+    try:
+        for cfg in range(hx.config_count(op)):
+            hx.config_select(op, M, N, K, cfg)
+            try:
+                got = to_np(hx.matmul_resident(ad, rw))
+                ref = to_np(hx.matmul(ad, bd, b_layout="nk"))
+            finally:
+                hx.config_select(op, M, N, K, -1)
+            assert np.array_equal(got.view(np.uint16), ref.view(np.uint16)), f"cfg {cfg}"
+        _check(got, a, np.ascontiguousarray(bt.T), dtype, f"packed {dtype} {shape}")
     finally:
         rw.release()
 

@@ -53,6 +53,12 @@ def test_manifest_records_plans_and_reasons(hx, dev):
         hx.matmul(x20, wf.t().contiguous(), b_layout="kn")       # tiled, B read in place
         hx.matmul(x20, wf[:1024], b_layout="nk")                 # N = 1024: tiled
         hx.matmul(torch.randn((40, 512), dtype=torch.float16, device=dev, generator=g), wf, b_layout="nk")
+        rf = hx.ResidentWeight(wf, None, layout="nk")           # f16: the packed decode image
+        try:
+            hx.matmul_resident(torch.randn((3, 512), dtype=torch.float16, device=dev, generator=g), rf)
+            hx.matmul_resident(torch.randn((28, 512), dtype=torch.float16, device=dev, generator=g), rf)
+        finally:
+            rf.release()
         torch.cuda.synchronize()
         recs = records(hx)
     finally:
@@ -87,6 +93,10 @@ def test_manifest_records_plans_and_reasons(hx, dev):
     assert find(entry="hx_matmul", m=20, n=2048, weight="argument-kn")["plan"] == "mfma-tiled"
     assert find(entry="hx_matmul", m=20, n=1024)["plan"] == "mfma-tiled"
     assert find(entry="hx_matmul", m=40, n=2048)["plan"] == "mfma-tiled"
+    r = find(entry="hx_matmul_resident", m=3, b="f16")
+    assert r["plan"] == "gemv-packed" and r["weight"] == "resident-packed" and r["reason"] == "min-rows"
+    r = find(entry="hx_matmul_resident", m=28, b="f16")
+    assert r["plan"] == "gemv-packed" and r["reason"] == "few-rows" and r["config"].startswith("rows")
 
 
 def test_manifest_reports_pinned_config(hx, dev):
