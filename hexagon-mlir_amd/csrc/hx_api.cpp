@@ -396,18 +396,22 @@ static int gemv_untuned(int op, int64_t M, int64_t N, int64_t K, bool in_place =
     if (M <= 4) return 5;
     return three_tiles ? 20 : tiles >= 512 ? 0 : 1;
   }
-  // untuned choice from the MI355X sweep (int8, K = 4096).  When the
-  // 16-column tiles need three per workgroup to fit one workgroup per CU
-  // (N = 11008: 688 tiles, 230 workgroups), the three-tile configs: 16
-  // waves for M <= 4, 8 for larger M (9.24 / 9.35 / 10.08 us at M = 1 / 4 /
-  // 16 against 9.43 / 10.14 / 11.07 for the configs below).  Otherwise
-  // LDS-staged activations and one column tile per workgroup for M <= 4 --
-  // staged by direct-to-LDS loads for M <= 2, through registers for M = 3, 4
-  // (the launcher falls back to the register-fragment base config when the
-  // rows do not fit in LDS) -- and four tiles (activation fragments reused
-  // 4x) over 8 waves with every K chunk in flight at once for larger M.
+  // untuned choice from the MI355X sweep (int8, K = 4096, tuner medians).
+  // When the 16-column tiles need three per workgroup to fit one workgroup
+  // per CU (N = 11008: 688 tiles, 230 workgroups), the three-tile configs:
+  // 16 waves for M <= 4, 8 for larger M (9.24 / 9.35 / 10.08 us at M = 1 /
+  // 4 / 16 against 9.43 / 10.14 / 11.07 for the configs below).  Otherwise,
+  // for M <= 4: up to 256 tiles one tile per workgroup over 16 waves (M = 1
+  // / 4, N = K = 4096: 5.11 / 5.23 against 5.31 / 5.59 with LDS-staged
+  // activations over 8), beyond two tiles over 8 waves (M = 4, N = 8192 /
+  // 16384: 7.67 / 12.73 against 8.15 / 13.97).
+  // For M > 4 the fewest tiles per workgroup (1 to 4) that keep the
+  // workgroups within one per CU, three beyond 1024 tiles (M = 16, N = 2048
+  // / 4096 / 8192 / 16384 / 22016: 6.83 / 7.08 / 8.85 / 13.64 / 18.97 us;
+  // four tiles everywhere took 9.63 / 9.86 / 10.5 / 13.64 / 22.25).
   if (three_tiles) return M <= 4 ? 20 : 19;
-  return M <= 2 ? 11 : M <= 4 ? 5 : 10;
+  if (M <= 4) return tiles > 256 ? 0 : 24;
+  return tiles <= 256 ? 1 : tiles <= 512 ? 0 : tiles <= 768 ? 19 : tiles <= 1024 ? 10 : 19;
 }
 
 static int resolve_gemv(int op, int64_t M, int64_t N, int64_t K, bool* was_pinned = nullptr,
@@ -511,7 +515,7 @@ static int run_gemm(int op, GemmArgs& a, hipStream_t s, const PlanCtx& ctx,
 // bf16 weights, else f16).
 static int run_gemv_hw(GemvArgs& a, int dt, const void* w, int64_t ldw, hipStream_t s, const PlanCtx& ctx,
                        const char* reason = nullptr) {
-  if (!reason) reason = a.M <= 16 ? "min-rows" : "few-rows";  // 16 < M <= 64: row-block configs
+  if (!reason) reason = a.M <= 16 ? "min-rows" : "few-rows";  // 16 < M: row-block configs
   const int op = dt == HX_BF16 ? HX_OP_GEMV_BF16 : dt == HX_I8 ? HX_OP_GEMV_W8 : HX_OP_GEMV_F16;
   bool pin = false;
   const int cfg = resolve_gemv(op, a.M, a.N, a.K, &pin, dt != HX_I8);
@@ -1211,7 +1215,7 @@ static int matmul_resident_impl(const View2& vx, hx_weight* w, const View2* vr, 
   if (M == 0) return HX_OK;
   // The packed GEMV reads activations as 8-element (16-byte) groups, with
   // 32-bit buffer offsets into the activation rows and one workgroup's tiles.
-  if (w->dtype == HX_I8 && w->packed && M <= kGemvMaxRows && !vr && y_dt == HX_F16 && w->K % 8 == 0 &&
+  if (w->dtype == HX_I8 && w->packed && gemv_rows_route(M, w->N, true, true) && !vr && y_dt == HX_F16 && w->K % 8 == 0 &&
       ((uintptr_t)vx.p & 15u) == 0 && (vx.ld * 2) % 16 == 0 && M * vx.ld * 2 < ((int64_t)1 << 31) &&
       (w->K + 63) / 64 * 4 * 1024 < ((int64_t)1 << 31)) {
     GemvArgs v{};
@@ -1223,9 +1227,8 @@ static int matmul_resident_impl(const View2& vx, hx_weight* w, const View2* vr, 
               gemv_packed_config(cfg)->name, pin ? "pinned" : "default", M <= 16 ? "min-rows" : "few-rows");
     return map_internal(launch_gemv_packed(cfg, v, (const int8_t*)w->packed, s), "gemv_packed");
   }
-  // An f16 / bf16 image is a [N][K] weight: the argument products' rule
-  // for the row blocks applies as it stands (the packed int8 weight above
-  // keeps them to kGemvMaxRows rows: its tiles read half the bytes).
+  // f16 / bf16: the packed image (the [N][K] image read in place when the
+  // packed path refuses the call)
   if (w->dtype != HX_I8 && gemv_rows_route(M, w->N, w->packed != nullptr) && !vr && y_dt == x_dt) {
     GemvArgs v{};
     v.x = vx.p; v.ldx = vx.ld; v.w = nullptr; v.ldw = 0;
@@ -1313,9 +1316,11 @@ int hx::swiglu_ffn_impl(const hx_memref2d* x, const hx_memref1d* gamma, float ep
   if (gamma && (rc = view1(gamma, HX_F16, "gamma", H, &vg))) return rc;
   if (T == 0) return HX_OK;
 
-  // up to 64 tokens: the row-block decode GEMVs (T = 17 / 64: 68.9 / 113.4 us
-  // against 78.1 / 119.2 with the fused gate/up GEMM at H = 4096, I = 11008)
-  const bool skinny = T <= kGemvMaxRows;
+  // up to 32 tokens: the decode GEMVs and their row blocks (H = 4096,
+  // I = 11008, T = 17 / 24 / 32: 61.1 / 63.8 / 69.2 us against 76.0 / 78.4 /
+  // 82.0 with the fused gate/up GEMM); beyond, the GEMMs (T = 48 / 64: 100.3
+  // / 107.4 us, the row blocks 103.0 / 112.8)
+  const bool skinny = T <= kGemvRowsMaxM;
   Carver cv;
   const size_t off_h = cv.take((size_t)T * H * 2);
   const size_t off_a = cv.take((size_t)T * I * 2);

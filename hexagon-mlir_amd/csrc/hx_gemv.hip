@@ -649,9 +649,13 @@ static const GemvStreamEntry kGemvStream[] = {
     {{3, 8, "packed_ct3_kw8", 0, 19, 1}, HX_GV(3, 8, 8, XS_NONE, false)},
     {{3, 16, "packed_ct3_kw16", 0, 20, 1}, HX_GV(3, 16, 4, XS_NONE, false)},
     // three tiles with two or four row blocks: one workgroup per CU at
-    // N = 11008 for 16 < M <= 64
+    // N = 11008 for 16 < M <= 32 (two blocks) or 64 (four)
     {{3, 8, "rows2_ct3_kw8", 0, 21, 2}, HX_GR(3, 8, 4, 2)},
     {{3, 8, "rows4_ct3_kw8", 0, 22, 4}, HX_GR(3, 8, 2, 4)},
+    // sixteen waves over K: more weight bytes in flight per CU when N gives
+    // one tile per CU (the FFN's down projection, N = 4096, K = 11008)
+    {{1, 16, "rows2_ct1_kw16", 0, 23, 2}, HX_GR(1, 16, 4, 2)},
+    {{1, 16, "packed_ct1_kw16", 0, 24, 1}, HX_GV(1, 16, 4, XS_NONE, false)},
 };
 #undef HX_GR
 #undef HX_GV
@@ -676,20 +680,26 @@ static int launch_gemv_stream(int cfg_idx, int wt, bool packed, const GemvArgs& 
   // 32-bit buffer offsets: one workgroup's weight range and the activation rows
   const int64_t wg_bytes = packed ? ct * kchunks * 1024 : 16 * ct * ldw * (wt == DT_I8 ? 1 : 2);
   if (wg_bytes >= ((int64_t)1 << 31) || a.M * a.ldx * 2 >= ((int64_t)1 << 31)) return HXI_ERR_SHAPE;
-  // xl: staged rows within 64 KiB of LDS
-  if (kGemvStream[cfg_idx].cfg.xl && (a.M > 4 || a.M * ((kchunks * kd + 511) / 512 * 512 + 8) * 2 > 65536))
+  if (kGemvStream[cfg_idx].cfg.xl && !gemv_xl_fits(kGemvStream[cfg_idx].cfg, a.M, a.K, wt))
     cfg_idx = kGemvStream[cfg_idx].cfg.base;
   kGemvStream[cfg_idx].fn[slot](a, w, ldw, (int)kchunks, s);
   return HXI_OK;
 }
-// Measured at M = 17..64 (rotating resident weights): when N leaves >= 160
-// workgroups of four tiles (int8 and f16, N = 11008), two tiles and two row
-// blocks up to 32 rows (int8 M = 17 / 24: 16.9 / 19.7 us against 21.7 / 22.2
-// for four and four) and four tiles and four row blocks beyond; else one
-// tile with two or four row blocks (f16, N = 4096).
+bool gemv_xl_fits(const GemvConfig& c, int64_t M, int64_t K, int wt) {
+  if (!c.xl) return true;
+  const int64_t kd = wt == DT_I8 ? 64 : 32;
+  return M <= 4 && M * (((K + kd - 1) / kd * kd + 511) / 512 * 512 + 8) * 2 <= 65536;
+}
+// Measured at M = 17..64 (tuner medians, rotating packed images): up to 32
+// rows two row blocks over three tiles where that gives one workgroup per
+// CU (int8 N = 11008, M = 17 / 24 / 32: 15.2 / 15.8 / 16.7 us against 17.1 /
+// 19.9 / 23.4 for two tiles), two tiles above 256 tiles, else one tile over
+// 16 waves (int8 N = 4096, K = 11008: 18.7 / 22.2 / 26.5 against 25.1 / 26.5
+// / 29.6 over 8 waves); beyond 32 rows (kernels only: the products route
+// those shapes to the tiled GEMM) four row blocks over four tiles or one.
 int gemv_rows_default(int64_t M, int64_t N) {
   const int64_t tiles = (N + 15) / 16;
-  if (M <= 32) return (tiles + 255) / 256 == 3 ? 21 : tiles > 256 ? 14 : 13;
+  if (M <= 32) return (tiles + 255) / 256 == 3 ? 21 : tiles > 256 ? 14 : 23;
   return N >= 160 * 64 ? 17 : 15;
 }
 int launch_gemv_packed(int cfg_idx, const GemvArgs& a, const int8_t* packed, hipStream_t s) {

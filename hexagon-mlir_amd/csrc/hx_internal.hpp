@@ -103,22 +103,27 @@ struct GemvConfig {
 };
 // Largest M the decode GEMV takes (row-block configs).
 constexpr int kGemvMaxRows = 64;
-// Where 16 < M <= kGemvRowsMaxM rows of an f16 / bf16 weight (registered or
-// argument) or an argument int8 weight take the decode GEMV's row blocks
-// rather than the tiled GEMM: N >= kGemvRowsMinN (fewer 16-column tiles
-// leave most CUs idle), and for a [N][K] weight read in place (sixteen
-// 64-byte runs per wave load, not one contiguous KiB) N <= kGemvRowsInPlaceMaxN.
-// A registered int8 weight's packed image takes them to kGemvMaxRows rows.
+// Where 16 < M <= kGemvRowsMaxM rows take the decode GEMV's row blocks
+// rather than the tiled GEMM: on a registered int8 weight's packed image
+// always; on an f16 / bf16 packed image when N >= kGemvRowsMinN (fewer
+// 16-column tiles leave most CUs idle); on a [N][K] weight read in place
+// (sixteen 64-byte runs per wave load, not one contiguous KiB) when also
+// N <= kGemvRowsInPlaceMaxN.  The kernels themselves take kGemvMaxRows.
 constexpr int64_t kGemvRowsMaxM = 32;
 constexpr int64_t kGemvRowsMinN = 2048;
 constexpr int64_t kGemvRowsInPlaceMaxN = 4096;
-inline bool gemv_rows_route(int64_t M, int64_t N, bool packed) {
+inline bool gemv_rows_route(int64_t M, int64_t N, bool packed, bool int8 = false) {
   if (M <= 16) return true;
-  if (M > kGemvRowsMaxM || N < kGemvRowsMinN) return false;
+  if (M > kGemvRowsMaxM) return false;
+  if (packed && int8) return true;
+  if (N < kGemvRowsMinN) return false;
   return packed || N <= kGemvRowsInPlaceMaxN;
 }
 // Untuned row-block config for 16 < M <= kGemvMaxRows.
 int gemv_rows_default(int64_t M, int64_t N);
+// Whether config c may stage M activation rows of K (wt: the weight's type)
+// in LDS; a config that may not runs as its base config.
+bool gemv_xl_fits(const GemvConfig& c, int64_t M, int64_t K, int wt);
 bool gemv_fast_ok(const GemvArgs& a);
 const char* gemv_fast_refusal(const GemvArgs& a);
 // Column tiles per workgroup (1, 2 or 4 as index 0..2) of the [N][K] kernel.

@@ -127,9 +127,7 @@ class Probe {
     if (gemv_op(op_)) {
       const GemvConfig* c = gemv_packed_config(t);
       if (m_ > 16 * c->mb) return "rows-exceed-blocks";
-      const int64_t kd = op_ == HX_OP_GEMV_W8 ? 64 : 32;
-      const int64_t kpad = ((k_ + kd - 1) / kd * kd + 511) / 512 * 512;
-      if (c->xl && (m_ > 4 || m_ * (kpad + 8) * 2 > 65536)) return "staging-limit";
+      if (!gemv_xl_fits(*c, m_, k_, wt_)) return "staging-limit";
       if (16 * c->ct > std::max<int64_t>(16, pad_pow2(n_))) return "tile-exceeds-extent";
       return nullptr;
     }
@@ -289,9 +287,9 @@ class Probe {
     const int xt = op_ == HX_OP_GEMV_BF16 ? DT_BF16 : DT_F16;
     out_dt_ = xt;
     exact_ = false;
-    // the shapes the products run on this family: the packed int8 weight's
-    // row blocks to kGemvMaxRows rows, the f16 / bf16 image's by the routing
-    if (m_ > kGemvMaxRows || (op_ != HX_OP_GEMV_W8 && !gemv_rows_route(m_, n_, true))) family_reason_ = "family-shape";
+    // the shapes the products run on this family (a registered weight's
+    // packed image)
+    if (m_ > kGemvMaxRows || !gemv_rows_route(m_, n_, true, op_ == HX_OP_GEMV_W8)) family_reason_ = "family-shape";
     const int64_t mm = std::min<int64_t>(m_, kGemvMaxRows);
     const size_t eb = es_of(wt_);
     // every family times the registered weight's packed image, the form a

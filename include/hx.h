@@ -222,7 +222,7 @@ int hx_weight_info(hx_weight_t w, int64_t* k, int64_t* n, int* dtype,
 
 /* Y = X . W * scale (+ residual) with a registered weight.  X [M, K] f16
  * (bf16 for a bf16 weight), Y [M, N] f16/bf16/f32.  Skinny products (int8
- * weights M <= 64; f16 / bf16 M <= 16, or M <= 32 with N >= 2048) run the
+ * weights M <= 32; f16 / bf16 M <= 16, or M <= 32 with N >= 2048) run the
  * decode GEMV on the weight's fragment-packed copy (registration keeps it
  * beside the [N, K] image: twice the weight's bytes), larger M the MFMA GEMM. */
 int hx_matmul_resident(const hx_memref2d* x, int x_dtype, hx_weight_t w,
@@ -249,7 +249,7 @@ int hx_swiglu_ffn(const hx_memref2d* x, const hx_memref1d* gamma, float eps,
  * K-split partials live in a fixed device array of HX_NOALLOC_SCRATCH_BYTES
  * that each GPU the library runs on holds until the process ends, instead
  * of the stream workspace.  The call makes no hipMalloc or hipFree.  It
- * needs T*(H + I)*2 bytes for T > 64 tokens (T*(H + 3 I)*2 for T <= 64, the
+ * needs T*(H + I)*2 bytes for T > 32 tokens (T*(H + 3 I)*2 for T <= 32, the
  * decode path), plus T*H*4 per K part when the down projection's
  * configuration splits K (256-byte aligned each); a shape that needs more
  * than the array returns HX_ERR_UNSUPPORTED before anything is enqueued.

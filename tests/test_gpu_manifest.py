@@ -41,7 +41,8 @@ def test_manifest_records_plans_and_reasons(hx, dev):
         rw = hx.ResidentWeight(w, s, layout="nk")
         try:
             hx.matmul_resident(x, rw)                            # packed decode GEMV
-            hx.matmul_resident(torch.randn((64, 512), dtype=torch.float16, device=dev), rw)   # row blocks
+            hx.matmul_resident(torch.randn((32, 512), dtype=torch.float16, device=dev), rw)   # row blocks
+            hx.matmul_resident(torch.randn((48, 512), dtype=torch.float16, device=dev), rw)   # tiled
             hx.matmul_resident(torch.randn((128, 512), dtype=torch.float16, device=dev), rw)  # tiled
         finally:
             rw.release()
@@ -84,8 +85,9 @@ def test_manifest_records_plans_and_reasons(hx, dev):
     assert find(entry="hx_gemm_i8", n=36, k=504)["reason"] == "row-stride"  # ldb = 504
     assert find(entry="hx_matmul", m=4, plan="gemv-stream")["reason"] == "min-rows"
     assert find(entry="hx_matmul_resident", m=4)["plan"] == "gemv-packed"
-    r = find(entry="hx_matmul_resident", m=64)
+    r = find(entry="hx_matmul_resident", m=32)
     assert r["plan"] == "gemv-packed" and r["reason"] == "few-rows" and r["config"].startswith("rows")
+    assert find(entry="hx_matmul_resident", m=48)["plan"] == "mfma-tiled"
     r = find(entry="hx_matmul_resident", m=128)
     assert r["plan"] == "mfma-tiled" and r["weight"] == "resident-image" and r["b"] == "i8"
     r = find(entry="hx_matmul", m=20, n=2048, weight="argument")
