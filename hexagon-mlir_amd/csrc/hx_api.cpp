@@ -371,7 +371,18 @@ static int resolve_gemm(int op, int64_t M, int64_t N, int64_t K, bool* was_pinne
 // Untuned GEMV config (table index = family index) for a shape.
 // in_place: an f16 / bf16 [N][K] weight read where it lies (argument
 // weights); otherwise a registered weight's packed image.
+static int gemv_untuned_table(int op, int64_t M, int64_t N, int64_t K, bool in_place);
+// The untuned config as it runs: a config that stages the activations in
+// LDS is named by its base config where the rows do not fit (the launcher
+// runs the base), so the tuner's control and the plan record match the
+// kernel that runs.
 static int gemv_untuned(int op, int64_t M, int64_t N, int64_t K, bool in_place = false) {
+  const int t = gemv_untuned_table(op, M, N, K, in_place);
+  const GemvConfig* c = gemv_packed_config(t);
+  const int wt = op == HX_OP_GEMV_W8 ? HX_I8 : op == HX_OP_GEMV_BF16 ? HX_BF16 : HX_F16;
+  return c && !gemv_xl_fits(*c, M, K, wt) ? c->base : t;
+}
+static int gemv_untuned_table(int op, int64_t M, int64_t N, int64_t K, bool in_place) {
   if (M > 16) return gemv_rows_default(M, N);
   const int64_t tiles = (N + 15) / 16;
   const bool three_tiles = (tiles + 255) / 256 == 3;  // N = 11008: 688 tiles, 230 workgroups

@@ -178,6 +178,11 @@ __device__ __forceinline__ v4f mfma16_f16(v8h a, v8h b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// Cache policy of buffer stores whose lines should not wait dirty in L2 for
+// the end-of-kernel write-back: SC0 | SC1 (system-scope coherent, i.e.
+// written through to memory).
+constexpr int kStoreWriteThrough = 1 | 16;
+
 // ---- direct-to-LDS staging (GEMM and attention) -------------------------
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 

@@ -63,9 +63,6 @@ template <> struct ModeTraits<GM_W8> {
 // (both the 32-bank/8-lane and the 64-bank/16-lane service patterns).
 __device__ __forceinline__ int swz128(int row) { return (row ^ (row >> 3)) & 7; }
 
-// Cache policy of the epilogue's buffer stores: SC0 | SC1 (system-scope
-// coherent, i.e. written through to memory).
-constexpr int kStoreWriteThrough = 1 | 16;
 // 64-byte rows (the W8 weight tile, 64-byte int8 stages): the chunk is XORed
 // with the row's index among groups of four.  Timed on the fragment read
 // pattern (32 rows x 2 adjacent chunks per wave read): 2.08 ns per wave read
