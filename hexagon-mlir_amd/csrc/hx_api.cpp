@@ -856,6 +856,18 @@ static int row_dtype_ok(int dt, const char* who) {
   return HX_OK;
 }
 
+// A row longer than the register path holds: the two-pass kernels, their
+// per-segment statistics in the stream's workspace.
+static int run_row_long(int op, int dtype, const View2& vx, const void* w, const void* b, float eps,
+                        const View2& vy, float* mean, float* rstd, hipStream_t s, const char* what) {
+  char* ws = nullptr;
+  int rc = ws_get(s, row_long_ws_bytes(dtype, vx.rows, vx.cols), &ws);
+  if (rc) return rc;
+  return map_internal(launch_row_long(op, dtype, vx.p, vx.ld, w, b, eps, vy.p, vy.ld, mean, rstd, vx.rows,
+                                      vx.cols, ws, s),
+                      what);
+}
+
 extern "C" int hx_softmax(const hx_memref2d* x, hx_memref2d* y, int dtype, hx_stream_t stream) {
   int rc;
   if ((rc = row_dtype_ok(dtype, "hx_softmax"))) return rc;
@@ -863,8 +875,11 @@ extern "C" int hx_softmax(const hx_memref2d* x, hx_memref2d* y, int dtype, hx_st
   if ((rc = view2(x, dtype, "x", &vx)) || (rc = view2(y, dtype, "y", &vy))) return rc;
   if (vx.rows != vy.rows || vx.cols != vy.cols) return fail(HX_ERR_SHAPE, "hx_softmax: x/y shape");
   if (vx.rows == 0 || vx.cols == 0) return HX_OK;
-  return map_internal(launch_softmax(dtype, vx.p, vx.ld, vy.p, vy.ld, vx.rows, vx.cols, (hipStream_t)stream),
-                      "softmax");
+  const hipStream_t s = (hipStream_t)stream;
+  rc = launch_softmax(dtype, vx.p, vx.ld, vy.p, vy.ld, vx.rows, vx.cols, s);
+  if (rc == HXI_ERR_UNSUPPORTED)
+    return run_row_long(ROW_OP_SOFTMAX, dtype, vx, nullptr, nullptr, 0.f, vy, nullptr, nullptr, s, "softmax");
+  return map_internal(rc, "softmax");
 }
 
 extern "C" int hx_rmsnorm(const hx_memref2d* x, const hx_memref1d* gamma, float eps, hx_memref2d* y,
@@ -877,9 +892,12 @@ extern "C" int hx_rmsnorm(const hx_memref2d* x, const hx_memref1d* gamma, float 
   if (vx.rows != vy.rows || vx.cols != vy.cols) return fail(HX_ERR_SHAPE, "hx_rmsnorm: x/y shape");
   if (gamma && (rc = view1(gamma, dtype, "gamma", vx.cols, &vg))) return rc;
   if (vx.rows == 0 || vx.cols == 0) return HX_OK;
-  return map_internal(launch_rmsnorm(dtype, vx.p, vx.ld, gamma ? vg.p : nullptr, eps, vy.p, vy.ld,
-                                     vx.rows, vx.cols, (hipStream_t)stream),
-                      "rmsnorm");
+  const hipStream_t s = (hipStream_t)stream;
+  rc = launch_rmsnorm(dtype, vx.p, vx.ld, gamma ? vg.p : nullptr, eps, vy.p, vy.ld, vx.rows, vx.cols, s);
+  if (rc == HXI_ERR_UNSUPPORTED)
+    return run_row_long(ROW_OP_RMSNORM, dtype, vx, gamma ? vg.p : nullptr, nullptr, eps, vy, nullptr, nullptr, s,
+                        "rmsnorm");
+  return map_internal(rc, "rmsnorm");
 }
 
 extern "C" int hx_layernorm(const hx_memref2d* x, const hx_memref1d* w, const hx_memref1d* b, float eps,
@@ -896,11 +914,15 @@ extern "C" int hx_layernorm(const hx_memref2d* x, const hx_memref1d* w, const hx
   if (mean && (rc = view1(mean, HX_F32, "mean", vx.rows, &vm))) return rc;
   if (rstd && (rc = view1(rstd, HX_F32, "rstd", vx.rows, &vr))) return rc;
   if (vx.rows == 0 || vx.cols == 0) return HX_OK;
-  return map_internal(launch_layernorm(dtype, vx.p, vx.ld, w ? vw.p : nullptr, b ? vb.p : nullptr, eps,
-                                       vy.p, vy.ld, mean ? (float*)vm.p : nullptr,
-                                       rstd ? (float*)vr.p : nullptr, vx.rows, vx.cols,
-                                       (hipStream_t)stream),
-                      "layernorm");
+  const hipStream_t s = (hipStream_t)stream;
+  float* mp = mean ? (float*)vm.p : nullptr;
+  float* rp = rstd ? (float*)vr.p : nullptr;
+  rc = launch_layernorm(dtype, vx.p, vx.ld, w ? vw.p : nullptr, b ? vb.p : nullptr, eps, vy.p, vy.ld, mp, rp,
+                        vx.rows, vx.cols, s);
+  if (rc == HXI_ERR_UNSUPPORTED)
+    return run_row_long(ROW_OP_LAYERNORM, dtype, vx, w ? vw.p : nullptr, b ? vb.p : nullptr, eps, vy, mp, rp, s,
+                        "layernorm");
+  return map_internal(rc, "layernorm");
 }
 
 extern "C" int hx_silu_mul(const hx_memref2d* g, const hx_memref2d* u, hx_memref2d* out, int dtype,

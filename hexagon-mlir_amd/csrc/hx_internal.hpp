@@ -28,6 +28,14 @@ int launch_layernorm(int dtype, const void* x, int64_t ldx, const void* w, const
                      int64_t rows, int64_t cols, hipStream_t s);
 int launch_silu_mul_f16(const void* g, int64_t ldg, const void* u, int64_t ldu, void* o,
                         int64_t ldo, int64_t rows, int64_t cols, hipStream_t s);
+// Rows longer than the launches above hold in registers (they return
+// HXI_ERR_UNSUPPORTED without launching): two streaming passes, with
+// row_long_ws_bytes() of per-segment statistics in `ws`.
+enum RowOpCode : int { ROW_OP_SOFTMAX = 0, ROW_OP_RMSNORM = 1, ROW_OP_LAYERNORM = 2 };
+size_t row_long_ws_bytes(int dtype, int64_t rows, int64_t cols);
+int launch_row_long(int op, int dtype, const void* x, int64_t ldx, const void* w, const void* b, float eps,
+                    void* y, int64_t ldy, float* mean, float* rstd, int64_t rows, int64_t cols, void* ws,
+                    hipStream_t s);
 
 // ---- MFMA GEMM (hx_gemm.hip) ---------------------------------------------
 // Operand modes.  B is always consumed K-contiguous ([N][K], "NK").

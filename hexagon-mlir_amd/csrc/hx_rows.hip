@@ -436,6 +436,281 @@ int launch_layernorm(int dtype, const void* x, int64_t ldx, const void* w, const
 }
 
 // ---------------------------------------------------------------------------
+// Rows longer than the register path holds (more than 4096 16-byte vectors):
+// two passes over the row, the two-phase form of the reference's online
+// softmax (test/python/triton/test_online_softmax.py:28-78; Milakov and
+// Gimelshein, "Online normalizer calculation for softmax", 2018) applied to
+// all three ops.  Each row is cut into S segments of L elements (L a
+// multiple of one 256-thread sweep); workgroup b handles segment b % S of
+// row b / S.
+//   pass 1 (row_long_stats_kernel) folds its segment into one statistic:
+//     softmax   (m, l): the maximum, and the sum of exp(x - m);
+//     RMSNorm   the sum of x^2;
+//     LayerNorm (n, mean, M2), merged with Chan, Golub and LeVeque's
+//               pairwise update (mean += d n2 / n, M2 += M2' + d^2 n1 n2 / n);
+//   pass 2 (row_long_apply_kernel) merges the row's S statistics and writes
+//   its segment as the register path would with the merged values.  It walks
+//   the workgroups in reverse, so the rows pass 1 read last are read again
+//   first, while the 256 MB MALL still holds them.
+// Every merge runs in a fixed order (lower index first), so results do not
+// depend on scheduling.  The row is read twice and written once; each thread
+// has kLongUnroll 16-byte loads in flight.
+struct RowStat { float a, b, c, d; };
+
+template <int OP>
+__device__ __forceinline__ RowStat stat_identity() {
+  if constexpr (OP == ROW_SOFTMAX) return RowStat{-INFINITY, 0.f, 0.f, 0.f};
+  else return RowStat{0.f, 0.f, 0.f, 0.f};
+}
+
+template <int OP>
+__device__ __forceinline__ RowStat stat_merge(RowStat x, RowStat y) {
+  if constexpr (OP == ROW_SOFTMAX) {
+    const float m = fmaxf(x.a, y.a);
+    if (m == -INFINITY) return x;  // nothing but -inf so far: l stays 0
+    return RowStat{m, x.b * fast_exp(x.a - m) + y.b * fast_exp(y.a - m), 0.f, 0.f};
+  } else if constexpr (OP == ROW_RMSNORM) {
+    return RowStat{x.a + y.a, 0.f, 0.f, 0.f};
+  } else {
+    // (a, b, c) = (n, mean, M2)
+    const float n = x.a + y.a;
+    if (n == 0.f) return x;
+    const float d = y.b - x.b;
+    const float f = y.a / n;
+    return RowStat{n, x.b + d * f, x.c + y.c + d * d * x.a * f, 0.f};
+  }
+}
+
+// Merge lane 0..63's statistics into lane 0 (lower lane first at each step).
+template <int OP>
+__device__ __forceinline__ RowStat stat_wave_reduce(RowStat v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    RowStat u{__shfl_down(v.a, o, 64), __shfl_down(v.b, o, 64), __shfl_down(v.c, o, 64), 0.f};
+    if ((threadIdx.x & 63) + o < 64) v = stat_merge<OP>(v, u);
+  }
+  return v;
+}
+
+// The statistic of `cnt` consecutive elements held by one thread.
+template <int OP, int EV>
+__device__ __forceinline__ RowStat stat_of(const float* v, int cnt) {
+  if constexpr (OP == ROW_SOFTMAX) {
+    float m = -INFINITY;
+    for (int j = 0; j < cnt; ++j) m = fmaxf(m, v[j]);
+    if (m == -INFINITY) return RowStat{m, 0.f, 0.f, 0.f};
+    float l = 0.f;
+    for (int j = 0; j < cnt; ++j) l += fast_exp(v[j] - m);
+    return RowStat{m, l, 0.f, 0.f};
+  } else if constexpr (OP == ROW_RMSNORM) {
+    float ss = 0.f;
+    for (int j = 0; j < cnt; ++j) ss += v[j] * v[j];
+    return RowStat{ss, 0.f, 0.f, 0.f};
+  } else {
+    if (cnt == 0) return RowStat{0.f, 0.f, 0.f, 0.f};
+    float s = 0.f;
+    for (int j = 0; j < cnt; ++j) s += v[j];
+    const float mean = s / (float)cnt;
+    float m2 = 0.f;
+    for (int j = 0; j < cnt; ++j) m2 += (v[j] - mean) * (v[j] - mean);
+    return RowStat{(float)cnt, mean, m2, 0.f};
+  }
+}
+
+// Load the EV elements of vector `vi` of the row (columns vi*EV ..), those
+// at or past `cols` reading as absent (the count is returned).
+template <int DT, bool VEC>
+__device__ __forceinline__ int load_vec(const typename Elem<DT>::storage* xr, int64_t vi, int64_t cols,
+                                        float* v) {
+  typedef typename Elem<DT>::storage S;
+  constexpr int EV = 16 / sizeof(S);
+  const int64_t c0 = vi * EV;
+  if (c0 >= cols) return 0;
+  if constexpr (VEC) {
+    const v4u raw = *reinterpret_cast<const v4u*>(xr + c0);
+    const S* e = reinterpret_cast<const S*>(&raw);
+#pragma unroll
+    for (int j = 0; j < EV; ++j) v[j] = Elem<DT>::load(e[j]);
+    return EV;
+  } else {
+    const int cnt = (int)min((int64_t)EV, cols - c0);
+    for (int j = 0; j < cnt; ++j) v[j] = Elem<DT>::load(xr[c0 + j]);
+    return cnt;
+  }
+}
+
+constexpr int kLongUnroll = 4;
+
+template <int OP, int DT, bool VEC>
+__global__ void __launch_bounds__(256) row_long_stats_kernel(RowArgs a, int S, int64_t seg_vecs, RowStat* st) {
+  typedef typename Elem<DT>::storage Sx;
+  constexpr int EV = 16 / sizeof(Sx);
+  __shared__ RowStat red[4];
+  const int64_t row = blockIdx.x / S;
+  const int seg = (int)(blockIdx.x - row * S);
+  const Sx* xr = reinterpret_cast<const Sx*>(a.x) + row * a.ldx;
+  const int64_t v0 = (int64_t)seg * seg_vecs;
+  RowStat acc = stat_identity<OP>();
+  for (int64_t i0 = threadIdx.x; i0 < seg_vecs; i0 += 256 * kLongUnroll) {
+    float v[kLongUnroll][EV];
+    int cnt[kLongUnroll];
+#pragma unroll
+    for (int u = 0; u < kLongUnroll; ++u) {
+      const int64_t i = i0 + 256 * u;
+      cnt[u] = i < seg_vecs ? load_vec<DT, VEC>(xr, v0 + i, a.cols, v[u]) : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kLongUnroll; ++u) acc = stat_merge<OP>(acc, stat_of<OP, EV>(v[u], cnt[u]));
+  }
+  acc = stat_wave_reduce<OP>(acc);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[wave] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    RowStat t = red[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) t = stat_merge<OP>(t, red[w]);
+    st[blockIdx.x] = t;
+  }
+}
+
+template <int OP, int DT, bool VEC>
+__global__ void __launch_bounds__(256) row_long_apply_kernel(RowArgs a, int S, int64_t seg_vecs, const RowStat* st) {
+  typedef typename Elem<DT>::storage Sx;
+  constexpr int EV = 16 / sizeof(Sx);
+  __shared__ RowStat row_stat;
+  const int64_t b = (int64_t)gridDim.x - 1 - blockIdx.x;  // reverse of pass 1's order
+  const int64_t row = b / S;
+  const int seg = (int)(b - row * S);
+  // the row's S <= 64 statistics, merged by the first wave in segment order
+  if (threadIdx.x < 64) {
+    RowStat t = threadIdx.x < S ? st[row * S + threadIdx.x] : stat_identity<OP>();
+    t = stat_wave_reduce<OP>(t);
+    if (threadIdx.x == 0) row_stat = t;
+  }
+  __syncthreads();
+  const RowStat rs = row_stat;
+  float scale, shift = 0.f;
+  if constexpr (OP == ROW_SOFTMAX) {
+    scale = 1.0f / rs.b;  // DivToMul: one reciprocal, then multiplies
+    shift = rs.a;
+  } else if constexpr (OP == ROW_RMSNORM) {
+    scale = 1.0f / sqrtf(rs.a / (float)a.cols + a.eps);
+  } else {
+    scale = 1.0f / sqrtf(rs.c / (float)a.cols + a.eps);
+    shift = rs.b;
+    if (seg == 0 && threadIdx.x == 0) {
+      if (a.mean) a.mean[row] = rs.b;
+      if (a.rstd) a.rstd[row] = scale;
+    }
+  }
+  const Sx* xr = reinterpret_cast<const Sx*>(a.x) + row * a.ldx;
+  Sx* yr = reinterpret_cast<Sx*>(a.y) + row * a.ldy;
+  const Sx* wp = reinterpret_cast<const Sx*>(a.w);
+  const Sx* bp = reinterpret_cast<const Sx*>(a.b);
+  const int64_t v0 = (int64_t)seg * seg_vecs;
+  for (int64_t i0 = threadIdx.x; i0 < seg_vecs; i0 += 256 * kLongUnroll) {
+    float v[kLongUnroll][EV];
+    int cnt[kLongUnroll];
+#pragma unroll
+    for (int u = 0; u < kLongUnroll; ++u) {
+      const int64_t i = i0 + 256 * u;
+      cnt[u] = i < seg_vecs ? load_vec<DT, VEC>(xr, v0 + i, a.cols, v[u]) : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kLongUnroll; ++u) {
+      const int64_t c0 = (v0 + i0 + 256 * u) * EV;
+      Sx out[EV];
+#pragma unroll
+      for (int j = 0; j < EV; ++j) {
+        if (j >= cnt[u]) break;
+        float r;
+        if constexpr (OP == ROW_SOFTMAX) {
+          r = fast_exp(v[u][j] - shift) * scale;
+        } else if constexpr (OP == ROW_RMSNORM) {
+          r = v[u][j] * scale;
+          if (wp) r = r * Elem<DT>::load(wp[c0 + j]);
+        } else {
+          r = (v[u][j] - shift) * scale;
+          if (wp) r = r * Elem<DT>::load(wp[c0 + j]);
+          if (bp) r = r + Elem<DT>::load(bp[c0 + j]);
+        }
+        out[j] = Elem<DT>::store(r);
+      }
+      if (VEC && cnt[u] == EV) {
+        __builtin_nontemporal_store(*reinterpret_cast<const v4u*>(out), reinterpret_cast<v4u*>(yr + c0));
+      } else {
+        for (int j = 0; j < cnt[u]; ++j) yr[c0 + j] = out[j];
+      }
+    }
+  }
+}
+
+// Segments: about 1024 workgroups over all rows, at most 64 per row, each
+// at least four vectors per thread.
+static void row_long_plan(int64_t rows, int64_t cols, int ev, int* S, int64_t* seg_vecs) {
+  const int64_t vecs = (cols + ev - 1) / ev;
+  int64_t s = std::min<int64_t>((1024 + rows - 1) / rows, 64);
+  s = std::max<int64_t>(1, std::min<int64_t>(s, vecs / (256 * 4)));
+  int64_t sv = (vecs + s - 1) / s;
+  sv = (sv + 255) / 256 * 256;
+  *seg_vecs = sv;
+  *S = (int)((vecs + sv - 1) / sv);
+}
+
+size_t row_long_ws_bytes(int dtype, int64_t rows, int64_t cols) {
+  int S;
+  int64_t sv;
+  row_long_plan(rows, cols, dtype == DT_F32 ? 4 : 8, &S, &sv);
+  return (size_t)rows * S * sizeof(RowStat);
+}
+
+template <int OP, int DT, bool VEC>
+static int launch_row_long_cfg(const RowArgs& a, void* ws, hipStream_t s) {
+  constexpr int EV = DT == DT_F32 ? 4 : 8;
+  int S;
+  int64_t sv;
+  row_long_plan(a.rows, a.cols, EV, &S, &sv);
+  const int64_t blocks = a.rows * S;
+  if (blocks >= ((int64_t)1 << 31)) return HXI_ERR_SHAPE;
+  RowStat* st = static_cast<RowStat*>(ws);
+  row_long_stats_kernel<OP, DT, VEC><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(a, S, sv, st);
+  row_long_apply_kernel<OP, DT, VEC><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(a, S, sv, st);
+  return 0;
+}
+
+template <int OP, int DT>
+static int launch_row_long_dt(const RowArgs& a, void* ws, hipStream_t s) {
+  typedef typename Elem<DT>::storage Sx;
+  constexpr int EV = 16 / sizeof(Sx);
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  const bool vec = (a.cols % EV) == 0 && al16(a.x) && al16(a.y) &&
+                   ((a.ldx * (int64_t)sizeof(Sx)) % 16) == 0 && ((a.ldy * (int64_t)sizeof(Sx)) % 16) == 0;
+  return vec ? launch_row_long_cfg<OP, DT, true>(a, ws, s) : launch_row_long_cfg<OP, DT, false>(a, ws, s);
+}
+
+int launch_row_long(int op, int dtype, const void* x, int64_t ldx, const void* w, const void* b, float eps,
+                    void* y, int64_t ldy, float* mean, float* rstd, int64_t rows, int64_t cols, void* ws,
+                    hipStream_t s) {
+  RowArgs a{x, ldx, y, ldy, w, b, mean, rstd, eps, rows, cols};
+  auto by_dt = [&](auto opc) -> int {
+    constexpr int OP = decltype(opc)::value;
+    switch (dtype) {
+      case DT_F16: return launch_row_long_dt<OP, DT_F16>(a, ws, s);
+      case DT_BF16: return launch_row_long_dt<OP, DT_BF16>(a, ws, s);
+      case DT_F32: return launch_row_long_dt<OP, DT_F32>(a, ws, s);
+      default: return HXI_ERR_DTYPE;
+    }
+  };
+  switch (op) {
+    case ROW_SOFTMAX: return by_dt(std::integral_constant<int, ROW_SOFTMAX>{});
+    case ROW_RMSNORM: return by_dt(std::integral_constant<int, ROW_RMSNORM>{});
+    case ROW_LAYERNORM: return by_dt(std::integral_constant<int, ROW_LAYERNORM>{});
+    default: return HXI_ERR_ARG;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // SiLU * mul: out = RNE(silu(g) * u), silu(g) = g / (1 + exp(-g)).  fp16
 // rows, 16-byte vectors; a grid-stride loop over 8-element groups.
 // ---------------------------------------------------------------------------

@@ -47,7 +47,7 @@ def test_attention_sweep(hx, dev, Z, H, Nq, Nk, D, causal, dt):
     assert np.linalg.norm(got - want) <= 1e-2 * max(np.linalg.norm(want), 1e-6)
 
 
-# longest row the row kernels take: 4096 16-byte vectors
+# longest row the register path holds: 4096 16-byte vectors
 MAX_COLS = {"f16": 32768, "bf16": 32768, "f32": 16384}
 
 
@@ -101,14 +101,12 @@ def test_resident_decode_sweep(hx, dev, M, N, K, layout, residual):
 
 
 @pytest.mark.parametrize("dtype", ["f16", "f32"])
-def test_rows_longest_and_refused(hx, dev, dtype):
-    """The longest row is taken; one element more is refused with
-    HX_ERR_UNSUPPORTED (no launch)."""
+def test_rows_longest_and_beyond(hx, dev, dtype):
+    """The longest row the register path holds, and one element more (the
+    two-pass streaming path), both against the oracle."""
     n = MAX_COLS[dtype]
-    xh, _ = make(dtype, (2, n), seed=5)
     rtol, atol = TOL[dtype]
-    y = hx.softmax(to_torch(xh, dtype, dev))
-    assert_close(values(to_np(y), dtype), values(oracle.softmax(xh), dtype), rtol, atol, "softmax longest row")
-    x2, _ = make(dtype, (2, n + 1), seed=6)
-    with pytest.raises(hx.HXError, match="UNSUPPORTED"):
-        hx.softmax(to_torch(x2, dtype, dev))
+    for cols, seed in ((n, 5), (n + 1, 6)):
+        xh, _ = make(dtype, (2, cols), seed=seed)
+        y = hx.softmax(to_torch(xh, dtype, dev))
+        assert_close(values(to_np(y), dtype), values(oracle.softmax(xh), dtype), rtol, atol, f"softmax {cols}")
