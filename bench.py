@@ -320,6 +320,15 @@ def cpu_baselines_secondary(march: str) -> dict:
                          us_per_call=round(t * 1e6, 1),
                          sample=f"full {name} fp16 [{R} x {C}], oracle row loop, median of 3 after a warm-up")
     del xr
+    # vocabulary-length softmax on a 64-row sample of the 2048 x 128256 rows
+    R, C = 64, 128256
+    xv = (r.normal(0, 2, (R, C))).astype(np.float16)
+    t = _median_time(lambda: oracle.softmax(xv), 3)
+    out["softmax_vocab"] = dict(base, value=round(2 * R * C * 2 / t / 1e9, 3), unit="GB/s", cores=threads,
+                                us_per_call=round(t * 1e6, 1),
+                                sample=f"softmax fp16 [{R} x {C}] (64 of the 2048 rows), oracle row loop, "
+                                       f"median of 3 after a warm-up")
+    del xv
     # C1: fp16 256^3
     a = r.uniform(-1, 1, (256, 256)).astype(np.float16)
     b = r.uniform(-1, 1, (256, 256)).astype(np.float16)
@@ -433,6 +442,35 @@ def bench_rows(hx, iters: int = 60):
                     "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s", traffic_of(f"{name}_f16_8192x4096")),
                     "mall_defeat": "rotating 6 input/output sets (768 MiB)", "queue_fed": fed})
     return out
+
+
+def bench_rows_long(hx, iters: int = 20):
+    """Softmax over vocabulary-length rows (2048 x 128256 fp16, beyond the
+    register path: the two-pass streaming kernels), two rotating input /
+    output sets (2.1 GB), torch.softmax on the same tensors beside.  GB/s
+    counts the algorithmic bytes (one read, one write); the kernels read the
+    row twice."""
+    import torch
+    R, C = 2048, 128256
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(8)
+    xs = [torch.randn((R, C), dtype=torch.float16, device=dev, generator=g) * 2.0 for _ in range(2)]
+    ys = [torch.empty_like(x) for x in xs]
+    try:
+        calls = [hx.bind_row_op("softmax", x, y) for x, y in zip(xs, ys)]
+        for c in calls:
+            c()
+        ev_ms, fed = event_timed(calls, iters)
+        t_ms, _ = event_timed([(lambda x=x, y=y: torch.softmax(x, dim=-1, out=y)) for x, y in zip(xs, ys)], iters)
+    finally:
+        del xs, ys
+        torch.cuda.empty_cache()
+    gbs = 2 * R * C * 2 / (ev_ms * 1e-3) / 1e9
+    return {"workload": f"softmax fp16 [{R} x {C}] (vocabulary-length rows, two-pass)", "value": round(gbs, 1),
+            "unit": "GB/s", "us_per_call": round(ev_ms * 1e3, 2),
+            "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s"),
+            "bytes_moved_per_call": 3 * R * C * 2, "torch_us_same_tensors": round(t_ms * 1e3, 2),
+            "queue_fed": fed}
 
 
 def bench_gemm_i8_i32(hx, inputs, iters: int = 50):
@@ -1150,6 +1188,7 @@ def main() -> int:
         secondary += bench_gemv(hx, tune_on=tune_on)
         log("[bench] row ops")
         secondary += bench_rows(hx)
+        secondary.append(bench_rows_long(hx))
         log("[bench] fp16 GEMM 256^3")
         secondary.append(bench_gemm_f16_small(hx))
         log("[bench] fp16 matmul at the reference's published shapes")
@@ -1172,7 +1211,8 @@ def main() -> int:
         if secondary:
             sec_cpu = cpu_baselines_secondary(march)
             keys = {"W8A16 GEMV M=1 ": "gemv_m1", "W8A16 GEMV M=4 ": "gemv_m4", "W8A16 GEMV M=16 ": "gemv_m16",
-                    "softmax fp16": "softmax", "rmsnorm fp16": "rmsnorm", "fp16 GEMM 256^3": "gemm_f16_256",
+                    "softmax fp16 [8192": "softmax", "softmax fp16 [2048 x 128256]": "softmax_vocab",
+                    "rmsnorm fp16": "rmsnorm", "fp16 GEMM 256^3": "gemm_f16_256",
                     "SwiGLU FFN": "ffn"}
             keys.update({f"fp16 matmul {M}x{N}x{K} ": f"ref_{M}x{N}x{K}" for (M, N, K) in REF_SHAPES})
             keys.update({f"fp16 decode {M}x{N}x{K},": f"dec_{M}x{N}x{K}" for (M, N, K) in ((1, 8192, 8192),
