@@ -229,17 +229,32 @@ __device__ __forceinline__ float vec_elem(const v4u& v, int j) {
   }
 }
 
+// 8-wave rows: each pass converts the raw vectors again.  Left to itself the
+// compiler keeps the 256 converted binary32 elements per lane live across the
+// reductions (for f16, spilling); an empty asm that may change the raw
+// vectors makes every pass start from the 128 raw VGPRs (same values).
+template <int VPL>
+__device__ __forceinline__ void opaque_vecs(v4u (&raw)[VPL]) {
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) asm volatile("" : "+v"(raw[i]));
+}
+
+// WPR = 8 (512 threads, 32 vectors per lane, softmax only): one row of up
+// to 16384 vectors per CU, still a single pass; two waves per SIMD leave
+// 256 VGPRs (the norms would also hold gamma / beta vectors per lane, and
+// 16 waves of 16 vectors spilled at the 128 VGPRs four waves leave).
 template <int OP, int DT, int WPR, int VPL>
-__global__ void __launch_bounds__(256) row_vec_kernel(RowArgs a) {
+__global__ void __launch_bounds__(WPR > 4 ? 64 * WPR : 256) row_vec_kernel(RowArgs a) {
   typedef typename Elem<DT>::storage S;
   constexpr int EV = 16 / sizeof(S);
-  __shared__ float red[4];
+  static_assert(WPR <= 4 || OP == ROW_SOFTMAX, "8-wave rows: softmax only");
+  __shared__ float red[WPR > 4 ? WPR : 4];
 
   const int lane = threadIdx.x & 63;
   // wave index and row as provably uniform values: the row's buffer
   // descriptors below are built from them and must live in scalar registers
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const int rows_per_block = 4 / WPR;
+  const int rows_per_block = WPR >= 4 ? 1 : 4 / WPR;
   const int wave_in_row = (WPR == 1) ? 0 : wave;
   const int64_t row = (int64_t)blockIdx.x * rows_per_block + (WPR == 1 ? wave : 0);
   if (row >= a.rows) return;
@@ -289,6 +304,7 @@ __global__ void __launch_bounds__(256) row_vec_kernel(RowArgs a) {
         for (int j = 0; j < EV; ++j) m = fmaxf(m, vec_elem<DT>(raw[i], j));
       }
     m = group_max<WPR>(m, red);
+    if constexpr (WPR > 4) opaque_vecs<VPL>(raw);
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < VPL; ++i)
@@ -337,6 +353,7 @@ __global__ void __launch_bounds__(256) row_vec_kernel(RowArgs a) {
     }
   }
 
+  if constexpr (WPR > 4) opaque_vecs<VPL>(raw);
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     if (!ok[i]) continue;
@@ -383,7 +400,13 @@ static int launch_row_cfg(const RowArgs& a, hipStream_t s) {
     else if (vecs <= 256 * 4) { row_vec_kernel<OP, DT, 4, 4><<<dim3(a.rows), block, 0, s>>>(a); }
     else if (vecs <= 256 * 8) { row_vec_kernel<OP, DT, 4, 8><<<dim3(a.rows), block, 0, s>>>(a); }
     else if (vecs <= 256 * 16) { row_vec_kernel<OP, DT, 4, 16><<<dim3(a.rows), block, 0, s>>>(a); }
-    else return HXI_ERR_UNSUPPORTED;
+    else if constexpr (OP == ROW_SOFTMAX) {
+      // one workgroup per row: with fewer than 64 rows most CUs would idle,
+      // and the segmented two passes win (32 x 128256 f16: 19.6 against
+      // 14.9 us; 64 x 32776: 10.2 against 13.9)
+      if (vecs <= 512 * 32 && a.rows >= 64) row_vec_kernel<OP, DT, 8, 32><<<dim3(a.rows), dim3(512), 0, s>>>(a);
+      else return HXI_ERR_UNSUPPORTED;
+    } else return HXI_ERR_UNSUPPORTED;
   } else {
     if (vecs <= 64 * 1) { row_kernel<OP, DT, 1, 1, false><<<dim3(g1), block, 0, s>>>(a); }
     else if (vecs <= 64 * 4) { row_kernel<OP, DT, 1, 4, false><<<dim3(g1), block, 0, s>>>(a); }

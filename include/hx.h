@@ -173,10 +173,11 @@ int hx_gemv_w8a16(const hx_memref2d* x, const hx_memref2d* w, int w_layout,
  * (QHB/lib/Transforms/DivToMulOptimizationPass.cpp:9-18). */
 /* Row kernels (softmax, RMSNorm, LayerNorm) hold a row in registers up to
  * 4096 16-byte vectors, i.e. 16384 binary32 or 32768 f16/bf16 elements per
- * row, and stream longer rows in two passes (the two-phase online softmax of
- * test/python/triton/test_online_softmax.py:28-78, and its counterparts for
- * the norms), with rows x (at most 64 segments) x 16 bytes of statistics in
- * the stream workspace. */
+ * row (softmax over 16-byte-aligned rows, 64 rows or more: up to 16384
+ * vectors), and stream longer rows in two passes (the two-phase online
+ * softmax of test/python/triton/test_online_softmax.py:28-78, and its
+ * counterparts for the norms), with rows x (at most 64 segments) x 16 bytes
+ * of statistics in the stream workspace. */
 int hx_softmax(const hx_memref2d* x, hx_memref2d* y, int dtype, hx_stream_t stream);
 
 /* y = x * rsqrt(sum(x^2)/N + eps) * gamma   (gamma may be NULL).

@@ -1,7 +1,9 @@
-"""Rows longer than the register path holds (more than 16,384 binary32 or
-32,768 f16/bf16 elements): the two-pass streaming kernels, the two-phase form
-of the reference's online softmax (test/python/triton/test_online_softmax.py:
-28-78), for softmax, RMSNorm and LayerNorm, against the CPU oracle.  Ragged
+"""Rows longer than the four-wave register path holds (more than 16,384
+binary32 or 32,768 f16/bf16 elements): the eight-wave single-pass softmax
+(16-byte rows up to 16,384 vectors) and the two-pass streaming kernels, the
+two-phase form of the reference's online softmax (test/python/triton/
+test_online_softmax.py:28-78), for softmax, RMSNorm and LayerNorm, against
+float64 arithmetic and the CPU oracle.  Ragged
 lengths (element loads), 16-byte rows (vector loads), one row and many,
 masked (-inf) logits, strided views."""
 import numpy as np
@@ -14,8 +16,12 @@ import oracle
 
 pytestmark = pytest.mark.gpu
 
+# 16-byte rows up to 16384 vectors, 64 rows or more, take the 8-wave
+# single-pass softmax (the norms stream); fewer, ragged or longer rows take
+# the two passes
 LONG = [(2, 32769, "f16"), (3, 65536, "bf16"), (2, 16385, "f32"), (300, 40000, "f16"),
-        (1, 1_000_000, "f32"), (5, 131_088, "f16"), (7, 50_003, "bf16")]
+        (1, 1_000_000, "f32"), (5, 131_088, "f16"), (7, 50_003, "bf16"), (64, 131_072, "f16"),
+        (70, 65_536, "f32"), (64, 98_312, "bf16")]
 
 
 @pytest.mark.parametrize("rows,cols,dtype", LONG, ids=["-".join(map(str, c)) for c in LONG])
