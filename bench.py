@@ -467,7 +467,7 @@ def bench_rows_long(hx, iters: int = 20):
     gbs = 2 * R * C * 2 / (ev_ms * 1e-3) / 1e9
     return {"workload": f"softmax fp16 [{R} x {C}] (vocabulary-length rows)", "value": round(gbs, 1),
             "unit": "GB/s", "us_per_call": round(ev_ms * 1e3, 2),
-            "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s"),
+            "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s", traffic_of(f"softmax_f16_{R}x{C}")),
             "torch_us_same_tensors": round(t_ms * 1e3, 2), "queue_fed": fed}
 
 
@@ -648,6 +648,7 @@ def bench_f16_decode(hx, iters: int = 300):
                     "value": round(gbs, 1), "unit": "GB/s", "us_per_call": round(ev_ms * 1e3, 2),
                     "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s"),
                     "kernel": f"{plan[0]['plan']}:{plan[0]['config']}" if plan else None,
+                    "traffic": traffic_of(f"f16_decode_{M}x{N}x{K}:gemv_{plan[0]['config']}") if plan else None,
                     "torch_us_same_weights": round(t_ms * 1e3, 2), "weight_copies": copies, "queue_fed": fed})
         del wts, rws, ys, calls
         torch.cuda.empty_cache()
@@ -774,6 +775,21 @@ def pmc_workload(hx, keys_path=None) -> None:
     for _ in range(3):
         hx.swiglu_ffn(x, gam, 1e-6, Wg, Wu, Wd, out=y)
     Wg.release(); Wu.release(); Wd.release()
+    del x, y
+    # fp16 decode on a registered weight (its packed image), then softmax
+    # over vocabulary-length rows
+    wf = torch.empty((8192, 8192), dtype=torch.float16, device=dev).uniform_(-1, 1, generator=g)
+    rf = hx.ResidentWeight(wf, None, layout="nk")
+    xf = torch.randn((1, 8192), dtype=torch.float16, device=dev, generator=g)
+    for _ in range(3):
+        hx.matmul_resident(xf, rf)
+    rf.release()
+    del wf
+    xv = torch.randn((2048, 128256), dtype=torch.float16, device=dev, generator=g)
+    yv = torch.empty_like(xv)
+    for _ in range(3):
+        hx.softmax(xv, out=yv)
+    del xv, yv
     torch.cuda.synchronize()
     if keys_path:
         Path(keys_path).write_text(json.dumps(pmc_sequence(hx)))
@@ -801,6 +817,8 @@ def pmc_sequence(hx):
     dn = hx.config_get(4, hx.config_lookup(4, 2048, 4096, 11008))["name"]
     for _ in range(3):
         seq += [("ffn_rmsnorm_2048x4096", 1), (f"ffn_gate_up:{gu}", 1), (f"ffn_down:{dn}", 1)]
+    fd = hx.config_get(7, hx.config_lookup(7, 1, 8192, 8192))["name"]
+    seq += [(f"f16_decode_1x8192x8192:{fd}", 3), ("softmax_f16_2048x128256", 3)]
     return seq
 
 
