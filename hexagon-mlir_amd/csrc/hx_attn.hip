@@ -290,46 +290,40 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
     // a row with every key masked so far keeps m = -inf; exponentiate
     // against 0 then so that p = 0 instead of NaN
     const float mu = m_i == -INFINITY ? 0.f : m_i;
+    // O^T += V^T . P^T, one 16-key step at a time: step t covers keys
+    // 16t + 4*lg + (0..3) and 16t + 8 + 4*lg + (0..3) in this lane's k
+    // slots -- exactly the scores held in registers 4g..4g+3, g = 2t' and
+    // 2t'+1 (t' = t % 2) of tile t/2.  The step's exponentials are taken,
+    // packed and multiplied into every column tile before the next step's
+    // are taken, so they run under the previous step's MFMAs; each column
+    // tile still accumulates the steps in order, and the row sum adds the
+    // exponentials in the same order as one pass over the block would.
     float rs = 0.f;
-    static_for<JT>([&](auto jc) {
-      constexpr int jt = decltype(jc)::value;
-      static_for<16>([&](auto rc) {
+    static_for<PS>([&](auto tc) {
+      constexpr int t = decltype(tc)::value;
+      constexpr int jt = t >> 1, g0 = 2 * (t & 1);
+      v4i vf[DTILES];
+      static_for<DTILES>([&](auto dc) {
+        constexpr int dt = decltype(dc)::value;
+        const v2i lo = read_vt(cv, dt, t, 0);
+        const v2i hi = read_vt(cv, dt, t, 1);
+        vf[dt] = v4i{lo[0], lo[1], hi[0], hi[1]};
+      });
+      float e[8];
+      static_for<8>([&](auto rc) {
         constexpr int r = decltype(rc)::value;
-        const float e = exp2_fast(__builtin_fmaf(s[jt][r], qk_scale, -mu));
-        s[jt][r] = e;
-        rs += e;
+        e[r] = exp2_fast(__builtin_fmaf(s[jt][4 * g0 + r], qk_scale, -mu));
+        rs += e[r];
+      });
+      const v4i pf = v4i{(int)pack2<DT>(e[0], e[1]), (int)pack2<DT>(e[2], e[3]), (int)pack2<DT>(e[4], e[5]),
+                         (int)pack2<DT>(e[6], e[7])};
+      static_for<DTILES>([&](auto dc) {
+        constexpr int dt = decltype(dc)::value;
+        oacc[dt] = mfma_att<DT>(vf[dt], pf, oacc[dt]);
       });
     });
     rs += __shfl_xor(rs, 32);
     l_i += rs;
-
-    // O^T += V^T . P^T over the block's 16-key steps.  Step t covers keys
-    // 16t + 4*lg + (0..3) and 16t + 8 + 4*lg + (0..3) in this lane's k slots:
-    // exactly the exponentials held in score registers 4g..4g+3, g = 2t' and
-    // 2t'+1 (t' = t % 2) of tile t/2 -- and the matching V^T reads.
-    v4i pf[PS];
-    static_for<PS>([&](auto tc) {
-      constexpr int t = decltype(tc)::value;
-      constexpr int jt = t >> 1, g0 = 2 * (t & 1);
-      pf[t] = v4i{(int)pack2<DT>(s[jt][4 * g0 + 0], s[jt][4 * g0 + 1]),
-                  (int)pack2<DT>(s[jt][4 * g0 + 2], s[jt][4 * g0 + 3]),
-                  (int)pack2<DT>(s[jt][4 * g0 + 4], s[jt][4 * g0 + 5]),
-                  (int)pack2<DT>(s[jt][4 * g0 + 6], s[jt][4 * g0 + 7])};
-    });
-    static_for<DTILES>([&](auto dc) {
-      constexpr int dt = decltype(dc)::value;
-      v4i vf[PS];
-      static_for<PS>([&](auto tc) {
-        constexpr int t = decltype(tc)::value;
-        const v2i lo = read_vt(cv, dt, t, 0);
-        const v2i hi = read_vt(cv, dt, t, 1);
-        vf[t] = v4i{lo[0], lo[1], hi[0], hi[1]};
-      });
-      static_for<PS>([&](auto tc) {
-        constexpr int t = decltype(tc)::value;
-        oacc[dt] = mfma_att<DT>(vf[t], pf[t], oacc[dt]);
-      });
-    });
   };
 
   // Blocks in pairs over the two buffers; each block's loads were issued
