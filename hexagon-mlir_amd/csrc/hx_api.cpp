@@ -521,6 +521,14 @@ static int run_gemm(int op, GemmArgs& a, hipStream_t s, const PlanCtx& ctx,
   return map_internal(launch_gemm_generic(mode, a, s), "gemm_generic");
 }
 
+// One activation row against an [N][K] matrix read in place, whole rows per
+// wave (dt: the matrix's type).
+static int run_rowdot(GemvArgs& a, int dt, const void* w, int64_t ldw, hipStream_t s, const PlanCtx& ctx,
+                      const char* reason) {
+  note_plan(ctx, a.M, a.N, a.K, dt == HX_BF16 ? HX_BF16 : HX_F16, "gemv-rowdot", "rowdot", "fixed", reason);
+  return map_internal(launch_rowdot(dt, a, w, ldw, s), "rowdot");
+}
+
 // f16 / bf16 weights read in place from [N][K] by the streaming GEMV.
 // dt: the weight's type (the output has the activations' type: bf16 for
 // bf16 weights, else f16).
@@ -672,6 +680,9 @@ extern "C" int hx_matmul(const hx_memref2d* a, int a_dtype, const hx_memref2d* b
     GemvArgs v{};
     v.x = vb.p; v.ldx = K; v.w = nullptr; v.ldw = 0;
     v.scale = nullptr; v.y = vc.p; v.ldy = M; v.M = 1; v.N = M; v.K = K;
+    if (!rowdot_refusal(a_dtype, v, va.p, va.ld))
+      return run_rowdot(v, a_dtype, va.p, va.ld, s, PlanCtx{"hx_matmul", "swapped-a-streamed", a_dtype, b_dtype},
+                        "n-is-one");
     if (!gemv_hw_refusal(a_dtype, v, va.p, va.ld))
       return run_gemv_hw(v, a_dtype, va.p, va.ld, s, PlanCtx{"hx_matmul", "swapped-a-streamed", a_dtype, b_dtype},
                          "n-is-one");
@@ -728,6 +739,7 @@ extern "C" int hx_matmul(const hx_memref2d* a, int a_dtype, const hx_memref2d* b
     GemvArgs v{};
     v.x = va.p; v.ldx = va.ld; v.w = (const int8_t*)vb.p; v.ldw = vb.ld;
     v.scale = sc32; v.scale16 = sc16; v.y = vc.p; v.ldy = vc.ld; v.M = M; v.N = N; v.K = K;
+    if (M == 1 && !rowdot_refusal(b_dtype, v, vb.p, vb.ld)) return run_rowdot(v, b_dtype, vb.p, vb.ld, s, nctx, "one-row");
     if (!gemv_hw_refusal(b_dtype, v, vb.p, vb.ld)) return run_gemv_hw(v, b_dtype, vb.p, vb.ld, s, nctx);
     if (op == HX_OP_MATMUL_W8 && M <= 16 && gemv_fast_ok(v)) return run_gemv(v, s, nctx);
   }

@@ -727,6 +727,130 @@ int launch_gemv_hw(int cfg_idx, int wt, const GemvArgs& a, const void* w, int64_
 }
 
 // ---------------------------------------------------------------------------
+// One activation row against the rows of a K-contiguous matrix:
+//   y[n] = RNE( (sum_k W[n][k] * x[k]) * s[n] ),  binary32 accumulation,
+// for the decode of one row against an [N][K] weight read in place and for
+// hx_matmul with N = 1 (A's rows against b).  The MFMA GEMV's fragment
+// layout reads such a weight as sixteen 64-byte runs per wave load; here
+// each wave owns whole rows and reads them in contiguous KiBs (lane l holds
+// bytes 16l .. 16l + 15 of each), which streams like the packed image.  x is
+// staged once per workgroup in LDS (zero past K); products accumulate with
+// v_dot2 (two f16 / bf16 products and the running sum per instruction; int8
+// widened to f16 exactly first), then a butterfly adds the 64 lanes.
+// Wave w of workgroup b takes rows n = 4b + w + 4 G t (G workgroups); all of
+// a row's loads are in flight together, and the next row's are issued
+// before this row's products.
+// acc + sum of the eight products of two 16-byte vectors of f16 (bf16)
+// pairs, in element order.  The components are copied into scalars first:
+// hipcc compiled __builtin_bit_cast of a component expression (w.y) as a
+// cast of component 0.
+template <int WT>
+__device__ __forceinline__ float dot8(v4u w, v4u x, float acc) {
+  const uint32_t w0 = w[0], w1 = w[1], w2 = w[2], w3 = w[3];
+  const uint32_t x0 = x[0], x1 = x[1], x2 = x[2], x3 = x[3];
+  if constexpr (WT == DT_BF16) {
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, w0), __builtin_bit_cast(v2bf, x0), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, w1), __builtin_bit_cast(v2bf, x1), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, w2), __builtin_bit_cast(v2bf, x2), acc, false);
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, w3), __builtin_bit_cast(v2bf, x3), acc, false);
+  } else {
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(v2h, w0), __builtin_bit_cast(v2h, x0), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(v2h, w1), __builtin_bit_cast(v2h, x1), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(v2h, w2), __builtin_bit_cast(v2h, x2), acc, false);
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2h, w3), __builtin_bit_cast(v2h, x3), acc, false);
+  }
+}
+
+template <int WT>
+__global__ void __launch_bounds__(256) rowdot_kernel(GemvArgs p, const void* wsrc, int64_t ldw) {
+  constexpr int ES = WT == DT_I8 ? 1 : 2;   // weight element bytes
+  constexpr int EPL = 16 / ES;              // weight elements per lane load
+  constexpr int CK = 64 * EPL;              // k per wave load (chunk)
+  constexpr int U = WT == DT_I8 ? 8 : 16;   // chunks per row held at once
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kc = (int)((p.K + CK - 1) / CK);  // chunks per row (<= U)
+  // stage x (K halves, 16-byte groups; K % 8 == 0), zero up to U * CK: the
+  // chunk loop always runs U chunks (fully unrolled; chunks past the row
+  // load zeros through the buffer range and add exact zeros)
+  {
+    const uint16_t* x = reinterpret_cast<const uint16_t*>(p.x);
+    for (int64_t i = tid; i < (int64_t)U * CK / 8; i += 256) {
+      v4u v = v4u{0u, 0u, 0u, 0u};
+      if (8 * i < p.K) v = *reinterpret_cast<const v4u*>(x + 8 * i);
+      *reinterpret_cast<v4u*>(xs + 8 * i) = v;
+    }
+  }
+  __syncthreads();
+  const int64_t rstep = (int64_t)gridDim.x * 4;
+  const char* wb = reinterpret_cast<const char*>(wsrc);
+  auto issue = [&](int64_t n, v4u (&q)[U]) {
+    const bool nin = n < p.N;
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(wb + (nin ? n : 0) * ldw * ES), 0, nin ? (int)(p.K * ES) : 0, 0x00020000);
+#pragma unroll
+    for (int c = 0; c < U; ++c) {
+      const uint32_t off = (uint32_t)(c * CK + EPL * lane) * ES;
+      q[c] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(r, c < kc ? (int)off : (int)0x80000000, 0, 2));
+    }
+  };
+  v4u qa[U], qb[U];
+  int64_t n = (int64_t)blockIdx.x * 4 + wave;
+  issue(n, qa);
+  for (; n < p.N; n += rstep) {
+    issue(n + rstep, qb);
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < U; ++c) {
+      const uint16_t* xl = xs + c * CK + EPL * lane;
+      if constexpr (WT == DT_I8) {
+        const v4u x0 = *reinterpret_cast<const v4u*>(xl), x1 = *reinterpret_cast<const v4u*>(xl + 8);
+        const v4u q = qa[c];
+        const uint32_t q0 = q[0], q1 = q[1], q2 = q[2], q3 = q[3];
+        acc = dot8<DT_F16>(__builtin_bit_cast(v4u, i8x8_to_v8h(q0, q1)), x0, acc);
+        acc = dot8<DT_F16>(__builtin_bit_cast(v4u, i8x8_to_v8h(q2, q3)), x1, acc);
+      } else {
+        acc = dot8<WT>(qa[c], *reinterpret_cast<const v4u*>(xl), acc);
+      }
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) {
+      const float v = gv_scaled(p, n, acc);
+      reinterpret_cast<uint16_t*>(p.y)[n] = WT == DT_BF16 ? f32_to_bf16(v) : f32_to_f16_bits(v);
+    }
+#pragma unroll
+    for (int c = 0; c < U; ++c) qa[c] = qb[c];
+  }
+}
+
+const char* rowdot_refusal(int wt, const GemvArgs& a, const void* w, int64_t ldw) {
+  auto al16 = [](const void* q) { return ((uintptr_t)q & 15u) == 0; };
+  const int64_t es = wt == DT_I8 ? 1 : 2;
+  const int64_t ck = 64 * (16 / es);
+  if (a.M != 1 || a.N < 1 || a.K < 1) return "row-count";
+  if (a.K % (16 / es) != 0) return "k-granularity";
+  if ((a.K + ck - 1) / ck > (wt == DT_I8 ? 8 : 16)) return "k-extent";  // K <= 8192
+  if ((ldw * es) % 16 != 0) return "row-stride";
+  if (!al16(a.x) || !al16(w)) return "unaligned-base";
+  return nullptr;
+}
+
+int launch_rowdot(int wt, const GemvArgs& a, const void* w, int64_t ldw, hipStream_t s) {
+  if (rowdot_refusal(wt, a, w, ldw)) return HXI_ERR_SHAPE;
+  const size_t lds = 8192 * 2;  // U chunks of x: 8192 halves
+  // about two workgroups per CU, each wave then taking N / 2048 rows
+  const int64_t blocks = std::min<int64_t>((a.N + 3) / 4, 512);
+  switch (wt) {
+    case DT_F16: rowdot_kernel<DT_F16><<<dim3((unsigned)blocks), dim3(256), lds, s>>>(a, w, ldw); break;
+    case DT_BF16: rowdot_kernel<DT_BF16><<<dim3((unsigned)blocks), dim3(256), lds, s>>>(a, w, ldw); break;
+    case DT_I8: rowdot_kernel<DT_I8><<<dim3((unsigned)blocks), dim3(256), lds, s>>>(a, w, ldw); break;
+    default: return HXI_ERR_ARG;
+  }
+  return HXI_OK;
+}
+
+// ---------------------------------------------------------------------------
 // Weights in the linalg [K][N] orientation (N contiguous), read in place: no
 // transpose of the weight.  f16 / bf16 weights, or int8 (W8A16, f16
 // activations).

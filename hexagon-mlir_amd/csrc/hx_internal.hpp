@@ -149,6 +149,11 @@ int launch_gemv_packed(int cfg_idx, const GemvArgs& a, const int8_t* packed, hip
 int64_t gemv_packed16_bytes(int64_t N, int64_t K);
 int launch_gemv_pack16(const uint16_t* w_nk, int64_t ldw, int64_t N, int64_t K, uint16_t* out, hipStream_t s);
 int launch_gemv_packed16(int cfg_idx, int wt, const GemvArgs& a, const void* packed, hipStream_t s);
+// One activation row (M = 1) against a K-contiguous [N][K] matrix read in
+// place, whole rows per wave in contiguous KiBs; K <= 8192.  Null when the
+// shape is taken.
+const char* rowdot_refusal(int wt, const GemvArgs& a, const void* w, int64_t ldw);
+int launch_rowdot(int wt, const GemvArgs& a, const void* w, int64_t ldw, hipStream_t s);
 // Weights read in place from a K-contiguous [N][K] matrix with row stride
 // ldw (elements): f16 / bf16 (wt = DT_F16 / DT_BF16), or int8 (DT_I8, f16
 // activations); the same config table as the packed int8 kernel.  Null when

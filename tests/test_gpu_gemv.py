@@ -138,3 +138,28 @@ def test_gemv_kn_in_place(hx, dev, shape):
     assert [(r["plan"], r["weight"], r["b"]) for r in recs] == [("gemv-kn", "argument-kn", "i8")], recs
     want = oracle.matmul(x, w, scale_n=s.astype(np.float32))
     assert_close(to_np(y).astype(np.float32), want.astype(np.float32), 1e-2, 1e-3, f"kn in place {shape}")
+
+
+@pytest.mark.parametrize("shape,scale32", [((11008, 4096), False), ((37, 1040), True), ((100, 8192), False),
+                                           ((100, 520), False), ((64, 8208), True)],
+                         ids=["11008x4096", "37x1040-f32scale", "100x8192", "100x520", "64x8208"])
+def test_gemv_one_row_nk(hx, dev, shape, scale32):
+    """One activation row against an [N][K] int8 argument weight: whole rows
+    per wave (K % 16 == 0 and K <= 8192), else the streaming GEMV; f16 or f32
+    scale, ragged N, against the oracle."""
+    N, K = shape
+    x, w, s = case(1, N, K, seed=N + K)
+    wt = np.ascontiguousarray(w.T)
+    sc = s.astype(np.float32) if scale32 else s
+    hx.manifest_enable(True)
+    hx.manifest_clear()
+    try:
+        y = hx.gemv_w8a16(to_dev(x, dev), to_dev(wt, dev), to_dev(sc, dev), w_layout="nk")
+        plans = [r["plan"] for r in hx.manifest()["records"]]
+    finally:
+        hx.manifest_enable(False)
+    assert plans == ["gemv-rowdot" if (K % 16 == 0 and K <= 8192) else plans[0]], plans
+    if not (K % 16 == 0 and K <= 8192):
+        assert plans[0] != "gemv-rowdot", plans
+    want = oracle.matmul(x, wt, b_trans=True, scale_n=s.astype(np.float32))
+    assert_close(to_np(y).astype(np.float32), want.astype(np.float32), 1e-2, 1e-3, f"one row {shape}")

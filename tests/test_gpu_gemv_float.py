@@ -71,8 +71,12 @@ def test_decode_float_argument(hx, dev, dtype, layout, shape):
         plans = _plans(hx)
     finally:
         hx.manifest_enable(False)
-    # [K][N] weights stream in place when N % 8 == 0, else after the transpose
-    assert plans == ["gemv-kn" if layout == "kn" and N % 8 == 0 else "gemv-stream"], plans
+    # [K][N] weights stream in place when N % 8 == 0, else after the
+    # transpose; one row against an [N][K] weight (K <= 8192): whole rows
+    # per wave
+    want = ("gemv-kn" if layout == "kn" and N % 8 == 0 else
+            "gemv-rowdot" if layout == "nk" and M == 1 and K <= 8192 else "gemv-stream")
+    assert plans == [want], plans
     _check(to_np(c), a, b, dtype, f"decode {dtype} {layout} {shape}")
 
 
@@ -136,21 +140,32 @@ def test_decode_float_resident_every_config(hx, dev, dtype, shape):
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 def test_decode_float_tuner_shape(hx, dev, dtype):
-    """The reference tuner's decode shape (1, 8192, 8192): resident and
-    argument weights run the same kernel and agree bit for bit."""
+    """The reference tuner's decode shape (1, 8192, 8192): a registered
+    weight runs the decode GEMV on its packed image, an argument [N][K]
+    weight the row-dot kernel (whole rows per wave); both match the oracle
+    and repeat bit for bit."""
     M, N, K = 1, 8192, 8192
     a = _fp(dtype, (M, K), 60)
     b = _fp(dtype, (K, N), 61)
     bt = _dev(np.ascontiguousarray(b.T), dtype, dev)
     ad = _dev(a, dtype, dev)
     rw = hx.ResidentWeight(bt, None, layout="nk")
+    hx.manifest_enable(True)
+    hx.manifest_clear()
     try:
         res = to_np(hx.matmul_resident(ad, rw))
         arg = to_np(hx.matmul(ad, bt, b_layout="nk"))
+        plans = [r["plan"] for r in hx.manifest()["records"]]
+        res2 = to_np(hx.matmul_resident(ad, rw))
+        arg2 = to_np(hx.matmul(ad, bt, b_layout="nk"))
     finally:
+        hx.manifest_enable(False)
         rw.release()
-    assert np.array_equal(res.view(np.uint16), arg.view(np.uint16))
-    _check(res, a, b, dtype, f"tuner shape {dtype}")
+    assert plans == ["gemv-packed", "gemv-rowdot"], plans
+    assert np.array_equal(res.view(np.uint16), res2.view(np.uint16))
+    assert np.array_equal(arg.view(np.uint16), arg2.view(np.uint16))
+    _check(res, a, b, dtype, f"tuner shape resident {dtype}")
+    _check(arg, a, b, dtype, f"tuner shape argument {dtype}")
 
 
 def test_decode_float_falls_back_off_grid(hx, dev):
@@ -172,10 +187,11 @@ def test_decode_float_falls_back_off_grid(hx, dev):
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 @pytest.mark.parametrize("layout", ["kn", "nk"])
-@pytest.mark.parametrize("mk", [(8192, 4096), (300, 520), (17, 64)], ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("mk", [(8192, 4096), (300, 520), (17, 64), (40, 9000)], ids=lambda s: "x".join(map(str, s)))
 def test_matvec_n_is_one(hx, dev, dtype, layout, mk):
-    """N = 1 (the reference tuner's (M, K, 1) rows): A [M][K] is streamed as
-    the decode GEMV's weight with b as the single activation row."""
+    """N = 1 (the reference tuner's (M, K, 1) rows): A's rows are dotted
+    with b, whole rows per wave (K <= 8192), or A is streamed as the decode
+    GEMV's weight with b as the single activation row."""
     M, K = mk
     a = _fp(dtype, (M, K), 80)
     b = _fp(dtype, (K, 1), 81)
@@ -187,7 +203,8 @@ def test_matvec_n_is_one(hx, dev, dtype, layout, mk):
         recs = hx.manifest()["records"]
     finally:
         hx.manifest_enable(False)
-    assert [(r["plan"], r["weight"], r["reason"]) for r in recs] == [("gemv-stream", "swapped-a-streamed", "n-is-one")]
+    plan = "gemv-rowdot" if K <= 8192 else "gemv-stream"
+    assert [(r["plan"], r["weight"], r["reason"]) for r in recs] == [(plan, "swapped-a-streamed", "n-is-one")]
     _check(to_np(c), a, b, dtype, f"matvec {dtype} {layout} {mk}")
 
 
