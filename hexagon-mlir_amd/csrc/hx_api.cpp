@@ -1252,20 +1252,32 @@ extern "C" int hx_weight_info(hx_weight_t w, int64_t* k, int64_t* n, int* dtype,
   return HX_OK;
 }
 
+// Whether a registered int8 weight's product with these activations runs
+// the packed decode GEMV.  The packed GEMV reads activations as 8-element
+// (16-byte) groups, with 32-bit buffer offsets into the activation rows and
+// one workgroup's tiles.
+static bool packed_gemv_takes(const View2& vx, const hx_weight* w, bool residual, int y_dt) {
+  const int64_t M = vx.rows;
+  return w->dtype == HX_I8 && w->packed && gemv_rows_route(M, w->N, true, true) && !residual && y_dt == HX_F16 &&
+         w->K % 8 == 0 && ((uintptr_t)vx.p & 15u) == 0 && (vx.ld * 2) % 16 == 0 &&
+         M * vx.ld * 2 < ((int64_t)1 << 31) && (w->K + 63) / 64 * 4 * 1024 < ((int64_t)1 << 31);
+}
+
+// gate (int8 packed GEMV only, see packed_gemv_takes): the output becomes
+// RNE(silu(gate) * RNE(x . W * s)), the SwiGLU gate fused into the epilogue.
 static int matmul_resident_impl(const View2& vx, hx_weight* w, const View2* vr, int r_dt,
                                 const View2& vy, int y_dt, hipStream_t s, const char* entry,
-                                const PartialsTarget& pt = PartialsTarget{}) {
+                                const PartialsTarget& pt = PartialsTarget{}, const View2* gate = nullptr) {
   const int x_dt = w->dtype == HX_BF16 ? HX_BF16 : HX_F16;
   const int64_t M = vx.rows;
   if (M == 0) return HX_OK;
-  // The packed GEMV reads activations as 8-element (16-byte) groups, with
-  // 32-bit buffer offsets into the activation rows and one workgroup's tiles.
-  if (w->dtype == HX_I8 && w->packed && gemv_rows_route(M, w->N, true, true) && !vr && y_dt == HX_F16 && w->K % 8 == 0 &&
-      ((uintptr_t)vx.p & 15u) == 0 && (vx.ld * 2) % 16 == 0 && M * vx.ld * 2 < ((int64_t)1 << 31) &&
-      (w->K + 63) / 64 * 4 * 1024 < ((int64_t)1 << 31)) {
+  if (gate && !packed_gemv_takes(vx, w, vr != nullptr, y_dt))
+    return fail(HX_ERR_ARG, "%s: fused gate needs the packed decode GEMV", entry);
+  if (packed_gemv_takes(vx, w, vr != nullptr, y_dt)) {
     GemvArgs v{};
     v.x = vx.p; v.ldx = vx.ld; v.w = nullptr; v.ldw = 0;
     v.scale = w->scale; v.y = vy.p; v.ldy = vy.ld; v.M = M; v.N = w->N; v.K = w->K;
+    if (gate) { v.gate = (const uint16_t*)gate->p; v.ldg = gate->ld; }
     bool pin = false;
     const int cfg = resolve_gemv(HX_OP_GEMV_W8, M, w->N, w->K, &pin);
     note_plan(PlanCtx{entry, "resident-packed", x_dt, w->dtype}, M, w->N, w->K, HX_F16, "gemv-packed",
@@ -1369,8 +1381,13 @@ int hx::swiglu_ffn_impl(const hx_memref2d* x, const hx_memref1d* gamma, float ep
   Carver cv;
   const size_t off_h = cv.take((size_t)T * H * 2);
   const size_t off_a = cv.take((size_t)T * I * 2);
+  // decode path: the up projection's epilogue applies the gate (silu(g)
+  // u, as the silu_mul kernel would) when it runs the packed GEMV, so u
+  // never leaves the kernel (the workspace's activations are 256-byte
+  // aligned with rows of H halves)
+  const bool fuse_gate = skinny && packed_gemv_takes(View2{nullptr, T, H, H}, wu, false, HX_F16);
   const size_t off_g = skinny ? cv.take((size_t)T * I * 2) : 0;
-  const size_t off_u = skinny ? cv.take((size_t)T * I * 2) : 0;
+  const size_t off_u = skinny && !fuse_gate ? cv.take((size_t)T * I * 2) : 0;
   char* ws;
   PartialsTarget pt;
   if (fixed) {
@@ -1404,11 +1421,16 @@ int hx::swiglu_ffn_impl(const hx_memref2d* x, const hx_memref1d* gamma, float ep
   if (rc) return rc;
   View2 vh{h, T, H, H}, va{act, T, I, I};
   if (skinny) {
-    View2 vgo{ws + off_g, T, I, I}, vuo{ws + off_u, T, I, I};
+    View2 vgo{ws + off_g, T, I, I};
     if ((rc = matmul_resident_impl(vh, wg, nullptr, 0, vgo, HX_F16, s, entry, pt))) return rc;
-    if ((rc = matmul_resident_impl(vh, wu, nullptr, 0, vuo, HX_F16, s, entry, pt))) return rc;
-    rc = map_internal(launch_silu_mul_f16(vgo.p, I, vuo.p, I, act, I, T, I, s), "silu_mul");
-    if (rc) return rc;
+    if (fuse_gate) {
+      if ((rc = matmul_resident_impl(vh, wu, nullptr, 0, va, HX_F16, s, entry, pt, &vgo))) return rc;
+    } else {
+      View2 vuo{ws + off_u, T, I, I};
+      if ((rc = matmul_resident_impl(vh, wu, nullptr, 0, vuo, HX_F16, s, entry, pt))) return rc;
+      rc = map_internal(launch_silu_mul_f16(vgo.p, I, vuo.p, I, act, I, T, I, s), "silu_mul");
+      if (rc) return rc;
+    }
   } else {
     GemmArgs g{};
     g.a = h; g.lda = H;

@@ -113,6 +113,15 @@ __device__ __forceinline__ float fast_exp(float x) {
   return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
 }
 
+// The SwiGLU gate on fp16 values: RNE(silu(g) * u), silu(g) = g / (1 +
+// exp(-g)) in binary32 (correctly rounded divide); shared by the silu_mul
+// kernel and the decode GEMV's fused epilogue so both give the same bits.
+__device__ __forceinline__ uint16_t silu_mul_h(uint16_t g, uint16_t u) {
+  const float x = f16_bits_to_f32(g);
+  const float sx = x / (1.0f + fast_exp(-x));
+  return f32_to_f16_bits(sx * f16_bits_to_f32(u));
+}
+
 // ---------------------------------------------------------------------------
 // int8 -> fp16 conversion of four packed signed bytes into two half2 words.
 // (b ^ 0x80) is the byte as an unsigned excess-128 value u in [1, 255]; the

@@ -238,6 +238,34 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
     }
   }
   const bool has_scale = p.scale != nullptr || p.scale16 != nullptr;
+  // The SwiGLU gate values of this thread's outputs (p.gate: the fused
+  // epilogue), loaded up front for the same reason as the scales; the
+  // (row, column) of each is the one the reduction below finalises.
+  uint16_t gv[MB][NSC];
+  if (p.gate) {
+    const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)p.gate, 0, (int)(p.M * p.ldg * 2), 0x00020000);
+#pragma unroll
+    for (int b = 0; b < MB; ++b)
+#pragma unroll
+      for (int i = 0; i < NSC; ++i) {
+        const int e = tid + NT * i;
+        int64_t m, n;
+        bool in;
+        if (few_rows) {
+          m = tid & 3;
+          n = (int64_t)(t0 + (tid >> 6)) * 16 + ((tid >> 2) & 15);
+          in = i == 0 && tid < 64 * CT;
+        } else {
+          const int l = (e >> 2) & 63;
+          m = 16 * b + 4 * (l >> 4) + (e & 3);
+          n = (int64_t)(t0 + (e >> 8)) * 16 + (l & 15);
+          in = e < CT * 256;
+        }
+        in = in && m < p.M && n < p.N;
+        gv[b][i] = __builtin_amdgcn_raw_buffer_load_b16(rg, in ? (int)((m * p.ldg + n) * 2) : (int)0x80000000, 0, 0);
+      }
+  }
 
   // Every global load below is a buffer load whose out-of-range offset
   // (0x80000000) reads zero, so no load sits behind a branch: a conditional
@@ -488,7 +516,8 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
       const int64_t n = (int64_t)(t0 + c) * 16 + l;
       if (r < p.M && n < p.N) {
         const float v = has_scale ? s * sc[0] : s;
-        y[(int64_t)r * p.ldy + n] = WT == DT_BF16 ? f32_to_bf16(v) : f32_to_f16_bits(v);
+        const uint16_t h = WT == DT_BF16 ? f32_to_bf16(v) : f32_to_f16_bits(v);
+        y[(int64_t)r * p.ldy + n] = p.gate ? silu_mul_h(gv[0][0], h) : h;
       }
     }
     return;
@@ -514,7 +543,8 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
       if (m < p.M && n < p.N) {
         // s * scale[n] in binary32 (an f16 scale widened exactly)
         const float v = has_scale ? s * sc[i] : s;
-        y[(int64_t)m * p.ldy + n] = WT == DT_BF16 ? f32_to_bf16(v) : f32_to_f16_bits(v);
+        const uint16_t h = WT == DT_BF16 ? f32_to_bf16(v) : f32_to_f16_bits(v);
+        y[(int64_t)m * p.ldy + n] = p.gate ? silu_mul_h(gv[b][i], h) : h;
       }
     }
   }

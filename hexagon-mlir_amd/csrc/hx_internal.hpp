@@ -101,6 +101,9 @@ struct GemvArgs {
   const uint16_t* scale16;      // [N] f16 scale, used when `scale` is null
   void* y; int64_t ldy;         // [M][N], the activations' type
   int64_t M, N, K;
+  // optional SwiGLU gate [M][N] f16 (streaming kernel, f16 output): each
+  // output becomes RNE(silu(gate) * RNE(result))
+  const uint16_t* gate = nullptr; int64_t ldg = 0;
 };
 struct GemvConfig {
   int ct, kw;        // 16-column tiles per workgroup, waves splitting K

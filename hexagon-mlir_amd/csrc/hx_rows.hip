@@ -751,11 +751,7 @@ __global__ void __launch_bounds__(256) silu_mul_f16_kernel(
     const uint16_t* ue = reinterpret_cast<const uint16_t*>(&uv);
     uint16_t out[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float x = f16_bits_to_f32(ge[j]);
-      const float sx = x / (1.0f + fast_exp(-x));
-      out[j] = f32_to_f16_bits(sx * f16_bits_to_f32(ue[j]));
-    }
+    for (int j = 0; j < 8; ++j) out[j] = silu_mul_h(ge[j], ue[j]);
     *reinterpret_cast<v4u*>(o + r * ldo + c) = *reinterpret_cast<const v4u*>(out);
   }
 }
@@ -767,9 +763,7 @@ __global__ void __launch_bounds__(256) silu_mul_f16_scalar_kernel(
   for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
        t += (int64_t)gridDim.x * blockDim.x) {
     const int64_t r = t / cols, c = t - r * cols;
-    const float x = f16_bits_to_f32(g[r * ldg + c]);
-    const float sx = x / (1.0f + fast_exp(-x));
-    o[r * ldo + c] = f32_to_f16_bits(sx * f16_bits_to_f32(u[r * ldu + c]));
+    o[r * ldo + c] = silu_mul_h(g[r * ldg + c], u[r * ldu + c]);
   }
 }
 

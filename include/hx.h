@@ -253,7 +253,7 @@ int hx_swiglu_ffn(const hx_memref2d* x, const hx_memref1d* gamma, float eps,
  * K-split partials live in a fixed device array of HX_NOALLOC_SCRATCH_BYTES
  * that each GPU the library runs on holds until the process ends, instead
  * of the stream workspace.  The call makes no hipMalloc or hipFree.  It
- * needs T*(H + I)*2 bytes for T > 32 tokens (T*(H + 3 I)*2 for T <= 32, the
+ * needs T*(H + I)*2 bytes for T > 32 tokens (at most T*(H + 3 I)*2 for T <= 32, the
  * decode path), plus T*H*4 per K part when the down projection's
  * configuration splits K (256-byte aligned each); a shape that needs more
  * than the array returns HX_ERR_UNSUPPORTED before anything is enqueued.

@@ -135,3 +135,30 @@ def test_swiglu_ffn_c5_full_size(hx, dev):
     assert_close(got, want.astype(np.float32), 2e-2, 2e-3, "swiglu C5 sampled rows")
     rel = np.linalg.norm(got - want) / np.linalg.norm(want.astype(np.float32))
     assert rel < 2e-3, rel
+
+
+@pytest.mark.parametrize("T", [1, 4, 16, 24, 32])
+def test_swiglu_decode_equals_composition(hx, dev, T):
+    """Decode-sized blocks fuse the gate into the up projection's epilogue
+    (RNE(silu(g) * u) on the rounded outputs): the block equals, bit for
+    bit, the composition of the public entry points -- RMSNorm, the gate and
+    up products, silu_mul, the down product."""
+    import torch
+    H, I = 512, 2048
+    wg, sg, wu, su, wd, sd = weights(H, I, 700 + T)
+    Wg = hx.ResidentWeight(to_dev(wg, dev), to_dev(sg, dev), layout="kn")
+    Wu = hx.ResidentWeight(to_dev(wu, dev), to_dev(su, dev), layout="kn")
+    Wd = hx.ResidentWeight(to_dev(wd, dev), to_dev(sd, dev), layout="kn")
+    try:
+        x = to_dev(rng(710 + T).normal(0, 1, (T, H)).astype(np.float16), dev)
+        gamma = to_dev(rng(711).normal(1, 0.1, H).astype(np.float16), dev)
+        y = hx.swiglu_ffn(x, gamma, 1e-6, Wg, Wu, Wd)
+        h = hx.rms_norm(x, gamma, eps=1e-6)
+        a = hx.silu_mul(hx.matmul_resident(h, Wg), hx.matmul_resident(h, Wu))
+        want = hx.matmul_resident(a, Wd)
+        torch.cuda.synchronize()
+        got, ref = to_np(y), to_np(want)
+        assert np.isfinite(ref.astype(np.float32)).all()
+        assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+    finally:
+        Wg.release(); Wu.release(); Wd.release()
