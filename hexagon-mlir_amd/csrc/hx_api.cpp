@@ -12,6 +12,7 @@
 // Passes.td:381-389 documents the reference's never-revalidated contents).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cmath>
@@ -142,6 +143,38 @@ static int part_get(hipStream_t s, size_t bytes, float** out) {
   }
   *out = reinterpret_cast<float*>(w.buf);
   return HX_OK;
+}
+
+// The K-split decode GEMV's buffers: its binary32 partials share the
+// K-split GEMM's region (one kernel uses it at a time on a stream), and its
+// per-group counters are a fixed region cleared once, when allocated (on
+// `s`, ahead of every kernel that uses it; each kernel returns the counters
+// it used to zero).  The first split GEMV on a stream therefore runs
+// outside graph capture, like the first use of the workspace.
+static std::map<std::pair<int, hipStream_t>, Workspace> g_cnt;
+int hx::gemv_split_buffers(hipStream_t s, size_t part_bytes, float** part, unsigned** cnt) {
+  if (part_get(s, part_bytes, part)) return HXI_ERR_NOMEM;
+  int dev;
+  if (current_device(&dev)) return HXI_ERR_NOMEM;
+  std::lock_guard<std::mutex> lk(g_mu);
+  Workspace& w = g_cnt[{dev, s}];
+  if (!w.buf) {
+    const size_t nb = (size_t)kGemvSplitCounters * sizeof(unsigned);
+    if (hipMalloc(&w.buf, nb) != hipSuccess) {
+      w.buf = nullptr;
+      fail(HX_ERR_NOMEM, "split GEMV counters of %zu bytes", nb);
+      return HXI_ERR_NOMEM;
+    }
+    if (hipMemsetAsync(w.buf, 0, nb, s) != hipSuccess) {
+      (void)hipFree(w.buf);
+      w.buf = nullptr;
+      fail(HX_ERR_HIP, "clearing the split GEMV counters");
+      return HXI_ERR_NOMEM;
+    }
+    w.bytes = nb;
+  }
+  *cnt = reinterpret_cast<unsigned*>(w.buf);
+  return HXI_OK;
 }
 
 // f32 operands quantised to f16 (hx_matmul): a third per-stream region, so
@@ -373,14 +406,14 @@ static int resolve_gemm(int op, int64_t M, int64_t N, int64_t K, bool* was_pinne
 // weights); otherwise a registered weight's packed image.
 static int gemv_untuned_table(int op, int64_t M, int64_t N, int64_t K, bool in_place);
 // The untuned config as it runs: a config that stages the activations in
-// LDS is named by its base config where the rows do not fit (the launcher
-// runs the base), so the tuner's control and the plan record match the
-// kernel that runs.
+// LDS, or splits K over workgroups, is named by its base config where the
+// rows do not fit it (the launcher runs the base), so the tuner's control
+// and the plan record match the kernel that runs.
 static int gemv_untuned(int op, int64_t M, int64_t N, int64_t K, bool in_place = false) {
   const int t = gemv_untuned_table(op, M, N, K, in_place);
   const GemvConfig* c = gemv_packed_config(t);
   const int wt = op == HX_OP_GEMV_W8 ? HX_I8 : op == HX_OP_GEMV_BF16 ? HX_BF16 : HX_F16;
-  return c && !gemv_xl_fits(*c, M, K, wt) ? c->base : t;
+  return c && (!gemv_xl_fits(*c, M, K, wt) || (c->split > 1 && !gemv_split_takes(*c, M, N))) ? c->base : t;
 }
 static int gemv_untuned_table(int op, int64_t M, int64_t N, int64_t K, bool in_place) {
   if (M > 16) return gemv_rows_default(M, N);
@@ -405,13 +438,20 @@ static int gemv_untuned_table(int op, int64_t M, int64_t N, int64_t K, bool in_p
     // (16 x 4096 x 16384: 30.6 against 39.5 for two)
     if (M <= 2) return 7;
     if (M <= 4) return 5;
+    // more than 8 rows with K >= 8192 on at most 128 tiles (one tile per
+    // workgroup would leave half the CUs idle), or with K >= 10240 on at
+    // most 256: two tiles per workgroup with K split over two workgroups
+    // (M = 9 / 12 / 16: 2048 x 8192 12.1 / 12.7 / 13.5 against 12.5 / 13.9 /
+    // 15.3 us; 4096 x 11008 17.9 / 18.4 / 19.3 against 18.4 / 20.0 / 22.1;
+    // at 4096 x 8192 the split lost, 16.8 against 14.8 at M = 9)
+    if (M > 8 && K >= 8192 && (tiles <= 128 || (tiles <= 256 && K >= 10240))) return 25;
     return three_tiles ? 20 : tiles >= 512 ? 0 : 1;
   }
   // untuned choice from the MI355X sweep (int8, K = 4096, tuner medians).
   // When the 16-column tiles need three per workgroup to fit one workgroup
-  // per CU (N = 11008: 688 tiles, 230 workgroups), the three-tile configs:
-  // 16 waves for M <= 4, 8 for larger M (9.24 / 9.35 / 10.08 us at M = 1 /
-  // 4 / 16 against 9.43 / 10.14 / 11.07 for the configs below).  Otherwise,
+  // per CU (N = 11008: 688 tiles, 230 workgroups), three tiles over 16 waves
+  // (M = 1 / 4 / 5 / 8 / 12 / 16: 9.23 / 9.30 / 9.28 / 9.36 / 9.69 / 10.24 us;
+  // over 8 waves 9.50 / 9.53 / 9.61 / 9.84 / 10.19 / 10.67).  Otherwise,
   // for M <= 4: up to 256 tiles one tile per workgroup over 16 waves (M = 1
   // / 4, N = K = 4096: 5.11 / 5.23 against 5.31 / 5.59 with LDS-staged
   // activations over 8), beyond two tiles over 8 waves (M = 4, N = 8192 /
@@ -420,8 +460,14 @@ static int gemv_untuned_table(int op, int64_t M, int64_t N, int64_t K, bool in_p
   // workgroups within one per CU, three beyond 1024 tiles (M = 16, N = 2048
   // / 4096 / 8192 / 16384 / 22016: 6.83 / 7.08 / 8.85 / 13.64 / 18.97 us;
   // four tiles everywhere took 9.63 / 9.86 / 10.5 / 13.64 / 22.25).
-  if (three_tiles) return M <= 4 ? 20 : 19;
+  if (three_tiles) return 20;
   if (M <= 4) return tiles > 256 ? 0 : 24;
+  // 12 rows or more on at most 256 tiles with K >= 8192: four tiles per
+  // workgroup with K split over four workgroups, one workgroup per CU
+  // (M = 12 / 16: 4096 x 11008 13.2 / 13.6 against 14.0 / 16.0 us; 2048 x
+  // 8192 8.8 / 9.1 against 10.2 / 11.8; 4096 x 8192 10.3 / 10.5 against
+  // 10.7 / 12.3; at M = 9 the split lost on N = 4096, 13.0 against 12.3)
+  if (M >= 12 && tiles <= 256 && K >= 8192) return 26;
   return tiles <= 256 ? 1 : tiles <= 512 ? 0 : tiles <= 768 ? 19 : tiles <= 1024 ? 10 : 19;
 }
 
@@ -475,6 +521,7 @@ struct PartialsTarget {
   float* buf = nullptr;
   size_t cap = 0;
   bool fixed = false;
+  unsigned* cnt = nullptr;  // the split decode GEMV's counters (fixed scratch)
 };
 
 // Partial bytes a run_gemm call of these args would need (0: no K split or
@@ -562,7 +609,7 @@ extern "C" int hx_init(void) {
     return fail(HX_ERR_UNSUPPORTED, "device %d is %s; libhxmi is built for gfx950 only", dev,
                 prop.gcnArchName);
   // the no-allocation entry point's scratch address on this device
-  return noalloc_setup(nullptr);
+  return noalloc_setup(nullptr, nullptr, nullptr);
 }
 
 extern "C" const char* hx_last_error(void) { return g_err.c_str(); }
@@ -1280,6 +1327,15 @@ static int matmul_resident_impl(const View2& vx, hx_weight* w, const View2* vr, 
     if (gate) { v.gate = (const uint16_t*)gate->p; v.ldg = gate->ld; }
     bool pin = false;
     const int cfg = resolve_gemv(HX_OP_GEMV_W8, M, w->N, w->K, &pin);
+    if (pt.fixed) {
+      // a K-split config's partials and counters come from the caller's
+      // fixed scratch (the launcher would otherwise take the stream's own)
+      const size_t need = gemv_split_bytes(cfg, M, w->N);
+      if (need > pt.cap || (need && (!pt.buf || !pt.cnt)))
+        return fail(HX_ERR_UNSUPPORTED, "%s: the decode GEMV's K split needs %zu bytes of scratch, %zu reserved",
+                    entry, need, pt.cap);
+      v.part = pt.buf; v.cnt = pt.cnt;
+    }
     note_plan(PlanCtx{entry, "resident-packed", x_dt, w->dtype}, M, w->N, w->K, HX_F16, "gemv-packed",
               gemv_packed_config(cfg)->name, pin ? "pinned" : "default", M <= 16 ? "min-rows" : "few-rows");
     return map_internal(launch_gemv_packed(cfg, v, (const int8_t*)w->packed, s), "gemv_packed");
@@ -1404,6 +1460,11 @@ int hx::swiglu_ffn_impl(const hx_memref2d* x, const hx_memref1d* gamma, float ep
       d.out_dtype = HX_F16;
       d.col_scale = wd->scale;
       part = gemm_partials_needed(HX_OP_MATMUL_W8, d);
+    } else {
+      // the decode GEMVs' K-split partials (one region, the largest need of
+      // the three products, which run one after another)
+      part = std::max(gemv_split_bytes(resolve_gemv(HX_OP_GEMV_W8, T, I, H), T, I),
+                      gemv_split_bytes(resolve_gemv(HX_OP_GEMV_W8, T, H, I), T, H));
     }
     const size_t off_p = part ? cv.take(part) : 0;
     if (cv.used > fixed->cap)
@@ -1412,6 +1473,7 @@ int hx::swiglu_ffn_impl(const hx_memref2d* x, const hx_memref1d* gamma, float ep
     pt.fixed = true;
     pt.buf = part ? reinterpret_cast<float*>(ws + off_p) : nullptr;
     pt.cap = part;
+    pt.cnt = fixed->cnt;
   } else if ((rc = ws_get(s, cv.used, &ws))) {
     return rc;
   }
@@ -1473,7 +1535,7 @@ extern "C" int hx_config_get(int op, int index, hx_kernel_config* out) {
     // that stage the activation rows in LDS, the 64 KiB staging limit
     out->bm = 16 * c->mb; out->bn = 16 * c->ct; out->bk = op == HX_OP_GEMV_W8 ? 64 : 32;
     out->waves_m = c->kw; out->waves_n = 1;
-    out->lds_stages = 0; out->split_k = c->kw; out->col_tiles = c->ct;
+    out->lds_stages = 0; out->split_k = c->split; out->col_tiles = c->ct;
     out->lds_bytes = c->kw * c->ct * 64 * 4 * 4 + (c->xl ? 65536 : 0);
     snprintf(out->name, sizeof(out->name), "gemv_%s", c->name);
     return HX_OK;

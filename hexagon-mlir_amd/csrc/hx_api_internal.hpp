@@ -38,11 +38,12 @@ std::vector<std::pair<int, double>> canary_references(int dev);
 struct FixedScratch {
   char* base;
   size_t cap;
+  unsigned* cnt;  // kGemvSplitCounters counters of the split decode GEMV, zero between calls
 };
 
 // The current device's fixed scratch (hx_noalloc.cpp), resolved once per
 // device; *out (may be null) receives its address.
-int noalloc_setup(char** out);
+int noalloc_setup(char** out, unsigned** cnt, hipStream_t s);
 
 // The SwiGLU FFN block (hx_swiglu_ffn); with `fixed` every intermediate and
 // K-split partial lives in that memory and the call allocates nothing.

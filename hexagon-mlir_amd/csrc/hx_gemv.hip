@@ -197,7 +197,13 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, g = lane >> 4;
-  const int t0 = blockIdx.x * CT;                    // first column tile
+  // K split (non-staged, non-pipelined configs): workgroup b is part
+  // b % parts of column-tile group b / parts and reduces chunks [kc0, kc1)
+  const int parts = p.parts;
+  const int part = (int)(blockIdx.x % (unsigned)parts), grp = (int)(blockIdx.x / (unsigned)parts);
+  const int cpp = (kchunks + parts - 1) / parts;
+  const int kc0 = part * cpp, kc1 = min(kchunks, kc0 + cpp);
+  const int t0 = grp * CT;                           // first column tile
   const int ntiles = (int)((p.N + 15) / 16);
   const int tiles_here = min(CT, ntiles - t0);
   const int rows_here = (int)min((int64_t)16 * CT, p.N - (int64_t)16 * t0);
@@ -411,13 +417,13 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
     // Written out here rather than through issue/compute: the compiler then
     // schedules the slice's loads among its MFMAs with fewer live registers,
     // which measured up to 2x faster for the wide (CT >= 2, CPW = 8) configs.
-    for (int c0 = 0; c0 < kchunks; c0 += STEP) {
+    for (int c0 = kc0; c0 < kc1; c0 += STEP) {
       v4u wq[CPW][CT];
       v4u xq[XL ? 1 : CPW][NE][MB];
 #pragma unroll
       for (int u = 0; u < CPW; ++u) {
         const int j = c0 + wave + KW * u;
-        const bool jv = j < kchunks;
+        const bool jv = j < kc1;
 #pragma unroll
         for (int c = 0; c < CT; ++c) {
           uint32_t off;
@@ -522,6 +528,12 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
     }
     return;
   }
+  // s * scale[n] in binary32 (an f16 scale widened exactly), rounded, gated
+  auto finish = [&](int b, int i, int m, int64_t n, float s) {
+    const float v = has_scale ? s * sc[i] : s;
+    const uint16_t h = WT == DT_BF16 ? f32_to_bf16(v) : f32_to_f16_bits(v);
+    y[(int64_t)m * p.ldy + n] = p.gate ? silu_mul_h(gv[b][i], h) : h;
+  };
 #pragma unroll
   for (int b = 0; b < MB; ++b) {
     if (b > 0) __syncthreads();  // the previous block's sums are read
@@ -541,13 +553,53 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
       const int m = 16 * b + 4 * (l >> 4) + r;
       const int64_t n = (int64_t)(t0 + c) * 16 + (l & 15);
       if (m < p.M && n < p.N) {
-        // s * scale[n] in binary32 (an f16 scale widened exactly)
-        const float v = has_scale ? s * sc[i] : s;
-        const uint16_t h = WT == DT_BF16 ? f32_to_bf16(v) : f32_to_f16_bits(v);
-        y[(int64_t)m * p.ldy + n] = p.gate ? silu_mul_h(gv[b][i], h) : h;
+        if (parts > 1)
+          __hip_atomic_store(p.part + ((int64_t)part * p.M + m) * p.N + n, s, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        else
+          finish(b, i, m, n, s);
       }
     }
   }
+  if (parts == 1) return;
+  // K split.  The partials, the counters and the reads of the partials are
+  // device-scope atomic accesses, which the hardware keeps coherent across
+  // the XCDs' L2s (written through, read past them); a device-scope fence
+  // would instead write back and invalidate the whole L2 of the XCD, per
+  // workgroup, which measured 10-30x slower.  Each wave waits for its
+  // partial stores to complete before the barrier, so the part is counted
+  // in only once every partial of the workgroup is visible; the workgroup
+  // that counts last (its count returned before any of its partial loads
+  // issue) finishes the outputs, adding the parts in part order whichever
+  // finished last (the result does not depend on scheduling).  No
+  // workgroup waits for another.
+  __shared__ int is_last;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0)
+    is_last = __hip_atomic_fetch_add(p.cnt + grp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+              (unsigned)(parts - 1);
+  __syncthreads();
+  if (!is_last) return;
+#pragma unroll
+  for (int b = 0; b < MB; ++b)
+#pragma unroll
+    for (int i = 0; i < NSC; ++i) {
+      const int e = tid + NT * i;
+      if (e >= CT * 256) break;
+      const int c = e >> 8, l = (e >> 2) & 63, r = e & 3;
+      const int m = 16 * b + 4 * (l >> 4) + r;
+      const int64_t n = (int64_t)(t0 + c) * 16 + (l & 15);
+      if (m < p.M && n < p.N) {
+        float* q = p.part + (int64_t)m * p.N + n;
+        const int64_t stride = p.M * p.N;
+        float s = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int k = 1; k < parts; ++k)
+          s += __hip_atomic_load(q + k * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        finish(b, i, m, n, s);
+      }
+    }
+  if (tid == 0) __hip_atomic_store(p.cnt + grp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Build the fragment-packed image from a K-contiguous [N][K] int8 weight:
@@ -623,7 +675,7 @@ template <int CT, int KW, int CPW, int XS, bool PIPE, int WT, int MB = 1, bool P
 static void gemv_stream_one(const GemvArgs& a, const void* w, int64_t ldw, int kchunks, hipStream_t s) {
   constexpr int KD = WT == DT_I8 ? 64 : 32;
   const int64_t ntiles = (a.N + 15) / 16;
-  const int64_t blocks = (ntiles + CT - 1) / CT;
+  const int64_t blocks = (ntiles + CT - 1) / CT * a.parts;
   const size_t lds = XS != XS_NONE ? (size_t)a.M * (((int64_t)kchunks * KD + 511) / 512 * 512 + 8) * 2 : 0;
   gemv_stream_kernel<CT, KW, CPW, XS, WT, PK, PIPE, MB>
       <<<dim3((unsigned)blocks), dim3(64 * KW), lds, s>>>(a, w, ldw, kchunks);
@@ -686,6 +738,14 @@ static const GemvStreamEntry kGemvStream[] = {
     // one tile per CU (the FFN's down projection, N = 4096, K = 11008)
     {{1, 16, "rows2_ct1_kw16", 0, 23, 2}, HX_GR(1, 16, 4, 2)},
     {{1, 16, "packed_ct1_kw16", 0, 24, 1}, HX_GV(1, 16, 4, XS_NONE, false)},
+    // K split over two or four workgroups per tile group (M > 4): each
+    // workgroup reads 1/parts of the activation rows for `ct` tiles, so the
+    // activation fragments it loads per weight byte drop by the tile count
+    // while the workgroup count stays at one per CU (N = 4096: 128 x 2 and
+    // 64 x 4; N = 11008: 115 x 2)
+    {{2, 16, "packed_ct2_kw16_s2", 0, 0, 1, 2}, HX_GV(2, 16, 4, XS_NONE, false)},
+    {{4, 16, "packed_ct4_kw16_s4", 0, 8, 1, 4}, HX_GV(4, 16, 2, XS_NONE, false)},
+    {{6, 16, "packed_ct6_kw16_s2", 0, 20, 1, 2}, HX_GV(6, 16, 2, XS_NONE, false)},
 };
 #undef HX_GR
 #undef HX_GV
@@ -712,8 +772,32 @@ static int launch_gemv_stream(int cfg_idx, int wt, bool packed, const GemvArgs& 
   if (wg_bytes >= ((int64_t)1 << 31) || a.M * a.ldx * 2 >= ((int64_t)1 << 31)) return HXI_ERR_SHAPE;
   if (kGemvStream[cfg_idx].cfg.xl && !gemv_xl_fits(kGemvStream[cfg_idx].cfg, a.M, a.K, wt))
     cfg_idx = kGemvStream[cfg_idx].cfg.base;
-  kGemvStream[cfg_idx].fn[slot](a, w, ldw, (int)kchunks, s);
+  const GemvConfig& c = kGemvStream[cfg_idx].cfg;
+  GemvArgs v = a;
+  v.parts = 1;
+  if (c.split > 1) {
+    if (!gemv_split_takes(c, a.M, a.N)) {
+      cfg_idx = c.base;
+    } else {
+      v.parts = c.split;
+      if (!v.part || !v.cnt) {
+        const int rc = gemv_split_buffers(s, gemv_split_bytes(cfg_idx, a.M, a.N), &v.part, &v.cnt);
+        if (rc) return rc;
+      }
+    }
+  }
+  kGemvStream[cfg_idx].fn[slot](v, w, ldw, (int)kchunks, s);
   return HXI_OK;
+}
+bool gemv_split_takes(const GemvConfig& c, int64_t M, int64_t N) {
+  // M <= 4 takes the few-row reduction, which finishes in place
+  return c.split > 1 && c.mb == 1 && !c.xl && M > 4 && M <= 16 &&
+         ((N + 15) / 16 + c.ct - 1) / c.ct <= kGemvSplitCounters;
+}
+size_t gemv_split_bytes(int cfg, int64_t M, int64_t N) {
+  const GemvConfig* c = gemv_packed_config(cfg);
+  if (!c || !gemv_split_takes(*c, M, N)) return 0;
+  return (size_t)c->split * (size_t)M * (size_t)N * 4;
 }
 bool gemv_xl_fits(const GemvConfig& c, int64_t M, int64_t K, int wt) {
   if (!c.xl) return true;

@@ -104,14 +104,34 @@ struct GemvArgs {
   // optional SwiGLU gate [M][N] f16 (streaming kernel, f16 output): each
   // output becomes RNE(silu(gate) * RNE(result))
   const uint16_t* gate = nullptr; int64_t ldg = 0;
+  // K split over workgroups (set by the launcher from the config): `parts`
+  // workgroups per column-tile group each reduce a contiguous K range into
+  // binary32 partials [parts][M][N]; the last of them to finish (one
+  // counter per group, returned to zero by that workgroup) adds the parts
+  // in part order and finishes the outputs.  Null buffers: the launcher
+  // takes the stream's own.
+  int parts = 1;
+  float* part = nullptr;
+  unsigned* cnt = nullptr;
 };
 struct GemvConfig {
   int ct, kw;        // 16-column tiles per workgroup, waves splitting K
   const char* name;
   int xl;            // activations staged in LDS (M <= 4, rows within 64 KiB)
-  int base;          // config that runs outside the xl limits
+  int base;          // config that runs outside the xl or split limits
   int mb;            // 16-row activation blocks (M <= 16 mb)
+  int split = 1;     // workgroups per column-tile group (K parts), M > 4 only
 };
+// Counters the split GEMV may use per launch (one per column-tile group).
+constexpr int64_t kGemvSplitCounters = 16384;
+// Partial bytes a launch of config `cfg` needs at this shape (0: it does
+// not split here).
+size_t gemv_split_bytes(int cfg, int64_t M, int64_t N);
+// Whether config `cfg` splits K at M rows and N columns.
+bool gemv_split_takes(const GemvConfig& c, int64_t M, int64_t N);
+// The stream's split buffers (at least part_bytes of partials and
+// kGemvSplitCounters zeroed counters); defined by the API layer.
+int gemv_split_buffers(hipStream_t s, size_t part_bytes, float** part, unsigned** cnt);
 // Largest M the decode GEMV takes (row-block configs).
 constexpr int kGemvMaxRows = 64;
 // Where 16 < M <= kGemvRowsMaxM rows take the decode GEMV's row blocks
@@ -196,6 +216,9 @@ int launch_transpose(const void* src, int64_t lds, void* dst, int64_t ldd, int64
                      int64_t cols, int elem_bytes, hipStream_t s);
 // f32 [rows][cols] (row stride lds) -> dense f16, (x + 0) rounded to
 // nearest even (-0 becomes +0): the reference's f32 pack quantisation.
+// n 32-bit words of p set to v by a kernel (graph-capturable, unlike a
+// memset node).
+int launch_fill_u32(unsigned* p, int64_t n, unsigned v, hipStream_t s);
 int launch_f32_to_f16_rne(const float* src, int64_t lds, uint16_t* dst, int64_t rows, int64_t cols,
                           hipStream_t s);
 // f16 -> f32 widening of a vector (scales).

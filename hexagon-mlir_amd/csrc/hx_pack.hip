@@ -152,6 +152,18 @@ int launch_f32_to_f16_rne(const float* src, int64_t lds, uint16_t* dst, int64_t 
   return HXI_OK;
 }
 
+__global__ void __launch_bounds__(256) fill_u32_kernel(unsigned* p, int64_t n, unsigned v) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = v;
+}
+
+int launch_fill_u32(unsigned* p, int64_t n, unsigned v, hipStream_t s) {
+  if (n <= 0) return HXI_OK;
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 1024) blocks = 1024;
+  fill_u32_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(p, n, v);
+  return HXI_OK;
+}
+
 // Content hash: H = sum over 8-byte words i of mix(word_i + (i+1)*phi), plus
 // the tail bytes folded into one last word.  The per-word mix includes the
 // position, so permutations change H; the sum is order-free, so the result

@@ -128,6 +128,7 @@ class Probe {
       const GemvConfig* c = gemv_packed_config(t);
       if (m_ > 16 * c->mb) return "rows-exceed-blocks";
       if (!gemv_xl_fits(*c, m_, k_, wt_)) return "staging-limit";
+      if (c->split > 1 && !gemv_split_takes(*c, m_, n_)) return "split-rows";
       if (16 * c->ct > std::max<int64_t>(16, pad_pow2(n_))) return "tile-exceeds-extent";
       return nullptr;
     }

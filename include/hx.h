@@ -255,10 +255,12 @@ int hx_swiglu_ffn(const hx_memref2d* x, const hx_memref1d* gamma, float eps,
  * of the stream workspace.  The call makes no hipMalloc or hipFree.  It
  * needs T*(H + I)*2 bytes for T > 32 tokens (at most T*(H + 3 I)*2 for T <= 32, the
  * decode path), plus T*H*4 per K part when the down projection's
- * configuration splits K (256-byte aligned each); a shape that needs more
- * than the array returns HX_ERR_UNSUPPORTED before anything is enqueued.
- * Every call on one GPU shares its array: calls that overlap on one GPU
- * race. */
+ * configuration splits K (on the decode path T*I*4 per part when a decode
+ * GEMV's configuration splits K; 256-byte aligned each), out of the array
+ * less its last 64 KiB (the split decode GEMV's counters, zero between
+ * calls); a shape that needs more returns HX_ERR_UNSUPPORTED before
+ * anything is enqueued.  Every call on one GPU shares its array: calls that
+ * overlap on one GPU race. */
 int hx_swiglu_ffn_noalloc(const hx_memref2d* x, const hx_memref1d* gamma, float eps,
                           hx_weight_t w_gate, hx_weight_t w_up, hx_weight_t w_down,
                           hx_memref2d* y, hx_stream_t stream);
@@ -282,8 +284,10 @@ enum {
 /* One compiled configuration.  GEMM families fill bm/bn/bk (K elements per
  * LDS stage)/waves_m/waves_n/lds_stages (K stages resident in LDS: 2 or 3)/
  * split_k (K parts, partials merged by a second kernel; 1: none); the GEMV
- * families fill col_tiles (16-column tiles per wave) and split_k
- * (workgroups per column tile).
+ * families fill col_tiles (16-column tiles per workgroup), waves_m (waves
+ * splitting K inside a workgroup) and split_k (workgroups splitting K per
+ * group of col_tiles tiles, the last of them to finish adding the parts;
+ * 1: none).
  * Replaces the (BM, BN, BK) tile space of enumerate_tile_configs
  * (QHB/backend/hmx_search.py:246-332), widened to the knobs that matter on
  * gfx950. */

@@ -582,6 +582,48 @@ def test_f32_quantisation_special_values(hx, dev):
     assert diag[6] == 0.0 and diag[7] == 2 ** -24 * 2
 
 
+def test_f32_weight_negative_zero_and_nan(hx, dev):
+    """The pack's `x + 0` turns -0 into +0 (the reference's prepack contract,
+    test_hmx_weight_prepack_f32.py:158-168), which the registry's byte-checked
+    dedupe makes observable: an f32 weight holding -0 shares the handle of the
+    f16 weight holding +0, and an f16 weight holding -0 (0x8000) gets a
+    handle of its own.  A NaN weight stays a NaN (:170-194): its output
+    column is NaN for every row, the other columns are the product of the
+    finite weights."""
+    K, N, M = 256, 512, 4
+    w32 = rng(87).normal(0, 0.5, (K, N)).astype(np.float32)
+    w32[::7, 3] = np.float32(-0.0)
+    w32[5, ::11] = np.float32(-0.0)
+    plus = _quant16(w32)
+    assert not np.signbit(plus[w32 == 0]).any()
+    minus = plus.copy()
+    minus[5, ::11] = np.float16(-0.0)
+    W = hx.ResidentWeight(to_dev(w32, dev), layout="kn")
+    Wp = hx.ResidentWeight(to_dev(plus, dev), layout="kn")
+    Wm = hx.ResidentWeight(to_dev(minus, dev), layout="kn")
+    try:
+        assert W.handle == Wp.handle and Wm.handle != W.handle
+        assert W.info()["refcount"] == 2 and Wm.info()["refcount"] == 1
+    finally:
+        W.release(); Wp.release(); Wm.release()
+
+    wn = w32.copy()
+    nan_cols = [1, 200, 511]
+    wn[17, nan_cols] = np.float32("nan")
+    wn[100, 200] = -np.float32("nan")
+    x = rng(88).normal(0, 1, (M, K)).astype(np.float16)
+    Wn = hx.ResidentWeight(to_dev(wn, dev), layout="kn")
+    try:
+        got = to_np(hx.matmul_resident(to_dev(x, dev), Wn)).astype(np.float32)
+    finally:
+        Wn.release()
+    assert np.isnan(got[:, nan_cols]).all()
+    finite = np.setdiff1d(np.arange(N), nan_cols)
+    assert np.isfinite(got[:, finite]).all()
+    want = oracle.matmul(x, _quant16(w32)).astype(np.float32)
+    assert_close(got[:, finite], want[:, finite], 1e-2, 1e-3, "finite columns of a NaN weight")
+
+
 @pytest.mark.parametrize("M,N", [(8, 512), (20, 2048), (40, 512)])
 def test_resident_f32_weight(hx, dev, M, N):
     """An f32 weight registers as its f16 quantisation: the resident product

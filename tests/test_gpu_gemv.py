@@ -163,3 +163,90 @@ def test_gemv_one_row_nk(hx, dev, shape, scale32):
         assert plans[0] != "gemv-rowdot", plans
     want = oracle.matmul(x, wt, b_trans=True, scale_n=s.astype(np.float32))
     assert_close(to_np(y).astype(np.float32), want.astype(np.float32), 1e-2, 1e-3, f"one row {shape}")
+
+
+def _split_configs(hx):
+    return [(i, hx.config_get(6, i)) for i in range(hx.config_count(6)) if hx.config_get(6, i)["split_k"] > 1]
+
+
+@pytest.mark.parametrize("shape", [(16, 4096, 11008), (9, 1000, 4112), (12, 37, 640), (6, 300, 8200)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_gemv_split_k_over_workgroups(hx, dev, shape):
+    """Configs that split K over workgroups (M > 4): every part's binary32
+    partials and the last workgroup's sum in part order.  Within tolerance of
+    the oracle, bit-identical over repeated calls (the parts are added in
+    the same order whichever workgroup finishes last, and every call returns
+    the counters to zero for the next), with N not a multiple of the tile
+    group and K not a multiple of the parts."""
+    M, N, K = shape
+    x, w, s = case(M, N, K, seed=700)
+    rw = hx.ResidentWeight(to_dev(w, dev), to_dev(s, dev))
+    want = oracle.matmul(x, w, scale_n=s.astype(np.float32)).astype(np.float32)
+    xd = to_dev(x, dev)
+    splits = _split_configs(hx)
+    assert {c["split_k"] for _, c in splits} == {2, 4}, splits
+    try:
+        for cfg, info in splits:
+            hx.config_select(6, M, N, K, cfg)
+            try:
+                runs = [to_np(hx.matmul_resident(xd, rw)) for _ in range(3)]
+            finally:
+                hx.config_select(6, M, N, K, -1)
+            assert_close(runs[0].astype(np.float32), want, 1e-2, 1e-3, f"{info['name']} {shape}")
+            for r in runs[1:]:
+                assert np.array_equal(r.view(np.uint16), runs[0].view(np.uint16)), f"{info['name']}: not repeatable"
+    finally:
+        rw.release()
+
+
+def test_gemv_split_k_few_rows_run_the_base(hx, dev):
+    """With M <= 4 a split config runs its base config (the few-row
+    reduction finishes in place): bit-identical to the base pinned itself,
+    and the tuner refuses it with a reason."""
+    M, N, K = 4, 4096, 11008
+    x, w, s = case(M, N, K, seed=710)
+    rw = hx.ResidentWeight(to_dev(w, dev), to_dev(s, dev))
+    xd = to_dev(x, dev)
+    names = [hx.config_get(6, i)["name"] for i in range(hx.config_count(6))]
+    base = {"gemv_packed_ct2_kw16_s2": "gemv_packed_ct2_kw8", "gemv_packed_ct4_kw16_s4": "gemv_packed_ct4_kw16",
+            "gemv_packed_ct6_kw16_s2": "gemv_packed_ct3_kw16"}
+    try:
+        for sname, bname in base.items():
+            got = []
+            for name in (sname, bname):
+                hx.config_select(6, M, N, K, names.index(name))
+                try:
+                    got.append(to_np(hx.matmul_resident(xd, rw)))
+                finally:
+                    hx.config_select(6, M, N, K, -1)
+            assert np.array_equal(got[0].view(np.uint16), got[1].view(np.uint16)), sname
+    finally:
+        rw.release()
+    r = hx.search.tune(6, M, N, K, canary_reference_us=-1.0, reps=3, budget_us=20_000.0, min_iters=5,
+                       max_iters=40, pin=False)
+    reasons = {e["cfg"]: e.get("reason") for e in r["entries"]}
+    assert all(reasons[n] == "split-rows" for n in base), reasons
+
+
+def test_gemv_split_k_is_the_default_where_it_pays(hx, dev):
+    """The untuned choice: 12 rows or more on at most 256 tiles with K of
+    8192 or more split K over workgroups (int8: four tiles, four parts);
+    8 rows, or N = 11008 (688 tiles), do not."""
+    N, K = 4096, 11008
+    x, w, s = case(16, N, K, seed=720)
+    rw = hx.ResidentWeight(to_dev(w, dev), to_dev(s, dev))
+    x2, w2, s2 = case(16, 11008, 4096, seed=721)
+    rw2 = hx.ResidentWeight(to_dev(w2, dev), to_dev(s2, dev))
+    hx.manifest_clear()
+    prev = hx.manifest_enable(True)
+    try:
+        for M in (16, 8):
+            hx.matmul_resident(to_dev(np.ascontiguousarray(x[:M]), dev), rw)
+        hx.matmul_resident(to_dev(x2, dev), rw2)
+        recs = hx.manifest()["records"]
+    finally:
+        hx.manifest_enable(prev)
+        rw.release(); rw2.release()
+    got = {(r["m"], r["n"]): r["config"] for r in recs}
+    assert got[(16, 4096)] == "packed_ct4_kw16_s4", got
+    assert "_s" not in got[(8, 4096)][-3:] and "_s" not in got[(16, 11008)][-3:], got

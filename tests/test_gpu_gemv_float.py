@@ -341,3 +341,34 @@ def test_decode_row_blocks_every_config(hx, dev):
             assert_close(got, want, 1e-2, 1e-3, f"int8 rows cfg {cfg}")
     finally:
         rw.release()
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("shape", [(16, 4096, 11008), (9, 523, 4104)], ids=lambda s: "x".join(map(str, s)))
+def test_decode_float_split_k(hx, dev, dtype, shape):
+    """The K split over workgroups on f16 / bf16 weights, on the packed image
+    and read in place (an argument [N][K] weight), every split config:
+    within the oracle's tolerances and repeatable bit for bit."""
+    import torch
+    M, N, K = shape
+    a = _fp(dtype, (M, K), 60)
+    b = _fp(dtype, (K, N), 61)
+    bnk = np.ascontiguousarray(b.T)
+    op = OP[dtype]
+    rw = hx.ResidentWeight(_dev(b, dtype, dev), layout="kn")
+    ad, bd = _dev(a, dtype, dev), _dev(bnk, dtype, dev)
+    splits = [i for i in range(hx.config_count(op)) if hx.config_get(op, i)["split_k"] > 1]
+    assert len(splits) == 3
+    try:
+        for cfg in splits:
+            hx.config_select(op, M, N, K, cfg)
+            try:
+                res = [to_np(hx.matmul_resident(ad, rw)) for _ in range(2)]
+                arg = [to_np(hx.matmul(ad, bd, b_layout="nk")) for _ in range(2)]
+            finally:
+                hx.config_select(op, M, N, K, -1)
+            for got, what in ((res, "packed"), (arg, "in place")):
+                _check(got[0], a, b, dtype, f"{what} {dtype} {shape} cfg {cfg}")
+                assert np.array_equal(got[0].view(np.uint16), got[1].view(np.uint16)), f"{what} cfg {cfg}"
+    finally:
+        rw.release()

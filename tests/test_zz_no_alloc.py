@@ -37,9 +37,11 @@ def _noalloc(hx, x, gamma, eps, Wg, Wu, Wd, y, stream):
 
 
 def test_noalloc_matches_and_allocates_nothing(hx, dev):
-    """Two no-allocation calls in a row (256 tokens: the fused gate/up GEMM and
-    the K-split down projection; then 24 tokens: the decode GEMVs) leave the
-    device's free memory unchanged and equal hx_swiglu_ffn bit for bit.  A
+    """No-allocation calls in a row (256 tokens: the fused gate/up GEMM and
+    the K-split down projection; then 24 tokens: the decode GEMVs; then 16:
+    the down projection's decode GEMV split over workgroups, its partials and
+    counters in the scratch) leave the device's free memory unchanged and
+    equal hx_swiglu_ffn bit for bit.  A
     warm-up pass first lets the HIP runtime load the kernels' code objects
     and set up the stream (its own lazy allocations, not the call's)."""
     import torch
@@ -50,7 +52,7 @@ def test_noalloc_matches_and_allocates_nothing(hx, dev):
     assert hx._abi.load().hx_init() == 0, hx._abi.last_error()
     try:
         gamma = to_dev(rng(501).normal(1, 0.1, H).astype(np.float16), dev)
-        shapes = (256, 24)
+        shapes = (256, 24, 16)
         xs = {T: to_dev(rng(502 + T).normal(0, 1, (T, H)).astype(np.float16), dev) for T in shapes}
         ys = {T: torch.full((T, H), 7.0, dtype=torch.float16, device=dev) for T in shapes}
         refs = {T: torch.full((T, H), 3.0, dtype=torch.float16, device=dev) for T in shapes}
@@ -61,7 +63,7 @@ def test_noalloc_matches_and_allocates_nothing(hx, dev):
             ys[T].fill_(7.0)
         torch.cuda.synchronize()
         free_before = torch.cuda.mem_get_info()[0]
-        for T in shapes:  # the measured calls: 256 tokens, then 24
+        for T in shapes:  # the measured calls: 256 tokens, then 24, then 16
             with torch.cuda.stream(stream):
                 rc = _noalloc(hx, xs[T], gamma, 1e-6, Wg, Wu, Wd, ys[T], stream)
             assert rc == 0, hx._abi.last_error()
@@ -78,10 +80,11 @@ def test_noalloc_matches_and_allocates_nothing(hx, dev):
         Wg.release(); Wu.release(); Wd.release()
 
 
-@pytest.mark.parametrize("T", [256, 24])
+@pytest.mark.parametrize("T", [256, 24, 16])
 def test_noalloc_in_a_hip_graph(hx, dev, T):
     """The call captured into a HIP graph (256 tokens: the GEMM path; 24: the
-    decode GEMVs), then three replays, each after eager work that rewrites
+    decode GEMVs; 16: with the K-split decode GEMV, whose counters every
+    replay returns to zero), then three replays, each after eager work that rewrites
     the activations and a synchronization, each equal bit for bit to the
     eager hx_swiglu_ffn on the same activations."""
     import torch
