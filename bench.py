@@ -309,6 +309,18 @@ def cpu_baselines_secondary(march: str) -> dict:
                                  sample=f"full W8A16 GEMV M={M} N={N} K={K}, hxo_matmul (i,k,j) loop, "
                                         f"median of 3 after a warm-up (rows over threads)")
     del w
+    # the same product at the FFN's down-projection shape, 16 rows
+    N, K, M = 4096, 11008, 16
+    w = r.integers(-127, 128, (K, N), dtype=np.int8)
+    sc = r.uniform(0.001, 0.02, N).astype(np.float32)
+    x = r.normal(0, 1, (M, K)).astype(np.float16)
+    t = _median_time(lambda: oracle.matmul(x, w, scale_n=sc), 3)
+    nbytes = N * K + 2 * N + 2 * M * K + 2 * M * N
+    out["gemv_down"] = dict(base, value=round(nbytes / t / 1e9, 3), unit="GB/s", cores=min(M, threads),
+                            us_per_call=round(t * 1e6, 1),
+                            sample=f"full W8A16 GEMV M={M} N={N} K={K}, hxo_matmul (i,k,j) loop, "
+                                   f"median of 3 after a warm-up (rows over threads)")
+    del w
     # C4: softmax / RMSNorm on the full 8192 x 4096 fp16 matrix
     R, C = 8192, 4096
     xr = (r.normal(0, 2, (R, C))).astype(np.float16)
@@ -417,6 +429,49 @@ def bench_gemv(hx, iters: int = 600, tune_on: bool = True, tune_fn=tune):
         for w in weights:
             w.release()
     return res
+
+
+def bench_gemv_down(hx, iters: int = 400):
+    """The int8 decode GEMV at 16 rows on the FFN's down-projection shape
+    (N = 4096, K = 11008): the untuned default splits K over workgroups; the
+    unsplit one-tile config is timed beside it on the same weights."""
+    import torch
+    M, N, K = 16, 4096, 11008
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(98)
+    copies = 12  # 12 x 45 MB > 2x the MALL
+    weights = []
+    for _ in range(copies):
+        w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+        sc = torch.empty(N, dtype=torch.float16, device=dev).uniform_(0.001, 0.02, generator=g)
+        weights.append(hx.ResidentWeight(w, sc, layout="nk"))
+        del w
+    try:
+        x = torch.randn((M, K), dtype=torch.float16, device=dev, generator=g)
+        ys = [torch.empty((M, N), dtype=torch.float16, device=dev) for _ in weights]
+        names = [hx.config_get(6, i)["name"] for i in range(hx.config_count(6))]
+        hx.config_select(6, M, N, K, -1)
+        cfg = hx.config_get(6, hx.config_lookup(6, M, N, K))["name"]
+        times = {}
+        for name in (cfg, "gemv_packed_ct1_kw8"):
+            hx.config_select(6, M, N, K, names.index(name))
+            calls = [hx.bind_matmul_resident(x, w, y) for w, y in zip(weights, ys)]
+            for c in calls:
+                c()
+            times[name] = event_timed(calls, iters)
+        hx.config_select(6, M, N, K, -1)
+        ev_ms, fed = times[cfg]
+        nbytes = N * K + 2 * N + 2 * M * K + 2 * M * N
+        gbs = nbytes / (ev_ms * 1e-3) / 1e9
+        return [{"workload": f"W8A16 GEMV M={M} N={N} K={K} (the FFN's down projection at 16 tokens)",
+                 "value": round(gbs, 1), "unit": "GB/s", "us_per_call": round(ev_ms * 1e3, 3),
+                 "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s", None),
+                 "bytes_per_call": nbytes, "kernel": cfg, "split_k": hx.config_get(6, names.index(cfg))["split_k"],
+                 "unsplit_us_same_weights": round(times["gemv_packed_ct1_kw8"][0] * 1e3, 3),
+                 "queue_fed": fed, "mall_defeat": f"rotating {copies} resident weight copies (541 MB)"}]
+    finally:
+        for w in weights:
+            w.release()
 
 
 def bench_rows(hx, iters: int = 60):
@@ -1202,6 +1257,8 @@ def main() -> int:
         secondary.append(bench_gemm_i8_kn(hx, h["inputs"]))
         log("[bench] W8A16 GEMV")
         secondary += bench_gemv(hx, tune_on=tune_on)
+        log("[bench] W8A16 GEMV, down-projection shape")
+        secondary += bench_gemv_down(hx)
         log("[bench] row ops")
         secondary += bench_rows(hx)
         secondary.append(bench_rows_long(hx))
@@ -1226,7 +1283,8 @@ def main() -> int:
         log(f"[bench] CPU: {cpu['value']} TOPS on {cpu['cores']} threads")
         if secondary:
             sec_cpu = cpu_baselines_secondary(march)
-            keys = {"W8A16 GEMV M=1 ": "gemv_m1", "W8A16 GEMV M=4 ": "gemv_m4", "W8A16 GEMV M=16 ": "gemv_m16",
+            keys = {"W8A16 GEMV M=1 ": "gemv_m1", "W8A16 GEMV M=4 ": "gemv_m4",
+                    "W8A16 GEMV M=16 N=11008 ": "gemv_m16", "W8A16 GEMV M=16 N=4096 ": "gemv_down",
                     "softmax fp16 [8192": "softmax", "softmax fp16 [2048 x 128256]": "softmax_vocab",
                     "rmsnorm fp16": "rmsnorm", "fp16 GEMM 256^3": "gemm_f16_256",
                     "SwiGLU FFN": "ffn"}
