@@ -438,13 +438,19 @@ static int gemv_untuned_table(int op, int64_t M, int64_t N, int64_t K, bool in_p
     // (16 x 4096 x 16384: 30.6 against 39.5 for two)
     if (M <= 2) return 7;
     if (M <= 4) return 5;
-    // more than 8 rows with K >= 8192 on at most 128 tiles (one tile per
-    // workgroup would leave half the CUs idle), or with K >= 10240 on at
-    // most 256: two tiles per workgroup with K split over two workgroups
-    // (M = 9 / 12 / 16: 2048 x 8192 12.1 / 12.7 / 13.5 against 12.5 / 13.9 /
-    // 15.3 us; 4096 x 11008 17.9 / 18.4 / 19.3 against 18.4 / 20.0 / 22.1;
-    // at 4096 x 8192 the split lost, 16.8 against 14.8 at M = 9)
-    if (M > 8 && K >= 8192 && (tiles <= 128 || (tiles <= 256 && K >= 10240))) return 25;
+    // K split over workgroups.  At most 128 tiles (one tile per workgroup
+    // leaves half the CUs idle), K >= 8192: one tile over two parts up to 8
+    // rows, two tiles over four beyond (M = 5 / 8 / 12 / 16 at 2048 x 8192:
+    // 9.4 / 9.9 / 10.4 / 10.6 against 10.6 / 12.3 / 13.9 / 15.3 us unsplit;
+    // 1024 x 8192: 8.3 / 9.0 / 9.0 / 9.4 against 10.1 / 11.7 / 11.8 / 12.7);
+    // K = 4096 from 12 rows one tile over two parts (2048 x 4096: 7.4 / 7.7
+    // against 8.0 / 8.8).  More than 8 rows with K >= 10240 on at most 256
+    // tiles: two tiles over two parts (4096 x 11008, M = 9 / 12 / 16: 17.9 /
+    // 18.4 / 19.3 against 18.4 / 20.0 / 22.1; at 4096 x 8192 the split lost,
+    // 16.8 against 14.8 at M = 9).
+    if (tiles <= 128 && K >= 8192) return M <= 8 ? 28 : 29;
+    if (tiles <= 128 && K >= 4096 && M >= 12) return 28;
+    if (M > 8 && tiles <= 256 && K >= 10240) return 25;
     return three_tiles ? 20 : tiles >= 512 ? 0 : 1;
   }
   // untuned choice from the MI355X sweep (int8, K = 4096, tuner medians).
@@ -462,6 +468,11 @@ static int gemv_untuned_table(int op, int64_t M, int64_t N, int64_t K, bool in_p
   // four tiles everywhere took 9.63 / 9.86 / 10.5 / 13.64 / 22.25).
   if (three_tiles) return 20;
   if (M <= 4) return tiles > 256 ? 0 : 24;
+  // at most 128 tiles with K >= 8192, up to 12 rows: one tile per
+  // workgroup over two parts (M = 5 / 8 / 12 at 2048 x 8192: 7.2 / 7.8 /
+  // 8.4 against 7.7 / 8.6 / 8.8 us; 1024 x 8192: 7.0 / 7.6 / 8.3 against
+  // 7.5 / 8.5 / 8.5).
+  if (tiles <= 128 && K >= 8192 && M <= 12) return 28;
   // 12 rows or more on at most 256 tiles with K >= 8192: four tiles per
   // workgroup with K split over four workgroups, one workgroup per CU
   // (M = 12 / 16: 4096 x 11008 13.2 / 13.6 against 14.0 / 16.0 us; 2048 x

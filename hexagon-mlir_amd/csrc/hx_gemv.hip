@@ -746,6 +746,10 @@ static const GemvStreamEntry kGemvStream[] = {
     {{2, 16, "packed_ct2_kw16_s2", 0, 0, 1, 2}, HX_GV(2, 16, 4, XS_NONE, false)},
     {{4, 16, "packed_ct4_kw16_s4", 0, 8, 1, 4}, HX_GV(4, 16, 2, XS_NONE, false)},
     {{6, 16, "packed_ct6_kw16_s2", 0, 20, 1, 2}, HX_GV(6, 16, 2, XS_NONE, false)},
+    // at most 128 tiles (N <= 2048): one or two tiles per workgroup with K
+    // split in two or four, 2x the workgroups of one tile each
+    {{1, 16, "packed_ct1_kw16_s2", 0, 24, 1, 2}, HX_GV(1, 16, 4, XS_NONE, false)},
+    {{2, 16, "packed_ct2_kw16_s4", 0, 0, 1, 4}, HX_GV(2, 16, 4, XS_NONE, false)},
 };
 #undef HX_GR
 #undef HX_GV

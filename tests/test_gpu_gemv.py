@@ -209,7 +209,8 @@ def test_gemv_split_k_few_rows_run_the_base(hx, dev):
     xd = to_dev(x, dev)
     names = [hx.config_get(6, i)["name"] for i in range(hx.config_count(6))]
     base = {"gemv_packed_ct2_kw16_s2": "gemv_packed_ct2_kw8", "gemv_packed_ct4_kw16_s4": "gemv_packed_ct4_kw16",
-            "gemv_packed_ct6_kw16_s2": "gemv_packed_ct3_kw16"}
+            "gemv_packed_ct6_kw16_s2": "gemv_packed_ct3_kw16", "gemv_packed_ct1_kw16_s2": "gemv_packed_ct1_kw16",
+            "gemv_packed_ct2_kw16_s4": "gemv_packed_ct2_kw8"}
     try:
         for sname, bname in base.items():
             got = []
@@ -230,23 +231,29 @@ def test_gemv_split_k_few_rows_run_the_base(hx, dev):
 
 def test_gemv_split_k_is_the_default_where_it_pays(hx, dev):
     """The untuned choice: 12 rows or more on at most 256 tiles with K of
-    8192 or more split K over workgroups (int8: four tiles, four parts);
-    8 rows, or N = 11008 (688 tiles), do not."""
+    8192 or more split K over workgroups (int8: four tiles, four parts),
+    and 5 to 12 rows on at most 128 tiles (one tile, two parts); 8 rows on
+    256 tiles, or N = 11008 (688 tiles), do not."""
     N, K = 4096, 11008
     x, w, s = case(16, N, K, seed=720)
     rw = hx.ResidentWeight(to_dev(w, dev), to_dev(s, dev))
     x2, w2, s2 = case(16, 11008, 4096, seed=721)
     rw2 = hx.ResidentWeight(to_dev(w2, dev), to_dev(s2, dev))
+    x3, w3, s3 = case(8, 2048, 8192, seed=722)
+    rw3 = hx.ResidentWeight(to_dev(w3, dev), to_dev(s3, dev))
     hx.manifest_clear()
     prev = hx.manifest_enable(True)
     try:
         for M in (16, 8):
             hx.matmul_resident(to_dev(np.ascontiguousarray(x[:M]), dev), rw)
         hx.matmul_resident(to_dev(x2, dev), rw2)
+        hx.matmul_resident(to_dev(x3, dev), rw3)
         recs = hx.manifest()["records"]
     finally:
         hx.manifest_enable(prev)
-        rw.release(); rw2.release()
+        rw.release(); rw2.release(); rw3.release()
     got = {(r["m"], r["n"]): r["config"] for r in recs}
     assert got[(16, 4096)] == "packed_ct4_kw16_s4", got
     assert "_s" not in got[(8, 4096)][-3:] and "_s" not in got[(16, 11008)][-3:], got
+    # at most 128 tiles (N = 2048), K = 8192: one tile per workgroup over two parts
+    assert got[(8, 2048)] == "packed_ct1_kw16_s2", got
