@@ -185,7 +185,7 @@ __device__ __forceinline__ v4f gv_mfma(v4u a, v4u b, v4f c) {
 
 // MB > 1 (16 < M <= 16 MB): MB blocks of 16 activation rows; every weight
 // fragment feeds MB MFMAs, so the weight is still streamed once.
-template <int CT, int KW, int CPW, int XS, int WT, bool PK, bool PIPE, int MB = 1>
+template <int CT, int KW, int CPW, int XS, int WT, bool PK, bool PIPE, int MB = 1, bool SPLIT = false>
 __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const void* wsrc, int64_t ldw,
                                                               int kchunks) {
   static_assert(MB == 1 || (XS == XS_NONE && !PIPE), "row blocks: register-fragment configs only");
@@ -199,7 +199,8 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
   const int col = lane & 15, g = lane >> 4;
   // K split (non-staged, non-pipelined configs): workgroup b is part
   // b % parts of column-tile group b / parts and reduces chunks [kc0, kc1)
-  const int parts = p.parts;
+  // (a compile-time variant: the unsplit configs keep their code as it was)
+  const int parts = SPLIT ? p.parts : 1;
   const int part = (int)(blockIdx.x % (unsigned)parts), grp = (int)(blockIdx.x / (unsigned)parts);
   const int cpp = (kchunks + parts - 1) / parts;
   const int kc0 = part * cpp, kc1 = min(kchunks, kc0 + cpp);
@@ -671,13 +672,14 @@ int launch_gemv_pack(const int8_t* w, int64_t ldw, int64_t N, int64_t K, int8_t*
 }
 
 typedef void (*GemvStreamLaunch)(const GemvArgs&, const void*, int64_t, int, hipStream_t);
-template <int CT, int KW, int CPW, int XS, bool PIPE, int WT, int MB = 1, bool PK = (WT == DT_I8)>
+template <int CT, int KW, int CPW, int XS, bool PIPE, int WT, int MB = 1, bool PK = (WT == DT_I8),
+          bool SPLIT = false>
 static void gemv_stream_one(const GemvArgs& a, const void* w, int64_t ldw, int kchunks, hipStream_t s) {
   constexpr int KD = WT == DT_I8 ? 64 : 32;
   const int64_t ntiles = (a.N + 15) / 16;
   const int64_t blocks = (ntiles + CT - 1) / CT * a.parts;
   const size_t lds = XS != XS_NONE ? (size_t)a.M * (((int64_t)kchunks * KD + 511) / 512 * 512 + 8) * 2 : 0;
-  gemv_stream_kernel<CT, KW, CPW, XS, WT, PK, PIPE, MB>
+  gemv_stream_kernel<CT, KW, CPW, XS, WT, PK, PIPE, MB, SPLIT>
       <<<dim3((unsigned)blocks), dim3(64 * KW), lds, s>>>(a, w, ldw, kchunks);
 }
 struct GemvStreamEntry {
@@ -688,6 +690,13 @@ struct GemvStreamEntry {
   {&gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_I8>, &gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_F16>, \
    &gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_BF16>, &gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_I8, 1, false>, \
    &gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_F16, 1, true>, &gemv_stream_one<CT, KW, CPW, XS, PIPE, DT_BF16, 1, true>}
+#define HX_GS(CT, KW, CPW)                                                                          \
+  {&gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_I8, 1, true, true>,                              \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_F16, 1, false, true>,                            \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_BF16, 1, false, true>,                           \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_I8, 1, false, true>,                             \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_F16, 1, true, true>,                             \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_BF16, 1, true, true>}
 #define HX_GR(CT, KW, CPW, MB)                                                                      \
   {&gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_I8, MB>,                                        \
    &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_F16, MB>,                                       \
@@ -743,15 +752,16 @@ static const GemvStreamEntry kGemvStream[] = {
     // activation fragments it loads per weight byte drop by the tile count
     // while the workgroup count stays at one per CU (N = 4096: 128 x 2 and
     // 64 x 4; N = 11008: 115 x 2)
-    {{2, 16, "packed_ct2_kw16_s2", 0, 0, 1, 2}, HX_GV(2, 16, 4, XS_NONE, false)},
-    {{4, 16, "packed_ct4_kw16_s4", 0, 8, 1, 4}, HX_GV(4, 16, 2, XS_NONE, false)},
-    {{6, 16, "packed_ct6_kw16_s2", 0, 20, 1, 2}, HX_GV(6, 16, 2, XS_NONE, false)},
+    {{2, 16, "packed_ct2_kw16_s2", 0, 0, 1, 2}, HX_GS(2, 16, 4)},
+    {{4, 16, "packed_ct4_kw16_s4", 0, 8, 1, 4}, HX_GS(4, 16, 2)},
+    {{6, 16, "packed_ct6_kw16_s2", 0, 20, 1, 2}, HX_GS(6, 16, 2)},
     // at most 128 tiles (N <= 2048): one or two tiles per workgroup with K
     // split in two or four, 2x the workgroups of one tile each
-    {{1, 16, "packed_ct1_kw16_s2", 0, 24, 1, 2}, HX_GV(1, 16, 4, XS_NONE, false)},
-    {{2, 16, "packed_ct2_kw16_s4", 0, 0, 1, 4}, HX_GV(2, 16, 4, XS_NONE, false)},
+    {{1, 16, "packed_ct1_kw16_s2", 0, 24, 1, 2}, HX_GS(1, 16, 4)},
+    {{2, 16, "packed_ct2_kw16_s4", 0, 0, 1, 4}, HX_GS(2, 16, 4)},
 };
 #undef HX_GR
+#undef HX_GS
 #undef HX_GV
 int gemv_packed_config_count() { return (int)(sizeof(kGemvStream) / sizeof(kGemvStream[0])); }
 const GemvConfig* gemv_packed_config(int idx) {
