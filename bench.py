@@ -1053,7 +1053,11 @@ def ceilings(hx=None) -> dict:
     operands with LDS reads (6 per 8 MFMAs is the GEMM's 128x64 wave tile)
     and L2-resident global loads beside it."""
     import torch
-    lib = ctypes.CDLL(str(ROOT / "hexagon-mlir_amd" / "libhxprobe.so"))
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("_hx_build", ROOT / "hexagon-mlir_amd" / "build.py")
+    b = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(b)
+    lib = ctypes.CDLL(str(b.build_probe()))
     vp, i64, ci = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
     lib.hxp_empty.argtypes = [vp]
     lib.hxp_read.argtypes = [vp, i64, ci, vp, vp]

@@ -96,7 +96,6 @@ def build(verbose: bool = False) -> Path:
         sys.stderr.write(r.stdout + r.stderr)
         raise RuntimeError("link of libhxmi.so failed")
     os.replace(tmp, OUT)
-    build_probe()
     return OUT
 
 
@@ -106,7 +105,8 @@ PROBE_OUT = PKG / "libhxprobe.so"
 
 def build_probe() -> Path:
     """libhxprobe.so: the measurement probes bench.py --ceilings times
-    (empty launch, streaming read, copy, MFMA issue); not part of the hx ABI."""
+    (empty launch, streaming read, copy, MFMA issue); not part of the hx ABI
+    and not part of build(): bench.py --ceilings compiles it when it runs."""
     tmp = PROBE_OUT.with_suffix(".so.tmp")
     cmd = [HIPCC, *COMMON, "-shared", str(PROBE_SRC), "-o", str(tmp)]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -79,6 +79,9 @@ static int map_internal(int rc, const char* what) {
     case HXI_ERR_UNSUPPORTED: return fail(HX_ERR_UNSUPPORTED, "%s: shape not supported", what);
     case HXI_ERR_DTYPE: return fail(HX_ERR_DTYPE, "%s: dtype not supported", what);
     case HXI_ERR_SHAPE: return fail(HX_ERR_SHAPE, "%s: bad shape", what);
+    // set-up failures whose helper already recorded the message
+    case HXI_ERR_NOMEM: return HX_ERR_NOMEM;
+    case HXI_ERR_CAPTURE: return HX_ERR_UNSUPPORTED;
     default: return fail(HX_ERR_ARG, "%s: internal argument error %d", what, rc);
   }
 }
@@ -147,15 +150,36 @@ static int part_get(hipStream_t s, size_t bytes, float** out) {
 
 // The K-split decode GEMV's buffers: its binary32 partials share the
 // K-split GEMM's region (one kernel uses it at a time on a stream), and its
-// per-group counters are a fixed region cleared once, when allocated (on
-// `s`, ahead of every kernel that uses it; each kernel returns the counters
-// it used to zero).  The first split GEMV on a stream therefore runs
-// outside graph capture, like the first use of the workspace.
+// per-group counters are a fixed region cleared once, when allocated, by a
+// fill kernel on `s` followed by a wait for it (each kernel that counts
+// returns the counters it used to zero).  Setting them up allocates and
+// waits, so it cannot happen while `s` is being captured into a graph: the
+// first split GEMV on a stream must run eagerly, and one captured before
+// that is refused with HX_ERR_UNSUPPORTED rather than recording a clear that
+// only a replay would run.
 static std::map<std::pair<int, hipStream_t>, Workspace> g_cnt;
+static int capture_refusal(hipStream_t s, const char* what) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &st) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(HX_ERR_HIP, "%s: querying the stream's capture status failed", what);
+  }
+  if (st != hipStreamCaptureStatusNone)
+    return fail(HX_ERR_UNSUPPORTED,
+                "%s: first use on this stream under graph capture (set-up allocates and waits; "
+                "run one such call on the stream before capturing)", what);
+  return HX_OK;
+}
 int hx::gemv_split_buffers(hipStream_t s, size_t part_bytes, float** part, unsigned** cnt) {
-  if (part_get(s, part_bytes, part)) return HXI_ERR_NOMEM;
   int dev;
   if (current_device(&dev)) return HXI_ERR_NOMEM;
+  bool ready;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    ready = g_cnt[{dev, s}].buf != nullptr && g_part[{dev, s}].bytes >= part_bytes;
+  }
+  if (!ready && capture_refusal(s, "split decode GEMV")) return HXI_ERR_CAPTURE;
+  if (part_get(s, part_bytes, part)) return HXI_ERR_NOMEM;
   std::lock_guard<std::mutex> lk(g_mu);
   Workspace& w = g_cnt[{dev, s}];
   if (!w.buf) {
@@ -165,10 +189,11 @@ int hx::gemv_split_buffers(hipStream_t s, size_t part_bytes, float** part, unsig
       fail(HX_ERR_NOMEM, "split GEMV counters of %zu bytes", nb);
       return HXI_ERR_NOMEM;
     }
-    if (hipMemsetAsync(w.buf, 0, nb, s) != hipSuccess) {
+    if (launch_fill_u32(reinterpret_cast<unsigned*>(w.buf), kGemvSplitCounters, 0u, s) != HXI_OK ||
+        hipGetLastError() != hipSuccess || hipStreamSynchronize(s) != hipSuccess) {
       (void)hipFree(w.buf);
       w.buf = nullptr;
-      fail(HX_ERR_HIP, "clearing the split GEMV counters");
+      fail(HX_ERR_NOMEM, "clearing the split GEMV counters");
       return HXI_ERR_NOMEM;
     }
     w.bytes = nb;

@@ -574,6 +574,21 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
   // issue) finishes the outputs, adding the parts in part order whichever
   // finished last (the result does not depend on scheduling).  No
   // workgroup waits for another.
+  //
+  // What this relies on (gfx942 / gfx950, the AMDGPU memory model's code
+  // sequences for agent scope): an agent-scope atomic store is a store
+  // with the device-coherence bit set, written through the XCD's L2, and a
+  // store's vmcnt decrement means it has been acknowledged at that
+  // coherence point -- the model's own release sequence ("buffer_wbl2;
+  // s_waitcnt vmcnt(0); store") rests on the same fact, its L2 write-back
+  // being needed only for cached (non-atomic) earlier stores, of which
+  // there are none here; an agent-scope atomic load bypasses the L2, so no
+  // acquire invalidate is needed for loads that are all atomic.  GFX10+
+  // counts stores separately (vscnt), where vmcnt(0) would not wait for
+  // them: the guard below keeps this protocol to the gfx9 targets.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__) && !defined(__gfx942__)
+#error "split decode GEMV: the last-arriver protocol is written for gfx942 / gfx950 (vmcnt counts stores)"
+#endif
   __shared__ int is_last;
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();

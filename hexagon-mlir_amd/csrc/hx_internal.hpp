@@ -16,6 +16,7 @@ enum : int {
   HXI_ERR_HIP = -5,
   HXI_ERR_NOMEM = -6,
   HXI_ERR_UNSUPPORTED = -7,
+  HXI_ERR_CAPTURE = -8,  // set-up refused under graph capture (message recorded)
 };
 
 // ---- row kernels (hx_rows.hip) -------------------------------------------
@@ -66,6 +67,13 @@ struct GemmArgs {
   // `part` is the partial buffer launch_gemm uses for a split config
   int64_t k_split;
   float* part;
+  // K split merged inside the kernel (null: a second kernel merges): one
+  // counter per output tile, zero on entry and returned to zero; the
+  // partials are then [parts][tiles][BM*BN] in the kernel's register order
+  unsigned* cnt;
+  // measurement hook (null: off): every workgroup adds its elapsed
+  // shader-clock cycles, constant-rate ticks and 1 to clk[0..2]
+  unsigned long long* clk;
 };
 
 struct GemmConfig {
@@ -74,14 +82,23 @@ struct GemmConfig {
   const char* name;
   int occ;              // workgroups resident per CU (LDS / register limit)
   float rate;           // measured output throughput of one CU, relative
-  int ksplit = 0;       // K parts (0 or 1: none); partials merged by a second kernel
+  int ksplit = 0;       // K parts (0 or 1: none); partials merged by the last part of each tile
   int sb = 128;         // bytes of A per row in one K stage (64, 128, 256)
   int stages = 2;       // K stages resident in LDS at once (2 or 3)
+  int persist = 0;      // 1: one workgroup per CU walks consecutive M-tiles of a B strip
 };
 // Partial-buffer bytes a launch of config cfg_idx needs (0 without a K split).
 size_t gemm_part_bytes(int mode, int cfg_idx, const GemmArgs& a);
+// Output tiles of a launch of config cfg_idx (the counters an in-kernel
+// K-split merge uses).
+int64_t gemm_tiles(int mode, int cfg_idx, const GemmArgs& a);
+// The clock hook: the per-device counters launch_gemm passes to the tiled
+// kernels while it is on (null: off).
+void gemm_clock_target(int dev, unsigned long long* clk);
 
 int gemm_config_count(int mode);
+// Compute units of the current device (the persistent configs' grid).
+int gemm_num_cus();
 const GemmConfig* gemm_config(int mode, int idx);
 // Default (untuned) config index for a shape.
 int gemm_default_config(int mode, int epi, int64_t M, int64_t N, int64_t K);

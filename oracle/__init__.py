@@ -18,7 +18,10 @@ gemm_i8_i32            numpy int64 matmul (exact), brute force on 5x7x3,
 dequant_i32_f16        numpy binary32 products + ``astype(float16)``, bitwise
 matmul (f16/bf16/i8)   numpy float64 matmul within the binary32 accumulation
                        bound; identity B reproduces A exactly; residual and
-                       scale each checked by a dropped-term negative control
+                       scale each checked by a dropped-term negative control;
+                       scale and residual together against float64
+                       (A.B).s + R, the swapped order (A.B + R).s failing;
+                       the column-split form bit-equal to the row form
 softmax                numpy float64; rows sum to 1; shift invariance;
                        torch-CPU softmax at the reference test's shape/atol
 rmsnorm                numpy float64; scale invariance; torch-CPU rms_norm at
@@ -111,6 +114,7 @@ def _bind(L):
         L.hxo_dequant_i32_f16.argtypes = [vp, i64, vp, vp, vp, i64, i64, i64]
         L.hxo_matmul.argtypes = [vp, i32, i64, vp, i32, i64, i32, vp, vp, i32, i64,
                                  vp, i32, i64, i64, i64, i64]
+        L.hxo_matmul_ncols.argtypes = L.hxo_matmul.argtypes
         L.hxo_softmax.argtypes = [vp, vp, i32, i64, i64, i64, i64]
         L.hxo_rmsnorm.argtypes = [vp, vp, f32, vp, i32, i64, i64, i64, i64]
         L.hxo_layernorm.argtypes = [vp, vp, vp, f32, vp, vp, vp, i32, i64, i64, i64, i64]
@@ -192,11 +196,13 @@ def dequant_i32_f16(c: np.ndarray, sa=None, sb=None) -> np.ndarray:
 
 
 def matmul(a, b, *, b_trans=False, scale_n=None, residual=None, out_dtype=np.float16,
-           a_bf16=False, b_bf16=False, r_bf16=False, out_bf16=False) -> np.ndarray:
+           a_bf16=False, b_bf16=False, r_bf16=False, out_bf16=False, split_cols=False) -> np.ndarray:
     """out = round(acc * scale_n + residual), acc in binary32 (i,k,j) order.
 
     fp16 arrays are numpy float16; bf16 arrays are passed as uint16 bit
-    patterns with the matching ``*_bf16`` flag."""
+    patterns with the matching ``*_bf16`` flag.  ``split_cols`` spreads the
+    host threads over output columns instead of rows (few-row products);
+    the result is bit-identical."""
     a, b = _rowmajor(a), _rowmajor(b)
     M, K = a.shape
     N = b.shape[0] if b_trans else b.shape[1]
@@ -207,9 +213,10 @@ def matmul(a, b, *, b_trans=False, scale_n=None, residual=None, out_dtype=np.flo
     else:
         out = np.empty((M, N), np.dtype(out_dtype))
         ocode = _code(out)
-    lib().hxo_matmul(_p(a), _code(a, a_bf16), K, _p(b), _code(b, b_bf16), b.shape[1],
-                     int(b_trans), _p(sc), _p(r), 0 if r is None else _code(r, r_bf16),
-                     0 if r is None else r.shape[1], _p(out), ocode, N, M, N, K)
+    fn = lib().hxo_matmul_ncols if split_cols else lib().hxo_matmul
+    fn(_p(a), _code(a, a_bf16), K, _p(b), _code(b, b_bf16), b.shape[1],
+       int(b_trans), _p(sc), _p(r), 0 if r is None else _code(r, r_bf16),
+       0 if r is None else r.shape[1], _p(out), ocode, N, M, N, K)
     return out
 
 

@@ -230,6 +230,47 @@ void hxo_matmul(const void* A, int a_dtype, int64_t lda,
     }
 }
 
+/* hxo_matmul with the threads splitting the output columns instead of the
+ * rows, for products with fewer rows than host threads (the decode GEMV's
+ * M = 1..16).  Each output element is still the sum over k in increasing
+ * order, accumulated in binary32, then scaled and added to the residual, so
+ * the result is bit-identical to hxo_matmul's (pinned by test_oracle.py).
+ * Column blocks of 64 keep a thread's accumulators in a stack row. */
+void hxo_matmul_ncols(const void* A, int a_dtype, int64_t lda,
+                      const void* B, int b_dtype, int64_t ldb, int b_trans,
+                      const float* scale_n, const void* R, int r_dtype, int64_t ldr,
+                      void* C, int c_dtype, int64_t ldc,
+                      int64_t M, int64_t N, int64_t K)
+{
+    const int64_t JB = 64;
+    const int64_t nblk = (N + JB - 1) / JB;
+#pragma omp parallel for schedule(static)
+    for (int64_t blk = 0; blk < nblk; ++blk) {
+        float acc[64];
+        const int64_t j0 = blk * JB;
+        const int64_t j1 = j0 + JB < N ? j0 + JB : N;
+        for (int64_t i = 0; i < M; ++i) {
+            for (int64_t j = j0; j < j1; ++j) acc[j - j0] = 0.0f;
+            for (int64_t k = 0; k < K; ++k) {
+                const float a = load_elem(A, a_dtype, i * lda + k);
+                if (!b_trans) {
+                    for (int64_t j = j0; j < j1; ++j)
+                        acc[j - j0] = acc[j - j0] + a * load_elem(B, b_dtype, k * ldb + j);
+                } else {
+                    for (int64_t j = j0; j < j1; ++j)
+                        acc[j - j0] = acc[j - j0] + a * load_elem(B, b_dtype, j * ldb + k);
+                }
+            }
+            for (int64_t j = j0; j < j1; ++j) {
+                float v = acc[j - j0];
+                if (scale_n) v = v * scale_n[j];
+                if (R) v = v + load_elem(R, r_dtype, i * ldr + j);
+                store_elem(C, c_dtype, i * ldc + j, v);
+            }
+        }
+    }
+}
+
 /* ------------------------------------------------------------------------ */
 /* Row reductions                                                            */
 /* ------------------------------------------------------------------------ */

@@ -143,3 +143,72 @@ def test_softmax_c4_relative(hx, dev, dtype):
     # each row's mass is 1 to within the outputs' own rounding
     assert np.abs(got.sum(axis=1) - 1.0).max() < (2e-3 if dtype == "f16" else 2e-2)
 
+
+
+def ulp_of(v, dtype):
+    """Spacing of the output type at |v| (fp16 via numpy, subnormals
+    included; bf16 as 2^(e - 7), with its smallest normal's spacing below)."""
+    a = np.abs(np.asarray(v, np.float64))
+    if dtype == "f16":
+        return np.spacing(a.astype(np.float16)).astype(np.float64)
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -126)))
+    return 2.0 ** (e - 7)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_rmsnorm_c4_ulps(hx, dev, dtype):
+    """C4 RMSNorm (8192 x 4096, x N(0, 2), gamma N(1, 0.1), eps 1e-6): every
+    output within 2 ulps of the type of the oracle's, and a relative
+    Frobenius error against float64 below 1e-3 (fp16; bf16's own rounding
+    alone gives about 1.6e-3, so 4e-3 there).  The two differ only in the
+    order of the binary32 sum of squares, so a dropped term, a wrong eps or
+    a 0.2% scale error (rstd off by one part in 500; 2% for bf16) fails."""
+    xh, xf = make(dtype, (8192, 4096), seed=12)
+    gh, gf = make(dtype, (4096,), sigma=0.1, mean=1.0, seed=13)
+    got = values(to_np(hx.rms_norm(to_torch(xh, dtype, dev), to_torch(gh, dtype, dev), eps=1e-6)),
+                 dtype).astype(np.float64)
+    want = values(oracle.rmsnorm(xh, gh, 1e-6, bf16=(dtype == "bf16")), dtype).astype(np.float64)
+    x64 = xf.astype(np.float64)
+    y64 = x64 / np.sqrt((x64 * x64).mean(axis=1, keepdims=True) + 1e-6) * gf.astype(np.float64)
+    err = np.abs(got - want)
+    lim = 2 * ulp_of(want, dtype)
+    assert (err <= lim).all(), (int((err > lim).sum()), float((err / np.maximum(lim, 1e-30)).max()))
+    rel = np.linalg.norm(got - y64) / np.linalg.norm(y64)
+    assert rel < (1e-3 if dtype == "f16" else 4e-3), rel
+    # the gate is not vacuous: the oracle scaled by 1.002 (fp16) or 1.02
+    # (bf16, whose two ulps span up to 1.6%) fails it
+    bump = 1.002 if dtype == "f16" else 1.02
+    assert not (np.abs(want * bump - want) <= lim).all()
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_layernorm_c4_ulps(hx, dev, dtype):
+    """LayerNorm at the C4 shape: every output within 2 ulps of the oracle's
+    plus a binary32 allowance relative to the terms it adds (y = t + b with
+    t = (x - mean) * rstd * w can cancel) and to the mean's own rounding, relative Frobenius against float64
+    below 1e-3 (bf16: 4e-3), and the mean / rstd outputs as in
+    test_layernorm."""
+    xh, xf = make(dtype, (8192, 4096), seed=14, mean=0.5)
+    wh, wf = make(dtype, (4096,), sigma=0.2, mean=1.0, seed=15)
+    bh, bf = make(dtype, (4096,), sigma=0.2, seed=16)
+    y, mean, rstd = hx.layer_norm(to_torch(xh, dtype, dev), to_torch(wh, dtype, dev), to_torch(bh, dtype, dev),
+                                  eps=1e-5, return_stats=True)
+    got = values(to_np(y), dtype).astype(np.float64)
+    want, wm, wr = oracle.layernorm(xh, wh, bh, 1e-5, bf16=(dtype == "bf16"))
+    want = values(want, dtype).astype(np.float64)
+    x64 = xf.astype(np.float64)
+    mu = x64.mean(axis=1, keepdims=True)
+    rs = 1.0 / np.sqrt(((x64 - mu) ** 2).mean(axis=1, keepdims=True) + 1e-5)
+    t64 = (x64 - mu) * rs * wf.astype(np.float64)
+    y64 = t64 + bf.astype(np.float64)
+    err = np.abs(got - want)
+    # allowance: binary32 rounding of the terms, and the mean's own binary32
+    # error (a sequential sum of 4096 terms, ~1e-6 here) carried through
+    # rstd * w
+    lim = (2 * ulp_of(want, dtype) + 2.0 ** -20 * (np.abs(t64) + np.abs(bf.astype(np.float64)))
+           + 2.0 ** -17 * rs * np.abs(wf.astype(np.float64)))
+    assert (err <= lim).all(), (int((err > lim).sum()), float((err / lim).max()))
+    rel = np.linalg.norm(got - y64) / np.linalg.norm(y64)
+    assert rel < (1e-3 if dtype == "f16" else 4e-3), rel
+    assert_close(to_np(mean), wm, 1e-5, 1e-5, "mean")
+    assert_close(to_np(rstd), wr, 1e-4, 1e-5, "rstd")

@@ -170,6 +170,50 @@ def test_matmul_residual_term():
     assert np.array_equal(got, want)
 
 
+def test_matmul_scale_and_residual_together():
+    """Both optional terms at once: out = (A.B) * s[j] + R[i, j], the scale
+    applied to the product only (the reference's per-channel read-out scale
+    followed by the residual add, MatmulToHmxPass.cpp:100-121,
+    HMXLayout.c:868-999).  Checked against an independent float64
+    composition within the binary32 accumulation bound plus the final
+    roundings; the swapped order (A.B + R) * s must fail the same gate."""
+    a = rng(24).uniform(-1, 1, (24, 200)).astype(np.float16)
+    b = rng(25).uniform(-1, 1, (200, 40)).astype(np.float16)
+    s = rng(26).uniform(0.5, 4.0, 40).astype(np.float32)
+    r = rng(27).normal(0, 3, (24, 40)).astype(np.float16)
+    ab = a.astype(np.float64) @ b.astype(np.float64)
+    want = ab * s.astype(np.float64) + r.astype(np.float64)
+    bound = _bound(a, b) * s.astype(np.float64) + 2.0 ** -23 * (np.abs(ab * s) + np.abs(want))
+    got32 = oracle.matmul(a, b, scale_n=s, residual=r, out_dtype=np.float32).astype(np.float64)
+    assert (np.abs(got32 - want) <= bound + 1e-12).all()
+    got16 = oracle.matmul(a, b, scale_n=s, residual=r).astype(np.float64)
+    assert np.array_equal(got16, got32.astype(np.float32).astype(np.float16).astype(np.float64))
+    swapped = (ab + r.astype(np.float64)) * s.astype(np.float64)
+    assert not (np.abs(got32 - swapped) <= bound + 1e-12).all(), "gate cannot tell the order apart"
+    # the int8-weight form (W8A16 with a residual) through the same path
+    w = rng(28).integers(-127, 128, (200, 40), dtype=np.int8)
+    got = oracle.matmul(a, w, scale_n=s, residual=r, out_dtype=np.float32).astype(np.float64)
+    aw = a.astype(np.float64) @ w.astype(np.float64)
+    want_w = aw * s + r.astype(np.float64)
+    bound_w = _bound(a, w) * s + 2.0 ** -23 * (np.abs(aw * s) + np.abs(want_w))
+    assert (np.abs(got - want_w) <= bound_w + 1e-12).all()
+
+
+@pytest.mark.parametrize("trans", [False, True])
+def test_matmul_column_split_is_bit_identical(trans):
+    """The column-split form (host threads over output columns, for the
+    few-row CPU baselines) sums each element in the same k order, so it is
+    bit-identical to the row form, with scale and residual."""
+    x = rng(29).normal(0, 1, (5, 300)).astype(np.float16)
+    w = rng(30).integers(-127, 128, (300, 1000), dtype=np.int8)
+    s = rng(31).uniform(0.001, 0.02, 1000).astype(np.float32)
+    r = rng(32).normal(0, 1, (5, 1000)).astype(np.float16)
+    wb = np.ascontiguousarray(w.T) if trans else w
+    want = oracle.matmul(x, wb, b_trans=trans, scale_n=s, residual=r)
+    got = oracle.matmul(x, wb, b_trans=trans, scale_n=s, residual=r, split_cols=True)
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+
+
 # --------------------------------------------------------------------------- #
 # Row reductions
 # --------------------------------------------------------------------------- #
