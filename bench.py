@@ -66,15 +66,45 @@ def _sleep_cycles_per_ms() -> float:
     return _SLEEP_CYCLES_PER_MS
 
 
-def event_timed(calls, iters: int):
-    """Mean device time per launch of ``iters`` calls (cycling through
-    ``calls``) issued back-to-back on the current stream, between one HIP
-    event pair on that stream.  When the host issues a call in well under the
-    device time of one, the queue stays ahead of the device by itself and
-    nothing else runs.  Otherwise a bounded spin kernel holds the stream
-    while the host queues the launches (so host launch cost opens no gaps),
-    followed by a few untimed launches that bring the clocks back up.
-    Returns (ms per launch, whether the queue stayed ahead of the device)."""
+class Timed(tuple):
+    """(ms per launch, whether the queue stayed ahead of the device), the
+    median over timed regions, with the per-region figures kept for the
+    spread."""
+
+    def __new__(cls, ms, fed, region_ms, launches):
+        t = super().__new__(cls, (ms, fed))
+        t.region_ms, t.launches = list(region_ms), launches
+        return t
+
+    @property
+    def ms(self):
+        return self[0]
+
+    def spread(self) -> dict:
+        """q20 / q50 / q80 of the per-region mean launch time, in us."""
+        import numpy as np
+        r = np.asarray(self.region_ms) * 1e3
+        return {"q20_us": round(float(np.quantile(r, 0.2)), 3), "q50_us": round(float(np.quantile(r, 0.5)), 3),
+                "q80_us": round(float(np.quantile(r, 0.8)), 3), "regions": len(r),
+                "launches_per_region": self.launches}
+
+
+#: timed regions behind every figure: the median is reported, q20 / q80
+#: beside it (the reference's bench returns [q50, q20, q80] per config,
+#: QHB/backend/hmx_search.py:1109-1156)
+REGIONS = 5
+
+
+def event_timed(calls, iters: int, regions: int = REGIONS) -> Timed:
+    """Device time per launch of ``iters`` calls (cycling through ``calls``)
+    issued back-to-back on the current stream between one HIP event pair on
+    that stream, in each of ``regions`` timed regions; the median region is
+    the figure.  When the host issues a call in well under the device time
+    of one, the queue stays ahead of the device by itself and nothing else
+    runs.  Otherwise a bounded spin kernel holds the stream while the host
+    queues each region's launches (so host launch cost opens no gaps),
+    followed by a few untimed launches that bring the clocks back up."""
+    import statistics
     import torch
     s = torch.cuda.current_stream()
     torch.cuda.synchronize()
@@ -94,20 +124,41 @@ def event_timed(calls, iters: int):
     hot = max(3, iters // 8)
     spin = host_ms > 0.5 * dev_ms
     hold_ms = 1.0 + 2.0 * host_ms * (iters + hot)
-    if spin:
-        torch.cuda._sleep(int(hold_ms * _sleep_cycles_per_ms()))
-    for i in range(hot):
-        calls[i % len(calls)]()
-    a.record(s)
-    t0 = time.perf_counter()
-    for i in range(iters):
-        calls[i % len(calls)]()
-    queued_ms = (time.perf_counter() - t0) * 1e3
-    b.record(s)
-    torch.cuda.synchronize()
-    ms = a.elapsed_time(b) / iters
-    fed = (queued_ms < hold_ms) if spin else (queued_ms < ms * iters)
-    return ms, fed
+    per, fed = [], True
+    for _ in range(regions):
+        if spin:
+            torch.cuda._sleep(int(hold_ms * _sleep_cycles_per_ms()))
+        for i in range(hot):
+            calls[i % len(calls)]()
+        a.record(s)
+        t0 = time.perf_counter()
+        for i in range(iters):
+            calls[i % len(calls)]()
+        queued_ms = (time.perf_counter() - t0) * 1e3
+        b.record(s)
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / iters
+        per.append(ms)
+        fed = fed and ((queued_ms < hold_ms) if spin else (queued_ms < ms * iters))
+    return Timed(statistics.median(per), fed, per, iters)
+
+
+def clock_during(hx, calls, iters: int) -> dict:
+    """The mean shader clock (MHz) of the tiled GEMM workgroups over one
+    region of ``iters`` launches (the library's clock probe), or None."""
+    try:
+        hx.clock_probe(True)
+        try:
+            for i in range(iters):
+                calls[i % len(calls)]()
+            r = hx.clock_read()
+        finally:
+            hx.clock_probe(False)
+        return {"mhz": round(r["mhz"], 1), "workgroups": r["workgroups"],
+                "method": "s_memtime / s_memrealtime per workgroup (hx_clock_probe), one region of "
+                          f"{iters} launches after the timed ones"}
+    except Exception as e:  # noqa: BLE001
+        return {"mhz": None, "error": str(e)}
 
 
 PROFILES = ROOT / "profiles"
@@ -204,6 +255,10 @@ def bench_gemm_i8(hx, steps: int, warmup: int, tune_on: bool = True):
     ev_ms = ev_a.elapsed_time(ev_b) / steps
     fed = queued_ms < ev_ms * steps  # the host stayed ahead of the device
     marker()
+    # the spread: more timed regions of the same number of launches (at
+    # least 20), and the shader clock the kernel ran at over one more
+    spread = event_timed([step], max(steps, 20), regions=7)
+    clock = clock_during(hx, [step], max(steps, 20))
     ops = 2.0 * M * N * K
     tops_wall = ops / (wall_ms * 1e-3) / 1e12
     tops_kernel = ops / (ev_ms * 1e-3) / 1e12
@@ -219,8 +274,8 @@ def bench_gemm_i8(hx, steps: int, warmup: int, tune_on: bool = True):
     cfg_idx = hx.config_lookup(1, M, N, K)
     cfg = hx.config_get(1, cfg_idx)["name"] if cfg_idx >= 0 else "generic"
     return dict(ms_per_step=wall_ms, kernel_ms=ev_ms, tops=tops_wall, tops_kernel=tops_kernel,
-                parity_sampled_rows_bitexact=exact, kernel=cfg, inputs=(a, bt, sa, sb),
-                tune=tune_report, queue_fed=fed, plan=plan)
+                parity_sampled_rows_bitexact=exact, kernel=cfg, inputs=(a, bt, sa, sb), output=c,
+                tune=tune_report, queue_fed=fed, plan=plan, spread=spread, clock=clock)
 
 
 def _host_threads():
@@ -252,10 +307,11 @@ def _median_time(fn, reps: int) -> float:
     return statistics.median(times)
 
 
-def cpu_baseline_gemm_i8(inputs, march: str, reps: int = 5):
+def cpu_baseline_gemm_i8(inputs, march: str, reps: int = 5, gpu_out=None):
     """The oracle's (i,k,j) int32 loop + dequant over the same inputs: one
     warm-up, then the median of ``reps`` runs of the full 4096^3 product on
-    all host threads (OpenMP), plus a 256-row sample on one thread."""
+    all host threads (OpenMP), plus a 256-row sample on one thread.  The
+    full product is also compared with the GPU's output, every element."""
     import numpy as np
     import oracle
     a, bt, sa, sb = inputs
@@ -264,110 +320,139 @@ def cpu_baseline_gemm_i8(inputs, march: str, reps: int = 5):
     sa_h, sb_h = sa.cpu().numpy(), sb.cpu().numpy()
     K, N = b_kn.shape
     M = a_h.shape[0]
+    last = {}
 
     def run(rows):
         acc = oracle.gemm_i8_i32(np.ascontiguousarray(a_h[:rows]), b_kn)
-        oracle.dequant_i32_f16(acc, sa_h[:rows], sb_h)
+        last["out"] = oracle.dequant_i32_f16(acc, sa_h[:rows], sb_h)
 
     gomp, threads = _host_threads()
     med = _median_time(lambda: run(M), reps)
+    full_exact = None
+    if gpu_out is not None:
+        full_exact = bool(np.array_equal(gpu_out.cpu().numpy().view(np.uint16), last["out"].view(np.uint16)))
     one_core = None
     if gomp is not None:
         gomp.omp_set_num_threads(1)
-        t1 = _median_time(lambda: run(256), 1)
-        gomp.omp_set_num_threads(threads)
+        try:
+            t1 = _median_time(lambda: run(256), 1)
+        finally:
+            gomp.omp_set_num_threads(threads)
         one_core = round(2.0 * 256 * N * K / t1 / 1e12, 5)
     return {"value": round(2.0 * M * N * K / med / 1e12, 5), "unit": "TOPS", "cores": int(threads),
             "kind": "port",
             "sample": f"full int8 4096^3 GEMM + dequant, oracle/hx_oracle.c hxo_gemm_i8_i32 "
                       f"(i,k,j) loop, median of {reps} runs ({med:.3f} s each) after a warm-up",
-            "one_core_tops": one_core, "one_core_sample": "256 of 4096 rows on 1 thread",
-            "cpu_model": _cpu_model(), "build": f"gcc -O3 -march=native ({march}) -fopenmp"}
+            "one_core_value": one_core, "one_core_sample": "256 of 4096 rows on 1 thread",
+            "cpu_model": _cpu_model(), "build": f"gcc -O3 -march=native ({march}) -fopenmp",
+            "gpu_output_bitexact_all_elements": full_exact}
+
+
+def _both(gomp, threads, fn_all, fn_one, reps_all=3):
+    """Median time of fn_all on every host thread, and of fn_one (usually a
+    row sample of the same work) on one thread."""
+    t_all = _median_time(fn_all, reps_all)
+    t_one = None
+    if gomp is not None:
+        gomp.omp_set_num_threads(1)
+        try:
+            t_one = _median_time(fn_one, 1)
+        finally:
+            gomp.omp_set_num_threads(threads)
+    return t_all, t_one
 
 
 def cpu_baselines_secondary(march: str) -> dict:
     """The oracle's restatement of the reference's linalg path for every
-    secondary workload, timed on this host on seeded inputs of the same shape
-    (medians after a warm-up; samples bounded so the whole leg stays within
-    about a minute).  Keys match the secondary workloads' names."""
+    secondary workload, timed on this host on seeded inputs of the same shape:
+    the figure on every host thread (OpenMP: rows, or output columns for the
+    few-row products, over the threads) and a one-thread figure beside it,
+    each on a stated sample (medians after a warm-up; samples bounded so the
+    whole leg stays within about a minute).  Keys match the secondary
+    workloads' names."""
     import numpy as np
     import oracle
     gomp, threads = _host_threads()
     r = np.random.default_rng(2024)
     out = {}
-    base = {"kind": "port", "cpu_model": _cpu_model(), "build": f"gcc -O3 -march=native ({march}) -fopenmp"}
-    # C3: W8A16 decode GEMV, the oracle's dequant matmul ((i,k,j), rows over threads)
+    base = {"kind": "port", "cpu_model": _cpu_model(), "build": f"gcc -O3 -march=native ({march}) -fopenmp",
+            "cores": threads}
+
+    def entry(value_all, value_one, unit, sample, one_sample, **kw):
+        return dict(base, value=value_all, unit=unit, sample=sample, one_core_value=value_one,
+                    one_core_sample=one_sample, **kw)
+
+    def gemv_like(key, M, N, K, w, sc):
+        x = r.normal(0, 1, (M, K)).astype(np.float16)
+        t_all, t_one = _both(gomp, threads, lambda: oracle.matmul(x, w, scale_n=sc, split_cols=True),
+                             lambda: oracle.matmul(x, w, scale_n=sc))
+        nbytes = N * K + 2 * N + 2 * M * K + 2 * M * N
+        out[key] = entry(round(nbytes / t_all / 1e9, 3), round(nbytes / t_one / 1e9, 3) if t_one else None,
+                         "GB/s", f"full W8A16 GEMV M={M} N={N} K={K}, hxo_matmul (i,k,j) loop with output "
+                                 f"columns over {threads} threads, median of 3 after a warm-up",
+                         "the same full product on 1 thread", us_per_call=round(t_all * 1e6, 1))
+
+    # C3: W8A16 decode GEMV
     N, K = 11008, 4096
     w = r.integers(-127, 128, (K, N), dtype=np.int8)
     sc = r.uniform(0.001, 0.02, N).astype(np.float32)
     for M in (1, 4, 16):
-        x = r.normal(0, 1, (M, K)).astype(np.float16)
-        t = _median_time(lambda: oracle.matmul(x, w, scale_n=sc), 3)
-        nbytes = N * K + 2 * N + 2 * M * K + 2 * M * N
-        out[f"gemv_m{M}"] = dict(base, value=round(nbytes / t / 1e9, 3), unit="GB/s",
-                                 cores=min(M, threads), us_per_call=round(t * 1e6, 1),
-                                 sample=f"full W8A16 GEMV M={M} N={N} K={K}, hxo_matmul (i,k,j) loop, "
-                                        f"median of 3 after a warm-up (rows over threads)")
+        gemv_like(f"gemv_m{M}", M, N, K, w, sc)
     del w
     # the same product at the FFN's down-projection shape, 16 rows
-    N, K, M = 4096, 11008, 16
+    N, K = 4096, 11008
     w = r.integers(-127, 128, (K, N), dtype=np.int8)
     sc = r.uniform(0.001, 0.02, N).astype(np.float32)
-    x = r.normal(0, 1, (M, K)).astype(np.float16)
-    t = _median_time(lambda: oracle.matmul(x, w, scale_n=sc), 3)
-    nbytes = N * K + 2 * N + 2 * M * K + 2 * M * N
-    out["gemv_down"] = dict(base, value=round(nbytes / t / 1e9, 3), unit="GB/s", cores=min(M, threads),
-                            us_per_call=round(t * 1e6, 1),
-                            sample=f"full W8A16 GEMV M={M} N={N} K={K}, hxo_matmul (i,k,j) loop, "
-                                   f"median of 3 after a warm-up (rows over threads)")
+    gemv_like("gemv_down", 16, N, K, w, sc)
     del w
-    # C4: softmax / RMSNorm on the full 8192 x 4096 fp16 matrix
+    # C4: softmax / RMSNorm on the full 8192 x 4096 fp16 matrix (1 thread: 512 rows)
     R, C = 8192, 4096
     xr = (r.normal(0, 2, (R, C))).astype(np.float16)
+    xs = np.ascontiguousarray(xr[:512])
     gam = r.normal(1, 0.1, C).astype(np.float16)
-    for name, fn in (("softmax", lambda: oracle.softmax(xr)), ("rmsnorm", lambda: oracle.rmsnorm(xr, gam, 1e-6))):
-        t = _median_time(fn, 3)
-        nbytes = 2 * R * C * 2 + (2 * C if name == "rmsnorm" else 0)
-        out[name] = dict(base, value=round(nbytes / t / 1e9, 3), unit="GB/s", cores=threads,
-                         us_per_call=round(t * 1e6, 1),
-                         sample=f"full {name} fp16 [{R} x {C}], oracle row loop, median of 3 after a warm-up")
-    del xr
+    for name, fa, fo in (("softmax", lambda: oracle.softmax(xr), lambda: oracle.softmax(xs)),
+                         ("rmsnorm", lambda: oracle.rmsnorm(xr, gam, 1e-6), lambda: oracle.rmsnorm(xs, gam, 1e-6))):
+        t_all, t_one = _both(gomp, threads, fa, fo)
+        g = 2 * C if name == "rmsnorm" else 0
+        out[name] = entry(round((2 * R * C * 2 + g) / t_all / 1e9, 3),
+                          round((2 * 512 * C * 2 + g) / t_one / 1e9, 3) if t_one else None, "GB/s",
+                          f"full {name} fp16 [{R} x {C}], oracle row loop, median of 3 after a warm-up",
+                          f"512 of the {R} rows on 1 thread", us_per_call=round(t_all * 1e6, 1))
+    del xr, xs
     # vocabulary-length softmax on a 64-row sample of the 2048 x 128256 rows
     R, C = 64, 128256
     xv = (r.normal(0, 2, (R, C))).astype(np.float16)
-    t = _median_time(lambda: oracle.softmax(xv), 3)
-    out["softmax_vocab"] = dict(base, value=round(2 * R * C * 2 / t / 1e9, 3), unit="GB/s", cores=threads,
-                                us_per_call=round(t * 1e6, 1),
-                                sample=f"softmax fp16 [{R} x {C}] (64 of the 2048 rows), oracle row loop, "
-                                       f"median of 3 after a warm-up")
-    del xv
-    # C1: fp16 256^3
-    a = r.uniform(-1, 1, (256, 256)).astype(np.float16)
-    b = r.uniform(-1, 1, (256, 256)).astype(np.float16)
-    t = _median_time(lambda: oracle.matmul(a, b), 5)
-    out["gemm_f16_256"] = dict(base, value=round(t * 1e6, 2), unit="us", cores=threads,
-                               tflops=round(2 * 256 ** 3 / t / 1e12, 5),
-                               sample="full fp16 256^3 matmul, hxo_matmul, median of 5 after a warm-up")
-    # the reference's published fp16 matmul shapes (S1, S2, S3)
-    for (M, N, K) in REF_SHAPES:
+    xv1 = np.ascontiguousarray(xv[:8])
+    t_all, t_one = _both(gomp, threads, lambda: oracle.softmax(xv), lambda: oracle.softmax(xv1))
+    out["softmax_vocab"] = entry(round(2 * R * C * 2 / t_all / 1e9, 3),
+                                 round(2 * 8 * C * 2 / t_one / 1e9, 3) if t_one else None, "GB/s",
+                                 f"softmax fp16 [{R} x {C}] (64 of the 2048 rows), oracle row loop, "
+                                 "median of 3 after a warm-up", "8 rows on 1 thread",
+                                 us_per_call=round(t_all * 1e6, 1))
+    del xv, xv1
+    # C1 and the reference's published fp16 matmul shapes (S1, S2, S3)
+    for key, (M, N, K) in [("gemm_f16_256", (256, 256, 256))] + [(f"ref_{m}x{n}x{k}", (m, n, k))
+                                                                  for (m, n, k) in REF_SHAPES]:
         a = r.uniform(-1, 1, (M, K)).astype(np.float16)
         b = r.uniform(-1, 1, (K, N)).astype(np.float16)
-        t = _median_time(lambda: oracle.matmul(a, b), 5)
-        out[f"ref_{M}x{N}x{K}"] = dict(base, value=round(t * 1e6, 2), unit="us", cores=threads,
-                                       tflops=round(2.0 * M * N * K / t / 1e12, 5),
-                                       sample=f"full fp16 {M}x{N}x{K} matmul, hxo_matmul, median of 5 after a warm-up")
-    # fp16 decode at the reference tuner's decode shapes (one row: one thread)
+        fn = (lambda a=a, b=b: oracle.matmul(a, b))
+        t_all, t_one = _both(gomp, threads, fn, fn, reps_all=5)
+        out[key] = entry(round(t_all * 1e6, 2), round(t_one * 1e6, 2) if t_one else None, "us",
+                         f"full fp16 {M}x{N}x{K} matmul, hxo_matmul, median of 5 after a warm-up",
+                         "the same product on 1 thread", tflops=round(2.0 * M * N * K / t_all / 1e12, 5))
+    # fp16 decode at the reference tuner's decode shapes (one row: columns over threads)
     for (M, N, K) in ((1, 8192, 8192), (1, 4096, 16384)):
         x = r.uniform(-1, 1, (M, K)).astype(np.float16)
         wk = r.uniform(-1, 1, (K, N)).astype(np.float16)
-        t = _median_time(lambda: oracle.matmul(x, wk), 3)
+        t_all, t_one = _both(gomp, threads, lambda: oracle.matmul(x, wk, split_cols=True),
+                             lambda: oracle.matmul(x, wk))
         nbytes = N * K * 2 + 2 * M * K + 2 * M * N
-        out[f"dec_{M}x{N}x{K}"] = dict(base, value=round(nbytes / t / 1e9, 3), unit="GB/s", cores=min(M, threads),
-                                       us_per_call=round(t * 1e6, 1),
-                                       sample=f"full fp16 decode {M}x{N}x{K}, hxo_matmul (i,k,j) loop, "
-                                              f"median of 3 after a warm-up")
+        out[f"dec_{M}x{N}x{K}"] = entry(round(nbytes / t_all / 1e9, 3), round(nbytes / t_one / 1e9, 3) if t_one else None,
+                                        "GB/s", f"full fp16 decode {M}x{N}x{K}, hxo_matmul (i,k,j) loop with output "
+                                                f"columns over {threads} threads, median of 3 after a warm-up",
+                                        "the same full product on 1 thread", us_per_call=round(t_all * 1e6, 1))
         del wk
-    # C5: the FFN block on a 64-token sample (tokens are independent rows)
+    # C5: the FFN block on a 64-token sample (tokens are independent rows; 1 thread: 4 tokens)
     T, H, I = 64, 4096, 11008
     wg = r.integers(-127, 128, (H, I), dtype=np.int8)
     wu = r.integers(-127, 128, (H, I), dtype=np.int8)
@@ -376,12 +461,29 @@ def cpu_baselines_secondary(march: str) -> dict:
     su = (r.uniform(0.5, 1.5, I) / (127 * np.sqrt(H / 3))).astype(np.float16)
     sd = (r.uniform(0.5, 1.5, H) / (127 * np.sqrt(I / 3))).astype(np.float16)
     xf = r.normal(0, 1, (T, H)).astype(np.float16)
+    x4 = np.ascontiguousarray(xf[:4])
     g1 = r.normal(1, 0.1, H).astype(np.float16)
-    t = _median_time(lambda: oracle.swiglu_ffn(xf, g1, 1e-6, wg, sg, wu, su, wd, sd), 1)
-    out["ffn"] = dict(base, value=round(3 * 2.0 * T * H * I / t / 1e12, 5), unit="TFLOP/s", cores=min(T, threads),
-                      us_per_call=round(t * 1e6, 1),
-                      sample=f"{T} of 2048 tokens through the full block (RMSNorm, gate/up/down W8A16 "
-                             "matmuls, SiLU*mul), oracle composition, one run after a warm-up")
+    t_all, t_one = _both(gomp, threads, lambda: oracle.swiglu_ffn(xf, g1, 1e-6, wg, sg, wu, su, wd, sd),
+                         lambda: oracle.swiglu_ffn(x4, g1, 1e-6, wg, sg, wu, su, wd, sd), reps_all=1)
+    out["ffn"] = entry(round(3 * 2.0 * T * H * I / t_all / 1e12, 5),
+                       round(3 * 2.0 * 4 * H * I / t_one / 1e12, 5) if t_one else None, "TFLOP/s",
+                       f"{T} of 2048 tokens through the full block (RMSNorm, gate/up/down W8A16 matmuls, "
+                       "SiLU*mul), oracle composition, one run after a warm-up", "4 tokens on 1 thread",
+                       us_per_call=round(t_all * 1e6, 1))
+    del wg, wu, wd
+    # attention: the reference test's shape in full, the multi-head shapes on 4 of their 64 heads
+    for key, (Z, H, N, D, causal, scale, heads) in (
+            ("attn_ref", (1, 1, 1024, 64, False, 0.5, 1)), ("attn_mh", (4, 16, 2048, 128, False, None, 4)),
+            ("attn_mh_causal", (4, 16, 2048, 128, True, None, 4))):
+        q, k, v = (r.random((heads, N, D)).astype(np.float16) for _ in range(3))
+        sc_ = scale if scale is not None else D ** -0.5
+        t_all, t_one = _both(gomp, threads, lambda: oracle.attention(q, k, v, sc_, causal),
+                             lambda: oracle.attention(q[:1], k[:1], v[:1], sc_, causal), reps_all=1)
+        fl = 4.0 * N * N * D * (0.5 if causal else 1.0)
+        out[key] = entry(round(heads * fl / t_all / 1e12, 6), round(fl / t_one / 1e12, 6) if t_one else None,
+                         "TFLOP/s", f"{heads} of the {Z * H} heads ({N} x {N} x {D}{', causal' if causal else ''}), "
+                                    "oracle binary32 softmax(QK^T s)V, one run after a warm-up",
+                         "1 head on 1 thread")
     return out
 
 
@@ -414,7 +516,8 @@ def bench_gemv(hx, iters: int = 600, tune_on: bool = True, tune_fn=tune):
             for c in calls:
                 c()
             tuned = tune_fn(hx, 6, M, N, K) if tune_on else None
-            ev_ms, fed = event_timed(calls, iters)
+            tm = event_timed(calls, iters)
+            ev_ms, fed = tm
             nbytes = N * K + 2 * N + 2 * M * K + 2 * M * N
             gbs = nbytes / (ev_ms * 1e-3) / 1e9
             cfg = hx.config_get(6, hx.config_lookup(6, M, N, K))["name"]
@@ -422,7 +525,8 @@ def bench_gemv(hx, iters: int = 600, tune_on: bool = True, tune_fn=tune):
                         "unit": "GB/s", "us_per_call": round(ev_ms * 1e3, 3),
                         "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s",
                                              traffic_of(f"gemv_w8a16_m{M}:{cfg}")),
-                        "bytes_per_call": nbytes, "kernel": cfg, "tune": tuned, "queue_fed": fed,
+                        "spread": tm.spread(), "bytes_per_call": nbytes, "kernel": cfg, "tune": tuned,
+                        "queue_fed": fed,
                         "mall_defeat": f"rotating {copies} resident weight copies (541 MB), "
                                        "each with its own output"})
     finally:
@@ -433,8 +537,9 @@ def bench_gemv(hx, iters: int = 600, tune_on: bool = True, tune_fn=tune):
 
 def bench_gemv_down(hx, iters: int = 400):
     """The int8 decode GEMV at 16 rows on the FFN's down-projection shape
-    (N = 4096, K = 11008): the untuned default splits K over workgroups; the
-    unsplit one-tile config is timed beside it on the same weights."""
+    (N = 4096, K = 11008): the untuned default splits K over workgroups; its
+    unsplit base config (the same tiles and waves, K in one part) is timed
+    beside it on the same weights."""
     import torch
     M, N, K = 16, 4096, 11008
     dev = torch.device("cuda:0")
@@ -452,22 +557,32 @@ def bench_gemv_down(hx, iters: int = 400):
         names = [hx.config_get(6, i)["name"] for i in range(hx.config_count(6))]
         hx.config_select(6, M, N, K, -1)
         cfg = hx.config_get(6, hx.config_lookup(6, M, N, K))["name"]
+        # the split config's own base: the same tiles per workgroup and waves
+        # over K with K in one part (packed_ctC_kwW_sP -> packed_ctC_kwW)
+        import re
+        base = re.sub(r"_s\d+$", "", cfg)
+        if base not in names:
+            base = cfg
         times = {}
-        for name in (cfg, "gemv_packed_ct1_kw8"):
-            hx.config_select(6, M, N, K, names.index(name))
-            calls = [hx.bind_matmul_resident(x, w, y) for w, y in zip(weights, ys)]
-            for c in calls:
-                c()
-            times[name] = event_timed(calls, iters)
-        hx.config_select(6, M, N, K, -1)
-        ev_ms, fed = times[cfg]
+        try:
+            for name in dict.fromkeys((cfg, base)):
+                hx.config_select(6, M, N, K, names.index(name))
+                calls = [hx.bind_matmul_resident(x, w, y) for w, y in zip(weights, ys)]
+                for c in calls:
+                    c()
+                times[name] = event_timed(calls, iters)
+        finally:
+            hx.config_select(6, M, N, K, -1)
+        tm = times[cfg]
+        ev_ms, fed = tm
         nbytes = N * K + 2 * N + 2 * M * K + 2 * M * N
         gbs = nbytes / (ev_ms * 1e-3) / 1e9
         return [{"workload": f"W8A16 GEMV M={M} N={N} K={K} (the FFN's down projection at 16 tokens)",
                  "value": round(gbs, 1), "unit": "GB/s", "us_per_call": round(ev_ms * 1e3, 3),
+                 "spread": tm.spread(),
                  "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s", None),
                  "bytes_per_call": nbytes, "kernel": cfg, "split_k": hx.config_get(6, names.index(cfg))["split_k"],
-                 "unsplit_us_same_weights": round(times["gemv_packed_ct1_kw8"][0] * 1e3, 3),
+                 "unsplit_base": base, "unsplit_base_us_same_weights": round(times[base][0] * 1e3, 3),
                  "queue_fed": fed, "mall_defeat": f"rotating {copies} resident weight copies (541 MB)"}]
     finally:
         for w in weights:
@@ -490,10 +605,11 @@ def bench_rows(hx, iters: int = 60):
                  for i in range(sets)]
         for c in calls:
             c()
-        ev_ms, fed = event_timed(calls, iters)
+        tm = event_timed(calls, iters)
+        ev_ms, fed = tm
         gbs = (nbytes + (2 * C if name == "rmsnorm" else 0)) / (ev_ms * 1e-3) / 1e9
         out.append({"workload": f"{name} fp16 [{R} x {C}]", "value": round(gbs, 1), "unit": "GB/s",
-                    "us_per_call": round(ev_ms * 1e3, 3),
+                    "us_per_call": round(ev_ms * 1e3, 3), "spread": tm.spread(),
                     "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s", traffic_of(f"{name}_f16_8192x4096")),
                     "mall_defeat": "rotating 6 input/output sets (768 MiB)", "queue_fed": fed})
     return out
@@ -514,7 +630,8 @@ def bench_rows_long(hx, iters: int = 20):
         calls = [hx.bind_row_op("softmax", x, y) for x, y in zip(xs, ys)]
         for c in calls:
             c()
-        ev_ms, fed = event_timed(calls, iters)
+        tm = event_timed(calls, iters)
+        ev_ms, fed = tm
         t_ms, _ = event_timed([(lambda x=x, y=y: torch.softmax(x, dim=-1, out=y)) for x, y in zip(xs, ys)], iters)
     finally:
         del xs, ys
@@ -523,13 +640,14 @@ def bench_rows_long(hx, iters: int = 20):
     return {"workload": f"softmax fp16 [{R} x {C}] (vocabulary-length rows)", "value": round(gbs, 1),
             "unit": "GB/s", "us_per_call": round(ev_ms * 1e3, 2),
             "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s", traffic_of(f"softmax_f16_{R}x{C}")),
-            "torch_us_same_tensors": round(t_ms * 1e3, 2), "queue_fed": fed}
+            "spread": tm.spread(), "torch_us_same_tensors": round(t_ms * 1e3, 2), "queue_fed": fed}
 
 
 def bench_gemm_i8_i32(hx, inputs, iters: int = 50):
     """The headline product with the exact int32 result stored (C 67 MB, no
     dequant): same operands and tile config as the headline, timed in
-    alternation with the fp16-dequant product (best of two rounds each),
+    right after the fp16-dequant product over the same regions (both see the
+    same clock and thermal state, so the output's cost is their ratio),
     sampled rows checked bit-exact against the oracle."""
     import numpy as np
     import torch
@@ -544,12 +662,10 @@ def bench_gemm_i8_i32(hx, inputs, iters: int = 50):
     # same clock and thermal state: the output's cost is their ratio
     c16 = torch.empty((M, N), dtype=torch.float16, device=a.device)
     step16 = hx.bind_gemm_i8(a, bt, c16, b_layout="nk", row_scale=sa, col_scale=sb)
-    ev_ms = ev16_ms = float("inf")
-    fed = True
-    for _ in range(2):
-        ms16, _ = event_timed([step16], iters)
-        ms, f = event_timed([step], iters)
-        ev16_ms, ev_ms, fed = min(ev16_ms, ms16), min(ev_ms, ms), fed and f
+    t16 = event_timed([step16], iters)
+    tm = event_timed([step], iters)
+    ev16_ms, ev_ms, fed = t16[0], tm[0], tm[1]
+    clk = clock_during(hx, [step], iters)
     tops = 2.0 * M * N * K / (ev_ms * 1e-3) / 1e12
     rows = np.array([0, 2047, 4095])
     want = oracle.gemm_i8_i32(a[rows].cpu().numpy(), bt.cpu().numpy(), b_trans=True)
@@ -559,6 +675,7 @@ def bench_gemm_i8_i32(hx, inputs, iters: int = 50):
             "value": round(tops, 1), "unit": "TOPS", "us_per_call": round(ev_ms * 1e3, 3),
             "kernel": hx.config_get(1, cfg_idx)["name"] if cfg_idx >= 0 else "generic",
             "roofline": roofline("mfma", tops, PEAK_INT8_TOPS, "TFLOP/s"),
+            "spread": tm.spread(), "clock": clk,
             "f16_dequant_us_same_phase": round(ev16_ms * 1e3, 3),
             "i32_over_f16": round(ev_ms / ev16_ms, 4),
             "parity": {"int32_sampled_rows_bitexact": exact}, "queue_fed": fed}
@@ -584,7 +701,8 @@ def bench_gemm_i8_kn(hx, inputs, iters: int = 50):
     step()
     hx.manifest_enable(False)
     plan = hx.manifest()["records"]
-    ev_ms, fed = event_timed([step], iters)
+    tm = event_timed([step], iters)
+    ev_ms, fed = tm
     tops = 2.0 * M * N * K / (ev_ms * 1e-3) / 1e12
     rows = np.array([0, 2047, 4095])
     acc = oracle.gemm_i8_i32(a[rows].cpu().numpy(), bt.cpu().numpy(), b_trans=True)
@@ -605,6 +723,7 @@ def bench_gemm_i8_kn(hx, inputs, iters: int = 50):
     return {"workload": f"int8 GEMM M=N=K={M} + dequant, B as [K][N]",
             "value": round(tops, 1), "unit": "TOPS", "us_per_call": round(ev_ms * 1e3, 3),
             "kernel": plan[0]["config"] if plan else None, "weight": plan[0]["weight"] if plan else None,
+            "spread": tm.spread(),
             "roofline": roofline("mfma", tops, PEAK_INT8_TOPS, "TFLOP/s"),
             "m2048": {"us_per_call": round(ev2_ms * 1e3, 3),
                                "TOPS": round(2.0 * half * N * K / (ev2_ms * 1e-3) / 1e12, 1),
@@ -622,10 +741,11 @@ def bench_gemm_f16_small(hx, iters: int = 200):
     c = torch.empty((256, 256), dtype=torch.float16, device=dev)
     call = lambda: hx.matmul(a, b, b_layout="nk", out=c)  # noqa: E731
     call()
-    ev_ms, _ = event_timed([call], iters)
+    tm = event_timed([call], iters)
+    ev_ms = tm[0]
     tf = 2 * 256 ** 3 / (ev_ms * 1e-3) / 1e12
     return {"workload": "fp16 GEMM 256^3 (configs[0], latency-bound plumbing case)",
-            "value": round(ev_ms * 1e3, 3), "unit": "us", "tflops": round(tf, 2),
+            "value": round(ev_ms * 1e3, 3), "unit": "us", "tflops": round(tf, 2), "spread": tm.spread(),
             "roofline": roofline("mfma", tf, PEAK_F16_TFLOPS, "TFLOP/s")}
 
 
@@ -655,10 +775,11 @@ def bench_reference_shapes(hx, iters: int = 200):
         call()
         hx.manifest_enable(False)
         plan = hx.manifest()["records"]
-        ev_ms, fed = event_timed([call], iters)
+        tm = event_timed([call], iters)
+        ev_ms, fed = tm
         tf = 2.0 * M * N * K / (ev_ms * 1e-3) / 1e12
         res.append({"workload": f"fp16 matmul {M}x{N}x{K} (the reference's published shape)",
-                    "value": round(ev_ms * 1e3, 3), "unit": "us", "tflops": round(tf, 3),
+                    "value": round(ev_ms * 1e3, 3), "unit": "us", "tflops": round(tf, 3), "spread": tm.spread(),
                     "roofline": roofline("mfma", tf, PEAK_F16_TFLOPS, "TFLOP/s"),
                     "kernel": f"{plan[0]['plan']}:{plan[0]['config']}" if plan else None,
                     "reference_published_us": REF_PUBLISHED_US[(M, N, K)],
@@ -692,7 +813,8 @@ def bench_f16_decode(hx, iters: int = 300):
             calls[0]()
             hx.manifest_enable(False)
             plan = hx.manifest()["records"]
-            ev_ms, fed = event_timed(calls, iters)
+            tm = event_timed(calls, iters)
+            ev_ms, fed = tm
             t_ms, _ = event_timed([(lambda w=w, y=y: torch.matmul(x, w.t(), out=y)) for w, y in zip(wts, ys)], iters)
         finally:
             for w in rws:
@@ -701,7 +823,7 @@ def bench_f16_decode(hx, iters: int = 300):
         gbs = alg / (ev_ms * 1e-3) / 1e9
         res.append({"workload": f"fp16 decode {M}x{N}x{K}, registered weight (the reference tuner's decode shape)",
                     "value": round(gbs, 1), "unit": "GB/s", "us_per_call": round(ev_ms * 1e3, 2),
-                    "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s"),
+                    "spread": tm.spread(), "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s"),
                     "kernel": f"{plan[0]['plan']}:{plan[0]['config']}" if plan else None,
                     "traffic": traffic_of(f"f16_decode_{M}x{N}x{K}:gemv_{plan[0]['config']}") if plan else None,
                     "torch_us_same_weights": round(t_ms * 1e3, 2), "weight_copies": copies, "queue_fed": fed})
@@ -732,13 +854,22 @@ def bench_ffn(hx, iters: int = 20, tune_on: bool = True, tune_fn=tune):
         if tune_on:
             # gate/up stage (fused SwiGLU epilogue), then the down projection
             tuned = {"swiglu": tune_fn(hx, 5, T, I, H), "down": tune_fn(hx, 4, T, H, I)}
-        ev_ms, _ = event_timed([call], iters)
+        tm = event_timed([call], iters)
+        ev_ms = tm[0]
+        clk = clock_during(hx, [call], iters)
+        hx.manifest_clear()
+        hx.manifest_enable(True)
+        call()
+        hx.manifest_enable(False)
+        plan = [{k: r[k] for k in ("m", "n", "k", "plan", "config", "config_source")}
+                for r in hx.manifest()["records"]]
     finally:
         Wg.release(); Wu.release(); Wd.release()
     flops = 3 * 2.0 * T * H * I
     tf = flops / (ev_ms * 1e-3) / 1e12
     return {"workload": f"SwiGLU FFN tokens={T} hidden={H} inter={I}, int8 weights",
             "value": round(tf, 1), "unit": "TFLOP/s", "us_per_call": round(ev_ms * 1e3, 1),
+            "spread": tm.spread(), "clock": clk, "plan": plan,
             "roofline": roofline("mfma", tf, PEAK_F16_TFLOPS, "TFLOP/s"), "tune": tuned}
 
 
@@ -758,11 +889,13 @@ def bench_attention(hx, iters: int = 20):
         o = torch.empty_like(q)
         call = lambda: hx.attention(q, k, v, scale=scale, causal=causal, out=o)  # noqa: E731
         call()
-        ev_ms, fed = event_timed([call], iters)
+        tm = event_timed([call], iters)
+        ev_ms, fed = tm
         fl = 4.0 * Z * H * N * N * D * (0.5 if causal else 1.0)
         tf = fl / (ev_ms * 1e-3) / 1e12
         out.append({"workload": f"attention Z={Z} H={H} N={N} D={D}{' causal' if causal else ''} fp16",
                     "value": round(tf, 1), "unit": "TFLOP/s", "us_per_call": round(ev_ms * 1e3, 2),
+                    "spread": tm.spread(),
                     "roofline": roofline("mfma", tf, PEAK_F16_TFLOPS, "TFLOP/s"), "queue_fed": fed})
     return out
 
@@ -1283,7 +1416,7 @@ def main() -> int:
         import oracle
         march = oracle.use_native_build()
         log(f"[bench] CPU baseline (oracle port, -march=native = {march})")
-        cpu = cpu_baseline_gemm_i8(h["inputs"], march)
+        cpu = cpu_baseline_gemm_i8(h["inputs"], march, gpu_out=h["output"])
         log(f"[bench] CPU: {cpu['value']} TOPS on {cpu['cores']} threads")
         if secondary:
             sec_cpu = cpu_baselines_secondary(march)
@@ -1295,6 +1428,9 @@ def main() -> int:
             keys.update({f"fp16 matmul {M}x{N}x{K} ": f"ref_{M}x{N}x{K}" for (M, N, K) in REF_SHAPES})
             keys.update({f"fp16 decode {M}x{N}x{K},": f"dec_{M}x{N}x{K}" for (M, N, K) in ((1, 8192, 8192),
                                                                                        (1, 4096, 16384))})
+            keys.update({"attention Z=1 H=1 N=1024 D=64 fp16": "attn_ref",
+                         "attention Z=4 H=16 N=2048 D=128 fp16": "attn_mh",
+                         "attention Z=4 H=16 N=2048 D=128 causal fp16": "attn_mh_causal"})
             for sec in secondary:
                 for prefix, key in keys.items():
                     if sec["workload"].startswith(prefix):
@@ -1327,8 +1463,12 @@ def main() -> int:
                          "per launch, one HIP event pair around the K back-to-back steps on the "
                          "launch stream",
         "kernel_us": round(h["kernel_ms"] * 1e3, 3),
+        "spread": dict(h["spread"].spread(), note="7 more timed regions of the same launches after the "
+                                                  "timed steps; the figure is the steps' own region"),
+        "clock": h["clock"],
         "queue_fed": h["queue_fed"],
-        "parity": {"int8_sampled_rows_bitexact": h["parity_sampled_rows_bitexact"]},
+        "parity": {"int8_sampled_rows_bitexact": h["parity_sampled_rows_bitexact"],
+                   "all_elements_bitexact": (cpu or {}).get("gpu_output_bitexact_all_elements")},
         "tune": h["tune"],
         "plan": h["plan"],
         "cpu_baseline": cpu,

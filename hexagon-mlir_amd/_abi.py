@@ -126,6 +126,9 @@ SIGNATURES = {
     "hx_manifest_enable": ([_i], _i),
     "hx_manifest_clear": ([], _i),
     "hx_manifest_json": ([ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)], _i),
+    "hx_clock_probe": ([_i], _i),
+    "hx_clock_read": ([ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
+                       ctypes.POINTER(ctypes.c_longlong)], _i),
 }
 
 _lib = None

@@ -341,6 +341,54 @@ static void note_plan(const PlanCtx& ctx, int64_t m, int64_t n, int64_t k, int c
 
 extern "C" int hx_manifest_enable(int on) { return g_manifest_on.exchange(on ? 1 : 0); }
 
+// ---------------------------------------------------------------------------
+// Clock probe: three 64-bit counters per device (cycles, ticks, workgroups)
+// that the tiled GEMM kernels add to while the probe is on.
+// ---------------------------------------------------------------------------
+static std::map<int, unsigned long long*> g_clk_buf;
+
+extern "C" int hx_clock_probe(int enable) {
+  int dev, rc;
+  if ((rc = current_device(&dev))) return rc;
+  std::lock_guard<std::mutex> lk(g_mu);
+  unsigned long long*& buf = g_clk_buf[dev];
+  if (!enable) {
+    gemm_clock_target(dev, nullptr);
+    return HX_OK;
+  }
+  if (!buf && hipMalloc(reinterpret_cast<void**>(&buf), 4 * sizeof(unsigned long long)) != hipSuccess) {
+    buf = nullptr;
+    return fail(HX_ERR_NOMEM, "hx_clock_probe: counters");
+  }
+  HX_HIP_TRY(hipDeviceSynchronize());
+  HX_HIP_TRY(hipMemset(buf, 0, 4 * sizeof(unsigned long long)));
+  HX_HIP_TRY(hipDeviceSynchronize());
+  gemm_clock_target(dev, buf);
+  return HX_OK;
+}
+
+extern "C" int hx_clock_read(double* mhz, double* workgroup_us, long long* workgroups) {
+  int dev, rc;
+  if ((rc = current_device(&dev))) return rc;
+  unsigned long long* buf;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_clk_buf.find(dev);
+    if (it == g_clk_buf.end() || !it->second) return fail(HX_ERR_ARG, "hx_clock_read: the probe was never enabled");
+    buf = it->second;
+  }
+  unsigned long long h[3] = {0, 0, 0};
+  HX_HIP_TRY(hipDeviceSynchronize());
+  HX_HIP_TRY(hipMemcpy(h, buf, sizeof(h), hipMemcpyDeviceToHost));
+  int khz = 0;
+  HX_HIP_TRY(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
+  const double us = khz > 0 ? (double)h[1] / ((double)khz * 1e-3) : 0.0;  // ticks / (ticks per us)
+  if (mhz) *mhz = us > 0 ? (double)h[0] / us : 0.0;
+  if (workgroup_us) *workgroup_us = us;
+  if (workgroups) *workgroups = (long long)h[2];
+  return HX_OK;
+}
+
 extern "C" int hx_manifest_clear(void) {
   std::lock_guard<std::mutex> lk(g_manifest_mu);
   g_manifest.clear();
@@ -583,14 +631,19 @@ static int run_gemm(int op, GemmArgs& a, hipStream_t s, const PlanCtx& ctx,
       note_plan(ctx, a.M, a.N, a.K, a.out_dtype, "mfma-tiled", gemm_config(mode, cfg)->name,
                 pin ? "pinned" : "default", "selected-aligned");
       if (const size_t pb = gemm_part_bytes(mode, cfg, a)) {
+        // K split: partials, and the per-tile counters that let the last
+        // part of each tile merge inside the kernel (the stream's split
+        // counters, shared with the decode GEMV's split: kernels on one
+        // stream run one at a time and leave them at zero)
         if (pt.fixed) {
           if (pb > pt.cap)
             return fail(HX_ERR_UNSUPPORTED, "%s: config %s needs %zu bytes of K-split partials, %zu reserved",
                         ctx.entry, gemm_config(mode, cfg)->name, pb, pt.cap);
           a.part = pt.buf;
+          a.cnt = pt.cnt;
         } else {
-          int rc = part_get(s, pb, &a.part);
-          if (rc) return rc;
+          int rc = gemv_split_buffers(s, pb, &a.part, &a.cnt);
+          if (rc) return map_internal(rc, "gemm split-K buffers");
         }
       }
       return map_internal(launch_gemm(mode, cfg, a, s), "gemm");

@@ -192,6 +192,10 @@ __device__ __forceinline__ v4f mfma16_f16(v8h a, v8h b, v4f c) {
 // the end-of-kernel write-back: SC0 | SC1 (system-scope coherent, i.e.
 // written through to memory).
 constexpr int kStoreWriteThrough = 1 | 16;
+// SC1 alone: the cache policy of an agent-scope atomic access on gfx942 /
+// gfx950 (stores written through the XCD's L2, loads not served by a stale
+// line of it).  Used for data one workgroup hands to another through memory.
+constexpr int kAgentCoherent = 16;
 
 // ---- direct-to-LDS staging (GEMM and attention) -------------------------
 typedef __attribute__((address_space(3))) void* lds_ptr_t;

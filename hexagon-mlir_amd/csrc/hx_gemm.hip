@@ -4,6 +4,9 @@
 // tables are in hx_gemm_{i8,f16,bf16,w8}.hip.
 #include "hx_gemm_kernel.hpp"
 
+#include <algorithm>
+#include <atomic>
+
 namespace hx {
 
 // ---------------------------------------------------------------------------
@@ -119,6 +122,7 @@ const GemmConfig* gemm_config(int mode, int idx) {
   return &t[idx].cfg;
 }
 
+int gemm_num_cus();
 static int g_num_cus = 0;
 static int num_cus() {
   if (g_num_cus == 0) {
@@ -130,6 +134,24 @@ static int num_cus() {
       g_num_cus = 256;
   }
   return g_num_cus;
+}
+int gemm_num_cus() { return num_cus(); }
+
+// The clock hook's per-device counters (null: off).
+static unsigned long long* g_clk[64];
+static std::atomic<int> g_clk_on{0};
+void gemm_clock_target(int dev, unsigned long long* clk) {
+  if (dev < 0 || dev >= 64) return;
+  g_clk[dev] = clk;
+  int on = 0;
+  for (int d = 0; d < 64; ++d) on |= g_clk[d] != nullptr;
+  g_clk_on.store(on, std::memory_order_release);
+}
+static unsigned long long* clock_target() {
+  if (!g_clk_on.load(std::memory_order_acquire)) return nullptr;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  return g_clk[dev];
 }
 
 // Untuned choice: estimated time = rounds * occ * tile_area / rate, where a
@@ -341,13 +363,24 @@ static int64_t split_k_elems(int mode, const GemmConfig& c, const GemmArgs& a) {
   return (per + bke - 1) / bke * bke;
 }
 
+// Partials of a split launch: [parts][M][N] for the merge kernel, or
+// [parts][tiles][BM*BN] for the merge inside the kernel; the larger of the
+// two (they differ on edge tiles), binary32 or int32.
 size_t gemm_part_bytes(int mode, int cfg_idx, const GemmArgs& a) {
   int n;
   const GemmEntry* t = table(mode, n);
   if (!t || cfg_idx < 0 || cfg_idx >= n || t[cfg_idx].cfg.ksplit <= 1) return 0;
-  const int64_t ks = split_k_elems(mode, t[cfg_idx].cfg, a);
+  const GemmConfig& c = t[cfg_idx].cfg;
+  const int64_t ks = split_k_elems(mode, c, a);
   const int64_t parts = (a.K + ks - 1) / ks;
-  return (size_t)parts * (size_t)(a.M * a.N) * sizeof(float);  // binary32 or int32 partials
+  const int64_t tiles = ((a.M + c.bm - 1) / c.bm) * ((a.N + c.bn - 1) / c.bn);
+  const int64_t per = std::max<int64_t>(a.M * a.N, tiles * c.bm * c.bn);
+  return (size_t)parts * (size_t)per * sizeof(float);
+}
+
+int64_t gemm_tiles(int mode, int cfg_idx, const GemmArgs& a) {
+  const GemmConfig* c = gemm_config(mode, cfg_idx);
+  return c ? ((a.M + c->bm - 1) / c->bm) * ((a.N + c->bn - 1) / c->bn) : 0;
 }
 
 int launch_gemm(int mode, int cfg_idx, const GemmArgs& a, hipStream_t s) {
@@ -360,13 +393,27 @@ int launch_gemm(int mode, int cfg_idx, const GemmArgs& a, hipStream_t s) {
   if (c.ksplit <= 1) {
     GemmArgs q = a;
     q.k_split = 0;
+    q.cnt = nullptr;
+    q.clk = clock_target();
     t[cfg_idx].fn(q, s);
     return HXI_OK;
   }
-  // K split: binary32 (int8: int32) partials into a.part, then the merge
-  // applies the epilogue (scales, residual, rounding)
   if (a.b2 || !a.part || (mode != GM_I8 && a.row_scale)) return HXI_ERR_ARG;
+  // K split with counters: the parts of each tile hand their partials to
+  // the last of them, which applies the epilogue -- one launch (B as
+  // [N][K]; a [K][N] B takes the merge kernel)
+  if (a.cnt && !a.b_kn && tiles <= kGemvSplitCounters) {
+    GemmArgs q = a;
+    q.k_split = split_k_elems(mode, c, a);
+    q.clk = clock_target();
+    t[cfg_idx].fn(q, s);
+    return HXI_OK;
+  }
+  // K split without counters: binary32 (int8: int32) partials into a.part,
+  // then a merge kernel applies the epilogue (scales, residual, rounding)
   GemmArgs q = a;
+  q.cnt = nullptr;
+  q.clk = clock_target();
   q.k_split = split_k_elems(mode, c, a);
   q.c = a.part;
   q.ldc = a.N;

@@ -11,10 +11,10 @@ const GemmEntry* gemm_table_f16(int& n) {
       HX_GEMM_CFGS(GM_F16),
       // K in two parts (binary32 partials and a merge): fills the chip when
       // the 256x256 tiles of a long-K product are fewer than the CUs
-      {{256, 256, 2, 4, GE_STORE, "256x256_w2x4_k2", 1, 1.00f, 2}, &launch_one<GM_F16, 256, 256, 2, 4, GE_STORE>},
+      {{256, 256, 2, 4, GE_STORE, "256x256_w2x4_k2", 1, 1.00f, 2}, &launch_one<GM_F16, 256, 256, 2, 4, GE_STORE, 128, 2, 1, false, true>},
       // small tiles with K in parts: more workgroups per CU for skinny M
-      {{128, 128, 2, 2, GE_STORE, "128x128_w2x2_k2", 2, 0.89f, 2}, &launch_one<GM_F16, 128, 128, 2, 2, GE_STORE>},
-      {{64, 64, 2, 2, GE_STORE, "64x64_w2x2_k4", 4, 0.61f, 4}, &launch_one<GM_F16, 64, 64, 2, 2, GE_STORE>},
+      {{128, 128, 2, 2, GE_STORE, "128x128_w2x2_k2", 2, 0.89f, 2}, &launch_one<GM_F16, 128, 128, 2, 2, GE_STORE, 128, 2, 1, false, true>},
+      {{64, 64, 2, 2, GE_STORE, "64x64_w2x2_k4", 4, 0.61f, 4}, &launch_one<GM_F16, 64, 64, 2, 2, GE_STORE, 128, 2, 1, false, true>},
       // K stage width and depth (a 128-byte stage is 64 k): 256-byte stages
       // halve the barriers per K of a deep product; three 64-byte stages
       // keep two stages of loads in flight

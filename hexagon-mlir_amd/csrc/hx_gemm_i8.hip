@@ -24,11 +24,19 @@ const GemmEntry* gemm_table_i8(int& n) {
        &launch_one<GM_I8, 128, 128, 2, 2, GE_STORE, 256, 2>},
       {{64, 64, 2, 2, GE_STORE, "64x64_w2x2_bk256", 2, 0.51f, 0, 256, 2},
        &launch_one<GM_I8, 64, 64, 2, 2, GE_STORE, 256, 2>},
+      // persistent (one workgroup per CU walking consecutive M-tiles of a B
+      // strip, each tile's epilogue overlapping the next tile's first K
+      // stages): 64-byte stages leave LDS room for the epilogue's own
+      // staging region
+      {{256, 256, 2, 4, GE_STORE, "256x256_w2x4_bk64_p", 1, 0.80f, 0, 64, 2, 1},
+       &launch_one<GM_I8, 256, 256, 2, 4, GE_STORE, 64, 2, 1, true>},
+      {{128, 256, 2, 4, GE_STORE, "128x256_w2x4_p", 1, 0.75f, 0, 128, 2, 1},
+       &launch_one<GM_I8, 128, 256, 2, 4, GE_STORE, 128, 2, 1, true>},
       // K in parts (int32 partials, exact, and a merge that dequantises):
       // fills the chip when the output tiles are fewer than the CUs
-      {{256, 256, 2, 4, GE_STORE, "256x256_w2x4_k2", 1, 1.00f, 2}, &launch_one<GM_I8, 256, 256, 2, 4, GE_STORE>},
-      {{128, 128, 2, 2, GE_STORE, "128x128_w2x2_k2", 2, 0.89f, 2}, &launch_one<GM_I8, 128, 128, 2, 2, GE_STORE>},
-      {{64, 64, 2, 2, GE_STORE, "64x64_w2x2_k4", 4, 0.61f, 4}, &launch_one<GM_I8, 64, 64, 2, 2, GE_STORE>},
+      {{256, 256, 2, 4, GE_STORE, "256x256_w2x4_k2", 1, 1.00f, 2}, &launch_one<GM_I8, 256, 256, 2, 4, GE_STORE, 128, 2, 1, false, true>},
+      {{128, 128, 2, 2, GE_STORE, "128x128_w2x2_k2", 2, 0.89f, 2}, &launch_one<GM_I8, 128, 128, 2, 2, GE_STORE, 128, 2, 1, false, true>},
+      {{64, 64, 2, 2, GE_STORE, "64x64_w2x2_k4", 4, 0.61f, 4}, &launch_one<GM_I8, 64, 64, 2, 2, GE_STORE, 128, 2, 1, false, true>},
   };
   n = (int)(sizeof(t) / sizeof(t[0]));
   return t;

@@ -166,8 +166,19 @@ __device__ __forceinline__ void interleave_reads_mfma_vmem() {
 // l = 16G + i, addressing row 32ks + 16(G/2) + 8h + i/2 at column
 // 16(G%2) + 8(i%2) of its 32-column sub-tile, receives column l % 32 at
 // k = 32ks + 16(l/32) + 8h + (0..7).
+//
+// PERSIST: one workgroup per CU walks a run of consecutive M-tiles of one B
+// strip (the weight strip stays hot while its M-tiles go by) and overlaps
+// each tile's epilogue with the next tile's first K stages: after the last
+// K stage the next tile's stage loads are issued first, then the finished
+// tile is converted and stored through a staging region of its own, so its
+// stores drain while the next tile's loads land and its first MFMAs run.
+// Interior shapes only (no EDGE), B as [N][K], 16-bit outputs.
+//
+// SPLITM: the K split's parts merge inside the kernel (p.cnt, p.part) -- a
+// compile-time variant, so the other kernels carry none of its code.
 template <int MODE, int BM, int BN, int WM, int WN, int EPI, int SB = 128, int MINW = 1, bool EDGE = false,
-          bool BKN = false, int STAGES = 2>
+          bool BKN = false, int STAGES = 2, bool PERSIST = false, bool SPLITM = false>
 __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(MINW, 8)))
 gemm_kernel(GemmArgs p) {
   typedef ModeTraits<MODE> T;
@@ -198,66 +209,122 @@ gemm_kernel(GemmArgs p) {
   // per-row / per-column scales of this tile, fetched in the prologue
   // (SC_ROWS floats each: one 1 KiB direct load covers 256)
   constexpr int SC_ROWS = (BM > BN ? BM : BN) < 256 ? 256 : (BM > BN ? BM : BN);
-  static_assert(STAGES * STAGE + (1 + NB) * SC_ROWS * 4 <= 160 * 1024, "LDS budget");
+  // PERSIST: the scales of two tiles (the finished one's epilogue reads its
+  // set while the next tile's set is loading) and a staging region of 32
+  // rows x WTN 16-bit outputs per wave, apart from the stage buffers
+  constexpr int SC_SETS = PERSIST ? 2 : 1;
+  constexpr int STG_WAVE = 32 * WTN * 2;
+  constexpr int STG = PERSIST ? NW * STG_WAVE : 16;
+  static_assert(!PERSIST || (!EDGE && !BKN), "persistent: interior shapes, B as [N][K]");
+  static_assert(!(PERSIST && SPLITM), "persistent configs do not split K");
+  static_assert(STAGES * STAGE + SC_SETS * (1 + NB) * SC_ROWS * 4 + (PERSIST ? STG : 0) <= 160 * 1024,
+                "LDS budget");
   static_assert(STAGES * P < 64, "vmcnt range");
 
   // The stages as distinct arrays: the compiler can then see that a direct
   // load into one stage never aliases the reads of another.
   __shared__ __attribute__((aligned(1024))) char st0[STAGE];
-  __shared__ __attribute__((aligned(1024))) float scl[(1 + NB) * SC_ROWS];
+  __shared__ __attribute__((aligned(1024))) float scl_all[SC_SETS * (1 + NB) * SC_ROWS];
   __shared__ __attribute__((aligned(1024))) char st1[STAGE];
   __shared__ __attribute__((aligned(1024))) char st2[STAGES == 3 ? STAGE : 16];
+  __shared__ __attribute__((aligned(1024))) char stg[STG];
+  __shared__ int is_last_part;
 
-  // K split: workgroup row blockIdx.y sums k in [y k_split, (y+1) k_split)
-  // into the binary32 slice y of c (launch_gemm merges the slices)
+  // measurement hook: this workgroup's shader-clock cycles and
+  // constant-rate ticks, added to p.clk when it ends
+  uint64_t clk_c0 = 0, clk_r0 = 0;
+  if (p.clk) {
+    clk_c0 = __builtin_amdgcn_s_memtime();
+    clk_r0 = __builtin_amdgcn_s_memrealtime();
+  }
+  auto clock_out = [&]() __attribute__((always_inline)) {
+    if (p.clk && threadIdx.x == 0) {
+      const uint64_t c1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+      atomicAdd(p.clk, (unsigned long long)(c1 - clk_c0));
+      atomicAdd(p.clk + 1, (unsigned long long)(r1 - clk_r0));
+      atomicAdd(p.clk + 2, 1ull);
+    }
+  };
+
+  // K split: workgroup row blockIdx.y sums k in [y k_split, (y+1) k_split).
+  // With counters (merge_in) the parts of a tile hand their partials to the
+  // last of them to finish, which runs the epilogue; without, part y writes
+  // the binary32 slice y of c and launch_gemm merges the slices.
+  constexpr bool merge_in = SPLITM;
   if (gridDim.y > 1) {
     const int64_t k0 = (int64_t)blockIdx.y * p.k_split;
     p.a = reinterpret_cast<const char*>(p.a) + k0 * T::EA;
     p.b = reinterpret_cast<const char*>(p.b) + k0 * (BKN ? p.ldb : 1) * T::EB;
     p.K = min(p.k_split, p.K - k0);
-    p.c = reinterpret_cast<char*>(p.c) + (int64_t)blockIdx.y * p.M * p.ldc * 4;
+    if (!merge_in) p.c = reinterpret_cast<char*>(p.c) + (int64_t)blockIdx.y * p.M * p.ldc * 4;
   }
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
+  // lane and wave: a persistent workgroup passes them through an empty asm
+  // at the start of every tile, so what derives from them is recomputed per
+  // tile instead of being held across the K loop
+  int lane = tid & 63;
   // wave index as a provably uniform (scalar) value: the direct-load LDS
   // address and scalar offset derive from it and must live in SGPRs
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave / WN, wn = wave % WN;
+  int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int tiles_m = (int)((p.M + BM - 1) / BM);
   const int tiles_n = (int)((p.N + BN - 1) / BN);
-  int tm, tn;
-  tile_of(tiles_m, tiles_n, tm, tn);
-  // The tile coordinates are workgroup-uniform, but the integer divisions in
-  // tile_of run on the vector ALU; readfirstlane states the uniformity, so
-  // the buffer descriptors built from them stay scalar (a descriptor the
-  // compiler believes divergent turns every buffer load into a loop over
-  // lanes).
-  tm = __builtin_amdgcn_readfirstlane(tm);
-  tn = __builtin_amdgcn_readfirstlane(tn);
-  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-  const int64_t rows_a = min((int64_t)BM, p.M - m0);
-  const int64_t rows_b = min((int64_t)BN, p.N - n0);
   const uint32_t lda_b = (uint32_t)(p.lda * T::EA);
   const uint32_t ldb_b = (uint32_t)(p.ldb * T::EB);
   const uint32_t ka_bytes = (uint32_t)(p.K * T::EA);
 
-  __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(reinterpret_cast<const char*>(p.a) + m0 * lda_b), 0, (int)(rows_a * lda_b), 0x00020000);
+  // Per-tile state: coordinates, rows in range, buffer descriptors.
+  int tm = 0, tn = 0;
+  int64_t m0 = 0, n0 = 0, rows_a = 0, rows_b = 0;
+  __amdgpu_buffer_rsrc_t ra;
   __amdgpu_buffer_rsrc_t rb[NB];
-  if constexpr (BKN) {
-    // columns n0.. of every row of k, up to the matrix's last element
-    rb[0] = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(reinterpret_cast<const char*>(p.b) + n0 * T::EB), 0,
-        (int)(((p.K - 1) * p.ldb + (p.N - n0)) * T::EB), 0x00020000);
+  auto set_tile = [&](int tm_, int tn_) __attribute__((always_inline)) {
+    // The tile coordinates are workgroup-uniform, but integer divisions run
+    // on the vector ALU; readfirstlane states the uniformity, so the buffer
+    // descriptors built from them stay scalar (a descriptor the compiler
+    // believes divergent turns every buffer load into a loop over lanes).
+    tm = __builtin_amdgcn_readfirstlane(tm_);
+    tn = __builtin_amdgcn_readfirstlane(tn_);
+    m0 = (int64_t)tm * BM;
+    n0 = (int64_t)tn * BN;
+    rows_a = min((int64_t)BM, p.M - m0);
+    rows_b = min((int64_t)BN, p.N - n0);
+    ra = __builtin_amdgcn_make_buffer_rsrc((void*)(reinterpret_cast<const char*>(p.a) + m0 * lda_b), 0,
+                                           (int)(rows_a * lda_b), 0x00020000);
+    if constexpr (BKN) {
+      // columns n0.. of every row of k, up to the matrix's last element
+      rb[0] = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(reinterpret_cast<const char*>(p.b) + n0 * T::EB), 0,
+          (int)(((p.K - 1) * p.ldb + (p.N - n0)) * T::EB), 0x00020000);
+    } else {
+      rb[0] = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(reinterpret_cast<const char*>(p.b) + n0 * ldb_b), 0, (int)(rows_b * ldb_b), 0x00020000);
+    }
+    if constexpr (NB == 2)
+      rb[1] = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(reinterpret_cast<const char*>(p.b2) + n0 * ldb_b), 0, (int)(rows_b * ldb_b),
+          0x00020000);
+  };
+  // PERSIST: this workgroup's run of tiles.  Tiles are numbered strip-major
+  // (t = tn * tiles_m + tm: consecutive numbers are consecutive M-tiles of
+  // one B strip) and cut into gridDim.x runs whose lengths differ by at
+  // most one; workgroup b runs on XCD b % 8, so the runs are renumbered to
+  // give each XCD a contiguous range of strips.
+  int t_cur = 0, t_end = 0;
+  if constexpr (PERSIST) {
+    const int ntiles = tiles_m * tiles_n;
+    const int G = gridDim.x;
+    int w = blockIdx.x;
+    if ((G & 7) == 0) w = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
+    t_cur = __builtin_amdgcn_readfirstlane((int)((int64_t)w * ntiles / G));
+    t_end = __builtin_amdgcn_readfirstlane((int)((int64_t)(w + 1) * ntiles / G));
+    set_tile(t_cur % tiles_m, t_cur / tiles_m);
   } else {
-    rb[0] = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(reinterpret_cast<const char*>(p.b) + n0 * ldb_b), 0, (int)(rows_b * ldb_b), 0x00020000);
+    int tm_, tn_;
+    tile_of(tiles_m, tiles_n, tm_, tn_);
+    set_tile(tm_, tn_);
   }
-  if constexpr (NB == 2)
-    rb[1] = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(reinterpret_cast<const char*>(p.b2) + n0 * ldb_b), 0, (int)(rows_b * ldb_b),
-        0x00020000);
+  int wm = wave / WN, wn = wave % WN;
 
   // Direct-load addressing.  Lane L of a 1 KiB block fills physical chunk
   // L % cpr of block row L / cpr (cpr = 16-byte chunks per row) and fetches
@@ -265,16 +332,12 @@ gemm_kernel(GemmArgs p) {
   // a wave-uniform offset (the instruction's scalar offset); the lane part
   // is a row offset plus the swizzled chunk, recomputed per block from the
   // block index rather than kept in registers.
-  const uint32_t a_lane_row = (uint32_t)(lane / A_CPR) * lda_b;
-  const uint32_t b_lane_row = (uint32_t)(lane / B_CPR) * ldb_b;
   // EDGE (M or N not a multiple of the tile): lanes whose row lies past the
   // tile's last row get an out-of-range vector offset.  The block's row
   // offset travels in the scalar offset, and the zero fill must not depend
   // on whether the range check includes it.  Block blk's lane row is past
   // the edge when blk * RPB >= lim.  Interior shapes skip the test (it costs
   // ~1% at 4096^3).
-  const int a_lim = (int)rows_a - lane / A_CPR;
-  const int b_lim = (int)rows_b - lane / B_CPR;
   constexpr int BKE = SB / T::EA;  // elements of K per stage
   // BKN stage layout: BKE rows of k, KROWB bytes each, 64-byte segments
   // XOR-swizzled so that the 8 rows one transposing read touches (4 + 4,
@@ -299,8 +362,12 @@ gemm_kernel(GemmArgs p) {
   // Enqueue the direct loads of K-stage kt into `st`.  Only the last stage
   // can overhang K; its chunks past K read as zero (offset out of range).
   // MASK = false is for stages known not to be the last one.
-  auto dma_stage = [&](char* st, int kt, auto maskc) {
+  auto dma_stage = [&](char* st, int kt, auto maskc) __attribute__((always_inline)) {
     constexpr bool MASK = decltype(maskc)::value;
+    const uint32_t a_lane_row = (uint32_t)(lane / A_CPR) * lda_b;
+    const uint32_t b_lane_row = (uint32_t)(lane / B_CPR) * ldb_b;
+    const int a_lim = (int)rows_a - lane / A_CPR;
+    const int b_lim = (int)rows_b - lane / B_CPR;
     const uint32_t ka = (uint32_t)kt * (uint32_t)SB;
     const uint32_t kb = (uint32_t)kt * (uint32_t)BROW;
     const bool tail = MASK && ka + (uint32_t)SB > ka_bytes;
@@ -366,7 +433,7 @@ gemm_kernel(GemmArgs p) {
     });
   });
 
-  const int lrow = lane & 31, lg = lane >> 5;
+  int lrow = lane & 31, lg = lane >> 5;
 
   // Operand fragments, double-buffered in registers: while the MFMAs of
   // k-step ks run, the LDS reads of step ks+1 are in flight.  A stage is
@@ -376,7 +443,7 @@ gemm_kernel(GemmArgs p) {
   v4i fa[2][TM];
   v4i fb[2][NB][TN];
 
-  auto read_frags = [&](const char* sa, auto ksc) {
+  auto read_frags = [&](const char* sa, auto ksc) __attribute__((always_inline)) {
     constexpr int ks = decltype(ksc)::value;
     constexpr int s = ks & 1;
     typedef short v4s_t __attribute__((ext_vector_type(4)));
@@ -448,7 +515,7 @@ gemm_kernel(GemmArgs p) {
   // The MFMAs of one k-step.  B is the first operand, so the accumulators
   // hold C transposed: lane (lrow, lg) of sub-tile (i, j) holds row lrow and
   // the four consecutive columns 8*g + 4*lg + (0..3) in registers 4g..4g+3.
-  auto mfmas = [&](auto ksc) {
+  auto mfmas = [&](auto ksc) __attribute__((always_inline)) {
     constexpr int ks = decltype(ksc)::value;
     constexpr int s = ks & 1;
     static_for<NB>([&](auto nbc) {
@@ -481,7 +548,7 @@ gemm_kernel(GemmArgs p) {
   // barrier with an empty queue.  LAST: no next stage.  WAITN: direct loads
   // (per wave) that may still be in flight at the barrier -- those of the
   // stages after the next one.
-  auto stage_body = [&](char* cur, char* nxt, int kt, auto dmac, auto lastc, auto waitc) {
+  auto stage_body = [&](char* cur, char* nxt, int kt, auto dmac, auto lastc, auto waitc) __attribute__((always_inline)) {
     constexpr int DMA = decltype(dmac)::value;
     constexpr bool LAST = decltype(lastc)::value;
     constexpr int WAITN = decltype(waitc)::value;
@@ -533,93 +600,198 @@ gemm_kernel(GemmArgs p) {
   // row scales, 1: column scales, 2: second column scales): issued first,
   // they are covered by the prologue's wait for stage 0.  A null scale
   // pointer gives an empty buffer range, so its slot reads as zeros.
-  {
+  float* scl = scl_all;  // the scale set of the tile being computed
+  auto dma_scales = [&](float* dst) __attribute__((always_inline)) {
     static_assert(NW >= 2 + NB - 1, "one wave per scale vector");
     auto sc_rsrc = [](const float* ptr, int64_t first, int64_t n) {
       return __builtin_amdgcn_make_buffer_rsrc((void*)(ptr ? ptr + first : nullptr), 0,
                                                ptr ? (int)((n - first) * 4) : 0, 0x00020000);
     };
     if (wave == 0)
-      dma16(sc_rsrc(MODE == GM_I8 ? p.row_scale : nullptr, m0, p.M), (char*)scl, lane * 16u, 0u);
-    if (wave == 1) dma16(sc_rsrc(p.col_scale, n0, p.N), (char*)(scl + SC_ROWS), lane * 16u, 0u);
+      dma16(sc_rsrc(MODE == GM_I8 ? p.row_scale : nullptr, m0, p.M), (char*)dst, lane * 16u, 0u);
+    if (wave == 1) dma16(sc_rsrc(p.col_scale, n0, p.N), (char*)(dst + SC_ROWS), lane * 16u, 0u);
     if constexpr (NB == 2)
-      if (wave == 2) dma16(sc_rsrc(p.col_scale2, n0, p.N), (char*)(scl + 2 * SC_ROWS), lane * 16u, 0u);
-  }
+      if (wave == 2) dma16(sc_rsrc(p.col_scale2, n0, p.N), (char*)(dst + 2 * SC_ROWS), lane * 16u, 0u);
+  };
   typedef std::integral_constant<int, 0> Wait0;
   typedef std::integral_constant<int, P> Wait1;  // one later stage's loads may be in flight
   typedef std::false_type More;
   auto first = [&](char* st) { read_frags(st, std::integral_constant<int, 0>{}); };
-  if constexpr (STAGES == 2) {
-    const bool odd = nk & 1;
-    if (odd) {
-      dma_stage(st1, 0, std::true_type{});
-      dma_stage(st0, 1, std::true_type{});
+  // The direct loads of the first STAGES stages of the current tile.
+  auto dma_prologue = [&]() __attribute__((always_inline)) {
+    if constexpr (STAGES == 2) {
+      if (nk & 1) {
+        dma_stage(st1, 0, std::true_type{});
+        dma_stage(st0, 1, std::true_type{});
+      } else {
+        dma_stage(st0, 0, std::true_type{});
+        dma_stage(st1, 1, std::true_type{});
+      }
     } else {
-      dma_stage(st0, 0, std::true_type{});
-      dma_stage(st1, 1, std::true_type{});
+      // Three-stage ring.  Stage kt lives in buffer (kt + 3 - nk3 % 3) % 3,
+      // so the final three stages are always (st0, st1, st2); the first
+      // nk3 % 3 stages are peeled.  Fewer than three stages of K run as
+      // three, the stages past K reading as zeros.
+      const int r = (nk < 3 ? 3 : nk) % 3;
+      if (r == 0) {
+        dma_stage(st0, 0, std::true_type{});
+        dma_stage(st1, 1, std::true_type{});
+        dma_stage(st2, 2, std::true_type{});
+      } else if (r == 1) {
+        dma_stage(st2, 0, std::true_type{});
+        dma_stage(st0, 1, std::true_type{});
+        dma_stage(st1, 2, std::true_type{});
+      } else {
+        dma_stage(st1, 0, std::true_type{});
+        dma_stage(st2, 1, std::true_type{});
+        dma_stage(st0, 2, std::true_type{});
+      }
     }
-    wait_vm<P>();
-    lds_barrier();
-    int kt = 0;
-    if (odd) {
-      first(st1);
-      stage_body(st1, st0, 0, LastDma{}, More{}, Wait0{});
-      kt = 1;
+  };
+  // The K loop over the prologue's stages and the rest.  EXTRA: memory
+  // operations this wave issued after the prologue's loads (a persistent
+  // workgroup's previous epilogue stores) that may still be in flight when
+  // stage 0 is waited for -- vmcnt retires in issue order.
+  auto k_loop = [&](auto extrac) __attribute__((always_inline)) {
+    constexpr int EXTRA = decltype(extrac)::value;
+    if constexpr (STAGES == 2) {
+      const bool odd = nk & 1;
+      wait_vm<P + EXTRA>();
+      lds_barrier();
+      int kt = 0;
+      if (odd) {
+        first(st1);
+        stage_body(st1, st0, 0, LastDma{}, More{}, Wait0{});
+        kt = 1;
+      } else {
+        first(st0);
+      }
+      // Steady state: straight-line pairs of stages (no conditional code, so
+      // the accumulators keep one register class across iterations).
+      for (; nk - kt > 2; kt += 2) {
+        stage_body(st0, st1, kt, LastDma{}, More{}, Wait0{});
+        stage_body(st1, st0, kt + 1, LastDma{}, More{}, Wait0{});
+      }
+      stage_body(st0, st1, kt, NoDma{}, More{}, Wait0{});
+      stage_body(st1, st0, kt + 1, NoDma{}, std::true_type{}, Wait0{});
     } else {
-      first(st0);
+      const int nk3 = nk < 3 ? 3 : nk;
+      const int r = nk3 % 3;
+      wait_vm<2 * P + EXTRA>();
+      lds_barrier();
+      int kt = 0;
+      if (r == 1) {
+        first(st2);
+        stage_body(st2, st0, 0, LastDma{}, More{}, Wait1{});
+        kt = 1;
+      } else if (r == 2) {
+        first(st1);
+        stage_body(st1, st2, 0, LastDma{}, More{}, Wait1{});
+        stage_body(st2, st0, 1, LastDma{}, More{}, Wait1{});
+        kt = 2;
+      } else {
+        first(st0);
+      }
+      for (; nk3 - kt > 3; kt += 3) {
+        stage_body(st0, st1, kt, LastDma{}, More{}, Wait1{});
+        stage_body(st1, st2, kt + 1, LastDma{}, More{}, Wait1{});
+        stage_body(st2, st0, kt + 2, LastDma{}, More{}, Wait1{});
+      }
+      stage_body(st0, st1, kt, NoDma{}, More{}, Wait1{});
+      stage_body(st1, st2, kt + 1, NoDma{}, More{}, Wait0{});
+      stage_body(st2, st0, kt + 2, NoDma{}, std::true_type{}, Wait0{});
     }
-    // Steady state: straight-line pairs of stages (no conditional code, so
-    // the accumulators keep one register class across iterations).
-    for (; nk - kt > 2; kt += 2) {
-      stage_body(st0, st1, kt, LastDma{}, More{}, Wait0{});
-      stage_body(st1, st0, kt + 1, LastDma{}, More{}, Wait0{});
+  };
+
+  // K split merged in the kernel: every part stores its partial tile (in
+  // register order: wave block, then (nb, i, j, g) 16-byte chunks of 64
+  // lanes, so each store instruction writes one contiguous KiB) with the
+  // agent-coherent policy, waits for the stores, and counts itself in on
+  // the tile's counter; the part that counts last resets the counter, reads
+  // every part's partial back (its own included) and adds them in part
+  // order from zero -- the order of the separate merge kernel, so the
+  // result is the same bit for bit -- then runs the epilogue.  The others
+  // end here.  The protocol is the split decode GEMV's (hx_gemv.hip), with
+  // the same gfx942 / gfx950 guarantees.  Returns false when this
+  // workgroup ends.
+  auto split_handoff = [&]() __attribute__((always_inline)) -> bool {
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__) && !defined(__gfx942__)
+#error "in-kernel K-split merge: the last-arriver protocol is written for gfx942 / gfx950 (vmcnt counts stores)"
+#endif
+    constexpr int CH = NB * TM * TN * 4;  // 16-byte chunks per lane
+    constexpr int TILE_BYTES = NB * BM * BN * 4;
+    const int parts = gridDim.y;
+    auto tile_rsrc = [&](int q) {
+      char* base = reinterpret_cast<char*>(p.part) + ((int64_t)q * gridDim.x + blockIdx.x) * TILE_BYTES;
+      return __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, TILE_BYTES, 0x00020000);
+    };
+    // the lane's 16 bytes in the vector offset, the wave's chunk (uniform)
+    // in the scalar offset
+    const uint32_t voff = (uint32_t)lane * 16u;
+    auto soff = [&](int c) -> uint32_t { return (uint32_t)((wave * CH + c) * 1024); };
+    {
+      const __amdgpu_buffer_rsrc_t mine = tile_rsrc(blockIdx.y);
+      static_for<NB>([&](auto nbc) {
+        static_for<TM>([&](auto ic) {
+          static_for<TN>([&](auto jc) {
+            static_for<4>([&](auto gc) {
+              constexpr int nb = decltype(nbc)::value, i = decltype(ic)::value, j = decltype(jc)::value,
+                            g = decltype(gc)::value;
+              constexpr int c = ((nb * TM + i) * TN + j) * 4 + g;
+              // the four components as one sub-vector, cast whole: hipcc
+              // compiles a bit cast of a single vector component as a cast
+              // of component 0
+              const Acc& v = acc[nb][i][j];
+              const v4i d = __builtin_bit_cast(v4i, __builtin_shufflevector(v, v, 4 * g, 4 * g + 1, 4 * g + 2,
+                                                                            4 * g + 3));
+              __builtin_amdgcn_raw_buffer_store_b128(d, mine, voff, soff(c), kAgentCoherent);
+            });
+          });
+        });
+      });
     }
-    stage_body(st0, st1, kt, NoDma{}, More{}, Wait0{});
-    stage_body(st1, st0, kt + 1, NoDma{}, std::true_type{}, Wait0{});
-  } else {
-    // Three-stage ring.  Stage kt lives in buffer (kt + 3 - nk3 % 3) % 3, so
-    // the final three stages are always (st0, st1, st2); the first nk3 % 3
-    // stages are peeled.  Fewer than three stages of K run as three, the
-    // stages past K reading as zeros.
-    const int nk3 = nk < 3 ? 3 : nk;
-    const int r = nk3 % 3;
-    if (r == 0) {
-      dma_stage(st0, 0, std::true_type{});
-      dma_stage(st1, 1, std::true_type{});
-      dma_stage(st2, 2, std::true_type{});
-    } else if (r == 1) {
-      dma_stage(st2, 0, std::true_type{});
-      dma_stage(st0, 1, std::true_type{});
-      dma_stage(st1, 2, std::true_type{});
-    } else {
-      dma_stage(st1, 0, std::true_type{});
-      dma_stage(st2, 1, std::true_type{});
-      dma_stage(st0, 2, std::true_type{});
-    }
-    wait_vm<2 * P>();
-    lds_barrier();
-    int kt = 0;
-    if (r == 1) {
-      first(st2);
-      stage_body(st2, st0, 0, LastDma{}, More{}, Wait1{});
-      kt = 1;
-    } else if (r == 2) {
-      first(st1);
-      stage_body(st1, st2, 0, LastDma{}, More{}, Wait1{});
-      stage_body(st2, st0, 1, LastDma{}, More{}, Wait1{});
-      kt = 2;
-    } else {
-      first(st0);
-    }
-    for (; nk3 - kt > 3; kt += 3) {
-      stage_body(st0, st1, kt, LastDma{}, More{}, Wait1{});
-      stage_body(st1, st2, kt + 1, LastDma{}, More{}, Wait1{});
-      stage_body(st2, st0, kt + 2, LastDma{}, More{}, Wait1{});
-    }
-    stage_body(st0, st1, kt, NoDma{}, More{}, Wait1{});
-    stage_body(st1, st2, kt + 1, NoDma{}, More{}, Wait0{});
-    stage_body(st2, st0, kt + 2, NoDma{}, std::true_type{}, Wait0{});
-  }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0)
+      is_last_part = __hip_atomic_fetch_add(p.cnt + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                     (unsigned)(parts - 1);
+    __syncthreads();
+    if (!is_last_part) return false;
+    if (tid == 0) __hip_atomic_store(p.cnt + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // one (nb, i, j) sub-tile at a time: its four chunks of every part
+    static_for<NB>([&](auto nbc) {
+      static_for<TM>([&](auto ic) {
+        static_for<TN>([&](auto jc) {
+          constexpr int nb = decltype(nbc)::value, i = decltype(ic)::value, j = decltype(jc)::value;
+          constexpr int c0 = ((nb * TM + i) * TN + j) * 4;
+          Acc& v = acc[nb][i][j];
+          v = Acc{};
+          for (int q = 0; q < parts; ++q) {
+            const __amdgpu_buffer_rsrc_t r = tile_rsrc(q);
+            typedef decltype(__builtin_shufflevector(v, v, 0, 1, 2, 3)) Part4;  // v4i or v4f
+            Part4 d[4];
+            static_for<4>([&](auto gc) {
+              constexpr int g = decltype(gc)::value;
+              d[g] = __builtin_bit_cast(Part4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff(c0 + g),
+                                                                                     kAgentCoherent));
+            });
+            static_for<4>([&](auto gc) {
+              constexpr int g = decltype(gc)::value;
+              static_for<4>([&](auto ec) {
+                constexpr int e = decltype(ec)::value;
+                if constexpr (MODE == GM_I8)
+                  v[4 * g + e] = (int)((uint32_t)v[4 * g + e] + (uint32_t)d[g][e]);
+                else
+                  v[4 * g + e] = v[4 * g + e] + d[g][e];
+              });
+            });
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        });
+      });
+    });
+    return true;
+  };
 
   // ---- epilogue ----------------------------------------------------------
   // Lane (lrow, lg) holds row wm*WTM + 32*i + lrow, columns
@@ -646,25 +818,24 @@ gemm_kernel(GemmArgs p) {
   // non-temporal: the tile is written once and not read back, and streamed
   // stores drain to memory as they go instead of waiting in L2 for the
   // end-of-kernel write-back.
-  lds_barrier();  // every wave is done reading the stage buffers
-  const int64_t row0w = m0 + wm * WTM;
-  const int64_t col0w = n0 + wn * WTN;
+  int64_t row0w = 0, col0w = 0;   // the finished tile's wave block
+  const float* scl_e = scl;        // and its scale set
   const bool has_rs = MODE == GM_I8 && p.row_scale != nullptr;
   const bool has_cs = p.col_scale != nullptr;
   const bool has_cs2 = NB == 2 && p.col_scale2 != nullptr;
   // scale of sub-tile row i / columns (j, g) of this lane, read from LDS
   // where it is used (holding a whole wave block's scales in registers
   // would cost 16 registers per sub-tile column)
-  auto row_scale_of = [&](int i) -> float { return has_rs ? scl[wm * WTM + i * 32 + lrow] : 1.f; };
+  auto row_scale_of = [&](int i) -> float { return has_rs ? scl_e[wm * WTM + i * 32 + lrow] : 1.f; };
   auto col_scale_of = [&](int j, int g, int which) -> v4f {
     const bool has = which ? has_cs2 : has_cs;
     const int c = wn * WTN + j * 32 + 8 * g + 4 * lg;
-    return has ? *reinterpret_cast<const v4f*>(scl + (1 + which) * SC_ROWS + c) : v4f{1.f, 1.f, 1.f, 1.f};
+    return has ? *reinterpret_cast<const v4f*>(scl_e + (1 + which) * SC_ROWS + c) : v4f{1.f, 1.f, 1.f, 1.f};
   };
   const bool has_res = MODE != GM_I8 && EPI != GE_SWIGLU && p.res != nullptr;
 
   // OK: output kind (DT_I32 / DT_F32 / DT_F16 / DT_BF16), a compile-time value
-  auto epilogue = [&](auto okc) {
+  auto epilogue = [&](auto okc) __attribute__((always_inline)) {
     constexpr int OK = decltype(okc)::value;
     constexpr int ES = (OK == DT_I32 || OK == DT_F32) ? 4 : 2;  // output element bytes
     constexpr int RB = WTN * ES;                 // bytes per row of the wave block
@@ -678,7 +849,9 @@ gemm_kernel(GemmArgs p) {
       else if constexpr (RB == 128) return (row >> 1) & 7;
       else return row & 15;
     };
-    char* region = (wave < PER_ARRAY ? st0 : st1) + (wave % PER_ARRAY) * (TMP * 32 * RB);
+    static_assert(!PERSIST || ES == 2, "persistent: 16-bit outputs");
+    char* region = PERSIST ? stg + wave * STG_WAVE
+                           : (wave < PER_ARRAY ? st0 : st1) + (wave % PER_ARRAY) * (TMP * 32 * RB);
     // the wave block's output rows: rows row0w.. (up to the matrix end),
     // columns from col0w; the fast path keeps 256 rows within 2^31 bytes
     const int64_t out_rows = p.M - row0w;
@@ -775,9 +948,14 @@ gemm_kernel(GemmArgs p) {
         const v4i d = *reinterpret_cast<const v4i*>(region + rl * RB + ((c ^ swz_out(rl)) << 4));
         const int64_t row = row0w + pp * TMP * 32 + rl;
         const int64_t col = col0w + c * EPC;
-        if (row < p.M) {
+        const uint32_t off = (uint32_t)((((int64_t)(pp * TMP * 32 + rl)) * p.ldc + c * EPC) * ES);
+        if constexpr (!EDGE) {
+          // interior tiles: every row and chunk is in range, so every wave
+          // issues exactly TM * NI stores (a persistent workgroup's next
+          // stage wait counts on it)
+          __builtin_amdgcn_raw_buffer_store_b128(d, rc_out, off, 0, kStoreWriteThrough);
+        } else if (row < p.M) {
           if (col + EPC <= p.N) {
-            const uint32_t off = (uint32_t)((((int64_t)(pp * TMP * 32 + rl)) * p.ldc + c * EPC) * ES);
             __builtin_amdgcn_raw_buffer_store_b128(d, rc_out, off, 0, kStoreWriteThrough);
           } else if (ES == 2 && col < p.N) {
             char* out = reinterpret_cast<char*>(p.c) + (row * p.ldc + col) * ES;
@@ -787,25 +965,124 @@ gemm_kernel(GemmArgs p) {
       });
     });
   };
-  switch (p.out_dtype) {
-    case DT_I32: if constexpr (MODE == GM_I8) epilogue(std::integral_constant<int, DT_I32>{}); break;
-    case DT_F32: if constexpr (EPI != GE_SWIGLU) epilogue(std::integral_constant<int, DT_F32>{}); break;
-    case DT_BF16: epilogue(std::integral_constant<int, DT_BF16>{}); break;
-    default: epilogue(std::integral_constant<int, DT_F16>{}); break;
+  // the epilogue of the tile whose wave block starts at (row0w, col0w)
+  auto epilogue_any = [&]() __attribute__((always_inline)) {
+    if constexpr (PERSIST) {
+      // launch_one runs persistent configs for 16-bit outputs only
+      if (p.out_dtype == DT_BF16) epilogue(std::integral_constant<int, DT_BF16>{});
+      else epilogue(std::integral_constant<int, DT_F16>{});
+    } else {
+      switch (p.out_dtype) {
+        case DT_I32: if constexpr (MODE == GM_I8) epilogue(std::integral_constant<int, DT_I32>{}); break;
+        case DT_F32: if constexpr (EPI != GE_SWIGLU) epilogue(std::integral_constant<int, DT_F32>{}); break;
+        case DT_BF16: epilogue(std::integral_constant<int, DT_BF16>{}); break;
+        default: epilogue(std::integral_constant<int, DT_F16>{}); break;
+      }
+    }
+  };
+  auto zero_acc = [&]() __attribute__((always_inline)) {
+    static_for<NB>([&](auto nbc) {
+      static_for<TM>([&](auto ic) {
+        static_for<TN>([&](auto jc) {
+          acc[decltype(nbc)::value][decltype(ic)::value][decltype(jc)::value] = Acc{};
+        });
+      });
+    });
+  };
+  (void)zero_acc;
+
+  if constexpr (!PERSIST) {
+    dma_scales(scl);
+    dma_prologue();
+    k_loop(std::integral_constant<int, 0>{});
+    if constexpr (SPLITM) {
+      if (!split_handoff()) {
+        clock_out();
+        return;
+      }
+    }
+    lds_barrier();  // every wave is done reading the stage buffers
+    row0w = m0 + wm * WTM;
+    col0w = n0 + wn * WTN;
+    scl_e = scl;
+    epilogue_any();
+  } else {
+    // stores per wave in one epilogue (16-bit output, interior tiles)
+    constexpr int NS = TM * (32 * WTN * 2 / 1024);
+    static_assert(STAGES * P + NS < 64, "vmcnt range");
+    dma_scales(scl);
+    dma_prologue();
+    bool first_tile = true;
+    for (;;) {
+      if (first_tile) k_loop(std::integral_constant<int, 0>{});
+      else k_loop(std::integral_constant<int, NS>{});
+      lds_barrier();  // every wave is done reading the stage buffers
+      row0w = m0 + wm * WTM;
+      col0w = n0 + wn * WTN;
+      scl_e = scl;
+      // the next tile's scales and first stages go out before this tile's
+      // epilogue, so they load while it converts and stores
+      const bool more = ++t_cur < t_end;
+      if (more) {
+        set_tile(t_cur % tiles_m, t_cur / tiles_m);
+        scl = scl == scl_all ? scl_all + (1 + NB) * SC_ROWS : scl_all;
+        dma_scales(scl);
+        dma_prologue();
+      }
+      epilogue_any();
+      if (!more) break;
+      first_tile = false;
+      zero_acc();
+      // what derives from lane and wave is recomputed for the next tile
+      // rather than held across its K loop
+      int t = tid;
+      asm volatile("" : "+v"(t));
+      lane = t & 63;
+      wave = __builtin_amdgcn_readfirstlane(t >> 6);
+      lrow = lane & 31;
+      lg = lane >> 5;
+      wm = wave / WN;
+      wn = wave % WN;
+    }
   }
+  clock_out();
 }
+
 
 // ---------------------------------------------------------------------------
 // Config table.  The autotuner searches over these instantiations.
 // ---------------------------------------------------------------------------
 typedef void (*GemmLaunch)(const GemmArgs&, hipStream_t);
 
-template <int MODE, int BM, int BN, int WM, int WN, int EPI, int SB = 128, int STAGES = 2, int MINW = 1>
+// PERSIST configs run the persistent kernel on interior shapes with 16-bit
+// outputs and no K split (one workgroup per CU, or fewer when there are
+// fewer tiles), and the one-tile-per-workgroup kernel of the same tile
+// otherwise.
+// SPLITM configs (the K-split ones) merge their parts inside the kernel
+// when the launch brings per-tile counters, and through launch_gemm's
+// merge kernel otherwise.
+template <int MODE, int BM, int BN, int WM, int WN, int EPI, int SB = 128, int STAGES = 2, int MINW = 1,
+          bool PERSIST = false, bool SPLITM = false>
 static void launch_one(const GemmArgs& a, hipStream_t s) {
   const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   const unsigned parts = a.k_split > 0 ? (unsigned)((a.K + a.k_split - 1) / a.k_split) : 1u;
   const dim3 grid((unsigned)tiles, parts), block(64 * WM * WN);
   const bool edge = a.M % BM != 0 || a.N % BN != 0;
+  if constexpr (PERSIST) {
+    if (!edge && !a.b_kn && parts == 1 && (a.out_dtype == DT_F16 || a.out_dtype == DT_BF16)) {
+      const int64_t g = tiles < gemm_num_cus() ? tiles : gemm_num_cus();
+      gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, false, false, STAGES, true>
+          <<<dim3((unsigned)g), block, 0, s>>>(a);
+      return;
+    }
+  }
+  if constexpr (SPLITM && EPI == GE_STORE) {
+    if (parts > 1 && a.cnt && !a.b_kn) {
+      if (edge) gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, true, false, STAGES, false, true><<<grid, block, 0, s>>>(a);
+      else gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, false, false, STAGES, false, true><<<grid, block, 0, s>>>(a);
+      return;
+    }
+  }
   if constexpr ((MODE == GM_F16 || MODE == GM_BF16 || MODE == GM_I8) && EPI == GE_STORE) {
     if (a.b_kn) {
       if (edge) gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, true, true, STAGES><<<grid, block, 0, s>>>(a);

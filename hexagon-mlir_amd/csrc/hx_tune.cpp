@@ -258,7 +258,16 @@ class Probe {
       part = std::max(part, gemm_part_bytes(mode_, idx_[i], t));
     }
     float* partials = nullptr;
-    if (part && !(partials = (float*)ar_.get(part))) return api_fail(HX_ERR_NOMEM, "hx_tune: partials");
+    unsigned* split_cnt = nullptr;
+    if (part) {
+      // the split configs merge inside the kernel with per-tile counters
+      // (zero here; every launch leaves them at zero), as the products run
+      if (!(partials = (float*)ar_.get(part)) ||
+          !(split_cnt = (unsigned*)ar_.get((size_t)kGemvSplitCounters * sizeof(unsigned))))
+        return api_fail(HX_ERR_NOMEM, "hx_tune: partials");
+      if (launch_fill_u32(split_cnt, kGemvSplitCounters, 0u, s_) != HXI_OK || hipGetLastError() != hipSuccess)
+        return api_fail(HX_ERR_HIP, "hx_tune: clearing the split counters");
+    }
     for (int c = 0; c < copies_; ++c) {
       void* b = ar_.get((size_t)n_ * k_ * eb);
       void* b2 = swiglu ? ar_.get((size_t)n_ * k_ * eb) : nullptr;
@@ -273,6 +282,7 @@ class Probe {
       g.out_dtype = out_dt_;
       g.row_scale = rs; g.col_scale = cs; g.col_scale2 = cs2;
       g.part = partials;
+      g.cnt = split_cnt;
       g_.push_back(g);
     }
     if (const char* why = gemm_fast_refusal(mode_, g_[0])) family_reason_ = why;

@@ -361,6 +361,19 @@ def manifest() -> dict:
     return json.loads(buf.value.decode())
 
 
+def clock_probe(enable: bool) -> None:
+    """Start (zeroing the counters) or stop the tiled GEMM kernels' clock
+    stamps on the current device (hx_clock_probe)."""
+    check(load().hx_clock_probe(1 if enable else 0), "hx_clock_probe")
+
+
+def clock_read() -> dict:
+    """Mean shader clock of the stamped GEMM workgroups (hx_clock_read)."""
+    mhz, us, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_longlong()
+    check(load().hx_clock_read(ctypes.byref(mhz), ctypes.byref(us), ctypes.byref(n)), "hx_clock_read")
+    return {"mhz": mhz.value, "workgroup_us": us.value, "workgroups": n.value}
+
+
 # --------------------------------------------------------------------------- #
 # Pre-bound calls: descriptors built once, so a repeated call costs one C-ABI
 # entry (for timing loops and serving loops; tensors must stay alive).

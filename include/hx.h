@@ -462,6 +462,25 @@ int hx_manifest_enable(int on);
 int hx_manifest_clear(void);
 int hx_manifest_json(char* buf, size_t cap, size_t* needed);
 
+/* ---------------------------------------------------------------------- */
+/* Clock probe                                                             */
+/* ---------------------------------------------------------------------- */
+
+/* A measurement hook with no counterpart in the reference (whose profiler
+ * reads the Hexagon cycle counters, QHB/backend/hmx_search.py:1109-1156
+ * "PerfPcycles"): it reports the shader clock MFMA-bound kernels actually
+ * ran at, which on MI355X varies with the operands' data.  While enabled on
+ * the current device, every workgroup of the tiled GEMM kernels (hx_gemm_i8,
+ * hx_matmul, hx_matmul_resident beyond the decode sizes, the GEMMs of
+ * hx_swiglu_ffn) adds its elapsed shader-clock cycles (s_memtime) and
+ * constant-rate ticks (s_memrealtime) to a per-device pair of counters.
+ * hx_clock_probe(1) allocates (first use) and zeroes the counters and waits
+ * for the device; hx_clock_probe(0) stops the stamping.  hx_clock_read waits
+ * for the device and returns the mean clock over the stamped workgroups in
+ * MHz, the summed workgroup time in microseconds and the workgroup count. */
+int hx_clock_probe(int enable);
+int hx_clock_read(double* mhz, double* workgroup_us, long long* workgroups);
+
 #ifdef __cplusplus
 }
 #endif
