@@ -259,6 +259,15 @@ def bench_gemm_i8(hx, steps: int, warmup: int, tune_on: bool = True):
     # least 20), and the shader clock the kernel ran at over one more
     spread = event_timed([step], max(steps, 20), regions=7)
     clock = clock_during(hx, [step], max(steps, 20))
+    # the same call on all-zero operands (same instructions and accesses, no
+    # data switching), timed and clocked the same way right after
+    az, bz = torch.zeros_like(a), torch.zeros_like(bt)
+    cz = torch.empty_like(c)
+    step_z = hx.bind_gemm_i8(az, bz, cz, b_layout="nk", row_scale=sa, col_scale=sb)
+    step_z()
+    zero_t = event_timed([step_z], max(steps, 20), regions=7)
+    zero_clock = clock_during(hx, [step_z], max(steps, 20))
+    del az, bz, cz
     ops = 2.0 * M * N * K
     tops_wall = ops / (wall_ms * 1e-3) / 1e12
     tops_kernel = ops / (ev_ms * 1e-3) / 1e12
@@ -275,7 +284,10 @@ def bench_gemm_i8(hx, steps: int, warmup: int, tune_on: bool = True):
     cfg = hx.config_get(1, cfg_idx)["name"] if cfg_idx >= 0 else "generic"
     return dict(ms_per_step=wall_ms, kernel_ms=ev_ms, tops=tops_wall, tops_kernel=tops_kernel,
                 parity_sampled_rows_bitexact=exact, kernel=cfg, inputs=(a, bt, sa, sb), output=c,
-                tune=tune_report, queue_fed=fed, plan=plan, spread=spread, clock=clock)
+                tune=tune_report, queue_fed=fed, plan=plan, spread=spread, clock=clock,
+                zero_operands={"us_per_call": round(zero_t[0] * 1e3, 3), "spread": zero_t.spread(),
+                               "clock": zero_clock,
+                               "note": "the same call on all-zero A and B, right after the spread regions"})
 
 
 def _host_threads():
@@ -732,6 +744,43 @@ def bench_gemm_i8_kn(hx, inputs, iters: int = 50):
             "parity": {"f16_sampled_rows_bitexact": exact and exact2}, "queue_fed": fed}
 
 
+def bench_vendor_gemms(hx, inputs, iters: int = 30):
+    """The vendor library beside the hand-written kernels on the same
+    devices and operands: torch._int_mm (hipBLASLt int8 -> int32) against
+    hx_gemm_i8 with the int32 output at 4096^3, and torch.mm (hipBLASLt fp16)
+    against hx_matmul at fp16 4096^3 (B as [N][K] for both).  Timed the same
+    way as every line (HIP events, regions, median)."""
+    import torch
+    a, bt, sa, sb = inputs
+    M, K = a.shape
+    N = bt.shape[0]
+    out = {"workload": "vendor GEMMs beside hx at 4096^3 (hipBLASLt through torch)", "unit": "us"}
+    c32 = torch.empty((M, N), dtype=torch.int32, device=a.device)
+    hx_i32 = event_timed([hx.bind_gemm_i8(a, bt, c32, b_layout="nk")], iters)
+    out["hx_gemm_i8_i32_us"] = round(hx_i32[0] * 1e3, 3)
+    try:
+        btt = bt.t()  # [K, N] view of the [N, K] weight: the column-major B hipBLASLt takes
+        ref = torch._int_mm(a, btt)
+        out["int_mm_equal_to_hx"] = bool(torch.equal(ref, c32))
+        t = event_timed([lambda: torch._int_mm(a, btt)], iters)
+        out["torch_int_mm_i32_us"] = round(t[0] * 1e3, 3)
+    except Exception as e:  # noqa: BLE001
+        out["torch_int_mm_i32_us"] = None
+        out["torch_int_mm_error"] = str(e)[:200]
+    g = torch.Generator(device=a.device).manual_seed(21)
+    x = torch.empty((M, K), dtype=torch.float16, device=a.device).uniform_(-1, 1, generator=g)
+    w = torch.empty((N, K), dtype=torch.float16, device=a.device).uniform_(-1, 1, generator=g)
+    y = torch.empty((M, N), dtype=torch.float16, device=a.device)
+    y2 = torch.empty_like(y)
+    t_hx = event_timed([lambda: hx.matmul(x, w, b_layout="nk", out=y)], iters)
+    t_mm = event_timed([lambda: torch.mm(x, w.t(), out=y2)], iters)
+    out["hx_matmul_f16_us"] = round(t_hx[0] * 1e3, 3)
+    out["torch_mm_f16_us"] = round(t_mm[0] * 1e3, 3)
+    out["value"] = out["hx_gemm_i8_i32_us"]
+    del x, w, y, y2, c32
+    return out
+
+
 def bench_gemm_f16_small(hx, iters: int = 200):
     import torch
     dev = torch.device("cuda:0")
@@ -902,6 +951,66 @@ def bench_attention(hx, iters: int = 20):
 
 # --------------------------------------------------------------------------- #
 
+def gemv_ab(hx, rounds: int = 5, iters: int = 400) -> str:
+    """Interleaved A/B of the decode GEMV configurations that compete for
+    the untuned default at the C3 shapes (int8, N = 11008, K = 4096,
+    registered weights rotating over 12 copies, each its own output) and at
+    the FFN's down projection (N = 4096, K = 11008): every round times every
+    candidate once (one region of ``iters`` launches), so all of them see the
+    same clock and thermal drift; the table gives the median and q20 / q80
+    over the rounds.  Markdown on stdout."""
+    import numpy as np
+    import torch
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(77)
+    names = [hx.config_get(6, i)["name"] for i in range(hx.config_count(6))]
+    lines = ["# Decode GEMV defaults: interleaved A/B (bench.py --gemv-ab)", "",
+             f"Every round times each candidate once ({iters} launches over 12 rotating registered weight copies, "
+             f"each with its own output; HIP events); {rounds} rounds; us per launch, median [q20, q80] over the "
+             "rounds.  `*` marks the untuned default.", ""]
+    shapes = [(11008, 4096, (1, 4, 8, 12, 16),
+               ("gemv_packed_ct3_kw16", "gemv_packed_ct3_kw8", "gemv_packed_ct4_kw8", "gemv_packed_ct4_kw8_c8",
+                "gemv_packed_ct1_kw8_xd", "gemv_packed_ct6_kw16_s2")),
+              (4096, 11008, (8, 12, 16),
+               ("gemv_packed_ct4_kw16_s4", "gemv_packed_ct2_kw16_s2", "gemv_packed_ct4_kw16", "gemv_packed_ct1_kw16",
+                "gemv_packed_ct2_kw8", "gemv_packed_ct1_kw8"))]
+    for N, K, Ms, cands in shapes:
+        ws = []
+        for _ in range(12):
+            w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+            sc = torch.empty(N, dtype=torch.float16, device=dev).uniform_(0.001, 0.02, generator=g)
+            ws.append(hx.ResidentWeight(w, sc, layout="nk"))
+            del w
+        try:
+            lines += [f"## N = {N}, K = {K}", "", "| M | " + " | ".join(c.replace("gemv_packed_", "") for c in cands)
+                      + " |", "|---:|" + "---:|" * len(cands)]
+            for M in Ms:
+                hx.config_select(6, M, N, K, -1)
+                default = names[hx.config_lookup(6, M, N, K)]
+                x = torch.randn((M, K), dtype=torch.float16, device=dev, generator=g)
+                ys = [torch.empty((M, N), dtype=torch.float16, device=dev) for _ in ws]
+                t = {c: [] for c in cands}
+                try:
+                    for _ in range(rounds):
+                        for c in cands:
+                            hx.config_select(6, M, N, K, names.index(c))
+                            calls = [hx.bind_matmul_resident(x, w, y) for w, y in zip(ws, ys)]
+                            t[c].append(event_timed(calls, iters, regions=1)[0] * 1e3)
+                finally:
+                    hx.config_select(6, M, N, K, -1)
+                cells = []
+                for c in cands:
+                    r = np.asarray(t[c])
+                    cells.append(f"{np.median(r):.2f} [{np.quantile(r, 0.2):.2f}, {np.quantile(r, 0.8):.2f}]"
+                                 + (" *" if c == default else ""))
+                lines.append(f"| {M} | " + " | ".join(cells) + " |")
+            lines.append("")
+        finally:
+            for w in ws:
+                w.release()
+    return "\n".join(lines) + "\n"
+
+
 def pmc_workload(hx, keys_path=None) -> None:
     """A few launches of every benchmarked kernel -- every compiled config of
     the headline GEMM and of the decode GEMV, so whichever one the tuner
@@ -931,7 +1040,12 @@ def pmc_workload(hx, keys_path=None) -> None:
     c32 = torch.empty((M, N), dtype=torch.int32, device=dev)
     for _ in range(3):
         hx.gemm_i8(a, bt, b_layout="nk", out=c32)
-    del c32, a, bt, c
+    # the headline's config on all-zero operands: the same instructions and
+    # accesses, no data switching in the MFMA units
+    az, bz = torch.zeros_like(a), torch.zeros_like(bt)
+    for _ in range(3):
+        hx.gemm_i8(az, bz, b_layout="nk", row_scale=sa, col_scale=sb, out=c)
+    del c32, a, bt, c, az, bz
     w = torch.randint(-127, 128, (11008, 4096), dtype=torch.int8, device=dev, generator=g)
     rw = hx.ResidentWeight(w, torch.rand(11008, device=dev).half() * 0.02, layout="nk")
     for m in (1, 4, 16):
@@ -962,6 +1076,12 @@ def pmc_workload(hx, keys_path=None) -> None:
     y = torch.empty_like(x)
     for _ in range(3):
         hx.swiglu_ffn(x, gam, 1e-6, Wg, Wu, Wd, out=y)
+    # the gate/up GEMM on its persistent config
+    sw = [hx.config_get(5, i)["name"] for i in range(hx.config_count(5))]
+    hx.config_select(5, T, I, H, sw.index("swiglu_256x128_w2x4_p"))
+    for _ in range(3):
+        hx.swiglu_ffn(x, gam, 1e-6, Wg, Wu, Wd, out=y)
+    hx.config_select(5, T, I, H, -1)
     Wg.release(); Wu.release(); Wd.release()
     del x, y
     # fp16 decode on a registered weight (its packed image), then softmax
@@ -997,6 +1117,7 @@ def pmc_sequence(hx):
         seq.append((f"gemm_i8_4096_dequant_f16:{hx.config_get(1, idx)['name']}", 3))
     head = hx.config_get(1, hx.config_lookup(1, 4096, 4096, 4096))["name"]
     seq.append((f"gemm_i8_4096_i32:{head}", 3))
+    seq.append((f"gemm_i8_4096_dequant_f16_zero_operands:{head}", 3))
     for m in (1, 4, 16):
         for idx in range(hx.config_count(6)):
             seq.append((f"gemv_w8a16_m{m}:{hx.config_get(6, idx)['name']}", 3))
@@ -1005,6 +1126,8 @@ def pmc_sequence(hx):
     dn = hx.config_get(4, hx.config_lookup(4, 2048, 4096, 11008))["name"]
     for _ in range(3):
         seq += [("ffn_rmsnorm_2048x4096", 1), (f"ffn_gate_up:{gu}", 1), (f"ffn_down:{dn}", 1)]
+    for _ in range(3):
+        seq += [("ffn_rmsnorm_2048x4096", 1), ("ffn_gate_up:swiglu_256x128_w2x4_p", 1), (f"ffn_down:{dn}", 1)]
     fd = hx.config_get(7, hx.config_lookup(7, 1, 8192, 8192))["name"]
     seq += [(f"f16_decode_1x8192x8192:{fd}", 3), ("softmax_f16_2048x128256", 3)]
     return seq
@@ -1082,9 +1205,11 @@ def mfma_from_pmc(pmc_csv: str, keys_json: str, command: str) -> str:
              "Per kernel, the median over its launches. MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / "
              "(GRBM_GUI_ACTIVE / 8 XCDs x 1024 SIMDs); clock = GRBM_GUI_ACTIVE / 8 / duration; "
              "MOPS x 512 = the operations the MFMA units counted (I8 or F16 MOPS); LDS conflict = "
-             "SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE.", "",
+             "SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE; waiting = SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES (the "
+             "share of wave-cycles a wave waited for any dependency: memory, LDS, MFMA results, barriers).",
+             "",
              "| kernel (workload:config) | duration us | clock GHz | MFMA busy | counted ops / algorithmic | "
-             "LDS conflict |", "|---|---:|---:|---:|---:|---:|"]
+             "LDS conflict | waiting |", "|---|---:|---:|---:|---:|---:|---:|"]
     for key, vals in _group(json.loads(Path(keys_json).read_text()), disp).items():
         if not (key.startswith("gemm_i8_4096") or key.startswith("ffn_gate") or key.startswith("ffn_down")):
             continue
@@ -1096,11 +1221,15 @@ def mfma_from_pmc(pmc_csv: str, keys_json: str, command: str) -> str:
             ops = 512.0 * (c.get("SQ_INSTS_VALU_MFMA_MOPS_I8", 0.0) + c.get("SQ_INSTS_VALU_MFMA_MOPS_F16", 0.0))
             lds = (c.get("SQ_LDS_BANK_CONFLICT", 0.0) / c["SQ_LDS_IDX_ACTIVE"]
                    if c.get("SQ_LDS_IDX_ACTIVE") else float("nan"))
-            rec.append((d_ns / 1e3 if d_ns else float("nan"), gui / d_ns if d_ns else float("nan"), busy, ops, lds))
-        med = [statistics.median(r[i] for r in rec) for i in range(5)]
+            wait = (c.get("SQ_WAIT_INST_ANY", float("nan")) / c["SQ_WAVE_CYCLES"]
+                    if c.get("SQ_WAVE_CYCLES") else float("nan"))
+            rec.append((d_ns / 1e3 if d_ns else float("nan"), gui / d_ns if d_ns else float("nan"), busy, ops, lds,
+                        wait))
+        med = [statistics.median(r[i] for r in rec) for i in range(6)]
         base = next((v for k, v in algo.items() if key.startswith(k)), None)
         ratio = f"{med[3] / base:.3f}" if base else "-"
-        lines.append(f"| {key} | {med[0]:.1f} | {med[1]:.3f} | {100 * med[2]:.1f}% | {ratio} | {100 * med[4]:.2f}% |")
+        lines.append(f"| {key} | {med[0]:.1f} | {med[1]:.3f} | {100 * med[2]:.1f}% | {ratio} | {100 * med[4]:.2f}% | "
+                     f"{100 * med[5]:.1f}% |")
     return "\n".join(lines) + "\n"
 
 
@@ -1338,6 +1467,8 @@ def main() -> int:
                     help="time the untuned default configs (skip the tile search)")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="launch each benchmarked kernel a few times for rocprofv3 --pmc")
+    ap.add_argument("--gemv-ab", action="store_true",
+                    help="interleaved A/B of the decode GEMV default candidates, markdown on stdout, exit")
     ap.add_argument("--ceilings", action="store_true",
                     help="time the libhxprobe probes (launch gap, read, copy, MFMA issue), print JSON, exit")
     ap.add_argument("--pmc-keys", metavar="JSON",
@@ -1377,6 +1508,9 @@ def main() -> int:
     if args.ceilings:
         print(json.dumps(ceilings(hx)), flush=True)
         return 0
+    if args.gemv_ab:
+        print(gemv_ab(hx), end="", flush=True)
+        return 0
     if args.pmc_workload:
         pmc_workload(hx, args.pmc_keys)
         return 0
@@ -1392,6 +1526,8 @@ def main() -> int:
         secondary.append(bench_gemm_i8_i32(hx, h["inputs"]))
         log("[bench] int8 GEMM 4096^3, [K][N] B in place")
         secondary.append(bench_gemm_i8_kn(hx, h["inputs"]))
+        log("[bench] vendor GEMMs beside hx")
+        secondary.append(bench_vendor_gemms(hx, h["inputs"]))
         log("[bench] W8A16 GEMV")
         secondary += bench_gemv(hx, tune_on=tune_on)
         log("[bench] W8A16 GEMV, down-projection shape")
@@ -1466,6 +1602,7 @@ def main() -> int:
         "spread": dict(h["spread"].spread(), note="7 more timed regions of the same launches after the "
                                                   "timed steps; the figure is the steps' own region"),
         "clock": h["clock"],
+        "zero_operands": h["zero_operands"],
         "queue_fed": h["queue_fed"],
         "parity": {"int8_sampled_rows_bitexact": h["parity_sampled_rows_bitexact"],
                    "all_elements_bitexact": (cpu or {}).get("gpu_output_bitexact_all_elements")},

@@ -526,11 +526,15 @@ static int gemv_untuned_table(int op, int64_t M, int64_t N, int64_t K, bool in_p
     if (M > 8 && tiles <= 256 && K >= 10240) return 25;
     return three_tiles ? 20 : tiles >= 512 ? 0 : 1;
   }
-  // untuned choice from the MI355X sweep (int8, K = 4096, tuner medians).
-  // When the 16-column tiles need three per workgroup to fit one workgroup
-  // per CU (N = 11008: 688 tiles, 230 workgroups), three tiles over 16 waves
-  // (M = 1 / 4 / 5 / 8 / 12 / 16: 9.23 / 9.30 / 9.28 / 9.36 / 9.69 / 10.24 us;
-  // over 8 waves 9.50 / 9.53 / 9.61 / 9.84 / 10.19 / 10.67).  Otherwise,
+  // untuned choice from the MI355X sweep (int8, K = 4096).  When the
+  // 16-column tiles need three per workgroup to fit one workgroup per CU
+  // (N = 11008: 688 tiles, 230 workgroups): three tiles over 16 waves up to
+  // 4 rows, over 8 waves from 8 rows -- interleaved A/B, five rounds on one
+  // box (bench.py --gemv-ab), M = 1 / 4 / 8 / 12 / 16: 16 waves 9.36 / 9.49 /
+  // 9.88 / 10.44 / 11.04 us, 8 waves 9.65 / 9.56 / 9.80 / 9.97 / 10.29.
+  // Past 4 rows every lane's accumulators go through the cross-wave LDS
+  // reduction at the end (up to 4 rows only lanes 0..15 do), and half the
+  // waves halve it; the weight and activation bytes are the same.  Otherwise,
   // for M <= 4: up to 256 tiles one tile per workgroup over 16 waves (M = 1
   // / 4, N = K = 4096: 5.11 / 5.23 against 5.31 / 5.59 with LDS-staged
   // activations over 8), beyond two tiles over 8 waves (M = 4, N = 8192 /
@@ -539,7 +543,7 @@ static int gemv_untuned_table(int op, int64_t M, int64_t N, int64_t K, bool in_p
   // workgroups within one per CU, three beyond 1024 tiles (M = 16, N = 2048
   // / 4096 / 8192 / 16384 / 22016: 6.83 / 7.08 / 8.85 / 13.64 / 18.97 us;
   // four tiles everywhere took 9.63 / 9.86 / 10.5 / 13.64 / 22.25).
-  if (three_tiles) return 20;
+  if (three_tiles) return M >= 8 ? 19 : 20;
   if (M <= 4) return tiles > 256 ? 0 : 24;
   // at most 128 tiles with K >= 8192, up to 12 rows: one tile per
   // workgroup over two parts (M = 5 / 8 / 12 at 2048 x 8192: 7.2 / 7.8 /

@@ -98,6 +98,21 @@ __device__ __forceinline__ float load_any(const void* p, int dt, int64_t idx) {
   return reinterpret_cast<const float*>(p)[idx];
 }
 
+// The grouped order: linear tile number -> tile, walking GROUP_M M-tiles of
+// one B strip, then the same M-tiles of the next strip, so a contiguous
+// run of numbers covers a GROUP_M x k block of tiles (its A and B strips
+// stay in one XCD's L2 while the block goes by).
+__device__ __forceinline__ void tile_of_lin(int lin, int tiles_m, int tiles_n, int& tm, int& tn) {
+  constexpr int GROUP_M = 4;
+  const int per_group = GROUP_M * tiles_n;
+  const int group = lin / per_group;
+  const int first_m = group * GROUP_M;
+  const int gm = min(tiles_m - first_m, GROUP_M);
+  const int in_group = lin - group * per_group;
+  tm = first_m + in_group % gm;
+  tn = in_group / gm;
+}
+
 // Map a workgroup to its output tile.  Workgroup b runs on XCD b % 8; the
 // renumbering makes the tiles of one XCD a contiguous run of `lin`, and the
 // grouped order turns that run into a GROUP_M x k block of tiles.
@@ -305,11 +320,12 @@ gemm_kernel(GemmArgs p) {
           (void*)(reinterpret_cast<const char*>(p.b2) + n0 * ldb_b), 0, (int)(rows_b * ldb_b),
           0x00020000);
   };
-  // PERSIST: this workgroup's run of tiles.  Tiles are numbered strip-major
-  // (t = tn * tiles_m + tm: consecutive numbers are consecutive M-tiles of
-  // one B strip) and cut into gridDim.x runs whose lengths differ by at
-  // most one; workgroup b runs on XCD b % 8, so the runs are renumbered to
-  // give each XCD a contiguous range of strips.
+  // PERSIST: this workgroup's run of tiles.  Tiles are numbered in the
+  // grouped order (consecutive numbers are consecutive M-tiles of one B
+  // strip, GROUP_M at a time) and cut into gridDim.x runs whose lengths
+  // differ by at most one; workgroup b runs on XCD b % 8, so the runs are
+  // renumbered to give each XCD a contiguous range of numbers -- a compact
+  // block of tiles whose A and B strips its L2 holds.
   int t_cur = 0, t_end = 0;
   if constexpr (PERSIST) {
     const int ntiles = tiles_m * tiles_n;
@@ -318,7 +334,9 @@ gemm_kernel(GemmArgs p) {
     if ((G & 7) == 0) w = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
     t_cur = __builtin_amdgcn_readfirstlane((int)((int64_t)w * ntiles / G));
     t_end = __builtin_amdgcn_readfirstlane((int)((int64_t)(w + 1) * ntiles / G));
-    set_tile(t_cur % tiles_m, t_cur / tiles_m);
+    int tm_, tn_;
+    tile_of_lin(t_cur, tiles_m, tiles_n, tm_, tn_);
+    set_tile(tm_, tn_);
   } else {
     int tm_, tn_;
     tile_of(tiles_m, tiles_n, tm_, tn_);
@@ -1024,7 +1042,9 @@ gemm_kernel(GemmArgs p) {
       // epilogue, so they load while it converts and stores
       const bool more = ++t_cur < t_end;
       if (more) {
-        set_tile(t_cur % tiles_m, t_cur / tiles_m);
+        int tm_, tn_;
+        tile_of_lin(t_cur, tiles_m, tiles_n, tm_, tn_);
+        set_tile(tm_, tn_);
         scl = scl == scl_all ? scl_all + (1 + NB) * SC_ROWS : scl_all;
         dma_scales(scl);
         dma_prologue();
