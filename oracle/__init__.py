@@ -83,15 +83,23 @@ def use_native_build() -> str:
     import tempfile
     d = Path(tempfile.mkdtemp(prefix="hx_oracle_native_"))
     out = d / "liboracle_native.so"
-    subprocess.run(["gcc", "-O3", "-march=native", "-fopenmp", "-ffp-contract=off", "-fno-math-errno",
+    r = subprocess.run(["gcc", "-march=native", "-Q", "--help=target"], capture_output=True, text=True)
+    enabled = {ln.split()[0] for ln in r.stdout.splitlines() if ln.strip().endswith("[enabled]")}
+    march = next((ln.split()[-1] for ln in r.stdout.splitlines() if ln.strip().startswith("-march=")), "native")
+    # an older gcc that does not know the host's core model resolves
+    # -march=native to an older one without its AVX-512: add what the CPU
+    # reports (the extensions gcc 11 can target)
+    try:
+        cpu = set(open("/proc/cpuinfo").read().split())
+    except OSError:
+        cpu = set()
+    extra = [f"-m{f}" for f in ("avx512f", "avx512bw", "avx512dq", "avx512vl", "avx512cd", "avx512vnni")
+             if f in cpu and f"-m{f}" not in enabled]
+    subprocess.run(["gcc", "-O3", "-march=native", *extra, "-fopenmp", "-ffp-contract=off", "-fno-math-errno",
                     "-fPIC", "-shared", str(SRC), "-o", str(out), "-lm"], check=True)
     _lib = None
     _bind(ctypes.CDLL(str(out)))
-    r = subprocess.run(["gcc", "-march=native", "-Q", "--help=target"], capture_output=True, text=True)
-    for line in r.stdout.splitlines():
-        if line.strip().startswith("-march="):
-            return line.split()[-1]
-    return "native"
+    return march + ("" if not extra else " " + " ".join(extra))
 
 
 def lib():
