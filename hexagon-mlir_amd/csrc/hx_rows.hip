@@ -51,6 +51,23 @@ __device__ __forceinline__ float group_sum(float v, float* red) {
     return s;
   }
 }
+// group_sum for a buffer this workgroup has not used before: no barrier
+// guards a previous use, so one barrier (the publish) remains.
+template <int WPR>
+__device__ __forceinline__ float group_sum_once(float v, float* red) {
+  v = wave_sum(v);
+  if constexpr (WPR == 1) {
+    return v;
+  } else {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < WPR; ++i) s += red[i];
+    return s;
+  }
+}
 template <int WPR>
 __device__ __forceinline__ float group_max(float v, float* red) {
   v = wave_max(v);
@@ -248,7 +265,10 @@ __global__ void __launch_bounds__(WPR > 4 ? 64 * WPR : 256) row_vec_kernel(RowAr
   typedef typename Elem<DT>::storage S;
   constexpr int EV = 16 / sizeof(S);
   static_assert(WPR <= 4 || OP == ROW_SOFTMAX, "8-wave rows: softmax only");
-  __shared__ float red[WPR > 4 ? WPR : 4];
+  // one reduction buffer per exchange (a row takes at most two), so no
+  // exchange waits for the readers of a previous one
+  constexpr int NRED = WPR > 4 ? WPR : 4;
+  __shared__ float red[2 * NRED];
 
   const int lane = threadIdx.x & 63;
   // wave index and row as provably uniform values: the row's buffer
@@ -296,6 +316,11 @@ __global__ void __launch_bounds__(WPR > 4 ? 64 * WPR : 256) row_vec_kernel(RowAr
 
   float scale = 1.f, shift = 0.f;
   if constexpr (OP == ROW_SOFTMAX) {
+    // One exchange across the row's waves: each wave reduces its own max m_w
+    // and sum s_w = sum exp(x - m_w), and the pairs combine as
+    // m = max m_w, s = sum s_w exp(m_w - m) (the online-softmax merge,
+    // test_online_softmax.py:28-78) -- one barrier per row instead of a max
+    // exchange and a sum exchange (four barriers).
     float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < VPL; ++i)
@@ -303,7 +328,7 @@ __global__ void __launch_bounds__(WPR > 4 ? 64 * WPR : 256) row_vec_kernel(RowAr
 #pragma unroll
         for (int j = 0; j < EV; ++j) m = fmaxf(m, vec_elem<DT>(raw[i], j));
       }
-    m = group_max<WPR>(m, red);
+    m = wave_max(m);
     if constexpr (WPR > 4) opaque_vecs<VPL>(raw);
     float s = 0.f;
 #pragma unroll
@@ -312,7 +337,22 @@ __global__ void __launch_bounds__(WPR > 4 ? 64 * WPR : 256) row_vec_kernel(RowAr
 #pragma unroll
         for (int j = 0; j < EV; ++j) s += fast_exp(vec_elem<DT>(raw[i], j) - m);
       }
-    s = group_sum<WPR>(s, red);
+    s = wave_sum(s);
+    if constexpr (WPR > 1) {
+      if (lane == 0) {
+        red[wave] = m;
+        red[NRED + wave] = s;
+      }
+      __syncthreads();
+      float mg = red[0];
+#pragma unroll
+      for (int i = 1; i < WPR; ++i) mg = fmaxf(mg, red[i]);
+      float sg = 0.f;
+#pragma unroll
+      for (int i = 0; i < WPR; ++i) sg += red[NRED + i] * fast_exp(red[i] - mg);
+      m = mg;
+      s = sg;
+    }
     scale = 1.0f / s;  // DivToMul: one reciprocal, then multiplies
     shift = m;
   } else if constexpr (OP == ROW_RMSNORM) {
@@ -324,7 +364,7 @@ __global__ void __launch_bounds__(WPR > 4 ? 64 * WPR : 256) row_vec_kernel(RowAr
         const float v = vec_elem<DT>(raw[i], j);  // zero where not loaded
         ss += v * v;
       }
-    ss = group_sum<WPR>(ss, red);
+    ss = group_sum_once<WPR>(ss, red);
     scale = 1.0f / sqrtf(ss / (float)cols + a.eps);
   } else {
     float s = 0.f;
@@ -332,7 +372,7 @@ __global__ void __launch_bounds__(WPR > 4 ? 64 * WPR : 256) row_vec_kernel(RowAr
     for (int i = 0; i < VPL; ++i)
 #pragma unroll
       for (int j = 0; j < EV; ++j) s += vec_elem<DT>(raw[i], j);
-    s = group_sum<WPR>(s, red);
+    s = group_sum_once<WPR>(s, red);
     const float mean = s / (float)cols;
     float vs = 0.f;
 #pragma unroll
@@ -344,7 +384,7 @@ __global__ void __launch_bounds__(WPR > 4 ? 64 * WPR : 256) row_vec_kernel(RowAr
           vs += d * d;
         }
       }
-    vs = group_sum<WPR>(vs, red);
+    vs = group_sum_once<WPR>(vs, red + NRED);
     scale = 1.0f / sqrtf(vs / (float)cols + a.eps);
     shift = mean;
     if (threadIdx.x == (WPR == 1 ? wave * 64 : 0)) {
