@@ -137,21 +137,22 @@ static int num_cus() {
 }
 int gemm_num_cus() { return num_cus(); }
 
-// The clock hook's per-device counters (null: off).
-static unsigned long long* g_clk[64];
+// The clock hook's per-device counters (null: off).  Launching threads read
+// them while the API thread sets them, hence atomics.
+static std::atomic<unsigned long long*> g_clk[64];
 static std::atomic<int> g_clk_on{0};
 void gemm_clock_target(int dev, unsigned long long* clk) {
   if (dev < 0 || dev >= 64) return;
-  g_clk[dev] = clk;
+  g_clk[dev].store(clk, std::memory_order_release);
   int on = 0;
-  for (int d = 0; d < 64; ++d) on |= g_clk[d] != nullptr;
+  for (int d = 0; d < 64; ++d) on |= g_clk[d].load(std::memory_order_relaxed) != nullptr;
   g_clk_on.store(on, std::memory_order_release);
 }
 static unsigned long long* clock_target() {
   if (!g_clk_on.load(std::memory_order_acquire)) return nullptr;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-  return g_clk[dev];
+  return g_clk[dev].load(std::memory_order_acquire);
 }
 
 // Untuned choice: estimated time = rounds * occ * tile_area / rate, where a
