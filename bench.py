@@ -1018,6 +1018,72 @@ def gemv_ab(hx, rounds: int = 5, iters: int = 400) -> str:
     return "\n".join(lines) + "\n"
 
 
+def rows_ab(hx, rounds: int = 5, iters: int = 60) -> str:
+    """Interleaved A/B of the row configurations (one row per workgroup
+    against the streaming form at 2, 4 and 8 workgroups per CU), pinned
+    through hx_config_select, for softmax, RMSNorm and LayerNorm at the C4
+    shape and at longer rows: every round times every configuration once
+    (one region of ``iters`` launches rotating over input / output sets of
+    more than 600 MB, so the MALL cannot serve them); the table gives the
+    median and q20 / q80 over the rounds, and checks every configuration's
+    output against the one-row form bit for bit.  Markdown on stdout."""
+    import numpy as np
+    import torch
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(78)
+    fams = {"softmax": 9, "rmsnorm": 10, "layernorm": 11}
+    names = [hx.config_get(9, i)["name"] for i in range(hx.config_count(9))]
+    code = {torch.float16: 1, torch.bfloat16: 2, torch.float32: 3}
+    lines = ["# Row configurations: interleaved A/B (bench.py --rows-ab)", "",
+             f"Every round times each configuration once ({iters} launches rotating over input / output sets of "
+             f"more than 600 MB; HIP events); {rounds} rounds; us per launch, median [q20, q80] over the rounds.  "
+             "`*` marks the untuned default.  Every configuration's output equals the one-row form's bit for bit.",
+             "", "| op | dtype | rows x cols | " + " | ".join(names) + " |", "|---|---|---|" + "---:|" * len(names)]
+    for R, C, dt in ((8192, 4096, torch.float16), (8192, 4096, torch.bfloat16), (8192, 4096, torch.float32),
+                     (2048, 4096, torch.float16), (4096, 8192, torch.float16), (4096, 16384, torch.float16),
+                     (4096, 32768, torch.float16)):
+        nbytes = R * C * torch.tensor([], dtype=dt).element_size()
+        sets = max(2, -(-(600 << 20) // (2 * nbytes)))
+        xs = [(torch.randn((R, C), device=dev, generator=g) * 2.0).to(dt) for _ in range(sets)]
+        ys = [torch.empty_like(x) for x in xs]
+        gam = (torch.randn(C, device=dev, generator=g) * 0.1 + 1.0).to(dt)
+        bet = (torch.randn(C, device=dev, generator=g) * 0.1).to(dt)
+        try:
+            for op, fam in fams.items():
+                hx.config_select(fam, R, C, code[dt], -1)
+                default = names[hx.config_lookup(fam, R, C, code[dt])]
+                calls = [hx.bind_row_op(op, x, y, weight=None if op == "softmax" else gam,
+                                        bias=bet if op == "layernorm" else None) for x, y in zip(xs, ys)]
+                t = {c: [] for c in names}
+                ref = None
+                try:
+                    for i, c in enumerate(names):
+                        hx.config_select(fam, R, C, code[dt], i)
+                        calls[0]()
+                        torch.cuda.synchronize()
+                        out = ys[0].view(torch.uint8).clone()
+                        if ref is None:
+                            ref = out
+                        elif not torch.equal(out, ref):
+                            raise RuntimeError(f"rows A/B: {op} {c} differs from {names[0]} at {R}x{C} {dt}")
+                    for _ in range(rounds):
+                        for i, c in enumerate(names):
+                            hx.config_select(fam, R, C, code[dt], i)
+                            t[c].append(event_timed(calls, iters, regions=1)[0] * 1e3)
+                finally:
+                    hx.config_select(fam, R, C, code[dt], -1)
+                cells = []
+                for c in names:
+                    r = np.asarray(t[c])
+                    cells.append(f"{np.median(r):.2f} [{np.quantile(r, 0.2):.2f}, {np.quantile(r, 0.8):.2f}]"
+                                 + (" *" if c == default else ""))
+                lines.append(f"| {op} | {str(dt)[6:]} | {R} x {C} | " + " | ".join(cells) + " |")
+        finally:
+            del xs, ys
+            torch.cuda.empty_cache()
+    return "\n".join(lines) + "\n"
+
+
 def pmc_workload(hx, keys_path=None) -> None:
     """A few launches of every benchmarked kernel -- every compiled config of
     the headline GEMM and of the decode GEMV, so whichever one the tuner
@@ -1112,7 +1178,7 @@ def pmc_workload(hx, keys_path=None) -> None:
 
 
 #: kernels the counter parsers read, in pmc_workload's launch order
-MEASURED_KERNELS = r"void hx::(gemm_kernel|gemm_generic_kernel|gemv_stream_kernel|row_vec_kernel|row_kernel)<"
+MEASURED_KERNELS = r"void hx::(gemm_kernel|gemm_generic_kernel|gemv_stream_kernel|row_vec_kernel|row_stream_kernel|row_kernel)<"
 
 
 def pmc_sequence(hx):
@@ -1476,6 +1542,8 @@ def main() -> int:
                     help="launch each benchmarked kernel a few times for rocprofv3 --pmc")
     ap.add_argument("--gemv-ab", action="store_true",
                     help="interleaved A/B of the decode GEMV default candidates, markdown on stdout, exit")
+    ap.add_argument("--rows-ab", action="store_true",
+                    help="interleaved A/B of the row configurations, markdown on stdout, exit")
     ap.add_argument("--ceilings", action="store_true",
                     help="time the libhxprobe probes (launch gap, read, copy, MFMA issue), print JSON, exit")
     ap.add_argument("--pmc-keys", metavar="JSON",
@@ -1517,6 +1585,9 @@ def main() -> int:
         return 0
     if args.gemv_ab:
         print(gemv_ab(hx), end="", flush=True)
+        return 0
+    if args.rows_ab:
+        print(rows_ab(hx), end="", flush=True)
         return 0
     if args.pmc_workload:
         pmc_workload(hx, args.pmc_keys)

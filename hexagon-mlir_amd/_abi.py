@@ -21,9 +21,11 @@ ERRORS = {
 }
 OP_GEMM_I8, OP_MATMUL_F16, OP_MATMUL_BF16, OP_MATMUL_W8, OP_SWIGLU_W8, OP_GEMV_W8 = 1, 2, 3, 4, 5, 6
 OP_GEMV_F16, OP_GEMV_BF16 = 7, 8
+OP_SOFTMAX, OP_RMSNORM, OP_LAYERNORM = 9, 10, 11  # row families: (m, n, k) = (rows, cols, dtype)
 OP_NAMES = {OP_GEMM_I8: "gemm_i8", OP_MATMUL_F16: "matmul_f16", OP_MATMUL_BF16: "matmul_bf16",
             OP_MATMUL_W8: "matmul_w8", OP_SWIGLU_W8: "swiglu_w8", OP_GEMV_W8: "gemv_w8",
-            OP_GEMV_F16: "gemv_f16", OP_GEMV_BF16: "gemv_bf16"}
+            OP_GEMV_F16: "gemv_f16", OP_GEMV_BF16: "gemv_bf16", OP_SOFTMAX: "softmax",
+            OP_RMSNORM: "rmsnorm", OP_LAYERNORM: "layernorm"}
 
 
 class MemRef2D(ctypes.Structure):

@@ -436,10 +436,19 @@ bool hx::gemv_op(int op) {
   return op == HX_OP_GEMV_W8 || op == HX_OP_GEMV_F16 || op == HX_OP_GEMV_BF16;
 }
 
+// The row families (softmax, RMSNorm, LayerNorm), keyed (rows, cols, dtype).
+bool hx::row_family(int op) {
+  return op == HX_OP_SOFTMAX || op == HX_OP_RMSNORM || op == HX_OP_LAYERNORM;
+}
+
 // Table indices (into the mode's table) of the configs of one family.
 std::vector<int> hx::family_indices(int op) {
   std::vector<int> out;
   int mode, epi;
+  if (row_family(op)) {
+    for (int i = 0; i < row_config_count(); ++i) out.push_back(i);
+    return out;
+  }
   if (gemv_op(op)) {
     for (int i = 0; i < gemv_packed_config_count(); ++i) out.push_back(i);
     return out;
@@ -567,7 +576,20 @@ static int resolve_gemv(int op, int64_t M, int64_t N, int64_t K, bool* was_pinne
   return gemv_untuned(op, M, N, K, in_place);
 }
 
+// RowOpCode of a row family.
+static int row_op_code(int op) {
+  return op == HX_OP_SOFTMAX ? ROW_OP_SOFTMAX : op == HX_OP_RMSNORM ? ROW_OP_RMSNORM : ROW_OP_LAYERNORM;
+}
+
+// Row configuration a call runs with: the pinned one, else the default.
+static int resolve_row(int op, int64_t rows, int64_t cols, int dtype) {
+  const int pin = pinned(op, rows, cols, dtype);
+  if (pin >= 0 && pin < row_config_count()) return pin;
+  return row_default_config(row_op_code(op), dtype, rows, cols);
+}
+
 int hx::untuned_family_index(int op, int64_t m, int64_t n, int64_t k) {
+  if (row_family(op)) return row_default_config(row_op_code(op), (int)k, m, n);
   if (gemv_op(op)) return gemv_untuned(op, m, n, k);
   int mode, epi;
   if (!op_gemm(op, &mode, &epi)) return -1;
@@ -1028,7 +1050,8 @@ extern "C" int hx_softmax(const hx_memref2d* x, hx_memref2d* y, int dtype, hx_st
   if (vx.rows != vy.rows || vx.cols != vy.cols) return fail(HX_ERR_SHAPE, "hx_softmax: x/y shape");
   if (vx.rows == 0 || vx.cols == 0) return HX_OK;
   const hipStream_t s = (hipStream_t)stream;
-  rc = launch_softmax(dtype, vx.p, vx.ld, vy.p, vy.ld, vx.rows, vx.cols, s);
+  rc = launch_softmax(dtype, vx.p, vx.ld, vy.p, vy.ld, vx.rows, vx.cols, s,
+                      resolve_row(HX_OP_SOFTMAX, vx.rows, vx.cols, dtype));
   if (rc == HXI_ERR_UNSUPPORTED)
     return run_row_long(ROW_OP_SOFTMAX, dtype, vx, nullptr, nullptr, 0.f, vy, nullptr, nullptr, s, "softmax");
   return map_internal(rc, "softmax");
@@ -1045,7 +1068,8 @@ extern "C" int hx_rmsnorm(const hx_memref2d* x, const hx_memref1d* gamma, float 
   if (gamma && (rc = view1(gamma, dtype, "gamma", vx.cols, &vg))) return rc;
   if (vx.rows == 0 || vx.cols == 0) return HX_OK;
   const hipStream_t s = (hipStream_t)stream;
-  rc = launch_rmsnorm(dtype, vx.p, vx.ld, gamma ? vg.p : nullptr, eps, vy.p, vy.ld, vx.rows, vx.cols, s);
+  rc = launch_rmsnorm(dtype, vx.p, vx.ld, gamma ? vg.p : nullptr, eps, vy.p, vy.ld, vx.rows, vx.cols, s,
+                      resolve_row(HX_OP_RMSNORM, vx.rows, vx.cols, dtype));
   if (rc == HXI_ERR_UNSUPPORTED)
     return run_row_long(ROW_OP_RMSNORM, dtype, vx, gamma ? vg.p : nullptr, nullptr, eps, vy, nullptr, nullptr, s,
                         "rmsnorm");
@@ -1070,7 +1094,7 @@ extern "C" int hx_layernorm(const hx_memref2d* x, const hx_memref1d* w, const hx
   float* mp = mean ? (float*)vm.p : nullptr;
   float* rp = rstd ? (float*)vr.p : nullptr;
   rc = launch_layernorm(dtype, vx.p, vx.ld, w ? vw.p : nullptr, b ? vb.p : nullptr, eps, vy.p, vy.ld, mp, rp,
-                        vx.rows, vx.cols, s);
+                        vx.rows, vx.cols, s, resolve_row(HX_OP_LAYERNORM, vx.rows, vx.cols, dtype));
   if (rc == HXI_ERR_UNSUPPORTED)
     return run_row_long(ROW_OP_LAYERNORM, dtype, vx, w ? vw.p : nullptr, b ? vb.p : nullptr, eps, vy, mp, rp, s,
                         "layernorm");
@@ -1621,6 +1645,14 @@ extern "C" int hx_config_get(int op, int index, hx_kernel_config* out) {
   memset(out, 0, sizeof(*out));
   out->op = op;
   out->index = index;
+  if (row_family(op)) {
+    // lds_bytes: the two alternating exchange buffers of 2 x 4 floats
+    out->col_tiles = row_config_per_cu(index);
+    out->waves_m = out->col_tiles ? 4 : 0;
+    out->lds_bytes = out->col_tiles ? 64 : 32;
+    snprintf(out->name, sizeof(out->name), "%s", row_config_name(index));
+    return HX_OK;
+  }
   if (gemv_op(op)) {
     const GemvConfig* c = gemv_packed_config(idx[index]);
     // bm: activation rows one launch covers (16-row blocks); lds_bytes: the
@@ -1665,6 +1697,7 @@ extern "C" int hx_config_select(int op, int64_t m, int64_t n, int64_t k, int ind
 static const char* config_name(int op, int index) {
   std::vector<int> idx = family_indices(op);
   if (index < 0 || index >= (int)idx.size()) return nullptr;
+  if (row_family(op)) return row_config_name(index);
   if (gemv_op(op)) return gemv_packed_config(idx[index])->name;
   int mode, epi;
   op_gemm(op, &mode, &epi);
@@ -1752,6 +1785,10 @@ extern "C" int hx_config_lookup(int op, int64_t m, int64_t n, int64_t k, int* in
   int dev;
   int rc = current_device(&dev);
   if (rc) return rc;
+  if (row_family(op)) {
+    *index = resolve_row(op, m, n, (int)k);
+    return HX_OK;
+  }
   if (gemv_op(op)) {
     *index = resolve_gemv(op, m, n, k);
     return HX_OK;

@@ -18,6 +18,9 @@ int api_fail(int code, const char* fmt, ...);
 bool op_gemm(int op, int* mode, int* epi);
 // The decode GEMV families (int8, f16, bf16 weights share one table).
 bool gemv_op(int op);
+// The row families (softmax, RMSNorm, LayerNorm): one shared table of row
+// configurations, keyed (m, n, k) = (rows, cols, dtype).
+bool row_family(int op);
 // Table indices (into the mode's config table, or the GEMV table) of the
 // configurations of family `op`, in family-index order.
 std::vector<int> family_indices(int op);

@@ -20,19 +20,28 @@ enum : int {
 };
 
 // ---- row kernels (hx_rows.hip) -------------------------------------------
+// cfg: an index into the row configurations (row_config_*), -1 for the
+// untuned default of the shape.
 int launch_softmax(int dtype, const void* x, int64_t ldx, void* y, int64_t ldy,
-                   int64_t rows, int64_t cols, hipStream_t s);
+                   int64_t rows, int64_t cols, hipStream_t s, int cfg = -1);
 int launch_rmsnorm(int dtype, const void* x, int64_t ldx, const void* gamma, float eps,
-                   void* y, int64_t ldy, int64_t rows, int64_t cols, hipStream_t s);
+                   void* y, int64_t ldy, int64_t rows, int64_t cols, hipStream_t s, int cfg = -1);
 int launch_layernorm(int dtype, const void* x, int64_t ldx, const void* w, const void* b,
                      float eps, void* y, int64_t ldy, float* mean, float* rstd,
-                     int64_t rows, int64_t cols, hipStream_t s);
+                     int64_t rows, int64_t cols, hipStream_t s, int cfg = -1);
 int launch_silu_mul_f16(const void* g, int64_t ldg, const void* u, int64_t ldu, void* o,
                         int64_t ldo, int64_t rows, int64_t cols, hipStream_t s);
 // Rows longer than the launches above hold in registers (they return
 // HXI_ERR_UNSUPPORTED without launching): two streaming passes, with
 // row_long_ws_bytes() of per-segment statistics in `ws`.
 enum RowOpCode : int { ROW_OP_SOFTMAX = 0, ROW_OP_RMSNORM = 1, ROW_OP_LAYERNORM = 2 };
+// Row configurations: index 0 runs one row per workgroup; the others run the
+// streaming form with row_config_per_cu() workgroups per CU.
+int row_config_count();
+const char* row_config_name(int cfg);
+int row_config_per_cu(int cfg);
+// Untuned choice (op: RowOpCode, dtype: HX_* code).
+int row_default_config(int op, int dtype, int64_t rows, int64_t cols);
 size_t row_long_ws_bytes(int dtype, int64_t rows, int64_t cols);
 int launch_row_long(int op, int dtype, const void* x, int64_t ldx, const void* w, const void* b, float eps,
                     void* y, int64_t ldy, float* mean, float* rstd, int64_t rows, int64_t cols, void* ws,

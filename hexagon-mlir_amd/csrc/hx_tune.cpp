@@ -520,6 +520,8 @@ extern "C" int hx_tune(int op, int64_t m, int64_t n, int64_t k, const hx_tune_op
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return api_fail(HX_ERR_NODEVICE, "hx_tune: no device");
   if (family_indices(op).empty()) return api_fail(HX_ERR_ARG, "hx_tune: unknown op %d", op);
+  if (row_family(op))
+    return api_fail(HX_ERR_UNSUPPORTED, "hx_tune: row family %d is not tuned (pin it with hx_config_select)", op);
   if (family_indices(op).size() > HX_TUNE_MAX_ENTRIES)
     return api_fail(HX_ERR_UNSUPPORTED, "hx_tune: family %d has more than %d configs", op, HX_TUNE_MAX_ENTRIES);
 

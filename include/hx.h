@@ -278,7 +278,10 @@ enum {
     HX_OP_SWIGLU_W8 = 5,    /* fused gate/up GEMM of hx_swiglu_ffn */
     HX_OP_GEMV_W8 = 6,      /* W8A16 decode GEMV (M <= 16) */
     HX_OP_GEMV_F16 = 7,     /* f16 x f16 decode GEMV (M <= 16), same configs as 6 */
-    HX_OP_GEMV_BF16 = 8     /* bf16 x bf16 decode GEMV (M <= 16), same configs as 6 */
+    HX_OP_GEMV_BF16 = 8,    /* bf16 x bf16 decode GEMV (M <= 16), same configs as 6 */
+    HX_OP_SOFTMAX = 9,      /* hx_softmax; row families: m = rows, n = cols, k = dtype */
+    HX_OP_RMSNORM = 10,     /* hx_rmsnorm */
+    HX_OP_LAYERNORM = 11    /* hx_layernorm */
 };
 
 /* One compiled configuration.  GEMM families fill bm/bn/bk (K elements per
@@ -287,7 +290,14 @@ enum {
  * families fill col_tiles (16-column tiles per workgroup), waves_m (waves
  * splitting K inside a workgroup) and split_k (workgroups splitting K per
  * group of col_tiles tiles, the last of them to finish adding the parts;
- * 1: none).
+ * 1: none).  The row families (softmax, RMSNorm, LayerNorm) fill col_tiles
+ * with the workgroups per CU of the streaming form ("stream_N": a grid of
+ * N workgroups per CU walks the rows, gamma / beta resident, two rows in
+ * flight per workgroup) or 0 ("row": one row per workgroup); waves_m is the
+ * streaming form's waves per row.  Every row configuration computes the
+ * same bits; rows that the streaming form does not take (under 4 KiB, over
+ * 64 KiB, unaligned) run "row" whatever is pinned.  hx_tune does not time
+ * row families: pin them with hx_config_select.
  * Replaces the (BM, BN, BK) tile space of enumerate_tile_configs
  * (QHB/backend/hmx_search.py:246-332), widened to the knobs that matter on
  * gfx950. */

@@ -68,7 +68,7 @@ def test_dtype_errors_are_reported_before_any_launch(hx):
 
 def test_config_surface(hx):
     total = 0
-    for op in range(1, 9):
+    for op in range(1, 12):
         n = hx.config_count(op)
         assert n >= 3
         for i in range(n):
@@ -81,8 +81,14 @@ def test_config_surface(hx):
     names = [[hx.config_get(op, i)["name"] for i in range(hx.config_count(op))] for op in (6, 7, 8)]
     assert names[0] == names[1] == names[2]
     assert hx.config_get(6, 0)["bk"] == 64 and hx.config_get(7, 0)["bk"] == 32
+    # the three row families (softmax, RMSNorm, LayerNorm) share one table:
+    # one row per workgroup, then the streaming form at 2, 4, 8 per CU
+    rows = [[hx.config_get(op, i) for i in range(hx.config_count(op))] for op in (9, 10, 11)]
+    assert [c["name"] for c in rows[0]] == [c["name"] for c in rows[1]] == [c["name"] for c in rows[2]]
+    assert [(c["name"], c["col_tiles"]) for c in rows[0]] == [("row", 0), ("stream_2", 2), ("stream_4", 4),
+                                                              ("stream_8", 8)]
     with pytest.raises(hx.HXError):
-        hx.config_count(9)
+        hx.config_count(12)
 
 
 def test_missing_library_fails_loudly(hx, monkeypatch, tmp_path):

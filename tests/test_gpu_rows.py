@@ -212,3 +212,85 @@ def test_layernorm_c4_ulps(hx, dev, dtype):
     assert rel < (1e-3 if dtype == "f16" else 4e-3), rel
     assert_close(to_np(mean), wm, 1e-5, 1e-5, "mean")
     assert_close(to_np(rstd), wr, 1e-4, 1e-5, "rstd")
+
+
+# (rows, cols): odd row counts around the streaming grid, fewer rows than the
+# grid, 2 / 4 / 8 / 16 vectors per lane in f16, a row the streaming form does
+# not take (1000 columns), and a strided view
+ROW_CFG_SHAPES = [(2085, 4096), (3, 4096), (1030, 8192), (517, 16384), (300, 32768), (700, 1000)]
+DT_CODE = {"f16": 1, "bf16": 2, "f32": 3}
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("op", ["softmax", "rmsnorm", "layernorm"])
+def test_row_configs_bit_equal(hx, dev, op, dtype):
+    """Every row configuration (one row per workgroup, the streaming form at
+    2, 4 and 8 workgroups per CU), pinned through hx_config_select, writes
+    the same bits as the one-row form -- outputs, and LayerNorm's mean and
+    rstd -- and the one-row form agrees with the oracle; views whose outer
+    stride exceeds the row are read and written only inside the view."""
+    import torch
+    fam = {"softmax": 9, "rmsnorm": 10, "layernorm": 11}[op]
+    n_cfg = hx.config_count(fam)
+    for rows, cols in ROW_CFG_SHAPES + [(2100, 4096 + 64)]:
+        strided = cols == 4096 + 64
+        xh, _ = make(dtype, (rows, cols), seed=rows + cols, mean=0.25)
+        gh, _ = make(dtype, (cols,), sigma=0.2, mean=1.0, seed=11)
+        bh, _ = make(dtype, (cols,), sigma=0.2, seed=12)
+        xt = to_torch(xh, dtype, dev)
+        width = cols - 64 if strided else cols
+        if strided:
+            xt = xt[:, :width]
+            gh, bh = gh[:width], bh[:width]
+        gt, bt = to_torch(np.ascontiguousarray(gh), dtype, dev), to_torch(np.ascontiguousarray(bh), dtype, dev)
+
+        def run(idx):
+            hx.config_select(fam, rows, width, DT_CODE[dtype], idx)
+            try:
+                full = torch.full((rows, cols), 3.0, dtype=xt.dtype, device=dev)
+                y = full[:, :width]
+                stats = ()
+                if op == "softmax":
+                    hx.softmax(xt, out=y)
+                elif op == "rmsnorm":
+                    hx.rms_norm(xt, gt, eps=1e-6, out=y)
+                else:
+                    _, m, r = hx.layer_norm(xt, gt, bt, eps=1e-5, out=y, return_stats=True)
+                    stats = (to_np(m), to_np(r))
+                return to_np(full), stats
+            finally:
+                hx.config_select(fam, rows, width, DT_CODE[dtype], -1)
+
+        base, base_stats = run(0)
+        if strided:
+            assert (values(base[:, width:], dtype) == 3.0).all(), "wrote outside the view"
+        for idx in range(1, n_cfg):
+            got, stats = run(idx)
+            name = hx.config_get(fam, idx)["name"]
+            assert np.array_equal(got.view(np.uint8), base.view(np.uint8)), (op, dtype, rows, cols, name)
+            for a, b in zip(stats, base_stats):
+                assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), (op, dtype, rows, cols, name, "stats")
+        if rows * width <= 2100 * 4096 and not strided:
+            xs = np.ascontiguousarray(xh)
+            if op == "softmax":
+                want = oracle.softmax(xs, bf16=(dtype == "bf16"))
+            elif op == "rmsnorm":
+                want = oracle.rmsnorm(xs, gh, 1e-6, bf16=(dtype == "bf16"))
+            else:
+                want = oracle.layernorm(xs, gh, bh, 1e-5, bf16=(dtype == "bf16"))[0]
+            rtol, atol = TOL[dtype]
+            assert_close(values(base, dtype), values(want, dtype), rtol, atol, f"{op} {dtype} {rows}x{cols}")
+
+
+def test_row_default_configs(hx, dev):
+    """The untuned choice: the norms stream at 4 KiB-or-longer rows once there
+    are two rows per workgroup of the grid; softmax runs one row per
+    workgroup."""
+    cus = __import__("torch").cuda.get_device_properties(0).multi_processor_count
+    look = lambda fam, r, c, dt=1: hx.config_get(fam, hx.config_lookup(fam, r, c, dt))["name"]  # noqa: E731
+    assert look(9, 8192, 4096) == "row"
+    assert look(10, 8192, 4096) == "stream_4" and look(11, 8192, 4096) == "stream_4"
+    assert look(10, 2 * 4 * cus - 1, 4096) == "row"
+    assert look(10, 4096, 8192) == "stream_2" and look(11, 4096, 32768) == "stream_2"
+    assert look(10, 8192, 1024) == "row"      # 2 KiB rows: one wave per row
+    assert look(10, 8192, 4096, 3) == "stream_2"  # f32: 16 KiB rows
