@@ -123,17 +123,21 @@ const GemmConfig* gemm_config(int mode, int idx) {
 }
 
 int gemm_num_cus();
-static int g_num_cus = 0;
+// CU count of the device (read once; every thread that races to read it
+// stores the same value).
+static std::atomic<int> g_num_cus{0};
 static int num_cus() {
-  if (g_num_cus == 0) {
+  int n = g_num_cus.load(std::memory_order_relaxed);
+  if (n == 0) {
     int dev = 0, v = 0;
     if (hipGetDevice(&dev) == hipSuccess &&
         hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-      g_num_cus = v;
+      n = v;
     else
-      g_num_cus = 256;
+      n = 256;
+    g_num_cus.store(n, std::memory_order_relaxed);
   }
-  return g_num_cus;
+  return n;
 }
 int gemm_num_cus() { return num_cus(); }
 

@@ -533,9 +533,28 @@ gemm_kernel(GemmArgs p) {
   // The MFMAs of one k-step.  B is the first operand, so the accumulators
   // hold C transposed: lane (lrow, lg) of sub-tile (i, j) holds row lrow and
   // the four consecutive columns 8*g + 4*lg + (0..3) in registers 4g..4g+3.
+  // Order (int8 / f16 / bf16): the A fragment fixed across the TN MFMAs of
+  // a row of sub-tiles, the B fragments walked back and forth so each row
+  // starts with the B fragment the previous one ended with (measured at
+  // 4096^3 int8, interleaved in one process: 58.5 against 59.1 us on random
+  // operands, 40.1 against 40.8 on zeros, against B fixed and A walked).
+  // W8 widens each B fragment once per k-step and keeps B fixed instead.
   auto mfmas = [&](auto ksc) __attribute__((always_inline)) {
     constexpr int ks = decltype(ksc)::value;
     constexpr int s = ks & 1;
+    if constexpr (MODE != GM_W8) {
+      static_for<NB>([&](auto nbc) {
+        constexpr int nb = decltype(nbc)::value;
+        static_for<TM>([&](auto ic) {
+          constexpr int i = decltype(ic)::value;
+          static_for<TN>([&](auto jc) {
+            constexpr int j = (i & 1) ? TN - 1 - decltype(jc)::value : decltype(jc)::value;
+            acc[nb][i][j] = mfma32<MODE>(fb[s][nb][j], fa[s][i], acc[nb][i][j]);
+          });
+        });
+      });
+      return;
+    }
     static_for<NB>([&](auto nbc) {
       constexpr int nb = decltype(nbc)::value;
       static_for<TN>([&](auto jc) {
