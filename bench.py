@@ -1454,6 +1454,19 @@ def ceilings(hx=None) -> dict:
         out[f"mfma_i8_4waves_{nr}_lds_per_16"] = {
             "us_per_launch": round(ms * 1e3, 2), "TOPS": round(ops.value / (ms * 1e-3) / 1e12, 1),
             "frac_of_5000": round(ops.value / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
+    # the GEMM's interleaved schedule against ping-pong (two groups of four
+    # waves alternating MFMA and read bursts between workgroup barriers)
+    lib.hxp_mfma_sched_i8.argtypes = [ci, ci, ci, vp, ctypes.POINTER(ctypes.c_double), vp]
+    sched = {0: ("interleaved", 1, 4096), 1: ("interleaved", 2, 2048), 2: ("pingpong", 1, 4096),
+             3: ("pingpong_setprio", 1, 4096), 4: ("pingpong", 2, 2048), 5: ("pingpong_setprio", 2, 2048),
+             6: ("pingpong_setprio", 4, 1024)}
+    for kind, (name, rounds, phases) in sched.items():
+        call = lambda kind=kind, phases=phases: lib.hxp_mfma_sched_i8(  # noqa: E731
+            kind, 256, phases, ctypes.c_void_p(sink.data_ptr()), ctypes.byref(ops), stream())
+        ms, _ = event_timed([call], 20)
+        out[f"mfma_i8_6_lds_per_8_{name}_{8 * rounds}_mfma_per_phase"] = {
+            "us_per_launch": round(ms * 1e3, 2), "TOPS": round(ops.value / (ms * 1e-3) / 1e12, 1),
+            "frac_of_5000": round(ops.value / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4)}
     if hx is not None:
         out.update(operand_data_ceiling(hx))
     return out

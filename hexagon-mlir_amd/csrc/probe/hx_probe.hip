@@ -121,7 +121,121 @@ __global__ void __launch_bounds__(256) probe_mfma4_kernel(int iters, int* out) {
   if (s == 0x5eed1234) out[blockIdx.x] = s;
 }
 
+// Two schedules of the same work: 8 waves, 8 int8 MFMA chains each, 6
+// 16-byte LDS operand reads per 8 MFMAs (the GEMM's 128x64 wave tile), the
+// operands of R rounds of 8 MFMAs read ahead.
+// Ping-pong: waves 0-3 and 4-7 (one of each per SIMD) alternate an MFMA
+// burst of R rounds with the read burst for their next one, workgroup
+// barriers between the phases and the second group one phase behind
+// (PRIO: the MFMA burst at raised wave priority).  Every wave passes the
+// same number of barriers.
+template <int R, int PRIO>
+__global__ void __launch_bounds__(512) probe_pingpong_kernel(int phases, int* out) {
+  __shared__ v4i tile[4096];
+  const int lane = threadIdx.x & 63;
+  for (int i = threadIdx.x; i < 4096; i += 512) tile[i] = v4i{i, i + 1, i + 2, i + 3};
+  __syncthreads();
+  const int grp = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8));
+  v4i a[R][2], b[R][4];
+  for (int r = 0; r < R; ++r) {
+    for (int i = 0; i < 2; ++i) a[r][i] = v4i{lane + i + r, 1, 2, 3};
+    for (int j = 0; j < 4; ++j) b[r][j] = v4i{j + r, lane, 5, 7};
+  }
+  v16i acc[8];
+  for (int t = 0; t < 8; ++t) acc[t] = v16i{};
+  const int base = (threadIdx.x * 5) & 4095;
+  if (grp == 1) __builtin_amdgcn_s_barrier();
+  for (int ph = 0; ph < phases; ++ph) {
+    // memory phase: the next compute phase's operands
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int q = 0; q < 6; ++q) {
+        const v4i t = tile[(base + 64 * (6 * r + q) + ph) & 4095];
+        if (q < 2) a[r][q] ^= t;
+        else b[r][q - 2] ^= t;
+      }
+    __builtin_amdgcn_s_barrier();
+    if (PRIO) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[4 * i + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[r][i], b[r][j], acc[4 * i + j], 0, 0, 0);
+    if (PRIO) __builtin_amdgcn_s_setprio(0);
+    __builtin_amdgcn_s_barrier();
+  }
+  if (grp == 0) __builtin_amdgcn_s_barrier();
+  int s = 0;
+  for (int t = 0; t < 8; ++t)
+    for (int r = 0; r < 16; ++r) s += acc[t][r];
+  if (s == 0x5eed1234) out[blockIdx.x] = s;
+}
+
+// Interleaved: every wave spreads the reads of its next R rounds between
+// the MFMAs of these (the GEMM kernel's schedule), no group barriers.
+template <int R>
+__global__ void __launch_bounds__(512) probe_interleave_kernel(int phases, int* out) {
+  __shared__ v4i tile[4096];
+  const int lane = threadIdx.x & 63;
+  for (int i = threadIdx.x; i < 4096; i += 512) tile[i] = v4i{i, i + 1, i + 2, i + 3};
+  __syncthreads();
+  v4i a[2][R][2], b[2][R][4];
+  for (int s = 0; s < 2; ++s)
+    for (int r = 0; r < R; ++r) {
+      for (int i = 0; i < 2; ++i) a[s][r][i] = v4i{lane + i + r + s, 1, 2, 3};
+      for (int j = 0; j < 4; ++j) b[s][r][j] = v4i{j + r + s, lane, 5, 7};
+    }
+  v16i acc[8];
+  for (int t = 0; t < 8; ++t) acc[t] = v16i{};
+  const int base = (threadIdx.x * 5) & 4095;
+  for (int ph = 0; ph < phases; ph += 2) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            acc[4 * i + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[s][r][i], b[s][r][j], acc[4 * i + j], 0, 0, 0);
+            const int q = 4 * i + j;
+            if (q < 6) {
+              const v4i t = tile[(base + 64 * (6 * r + q) + ph + s) & 4095];
+              if (q < 2) a[s ^ 1][r][q] ^= t;
+              else b[s ^ 1][r][q - 2] ^= t;
+            }
+          }
+  }
+  int s = 0;
+  for (int t = 0; t < 8; ++t)
+    for (int r = 0; r < 16; ++r) s += acc[t][r];
+  if (s == 0x5eed1234) out[blockIdx.x] = s;
+}
+
 extern "C" {
+// blocks x 512 threads: the schedules above (kind 0, 1: interleaved, 1 or 2
+// rounds read ahead; 2..6: ping-pong with R = 1, 1, 2, 2, 4 rounds per
+// phase, the odd kinds and 6 with raised priority); `phases` phases of R
+// rounds; int8 ops per launch in *ops
+int hxp_mfma_sched_i8(int kind, int blocks, int phases, int* out, double* ops, hipStream_t s) {
+  int r = 0;
+  switch (kind) {
+    case 0: probe_interleave_kernel<1><<<blocks, 512, 0, s>>>(phases, out); r = 1; break;
+    case 1: probe_interleave_kernel<2><<<blocks, 512, 0, s>>>(phases, out); r = 2; break;
+    case 2: probe_pingpong_kernel<1, 0><<<blocks, 512, 0, s>>>(phases, out); r = 1; break;
+    case 3: probe_pingpong_kernel<1, 1><<<blocks, 512, 0, s>>>(phases, out); r = 1; break;
+    case 4: probe_pingpong_kernel<2, 0><<<blocks, 512, 0, s>>>(phases, out); r = 2; break;
+    case 5: probe_pingpong_kernel<2, 1><<<blocks, 512, 0, s>>>(phases, out); r = 2; break;
+    case 6: probe_pingpong_kernel<4, 1><<<blocks, 512, 0, s>>>(phases, out); r = 4; break;
+    default: return -1;
+  }
+  *ops = (double)blocks * 8 /*waves*/ * phases * r * 8 /*mfma*/ * 65536.0;
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 // blocks x 256 threads (4 waves, 128x128 wave tiles), 0, 4 or 8 LDS reads
 // per 16 MFMAs
 int hxp_mfma4_i8(int blocks, int iters, int lds_reads, int* out, double* ops, hipStream_t s) {
