@@ -755,23 +755,35 @@ def bench_vendor_gemms(hx, inputs, iters: int = 30):
     """The vendor library beside the hand-written kernels on the same
     devices and operands: torch._int_mm (hipBLASLt int8 -> int32) against
     hx_gemm_i8 with the int32 output at 4096^3, and torch.mm (hipBLASLt fp16)
-    against hx_matmul at fp16 4096^3 (B as [N][K] for both).  Timed the same
-    way as every line (HIP events, regions, median)."""
+    against hx_matmul at fp16 4096^3 (B as [N][K] for both).  Each pair is
+    timed alternately, one region of ``iters`` launches each per round over
+    REGIONS rounds, so both see the same clock and thermal state; the
+    figures are the medians over the rounds."""
+    import statistics
     import torch
     a, bt, sa, sb = inputs
     M, K = a.shape
     N = bt.shape[0]
-    out = {"workload": "vendor GEMMs beside hx at 4096^3 (hipBLASLt through torch)", "unit": "us"}
+    out = {"workload": "vendor GEMMs beside hx at 4096^3 (hipBLASLt through torch)", "unit": "us",
+           "timing": f"alternating regions of {iters} launches, median of {REGIONS} rounds"}
+
+    def alternate(fa, fb):
+        ta, tb = [], []
+        for _ in range(REGIONS):
+            ta.append(event_timed([fa], iters, regions=1)[0] * 1e3)
+            tb.append(event_timed([fb], iters, regions=1)[0] * 1e3)
+        return round(statistics.median(ta), 3), round(statistics.median(tb), 3)
+
     c32 = torch.empty((M, N), dtype=torch.int32, device=a.device)
-    hx_i32 = event_timed([hx.bind_gemm_i8(a, bt, c32, b_layout="nk")], iters)
-    out["hx_gemm_i8_i32_us"] = round(hx_i32[0] * 1e3, 3)
+    hx_call = hx.bind_gemm_i8(a, bt, c32, b_layout="nk")
     try:
         btt = bt.t()  # [K, N] view of the [N, K] weight: the column-major B hipBLASLt takes
+        hx_call()
         ref = torch._int_mm(a, btt)
         out["int_mm_equal_to_hx"] = bool(torch.equal(ref, c32))
-        t = event_timed([lambda: torch._int_mm(a, btt)], iters)
-        out["torch_int_mm_i32_us"] = round(t[0] * 1e3, 3)
+        out["hx_gemm_i8_i32_us"], out["torch_int_mm_i32_us"] = alternate(hx_call, lambda: torch._int_mm(a, btt))
     except Exception as e:  # noqa: BLE001
+        out["hx_gemm_i8_i32_us"] = round(event_timed([hx_call], iters)[0] * 1e3, 3)
         out["torch_int_mm_i32_us"] = None
         out["torch_int_mm_error"] = str(e)[:200]
     g = torch.Generator(device=a.device).manual_seed(21)
@@ -779,10 +791,9 @@ def bench_vendor_gemms(hx, inputs, iters: int = 30):
     w = torch.empty((N, K), dtype=torch.float16, device=a.device).uniform_(-1, 1, generator=g)
     y = torch.empty((M, N), dtype=torch.float16, device=a.device)
     y2 = torch.empty_like(y)
-    t_hx = event_timed([lambda: hx.matmul(x, w, b_layout="nk", out=y)], iters)
-    t_mm = event_timed([lambda: torch.mm(x, w.t(), out=y2)], iters)
-    out["hx_matmul_f16_us"] = round(t_hx[0] * 1e3, 3)
-    out["torch_mm_f16_us"] = round(t_mm[0] * 1e3, 3)
+    f_hx = hx.bind_matmul(x, w, y, b_layout="nk")
+    f_hx()
+    out["hx_matmul_f16_us"], out["torch_mm_f16_us"] = alternate(f_hx, lambda: torch.mm(x, w.t(), out=y2))
     out["value"] = out["hx_gemm_i8_i32_us"]
     del x, w, y, y2, c32
     return out
@@ -1555,6 +1566,8 @@ def main() -> int:
                     help="launch each benchmarked kernel a few times for rocprofv3 --pmc")
     ap.add_argument("--gemv-ab", action="store_true",
                     help="interleaved A/B of the decode GEMV default candidates, markdown on stdout, exit")
+    ap.add_argument("--vendor", action="store_true",
+                    help="only the vendor GEMMs beside hx at 4096^3 (for a kernel trace), JSON on stdout, exit")
     ap.add_argument("--rows-ab", action="store_true",
                     help="interleaved A/B of the row configurations, markdown on stdout, exit")
     ap.add_argument("--ceilings", action="store_true",
@@ -1601,6 +1614,14 @@ def main() -> int:
         return 0
     if args.rows_ab:
         print(rows_ab(hx), end="", flush=True)
+        return 0
+    if args.vendor:
+        M = N = K = 4096
+        dev = torch.device("cuda:0")
+        g = torch.Generator(device=dev).manual_seed(1234)
+        a = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev, generator=g)
+        bt = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+        print(json.dumps(bench_vendor_gemms(hx, (a, bt, None, None))), flush=True)
         return 0
     if args.pmc_workload:
         pmc_workload(hx, args.pmc_keys)

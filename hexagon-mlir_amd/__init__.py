@@ -13,7 +13,7 @@ The directory name is not a Python identifier; load it with
 """
 from . import _abi, ops, search  # noqa: F401
 from ._abi import HXError, load  # noqa: F401
-from .ops import (Bound, ResidentWeight, attention, bind_gemm_i8, bind_matmul_resident, bind_row_op,  # noqa: F401
+from .ops import (Bound, ResidentWeight, attention, bind_gemm_i8, bind_matmul, bind_matmul_resident, bind_row_op,  # noqa: F401
                   build_id, clock_probe, clock_read, config_count, config_pins_load, config_pins_save, manifest, manifest_clear, manifest_enable, config_get, config_lookup,  # noqa: F401
                   config_select, gemm_i8, gemv_w8a16, layer_norm, matmul, matmul_resident,
                   rms_norm, silu_mul, softmax, swiglu_ffn)

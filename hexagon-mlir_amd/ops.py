@@ -400,6 +400,13 @@ def bind_gemm_i8(a, b, out, *, b_layout="kn", row_scale=None, col_scale=None) ->
     return Bound(load().hx_gemm_i8, args, (ma, mb, mc, mrs, mcs, a, b, out, row_scale, col_scale))
 
 
+def bind_matmul(a, b, out, *, b_layout="kn") -> Bound:
+    ma, mb, mc = memref2d(a, "a"), memref2d(b, "b"), memref2d(out, "out")
+    args = (ctypes.byref(ma), dtype_code(a), ctypes.byref(mb), dtype_code(b), _LAYOUT[b_layout], None, 0, None, 0,
+            ctypes.byref(mc), dtype_code(out), _stream())
+    return Bound(load().hx_matmul, args, (ma, mb, mc, a, b, out))
+
+
 def bind_matmul_resident(x, w: ResidentWeight, out) -> Bound:
     mx, my = memref2d(x, "x"), memref2d(out, "out")
     args = (ctypes.byref(mx), dtype_code(x), w.handle, None, 0, ctypes.byref(my), dtype_code(out),
