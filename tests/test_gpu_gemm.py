@@ -145,7 +145,7 @@ def test_gemm_i8_4096_cube(hx, dev):
     assert not bad16.any(), f"{int(bad16.sum())} fp16 outputs differ"
 
 
-N_I8_CONFIGS = 17
+N_I8_CONFIGS = 18
 
 
 @pytest.mark.parametrize("K", [1024, 1072, 1152, 208, 144, 112, 32])
