@@ -1317,6 +1317,53 @@ def mfma_from_pmc(pmc_csv: str, keys_json: str, command: str) -> str:
     return "\n".join(lines) + "\n"
 
 
+def gemv_from_pmc(pmc_csv: str, keys_json: str, command: str) -> str:
+    """Markdown summary of the decode-GEMV counters of a ``--pmc-workload``
+    run (every GEMV config at M = 1, 4, 16, N = 11008, K = 4096): per config,
+    the median over its launches of the duration, the launch shape (waves,
+    VGPRs, LDS from the dispatch record), the share of wave-cycles spent
+    waiting, vector-memory read instructions and L1-to-L2 read requests per
+    launch against the weight's 1 KiB chunks, the L1's pending-stall cycles
+    per wave and the texture-addresser busy share."""
+    import statistics
+    disp = _per_dispatch(pmc_csv)
+    xcc = 8
+    chunks = 11008 * 4096 // 1024
+    lines = ["# Decode GEMV counters per config (rocprofv3 --pmc)", "",
+             f"Command: `{command}`", "",
+             "W8A16 GEMV, N = 11008, K = 4096, registered (fragment-packed) weight: 44,032 weight chunks of "
+             "1 KiB, one 16-byte load per lane each. Per config and M, the median over its launches. "
+             "waves = SQ_WAVES; VGPR / AGPR / LDS from the dispatch record; waiting = SQ_WAIT_INST_ANY / "
+             "SQ_WAVE_CYCLES; vmem reads = SQ_INSTS_VMEM_RD (wave instructions, weight and activation); "
+             "L2 requests = TCP_TCC_READ_REQ_sum (64-byte requests from the L1s); pending stall = "
+             "TCP_PENDING_STALL_CYCLES_sum per wave; TA busy = TA_BUSY_avr / (GRBM_GUI_ACTIVE / 8).", "",
+             "| M | config | duration us | waves | VGPR | AGPR | LDS B | waiting | vmem reads / chunk | "
+             "L2 requests / chunk | pending stall / wave | TA busy |",
+             "|---:|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    for key, vals in _group(json.loads(Path(keys_json).read_text()), disp).items():
+        if not key.startswith("gemv_w8a16_m"):
+            continue
+        m = key.split("_m", 1)[1].split(":", 1)[0]
+        cfg = key.split(":", 1)[1].replace("gemv_", "")
+        rec = []
+        for name, c, row in vals:
+            d_ns = int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
+            waves = c.get("SQ_WAVES", float("nan"))
+            gui = c.get("GRBM_GUI_ACTIVE", 0.0) / xcc
+            rec.append((d_ns / 1e3 if d_ns else float("nan"), waves,
+                        c["SQ_WAIT_INST_ANY"] / c["SQ_WAVE_CYCLES"] if c.get("SQ_WAVE_CYCLES") else float("nan"),
+                        c.get("SQ_INSTS_VMEM_RD", float("nan")) / chunks,
+                        c.get("TCP_TCC_READ_REQ_sum", float("nan")) / chunks,
+                        c.get("TCP_PENDING_STALL_CYCLES_sum", float("nan")) / waves if waves else float("nan"),
+                        c.get("TA_BUSY_avr", float("nan")) / gui if gui else float("nan")))
+        med = [statistics.median(r[i] for r in rec) for i in range(7)]
+        row = vals[0][2]
+        lines.append(f"| {m} | {cfg} | {med[0]:.2f} | {med[1]:.0f} | {row['VGPR_Count']} | {row['Accum_VGPR_Count']} | "
+                     f"{row['LDS_Block_Size']} | {100 * med[2]:.1f}% | {med[3]:.2f} | {med[4]:.1f} | {med[5]:.0f} | "
+                     f"{100 * med[6]:.1f}% |")
+    return "\n".join(lines) + "\n"
+
+
 def stats_from_trace(stats_csv: str, trace_csv: str, bench_json: str, command: str) -> str:
     """Markdown summary of a ``rocprofv3 --kernel-trace --stats`` run of
     the bench: the hx kernels of the stats CSV, the phases of the trace
@@ -1578,6 +1625,8 @@ def main() -> int:
                     help="print the traffic.txt lines of two --pmc-workload counter CSVs and exit")
     ap.add_argument("--stats-from", nargs=4, metavar=("STATS_CSV", "TRACE_CSV", "BENCH_JSON", "COMMAND"),
                     help="markdown summary of a rocprofv3 --kernel-trace --stats run of the bench")
+    ap.add_argument("--gemv-from", nargs=3, metavar=("PMC_CSV", "KEYS_JSON", "COMMAND"),
+                    help="print the decode-GEMV counter summary of a --pmc-workload counter CSV and exit")
     ap.add_argument("--mfma-from", nargs=3, metavar=("PMC_CSV", "KEYS_JSON", "COMMAND"),
                     help="print the MFMA counter summary of a --pmc-workload counter CSV (and the "
                          "command that made it) and exit")
@@ -1595,6 +1644,9 @@ def main() -> int:
         return 0
     if args.mfma_from:
         print(mfma_from_pmc(*args.mfma_from), end="")
+        return 0
+    if args.gemv_from:
+        print(gemv_from_pmc(*args.gemv_from), end="")
         return 0
     import torch
     from __graft_entry__ import load_package
