@@ -1486,6 +1486,20 @@ def ceilings(hx=None) -> dict:
             (lambda b=b: lib.hxp_read(ctypes.c_void_p(b.data_ptr()), nbytes, blocks,
                                       ctypes.c_void_p(sink.data_ptr()), stream())) for b in bufs])
         del bufs
+    # the decode GEMV's weight read in the GEMV's own launch shape (no
+    # arithmetic), 12 rotating copies like the GEMV's bench line
+    lib.hxp_read_gemv_shape.argtypes = [vp, i64, vp, ci, vp, vp]
+    gbytes = 11008 * 4096
+    wcopies = [torch.randint(-2**31, 2**31 - 1, (gbytes // 4,), dtype=torch.int32, device=dev, generator=gr)
+               for _ in range(12)]
+    scales = torch.ones(11008, dtype=torch.float32, device=dev)
+    ms, _ = event_timed([(lambda w=w: lib.hxp_read_gemv_shape(ctypes.c_void_p(w.data_ptr()), gbytes,
+                                                              ctypes.c_void_p(scales.data_ptr()), 11008,
+                                                              ctypes.c_void_p(sink.data_ptr()), stream()))
+                         for w in wcopies], 400)
+    out["read_45MB_gemv_shape"] = {"bytes": gbytes, "us_per_launch": round(ms * 1e3, 3),
+                                   "GB_s": round(gbytes / (ms * 1e-3) / 1e9, 1), "blocks": -(-gbytes // (3 * 65536))}
+    del wcopies
     nbytes = 64 << 20
     pairs = [(torch.randint(-2**31, 2**31 - 1, (nbytes // 4,), dtype=torch.int32, device=dev, generator=gr),
               torch.empty(nbytes // 4, dtype=torch.int32, device=dev))
