@@ -406,8 +406,8 @@ int launch_gemm(int mode, int cfg_idx, const GemmArgs& a, hipStream_t s) {
   if (a.b2 || !a.part || (mode != GM_I8 && a.row_scale)) return HXI_ERR_ARG;
   // K split with counters: the parts of each tile hand their partials to
   // the last of them, which applies the epilogue -- one launch (B as
-  // [N][K]; a [K][N] B takes the merge kernel)
-  if (a.cnt && !a.b_kn && tiles <= kGemvSplitCounters) {
+  // [N][K], or [K][N] read in place)
+  if (a.cnt && tiles <= kGemvSplitCounters) {
     GemmArgs q = a;
     q.k_split = split_k_elems(mode, c, a);
     q.clk = clock_target();

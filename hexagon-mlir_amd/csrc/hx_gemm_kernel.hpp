@@ -1116,7 +1116,14 @@ static void launch_one(const GemmArgs& a, hipStream_t s) {
     }
   }
   if constexpr (SPLITM && EPI == GE_STORE) {
-    if (parts > 1 && a.cnt && !a.b_kn) {
+    if (parts > 1 && a.cnt) {
+      if constexpr (MODE == GM_F16 || MODE == GM_BF16 || MODE == GM_I8) {
+        if (a.b_kn) {
+          if (edge) gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, true, true, STAGES, false, true><<<grid, block, 0, s>>>(a);
+          else gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, false, true, STAGES, false, true><<<grid, block, 0, s>>>(a);
+          return;
+        }
+      }
       if (edge) gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, true, false, STAGES, false, true><<<grid, block, 0, s>>>(a);
       else gemm_kernel<MODE, BM, BN, WM, WN, EPI, SB, MINW, false, false, STAGES, false, true><<<grid, block, 0, s>>>(a);
       return;
