@@ -272,6 +272,11 @@ __device__ __forceinline__ void row_vec_finish(const RowArgs& a, int64_t row, in
 #pragma unroll
   for (int i = 0; i < VPL; ++i) ok[i] = ((int64_t)(i * WPR + wave_in_row) * 64 + lane) * EV < cols;
 
+  // Softmax rows of at most 4 vectors per lane keep the exponentials of the
+  // sum pass (binary32, 4 VGPRs per vector) and scale them in the output
+  // pass instead of taking every exponential twice.
+  constexpr bool KEEP_EXP = OP == ROW_SOFTMAX && VPL <= 4;
+  float ex[KEEP_EXP ? VPL : 1][KEEP_EXP ? EV : 1];
   float scale = 1.f, shift = 0.f;
   if constexpr (OP == ROW_SOFTMAX) {
     // One exchange across the row's waves: each wave reduces its own max m_w
@@ -293,9 +298,14 @@ __device__ __forceinline__ void row_vec_finish(const RowArgs& a, int64_t row, in
     for (int i = 0; i < VPL; ++i)
       if (ok[i]) {
 #pragma unroll
-        for (int j = 0; j < EV; ++j) s += fast_exp(vec_elem<DT>(raw[i], j) - m);
+        for (int j = 0; j < EV; ++j) {
+          const float e = fast_exp(vec_elem<DT>(raw[i], j) - m);
+          if constexpr (KEEP_EXP) ex[i][j] = e;
+          s += e;
+        }
       }
     s = wave_sum(s);
+    const float m_w = m;
     if constexpr (WPR > 1) {
       if (lane == 0) {
         red[wave] = m;
@@ -313,6 +323,9 @@ __device__ __forceinline__ void row_vec_finish(const RowArgs& a, int64_t row, in
     }
     scale = 1.0f / s;  // DivToMul: one reciprocal, then multiplies
     shift = m;
+    // kept exponentials are relative to this wave's own maximum:
+    // exp(x - m) = exp(x - m_w) exp(m_w - m)
+    if constexpr (KEEP_EXP && WPR > 1) scale = fast_exp(m_w - m) * scale;
   } else if constexpr (OP == ROW_RMSNORM) {
     float ss = 0.f;
 #pragma unroll
@@ -362,7 +375,9 @@ __device__ __forceinline__ void row_vec_finish(const RowArgs& a, int64_t row, in
     for (int j = 0; j < EV; ++j) {
       const float x = vec_elem<DT>(raw[i], j);
       float r;
-      if constexpr (OP == ROW_SOFTMAX) {
+      if constexpr (KEEP_EXP) {
+        r = ex[i][j] * scale;
+      } else if constexpr (OP == ROW_SOFTMAX) {
         r = fast_exp(x - shift) * scale;
       } else if constexpr (OP == ROW_RMSNORM) {
         r = x * scale;
