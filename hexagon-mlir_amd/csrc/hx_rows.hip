@@ -179,7 +179,7 @@ __global__ void __launch_bounds__(256) row_kernel(RowArgs a) {
     vs = group_sum<WPR>(vs, red);
     scale = 1.0f / sqrtf(vs / (float)cols + a.eps);
     shift = mean;
-    if (threadIdx.x == (WPR == 1 ? wave * 64 : 0)) {
+    if ((int)threadIdx.x == (WPR == 1 ? wave * 64 : 0)) {
       if (a.mean) a.mean[row] = mean;
       if (a.rstd) a.rstd[row] = scale;
     }
@@ -358,7 +358,7 @@ __device__ __forceinline__ void row_vec_finish(const RowArgs& a, int64_t row, in
     vs = group_sum_once<WPR>(vs, red + NRED);
     scale = 1.0f / sqrtf(vs / (float)cols + a.eps);
     shift = mean;
-    if (threadIdx.x == (WPR == 1 ? wave * 64 : 0)) {
+    if ((int)threadIdx.x == (WPR == 1 ? wave * 64 : 0)) {
       if (a.mean) a.mean[row] = mean;
       if (a.rstd) a.rstd[row] = scale;
     }
@@ -765,7 +765,7 @@ __global__ void __launch_bounds__(256) row_long_apply_kernel(RowArgs a, int S, i
   const int seg = (int)(b - row * S);
   // the row's S <= 64 statistics, merged by the first wave in segment order
   if (threadIdx.x < 64) {
-    RowStat t = threadIdx.x < S ? st[row * S + threadIdx.x] : stat_identity<OP>();
+    RowStat t = (int)threadIdx.x < S ? st[row * S + threadIdx.x] : stat_identity<OP>();
     t = stat_wave_reduce<OP>(t);
     if (threadIdx.x == 0) row_stat = t;
   }
