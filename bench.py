@@ -577,9 +577,9 @@ def bench_gemv_down(hx, iters: int = 400):
         hx.config_select(6, M, N, K, -1)
         cfg = hx.config_get(6, hx.config_lookup(6, M, N, K))["name"]
         # the split config's own base: the same tiles per workgroup and waves
-        # over K with K in one part (packed_ctC_kwW_sP -> packed_ctC_kwW)
+        # over K with K in one part (packed_ctC_kwW_sP[_e] -> packed_ctC_kwW)
         import re
-        base = re.sub(r"_s\d+$", "", cfg)
+        base = re.sub(r"_s\d+(_e)?$", "", cfg)
         if base not in names:
             base = cfg
         times = {}
@@ -976,8 +976,9 @@ def bench_attention(hx, iters: int = 20):
 def gemv_ab(hx, rounds: int = 5, iters: int = 400) -> str:
     """Interleaved A/B of the decode GEMV configurations that compete for
     the untuned default at the C3 shapes (int8, N = 11008, K = 4096,
-    registered weights rotating over 12 copies, each its own output) and at
-    the FFN's down projection (N = 4096, K = 11008): every round times every
+    registered weights rotating over 12 copies, each its own output), at
+    the FFN's down projection (N = 4096, K = 11008) and at N = K = 4096
+    (whose 12 copies, 192 MB, fit the 256 MB MALL): every round times every
     candidate once (one region of ``iters`` launches), so all of them see the
     same clock and thermal drift; the table gives the median and q20 / q80
     over the rounds.  Markdown on stdout."""
@@ -991,11 +992,14 @@ def gemv_ab(hx, rounds: int = 5, iters: int = 400) -> str:
              f"each with its own output; HIP events); {rounds} rounds; us per launch, median [q20, q80] over the "
              "rounds.  `*` marks the untuned default.", ""]
     shapes = [(11008, 4096, (1, 4, 8, 12, 16),
-               ("gemv_packed_ct3_kw16", "gemv_packed_ct3_kw8", "gemv_packed_ct4_kw8", "gemv_packed_ct4_kw8_c8",
+               ("gemv_packed_ct3_kw16", "gemv_packed_ct3_kw16_e", "gemv_packed_ct3_kw8", "gemv_packed_ct4_kw8",
                 "gemv_packed_ct1_kw8_xd", "gemv_packed_ct6_kw16_s2")),
               (4096, 11008, (8, 12, 16),
-               ("gemv_packed_ct4_kw16_s4", "gemv_packed_ct2_kw16_s2", "gemv_packed_ct4_kw16", "gemv_packed_ct1_kw16",
-                "gemv_packed_ct2_kw8", "gemv_packed_ct1_kw8"))]
+               ("gemv_packed_ct4_kw16_s4", "gemv_packed_ct4_kw16_s4_e", "gemv_packed_ct2_kw16_s2",
+                "gemv_packed_ct1_kw16", "gemv_packed_ct1_kw16_e", "gemv_packed_ct1_kw8", "gemv_packed_ct1_kw8_e")),
+              (4096, 4096, (1, 4, 8, 16),
+               ("gemv_packed_ct1_kw16", "gemv_packed_ct1_kw16_e", "gemv_packed_ct1_kw8", "gemv_packed_ct1_kw8_e",
+                "gemv_packed_ct2_kw8", "gemv_packed_ct1_kw8_xd"))]
     for N, K, Ms, cands in shapes:
         ws = []
         for _ in range(12):
@@ -1503,6 +1507,16 @@ def ceilings(hx=None) -> dict:
                          for w in wcopies], 400)
     out["read_45MB_gemv_shape"] = {"bytes": gbytes, "us_per_launch": round(ms * 1e3, 3),
                                    "GB_s": round(gbytes / (ms * 1e-3) / 1e9, 1), "blocks": -(-gbytes // (3 * 65536))}
+    # the same read in the launch shapes of other GEMV configs (tiles per
+    # workgroup, waves)
+    lib.hxp_read_tiles.argtypes = [ci, ci, vp, i64, vp, ci, vp, vp]
+    for ct, kw in ((3, 8), (1, 8), (1, 4)):
+        ms, _ = event_timed([(lambda w=w, ct=ct, kw=kw: lib.hxp_read_tiles(
+            ct, kw, ctypes.c_void_p(w.data_ptr()), gbytes, ctypes.c_void_p(scales.data_ptr()), 11008,
+            ctypes.c_void_p(sink.data_ptr()), stream())) for w in wcopies], 400)
+        out[f"read_45MB_gemv_shape_ct{ct}_kw{kw}"] = {
+            "bytes": gbytes, "us_per_launch": round(ms * 1e3, 3), "GB_s": round(gbytes / (ms * 1e-3) / 1e9, 1),
+            "blocks": -(-gbytes // (ct * 65536))}
     del wcopies
     nbytes = 64 << 20
     pairs = [(torch.randint(-2**31, 2**31 - 1, (nbytes // 4,), dtype=torch.int32, device=dev, generator=gr),

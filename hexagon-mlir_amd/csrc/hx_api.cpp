@@ -537,22 +537,23 @@ static int gemv_untuned_table(int op, int64_t M, int64_t N, int64_t K, bool in_p
   }
   // untuned choice from the MI355X sweep (int8, K = 4096).  When the
   // 16-column tiles need three per workgroup to fit one workgroup per CU
-  // (N = 11008: 688 tiles, 230 workgroups): three tiles over 16 waves up to
-  // 4 rows, over 8 waves from 8 rows -- interleaved A/B, five rounds on one
-  // box (bench.py --gemv-ab), M = 1 / 4 / 8 / 12 / 16: 16 waves 9.36 / 9.49 /
-  // 9.88 / 10.44 / 11.04 us, 8 waves 9.65 / 9.56 / 9.80 / 9.97 / 10.29.
-  // Past 4 rows every lane's accumulators go through the cross-wave LDS
-  // reduction at the end (up to 4 rows only lanes 0..15 do), and half the
-  // waves halve it; the weight and activation bytes are the same.  Otherwise,
-  // for M <= 4: up to 256 tiles one tile per workgroup over 16 waves (M = 1
-  // / 4, N = K = 4096: 5.11 / 5.23 against 5.31 / 5.59 with LDS-staged
+  // (N = 11008: 688 tiles, 230 workgroups): three tiles over 16 waves with
+  // every slice load issued ahead of the MFMAs -- interleaved A/B, five
+  // rounds on one box (bench.py --gemv-ab), M = 1 / 4 / 8 / 12 / 16: 9.40 /
+  // 9.38 / 9.54 / 9.85 / 10.31 us, against 9.40 / 9.52 / 9.92 / 10.46 /
+  // 11.07 for the compiler's load schedule and 9.67 / 9.60 / 9.82 / 10.00 /
+  // 10.33 over 8 waves.  Otherwise, for M <= 4: up to 256 tiles one tile
+  // per workgroup over 16 waves (M = 1 / 4, N = K = 4096: 5.19 / 5.30
+  // against 5.24 / 5.38 issuing ahead, 5.50 / 5.63 with LDS-staged
   // activations over 8), beyond two tiles over 8 waves (M = 4, N = 8192 /
   // 16384: 7.67 / 12.73 against 8.15 / 13.97).
   // For M > 4 the fewest tiles per workgroup (1 to 4) that keep the
   // workgroups within one per CU, three beyond 1024 tiles (M = 16, N = 2048
   // / 4096 / 8192 / 16384 / 22016: 6.83 / 7.08 / 8.85 / 13.64 / 18.97 us;
-  // four tiles everywhere took 9.63 / 9.86 / 10.5 / 13.64 / 22.25).
-  if (three_tiles) return M >= 8 ? 19 : 20;
+  // four tiles everywhere took 9.63 / 9.86 / 10.5 / 13.64 / 22.25); one
+  // tile issues its loads ahead (N = K = 4096, M = 8 / 16: 5.82 / 7.00
+  // against 5.96 / 7.36; N = 4096, K = 11008, M = 8: 11.82 against 12.18).
+  if (three_tiles) return 30;
   if (M <= 4) return tiles > 256 ? 0 : 24;
   // at most 128 tiles with K >= 8192, up to 12 rows: one tile per
   // workgroup over two parts (M = 5 / 8 / 12 at 2048 x 8192: 7.2 / 7.8 /
@@ -563,9 +564,11 @@ static int gemv_untuned_table(int op, int64_t M, int64_t N, int64_t K, bool in_p
   // workgroup with K split over four workgroups, one workgroup per CU
   // (M = 12 / 16: 4096 x 11008 13.2 / 13.6 against 14.0 / 16.0 us; 2048 x
   // 8192 8.8 / 9.1 against 10.2 / 11.8; 4096 x 8192 10.3 / 10.5 against
-  // 10.7 / 12.3; at M = 9 the split lost on N = 4096, 13.0 against 12.3)
-  if (M >= 12 && tiles <= 256 && K >= 8192) return 26;
-  return tiles <= 256 ? 1 : tiles <= 512 ? 0 : tiles <= 768 ? 19 : tiles <= 1024 ? 10 : 19;
+  // 10.7 / 12.3; at M = 9 the split lost on N = 4096, 13.0 against 12.3),
+  // its loads issued ahead (4096 x 11008: 13.07 / 13.40 against 13.24 /
+  // 13.62 in the same A/B)
+  if (M >= 12 && tiles <= 256 && K >= 8192) return 33;
+  return tiles <= 256 ? 31 : tiles <= 512 ? 0 : tiles <= 768 ? 19 : tiles <= 1024 ? 10 : 19;
 }
 
 static int resolve_gemv(int op, int64_t M, int64_t N, int64_t K, bool* was_pinned = nullptr,

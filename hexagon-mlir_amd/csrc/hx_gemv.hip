@@ -161,7 +161,9 @@ __global__ void __launch_bounds__(256) gemv_w8a16_kernel(GemvArgs p) {
 // loads CPW chunks of each of its CT tiles per slice, ahead of the MFMAs
 // that use them (how far ahead is the compiler's schedule: for the wide
 // configs it interleaves loads and MFMAs with fewer live registers, which
-// measured faster than holding the whole slice).  With K = 4096 int8 and
+// measured faster than holding the whole slice).  EAGER: a scheduling
+// barrier keeps every load of the slice ahead of its first MFMA instead,
+// which the narrower configs gain from.  With K = 4096 int8 and
 // CPW * KW = 64 a slice is all of K.  PIPE: two register sets, the next
 // slice's loads issued before the current slice's MFMAs.
 //
@@ -185,7 +187,8 @@ __device__ __forceinline__ v4f gv_mfma(v4u a, v4u b, v4f c) {
 
 // MB > 1 (16 < M <= 16 MB): MB blocks of 16 activation rows; every weight
 // fragment feeds MB MFMAs, so the weight is still streamed once.
-template <int CT, int KW, int CPW, int XS, int WT, bool PK, bool PIPE, int MB = 1, bool SPLIT = false>
+template <int CT, int KW, int CPW, int XS, int WT, bool PK, bool PIPE, int MB = 1, bool SPLIT = false,
+          bool EAGER = false>
 __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const void* wsrc, int64_t ldw,
                                                               int kchunks) {
   static_assert(MB == 1 || (XS == XS_NONE && !PIPE), "row blocks: register-fragment configs only");
@@ -451,6 +454,8 @@ __global__ void __launch_bounds__(64 * KW) gemv_stream_kernel(GemvArgs p, const 
             }
         }
       }
+      // EAGER: the whole slice's loads stay ahead of its MFMAs
+      if constexpr (EAGER) __builtin_amdgcn_sched_barrier(0);
       if constexpr (XL)
         if (c0 == 0) publish(std::integral_constant<int, CPW * CT>{});
 #pragma unroll
@@ -688,13 +693,13 @@ int launch_gemv_pack(const int8_t* w, int64_t ldw, int64_t N, int64_t K, int8_t*
 
 typedef void (*GemvStreamLaunch)(const GemvArgs&, const void*, int64_t, int, hipStream_t);
 template <int CT, int KW, int CPW, int XS, bool PIPE, int WT, int MB = 1, bool PK = (WT == DT_I8),
-          bool SPLIT = false>
+          bool SPLIT = false, bool EAGER = false>
 static void gemv_stream_one(const GemvArgs& a, const void* w, int64_t ldw, int kchunks, hipStream_t s) {
   constexpr int KD = WT == DT_I8 ? 64 : 32;
   const int64_t ntiles = (a.N + 15) / 16;
   const int64_t blocks = (ntiles + CT - 1) / CT * a.parts;
   const size_t lds = XS != XS_NONE ? (size_t)a.M * (((int64_t)kchunks * KD + 511) / 512 * 512 + 8) * 2 : 0;
-  gemv_stream_kernel<CT, KW, CPW, XS, WT, PK, PIPE, MB, SPLIT>
+  gemv_stream_kernel<CT, KW, CPW, XS, WT, PK, PIPE, MB, SPLIT, EAGER>
       <<<dim3((unsigned)blocks), dim3(64 * KW), lds, s>>>(a, w, ldw, kchunks);
 }
 struct GemvStreamEntry {
@@ -712,6 +717,13 @@ struct GemvStreamEntry {
    &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_I8, 1, false, true>,                             \
    &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_F16, 1, true, true>,                             \
    &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_BF16, 1, true, true>}
+#define HX_GE(CT, KW, CPW, SP)                                                                      \
+  {&gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_I8, 1, true, SP, true>,                          \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_F16, 1, false, SP, true>,                        \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_BF16, 1, false, SP, true>,                       \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_I8, 1, false, SP, true>,                         \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_F16, 1, true, SP, true>,                         \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_BF16, 1, true, SP, true>}
 #define HX_GR(CT, KW, CPW, MB)                                                                      \
   {&gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_I8, MB>,                                        \
    &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_F16, MB>,                                       \
@@ -774,8 +786,22 @@ static const GemvStreamEntry kGemvStream[] = {
     // split in two or four, 2x the workgroups of one tile each
     {{1, 16, "packed_ct1_kw16_s2", 0, 24, 1, 2}, HX_GS(1, 16, 4)},
     {{2, 16, "packed_ct2_kw16_s4", 0, 0, 1, 4}, HX_GS(2, 16, 4)},
+    // every slice load issued before the slice's first MFMA (the compiler
+    // otherwise spreads the loads among the MFMAs, about 6 of a wave's 20
+    // in flight for ct3_kw16): 1-3% faster on these shapes (interleaved A/B,
+    // int8 packed image; N = 11008, K = 4096, M = 1 / 4 / 8 / 12 / 16: 9.48 /
+    // 9.45 / 9.55 / 9.86 / 10.39 against 9.55 / 9.67 / 9.98 / 10.46 / 11.06 us
+    // for ct3_kw16; N = 4096, K = 11008, M = 8 / 12 / 16: ct1_kw16 11.84 /
+    // 13.56 / 15.03 against 12.35 / 13.99 / 16.07, ct4_kw16_s4 12.78 / 13.09 /
+    // 13.38 against 12.95 / 13.27 / 13.62); it lost on ct4_kw16, ct3_kw8 at
+    // 16 rows and ct2_kw16_s2
+    {{3, 16, "packed_ct3_kw16_e", 0, 30, 1}, HX_GE(3, 16, 4, false)},
+    {{1, 8, "packed_ct1_kw8_e", 0, 31, 1}, HX_GE(1, 8, 8, false)},
+    {{1, 16, "packed_ct1_kw16_e", 0, 32, 1}, HX_GE(1, 16, 4, false)},
+    {{4, 16, "packed_ct4_kw16_s4_e", 0, 8, 1, 4}, HX_GE(4, 16, 2, true)},
 };
 #undef HX_GR
+#undef HX_GE
 #undef HX_GS
 #undef HX_GV
 int gemv_packed_config_count() { return (int)(sizeof(kGemvStream) / sizeof(kGemvStream[0])); }

@@ -216,38 +216,43 @@ __global__ void __launch_bounds__(512) probe_interleave_kernel(int phases, int* 
 }
 
 
-// A read of the decode GEMV's weight in the GEMV's own launch shape (N =
-// 11008, K = 4096 int8: 230 workgroups of 16 waves, 3 x 64 chunks of 1 KiB
-// per workgroup, wave w loading chunks w + 16u of each tile with 16-byte
-// buffer loads), with its column-scale load first and its LDS exchange and
-// barrier at the end, and no arithmetic: what the GEMV's memory side alone
-// costs.  The data is folded into one word per lane so no load is dead.
-__global__ void __launch_bounds__(1024) probe_read_gemv_shape_kernel(const char* __restrict__ p, long bytes,
-                                                                     const float* sc, int nsc, int* sink) {
+// A read of the decode GEMV's weight in a GEMV launch shape (N = 11008,
+// K = 4096 int8, the packed image: 688 tiles of 64 chunks of 1 KiB; CT tiles
+// per workgroup of KW waves, wave w loading chunks w + KW u of each tile with
+// 16-byte buffer loads), with the column-scale load first and the LDS
+// exchange and barrier at the end, and no arithmetic: what the GEMV's memory
+// side alone costs in that shape.  CT = 3, KW = 16 is the default's shape
+// (230 workgroups).  The data is folded into one word per lane so no load is
+// dead.
+template <int CT, int KW>
+__global__ void __launch_bounds__(64 * KW) probe_read_tiles_kernel(const char* __restrict__ p, long bytes,
+                                                                  const float* sc, int nsc, int* sink) {
+  constexpr int CPW = 64 / KW;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const long region = 3L * 64 * 1024;
+  const long region = (long)CT * 64 * 1024;
   const long rem = bytes - (long)blockIdx.x * region;
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(p + (long)blockIdx.x * region), 0, rem < region ? (int)rem : (int)region, 0x00020000);
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)sc, 0, nsc * 4, 0x00020000);
-  const unsigned s0 = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)((blockIdx.x * 48 + (tid % 48)) * 4), 0, 0);
-  v4i v[12];
+  const unsigned s0 =
+      __builtin_amdgcn_raw_buffer_load_b32(rs, (int)((blockIdx.x * 16 * CT + (tid % (16 * CT))) * 4), 0, 0);
+  v4i v[CPW * CT];
 #pragma unroll
-  for (int u = 0; u < 4; ++u)
+  for (int u = 0; u < CPW; ++u)
 #pragma unroll
-    for (int c = 0; c < 3; ++c)
-      v[u * 3 + c] = __builtin_bit_cast(
-          v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, (c * 64 + wave + 16 * u) * 1024 + lane * 16, 0, 2));
+    for (int c = 0; c < CT; ++c)
+      v[u * CT + c] = __builtin_bit_cast(
+          v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, (c * 64 + wave + KW * u) * 1024 + lane * 16, 0, 2));
   v4i acc{0, 0, 0, 0};
 #pragma unroll
-  for (int j = 0; j < 12; ++j) acc ^= v[j];
-  __shared__ unsigned red[16][64];
+  for (int j = 0; j < CPW * CT; ++j) acc ^= v[j];
+  __shared__ unsigned red[KW][64];
   red[wave][lane] = (unsigned)(acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) ^ s0;
   __syncthreads();
   if (tid < 64) {
     unsigned q = 0;
-    for (int w = 0; w < 16; ++w) q ^= red[w][tid];
+    for (int w = 0; w < KW; ++w) q ^= red[w][tid];
     if (q == 0x5eed1234u) sink[1] = 1;
   }
 }
@@ -283,14 +288,24 @@ int hxp_mfma4_i8(int blocks, int iters, int lds_reads, int* out, double* ops, hi
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-// one launch of probe_read_gemv_shape_kernel over `bytes` (a multiple of
-// nothing in particular: the last workgroup's range is cut to the buffer),
-// column scales `sc` [nsc] binary32
-int hxp_read_gemv_shape(const void* p, int64_t bytes, const float* sc, int nsc, int* sink, hipStream_t s) {
-  const long region = 3L * 64 * 1024;
-  probe_read_gemv_shape_kernel<<<(unsigned)((bytes + region - 1) / region), 1024, 0, s>>>(
-      (const char*)p, bytes, sc, nsc, sink);
+// one launch of probe_read_tiles_kernel<CT, KW> over `bytes` (whole 64 KiB
+// tiles; the last workgroup's range is cut to the buffer), column scales
+// `sc` [nsc] binary32; (CT, KW) in {(3, 16), (3, 8), (1, 8), (1, 4)}
+int hxp_read_tiles(int ct, int kw, const void* p, int64_t bytes, const float* sc, int nsc, int* sink,
+                   hipStream_t s) {
+  const char* q = (const char*)p;
+  const long tiles = (long)((bytes + 65535) / 65536);
+  const unsigned g = (unsigned)((tiles + ct - 1) / ct);
+  if (ct == 3 && kw == 16) probe_read_tiles_kernel<3, 16><<<g, 1024, 0, s>>>(q, bytes, sc, nsc, sink);
+  else if (ct == 3 && kw == 8) probe_read_tiles_kernel<3, 8><<<g, 512, 0, s>>>(q, bytes, sc, nsc, sink);
+  else if (ct == 1 && kw == 8) probe_read_tiles_kernel<1, 8><<<g, 512, 0, s>>>(q, bytes, sc, nsc, sink);
+  else if (ct == 1 && kw == 4) probe_read_tiles_kernel<1, 4><<<g, 256, 0, s>>>(q, bytes, sc, nsc, sink);
+  else return -1;
   return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+// the default's shape (three tiles over 16 waves)
+int hxp_read_gemv_shape(const void* p, int64_t bytes, const float* sc, int nsc, int* sink, hipStream_t s) {
+  return hxp_read_tiles(3, 16, p, bytes, sc, nsc, sink, s);
 }
 int hxp_empty(hipStream_t s) {
   probe_empty_kernel<<<1, 64, 0, s>>>();

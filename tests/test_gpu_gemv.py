@@ -210,7 +210,7 @@ def test_gemv_split_k_few_rows_run_the_base(hx, dev):
     names = [hx.config_get(6, i)["name"] for i in range(hx.config_count(6))]
     base = {"gemv_packed_ct2_kw16_s2": "gemv_packed_ct2_kw8", "gemv_packed_ct4_kw16_s4": "gemv_packed_ct4_kw16",
             "gemv_packed_ct6_kw16_s2": "gemv_packed_ct3_kw16", "gemv_packed_ct1_kw16_s2": "gemv_packed_ct1_kw16",
-            "gemv_packed_ct2_kw16_s4": "gemv_packed_ct2_kw8"}
+            "gemv_packed_ct2_kw16_s4": "gemv_packed_ct2_kw8", "gemv_packed_ct4_kw16_s4_e": "gemv_packed_ct4_kw16"}
     try:
         for sname, bname in base.items():
             got = []
@@ -253,7 +253,7 @@ def test_gemv_split_k_is_the_default_where_it_pays(hx, dev):
         hx.manifest_enable(prev)
         rw.release(); rw2.release(); rw3.release()
     got = {(r["m"], r["n"]): r["config"] for r in recs}
-    assert got[(16, 4096)] == "packed_ct4_kw16_s4", got
+    assert got[(16, 4096)] == "packed_ct4_kw16_s4_e", got
     assert "_s" not in got[(8, 4096)][-3:] and "_s" not in got[(16, 11008)][-3:], got
     # at most 128 tiles (N = 2048), K = 8192: one tile per workgroup over two parts
     assert got[(8, 2048)] == "packed_ct1_kw16_s2", got
