@@ -511,14 +511,18 @@ static int gemv_untuned_table(int op, int64_t M, int64_t N, int64_t K, bool in_p
     return K >= 8192 ? 0 : 1;
   }
   if (op != HX_OP_GEMV_W8) {
-    // the packed f16 / bf16 image (tuner medians, rotating copies): 16 waves
-    // with staged activations for M <= 2 (1 x 8192 x 8192: 22.8 us, within
-    // 4% of the best at N, K in {4096, 8192, 11008, 16384}), 8 for M <= 4;
-    // beyond, three tiles over 16 waves where they give one workgroup per
-    // CU (16 x 11008 x 4096: 16.9 against 24.7 us for one tile), two tiles
-    // from 512 tiles (16 x 8192 x 8192: 24.4 against 33.4) and one below
-    // (16 x 4096 x 16384: 30.6 against 39.5 for two)
-    if (M <= 2) return 7;
+    // the packed f16 / bf16 image: staged activations for M <= 4, over 16
+    // or 8 waves.  M <= 2 from an interleaved A/B (five rounds, rotating
+    // copies; M = 1, 16 against 8 waves, us): N = 4096 and K = 4096 / 8192 /
+    // 11008 / 16384: 7.48 / 13.48 / 16.67 / 24.21 against 7.55 / 14.83 /
+    // 16.69 / 23.27; N = 8192, K = 4096 / 8192: 13.50 / 23.66 against 12.69 /
+    // 25.93; K = 4096, N = 11008 / 16384: 17.66 / 23.86 against 16.44 /
+    // 21.85.  8 waves for M <= 4 otherwise; beyond, three tiles over 16 waves
+    // where they give one workgroup per CU (16 x 11008 x 4096: 16.9 against
+    // 24.7 us for one tile), two tiles from 512 tiles (16 x 8192 x 8192: 24.4
+    // against 33.4) and one below (16 x 4096 x 16384: 30.6 against 39.5 for
+    // two)
+    if (M <= 2) return (K <= 4096 && tiles >= 512) || K >= 16384 ? 5 : 7;
     if (M <= 4) return 5;
     // K split over workgroups.  At most 128 tiles (one tile per workgroup
     // leaves half the CUs idle), K >= 8192: one tile over two parts up to 8
