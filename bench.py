@@ -1341,7 +1341,9 @@ def gemv_from_pmc(pmc_csv: str, keys_json: str, command: str) -> str:
              f"Command: `{command}`", "",
              "W8A16 GEMV, N = 11008, K = 4096, registered (fragment-packed) weight: 44,032 weight chunks of "
              "1 KiB, one 16-byte load per lane each. Per config and M, the median over its launches. "
-             "waves = SQ_WAVES; VGPR / AGPR / LDS from the dispatch record; waiting = SQ_WAIT_INST_ANY / "
+             "waves = SQ_WAVES; VGPR / AGPR / LDS from the dispatch record (its VGPR field reads half the "
+             "compiler's count for these kernels, rounded up to 4: 44 for the 82 VGPRs of packed_ct3_kw8, "
+             "60 for the 114 of packed_ct3_kw16_e); waiting = SQ_WAIT_INST_ANY / "
              "SQ_WAVE_CYCLES; vmem reads = SQ_INSTS_VMEM_RD (wave instructions, weight and activation); "
              "L2 requests = TCP_TCC_READ_REQ_sum (64-byte requests from the L1s); pending stall = "
              "TCP_PENDING_STALL_CYCLES_sum per wave; TA busy = TA_BUSY_avr / (GRBM_GUI_ACTIVE / 8).", "",
