@@ -484,8 +484,9 @@ static int resolve_gemm(int op, int64_t M, int64_t N, int64_t K, bool* was_pinne
   return gemm_default_config(mode, epi, M, N, K);
 }
 // Untuned GEMV config (table index = family index) for a shape.
-// in_place: an f16 / bf16 [N][K] weight read where it lies (argument
-// weights); otherwise a registered weight's packed image.
+// in_place: an [N][K] weight read where it lies (argument weights; f16 /
+// bf16 have their own rules, int8 one of its own); otherwise a registered
+// weight's packed image.
 static int gemv_untuned_table(int op, int64_t M, int64_t N, int64_t K, bool in_place);
 // The untuned config as it runs: a config that stages the activations in
 // LDS, or splits K over workgroups, is named by its base config where the
@@ -572,6 +573,11 @@ static int gemv_untuned_table(int op, int64_t M, int64_t N, int64_t K, bool in_p
   // its loads issued ahead (4096 x 11008: 13.07 / 13.40 against 13.24 /
   // 13.62 in the same A/B)
   if (M >= 12 && tiles <= 256 && K >= 8192) return 33;
+  // an [N][K] weight read in place (sixteen 64-byte runs per wave load)
+  // from 5 rows on at most 256 tiles with K >= 8192: the same split (M = 8,
+  // 4096 x 11008: 16.13 us against 16.90 for ct1_kw8 and 19.44 for
+  // ct1_kw8_e, which the packed image prefers)
+  if (in_place && M > 4 && tiles <= 256 && K >= 8192) return 33;
   return tiles <= 256 ? 31 : tiles <= 512 ? 0 : tiles <= 768 ? 19 : tiles <= 1024 ? 10 : 19;
 }
 
@@ -706,7 +712,7 @@ static int run_gemv_hw(GemvArgs& a, int dt, const void* w, int64_t ldw, hipStrea
   if (!reason) reason = a.M <= 16 ? "min-rows" : "few-rows";  // 16 < M: row-block configs
   const int op = dt == HX_BF16 ? HX_OP_GEMV_BF16 : dt == HX_I8 ? HX_OP_GEMV_W8 : HX_OP_GEMV_F16;
   bool pin = false;
-  const int cfg = resolve_gemv(op, a.M, a.N, a.K, &pin, dt != HX_I8);
+  const int cfg = resolve_gemv(op, a.M, a.N, a.K, &pin, true);
   note_plan(ctx, a.M, a.N, a.K, dt == HX_BF16 ? HX_BF16 : HX_F16, "gemv-stream", gemv_packed_config(cfg)->name,
             pin ? "pinned" : "default", reason);
   return map_internal(launch_gemv_hw(cfg, dt, a, w, ldw, s), "gemv_stream");
