@@ -257,3 +257,19 @@ def test_gemv_split_k_is_the_default_where_it_pays(hx, dev):
     assert "_s" not in got[(8, 4096)][-3:] and "_s" not in got[(16, 11008)][-3:], got
     # at most 128 tiles (N = 2048), K = 8192: one tile per workgroup over two parts
     assert got[(8, 2048)] == "packed_ct1_kw16_s2", got
+
+
+def test_gemv_defaults_follow_the_ab(hx):
+    """The untuned defaults at the C3 shapes, the FFN's down projection and
+    the reference tuner's fp16 decode shapes are the configs that the
+    interleaved A/B in one process (bench.py --gemv-ab and the f16 decode
+    sweep) timed fastest: three tiles over 16 waves with every slice load
+    issued ahead at N = 11008; the four-part K split at 16 rows of the down
+    projection and one tile over 8 waves at 8; for an f16 packed image with
+    one row, 16 waves at 8192 x 8192 and 8 at 4096 x 16384."""
+    want = {(6, 1, 11008, 4096): "packed_ct3_kw16_e", (6, 4, 11008, 4096): "packed_ct3_kw16_e",
+            (6, 16, 11008, 4096): "packed_ct3_kw16_e", (6, 16, 4096, 11008): "packed_ct4_kw16_s4_e",
+            (6, 8, 4096, 11008): "packed_ct1_kw8_e", (7, 1, 8192, 8192): "packed_ct1_kw16_xl",
+            (7, 1, 4096, 16384): "packed_ct1_kw8_xl"}
+    got = {k: hx.config_get(k[0], hx.config_lookup(*k))["name"] for k in want}
+    assert all(got[k].endswith(v) for k, v in want.items()), got
