@@ -1527,6 +1527,12 @@ def ceilings(hx=None) -> dict:
     sweep("copy_64MiB_in_64MiB_out", 2 * nbytes, lambda blocks: [
         (lambda s_=s_, d_=d_: lib.hxp_copy(ctypes.c_void_p(s_.data_ptr()), ctypes.c_void_p(d_.data_ptr()), nbytes,
                                            blocks, stream())) for s_, d_ in pairs])
+    # the same bytes in the row kernels' pattern: one workgroup per 8 KiB row
+    lib.hxp_copy_rows.argtypes = [vp, vp, i64, vp]
+    ms, _ = event_timed([(lambda s_=s_, d_=d_: lib.hxp_copy_rows(
+        ctypes.c_void_p(s_.data_ptr()), ctypes.c_void_p(d_.data_ptr()), nbytes, stream())) for s_, d_ in pairs], 200)
+    out["copy_64MiB_row_pattern"] = {"bytes": 2 * nbytes, "us_per_launch": round(ms * 1e3, 3),
+                                     "GB_s": round(2 * nbytes / (ms * 1e-3) / 1e9, 1), "blocks": nbytes // 8192}
     del pairs
     ops = ctypes.c_double()
     gbuf = torch.ones(1 << 18, dtype=torch.int32, device=dev)  # 1 MiB, L2-resident

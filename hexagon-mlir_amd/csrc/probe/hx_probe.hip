@@ -33,6 +33,26 @@ __global__ void __launch_bounds__(256) probe_copy_kernel(const v4i* __restrict__
     __builtin_nontemporal_store(__builtin_nontemporal_load(s + i), d + i);
 }
 
+// The same copy in the one-row-per-workgroup pattern of the row kernels:
+// workgroup b copies the 8 KiB at 8192 b with two 16-byte loads per thread
+// (both issued before either store), as a softmax row of 4096 fp16 is read
+// and written.
+__global__ void __launch_bounds__(256) probe_copy_rows_kernel(const v4i* __restrict__ s, v4i* __restrict__ d,
+                                                              int64_t n16) {
+  const int64_t base = (int64_t)blockIdx.x * 512;
+  v4i v[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int64_t i = base + u * 256 + threadIdx.x;
+    if (i < n16) v[u] = __builtin_nontemporal_load(s + i);
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int64_t i = base + u * 256 + threadIdx.x;
+    if (i < n16) __builtin_nontemporal_store(v[u], d + i);
+  }
+}
+
 // 8 independent int8 MFMA chains per wave, `iters` rounds of 8 MFMAs; NR
 // 16-byte LDS reads per round beside them (6 is the GEMM's 128x64 wave
 // tile), and NG coalesced 16-byte-per-lane loads of an L2-resident 1 MiB
@@ -313,6 +333,12 @@ int hxp_empty(hipStream_t s) {
 }
 int hxp_read(const void* p, int64_t bytes, int blocks, int* sink, hipStream_t s) {
   probe_read_kernel<<<blocks, 256, 0, s>>>((const v4i*)p, bytes / 16, sink);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+// one workgroup per 8 KiB
+int hxp_copy_rows(const void* src, void* dst, int64_t bytes, hipStream_t s) {
+  const int64_t n16 = bytes / 16;
+  probe_copy_rows_kernel<<<(unsigned)((n16 + 511) / 512), 256, 0, s>>>((const v4i*)src, (v4i*)dst, n16);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 int hxp_copy(const void* src, void* dst, int64_t bytes, int blocks, hipStream_t s) {
