@@ -537,8 +537,16 @@ static int gemv_untuned_table(int op, int64_t M, int64_t N, int64_t K, bool in_p
     // 16.8 against 14.8 at M = 9).
     if (tiles <= 128 && K >= 8192) return M <= 8 ? 28 : 29;
     if (tiles <= 128 && K >= 4096 && M >= 12) return 28;
-    if (M > 8 && tiles <= 256 && K >= 10240) return 25;
-    return three_tiles ? 20 : tiles >= 512 ? 0 : 1;
+    // from 13 rows there four tiles over four parts with the loads issued
+    // ahead (4096 x 11008, interleaved A/B, f16 / bf16 M = 9 / 12 / 14 / 16:
+    // 18.11 / 18.26 / 18.43 / 18.61 and 18.92 / 18.38 / 18.51 / 18.67
+    // against 17.79 / 18.33 / 18.81 / 19.24 and 18.73 / 18.34 / 18.77 /
+    // 19.26 us for two tiles over two parts)
+    if (M > 8 && tiles <= 256 && K >= 10240) return M > 12 ? 33 : 25;
+    // one tile per workgroup issues its loads ahead (M = 8, f16 / bf16: 4096
+    // x 4096 8.55 / 8.62 against 8.83 / 8.88 us, 4096 x 11008 17.62 / 18.03
+    // against 18.00 / 18.18; at 16 rows 4096 x 4096 ties)
+    return three_tiles ? 20 : tiles >= 512 ? 0 : 31;
   }
   // untuned choice from the MI355X sweep (int8, K = 4096).  When the
   // 16-column tiles need three per workgroup to fit one workgroup per CU

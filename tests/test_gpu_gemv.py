@@ -266,10 +266,12 @@ def test_gemv_defaults_follow_the_ab(hx):
     sweep) timed fastest: three tiles over 16 waves with every slice load
     issued ahead at N = 11008; the four-part K split at 16 rows of the down
     projection and one tile over 8 waves at 8; for an f16 packed image with
-    one row, 16 waves at 8192 x 8192 and 8 at 4096 x 16384."""
+    one row, 16 waves at 8192 x 8192 and 8 at 4096 x 16384, and on the down
+    projection's shape four parts from 13 rows, two up to 12."""
     want = {(6, 1, 11008, 4096): "packed_ct3_kw16_e", (6, 4, 11008, 4096): "packed_ct3_kw16_e",
             (6, 16, 11008, 4096): "packed_ct3_kw16_e", (6, 16, 4096, 11008): "packed_ct4_kw16_s4_e",
             (6, 8, 4096, 11008): "packed_ct1_kw8_e", (7, 1, 8192, 8192): "packed_ct1_kw16_xl",
-            (7, 1, 4096, 16384): "packed_ct1_kw8_xl"}
+            (7, 1, 4096, 16384): "packed_ct1_kw8_xl", (7, 16, 4096, 11008): "packed_ct4_kw16_s4_e",
+            (7, 12, 4096, 11008): "packed_ct2_kw16_s2", (7, 8, 4096, 4096): "packed_ct1_kw8_e"}
     got = {k: hx.config_get(k[0], hx.config_lookup(*k))["name"] for k in want}
     assert all(got[k].endswith(v) for k, v in want.items()), got
