@@ -975,55 +975,70 @@ def bench_attention(hx, iters: int = 20):
 
 def gemv_ab(hx, rounds: int = 5, iters: int = 400) -> str:
     """Interleaved A/B of the decode GEMV configurations that compete for
-    the untuned default at the C3 shapes (int8, N = 11008, K = 4096,
+    the untuned default: int8 at the C3 shapes (N = 11008, K = 4096,
     registered weights rotating over 12 copies, each its own output), at
     the FFN's down projection (N = 4096, K = 11008) and at N = K = 4096
-    (whose 12 copies, 192 MB, fit the 256 MB MALL): every round times every
-    candidate once (one region of ``iters`` launches), so all of them see the
-    same clock and thermal drift; the table gives the median and q20 / q80
-    over the rounds.  Markdown on stdout."""
+    (whose 12 copies, 192 MB, fit the 256 MB MALL); f16 packed images at the
+    reference tuner's decode shapes and their neighbours (one row) and at
+    the down projection's shape (copies totalling more than 600 MB).  Every
+    round times every candidate once (one region of ``iters`` launches), so
+    all of them see the same clock and thermal drift; the table gives the
+    median and q20 / q80 over the rounds.  Markdown on stdout."""
     import numpy as np
     import torch
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(77)
-    names = [hx.config_get(6, i)["name"] for i in range(hx.config_count(6))]
     lines = ["# Decode GEMV defaults: interleaved A/B (bench.py --gemv-ab)", "",
-             f"Every round times each candidate once ({iters} launches over 12 rotating registered weight copies, "
+             f"Every round times each candidate once ({iters} launches over rotating registered weight copies, "
              f"each with its own output; HIP events); {rounds} rounds; us per launch, median [q20, q80] over the "
              "rounds.  `*` marks the untuned default.", ""]
-    shapes = [(11008, 4096, (1, 4, 8, 12, 16),
+    xl = ("gemv_packed_ct1_kw16_xl", "gemv_packed_ct1_kw8_xl", "gemv_packed_ct1_kw16_xl_p")
+    shapes = [(6, 11008, 4096, (1, 4, 8, 12, 16),
                ("gemv_packed_ct3_kw16", "gemv_packed_ct3_kw16_e", "gemv_packed_ct3_kw8", "gemv_packed_ct4_kw8",
                 "gemv_packed_ct1_kw8_xd", "gemv_packed_ct6_kw16_s2")),
-              (4096, 11008, (8, 12, 16),
+              (6, 4096, 11008, (8, 12, 16),
                ("gemv_packed_ct4_kw16_s4", "gemv_packed_ct4_kw16_s4_e", "gemv_packed_ct2_kw16_s2",
                 "gemv_packed_ct1_kw16", "gemv_packed_ct1_kw16_e", "gemv_packed_ct1_kw8", "gemv_packed_ct1_kw8_e")),
-              (4096, 4096, (1, 4, 8, 16),
+              (6, 4096, 4096, (1, 4, 8, 16),
                ("gemv_packed_ct1_kw16", "gemv_packed_ct1_kw16_e", "gemv_packed_ct1_kw8", "gemv_packed_ct1_kw8_e",
-                "gemv_packed_ct2_kw8", "gemv_packed_ct1_kw8_xd"))]
-    for N, K, Ms, cands in shapes:
+                "gemv_packed_ct2_kw8", "gemv_packed_ct1_kw8_xd")),
+              (7, 8192, 8192, (1,), xl), (7, 4096, 16384, (1,), xl), (7, 4096, 8192, (1,), xl),
+              (7, 11008, 4096, (1,), xl), (7, 16384, 4096, (1,), xl),
+              (7, 4096, 11008, (8, 12, 16),
+               ("gemv_packed_ct2_kw16_s2", "gemv_packed_ct4_kw16_s4_e", "gemv_packed_ct1_kw8", "gemv_packed_ct1_kw8_e")),
+              (7, 4096, 4096, (8, 16), ("gemv_packed_ct1_kw8", "gemv_packed_ct1_kw8_e"))]
+    for op, N, K, Ms, cands in shapes:
+        names = [hx.config_get(op, i)["name"] for i in range(hx.config_count(op))]
         ws = []
-        for _ in range(12):
-            w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
-            sc = torch.empty(N, dtype=torch.float16, device=dev).uniform_(0.001, 0.02, generator=g)
-            ws.append(hx.ResidentWeight(w, sc, layout="nk"))
-            del w
+        if op == 6:
+            for _ in range(12):
+                w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+                sc = torch.empty(N, dtype=torch.float16, device=dev).uniform_(0.001, 0.02, generator=g)
+                ws.append(hx.ResidentWeight(w, sc, layout="nk"))
+                del w
+        else:
+            for _ in range(max(2, -(-(600 << 20) // (2 * N * K)))):
+                w = torch.empty((N, K), dtype=torch.float16, device=dev).uniform_(-1, 1, generator=g)
+                ws.append(hx.ResidentWeight(w, None, layout="nk"))
+                del w
         try:
-            lines += [f"## N = {N}, K = {K}", "", "| M | " + " | ".join(c.replace("gemv_packed_", "") for c in cands)
-                      + " |", "|---:|" + "---:|" * len(cands)]
+            lines += [f"## {'int8' if op == 6 else 'f16'}, N = {N}, K = {K}", "",
+                      "| M | " + " | ".join(c.replace("gemv_packed_", "") for c in cands) + " |",
+                      "|---:|" + "---:|" * len(cands)]
             for M in Ms:
-                hx.config_select(6, M, N, K, -1)
-                default = names[hx.config_lookup(6, M, N, K)]
+                hx.config_select(op, M, N, K, -1)
+                default = names[hx.config_lookup(op, M, N, K)]
                 x = torch.randn((M, K), dtype=torch.float16, device=dev, generator=g)
                 ys = [torch.empty((M, N), dtype=torch.float16, device=dev) for _ in ws]
                 t = {c: [] for c in cands}
                 try:
                     for _ in range(rounds):
                         for c in cands:
-                            hx.config_select(6, M, N, K, names.index(c))
+                            hx.config_select(op, M, N, K, names.index(c))
                             calls = [hx.bind_matmul_resident(x, w, y) for w, y in zip(ws, ys)]
                             t[c].append(event_timed(calls, iters, regions=1)[0] * 1e3)
                 finally:
-                    hx.config_select(6, M, N, K, -1)
+                    hx.config_select(op, M, N, K, -1)
                 cells = []
                 for c in cands:
                     r = np.asarray(t[c])
@@ -1034,6 +1049,8 @@ def gemv_ab(hx, rounds: int = 5, iters: int = 400) -> str:
         finally:
             for w in ws:
                 w.release()
+            del ws
+            torch.cuda.empty_cache()
     return "\n".join(lines) + "\n"
 
 
