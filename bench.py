@@ -1054,6 +1054,53 @@ def gemv_ab(hx, rounds: int = 5, iters: int = 400) -> str:
     return "\n".join(lines) + "\n"
 
 
+def ffn_decode_table(hx, iters: int = 200) -> str:
+    """The SwiGLU FFN block (H = 4096, I = 11008, int8 weights) at decode and
+    small-prefill token counts: each call alternates between two registered
+    weight sets (so the weights stream from HBM, 2 x 271 MB), five timed
+    regions of ``iters`` calls, with each stage's route and config from the
+    plan manifest.  Markdown on stdout."""
+    import torch
+    H, I = 4096, 11008
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(17)
+
+    def w(k, n):
+        wt = torch.randint(-127, 128, (k, n), dtype=torch.int8, device=dev, generator=g)
+        s = torch.empty(n, dtype=torch.float16, device=dev).uniform_(0.5, 1.5, generator=g) / (127 * (k / 3) ** 0.5)
+        return hx.ResidentWeight(wt, s.half(), layout="kn")
+
+    sets = [(w(H, I), w(H, I), w(I, H)) for _ in range(2)]
+    gamma = torch.randn(H, dtype=torch.float16, device=dev, generator=g) * 0.1 + 1.0
+    lines = ["# SwiGLU FFN block at decode token counts (bench.py --ffn-decode)", "",
+             f"H = {H}, I = {I}, int8 weights with per-channel scales; calls alternate between two registered "
+             f"weight sets; five timed regions of {iters} calls (HIP events); us per call, median [q20, q80]; "
+             "the route and config of each stage from the plan manifest.", "",
+             "| tokens | us per call | weight GB/s | stages |", "|---:|---:|---:|---|"]
+    try:
+        for T in (1, 4, 8, 12, 16, 17, 24, 32, 33, 48, 64):
+            x = torch.randn((T, H), dtype=torch.float16, device=dev, generator=g)
+            y = torch.empty_like(x)
+            calls = [(lambda ws=ws: hx.swiglu_ffn(x, gamma, 1e-6, *ws, out=y)) for ws in sets]
+            for c in calls:
+                c()
+            hx.manifest_clear()
+            hx.manifest_enable(True)
+            calls[0]()
+            hx.manifest_enable(False)
+            stages = "; ".join(f"{r['plan']}:{r['config']}" for r in hx.manifest()["records"])
+            tm = event_timed(calls, iters, regions=5)
+            sp = tm.spread()
+            us = tm[0] * 1e3
+            gbs = 3 * H * I / (us * 1e-6) / 1e9
+            lines.append(f"| {T} | {us:.2f} [{sp['q20_us']:.2f}, {sp['q80_us']:.2f}] | {gbs:.0f} | {stages} |")
+    finally:
+        for ws in sets:
+            for r in ws:
+                r.release()
+    return "\n".join(lines) + "\n"
+
+
 def rows_ab(hx, rounds: int = 5, iters: int = 60) -> str:
     """Interleaved A/B of the row configurations (one row per workgroup
     against the streaming form at 2, 4 and 8 workgroups per CU), pinned
@@ -1668,6 +1715,8 @@ def main() -> int:
                     help="time the untuned default configs (skip the tile search)")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="launch each benchmarked kernel a few times for rocprofv3 --pmc")
+    ap.add_argument("--ffn-decode", action="store_true",
+                    help="the SwiGLU FFN block at decode token counts, markdown on stdout, exit")
     ap.add_argument("--gemv-ab", action="store_true",
                     help="interleaved A/B of the decode GEMV default candidates, markdown on stdout, exit")
     ap.add_argument("--vendor", action="store_true",
@@ -1720,6 +1769,9 @@ def main() -> int:
         return 0
     if args.gemv_ab:
         print(gemv_ab(hx), end="", flush=True)
+        return 0
+    if args.ffn_decode:
+        print(ffn_decode_table(hx), end="", flush=True)
         return 0
     if args.rows_ab:
         print(rows_ab(hx), end="", flush=True)

@@ -499,7 +499,7 @@ static int gemv_untuned(int op, int64_t M, int64_t N, int64_t K, bool in_place =
   return c && (!gemv_xl_fits(*c, M, K, wt) || (c->split > 1 && !gemv_split_takes(*c, M, N))) ? c->base : t;
 }
 static int gemv_untuned_table(int op, int64_t M, int64_t N, int64_t K, bool in_place) {
-  if (M > 16) return gemv_rows_default(M, N);
+  if (M > 16) return gemv_rows_default(M, N, K);
   const int64_t tiles = (N + 15) / 16;
   const bool three_tiles = (tiles + 255) / 256 == 3;  // N = 11008: 688 tiles, 230 workgroups
   if (op != HX_OP_GEMV_W8 && in_place) {

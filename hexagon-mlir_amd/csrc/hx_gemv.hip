@@ -724,6 +724,13 @@ struct GemvStreamEntry {
    &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_I8, 1, false, SP, true>,                         \
    &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_F16, 1, true, SP, true>,                         \
    &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_BF16, 1, true, SP, true>}
+#define HX_GSR(CT, KW, CPW, MB)                                                                     \
+  {&gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_I8, MB, true, true, true>,                       \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_F16, MB, false, true, true>,                     \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_BF16, MB, false, true, true>,                    \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_I8, MB, false, true, true>,                      \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_F16, MB, true, true, true>,                      \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_BF16, MB, true, true, true>}
 #define HX_GR(CT, KW, CPW, MB)                                                                      \
   {&gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_I8, MB>,                                        \
    &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_F16, MB>,                                       \
@@ -799,9 +806,14 @@ static const GemvStreamEntry kGemvStream[] = {
     {{1, 8, "packed_ct1_kw8_e", 0, 31, 1}, HX_GE(1, 8, 8, false)},
     {{1, 16, "packed_ct1_kw16_e", 0, 32, 1}, HX_GE(1, 16, 4, false)},
     {{4, 16, "packed_ct4_kw16_s4_e", 0, 8, 1, 4}, HX_GE(4, 16, 2, true)},
+    // two row blocks (16 < M <= 32) with K split over workgroups and the
+    // loads issued ahead
+    {{4, 16, "rows2_ct4_kw16_s4_e", 0, 8, 2, 4}, HX_GSR(4, 16, 2, 2)},
+    {{2, 16, "rows2_ct2_kw16_s2_e", 0, 0, 2, 2}, HX_GSR(2, 16, 2, 2)},
 };
 #undef HX_GR
 #undef HX_GE
+#undef HX_GSR
 #undef HX_GS
 #undef HX_GV
 int gemv_packed_config_count() { return (int)(sizeof(kGemvStream) / sizeof(kGemvStream[0])); }
@@ -816,7 +828,7 @@ static int launch_gemv_stream(int cfg_idx, int wt, bool packed, const GemvArgs& 
   if (cfg_idx < 0 || cfg_idx >= gemv_packed_config_count()) return HXI_ERR_ARG;
   if (a.M < 1 || a.M > kGemvMaxRows) return HXI_ERR_SHAPE;
   // a config whose row blocks cannot hold M runs as the row-block default
-  if (a.M > 16 * kGemvStream[cfg_idx].cfg.mb) cfg_idx = gemv_rows_default(a.M, a.N);
+  if (a.M > 16 * kGemvStream[cfg_idx].cfg.mb) cfg_idx = gemv_rows_default(a.M, a.N, a.K);
   const int slot = wt == DT_I8 ? (packed ? 0 : 3) : wt == DT_F16 ? (packed ? 4 : 1) : wt == DT_BF16 ? (packed ? 5 : 2) : -1;
   if (slot < 0) return HXI_ERR_ARG;
   const int64_t kd = wt == DT_I8 ? 64 : 32;
@@ -846,7 +858,7 @@ static int launch_gemv_stream(int cfg_idx, int wt, bool packed, const GemvArgs& 
 }
 bool gemv_split_takes(const GemvConfig& c, int64_t M, int64_t N) {
   // M <= 4 takes the few-row reduction, which finishes in place
-  return c.split > 1 && c.mb == 1 && !c.xl && M > 4 && M <= 16 &&
+  return c.split > 1 && c.mb <= 2 && !c.xl && M > 4 && M <= 16 * c.mb &&
          ((N + 15) / 16 + c.ct - 1) / c.ct <= kGemvSplitCounters;
 }
 size_t gemv_split_bytes(int cfg, int64_t M, int64_t N) {
@@ -862,12 +874,20 @@ bool gemv_xl_fits(const GemvConfig& c, int64_t M, int64_t K, int wt) {
 // Measured at M = 17..64 (tuner medians, rotating packed images): up to 32
 // rows two row blocks over three tiles where that gives one workgroup per
 // CU (int8 N = 11008, M = 17 / 24 / 32: 15.2 / 15.8 / 16.7 us against 17.1 /
-// 19.9 / 23.4 for two tiles), two tiles above 256 tiles, else one tile over
-// 16 waves (int8 N = 4096, K = 11008: 18.7 / 22.2 / 26.5 against 25.1 / 26.5
+// 19.9 / 23.4 for two tiles), two tiles above 256 tiles, the K split below
+// on the down projection's shapes, else one tile over 16 waves (int8 N =
+// 4096, K = 11008, before the split: 18.7 / 22.2 / 26.5 against 25.1 / 26.5
 // / 29.6 over 8 waves); beyond 32 rows (kernels only: the products route
 // those shapes to the tiled GEMM) four row blocks over four tiles or one.
-int gemv_rows_default(int64_t M, int64_t N) {
+int gemv_rows_default(int64_t M, int64_t N, int64_t K) {
   const int64_t tiles = (N + 15) / 16;
+  // more than 128 and at most 256 tiles with K >= 8192 (the FFN's down
+  // projection): two row blocks with K split over workgroups, loads issued
+  // ahead -- two tiles over two parts up to 20 rows, four over four beyond
+  // (4096 x 11008, M = 17 / 20 / 24 / 28 / 32: 14.81 / 15.74 / 16.82 /
+  // 18.02 / 19.18 and 15.89 / 16.22 / 16.64 / 17.27 / 17.75 us against
+  // 18.53 / 20.31 / 22.25 / 24.10 / 26.02 for one tile over 16 waves)
+  if (M <= 32 && tiles > 128 && tiles <= 256 && K >= 8192) return M <= 20 ? 35 : 34;
   if (M <= 32) return (tiles + 255) / 256 == 3 ? 21 : tiles > 256 ? 14 : 23;
   return N >= 160 * 64 ? 17 : 15;
 }

@@ -177,7 +177,7 @@ inline bool gemv_rows_route(int64_t M, int64_t N, bool packed, bool int8 = false
   return packed || N <= kGemvRowsInPlaceMaxN;
 }
 // Untuned row-block config for 16 < M <= kGemvMaxRows.
-int gemv_rows_default(int64_t M, int64_t N);
+int gemv_rows_default(int64_t M, int64_t N, int64_t K);
 // Whether config c may stage M activation rows of K (wt: the weight's type)
 // in LDS; a config that may not runs as its base config.
 bool gemv_xl_fits(const GemvConfig& c, int64_t M, int64_t K, int wt);

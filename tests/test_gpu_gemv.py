@@ -169,11 +169,13 @@ def _split_configs(hx):
     return [(i, hx.config_get(6, i)) for i in range(hx.config_count(6)) if hx.config_get(6, i)["split_k"] > 1]
 
 
-@pytest.mark.parametrize("shape", [(16, 4096, 11008), (9, 1000, 4112), (12, 37, 640), (6, 300, 8200)],
+@pytest.mark.parametrize("shape", [(16, 4096, 11008), (9, 1000, 4112), (12, 37, 640), (6, 300, 8200),
+                                   (24, 4096, 11008), (31, 300, 8200)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_gemv_split_k_over_workgroups(hx, dev, shape):
-    """Configs that split K over workgroups (M > 4): every part's binary32
-    partials and the last workgroup's sum in part order.  Within tolerance of
+    """Configs that split K over workgroups (M > 4; up to 32 rows for the
+    two-row-block ones): every part's binary32 partials and the last
+    workgroup's sum in part order.  Within tolerance of
     the oracle, bit-identical over repeated calls (the parts are added in
     the same order whichever workgroup finishes last, and every call returns
     the counters to zero for the next), with N not a multiple of the tile
@@ -210,7 +212,8 @@ def test_gemv_split_k_few_rows_run_the_base(hx, dev):
     names = [hx.config_get(6, i)["name"] for i in range(hx.config_count(6))]
     base = {"gemv_packed_ct2_kw16_s2": "gemv_packed_ct2_kw8", "gemv_packed_ct4_kw16_s4": "gemv_packed_ct4_kw16",
             "gemv_packed_ct6_kw16_s2": "gemv_packed_ct3_kw16", "gemv_packed_ct1_kw16_s2": "gemv_packed_ct1_kw16",
-            "gemv_packed_ct2_kw16_s4": "gemv_packed_ct2_kw8", "gemv_packed_ct4_kw16_s4_e": "gemv_packed_ct4_kw16"}
+            "gemv_packed_ct2_kw16_s4": "gemv_packed_ct2_kw8", "gemv_packed_ct4_kw16_s4_e": "gemv_packed_ct4_kw16",
+            "gemv_rows2_ct4_kw16_s4_e": "gemv_packed_ct4_kw16", "gemv_rows2_ct2_kw16_s2_e": "gemv_packed_ct2_kw8"}
     try:
         for sname, bname in base.items():
             got = []
@@ -267,11 +270,14 @@ def test_gemv_defaults_follow_the_ab(hx):
     issued ahead at N = 11008; the four-part K split at 16 rows of the down
     projection and one tile over 8 waves at 8; for an f16 packed image with
     one row, 16 waves at 8192 x 8192 and 8 at 4096 x 16384, and on the down
-    projection's shape four parts from 13 rows, two up to 12."""
+    projection's shape four parts from 13 rows, two up to 12; past 16 rows
+    two row blocks, split over K on the down projection's shape."""
     want = {(6, 1, 11008, 4096): "packed_ct3_kw16_e", (6, 4, 11008, 4096): "packed_ct3_kw16_e",
             (6, 16, 11008, 4096): "packed_ct3_kw16_e", (6, 16, 4096, 11008): "packed_ct4_kw16_s4_e",
             (6, 8, 4096, 11008): "packed_ct1_kw8_e", (7, 1, 8192, 8192): "packed_ct1_kw16_xl",
             (7, 1, 4096, 16384): "packed_ct1_kw8_xl", (7, 16, 4096, 11008): "packed_ct4_kw16_s4_e",
-            (7, 12, 4096, 11008): "packed_ct2_kw16_s2", (7, 8, 4096, 4096): "packed_ct1_kw8_e"}
+            (7, 12, 4096, 11008): "packed_ct2_kw16_s2", (7, 8, 4096, 4096): "packed_ct1_kw8_e",
+            (6, 17, 4096, 11008): "rows2_ct2_kw16_s2_e", (6, 24, 4096, 11008): "rows2_ct4_kw16_s4_e",
+            (6, 24, 11008, 4096): "rows2_ct3_kw8"}
     got = {k: hx.config_get(k[0], hx.config_lookup(*k))["name"] for k in want}
     assert all(got[k].endswith(v) for k, v in want.items()), got

@@ -135,7 +135,7 @@ def test_c3_kn_argument_tight(hx, dev, c3, M):
     assert c3_gate_failures(to_np(y).astype(np.float64), *ref[M]) == []
 
 
-SPLIT_SHAPES = [(16, 4096, 11008), (12, 2048, 8192)]
+SPLIT_SHAPES = [(16, 4096, 11008), (12, 2048, 8192), (28, 4096, 11008)]
 LAUNCHES = 2000
 BATCH = 100
 
