@@ -255,8 +255,9 @@ int hx_swiglu_ffn(const hx_memref2d* x, const hx_memref1d* gamma, float eps,
  * of the stream workspace.  The call makes no hipMalloc or hipFree.  It
  * needs T*(H + I)*2 bytes for T > 32 tokens (at most T*(H + 3 I)*2 for T <= 32, the
  * decode path), plus T*H*4 per K part when the down projection's
- * configuration splits K (on the decode path T*I*4 per part when a decode
- * GEMV's configuration splits K; 256-byte aligned each), out of the array
+ * configuration splits K (on the decode path T*N*4 per part, N = I or H,
+ * for the decode GEMVs whose configuration splits K; 256-byte aligned
+ * each), out of the array
  * less its last 64 KiB (the split decode GEMV's counters, zero between
  * calls); a shape that needs more returns HX_ERR_UNSUPPORTED before
  * anything is enqueued.  Every call on one GPU shares its array: calls that
@@ -286,7 +287,9 @@ enum {
 
 /* One compiled configuration.  GEMM families fill bm/bn/bk (K elements per
  * LDS stage)/waves_m/waves_n/lds_stages (K stages resident in LDS: 2 or 3)/
- * split_k (K parts, partials merged by a second kernel; 1: none); the GEMV
+ * split_k (K parts, merged inside the kernel by the last part of each
+ * tile to finish, or by a merge kernel when the tiles outnumber the split
+ * counters; 1: none); the GEMV
  * families fill col_tiles (16-column tiles per workgroup), waves_m (waves
  * splitting K inside a workgroup) and split_k (workgroups splitting K per
  * group of col_tiles tiles, the last of them to finish adding the parts;
