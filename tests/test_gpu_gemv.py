@@ -281,3 +281,35 @@ def test_gemv_defaults_follow_the_ab(hx):
             (6, 24, 11008, 4096): "rows2_ct3_kw8"}
     got = {k: hx.config_get(k[0], hx.config_lookup(*k))["name"] for k in want}
     assert all(got[k].endswith(v) for k, v in want.items()), got
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_gemv_load_schedule_keeps_the_bits(hx, dev, M):
+    """The `_e` configs change only when the slice's loads issue: each one
+    gives the bits of its twin with the compiler's load schedule (same
+    tiles, waves, K split and summation order), on the int8 image at the C3
+    width and on an f16 image."""
+    import torch
+    twins = {"gemv_packed_ct3_kw16_e": "gemv_packed_ct3_kw16", "gemv_packed_ct1_kw8_e": "gemv_packed_ct1_kw8",
+             "gemv_packed_ct1_kw16_e": "gemv_packed_ct1_kw16",
+             "gemv_packed_ct4_kw16_s4_e": "gemv_packed_ct4_kw16_s4"}
+    N, K = 11008, 4096
+    x, w, s = case(M, N, K, seed=730 + M)
+    g = torch.Generator(device=dev).manual_seed(731 + M)
+    wf = torch.empty((N, K), dtype=torch.float16, device=dev).uniform_(-1, 1, generator=g)
+    xf = torch.randn((M, K), dtype=torch.float16, device=dev, generator=g)
+    for op, rw, xd in ((6, hx.ResidentWeight(to_dev(w, dev), to_dev(s, dev)), to_dev(x, dev)),
+                       (7, hx.ResidentWeight(wf, None, layout="nk"), xf)):
+        names = [hx.config_get(op, i)["name"] for i in range(hx.config_count(op))]
+        try:
+            for e, base in twins.items():
+                got = []
+                for name in (e, base):
+                    hx.config_select(op, M, N, K, names.index(name))
+                    try:
+                        got.append(to_np(hx.matmul_resident(xd, rw)))
+                    finally:
+                        hx.config_select(op, M, N, K, -1)
+                assert np.array_equal(got[0].view(np.uint16), got[1].view(np.uint16)), f"op {op} {e} M={M}"
+        finally:
+            rw.release()
