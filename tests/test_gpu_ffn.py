@@ -139,14 +139,16 @@ def test_swiglu_ffn_c5_full_size(hx, dev):
     assert rel < 2e-3, rel
 
 
-@pytest.mark.parametrize("T", [1, 4, 16, 24, 32])
-def test_swiglu_decode_equals_composition(hx, dev, T):
+@pytest.mark.parametrize("H,I,T", [(512, 2048, 1), (512, 2048, 4), (512, 2048, 16), (512, 2048, 24),
+                                   (512, 2048, 32), (4096, 11008, 1), (4096, 11008, 12), (4096, 11008, 24)])
+def test_swiglu_decode_equals_composition(hx, dev, H, I, T):
     """Decode-sized blocks fuse the gate into the up projection's epilogue
     (RNE(silu(g) * u) on the rounded outputs): the block equals, bit for
     bit, the composition of the public entry points -- RMSNorm, the gate and
-    up products, silu_mul, the down product."""
+    up products, silu_mul, the down product -- also at the north_star
+    widths, where the down projection splits K over workgroups from 12
+    tokens (two row blocks past 16)."""
     import torch
-    H, I = 512, 2048
     wg, sg, wu, su, wd, sd = weights(H, I, 700 + T)
     Wg = hx.ResidentWeight(to_dev(wg, dev), to_dev(sg, dev), layout="kn")
     Wu = hx.ResidentWeight(to_dev(wu, dev), to_dev(su, dev), layout="kn")
