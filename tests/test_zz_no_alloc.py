@@ -38,8 +38,9 @@ def _noalloc(hx, x, gamma, eps, Wg, Wu, Wd, y, stream):
 
 def test_noalloc_matches_and_allocates_nothing(hx, dev):
     """No-allocation calls in a row (256 tokens: the fused gate/up GEMM and
-    the K-split down projection; then 24 tokens: the decode GEMVs; then 16:
-    the down projection's decode GEMV split over workgroups, its partials and
+    the K-split down projection; then 24 tokens: the decode GEMVs, the down
+    projection's two row blocks split over workgroups; then 16: the down
+    projection's decode GEMV split over workgroups; the splits' partials and
     counters in the scratch) leave the device's free memory unchanged and
     equal hx_swiglu_ffn bit for bit.  A
     warm-up pass first lets the HIP runtime load the kernels' code objects
