@@ -298,10 +298,16 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
     // are taken, so they run under the previous step's MFMAs; each column
     // tile still accumulates the steps in order, and the row sum adds the
     // exponentials in the same order as one pass over the block would.
+    // D = 128: each step, from its V^T reads to its MFMAs, runs at wave
+    // priority 1 (s_setprio), so the SIMD issues it ahead of the other
+    // wave's instructions and the step's MFMAs reach the matrix core sooner
+    // (MI355X, interleaved A/B: causal 4096 x 2048 x 128 heads 5% faster,
+    // non-causal 1-2%; D = 64 7% slower with it, so it stays at 0 there).
     float rs = 0.f;
     static_for<PS>([&](auto tc) {
       constexpr int t = decltype(tc)::value;
       constexpr int jt = t >> 1, g0 = 2 * (t & 1);
+      if constexpr (D == 128) __builtin_amdgcn_s_setprio(1);
       v4i vf[DTILES];
       static_for<DTILES>([&](auto dc) {
         constexpr int dt = decltype(dc)::value;
@@ -321,6 +327,7 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs p) {
         constexpr int dt = decltype(dc)::value;
         oacc[dt] = mfma_att<DT>(vf[dt], pf, oacc[dt]);
       });
+      if constexpr (D == 128) __builtin_amdgcn_s_setprio(0);
     });
     rs += __shfl_xor(rs, 32);
     l_i += rs;
