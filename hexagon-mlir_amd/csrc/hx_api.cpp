@@ -1443,7 +1443,7 @@ extern "C" int hx_weight_info(hx_weight_t w, int64_t* k, int64_t* n, int* dtype,
 // one workgroup's tiles.
 static bool packed_gemv_takes(const View2& vx, const hx_weight* w, bool residual, int y_dt) {
   const int64_t M = vx.rows;
-  return w->dtype == HX_I8 && w->packed && gemv_rows_route(M, w->N, true, true) && !residual && y_dt == HX_F16 &&
+  return w->dtype == HX_I8 && w->packed && gemv_rows_route(M, w->N, true, true, w->K) && !residual && y_dt == HX_F16 &&
          w->K % 8 == 0 && ((uintptr_t)vx.p & 15u) == 0 && (vx.ld * 2) % 16 == 0 &&
          M * vx.ld * 2 < ((int64_t)1 << 31) && (w->K + 63) / 64 * 4 * 1024 < ((int64_t)1 << 31);
 }
@@ -1569,9 +1569,14 @@ int hx::swiglu_ffn_impl(const hx_memref2d* x, const hx_memref1d* gamma, float ep
 
   // up to 32 tokens: the decode GEMVs and their row blocks (H = 4096,
   // I = 11008, T = 17 / 24 / 32: 61.1 / 63.8 / 69.2 us against 76.0 / 78.4 /
-  // 82.0 with the fused gate/up GEMM); beyond, the GEMMs (T = 48 / 64: 100.3
-  // / 107.4 us, the row blocks 103.0 / 112.8)
-  const bool skinny = T <= kGemvRowsMaxM;
+  // 82.0 with the fused gate/up GEMM); up to 64 where all three products
+  // take the packed GEMV's four row blocks (gemv_rows4_i8: at H = 4096,
+  // I = 11008 up to 48 tokens); beyond, the fused gate/up GEMM, whose down
+  // projection still takes the row blocks where they win
+  const bool skinny = T <= kGemvRowsMaxM ||
+                      (T <= kGemvRowsMaxMI8 && packed_gemv_takes(View2{nullptr, T, H, H}, wg, false, HX_F16) &&
+                       packed_gemv_takes(View2{nullptr, T, H, H}, wu, false, HX_F16) &&
+                       packed_gemv_takes(View2{nullptr, T, I, I}, wd, false, HX_F16));
   Carver cv;
   const size_t off_h = cv.take((size_t)T * H * 2);
   const size_t off_a = cv.take((size_t)T * I * 2);
@@ -1589,7 +1594,10 @@ int hx::swiglu_ffn_impl(const hx_memref2d* x, const hx_memref1d* gamma, float ep
     // the same scratch, after the intermediates
     ws = fixed->base;
     size_t part = 0;
-    if (!skinny) {
+    if (!skinny && packed_gemv_takes(View2{nullptr, T, I, I}, wd, false, HX_F16)) {
+      // the down projection takes the packed GEMV's row blocks
+      part = gemv_split_bytes(resolve_gemv(HX_OP_GEMV_W8, T, H, I), T, H);
+    } else if (!skinny) {
       GemmArgs d{};
       d.a = ws + off_a; d.lda = I;
       d.b = wd->image; d.ldb = I;

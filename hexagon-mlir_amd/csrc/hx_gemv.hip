@@ -731,6 +731,13 @@ struct GemvStreamEntry {
    &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_I8, MB, false, true, true>,                      \
    &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_F16, MB, true, true, true>,                      \
    &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_BF16, MB, true, true, true>}
+#define HX_GRE(CT, KW, CPW, MB)                                                                     \
+  {&gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_I8, MB, true, false, true>,                      \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_F16, MB, false, false, true>,                    \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_BF16, MB, false, false, true>,                   \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_I8, MB, false, false, true>,                     \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_F16, MB, true, false, true>,                     \
+   &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_BF16, MB, true, false, true>}
 #define HX_GR(CT, KW, CPW, MB)                                                                      \
   {&gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_I8, MB>,                                        \
    &gemv_stream_one<CT, KW, CPW, XS_NONE, false, DT_F16, MB>,                                       \
@@ -810,8 +817,18 @@ static const GemvStreamEntry kGemvStream[] = {
     // loads issued ahead
     {{4, 16, "rows2_ct4_kw16_s4_e", 0, 8, 2, 4}, HX_GSR(4, 16, 2, 2)},
     {{2, 16, "rows2_ct2_kw16_s2_e", 0, 0, 2, 2}, HX_GSR(2, 16, 2, 2)},
+    // four row blocks (32 < M <= 64), loads issued ahead: three tiles over
+    // sixteen waves, and four tiles with K split in four (interleaved A/B
+    // against the tiled W8A16 GEMM, int8 packed images rotating over 600 MB;
+    // N = 11008, K = 4096, M = 33 / 48 / 64: 16.90 / 20.88 / 23.33 against
+    // 21.03 / 22.35 / 22.62 us; N = 4096, K = 11008: 22.37 / 24.21 / 28.30
+    // against 31.11 / 31.30 / 31.32, where the unsplit rows4_ct1_kw8 took
+    // 37.5 / 44.4 / 50.0)
+    {{3, 16, "rows4_ct3_kw16_e", 0, 22, 4}, HX_GRE(3, 16, 1, 4)},
+    {{4, 8, "rows4_ct4_kw8_s4_e", 0, 17, 4, 4}, HX_GSR(4, 8, 2, 4)},
 };
 #undef HX_GR
+#undef HX_GRE
 #undef HX_GE
 #undef HX_GSR
 #undef HX_GS
@@ -858,7 +875,7 @@ static int launch_gemv_stream(int cfg_idx, int wt, bool packed, const GemvArgs& 
 }
 bool gemv_split_takes(const GemvConfig& c, int64_t M, int64_t N) {
   // M <= 4 takes the few-row reduction, which finishes in place
-  return c.split > 1 && c.mb <= 2 && !c.xl && M > 4 && M <= 16 * c.mb &&
+  return c.split > 1 && !c.xl && M > 4 && M <= 16 * c.mb &&
          ((N + 15) / 16 + c.ct - 1) / c.ct <= kGemvSplitCounters;
 }
 size_t gemv_split_bytes(int cfg, int64_t M, int64_t N) {
@@ -877,8 +894,7 @@ bool gemv_xl_fits(const GemvConfig& c, int64_t M, int64_t K, int wt) {
 // 19.9 / 23.4 for two tiles), two tiles above 256 tiles, the K split below
 // on the down projection's shapes, else one tile over 16 waves (int8 N =
 // 4096, K = 11008, before the split: 18.7 / 22.2 / 26.5 against 25.1 / 26.5
-// / 29.6 over 8 waves); beyond 32 rows (kernels only: the products route
-// those shapes to the tiled GEMM) four row blocks over four tiles or one.
+// / 29.6 over 8 waves); beyond 32 rows four row blocks (below).
 int gemv_rows_default(int64_t M, int64_t N, int64_t K) {
   const int64_t tiles = (N + 15) / 16;
   // more than 128 and at most 256 tiles with K >= 8192 (the FFN's down
@@ -889,6 +905,13 @@ int gemv_rows_default(int64_t M, int64_t N, int64_t K) {
   // 18.53 / 20.31 / 22.25 / 24.10 / 26.02 for one tile over 16 waves)
   if (M <= 32 && tiles > 128 && tiles <= 256 && K >= 8192) return M <= 20 ? 35 : 34;
   if (M <= 32) return (tiles + 255) / 256 == 3 ? 21 : tiles > 256 ? 14 : 23;
+  // Beyond 32 rows, four row blocks with the loads issued ahead: four tiles
+  // with K split in four on the down projection's shapes, three tiles over
+  // sixteen waves where that gives one workgroup per CU (N = 11008).  The
+  // products route only these shapes here (gemv_rows_route); elsewhere the
+  // four-block kernels lost to the tiled GEMM.
+  if (tiles > 128 && tiles <= 256 && K >= 8192) return 37;
+  if ((tiles + 255) / 256 == 3) return 36;
   return N >= 160 * 64 ? 17 : 15;
 }
 int launch_gemv_packed(int cfg_idx, const GemvArgs& a, const int8_t* packed, hipStream_t s) {

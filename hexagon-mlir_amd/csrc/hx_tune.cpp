@@ -300,7 +300,7 @@ class Probe {
     exact_ = false;
     // the shapes the products run on this family (a registered weight's
     // packed image)
-    if (m_ > kGemvMaxRows || !gemv_rows_route(m_, n_, true, op_ == HX_OP_GEMV_W8)) family_reason_ = "family-shape";
+    if (m_ > kGemvMaxRows || !gemv_rows_route(m_, n_, true, op_ == HX_OP_GEMV_W8, k_)) family_reason_ = "family-shape";
     const int64_t mm = std::min<int64_t>(m_, kGemvMaxRows);
     const size_t eb = es_of(wt_);
     // every family times the registered weight's packed image, the form a

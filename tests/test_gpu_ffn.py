@@ -2,8 +2,10 @@
 so the oracle finishes in seconds): RMSNorm -> int8 gate/up GEMMs with
 per-channel scales -> SiLU*mul -> int8 down GEMM, every stage rounded to fp16
 as separate linalg ops would be.  Both the fused gate/up MFMA path (T > 32)
-and the decode path (T <= 32: two GEMVs, with 16-row blocks past 16 tokens)
-are covered."""
+and the decode path (T <= 32: two GEMVs, with 16-row blocks past 16 tokens;
+up to 64 tokens where all three products take the GEMV's four row blocks,
+48 at H = 4096, I = 11008) are covered, and the fused path whose down
+projection takes the row blocks (64 tokens at those widths)."""
 import numpy as np
 import pytest
 
@@ -26,7 +28,8 @@ def weights(H, I, seed):
     return wg, sg, wu, su, wd, sd
 
 
-@pytest.mark.parametrize("T,H,I", [(256, 512, 1376), (4, 512, 1376), (24, 512, 1376), (40, 512, 1376), (130, 256, 704)])
+@pytest.mark.parametrize("T,H,I", [(256, 512, 1376), (4, 512, 1376), (24, 512, 1376), (40, 512, 1376), (130, 256, 704),
+                                   (40, 4096, 11008), (64, 4096, 11008)])
 def test_swiglu_ffn(hx, dev, T, H, I):
     wg, sg, wu, su, wd, sd = weights(H, I, 300)
     x = rng(301).normal(0, 1, (T, H)).astype(np.float16)
@@ -140,14 +143,15 @@ def test_swiglu_ffn_c5_full_size(hx, dev):
 
 
 @pytest.mark.parametrize("H,I,T", [(512, 2048, 1), (512, 2048, 4), (512, 2048, 16), (512, 2048, 24),
-                                   (512, 2048, 32), (4096, 11008, 1), (4096, 11008, 12), (4096, 11008, 24)])
+                                   (512, 2048, 32), (4096, 11008, 1), (4096, 11008, 12), (4096, 11008, 24),
+                                   (4096, 11008, 40), (4096, 11008, 48)])
 def test_swiglu_decode_equals_composition(hx, dev, H, I, T):
     """Decode-sized blocks fuse the gate into the up projection's epilogue
     (RNE(silu(g) * u) on the rounded outputs): the block equals, bit for
     bit, the composition of the public entry points -- RMSNorm, the gate and
     up products, silu_mul, the down product -- also at the north_star
     widths, where the down projection splits K over workgroups from 12
-    tokens (two row blocks past 16)."""
+    tokens (two row blocks past 16, four past 32)."""
     import torch
     wg, sg, wu, su, wd, sd = weights(H, I, 700 + T)
     Wg = hx.ResidentWeight(to_dev(wg, dev), to_dev(sg, dev), layout="kn")

@@ -170,11 +170,12 @@ def _split_configs(hx):
 
 
 @pytest.mark.parametrize("shape", [(16, 4096, 11008), (9, 1000, 4112), (12, 37, 640), (6, 300, 8200),
-                                   (24, 4096, 11008), (31, 300, 8200)],
+                                   (24, 4096, 11008), (31, 300, 8200), (40, 4096, 11008), (64, 300, 8200)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_gemv_split_k_over_workgroups(hx, dev, shape):
-    """Configs that split K over workgroups (M > 4; up to 32 rows for the
-    two-row-block ones): every part's binary32 partials and the last
+    """Configs that split K over workgroups (M > 4; up to 16 rows per row
+    block: 32 for two blocks, 64 for four; a config whose blocks cannot hold
+    M runs the row-block default): every part's binary32 partials and the last
     workgroup's sum in part order.  Within tolerance of
     the oracle, bit-identical over repeated calls (the parts are added in
     the same order whichever workgroup finishes last, and every call returns
@@ -213,7 +214,8 @@ def test_gemv_split_k_few_rows_run_the_base(hx, dev):
     base = {"gemv_packed_ct2_kw16_s2": "gemv_packed_ct2_kw8", "gemv_packed_ct4_kw16_s4": "gemv_packed_ct4_kw16",
             "gemv_packed_ct6_kw16_s2": "gemv_packed_ct3_kw16", "gemv_packed_ct1_kw16_s2": "gemv_packed_ct1_kw16",
             "gemv_packed_ct2_kw16_s4": "gemv_packed_ct2_kw8", "gemv_packed_ct4_kw16_s4_e": "gemv_packed_ct4_kw16",
-            "gemv_rows2_ct4_kw16_s4_e": "gemv_packed_ct4_kw16", "gemv_rows2_ct2_kw16_s2_e": "gemv_packed_ct2_kw8"}
+            "gemv_rows2_ct4_kw16_s4_e": "gemv_packed_ct4_kw16", "gemv_rows2_ct2_kw16_s2_e": "gemv_packed_ct2_kw8",
+            "gemv_rows4_ct4_kw8_s4_e": "gemv_rows4_ct4_kw8"}
     try:
         for sname, bname in base.items():
             got = []
@@ -271,16 +273,47 @@ def test_gemv_defaults_follow_the_ab(hx):
     projection and one tile over 8 waves at 8; for an f16 packed image with
     one row, 16 waves at 8192 x 8192 and 8 at 4096 x 16384, and on the down
     projection's shape four parts from 13 rows, two up to 12; past 16 rows
-    two row blocks, split over K on the down projection's shape."""
+    two row blocks, split over K on the down projection's shape; past 32
+    rows four row blocks, three tiles over 16 waves at N = 11008 and four
+    tiles over four K parts on the down projection's shape."""
     want = {(6, 1, 11008, 4096): "packed_ct3_kw16_e", (6, 4, 11008, 4096): "packed_ct3_kw16_e",
             (6, 16, 11008, 4096): "packed_ct3_kw16_e", (6, 16, 4096, 11008): "packed_ct4_kw16_s4_e",
             (6, 8, 4096, 11008): "packed_ct1_kw8_e", (7, 1, 8192, 8192): "packed_ct1_kw16_xl",
             (7, 1, 4096, 16384): "packed_ct1_kw8_xl", (7, 16, 4096, 11008): "packed_ct4_kw16_s4_e",
             (7, 12, 4096, 11008): "packed_ct2_kw16_s2", (7, 8, 4096, 4096): "packed_ct1_kw8_e",
             (6, 17, 4096, 11008): "rows2_ct2_kw16_s2_e", (6, 24, 4096, 11008): "rows2_ct4_kw16_s4_e",
-            (6, 24, 11008, 4096): "rows2_ct3_kw8"}
+            (6, 24, 11008, 4096): "rows2_ct3_kw8", (6, 33, 11008, 4096): "rows4_ct3_kw16_e",
+            (6, 48, 11008, 4096): "rows4_ct3_kw16_e", (6, 33, 4096, 11008): "rows4_ct4_kw8_s4_e",
+            (6, 64, 4096, 11008): "rows4_ct4_kw8_s4_e"}
     got = {k: hx.config_get(k[0], hx.config_lookup(*k))["name"] for k in want}
     assert all(got[k].endswith(v) for k, v in want.items()), got
+
+
+def test_gemv_four_row_blocks_route(hx, dev):
+    """A registered int8 weight takes the packed GEMV's four row blocks past
+    32 rows only where they beat the tiled GEMM: on the down projection's
+    shape (4096 x 11008) up to 64 rows, at N = 11008, K = 4096 up to 48;
+    65 rows, 64 rows at N = 11008, and a narrow weight take the GEMM.  Each
+    result is within the oracle's tolerance."""
+    cases = [(40, 4096, 11008, "gemv"), (64, 4096, 11008, "gemv"), (65, 4096, 11008, "tiled"),
+             (48, 11008, 4096, "gemv"), (64, 11008, 4096, "tiled"), (40, 512, 512, "tiled")]
+    for M, N, K, route in cases:
+        x, w, s = case(M, N, K, seed=760 + M)
+        rw = hx.ResidentWeight(to_dev(w, dev), to_dev(s, dev))
+        hx.manifest_clear()
+        hx.manifest_enable(True)
+        try:
+            y = hx.matmul_resident(to_dev(x, dev), rw)
+            plans = [r["plan"] for r in hx.manifest()["records"]]
+        finally:
+            hx.manifest_enable(False)
+            rw.release()
+        if route == "gemv":
+            assert plans and all(p.startswith("gemv") for p in plans), (M, N, K, plans)
+        else:
+            assert plans and all(p.startswith("mfma") for p in plans), (M, N, K, plans)
+        want = oracle.matmul(x, w, scale_n=s.astype(np.float32)).astype(np.float32)
+        assert_close(to_np(y).astype(np.float32), want, 1e-2, 1e-3, f"{M}x{N}x{K}")
 
 
 @pytest.mark.parametrize("M", [1, 4, 16])

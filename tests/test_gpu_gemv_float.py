@@ -358,7 +358,7 @@ def test_decode_float_split_k(hx, dev, dtype, shape):
     rw = hx.ResidentWeight(_dev(b, dtype, dev), layout="kn")
     ad, bd = _dev(a, dtype, dev), _dev(bnk, dtype, dev)
     splits = [i for i in range(hx.config_count(op)) if hx.config_get(op, i)["split_k"] > 1]
-    assert len(splits) == 8
+    assert len(splits) == 9
     try:
         for cfg in splits:
             hx.config_select(op, M, N, K, cfg)

@@ -38,7 +38,9 @@ def _noalloc(hx, x, gamma, eps, Wg, Wu, Wd, y, stream):
 
 def test_noalloc_matches_and_allocates_nothing(hx, dev):
     """No-allocation calls in a row (256 tokens: the fused gate/up GEMM and
-    the K-split down projection; then 24 tokens: the decode GEMVs, the down
+    the K-split down projection; 64: the fused gate/up GEMM and the down
+    projection's four row blocks split over workgroups; 40: the decode
+    GEMVs' four row blocks; then 24 tokens: the decode GEMVs, the down
     projection's two row blocks split over workgroups; then 16: the down
     projection's decode GEMV split over workgroups; the splits' partials and
     counters in the scratch) leave the device's free memory unchanged and
@@ -53,7 +55,7 @@ def test_noalloc_matches_and_allocates_nothing(hx, dev):
     assert hx._abi.load().hx_init() == 0, hx._abi.last_error()
     try:
         gamma = to_dev(rng(501).normal(1, 0.1, H).astype(np.float16), dev)
-        shapes = (256, 24, 16)
+        shapes = (256, 64, 40, 24, 16)
         xs = {T: to_dev(rng(502 + T).normal(0, 1, (T, H)).astype(np.float16), dev) for T in shapes}
         ys = {T: torch.full((T, H), 7.0, dtype=torch.float16, device=dev) for T in shapes}
         refs = {T: torch.full((T, H), 3.0, dtype=torch.float16, device=dev) for T in shapes}
@@ -64,7 +66,7 @@ def test_noalloc_matches_and_allocates_nothing(hx, dev):
             ys[T].fill_(7.0)
         torch.cuda.synchronize()
         free_before = torch.cuda.mem_get_info()[0]
-        for T in shapes:  # the measured calls: 256 tokens, then 24, then 16
+        for T in shapes:  # the measured calls, in that order
             with torch.cuda.stream(stream):
                 rc = _noalloc(hx, xs[T], gamma, 1e-6, Wg, Wu, Wd, ys[T], stream)
             assert rc == 0, hx._abi.last_error()
