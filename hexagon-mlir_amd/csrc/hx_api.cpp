@@ -1441,9 +1441,11 @@ extern "C" int hx_weight_info(hx_weight_t w, int64_t* k, int64_t* n, int* dtype,
 // the packed decode GEMV.  The packed GEMV reads activations as 8-element
 // (16-byte) groups, with 32-bit buffer offsets into the activation rows and
 // one workgroup's tiles.
-static bool packed_gemv_takes(const View2& vx, const hx_weight* w, bool residual, int y_dt) {
+// ffn: a product of the FFN block (gemv_rows4_i8).
+static bool packed_gemv_takes(const View2& vx, const hx_weight* w, bool residual, int y_dt, bool ffn = false) {
   const int64_t M = vx.rows;
-  return w->dtype == HX_I8 && w->packed && gemv_rows_route(M, w->N, true, true, w->K) && !residual && y_dt == HX_F16 &&
+  const bool route = gemv_rows_route(M, w->N, true, true, w->K) || (ffn && gemv_rows4_i8(M, w->N, w->K, true));
+  return w->dtype == HX_I8 && w->packed && route && !residual && y_dt == HX_F16 &&
          w->K % 8 == 0 && ((uintptr_t)vx.p & 15u) == 0 && (vx.ld * 2) % 16 == 0 &&
          M * vx.ld * 2 < ((int64_t)1 << 31) && (w->K + 63) / 64 * 4 * 1024 < ((int64_t)1 << 31);
 }
@@ -1452,13 +1454,14 @@ static bool packed_gemv_takes(const View2& vx, const hx_weight* w, bool residual
 // RNE(silu(gate) * RNE(x . W * s)), the SwiGLU gate fused into the epilogue.
 static int matmul_resident_impl(const View2& vx, hx_weight* w, const View2* vr, int r_dt,
                                 const View2& vy, int y_dt, hipStream_t s, const char* entry,
-                                const PartialsTarget& pt = PartialsTarget{}, const View2* gate = nullptr) {
+                                const PartialsTarget& pt = PartialsTarget{}, const View2* gate = nullptr,
+                                bool ffn = false) {
   const int x_dt = w->dtype == HX_BF16 ? HX_BF16 : HX_F16;
   const int64_t M = vx.rows;
   if (M == 0) return HX_OK;
-  if (gate && !packed_gemv_takes(vx, w, vr != nullptr, y_dt))
+  if (gate && !packed_gemv_takes(vx, w, vr != nullptr, y_dt, ffn))
     return fail(HX_ERR_ARG, "%s: fused gate needs the packed decode GEMV", entry);
-  if (packed_gemv_takes(vx, w, vr != nullptr, y_dt)) {
+  if (packed_gemv_takes(vx, w, vr != nullptr, y_dt, ffn)) {
     GemvArgs v{};
     v.x = vx.p; v.ldx = vx.ld; v.w = nullptr; v.ldw = 0;
     v.scale = w->scale; v.y = vy.p; v.ldy = vy.ld; v.M = M; v.N = w->N; v.K = w->K;
@@ -1570,13 +1573,14 @@ int hx::swiglu_ffn_impl(const hx_memref2d* x, const hx_memref1d* gamma, float ep
   // up to 32 tokens: the decode GEMVs and their row blocks (H = 4096,
   // I = 11008, T = 17 / 24 / 32: 61.1 / 63.8 / 69.2 us against 76.0 / 78.4 /
   // 82.0 with the fused gate/up GEMM); up to 64 where all three products
-  // take the packed GEMV's four row blocks (gemv_rows4_i8: at H = 4096,
-  // I = 11008 up to 48 tokens); beyond, the fused gate/up GEMM, whose down
+  // take the packed GEMV's four row blocks (gemv_rows4_i8; H = 4096,
+  // I = 11008, T = 33 / 48 / 64: 60.2 / 69.9 / 80.3 us against 84.6 / 86.0
+  // / 87.1 through the GEMMs); beyond, the fused gate/up GEMM, whose down
   // projection still takes the row blocks where they win
   const bool skinny = T <= kGemvRowsMaxM ||
-                      (T <= kGemvRowsMaxMI8 && packed_gemv_takes(View2{nullptr, T, H, H}, wg, false, HX_F16) &&
-                       packed_gemv_takes(View2{nullptr, T, H, H}, wu, false, HX_F16) &&
-                       packed_gemv_takes(View2{nullptr, T, I, I}, wd, false, HX_F16));
+                      (T <= kGemvRowsMaxMI8 && packed_gemv_takes(View2{nullptr, T, H, H}, wg, false, HX_F16, true) &&
+                       packed_gemv_takes(View2{nullptr, T, H, H}, wu, false, HX_F16, true) &&
+                       packed_gemv_takes(View2{nullptr, T, I, I}, wd, false, HX_F16, true));
   Carver cv;
   const size_t off_h = cv.take((size_t)T * H * 2);
   const size_t off_a = cv.take((size_t)T * I * 2);
@@ -1584,7 +1588,7 @@ int hx::swiglu_ffn_impl(const hx_memref2d* x, const hx_memref1d* gamma, float ep
   // u, as the silu_mul kernel would) when it runs the packed GEMV, so u
   // never leaves the kernel (the workspace's activations are 256-byte
   // aligned with rows of H halves)
-  const bool fuse_gate = skinny && packed_gemv_takes(View2{nullptr, T, H, H}, wu, false, HX_F16);
+  const bool fuse_gate = skinny && packed_gemv_takes(View2{nullptr, T, H, H}, wu, false, HX_F16, true);
   const size_t off_g = skinny ? cv.take((size_t)T * I * 2) : 0;
   const size_t off_u = skinny && !fuse_gate ? cv.take((size_t)T * I * 2) : 0;
   char* ws;
@@ -1630,12 +1634,12 @@ int hx::swiglu_ffn_impl(const hx_memref2d* x, const hx_memref1d* gamma, float ep
   View2 vh{h, T, H, H}, va{act, T, I, I};
   if (skinny) {
     View2 vgo{ws + off_g, T, I, I};
-    if ((rc = matmul_resident_impl(vh, wg, nullptr, 0, vgo, HX_F16, s, entry, pt))) return rc;
+    if ((rc = matmul_resident_impl(vh, wg, nullptr, 0, vgo, HX_F16, s, entry, pt, nullptr, true))) return rc;
     if (fuse_gate) {
-      if ((rc = matmul_resident_impl(vh, wu, nullptr, 0, va, HX_F16, s, entry, pt, &vgo))) return rc;
+      if ((rc = matmul_resident_impl(vh, wu, nullptr, 0, va, HX_F16, s, entry, pt, &vgo, true))) return rc;
     } else {
       View2 vuo{ws + off_u, T, I, I};
-      if ((rc = matmul_resident_impl(vh, wu, nullptr, 0, vuo, HX_F16, s, entry, pt))) return rc;
+      if ((rc = matmul_resident_impl(vh, wu, nullptr, 0, vuo, HX_F16, s, entry, pt, nullptr, true))) return rc;
       rc = map_internal(launch_silu_mul_f16(vgo.p, I, vuo.p, I, act, I, T, I, s), "silu_mul");
       if (rc) return rc;
     }
@@ -1649,7 +1653,7 @@ int hx::swiglu_ffn_impl(const hx_memref2d* x, const hx_memref1d* gamma, float ep
     g.col_scale = wg->scale; g.col_scale2 = wu->scale;
     if ((rc = run_gemm(HX_OP_SWIGLU_W8, g, s, PlanCtx{entry, "resident-image", HX_F16, HX_I8}, pt))) return rc;
   }
-  return matmul_resident_impl(va, wd, nullptr, 0, vy, HX_F16, s, entry, pt);
+  return matmul_resident_impl(va, wd, nullptr, 0, vy, HX_F16, s, entry, pt, nullptr, skinny);
 }
 
 extern "C" int hx_swiglu_ffn(const hx_memref2d* x, const hx_memref1d* gamma, float eps, hx_weight_t w_gate,

@@ -173,13 +173,15 @@ constexpr int64_t kGemvRowsInPlaceMaxN = 4096;
 // (32 < M <= 64) where they beat the tiled GEMM (interleaved A/B, rotating
 // images): the down projection's shapes (129..256 tiles of 16 columns,
 // K >= 8192) up to 64 rows, three tiles per CU (641..768 tiles, N = 11008)
-// up to 48 rows (at 64 rows the tiled GEMM is 3% faster there).
+// up to 48 rows (at 64 rows the tiled GEMM is 3% faster there).  In the FFN
+// block (ffn) the gate and up projections take them up to 64 rows: two
+// GEMVs then beat the fused gate/up GEMM.
 constexpr int64_t kGemvRowsMaxMI8 = 64;
-inline bool gemv_rows4_i8(int64_t M, int64_t N, int64_t K) {
+inline bool gemv_rows4_i8(int64_t M, int64_t N, int64_t K, bool ffn = false) {
   const int64_t tiles = (N + 15) / 16;
   if (M <= kGemvRowsMaxM || M > kGemvRowsMaxMI8) return false;
   if (tiles > 128 && tiles <= 256 && K >= 8192) return true;
-  return (tiles + 255) / 256 == 3 && M <= 48;
+  return (tiles + 255) / 256 == 3 && (ffn || M <= 48);
 }
 inline bool gemv_rows_route(int64_t M, int64_t N, bool packed, bool int8 = false, int64_t K = 0) {
   if (M <= 16) return true;

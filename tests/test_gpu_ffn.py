@@ -3,9 +3,10 @@ so the oracle finishes in seconds): RMSNorm -> int8 gate/up GEMMs with
 per-channel scales -> SiLU*mul -> int8 down GEMM, every stage rounded to fp16
 as separate linalg ops would be.  Both the fused gate/up MFMA path (T > 32)
 and the decode path (T <= 32: two GEMVs, with 16-row blocks past 16 tokens;
-up to 64 tokens where all three products take the GEMV's four row blocks,
-48 at H = 4096, I = 11008) are covered, and the fused path whose down
-projection takes the row blocks (64 tokens at those widths)."""
+up to 64 tokens where all three products take the GEMV's four row blocks)
+are covered, and the fused gate/up path whose down projection takes the
+row blocks (40 tokens at H = 4096, I = 8192: 512 tiles of the gate and up
+products take the GEMM)."""
 import numpy as np
 import pytest
 
@@ -29,7 +30,7 @@ def weights(H, I, seed):
 
 
 @pytest.mark.parametrize("T,H,I", [(256, 512, 1376), (4, 512, 1376), (24, 512, 1376), (40, 512, 1376), (130, 256, 704),
-                                   (40, 4096, 11008), (64, 4096, 11008)])
+                                   (40, 4096, 11008), (64, 4096, 11008), (40, 4096, 8192)])
 def test_swiglu_ffn(hx, dev, T, H, I):
     wg, sg, wu, su, wd, sd = weights(H, I, 300)
     x = rng(301).normal(0, 1, (T, H)).astype(np.float16)

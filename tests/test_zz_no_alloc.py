@@ -38,9 +38,9 @@ def _noalloc(hx, x, gamma, eps, Wg, Wu, Wd, y, stream):
 
 def test_noalloc_matches_and_allocates_nothing(hx, dev):
     """No-allocation calls in a row (256 tokens: the fused gate/up GEMM and
-    the K-split down projection; 64: the fused gate/up GEMM and the down
-    projection's four row blocks split over workgroups; 40: the decode
-    GEMVs' four row blocks; then 24 tokens: the decode GEMVs, the down
+    the K-split down projection; 64 and 40: the decode GEMVs' four row
+    blocks, the down projection's split over workgroups; then 24 tokens:
+    the decode GEMVs, the down
     projection's two row blocks split over workgroups; then 16: the down
     projection's decode GEMV split over workgroups; the splits' partials and
     counters in the scratch) leave the device's free memory unchanged and
@@ -79,6 +79,38 @@ def test_noalloc_matches_and_allocates_nothing(hx, dev):
             a, b = to_np(refs[T]), to_np(ys[T])
             assert np.isfinite(a.astype(np.float32)).all()
             assert np.array_equal(a.view(np.uint16), b.view(np.uint16)), f"T={T}"
+    finally:
+        Wg.release(); Wu.release(); Wd.release()
+
+
+def test_noalloc_fused_gate_up_with_split_down_gemv(hx, dev):
+    """At H = 4096, I = 8192 and 40 tokens the gate and up products take the
+    fused GEMM (512 column tiles) while the down projection takes the
+    decode GEMV's four row blocks split over workgroups: its partials and
+    counters come from the scratch, and the no-allocation call equals
+    hx_swiglu_ffn bit for bit."""
+    import torch
+    Hs, Is, T = 4096, 8192, 40
+    r = rng(520)
+    ws = []
+    for shape, n in (((Hs, Is), Is), ((Hs, Is), Is), ((Is, Hs), Hs)):
+        w = to_dev(r.integers(-127, 128, shape, dtype=np.int8), dev)
+        sc = to_dev((r.uniform(0.5, 1.5, n) / (127 * np.sqrt(shape[0] / 3))).astype(np.float16), dev)
+        ws.append(hx.ResidentWeight(w, sc))
+    Wg, Wu, Wd = ws
+    stream = torch.cuda.Stream()
+    try:
+        x = to_dev(rng(521).normal(0, 1, (T, Hs)).astype(np.float16), dev)
+        gamma = to_dev(rng(522).normal(1, 0.1, Hs).astype(np.float16), dev)
+        y = torch.full((T, Hs), 7.0, dtype=torch.float16, device=dev)
+        ref = torch.full((T, Hs), 3.0, dtype=torch.float16, device=dev)
+        with torch.cuda.stream(stream):
+            assert _noalloc(hx, x, gamma, 1e-6, Wg, Wu, Wd, y, stream) == 0, hx._abi.last_error()
+            hx.swiglu_ffn(x, gamma, 1e-6, Wg, Wu, Wd, out=ref)
+        stream.synchronize()
+        a, b = to_np(ref), to_np(y)
+        assert np.isfinite(a.astype(np.float32)).all()
+        assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
     finally:
         Wg.release(); Wu.release(); Wd.release()
 
