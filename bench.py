@@ -996,7 +996,7 @@ def gemv_ab(hx, rounds: int = 5, iters: int = 400) -> str:
     shapes = [(6, 11008, 4096, (1, 4, 8, 12, 16),
                ("gemv_packed_ct3_kw16", "gemv_packed_ct3_kw16_e", "gemv_packed_ct3_kw8", "gemv_packed_ct4_kw8",
                 "gemv_packed_ct1_kw8_xd", "gemv_packed_ct6_kw16_s2")),
-              (6, 4096, 11008, (8, 12, 16),
+              (6, 4096, 11008, (1, 4, 8, 12, 16),
                ("gemv_packed_ct4_kw16_s4", "gemv_packed_ct4_kw16_s4_e", "gemv_packed_ct2_kw16_s2",
                 "gemv_packed_ct1_kw16", "gemv_packed_ct1_kw16_e", "gemv_packed_ct1_kw8", "gemv_packed_ct1_kw8_e")),
               (6, 4096, 4096, (1, 4, 8, 16),
