@@ -1483,7 +1483,7 @@ static int matmul_resident_impl(const View2& vx, hx_weight* w, const View2* vr, 
   }
   // f16 / bf16: the packed image (the [N][K] image read in place when the
   // packed path refuses the call)
-  if (w->dtype != HX_I8 && gemv_rows_route(M, w->N, w->packed != nullptr) && !vr && y_dt == x_dt) {
+  if (w->dtype != HX_I8 && gemv_rows_route(M, w->N, w->packed != nullptr, false, w->K) && !vr && y_dt == x_dt) {
     GemvArgs v{};
     v.x = vx.p; v.ldx = vx.ld; v.w = nullptr; v.ldw = 0;
     v.scale = w->scale; v.y = vy.p; v.ldy = vy.ld; v.M = M; v.N = w->N; v.K = w->K;

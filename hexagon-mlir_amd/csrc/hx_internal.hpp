@@ -183,9 +183,19 @@ inline bool gemv_rows4_i8(int64_t M, int64_t N, int64_t K, bool ffn = false) {
   if (tiles > 128 && tiles <= 256 && K >= 8192) return true;
   return (tiles + 255) / 256 == 3 && (ffn || M <= 48);
 }
+// An f16 / bf16 packed image takes them (32 < M <= 64) at three tiles per
+// CU with K >= 4096 (N = 11008, K = 4096, M = 33 / 48 / 64: 21.97 / 24.54 /
+// 28.01 us against 33.25 / 34.73 / 34.11 tiled); on the down projection's
+// shape (4096 x 11008) the tiled GEMM stays ahead (28.0-28.6 against
+// 29.4-34.2 us).
+inline bool gemv_rows4_f16(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles = (N + 15) / 16;
+  return M > kGemvRowsMaxM && M <= kGemvRowsMaxMI8 && (tiles + 255) / 256 == 3 && K >= 4096;
+}
 inline bool gemv_rows_route(int64_t M, int64_t N, bool packed, bool int8 = false, int64_t K = 0) {
   if (M <= 16) return true;
   if (packed && int8 && gemv_rows4_i8(M, N, K)) return true;
+  if (packed && !int8 && gemv_rows4_f16(M, N, K)) return true;
   if (M > kGemvRowsMaxM) return false;
   if (packed && int8) return true;
   if (N < kGemvRowsMinN) return false;

@@ -228,7 +228,8 @@ int hx_weight_info(hx_weight_t w, int64_t* k, int64_t* n, int* dtype,
  * (bf16 for a bf16 weight), Y [M, N] f16/bf16/f32.  Skinny products (int8
  * weights M <= 32, and up to 64 where the GEMV's four row blocks beat the
  * GEMM: 129..256 column tiles of 16 with K >= 8192, or 641..768 tiles up to
- * M = 48; f16 / bf16 M <= 16, or M <= 32 with N >= 2048) run the decode GEMV
+ * M = 48; f16 / bf16 M <= 16, or M <= 32 with N >= 2048, or M <= 64 on
+ * 641..768 tiles with K >= 4096) run the decode GEMV
  * on the weight's fragment-packed copy (registration keeps it beside the
  * [N, K] image: twice the weight's bytes), larger M the MFMA GEMM. */
 int hx_matmul_resident(const hx_memref2d* x, int x_dtype, hx_weight_t w,

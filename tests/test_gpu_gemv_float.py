@@ -234,17 +234,18 @@ def test_matvec_n_is_one_fallbacks(hx, dev):
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 @pytest.mark.parametrize("shape", [(17, 2048, 520), (24, 4096, 4096), (20, 11008, 1024), (23, 2053, 72),
                                    (32, 4096, 1024), (17, 1000, 520), (33, 4096, 4096), (48, 11008, 1024),
-                                   (64, 300, 8192), (63, 37, 72)],
+                                   (64, 300, 8192), (63, 37, 72), (48, 11008, 4096), (64, 4096, 11008)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_decode_float_row_blocks(hx, dev, dtype, shape):
     """16 < M <= 32 with N >= 2048: the streaming kernel with 2 blocks of 16
     activation rows (each weight fragment feeds every block), on a registered
     weight's packed image, and on an argument [N][K] weight read in place up
-    to N = 4096; fewer columns or more rows: the tiled GEMM.  Same numerics
-    either way."""
+    to N = 4096; on the packed image also 32 < M <= 64 with four blocks at
+    641..768 column tiles and K >= 4096; fewer columns or more rows: the
+    tiled GEMM.  Same numerics either way."""
     M, N, K = shape
     rows = 16 < M <= 32 and 2048 <= N <= 4096
-    rows_resident = 16 < M <= 32 and N >= 2048
+    rows_resident = (16 < M <= 32 and N >= 2048) or (32 < M <= 64 and 641 <= -(-N // 16) <= 768 and K >= 4096)
     a = _fp(dtype, (M, K), 110)
     b = _fp(dtype, (K, N), 111)
     bt = _dev(np.ascontiguousarray(b.T), dtype, dev)
